@@ -1,0 +1,222 @@
+"""Benchmark of the MI355X kael backend; prints ONE JSON line.
+
+Headline (BASELINE.json metric): f32 matmul TFLOP/s as a fraction of FP32 MFMA peak, on the
+north-star size 4096^3 (C = A.B, A and B contiguous row-major, uniform[-1,1]); a "step" is one
+kd_matmul call over inputs already resident in HBM. Secondary figures in "extra": the C1 shape
+(512^3), the C2 elementwise/reduction ops in GB/s, and the fused row kernels.
+
+Timing: W untimed warm-up steps, then K steps bracketed by kd_synchronize(); the kernel time comes
+from HIP events recorded on the backend stream (the stream every kd_* launch uses).
+The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference sources,
+threaded over the host cores) on a bounded sample, reported beside the GPU figure.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only matmul]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kael.cpp_amd"))
+
+import kd  # noqa: E402
+
+FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense FP32 matrix (AMD spec)
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+
+
+class Timer:
+    """HIP events on the backend stream around a region."""
+
+    def __init__(self, backend: kd.Backend):
+        self.b = backend
+        self.start, self.stop = ctypes.c_void_p(), ctypes.c_void_p()
+        backend.check(backend.lib.kd_event_create(ctypes.byref(self.start)), "event")
+        backend.check(backend.lib.kd_event_create(ctypes.byref(self.stop)), "event")
+
+    def __enter__(self):
+        self.b.check(self.b.lib.kd_event_record(self.start), "record")
+        return self
+
+    def __exit__(self, *exc):
+        self.b.check(self.b.lib.kd_event_record(self.stop), "record")
+        ms = ctypes.c_float()
+        self.b.check(self.b.lib.kd_event_elapsed_ms(ctypes.byref(ms), self.start, self.stop), "elapsed")
+        self.ms = ms.value
+
+
+def time_steps(backend, step, steps, warmup):
+    for _ in range(warmup):
+        step(0)
+    backend.synchronize()
+    t0 = time.perf_counter()
+    with Timer(backend) as t:
+        for i in range(steps):
+            step(i)
+    backend.synchronize()
+    wall = time.perf_counter() - t0
+    return t.ms / steps, wall
+
+
+def bench_matmul(backend, n, steps, warmup, seed=0):
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    da, db, dc = backend.to_device(a), backend.to_device(b), backend.empty((n, n), np.float32)
+    sizes = kd.MatmulSizes(1, n, n, n)
+    fn = backend.lib.kd_matmul
+
+    def step(_):
+        rc = fn(kd.F32, da.ptr, db.ptr, dc.ptr, sizes)
+        if rc:
+            backend.check(rc, "kd_matmul")
+
+    ms, wall = time_steps(backend, step, steps, warmup)
+    flops = 2.0 * n ** 3
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "wall_s": wall, "flops_per_launch": flops}
+
+
+def bench_c2(backend, steps, warmup):
+    """C2 ops with 4 rotating buffer sets (>256 MB) so the last-level cache cannot serve them."""
+    rows = cols = 4096
+    rng = np.random.default_rng(1)
+    sets = 4
+    a = [backend.to_device(rng.uniform(-1, 1, (rows, cols)).astype(np.float32)) for _ in range(sets)]
+    o = [backend.empty((rows, cols), np.float32) for _ in range(sets)]
+    b = backend.to_device(rng.uniform(-1, 1, (rows, 1)).astype(np.float32))
+    red = [backend.empty((rows,), np.float32) for _ in range(sets)]
+    out = {}
+    algo_bytes = {"add": 2 * rows * cols * 4 + rows * 4, "mul": 2 * rows * cols * 4 + rows * 4,
+                  "transposed_add": 2 * rows * cols * 4 + rows * 4, "sum_dim1": rows * cols * 4 + rows * 4,
+                  "max_all": rows * cols * 4 + 4}
+    lays = {}
+    for name in ("add", "mul"):
+        lays[name] = [kd.element_layout((rows, cols), [(cols * 4, 4), (cols * 4, 4), (4, 0)], [o[i].ptr, a[i].ptr, b.ptr])
+                      for i in range(sets)]
+    lays["transposed_add"] = [kd.element_layout((rows, cols), [(cols * 4, 4), (4, cols * 4), (4, 0)],
+                                                [o[i].ptr, a[i].ptr, b.ptr]) for i in range(sets)]
+    p = kd.params()
+    ew = backend.lib.kd_elementwise
+    rd = backend.lib.kd_reduce
+    for name, op in (("add", kd.OP["PLUS"]), ("mul", kd.OP["TIMES"]), ("transposed_add", kd.OP["PLUS"])):
+        ls = lays[name]
+        ms, _ = time_steps(backend, lambda i: ew(op, kd.F32, kd.F32, ctypes.byref(ls[i % sets]), p), steps, warmup)
+        out[name] = {"us": ms * 1e3, "gbps": algo_bytes[name] / (ms * 1e-3) / 1e9}
+    ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_SUM, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr, cols, rows),
+                       steps, warmup)
+    out["sum_dim1"] = {"us": ms * 1e3, "gbps": algo_bytes["sum_dim1"] / (ms * 1e-3) / 1e9}
+    ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_MAX, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr,
+                                             rows * cols, 1), steps, warmup)
+    out["max_all"] = {"us": ms * 1e3, "gbps": algo_bytes["max_all"] / (ms * 1e-3) / 1e9}
+    for v in out.values():
+        v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
+    return out
+
+
+def bench_rows(backend, steps, warmup):
+    """Fused row kernels on [32768, 1024] f32 (128 MiB in, 128 MiB out), 2 rotating sets."""
+    rows, cols = 32768, 1024
+    rng = np.random.default_rng(2)
+    sets = 2
+    x = [backend.to_device(rng.normal(size=(rows, cols)).astype(np.float32)) for _ in range(sets)]
+    y = [backend.empty((rows, cols), np.float32) for _ in range(sets)]
+    w = backend.to_device(np.ones(cols, np.float32))
+    bb = backend.to_device(np.zeros(cols, np.float32))
+    nbytes = 2 * rows * cols * 4
+    out = {}
+    sm = backend.lib.kd_softmax_rows
+    ms, _ = time_steps(backend, lambda i: sm(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 0), steps, warmup)
+    out["softmax_1024"] = {"us": ms * 1e3, "gbps": nbytes / (ms * 1e-3) / 1e9}
+    st = backend.lib.kd_standardize_rows
+    ms, _ = time_steps(backend, lambda i: st(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 1e-5, w.ptr, bb.ptr),
+                       steps, warmup)
+    out["layernorm_1024"] = {"us": ms * 1e3, "gbps": (nbytes + 2 * cols * 4) / (ms * 1e-3) / 1e9}
+    for v in out.values():
+        v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
+    return out
+
+
+def cpu_baseline(n, budget_s=20.0):
+    """kael's CPU matmul (reference build, threaded) on a bounded sample of the same workload."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import support
+
+    lib = support.load_ref("ref")
+    threads = int(os.environ.get("KAEL_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    lib.ref_set_threads(threads)
+    t = ctypes.c_double()
+    # one probe call sizes the sample to about `budget_s` seconds
+    if lib.ref_time_matmul(n, n, n, 1, ctypes.byref(t)) != 0:
+        raise RuntimeError(support.ref_error(lib))
+    iters = max(1, min(10, int(budget_s / max(t.value, 1e-3)) - 1))
+    if lib.ref_time_matmul(n, n, n, iters, ctypes.byref(t)) != 0:
+        raise RuntimeError(support.ref_error(lib))
+    tflops = 2.0 * n ** 3 / t.value / 1e12
+    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"kael::matmul f32 {n}^3 (CPU path, matmul_versions v6), median of {iters} calls after 2 warm-up calls, "
+                      f"KAEL_NUM_THREADS={threads}", "median_s": t.value}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this backend drives one GPU; multi-GPU runs are out of scope (bench.py --gpus 1)"}))
+        return 2
+    backend = kd.load()
+    if not backend.lib.kd_available():
+        raise SystemExit(f"no usable gfx950 device: {backend.error()}")
+    info = backend.device_info()
+    n = 4096
+    main_run = bench_matmul(backend, n, args.steps, args.warmup)
+    extra = {"device": info}
+    if args.only in ("", "all"):
+        extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup)
+        extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
+        extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(n)
+        except Exception as e:  # the baseline is reported, never required
+            cpu = {"error": str(e)}
+    achieved = main_run["tflops"]
+    line = {
+        "metric": "f32 matmul TFLOP/s (% FP32 MFMA peak)",
+        "value": round(achieved, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_run["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic uniform[-1,1] (numpy seed 0), resident in HBM",
+        "config": {"workload": "f32 matmul C=A.B, M=N=K=4096, contiguous row-major (BASELINE C1 recipe at the north-star size)",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

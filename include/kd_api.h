@@ -1,0 +1,272 @@
+/*
+ * kd_api.h - C ABI of the MI355X (gfx950) device backend for kael.
+ *
+ * Every entry point replaces one function of kael's device boundary,
+ * `namespace kael::device` in include/kael/device_kernels.h:96-116 of the reference
+ * (JetBerri/kael.cpp 1.0.1). The C++ adapter kael.cpp_amd/host/backend_hip.cpp
+ * implements those `kael::device::*` symbols on top of this header and turns a
+ * non-zero status into `kael::Error` carrying kd_last_error().
+ *
+ * Conventions
+ *  - Plain C: pointers, sizes and POD structs only. No C++ or torch types.
+ *  - Every call returns KD_OK (0) or a negative KD_E_* status; the message of the
+ *    last failure on the calling thread is returned by kd_last_error().
+ *  - All device work is issued on one in-order HIP stream (kd_set_stream; default
+ *    is the null stream), so kernels run in issue order, exactly like the
+ *    reference's default-stream backend (reference src/cuda/backend.cu:45-53).
+ *  - kd_copy_h2d and kd_copy_d2h return only after the bytes have landed, as the
+ *    synchronous cudaMemcpy of reference src/cuda/backend.cu:92-100 does.
+ *  - count == 0 (or an empty matrix) is a no-op for every operation.
+ *  - Pointers inside layouts already include the tensor offset (reference
+ *    src/tensor.cpp:37-41); strides in kd_element_layout are in BYTES, strides in
+ *    kd_index_layout are in ELEMENTS (reference device_kernels.h:70-87).
+ */
+#ifndef KD_API_H
+#define KD_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KD_MAX_DIMS 8     /* reference device_kernels.h:12 kMaxDims */
+#define KD_MAX_OPERANDS 4 /* reference device_kernels.h:13 kMaxOperands */
+
+/* Status codes. */
+#define KD_OK 0
+#define KD_E_INVALID (-1)     /* bad argument (dtype, op, sizes, layout) */
+#define KD_E_RUNTIME (-2)     /* a HIP runtime call failed */
+#define KD_E_NO_DEVICE (-3)   /* no usable gfx950 device */
+#define KD_E_UNSUPPORTED (-4) /* combination the reference also rejects */
+
+/* dtype tags; same order as `enum class DType { F32, F64, I64, Bool }`
+ * (reference include/kael/dtype.h:22). Bool is stored as one byte 0/1. */
+typedef enum kd_dtype { KD_F32 = 0, KD_F64 = 1, KD_I64 = 2, KD_BOOL = 3 } kd_dtype;
+
+/* Element operations; values 0..35 are `enum class ElementOp` in the order of
+ * reference include/kael/device_kernels.h:15-52. Values from 64 on are this
+ * backend's extensions (no reference counterpart; they replace host round trips
+ * or composed launches of the reference, see each comment). */
+typedef enum kd_element_op {
+    KD_OP_PLUS = 0,
+    KD_OP_MINUS,
+    KD_OP_TIMES,
+    KD_OP_DIVIDES,
+    KD_OP_POWER,
+    KD_OP_MAXIMUM,
+    KD_OP_MINIMUM,
+    KD_OP_EQUAL,
+    KD_OP_NOT_EQUAL,
+    KD_OP_LESS,
+    KD_OP_LESS_EQUAL,
+    KD_OP_GREATER,
+    KD_OP_GREATER_EQUAL,
+    KD_OP_LOGICAL_AND,
+    KD_OP_LOGICAL_OR,
+    KD_OP_LOGICAL_XOR,
+    KD_OP_IS_ZERO,
+    KD_OP_NEGATE,
+    KD_OP_ABSOLUTE,
+    KD_OP_SIGN,
+    KD_OP_EXP,
+    KD_OP_LOG,
+    KD_OP_LOG1P,
+    KD_OP_EXPM1,
+    KD_OP_SQRT,
+    KD_OP_RSQRT,
+    KD_OP_SIN,
+    KD_OP_COS,
+    KD_OP_TANH,
+    KD_OP_SIGMOID,
+    KD_OP_RELU,
+    KD_OP_GELU_EXACT,
+    KD_OP_GELU_TANH,
+    KD_OP_CLAMP,
+    KD_OP_WHERE,
+    KD_OP_MASKED_FILL,
+    /* out = grad * d/dx gelu(x), operands (out, x, grad). Replaces the untagged
+     * host lambda of reference src/autograd/functions_math.cpp:221-231, which
+     * round-trips a device tensor through the host (include/kael/kernels.h:130-133).
+     * Slopes follow functions_math.cpp:35-46. Floating dtypes only. */
+    KD_OP_GELU_EXACT_BACKWARD = 64,
+    KD_OP_GELU_TANH_BACKWARD = 65
+} kd_element_op;
+
+/* `enum class ReduceOp { Sum, Max, Min }` (reference device_kernels.h:54). */
+typedef enum kd_reduce_op { KD_REDUCE_SUM = 0, KD_REDUCE_MAX = 1, KD_REDUCE_MIN = 2 } kd_reduce_op;
+
+/* Mirror of `struct ElementParameters` (reference device_kernels.h:57-68): integer
+ * arguments travel apart from real ones so that every int64 survives. */
+typedef struct kd_element_parameters {
+    double reals[2];
+    int64_t integers[2];
+} kd_element_parameters;
+
+/* Mirror of `struct ElementLayout` (reference device_kernels.h:70-77), same field
+ * order and size (368 bytes). Operand 0 is the output; strides are bytes. */
+typedef struct kd_element_layout {
+    int32_t dims;
+    int32_t operands;
+    int64_t count;
+    int64_t shape[KD_MAX_DIMS];
+    int64_t strides[KD_MAX_OPERANDS][KD_MAX_DIMS];
+    void* base[KD_MAX_OPERANDS];
+} kd_element_layout;
+
+/* Mirror of `struct IndexLayout` (reference device_kernels.h:79-87); strides are
+ * elements. */
+typedef struct kd_index_layout {
+    int32_t dims;
+    int32_t axis;
+    int64_t count;
+    int64_t shape[KD_MAX_DIMS];
+    int64_t data_strides[KD_MAX_DIMS];
+    int64_t index_strides[KD_MAX_DIMS];
+    int64_t source_strides[KD_MAX_DIMS];
+} kd_index_layout;
+
+/* Mirror of `struct MatmulSizes` (reference device_kernels.h:89-94). */
+typedef struct kd_matmul_sizes {
+    int64_t batches;
+    int64_t rows;
+    int64_t inner;
+    int64_t columns;
+} kd_matmul_sizes;
+
+/* ---- errors and runtime ------------------------------------------------ */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kd_last_error(void);
+
+/* reference device_kernels.h:96 `bool available()`: 1 if a gfx950 device is usable. */
+int kd_available(void);
+/* reference device_kernels.h:97 `void synchronize()`: drains the backend stream. */
+int kd_synchronize(void);
+/* Selects the stream every later call issues on (hipStream_t; NULL = null stream).
+ * No reference counterpart: the reference always uses the default stream. */
+int kd_set_stream(void* stream);
+void* kd_get_stream(void);
+
+/* reference device_kernels.h:99 `std::byte* allocate(int64 bytes)`. */
+int kd_malloc(void** out, int64_t bytes);
+/* reference device_kernels.h:100 `void release(std::byte*) noexcept`: never fails. */
+void kd_free(void* block);
+/* reference device_kernels.h:101-103 copy_to_device / copy_to_host / copy_within_device. */
+int kd_copy_h2d(void* target, const void* source, int64_t bytes);
+int kd_copy_d2h(void* target, const void* source, int64_t bytes);
+int kd_copy_d2d(void* target, const void* source, int64_t bytes);
+
+/* ---- the hot path ------------------------------------------------------ */
+
+/* reference device_kernels.h:105 `fill(DType, std::byte*, int64 count, const void* value)`:
+ * `value` is a host pointer to one element of `dtype`, read during the call. */
+int kd_fill(int dtype, void* target, int64_t count, const void* value);
+
+/* reference device_kernels.h:106 `convert(DType out, DType in, const ElementLayout&)`:
+ * strided copy with the cast rules of reference src/cuda/kernels.inl:5-13
+ * (bool normalisation, saturating float->int). Operands: (out, in). */
+int kd_convert(int out_dtype, int in_dtype, const kd_element_layout* layout);
+
+/* reference device_kernels.h:107-108 `elementwise(ElementOp, DType out, DType in,
+ * const ElementLayout&, ElementParameters)`. As in the reference, the output dtype
+ * is implied by the op (In for arithmetic, Bool for comparisons) and `out_dtype`
+ * is only checked for consistency. */
+int kd_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout* layout,
+                   kd_element_parameters parameters);
+
+/* reference device_kernels.h:109-110 `reduce(ReduceOp, DType out, DType in, std::byte*
+ * results, const std::byte* data, int64 chunk_size, int64 output_count)`:
+ * results[r] = op over data[r*chunk_size .. (r+1)*chunk_size). Sum of f32/f64
+ * accumulates in double and stores In; Sum of i64/bool accumulates wrapping int64
+ * and stores int64; Max/Min are NaN-propagating and store In
+ * (reference src/cuda/kernels.inl:426-445). Max/Min of an empty chunk is an error. */
+int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
+              int64_t chunk_size, int64_t output_count);
+
+/* reference device_kernels.h:111-112 `matmul(DType, const std::byte* a, const std::byte* b,
+ * std::byte* out, const MatmulSizes&)`: out[b] = a[b] . b[b] for contiguous row-major
+ * batches, overwriting out. f32 and f64 on matrix cores, i64 wrapping, bool rejected. */
+int kd_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes);
+
+/* Extension of kd_matmul with element strides per operand, so that transposed or
+ * batch-broadcast operands are read in place instead of being materialised by
+ * convert (reference src/ops/linalg.cpp:56-76, src/nn/layers.cpp:43,
+ * src/autograd/functions_linalg.cpp:37,44). Strides are in elements, for
+ * (batch, row, column) of each operand; a batch stride of 0 broadcasts. */
+typedef struct kd_matmul_strides {
+    int64_t a[3];
+    int64_t b[3];
+    int64_t out[3];
+} kd_matmul_strides;
+int kd_matmul_strided(int dtype, const void* a, const void* b, void* out,
+                      const kd_matmul_sizes* sizes, const kd_matmul_strides* strides);
+
+/* reference device_kernels.h:113-114 `gather(DType, std::byte* out, const std::byte* data,
+ * const int64* indices, const IndexLayout&)`; indices must already be range-checked
+ * by the caller (reference src/internal/index_checks.h:37-43). */
+int kd_gather(int dtype, void* out, const void* data, const int64_t* indices,
+              const kd_index_layout* layout);
+
+/* reference device_kernels.h:115-116 `scatter_add(DType, std::byte* data, const int64*
+ * indices, const std::byte* source, const IndexLayout&)`: atomic data[pos] += source[e];
+ * i64 wraps; dtypes f32, f64, i64 (the reference sends bool to the host). */
+int kd_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
+                   const kd_index_layout* layout);
+
+/* ---- fused row kernels (extensions replacing composed device paths) ---- */
+
+/* Row softmax over `rows` contiguous rows of `cols`: max, exp(x-max), sum in double,
+ * divide by the float-rounded sum. `log_softmax` != 0 gives x-max-log(sum).
+ * Follows reference src/ops/nn.cpp:60-84; replaces the 5-kernel composition of
+ * nn.cpp:158-159 / 176-177. dtype f32 or f64. */
+int kd_softmax_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols,
+                    int log_softmax);
+
+/* Row standardisation (LayerNorm core): mean and population variance in double,
+ * out = (x - mean) / sqrt(var + eps). With `weight`/`bias` non-NULL (length cols)
+ * the affine `* weight + bias` is fused in (each rounded as the reference's separate
+ * mul and add kernels round it). Follows reference src/ops/nn.cpp:114-129 and
+ * src/nn/layers.cpp:60-68; replaces the ~10 launches of nn.cpp:253-258. */
+int kd_standardize_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols,
+                        double eps, const void* weight, const void* bias);
+
+/* Per-row cross-entropy loss: log(sum exp(x - max)) - (x[target] - max), sum in
+ * double. Follows reference src/ops/nn.cpp:105-112 (replaces the device branch
+ * nn.cpp:185-187). targets are int64 in [0, cols), range-checked by the caller. */
+int kd_cross_entropy_rows(int dtype, void* losses, const void* logits, const int64_t* targets,
+                          int64_t rows, int64_t cols);
+
+/* Cross-entropy gradient: out = softmax(x) * w[row] - w[row] * onehot(target).
+ * Follows reference src/ops/nn.cpp:214-240 (CPU only in the reference). */
+int kd_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
+                          const void* row_weights, int64_t rows, int64_t cols);
+
+/* ---- host-side layout planning ----------------------------------------- */
+
+/* Builds the kd_element_layout that kael's TensorIterator would hand to the device for
+ * these operands (reference src/iterator.cpp:152-172 prepare_loop, :47-63 coalesce_dims,
+ * :112-132 device_layout; src/shape.cpp:123-145 broadcast_strides): operand 0 is the output
+ * with `ranks[0]` dims; inputs broadcast against it (trailing alignment; size-1 dims get
+ * stride 0); strides are converted to bytes; size-1 dims are dropped and mergeable dims
+ * coalesced from the innermost outward; an empty result becomes one dim of size 1.
+ * shapes/strides are [operands][KD_MAX_DIMS] arrays of ELEMENT counts. Host only. */
+int kd_layout_build(kd_element_layout* out, int operands, const int* ranks, const int64_t* shapes,
+                    const int64_t* strides, const int* element_sizes, void* const* bases);
+
+/* ---- measurement helpers (no reference counterpart; used by the bench) -- */
+
+/* HIP events recorded on the backend stream. */
+int kd_event_create(void** event);
+int kd_event_destroy(void* event);
+int kd_event_record(void* event);
+int kd_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Device properties: compute units, max engine clock (kHz), and the gfx arch name. */
+int kd_device_info(int* compute_units, int* clock_khz, char* arch, int arch_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KD_API_H */

@@ -1,0 +1,178 @@
+// kd_index.hip - gather and scatter_add for gfx950.
+//
+// Contract of reference src/cuda/kernels.inl:179-221 and 447-465: element e of the index
+// space decodes to (index position, source position, data position) with IndexLayout's
+// element strides; the data position along `axis` comes from indices[]. gather copies
+// data -> out[e] (out is contiguous in e), scatter_add atomically adds source into data (i64
+// wraps because two's-complement addition is the same operation as unsigned addition).
+// Indices are range-checked by the host before the call (src/internal/index_checks.h:37-43).
+//
+// Decoding uses multiply-high division per dim. When the innermost dim is not the indexed
+// axis and is contiguous in every role, consecutive lanes touch consecutive elements of the
+// same gathered row, so an embedding lookup reads and writes whole rows coalesced.
+#include <algorithm>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct IndexPlan {
+    int dims;
+    int axis;
+    FastDiv div[KD_MAX_DIMS];  // innermost first
+    int64_t data_stride[KD_MAX_DIMS];
+    int64_t index_stride[KD_MAX_DIMS];
+    int64_t source_stride[KD_MAX_DIMS];
+    int axis_slot;             // position of `axis` in the innermost-first order
+    int64_t axis_data_stride;
+};
+
+struct Position {
+    int64_t data, index, source;
+};
+
+__device__ __forceinline__ Position locate(const IndexPlan& p, const int64_t* __restrict__ indices, uint32_t e) {
+    Position pos{0, 0, 0};
+    for (int k = 0; k < p.dims; ++k) {
+        const uint32_t q = p.div[k].div(e);
+        const int64_t c = static_cast<int64_t>(e - q * p.div[k].divisor);
+        e = q;
+        pos.index += c * p.index_stride[k];
+        pos.source += c * p.source_stride[k];
+        if (k != p.axis_slot) pos.data += c * p.data_stride[k];
+    }
+    pos.data += indices[pos.index] * p.axis_data_stride;
+    return pos;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gather_kernel(T* __restrict__ out, const T* __restrict__ data,
+                                                          const int64_t* __restrict__ indices, IndexPlan p,
+                                                          uint32_t count) {
+    for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < count; e += gridDim.x * kThreads) {
+        out[e] = data[locate(p, indices, e).data];
+    }
+}
+
+__device__ __forceinline__ void atomic_add_value(float* t, float v) { atomicAdd(t, v); }
+__device__ __forceinline__ void atomic_add_value(double* t, double v) { atomicAdd(t, v); }
+__device__ __forceinline__ void atomic_add_value(int64_t* t, int64_t v) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(t), static_cast<unsigned long long>(v));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void scatter_add_kernel(T* data, const int64_t* __restrict__ indices,
+                                                               const T* __restrict__ source, IndexPlan p,
+                                                               uint32_t count) {
+    for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < count; e += gridDim.x * kThreads) {
+        const Position pos = locate(p, indices, e);
+        atomic_add_value(data + pos.data, source[pos.source]);
+    }
+}
+
+// 64-bit decode for index spaces of 2^31 elements or more.
+template <typename T, bool Scatter>
+__global__ __launch_bounds__(kThreads) void index64_kernel(T* out_or_data, const T* in, const int64_t* indices,
+                                                           kd_index_layout l) {
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; e < l.count;
+         e += static_cast<int64_t>(gridDim.x) * kThreads) {
+        int64_t rem = e, d = 0, ix = 0, s = 0;
+        for (int dim = l.dims - 1; dim >= 0; --dim) {
+            const int64_t c = rem % l.shape[dim];
+            rem /= l.shape[dim];
+            ix += c * l.index_strides[dim];
+            s += c * l.source_strides[dim];
+            if (dim != l.axis) d += c * l.data_strides[dim];
+        }
+        d += indices[ix] * l.data_strides[l.axis];
+        if constexpr (Scatter) atomic_add_value(out_or_data + d, in[s]);
+        else out_or_data[e] = in[d];
+    }
+}
+
+int plan(const kd_index_layout& l, IndexPlan& p) {
+    if (l.dims < 1 || l.dims > KD_MAX_DIMS) return fail(KD_E_INVALID, "index layout dims out of range");
+    if (l.axis < 0 || l.axis >= l.dims) return fail(KD_E_INVALID, "index layout axis out of range");
+    p.dims = l.dims;
+    p.axis = l.axis;
+    int k = 0;
+    for (int dim = l.dims - 1; dim >= 0; --dim, ++k) {
+        if (l.shape[dim] <= 0) return fail(KD_E_INVALID, "index layout has an empty dim with count > 0");
+        p.div[k] = FastDiv(static_cast<uint32_t>(l.shape[dim]));
+        p.data_stride[k] = l.data_strides[dim];
+        p.index_stride[k] = l.index_strides[dim];
+        p.source_stride[k] = l.source_strides[dim];
+        if (dim == l.axis) p.axis_slot = k;
+    }
+    p.axis_data_stride = l.data_strides[l.axis];
+    return KD_OK;
+}
+
+int grid_for(int64_t count) {
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((count + kThreads - 1) / kThreads,
+                                                                    int64_t{compute_units()} * 32)));
+}
+
+template <typename T> int gather_typed(void* out, const void* data, const int64_t* indices, const kd_index_layout& l) {
+    if (l.count < (int64_t{1} << 31)) {
+        IndexPlan p;
+        if (int rc = plan(l, p)) return rc;
+        hipLaunchKernelGGL((gather_kernel<T>), dim3(grid_for(l.count)), dim3(kThreads), 0, stream(), static_cast<T*>(out),
+                           static_cast<const T*>(data), indices, p, static_cast<uint32_t>(l.count));
+    } else {
+        hipLaunchKernelGGL((index64_kernel<T, false>), dim3(grid_for(l.count)), dim3(kThreads), 0, stream(),
+                           static_cast<T*>(out), static_cast<const T*>(data), indices, l);
+    }
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <typename T> int scatter_typed(void* data, const int64_t* indices, const void* source, const kd_index_layout& l) {
+    if (l.count < (int64_t{1} << 31)) {
+        IndexPlan p;
+        if (int rc = plan(l, p)) return rc;
+        hipLaunchKernelGGL((scatter_add_kernel<T>), dim3(grid_for(l.count)), dim3(kThreads), 0, stream(),
+                           static_cast<T*>(data), indices, static_cast<const T*>(source), p, static_cast<uint32_t>(l.count));
+    } else {
+        hipLaunchKernelGGL((index64_kernel<T, true>), dim3(grid_for(l.count)), dim3(kThreads), 0, stream(),
+                           static_cast<T*>(data), static_cast<const T*>(source), indices, l);
+    }
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" int kd_gather(int dtype, void* out, const void* data, const int64_t* indices, const kd_index_layout* layout) {
+    if (layout == nullptr) return fail(KD_E_INVALID, "kd_gather: null layout");
+    if (layout->count == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    switch (dtype) {
+    case KD_F32: return gather_typed<float>(out, data, indices, *layout);
+    case KD_F64: return gather_typed<double>(out, data, indices, *layout);
+    case KD_I64: return gather_typed<int64_t>(out, data, indices, *layout);
+    case KD_BOOL: return gather_typed<uint8_t>(out, data, indices, *layout);
+    }
+    return fail(KD_E_INVALID, "kd_gather: unknown dtype");
+}
+
+extern "C" int kd_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
+                              const kd_index_layout* layout) {
+    if (layout == nullptr) return fail(KD_E_INVALID, "kd_scatter_add: null layout");
+    if (layout->count == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    switch (dtype) {
+    case KD_F32: return scatter_typed<float>(data, indices, source, *layout);
+    case KD_F64: return scatter_typed<double>(data, indices, source, *layout);
+    case KD_I64: return scatter_typed<int64_t>(data, indices, source, *layout);
+    }
+    return fail(KD_E_UNSUPPORTED, "kd_scatter_add: dtype must be f32, f64 or i64");
+}

@@ -1,0 +1,665 @@
+// kd_matmul.hip - batched matrix products for gfx950.
+//
+// Contract of reference include/kael/device_kernels.h:111-112 / src/cuda/backend.cu:142-171:
+// out[b] = a[b] . b[b] for `batches` row-major matrices, `out` overwritten (never accumulated).
+// f32 and f64 are floating point, i64 wraps (kernels.inl:160-169), bool is rejected
+// (src/ops/linalg.cpp:72). The reference computes a 4x4 register tile per thread straight from
+// global memory (kernels.inl:136-177). Here, per shape:
+//
+//   mfma   f32, M and N large: 128x128 workgroup tiles, four waves of 64x64, each a 2x2 grid of
+//          v_mfma_f32_32x32x2f32 accumulators. K advances 16 at a time through double-buffered
+//          LDS; global loads for step k+1 are in flight while step k multiplies.
+//   skinny f32, M <= 16 (decode-shaped): lanes own 4 columns each, K is split across the
+//          workgroup's waves and, when N alone cannot fill the device, across workgroups whose
+//          partial sums land in a workspace and are added in a fixed order by a second launch.
+//   rowdot f32, N <= 4 (e.g. the GPT head computing W . x^T): one wave per output row, a
+//          coalesced dot product along K.
+//   tiled  f64 and i64: 64x64 LDS tiles, 4x4 outputs per lane (exact wrapping for i64).
+//
+// Every kernel takes per-operand element strides (batch, row, column), which is how
+// kd_matmul_strided reads transposed or batch-broadcast operands in place.
+#include <algorithm>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+struct Strides3 {
+    int64_t b, r, c;
+};
+
+struct MatmulArgs {
+    int64_t batches, M, K, N;
+    Strides3 sa, sb, so;
+};
+
+constexpr int kThreads = 256;
+
+// ---- mfma family (f32) ---------------------------------------------------------------------
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 16;
+constexpr int kAld = kBK + 4;   // A tile [m][k]: row stride 20 floats, conflict-free 16-byte reads
+constexpr int kBld = kBN + 4;   // B tile [k][n]
+constexpr int kAsize = kBM * kAld;
+constexpr int kBsize = kBK * kBld;
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Operand access modes, chosen on the host.
+//   A: kRowVec = K contiguous (row-major), kColVec = M contiguous (a transposed view)
+//   B: kRowVec = N contiguous (row-major), kColVec = K contiguous (a transposed view)
+enum { kRowVec = 0, kColVec = 1, kGeneric = 2 };
+
+template <int AMode>
+__device__ __forceinline__ void load_a(float (&reg)[8], const float* a, const MatmulArgs& p, int64_t m0, int64_t k0) {
+    const int t = threadIdx.x;
+    if constexpr (AMode == kRowVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t m = m0 + t / 4 + 64 * i;
+            const int64_t k = k0 + 4 * (t % 4);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < p.M && k < p.K) v = *reinterpret_cast<const float4*>(a + m * p.sa.r + k);
+            reg[4 * i + 0] = v.x;
+            reg[4 * i + 1] = v.y;
+            reg[4 * i + 2] = v.z;
+            reg[4 * i + 3] = v.w;
+        }
+    } else if constexpr (AMode == kColVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t m = m0 + 4 * (t % 32);
+            const int64_t k = k0 + t / 32 + 8 * i;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < p.M && k < p.K) v = *reinterpret_cast<const float4*>(a + k * p.sa.c + m);
+            reg[4 * i + 0] = v.x;
+            reg[4 * i + 1] = v.y;
+            reg[4 * i + 2] = v.z;
+            reg[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + kThreads * i;
+            const int64_t m = m0 + idx / kBK;
+            const int64_t k = k0 + idx % kBK;
+            reg[i] = (m < p.M && k < p.K) ? a[m * p.sa.r + k * p.sa.c] : 0.f;
+        }
+    }
+}
+
+template <int AMode> __device__ __forceinline__ void store_a(float* As, const float (&reg)[8]) {
+    const int t = threadIdx.x;
+    if constexpr (AMode == kRowVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = t / 4 + 64 * i;
+            const int k = 4 * (t % 4);
+            *reinterpret_cast<float4*>(As + row * kAld + k) =
+                make_float4(reg[4 * i], reg[4 * i + 1], reg[4 * i + 2], reg[4 * i + 3]);
+        }
+    } else if constexpr (AMode == kColVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int m = 4 * (t % 32);
+            const int k = t / 32 + 8 * i;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) As[(m + e) * kAld + k] = reg[4 * i + e];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + kThreads * i;
+            As[(idx / kBK) * kAld + idx % kBK] = reg[i];
+        }
+    }
+}
+
+template <int BMode>
+__device__ __forceinline__ void load_b(float (&reg)[8], const float* b, const MatmulArgs& p, int64_t k0, int64_t n0) {
+    const int t = threadIdx.x;
+    if constexpr (BMode == kRowVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t k = k0 + t / 32 + 8 * i;
+            const int64_t n = n0 + 4 * (t % 32);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < p.K && n < p.N) v = *reinterpret_cast<const float4*>(b + k * p.sb.r + n);
+            reg[4 * i + 0] = v.x;
+            reg[4 * i + 1] = v.y;
+            reg[4 * i + 2] = v.z;
+            reg[4 * i + 3] = v.w;
+        }
+    } else if constexpr (BMode == kColVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t n = n0 + t / 4 + 64 * i;
+            const int64_t k = k0 + 4 * (t % 4);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < p.K && n < p.N) v = *reinterpret_cast<const float4*>(b + n * p.sb.c + k);
+            reg[4 * i + 0] = v.x;
+            reg[4 * i + 1] = v.y;
+            reg[4 * i + 2] = v.z;
+            reg[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + kThreads * i;
+            const int64_t k = k0 + idx / kBN;
+            const int64_t n = n0 + idx % kBN;
+            reg[i] = (k < p.K && n < p.N) ? b[k * p.sb.r + n * p.sb.c] : 0.f;
+        }
+    }
+}
+
+template <int BMode> __device__ __forceinline__ void store_b(float* Bs, const float (&reg)[8]) {
+    const int t = threadIdx.x;
+    if constexpr (BMode == kRowVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int k = t / 32 + 8 * i;
+            const int n = 4 * (t % 32);
+            *reinterpret_cast<float4*>(Bs + k * kBld + n) =
+                make_float4(reg[4 * i], reg[4 * i + 1], reg[4 * i + 2], reg[4 * i + 3]);
+        }
+    } else if constexpr (BMode == kColVec) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int n = t / 4 + 64 * i;
+            const int k = 4 * (t % 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Bs[(k + e) * kBld + n] = reg[4 * i + e];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + kThreads * i;
+            Bs[(idx / kBN) * kBld + idx % kBN] = reg[i];
+        }
+    }
+}
+
+// Maps the linear workgroup id to a (tile_m, tile_n) pair so that the workgroups that one XCD
+// runs (ids congruent mod 8 are dispatched to the same XCD) cover a compact block of tiles,
+// sharing A rows and B columns in that XCD's L2.
+__device__ __forceinline__ void tile_of(int64_t id, int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
+    const int64_t total = tiles_m * tiles_n;
+    int64_t local = id;
+    if (total % 8 == 0) local = (id % 8) * (total / 8) + id / 8;
+    // Grouped order: columns of 8 tile-rows walked along N.
+    constexpr int64_t kGroup = 8;
+    const int64_t group_size = kGroup * tiles_n;
+    const int64_t group = local / group_size;
+    const int64_t first_m = group * kGroup;
+    const int64_t rows_in_group = std::min<int64_t>(kGroup, tiles_m - first_m);
+    const int64_t in_group = local % group_size;
+    tm = first_m + in_group % rows_in_group;
+    tn = in_group / rows_in_group;
+}
+
+template <int AMode, int BMode>
+__global__ __launch_bounds__(kThreads) void mfma_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                            float* __restrict__ out, MatmulArgs p) {
+    __shared__ float As[2][kAsize];
+    __shared__ float Bs[2][kBsize];
+
+    const int64_t tiles_m = (p.M + kBM - 1) / kBM;
+    const int64_t tiles_n = (p.N + kBN - 1) / kBN;
+    int64_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t batch = blockIdx.y;
+    const int64_t m0 = tm * kBM;
+    const int64_t n0 = tn * kBN;
+    a += batch * p.sa.b;
+    b += batch * p.sb.b;
+    out += batch * p.so.b;
+
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const int wm = wave / 2;  // wave tile row (0..1), 64 rows each
+    const int wn = wave % 2;  // wave tile col (0..1), 64 cols each
+    const int li = lane % 32;
+    const int lh = lane / 32;
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    float ra[8], rb[8];
+    const int64_t ksteps = (p.K + kBK - 1) / kBK;
+    load_a<AMode>(ra, a, p, m0, 0);
+    load_b<BMode>(rb, b, p, 0, n0);
+    store_a<AMode>(As[0], ra);
+    store_b<BMode>(Bs[0], rb);
+    __syncthreads();
+
+    for (int64_t ks = 0; ks < ksteps; ++ks) {
+        const int cur = ks & 1;
+        const bool more = ks + 1 < ksteps;
+        if (more) {
+            load_a<AMode>(ra, a, p, m0, (ks + 1) * kBK);
+            load_b<BMode>(rb, b, p, (ks + 1) * kBK, n0);
+        }
+        const float* as = As[cur];
+        const float* bs = Bs[cur];
+#pragma unroll
+        for (int kg = 0; kg < kBK; kg += 8) {
+            // Lane (li, lh) feeds k = kg + 4*lh + s to MFMA step s (s = 0..3): the same k for
+            // its A element and its B element, so the 2-deep MFMA sums cover k = kg..kg+7.
+            float4 af[2];
+            float bf[2][4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = *reinterpret_cast<const float4*>(as + (wm * 64 + i * 32 + li) * kAld + kg + 4 * lh);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) bf[j][s] = bs[(kg + 4 * lh + s) * kBld + wn * 64 + j * 32 + li];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const float av = s == 0 ? af[i].x : s == 1 ? af[i].y : s == 2 ? af[i].z : af[i].w;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bf[j][s], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (more) {
+            store_a<AMode>(As[cur ^ 1], ra);
+            store_b<BMode>(Bs[cur ^ 1], rb);
+        }
+        __syncthreads();
+    }
+
+    // Accumulator element r of lane (li, lh) is row 8*(r/4) + 4*lh + r%4, column li of its
+    // 32x32 block.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t col = n0 + wn * 64 + j * 32 + li;
+            if (col >= p.N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * lh + (r % 4);
+                if (row < p.M) out[row * p.so.r + col * p.so.c] = acc[i][j][r];
+            }
+        }
+}
+
+// ---- skinny family (f32, small M) ------------------------------------------------------------
+
+constexpr int kSkinnyMaxM = 16;
+constexpr int kSkinnyCols = 256;  // 64 lanes x 4 columns
+
+// Partial sums of rows [0, M) x columns [n0, n0+256) over k in [k_begin, k_end): the four waves
+// take interleaved k, then combine in LDS in wave order. `partial` (if non-null) receives the
+// workgroup's sum for split index blockIdx.y; otherwise the result goes to `out` directly.
+template <int MT, bool BVec>
+__global__ __launch_bounds__(kThreads) void skinny_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                          float* __restrict__ out, float* __restrict__ partial,
+                                                          MatmulArgs p, int64_t k_chunk) {
+    __shared__ float red[4][MT][kSkinnyCols];
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const int64_t batch = blockIdx.z;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kSkinnyCols + lane * 4;
+    const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * k_chunk;
+    const int64_t k_end = std::min<int64_t>(p.K, k_begin + k_chunk);
+    a += batch * p.sa.b;
+    b += batch * p.sb.b;
+
+    float acc[MT][4];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[m][c] = 0.f;
+
+    for (int64_t k = k_begin + wave; k < k_end; k += 4) {
+        float bv[4];
+        if (BVec && n0 + 3 < p.N) {
+            const float4 v = *reinterpret_cast<const float4*>(b + k * p.sb.r + n0);
+            bv[0] = v.x;
+            bv[1] = v.y;
+            bv[2] = v.z;
+            bv[3] = v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) bv[c] = n0 + c < p.N ? b[k * p.sb.r + (n0 + c) * p.sb.c] : 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m < p.M) {
+                const float av = a[m * p.sa.r + k * p.sa.c];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[m][c] += av * bv[c];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[wave][m][lane * 4 + c] = acc[m][c];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < MT * kSkinnyCols; idx += kThreads) {
+        const int m = idx / kSkinnyCols;
+        const int col = idx % kSkinnyCols;
+        const int64_t n = static_cast<int64_t>(blockIdx.x) * kSkinnyCols + col;
+        if (m >= p.M || n >= p.N) continue;
+        const float v = ((red[0][m][col] + red[1][m][col]) + red[2][m][col]) + red[3][m][col];
+        if (partial != nullptr) {
+            partial[((batch * gridDim.y + blockIdx.y) * p.M + m) * p.N + n] = v;
+        } else {
+            out[batch * p.so.b + m * p.so.r + n * p.so.c] = v;
+        }
+    }
+}
+
+// Adds the split partials in split order and writes the output.
+__global__ __launch_bounds__(kThreads) void split_sum_kernel(const float* __restrict__ partial, float* __restrict__ out,
+                                                             MatmulArgs p, int64_t splits) {
+    const int64_t per_batch = p.M * p.N;
+    const int64_t total = p.batches * per_batch;
+    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < total;
+         idx += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t batch = idx / per_batch;
+        const int64_t mn = idx % per_batch;
+        float v = 0.f;
+        for (int64_t s = 0; s < splits; ++s) v += partial[(batch * splits + s) * per_batch + mn];
+        const int64_t m = mn / p.N;
+        const int64_t n = mn % p.N;
+        out[batch * p.so.b + m * p.so.r + n * p.so.c] = v;
+    }
+}
+
+// ---- rowdot family (f32, small N) ---------------------------------------------------------------
+
+constexpr int kRowdotMaxN = 4;
+
+// One wave per (batch, row); lanes stride along K.
+template <bool AVec>
+__global__ __launch_bounds__(kThreads) void rowdot_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                          float* __restrict__ out, MatmulArgs p) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row_id = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    if (row_id >= p.batches * p.M) return;
+    const int64_t batch = row_id / p.M;
+    const int64_t m = row_id % p.M;
+    const float* arow = a + batch * p.sa.b + m * p.sa.r;
+    const float* bb = b + batch * p.sb.b;
+    float acc[kRowdotMaxN] = {0.f, 0.f, 0.f, 0.f};
+    if (AVec) {
+        const int64_t vecs = p.K / 4;
+        for (int64_t v = lane; v < vecs; v += 64) {
+            const float4 x = *reinterpret_cast<const float4*>(arow + 4 * v);
+            const int64_t k = 4 * v;
+#pragma unroll
+            for (int n = 0; n < kRowdotMaxN; ++n) {
+                if (n < p.N) {
+                    const float* bc = bb + n * p.sb.c;
+                    acc[n] += x.x * bc[k * p.sb.r] + x.y * bc[(k + 1) * p.sb.r] + x.z * bc[(k + 2) * p.sb.r] +
+                              x.w * bc[(k + 3) * p.sb.r];
+                }
+            }
+        }
+        for (int64_t k = vecs * 4 + lane; k < p.K; k += 64) {
+#pragma unroll
+            for (int n = 0; n < kRowdotMaxN; ++n)
+                if (n < p.N) acc[n] += arow[k] * bb[k * p.sb.r + n * p.sb.c];
+        }
+    } else {
+        for (int64_t k = lane; k < p.K; k += 64) {
+            const float x = arow[k * p.sa.c];
+#pragma unroll
+            for (int n = 0; n < kRowdotMaxN; ++n)
+                if (n < p.N) acc[n] += x * bb[k * p.sb.r + n * p.sb.c];
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < kRowdotMaxN; ++n) {
+#pragma unroll
+        for (int off = 32; off > 0; off /= 2) acc[n] += __shfl_xor(acc[n], off, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int n = 0; n < kRowdotMaxN; ++n)
+            if (n < p.N) out[batch * p.so.b + m * p.so.r + n * p.so.c] = acc[n];
+    }
+}
+
+// ---- tiled family (f64 / i64) ----------------------------------------------------------------------
+
+constexpr int kTT = 64;  // tile edge
+constexpr int kTK = 16;
+
+template <typename T> __device__ __forceinline__ T mul_add(T acc, T x, T y) {
+    if constexpr (std::is_same_v<T, int64_t>) return wrap_add(acc, wrap_mul(x, y));
+    else return acc + x * y;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void tiled_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                         T* __restrict__ out, MatmulArgs p) {
+    __shared__ T As[kTK][kTT + 1];
+    __shared__ T Bs[kTK][kTT + 1];
+    const int64_t batch = blockIdx.z;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTT;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTT;
+    a += batch * p.sa.b;
+    b += batch * p.sb.b;
+    const int tr = threadIdx.x / 16;  // 0..15 -> rows tr*4 .. +3
+    const int tc = threadIdx.x % 16;  // cols tc + 16*j
+    T acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = T(0);
+    for (int64_t k0 = 0; k0 < p.K; k0 += kTK) {
+        for (int idx = threadIdx.x; idx < kTK * kTT; idx += kThreads) {
+            const int kk = idx % kTK;
+            const int mm = idx / kTK;
+            const int64_t m = m0 + mm, k = k0 + kk;
+            As[kk][mm] = (m < p.M && k < p.K) ? a[m * p.sa.r + k * p.sa.c] : T(0);
+            const int nn = idx % kTT;
+            const int kb = idx / kTT;
+            const int64_t n = n0 + nn, k2 = k0 + kb;
+            Bs[kb][nn] = (n < p.N && k2 < p.K) ? b[k2 * p.sb.r + n * p.sb.c] : T(0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kTK; ++kk) {
+            T av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = As[kk][tr * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tc + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mul_add(acc[i][j], av[i], bv[j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + tr * 4 + i;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + tc + 16 * j;
+            if (n < p.N) out[batch * p.so.b + m * p.so.r + n * p.so.c] = acc[i][j];
+        }
+    }
+}
+
+// ---- dispatch ----------------------------------------------------------------------------------
+
+bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
+
+template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, float* out, const MatmulArgs& p) {
+    const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN);
+    if (p.batches > 65535) return fail(KD_E_INVALID, "kd_matmul: too many batches");
+    hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(p.batches)),
+                       dim3(kThreads), 0, stream(), a, b, out, p);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <int AMode> int launch_mfma_b(const float* a, const float* b, float* out, const MatmulArgs& p, int bmode) {
+    switch (bmode) {
+    case kRowVec: return launch_mfma<AMode, kRowVec>(a, b, out, p);
+    case kColVec: return launch_mfma<AMode, kColVec>(a, b, out, p);
+    default: return launch_mfma<AMode, kGeneric>(a, b, out, p);
+    }
+}
+
+int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) {
+    const int cus = compute_units();
+    if (p.N <= kRowdotMaxN) {
+        const bool avec = p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && aligned16(a);
+        const int64_t waves = p.batches * p.M;
+        const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+        if (avec) hipLaunchKernelGGL((rowdot_kernel<true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+        else hipLaunchKernelGGL((rowdot_kernel<false>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    if (p.M <= kSkinnyMaxM) {
+        const bool bvec = p.sb.c == 1 && p.sb.r % 4 == 0 && p.sb.b % 4 == 0 && aligned16(b);
+        const int64_t col_blocks = (p.N + kSkinnyCols - 1) / kSkinnyCols;
+        int64_t splits = 1;
+        const int64_t want = 2 * int64_t{cus};
+        if (col_blocks * p.batches < want) {
+            splits = std::min<int64_t>((want + col_blocks * p.batches - 1) / (col_blocks * p.batches),
+                                       std::max<int64_t>(1, p.K / 32));
+        }
+        const int64_t k_chunk = (p.K + splits - 1) / splits;
+        splits = (p.K + k_chunk - 1) / k_chunk;
+        if (splits < 1) splits = 1;
+        float* partial = nullptr;
+        if (splits > 1) {
+            void* ws = nullptr;
+            if (int rc = workspace(&ws, static_cast<size_t>(p.batches * splits * p.M * p.N) * sizeof(float))) return rc;
+            partial = static_cast<float*>(ws);
+        }
+        if (p.batches > 65535 || splits > 65535) return fail(KD_E_INVALID, "kd_matmul: grid too large");
+        const dim3 grid(static_cast<uint32_t>(col_blocks), static_cast<uint32_t>(splits), static_cast<uint32_t>(p.batches));
+#define KD_SKINNY(MT)                                                                                               \
+    if (bvec) hipLaunchKernelGGL((skinny_kernel<MT, true>), grid, dim3(kThreads), 0, stream(), a, b, out, partial, p, k_chunk); \
+    else hipLaunchKernelGGL((skinny_kernel<MT, false>), grid, dim3(kThreads), 0, stream(), a, b, out, partial, p, k_chunk);
+        if (p.M <= 1) { KD_SKINNY(1) }
+        else if (p.M <= 4) { KD_SKINNY(4) }
+        else if (p.M <= 8) { KD_SKINNY(8) }
+        else { KD_SKINNY(16) }
+#undef KD_SKINNY
+        KD_LAUNCH_CHECK();
+        if (splits > 1) {
+            const int64_t total = p.batches * p.M * p.N;
+            const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{cus} * 16);
+            hipLaunchKernelGGL(split_sum_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream(), partial,
+                               out, p, splits);
+            KD_LAUNCH_CHECK();
+        }
+        return KD_OK;
+    }
+    int amode = kGeneric, bmode = kGeneric;
+    if (p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && p.K % 4 == 0 && aligned16(a)) amode = kRowVec;
+    else if (p.sa.r == 1 && p.sa.c % 4 == 0 && p.sa.b % 4 == 0 && p.M % 4 == 0 && aligned16(a)) amode = kColVec;
+    if (p.sb.c == 1 && p.sb.r % 4 == 0 && p.sb.b % 4 == 0 && p.N % 4 == 0 && aligned16(b)) bmode = kRowVec;
+    else if (p.sb.r == 1 && p.sb.c % 4 == 0 && p.sb.b % 4 == 0 && p.K % 4 == 0 && aligned16(b)) bmode = kColVec;
+    switch (amode) {
+    case kRowVec: return launch_mfma_b<kRowVec>(a, b, out, p, bmode);
+    case kColVec: return launch_mfma_b<kColVec>(a, b, out, p, bmode);
+    default: return launch_mfma_b<kGeneric>(a, b, out, p, bmode);
+    }
+}
+
+template <typename T> int matmul_tiled(const T* a, const T* b, T* out, const MatmulArgs& p) {
+    if (p.batches > 65535) return fail(KD_E_INVALID, "kd_matmul: too many batches");
+    const int64_t gm = (p.M + kTT - 1) / kTT, gn = (p.N + kTT - 1) / kTT;
+    if (gm > 65535) return fail(KD_E_INVALID, "kd_matmul: too many rows");
+    hipLaunchKernelGGL((tiled_kernel<T>), dim3(static_cast<uint32_t>(gn), static_cast<uint32_t>(gm), static_cast<uint32_t>(p.batches)),
+                       dim3(kThreads), 0, stream(), a, b, out, p);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void zero_kernel(T* out, MatmulArgs p) {
+    const int64_t total = p.batches * p.M * p.N;
+    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < total;
+         idx += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t batch = idx / (p.M * p.N);
+        const int64_t m = (idx / p.N) % p.M;
+        const int64_t n = idx % p.N;
+        out[batch * p.so.b + m * p.so.r + n * p.so.c] = T(0);
+    }
+}
+
+int dispatch(int dtype, const void* a, const void* b, void* out, const MatmulArgs& p) {
+    if (dtype == KD_BOOL) return fail(KD_E_UNSUPPORTED, "matmul does not support dtype bool");
+    if (dtype_size(dtype) == 0) return fail(KD_E_INVALID, "kd_matmul: unknown dtype");
+    if (p.batches < 0 || p.M < 0 || p.K < 0 || p.N < 0) return fail(KD_E_INVALID, "kd_matmul: negative size");
+    if (p.batches == 0 || p.M == 0 || p.N == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    if (p.K == 0) {
+        // An empty inner dimension yields zeros (the reference's accumulators start at zero).
+        const int64_t total = p.batches * p.M * p.N;
+        const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{compute_units()} * 16);
+        const dim3 grid(static_cast<uint32_t>(blocks));
+        if (dtype == KD_F32) hipLaunchKernelGGL((zero_kernel<float>), grid, dim3(kThreads), 0, stream(), static_cast<float*>(out), p);
+        else if (dtype == KD_F64) hipLaunchKernelGGL((zero_kernel<double>), grid, dim3(kThreads), 0, stream(), static_cast<double*>(out), p);
+        else hipLaunchKernelGGL((zero_kernel<int64_t>), grid, dim3(kThreads), 0, stream(), static_cast<int64_t*>(out), p);
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    switch (dtype) {
+    case KD_F32: return matmul_f32(static_cast<const float*>(a), static_cast<const float*>(b), static_cast<float*>(out), p);
+    case KD_F64: return matmul_tiled<double>(static_cast<const double*>(a), static_cast<const double*>(b), static_cast<double*>(out), p);
+    default: return matmul_tiled<int64_t>(static_cast<const int64_t*>(a), static_cast<const int64_t*>(b), static_cast<int64_t*>(out), p);
+    }
+}
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" int kd_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes) {
+    if (sizes == nullptr) return fail(KD_E_INVALID, "kd_matmul: null sizes");
+    MatmulArgs p;
+    p.batches = sizes->batches;
+    p.M = sizes->rows;
+    p.K = sizes->inner;
+    p.N = sizes->columns;
+    p.sa = {p.M * p.K, p.K, 1};
+    p.sb = {p.K * p.N, p.N, 1};
+    p.so = {p.M * p.N, p.N, 1};
+    return dispatch(dtype, a, b, out, p);
+}
+
+extern "C" int kd_matmul_strided(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                                 const kd_matmul_strides* strides) {
+    if (sizes == nullptr || strides == nullptr) return fail(KD_E_INVALID, "kd_matmul_strided: null argument");
+    MatmulArgs p;
+    p.batches = sizes->batches;
+    p.M = sizes->rows;
+    p.K = sizes->inner;
+    p.N = sizes->columns;
+    p.sa = {strides->a[0], strides->a[1], strides->a[2]};
+    p.sb = {strides->b[0], strides->b[1], strides->b[2]};
+    p.so = {strides->out[0], strides->out[1], strides->out[2]};
+    return dispatch(dtype, a, b, out, p);
+}

@@ -1,0 +1,258 @@
+// kd_reduce.hip - row reductions (sum / max / min) over contiguous chunks for gfx950.
+//
+// Contract of reference src/cuda/kernels.inl:426-445: results[r] = op over
+// data[r*chunk .. (r+1)*chunk). Sum accumulates in double for f32/f64 inputs and stores the
+// input dtype; for i64/bool it accumulates wrapping int64 and stores int64. Max/Min are
+// NaN-propagating (element_functions.h:27-43) and store the input dtype.
+//
+// The reference runs one thread per row (uncoalesced) and, for rows longer than 4096, a host
+// loop of per-row launches with cudaMalloc'd scratch (kernels.inl:278-307). Here:
+//   group  rows of <= 512 elements: a group of G lanes per row (G a power of two), so a wave
+//          covers 64/G rows with coalesced loads; group reduction with cross-lane shuffles.
+//   block  many long rows: one 256-lane workgroup per row, 16-byte loads, wave shuffles + LDS.
+//   split  few long rows: each row is cut into S segments reduced by separate workgroups into
+//          a persistent workspace, then combined in a fixed order by a second launch.
+// Every path reduces in an order fixed by (chunk, rows), so results are deterministic.
+#include <algorithm>
+#include <climits>
+#include <cfloat>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int Op, typename In> struct ReduceTraits;
+
+template <typename In> struct SumAcc {
+    using type = std::conditional_t<std::is_floating_point_v<In>, double, int64_t>;
+};
+
+template <int Op, typename In> struct Combiner {
+    using Acc = std::conditional_t<Op == KD_REDUCE_SUM, typename SumAcc<In>::type, In>;
+    using Out = std::conditional_t<Op == KD_REDUCE_SUM,
+                                   std::conditional_t<std::is_floating_point_v<In>, In, int64_t>, In>;
+    __device__ __forceinline__ static Acc identity() {
+        if constexpr (Op == KD_REDUCE_SUM) {
+            return Acc(0);
+        } else if constexpr (std::is_floating_point_v<In>) {
+            return Op == KD_REDUCE_MAX ? static_cast<In>(-INFINITY) : static_cast<In>(INFINITY);
+        } else if constexpr (std::is_same_v<In, int64_t>) {
+            return Op == KD_REDUCE_MAX ? INT64_MIN : INT64_MAX;
+        } else {
+            return Op == KD_REDUCE_MAX ? uint8_t{0} : uint8_t{255};
+        }
+    }
+    __device__ __forceinline__ static Acc load(In v) { return static_cast<Acc>(v); }
+    __device__ __forceinline__ static Acc combine(Acc a, Acc b) {
+        if constexpr (Op == KD_REDUCE_SUM) {
+            if constexpr (std::is_same_v<Acc, int64_t>) return wrap_add(a, b);
+            else return a + b;
+        } else if constexpr (Op == KD_REDUCE_MAX) {
+            return max_na(a, b);
+        } else {
+            return min_na(a, b);
+        }
+    }
+};
+
+template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
+    if constexpr (std::is_same_v<T, uint8_t>) {
+        return static_cast<uint8_t>(__shfl_xor(static_cast<int>(v), mask, 64));
+    } else {
+        return __shfl_xor(v, mask, 64);
+    }
+}
+
+// Reduces within aligned groups of `G` lanes (G a power of two <= 64).
+template <typename C, int G>
+__device__ __forceinline__ typename C::Acc group_reduce(typename C::Acc v) {
+#pragma unroll
+    for (int m = G / 2; m > 0; m /= 2) v = C::combine(v, shfl_xor(v, m));
+    return v;
+}
+
+// Whole-workgroup reduction; the result is valid in thread 0.
+template <typename C>
+__device__ __forceinline__ typename C::Acc block_reduce(typename C::Acc v) {
+    using Acc = typename C::Acc;
+    __shared__ Acc partial[kBlock / 64];
+    v = group_reduce<C, 64>(v);
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    if (lane == 0) partial[wave] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        v = partial[0];
+#pragma unroll
+        for (int w = 1; w < kBlock / 64; ++w) v = C::combine(v, partial[w]);
+    }
+    __syncthreads();
+    return v;
+}
+
+template <typename In> struct alignas(16) Vec16 {
+    In v[16 / sizeof(In)];
+};
+
+// Reduces data[begin, end) with all lanes of the block; 16-byte loads when `data + begin` is
+// 16-byte aligned. Lane-level order is fixed by the block size.
+template <typename C, typename In>
+__device__ __forceinline__ typename C::Acc block_range(const In* data, int64_t begin, int64_t end) {
+    using Acc = typename C::Acc;
+    constexpr int V = 16 / sizeof(In);
+    Acc acc = C::identity();
+    int64_t i = begin;
+    // Scalar head up to 16-byte alignment.
+    const int64_t misalign = (reinterpret_cast<uintptr_t>(data + begin) % 16) / sizeof(In);
+    if (misalign != 0) {
+        const int64_t head_end = std::min<int64_t>(end, begin + (V - misalign));
+        for (int64_t j = begin + threadIdx.x; j < head_end; j += kBlock) acc = C::combine(acc, C::load(data[j]));
+        i = head_end;
+    }
+    const int64_t vectors = (end - i) / V;
+    const Vec16<In>* vp = reinterpret_cast<const Vec16<In>*>(data + i);
+    for (int64_t k = threadIdx.x; k < vectors; k += kBlock) {
+        const Vec16<In> x = vp[k];
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x.v[e]));
+    }
+    for (int64_t j = i + vectors * V + threadIdx.x; j < end; j += kBlock) acc = C::combine(acc, C::load(data[j]));
+    return block_reduce<C>(acc);
+}
+
+template <typename C, typename In>
+__global__ __launch_bounds__(kBlock) void block_kernel(typename C::Out* results, const In* data, int64_t chunk,
+                                                       int64_t rows) {
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const typename C::Acc v = block_range<C, In>(data + r * chunk, 0, chunk);
+        if (threadIdx.x == 0) results[r] = static_cast<typename C::Out>(v);
+    }
+}
+
+template <typename C, typename In, int G>
+__global__ __launch_bounds__(kBlock) void group_kernel(typename C::Out* results, const In* data, int64_t chunk,
+                                                       int64_t rows) {
+    constexpr int rows_per_block = kBlock / G;
+    const int g = threadIdx.x / G;
+    const int lane = threadIdx.x % G;
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block; base < rows;
+         base += static_cast<int64_t>(gridDim.x) * rows_per_block) {
+        const int64_t r = base + g;
+        typename C::Acc acc = C::identity();
+        if (r < rows) {
+            const In* row = data + r * chunk;
+            for (int64_t j = lane; j < chunk; j += G) acc = C::combine(acc, C::load(row[j]));
+        }
+        acc = group_reduce<C, G>(acc);
+        if (lane == 0 && r < rows) results[r] = static_cast<typename C::Out>(acc);
+    }
+}
+
+template <typename C, typename In>
+__global__ __launch_bounds__(kBlock) void split_kernel(typename C::Acc* partial, const In* data, int64_t chunk,
+                                                       int64_t segments, int64_t segment) {
+    const int64_t r = blockIdx.y;
+    const int64_t s = blockIdx.x;
+    const int64_t begin = s * segment;
+    const int64_t end = std::min<int64_t>(chunk, begin + segment);
+    const typename C::Acc v = block_range<C, In>(data + r * chunk, begin, end);
+    if (threadIdx.x == 0) partial[r * segments + s] = v;
+}
+
+template <typename C>
+__global__ __launch_bounds__(kBlock) void combine_kernel(typename C::Out* results, const typename C::Acc* partial,
+                                                         int64_t segments) {
+    // One workgroup per row: a fixed tree over the segment partials.
+    const int64_t r = blockIdx.x;
+    typename C::Acc acc = C::identity();
+    for (int64_t s = threadIdx.x; s < segments; s += kBlock) acc = C::combine(acc, partial[r * segments + s]);
+    acc = block_reduce<C>(acc);
+    if (threadIdx.x == 0) results[r] = static_cast<typename C::Out>(acc);
+}
+
+template <int Op, typename In> int reduce_typed(void* results, const void* data_v, int64_t chunk, int64_t rows) {
+    using C = Combiner<Op, In>;
+    using Out = typename C::Out;
+    using Acc = typename C::Acc;
+    Out* out = static_cast<Out*>(results);
+    const In* data = static_cast<const In*>(data_v);
+    const int cus = compute_units();
+    if (chunk <= 512) {
+        int g = 1;
+        while (g < 64 && g * 8 < chunk) g *= 2;
+        const int64_t rows_per_block = kBlock / g;
+        const int64_t blocks = std::min<int64_t>((rows + rows_per_block - 1) / rows_per_block, int64_t{cus} * 64);
+        const dim3 grid(static_cast<uint32_t>(std::max<int64_t>(blocks, 1)));
+        switch (g) {
+#define KD_GROUP_CASE(G)                                                                                   \
+    case G:                                                                                                \
+        hipLaunchKernelGGL((group_kernel<C, In, G>), grid, dim3(kBlock), 0, stream(), out, data, chunk, rows); \
+        break;
+            KD_GROUP_CASE(1) KD_GROUP_CASE(2) KD_GROUP_CASE(4) KD_GROUP_CASE(8) KD_GROUP_CASE(16)
+            KD_GROUP_CASE(32) KD_GROUP_CASE(64)
+#undef KD_GROUP_CASE
+        }
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    // Enough rows to fill the device: one workgroup per row.
+    if (rows >= 2 * cus || chunk < 16384) {
+        const int64_t blocks = std::min<int64_t>(rows, int64_t{cus} * 64);
+        hipLaunchKernelGGL((block_kernel<C, In>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream(), out,
+                           data, chunk, rows);
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    // Few long rows: split each row so that about 4 workgroups per CU are busy.
+    int64_t segments = std::max<int64_t>(1, (int64_t{cus} * 4 + rows - 1) / rows);
+    int64_t segment = (chunk + segments - 1) / segments;
+    segment = std::max<int64_t>(segment, 8192);
+    segment = (segment + 63) / 64 * 64;
+    segments = (chunk + segment - 1) / segment;
+    if (rows > 65535) return fail(KD_E_INVALID, "kd_reduce: too many rows for the split path");
+    void* ws = nullptr;
+    if (int rc = workspace(&ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
+    hipLaunchKernelGGL((split_kernel<C, In>), dim3(static_cast<uint32_t>(segments), static_cast<uint32_t>(rows)),
+                       dim3(kBlock), 0, stream(), static_cast<Acc*>(ws), data, chunk, segments, segment);
+    KD_LAUNCH_CHECK();
+    hipLaunchKernelGGL((combine_kernel<C>), dim3(static_cast<uint32_t>(rows)), dim3(kBlock), 0, stream(), out,
+                       static_cast<const Acc*>(ws), segments);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <int Op> int reduce_dtype(int in, void* results, const void* data, int64_t chunk, int64_t rows) {
+    switch (in) {
+    case KD_F32: return reduce_typed<Op, float>(results, data, chunk, rows);
+    case KD_F64: return reduce_typed<Op, double>(results, data, chunk, rows);
+    case KD_I64: return reduce_typed<Op, int64_t>(results, data, chunk, rows);
+    case KD_BOOL: return reduce_typed<Op, uint8_t>(results, data, chunk, rows);
+    }
+    return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
+}
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data, int64_t chunk_size,
+                         int64_t output_count) {
+    (void)out_dtype;  // implied by op and input dtype, as in the reference (kernels.inl:444)
+    if (chunk_size < 0 || output_count < 0) return fail(KD_E_INVALID, "kd_reduce: negative size");
+    if (dtype_size(in_dtype) == 0) return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
+    if (output_count == 0) return KD_OK;
+    if (chunk_size == 0 && op != KD_REDUCE_SUM) return fail(KD_E_INVALID, "kd_reduce: max/min of an empty chunk");
+    if (int rc = ensure_device()) return rc;
+    switch (op) {
+    case KD_REDUCE_SUM: return reduce_dtype<KD_REDUCE_SUM>(in_dtype, results, data, chunk_size, output_count);
+    case KD_REDUCE_MAX: return reduce_dtype<KD_REDUCE_MAX>(in_dtype, results, data, chunk_size, output_count);
+    case KD_REDUCE_MIN: return reduce_dtype<KD_REDUCE_MIN>(in_dtype, results, data, chunk_size, output_count);
+    }
+    return fail(KD_E_INVALID, "kd_reduce: unknown op");
+}

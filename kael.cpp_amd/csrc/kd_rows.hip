@@ -1,0 +1,351 @@
+// kd_rows.hip - fused row kernels: softmax / log_softmax, standardize (+ LayerNorm affine),
+// cross-entropy loss and its gradient, for gfx950.
+//
+// The arithmetic restates kael's CPU row kernels (reference src/ops/nn.cpp:52-129 and
+// 214-240): the row maximum is NaN-propagating, exponentials are evaluated in the element type,
+// their sum is accumulated in double and rounded to the element type before the divide (or
+// log); standardize takes mean and population variance in double. On the device the reference
+// composes these from 5-12 separate elementwise/reduce launches (nn.cpp:153-160, 176-177,
+// 185-187, 253-258); here each is one launch.
+//
+// Rows of up to 1024 elements are held in registers by one wave (one HBM read, one write);
+// longer rows use a 256-lane workgroup per row and re-read the row (L2-resident) per pass.
+#include <algorithm>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename T> __device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) v = max_na(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// Multiply and add without contraction into FMA, so the LayerNorm affine rounds twice, as the
+// reference's separate `* weight` and `+ bias` kernels do.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ double mul_rn(double a, double b) { return __dmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ double add_rn(double a, double b) { return __dadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+__device__ __forceinline__ double sub_rn(double a, double b) { return __dsub_rn(a, b); }
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+__device__ __forceinline__ double div_rn(double a, double b) { return __ddiv_rn(a, b); }
+
+template <typename T> __device__ __forceinline__ T neg_inf() { return static_cast<T>(-INFINITY); }
+
+enum RowOp { kSoftmax = 0, kLogSoftmax = 1, kCrossEntropy = 2, kCrossEntropyGrad = 3 };
+
+// ---- softmax family, one wave per row ---------------------------------------------------------
+
+template <typename T, int V, int Op>
+__global__ __launch_bounds__(kThreads) void softmax_wave_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                                const int64_t* __restrict__ targets,
+                                                                const T* __restrict__ weights, int64_t rows,
+                                                                int64_t cols) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    const T* x = in + row * cols;
+    T v[V];
+    T largest = neg_inf<T>();
+    bool first = true;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int64_t c = lane + 64 * j;
+        v[j] = c < cols ? x[c] : neg_inf<T>();
+        if (c < cols) {
+            largest = first ? v[j] : max_na(largest, v[j]);
+            first = false;
+        }
+    }
+    // Lanes without elements hold -inf, the identity of the NaN-propagating max.
+    largest = wave_max(largest);
+    double total = 0.0;
+    T e[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int64_t c = lane + 64 * j;
+        e[j] = std::exp(sub_rn(v[j], largest));
+        if (c < cols) total += static_cast<double>(e[j]);
+    }
+    total = wave_sum(total);
+    const T denominator = static_cast<T>(total);
+    if constexpr (Op == kSoftmax) {
+        T* y = out + row * cols;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int64_t c = lane + 64 * j;
+            if (c < cols) y[c] = div_rn(e[j], denominator);
+        }
+    } else if constexpr (Op == kLogSoftmax) {
+        const T log_total = std::log(denominator);
+        T* y = out + row * cols;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int64_t c = lane + 64 * j;
+            if (c < cols) y[c] = sub_rn(sub_rn(v[j], largest), log_total);
+        }
+    } else if constexpr (Op == kCrossEntropy) {
+        if (lane == 0) {
+            const int64_t t = targets[row];
+            out[row] = sub_rn(std::log(denominator), sub_rn(x[t], largest));
+        }
+    } else {
+        const T w = weights[row];
+        const int64_t t = targets[row];
+        T* y = out + row * cols;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int64_t c = lane + 64 * j;
+            if (c < cols) {
+                T g = mul_rn(div_rn(e[j], denominator), w);
+                if (c == t) g = sub_rn(g, w);
+                y[c] = g;
+            }
+        }
+    }
+}
+
+// ---- softmax family, one workgroup per row (long rows) -------------------------------------------
+
+template <typename T> __device__ __forceinline__ T block_max(T v, T* scratch) {
+    v = wave_max(v);
+    if (threadIdx.x % 64 == 0) scratch[threadIdx.x / 64] = v;
+    __syncthreads();
+    T r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r = max_na(r, scratch[w]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ double block_sum(double v, double* scratch) {
+    v = wave_sum(v);
+    if (threadIdx.x % 64 == 0) scratch[threadIdx.x / 64] = v;
+    __syncthreads();
+    double r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r += scratch[w];
+    __syncthreads();
+    return r;
+}
+
+template <typename T, int Op>
+__global__ __launch_bounds__(kThreads) void softmax_block_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                                 const int64_t* __restrict__ targets,
+                                                                 const T* __restrict__ weights, int64_t rows,
+                                                                 int64_t cols) {
+    __shared__ T tmax[kThreads / 64];
+    __shared__ double tsum[kThreads / 64];
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const T* x = in + row * cols;
+        T largest = neg_inf<T>();
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) largest = max_na(largest, x[c]);
+        largest = block_max(largest, tmax);
+        double total = 0.0;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) total += static_cast<double>(std::exp(sub_rn(x[c], largest)));
+        total = block_sum(total, tsum);
+        const T denominator = static_cast<T>(total);
+        if constexpr (Op == kSoftmax) {
+            T* y = out + row * cols;
+            for (int64_t c = threadIdx.x; c < cols; c += kThreads) y[c] = div_rn(std::exp(sub_rn(x[c], largest)), denominator);
+        } else if constexpr (Op == kLogSoftmax) {
+            const T log_total = std::log(denominator);
+            T* y = out + row * cols;
+            for (int64_t c = threadIdx.x; c < cols; c += kThreads) y[c] = sub_rn(sub_rn(x[c], largest), log_total);
+        } else if constexpr (Op == kCrossEntropy) {
+            if (threadIdx.x == 0) out[row] = sub_rn(std::log(denominator), sub_rn(x[targets[row]], largest));
+        } else {
+            const T w = weights[row];
+            const int64_t t = targets[row];
+            T* y = out + row * cols;
+            for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+                T g = mul_rn(div_rn(std::exp(sub_rn(x[c], largest)), denominator), w);
+                if (c == t) g = sub_rn(g, w);
+                y[c] = g;
+            }
+        }
+    }
+}
+
+template <typename T, int Op>
+int softmax_family(T* out, const T* in, const int64_t* targets, const T* weights, int64_t rows, int64_t cols) {
+    if (rows == 0 || cols == 0) return KD_OK;
+    const dim3 block(kThreads);
+    if (cols <= 1024) {
+        const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
+        if (rows > int64_t{0xffffffff} * 4) return fail(KD_E_INVALID, "row kernel: too many rows");
+#define KD_WAVE(V) hipLaunchKernelGGL((softmax_wave_kernel<T, V, Op>), grid, block, 0, stream(), out, in, targets, weights, rows, cols)
+        if (cols <= 64) KD_WAVE(1);
+        else if (cols <= 128) KD_WAVE(2);
+        else if (cols <= 256) KD_WAVE(4);
+        else if (cols <= 512) KD_WAVE(8);
+        else KD_WAVE(16);
+#undef KD_WAVE
+    } else {
+        const int64_t blocks = std::min<int64_t>(rows, int64_t{compute_units()} * 32);
+        hipLaunchKernelGGL((softmax_block_kernel<T, Op>), dim3(static_cast<uint32_t>(blocks)), block, 0, stream(), out, in,
+                           targets, weights, rows, cols);
+    }
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+// ---- standardize -------------------------------------------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ T standardized(T x, double center, double scale, const T* w, const T* b, int64_t c) {
+    T y = static_cast<T>((static_cast<double>(x) - center) / scale);
+    if (w != nullptr) y = add_rn(mul_rn(y, w[c]), b[c]);
+    return y;
+}
+
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void standardize_wave_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                                    int64_t rows, int64_t cols, double eps,
+                                                                    const T* __restrict__ w, const T* __restrict__ b) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    const T* x = in + row * cols;
+    T v[V];
+    double total = 0.0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int64_t c = lane + 64 * j;
+        v[j] = c < cols ? x[c] : T(0);
+        total += static_cast<double>(v[j]);
+    }
+    const double center = wave_sum(total) / static_cast<double>(cols);
+    double squares = 0.0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int64_t c = lane + 64 * j;
+        if (c < cols) {
+            const double d = static_cast<double>(v[j]) - center;
+            squares += d * d;
+        }
+    }
+    const double scale = std::sqrt(wave_sum(squares) / static_cast<double>(cols) + eps);
+    T* y = out + row * cols;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int64_t c = lane + 64 * j;
+        if (c < cols) y[c] = standardized(v[j], center, scale, w, b, c);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void standardize_block_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                                     int64_t rows, int64_t cols, double eps,
+                                                                     const T* __restrict__ w, const T* __restrict__ b) {
+    __shared__ double tsum[kThreads / 64];
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const T* x = in + row * cols;
+        double total = 0.0;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) total += static_cast<double>(x[c]);
+        const double center = block_sum(total, tsum) / static_cast<double>(cols);
+        double squares = 0.0;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+            const double d = static_cast<double>(x[c]) - center;
+            squares += d * d;
+        }
+        const double scale = std::sqrt(block_sum(squares, tsum) / static_cast<double>(cols) + eps);
+        T* y = out + row * cols;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) y[c] = standardized(x[c], center, scale, w, b, c);
+    }
+}
+
+template <typename T>
+int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double eps, const T* w, const T* b) {
+    if (rows == 0 || cols == 0) return KD_OK;
+    const dim3 block(kThreads);
+    if (cols <= 1024) {
+        const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
+#define KD_WAVE(V) hipLaunchKernelGGL((standardize_wave_kernel<T, V>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b)
+        if (cols <= 64) KD_WAVE(1);
+        else if (cols <= 128) KD_WAVE(2);
+        else if (cols <= 256) KD_WAVE(4);
+        else if (cols <= 512) KD_WAVE(8);
+        else KD_WAVE(16);
+#undef KD_WAVE
+    } else {
+        const int64_t blocks = std::min<int64_t>(rows, int64_t{compute_units()} * 32);
+        hipLaunchKernelGGL((standardize_block_kernel<T>), dim3(static_cast<uint32_t>(blocks)), block, 0, stream(), out, in,
+                           rows, cols, eps, w, b);
+    }
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+int check_rows(int dtype, int64_t rows, int64_t cols) {
+    if (dtype != KD_F32 && dtype != KD_F64) return fail(KD_E_INVALID, "row kernel: dtype must be f32 or f64");
+    if (rows < 0 || cols < 0) return fail(KD_E_INVALID, "row kernel: negative size");
+    return KD_OK;
+}
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" int kd_softmax_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols, int log_softmax) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (rows == 0 || cols == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32) {
+        return log_softmax ? softmax_family<float, kLogSoftmax>(static_cast<float*>(out), static_cast<const float*>(in), nullptr, nullptr, rows, cols)
+                           : softmax_family<float, kSoftmax>(static_cast<float*>(out), static_cast<const float*>(in), nullptr, nullptr, rows, cols);
+    }
+    return log_softmax ? softmax_family<double, kLogSoftmax>(static_cast<double*>(out), static_cast<const double*>(in), nullptr, nullptr, rows, cols)
+                       : softmax_family<double, kSoftmax>(static_cast<double*>(out), static_cast<const double*>(in), nullptr, nullptr, rows, cols);
+}
+
+extern "C" int kd_standardize_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols, double eps,
+                                   const void* weight, const void* bias) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if ((weight == nullptr) != (bias == nullptr)) return fail(KD_E_INVALID, "kd_standardize_rows: weight and bias go together");
+    if (rows == 0 || cols == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32)
+        return standardize_typed<float>(static_cast<float*>(out), static_cast<const float*>(in), rows, cols, eps,
+                                        static_cast<const float*>(weight), static_cast<const float*>(bias));
+    return standardize_typed<double>(static_cast<double*>(out), static_cast<const double*>(in), rows, cols, eps,
+                                     static_cast<const double*>(weight), static_cast<const double*>(bias));
+}
+
+extern "C" int kd_cross_entropy_rows(int dtype, void* losses, const void* logits, const int64_t* targets, int64_t rows,
+                                     int64_t cols) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (rows == 0) return KD_OK;
+    if (cols == 0) return fail(KD_E_INVALID, "kd_cross_entropy_rows: no classes");
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32)
+        return softmax_family<float, kCrossEntropy>(static_cast<float*>(losses), static_cast<const float*>(logits), targets, nullptr, rows, cols);
+    return softmax_family<double, kCrossEntropy>(static_cast<double*>(losses), static_cast<const double*>(logits), targets, nullptr, rows, cols);
+}
+
+extern "C" int kd_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
+                                     const void* row_weights, int64_t rows, int64_t cols) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (rows == 0) return KD_OK;
+    if (cols == 0) return fail(KD_E_INVALID, "kd_cross_entropy_grad: no classes");
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32)
+        return softmax_family<float, kCrossEntropyGrad>(static_cast<float*>(out), static_cast<const float*>(logits), targets,
+                                                        static_cast<const float*>(row_weights), rows, cols);
+    return softmax_family<double, kCrossEntropyGrad>(static_cast<double*>(out), static_cast<const double*>(logits), targets,
+                                                     static_cast<const double*>(row_weights), rows, cols);
+}

@@ -1,0 +1,115 @@
+// backend_hip.cpp - the drop-in kael device backend for MI355X.
+//
+// Defines every function of `namespace kael::device` (reference include/kael/device_kernels.h:96-116)
+// on top of the C ABI in include/kd_api.h. It takes the place of the backend translation unit
+// that kael's build picks (reference CMakeLists.txt:26-36: src/cuda/backend.cu, backend_fake.cpp
+// or backend_none.cpp): compile this file with kael's include directory and link libkd.so.
+// Failures become kael::Error carrying the backend's message (as KAEL_CUDA_CHECK does in
+// reference src/cuda/backend.cu:17-32); release() never throws (backend.cu:88-90).
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "kael/device_kernels.h"
+#include "kael/error.h"
+
+#include "kd_api.h"
+
+namespace kael::device {
+
+namespace {
+
+// The C mirrors must be byte-for-byte the reference structs: they are passed by pointer.
+static_assert(sizeof(kd_element_layout) == sizeof(ElementLayout));
+static_assert(offsetof(kd_element_layout, count) == offsetof(ElementLayout, count));
+static_assert(offsetof(kd_element_layout, shape) == offsetof(ElementLayout, shape));
+static_assert(offsetof(kd_element_layout, strides) == offsetof(ElementLayout, strides));
+static_assert(offsetof(kd_element_layout, base) == offsetof(ElementLayout, base));
+static_assert(sizeof(kd_index_layout) == sizeof(IndexLayout));
+static_assert(offsetof(kd_index_layout, shape) == offsetof(IndexLayout, shape));
+static_assert(offsetof(kd_index_layout, source_strides) == offsetof(IndexLayout, source_strides));
+static_assert(sizeof(kd_matmul_sizes) == sizeof(MatmulSizes));
+static_assert(static_cast<int>(DType::F32) == KD_F32 && static_cast<int>(DType::Bool) == KD_BOOL);
+static_assert(static_cast<int>(ElementOp::MaskedFill) == KD_OP_MASKED_FILL);
+static_assert(static_cast<int>(ReduceOp::Min) == KD_REDUCE_MIN);
+
+void check(int status, const char* what) {
+    if (status != KD_OK) {
+        throw Error(std::string("MI355X backend: ") + what + " failed: " + kd_last_error());
+    }
+}
+
+const kd_element_layout* c_layout(const ElementLayout& layout) {
+    return reinterpret_cast<const kd_element_layout*>(&layout);
+}
+
+} // namespace
+
+bool available() { return kd_available() != 0; }
+
+void synchronize() { check(kd_synchronize(), "synchronize"); }
+
+std::byte* allocate(std::int64_t bytes) {
+    void* block = nullptr;
+    check(kd_malloc(&block, bytes), "allocate");
+    return static_cast<std::byte*>(block);
+}
+
+void release(std::byte* block) noexcept { kd_free(block); }
+
+void copy_to_device(std::byte* target, const std::byte* source, std::int64_t bytes) {
+    check(kd_copy_h2d(target, source, bytes), "copy_to_device");
+}
+
+void copy_to_host(std::byte* target, const std::byte* source, std::int64_t bytes) {
+    check(kd_copy_d2h(target, source, bytes), "copy_to_host");
+}
+
+void copy_within_device(std::byte* target, const std::byte* source, std::int64_t bytes) {
+    check(kd_copy_d2d(target, source, bytes), "copy_within_device");
+}
+
+void fill(DType dtype, std::byte* target, std::int64_t count, const void* value) {
+    check(kd_fill(static_cast<int>(dtype), target, count, value), "fill");
+}
+
+void convert(DType out, DType in, const ElementLayout& layout) {
+    check(kd_convert(static_cast<int>(out), static_cast<int>(in), c_layout(layout)), "convert");
+}
+
+void elementwise(ElementOp op, DType out, DType in, const ElementLayout& layout, ElementParameters parameters) {
+    kd_element_parameters p;
+    p.reals[0] = parameters.reals[0];
+    p.reals[1] = parameters.reals[1];
+    p.integers[0] = parameters.integers[0];
+    p.integers[1] = parameters.integers[1];
+    check(kd_elementwise(static_cast<int>(op), static_cast<int>(out), static_cast<int>(in), c_layout(layout), p),
+          "elementwise");
+}
+
+void reduce(ReduceOp op, DType out, DType in, std::byte* results, const std::byte* data, std::int64_t chunk_size,
+            std::int64_t output_count) {
+    check(kd_reduce(static_cast<int>(op), static_cast<int>(out), static_cast<int>(in), results, data, chunk_size,
+                    output_count),
+          "reduce");
+}
+
+void matmul(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes) {
+    const kd_matmul_sizes s{sizes.batches, sizes.rows, sizes.inner, sizes.columns};
+    check(kd_matmul(static_cast<int>(dtype), a, b, out, &s), "matmul");
+}
+
+void gather(DType dtype, std::byte* out, const std::byte* data, const std::int64_t* indices,
+            const IndexLayout& layout) {
+    check(kd_gather(static_cast<int>(dtype), out, data, indices, reinterpret_cast<const kd_index_layout*>(&layout)),
+          "gather");
+}
+
+void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, const std::byte* source,
+                 const IndexLayout& layout) {
+    check(kd_scatter_add(static_cast<int>(dtype), data, indices, source,
+                         reinterpret_cast<const kd_index_layout*>(&layout)),
+          "scatter_add");
+}
+
+} // namespace kael::device

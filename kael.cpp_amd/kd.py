@@ -1,0 +1,246 @@
+"""ctypes binding of the gfx950 backend's C ABI (include/kd_api.h).
+
+`load()` opens kael.cpp_amd/lib/libkd.so and returns a `Backend` whose methods raise
+`KdError` on a non-zero status. There is no fallback: a missing library or device is an error.
+The same structure classes describe layouts for the test oracle, whose entry points share
+these signatures.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "lib" / "libkd.so"
+
+MAX_DIMS = 8
+MAX_OPERANDS = 4
+
+F32, F64, I64, BOOL = 0, 1, 2, 3
+NUMPY_DTYPE = {F32: np.float32, F64: np.float64, I64: np.int64, BOOL: np.uint8}
+DTYPE_OF = {np.dtype(np.float32): F32, np.dtype(np.float64): F64, np.dtype(np.int64): I64,
+            np.dtype(np.uint8): BOOL, np.dtype(np.bool_): BOOL}
+
+OPS = [
+    "PLUS", "MINUS", "TIMES", "DIVIDES", "POWER", "MAXIMUM", "MINIMUM", "EQUAL", "NOT_EQUAL",
+    "LESS", "LESS_EQUAL", "GREATER", "GREATER_EQUAL", "LOGICAL_AND", "LOGICAL_OR",
+    "LOGICAL_XOR", "IS_ZERO", "NEGATE", "ABSOLUTE", "SIGN", "EXP", "LOG", "LOG1P", "EXPM1",
+    "SQRT", "RSQRT", "SIN", "COS", "TANH", "SIGMOID", "RELU", "GELU_EXACT", "GELU_TANH",
+    "CLAMP", "WHERE", "MASKED_FILL",
+]
+OP = {name: i for i, name in enumerate(OPS)}
+OP["GELU_EXACT_BACKWARD"] = 64
+OP["GELU_TANH_BACKWARD"] = 65
+COMPARE_OPS = {OP[n] for n in ("EQUAL", "NOT_EQUAL", "LESS", "LESS_EQUAL", "GREATER",
+                               "GREATER_EQUAL", "LOGICAL_AND", "LOGICAL_OR", "LOGICAL_XOR")}
+FLOATING_OPS = {OP[n] for n in ("EXP", "LOG", "LOG1P", "EXPM1", "SQRT", "RSQRT", "SIN", "COS",
+                                "TANH", "SIGMOID", "GELU_EXACT", "GELU_TANH",
+                                "GELU_EXACT_BACKWARD", "GELU_TANH_BACKWARD")}
+REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
+
+
+def op_inputs(op: int) -> int:
+    if op <= OP["LOGICAL_XOR"]:
+        return 2
+    if op == OP["WHERE"]:
+        return 3
+    if op in (OP["MASKED_FILL"], OP["GELU_EXACT_BACKWARD"], OP["GELU_TANH_BACKWARD"]):
+        return 2
+    return 1
+
+
+class KdError(RuntimeError):
+    pass
+
+
+class ElementParameters(Structure):
+    _fields_ = [("reals", c_double * 2), ("integers", c_int64 * 2)]
+
+
+class ElementLayout(Structure):
+    _fields_ = [("dims", c_int32), ("operands", c_int32), ("count", c_int64),
+                ("shape", c_int64 * MAX_DIMS), ("strides", (c_int64 * MAX_DIMS) * MAX_OPERANDS),
+                ("base", c_void_p * MAX_OPERANDS)]
+
+
+class IndexLayout(Structure):
+    _fields_ = [("dims", c_int32), ("axis", c_int32), ("count", c_int64),
+                ("shape", c_int64 * MAX_DIMS), ("data_strides", c_int64 * MAX_DIMS),
+                ("index_strides", c_int64 * MAX_DIMS), ("source_strides", c_int64 * MAX_DIMS)]
+
+
+class MatmulSizes(Structure):
+    _fields_ = [("batches", c_int64), ("rows", c_int64), ("inner", c_int64), ("columns", c_int64)]
+
+
+class MatmulStrides(Structure):
+    _fields_ = [("a", c_int64 * 3), ("b", c_int64 * 3), ("out", c_int64 * 3)]
+
+
+assert ctypes.sizeof(ElementLayout) == 368
+assert ctypes.sizeof(IndexLayout) == 272
+
+
+def params(reals=(0.0, 0.0), integers=(0, 0)) -> ElementParameters:
+    p = ElementParameters()
+    p.reals[0], p.reals[1] = float(reals[0]), float(reals[1])
+    p.integers[0], p.integers[1] = int(integers[0]), int(integers[1])
+    return p
+
+
+# name -> (restype, argtypes); shared by the backend (prefix kd_) and the oracle (oracle_).
+SIGNATURES = {
+    "fill": (c_int, [c_int, c_void_p, c_int64, c_void_p]),
+    "convert": (c_int, [c_int, c_int, POINTER(ElementLayout)]),
+    "elementwise": (c_int, [c_int, c_int, c_int, POINTER(ElementLayout), ElementParameters]),
+    "reduce": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
+    "scatter_add": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
+    "softmax_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int]),
+    "standardize_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
+    "cross_entropy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
+    "cross_entropy_grad": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
+    "matmul_strided": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides)]),
+    "layout_build": (c_int, [POINTER(ElementLayout), c_int, POINTER(c_int), POINTER(c_int64),
+                             POINTER(c_int64), POINTER(c_int), POINTER(c_void_p)]),
+}
+BACKEND_ONLY = {
+    "last_error": (c_char_p, []),
+    "available": (c_int, []),
+    "synchronize": (c_int, []),
+    "set_stream": (c_int, [c_void_p]),
+    "get_stream": (c_void_p, []),
+    "malloc": (c_int, [POINTER(c_void_p), c_int64]),
+    "free": (None, [c_void_p]),
+    "copy_h2d": (c_int, [c_void_p, c_void_p, c_int64]),
+    "copy_d2h": (c_int, [c_void_p, c_void_p, c_int64]),
+    "copy_d2d": (c_int, [c_void_p, c_void_p, c_int64]),
+    "matmul": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes)]),
+    "event_create": (c_int, [POINTER(c_void_p)]),
+    "event_destroy": (c_int, [c_void_p]),
+    "event_record": (c_int, [c_void_p]),
+    "event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
+    "device_info": (c_int, [POINTER(c_int), POINTER(c_int), ctypes.c_char_p, c_int]),
+}
+
+# Every symbol include/kd_api.h declares.
+EXPORTED = sorted({"kd_" + n for n in SIGNATURES} | {"kd_" + n for n in BACKEND_ONLY})
+
+
+def bind(lib: ctypes.CDLL, prefix: str, names: dict) -> None:
+    for name, (restype, argtypes) in names.items():
+        fn = getattr(lib, prefix + name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+
+
+class Backend:
+    """The loaded library plus thin checked wrappers."""
+
+    def __init__(self, path: Path = LIB_PATH):
+        if not Path(path).is_file():
+            raise KdError(f"{path} is missing: build it with `python kael.cpp_amd/build.py`")
+        self.lib = ctypes.CDLL(str(path), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+        bind(self.lib, "kd_", SIGNATURES)
+        bind(self.lib, "kd_", BACKEND_ONLY)
+        self.path = Path(path)
+
+    def error(self) -> str:
+        msg = self.lib.kd_last_error()
+        return msg.decode() if msg else ""
+
+    def check(self, rc: int, what: str = "") -> None:
+        if rc != 0:
+            raise KdError(f"{what} failed ({rc}): {self.error()}")
+
+    def call(self, name: str, *args) -> None:
+        self.check(getattr(self.lib, "kd_" + name)(*args), "kd_" + name)
+
+    # -- memory --
+    def malloc(self, nbytes: int) -> int:
+        p = c_void_p()
+        self.check(self.lib.kd_malloc(ctypes.byref(p), int(nbytes)), "kd_malloc")
+        return p.value or 0
+
+    def free(self, ptr: int) -> None:
+        self.lib.kd_free(c_void_p(ptr))
+
+    def to_device(self, arr: np.ndarray) -> "DeviceArray":
+        arr = np.ascontiguousarray(arr)
+        buf = DeviceArray(self, arr.shape, arr.dtype)
+        self.check(self.lib.kd_copy_h2d(c_void_p(buf.ptr), arr.ctypes.data_as(c_void_p), arr.nbytes), "kd_copy_h2d")
+        return buf
+
+    def empty(self, shape, dtype) -> "DeviceArray":
+        return DeviceArray(self, tuple(shape), np.dtype(dtype))
+
+    def synchronize(self) -> None:
+        self.check(self.lib.kd_synchronize(), "kd_synchronize")
+
+    def device_info(self) -> dict:
+        cus, clk = c_int(), c_int()
+        arch = ctypes.create_string_buffer(64)
+        self.check(self.lib.kd_device_info(ctypes.byref(cus), ctypes.byref(clk), arch, 64), "kd_device_info")
+        return {"compute_units": cus.value, "clock_khz": clk.value, "arch": arch.value.decode()}
+
+
+class DeviceArray:
+    """A device allocation with a numpy-like shape/dtype; freed when collected."""
+
+    def __init__(self, backend: Backend, shape, dtype):
+        self.backend = backend
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self.ptr = backend.malloc(max(self.nbytes, 1))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            self.backend.check(self.backend.lib.kd_copy_d2h(out.ctypes.data_as(c_void_p), c_void_p(self.ptr), self.nbytes),
+                               "kd_copy_d2h")
+        return out
+
+    def upload(self, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr, dtype=self.dtype)
+        assert arr.nbytes == self.nbytes
+        self.backend.check(self.backend.lib.kd_copy_h2d(c_void_p(self.ptr), arr.ctypes.data_as(c_void_p), arr.nbytes),
+                           "kd_copy_h2d")
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                self.backend.free(self.ptr)
+                self.ptr = 0
+        except Exception:
+            pass
+
+
+_BACKEND: Backend | None = None
+
+
+def load() -> Backend:
+    global _BACKEND
+    if _BACKEND is None:
+        _BACKEND = Backend()
+    return _BACKEND
+
+
+def element_layout(shape, strides_bytes, bases) -> ElementLayout:
+    """An ElementLayout from explicit dims: shape (d), per-operand byte strides [ops][d]."""
+    lay = ElementLayout()
+    lay.dims = len(shape)
+    lay.operands = len(bases)
+    lay.count = int(np.prod(shape, dtype=np.int64)) if len(shape) else 1
+    for d, s in enumerate(shape):
+        lay.shape[d] = int(s)
+    for op, st in enumerate(strides_bytes):
+        for d, s in enumerate(st):
+            lay.strides[op][d] = int(s)
+    for op, b in enumerate(bases):
+        lay.base[op] = b
+    return lay

@@ -1,0 +1,886 @@
+/*
+ * kd_oracle.c - TEST INFRASTRUCTURE ONLY: the checker, never the product.
+ *
+ * A plain-C CPU restatement of the reference device semantics (JetBerri/kael.cpp 1.0.1):
+ *   - cast rules             src/cuda/kernels.inl:5-13, include/kael/dtype.h:130-155,
+ *                            src/internal/element_functions.h:75-90
+ *   - element ops (36)       src/internal/element_functions.h:27-323, dispatch kernels.inl:333-424
+ *   - strided addressing     src/cuda/kernels.inl:15-28 (locate)
+ *   - fill / convert         src/cuda/kernels.inl:53-57, 316-331
+ *   - reduce                 src/cuda/kernels.inl:59-134, 278-307, 426-445
+ *   - matmul                 src/cuda/kernels.inl:136-177
+ *   - gather / scatter_add   src/cuda/kernels.inl:185-221, 447-465
+ *   - row kernels            src/ops/nn.cpp:52-129, 214-240; src/nn/layers.cpp:60-68
+ *   - GELU slopes            src/autograd/functions_math.cpp:35-46, 221-231
+ *   - layout planning        src/iterator.cpp:12-63, 112-132, 152-172
+ *
+ * Deliberate choices where the reference is undefined: integer division by zero yields 0 and
+ * INT64_MIN / -1 yields INT64_MIN (the reference host would trap). Floating ops on integer
+ * dtypes, Max/Min of an empty chunk and bool scatter_add are errors (the reference host never
+ * issues them).
+ */
+#include "kd_oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static _Thread_local char g_error[256];
+
+static int fail(const char* message) {
+    snprintf(g_error, sizeof g_error, "%s", message);
+    return KD_E_INVALID;
+}
+
+const char* oracle_last_error(void) { return g_error; }
+
+typedef unsigned char u8;
+
+/* ---- scalar helpers ----------------------------------------------------------------- */
+
+/* wrapping_add / _subtract / _multiply: element_functions.h:48-73 */
+static int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+static int64_t wsub(int64_t a, int64_t b) { return (int64_t)((uint64_t)a - (uint64_t)b); }
+static int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+
+/* saturating_cast<int64_t>: element_functions.h:76-90, dtype.h:132-144 */
+static int64_t sat_i64(double v) {
+    if (v != v) return 0;
+    if (v <= -9223372036854775808.0) return INT64_MIN;
+    if (v >= 9223372036854775808.0) return INT64_MAX;
+    return (int64_t)v;
+}
+
+/* integer_power: element_functions.h:92-119 */
+static int64_t ipow(int64_t base, int64_t exponent) {
+    if (exponent < 0) {
+        if (base == 1) return base;
+        if (base == -1) return exponent % 2 == 0 ? 1 : base;
+        return 0;
+    }
+    uint64_t result = 1, factor = (uint64_t)base;
+    while (exponent > 0) {
+        if (exponent % 2 == 1) result = result * factor;
+        exponent /= 2;
+        if (exponent > 0) factor = factor * factor;
+    }
+    return (int64_t)result;
+}
+
+static int64_t idiv(int64_t a, int64_t b) {
+    if (b == 0) return 0;
+    if (b == -1) return wsub(0, a);
+    return a / b;
+}
+
+/* nan_aware_max / _min: element_functions.h:27-43 */
+static double fmaxna(double a, double b) {
+    if (isnan(a) || isnan(b)) return isnan(a) ? a : b;
+    return a < b ? b : a;
+}
+static double fminna(double a, double b) {
+    if (isnan(a) || isnan(b)) return isnan(a) ? a : b;
+    return b < a ? b : a;
+}
+static float fmaxnaf(float a, float b) {
+    if (isnan(a) || isnan(b)) return isnan(a) ? a : b;
+    return a < b ? b : a;
+}
+static float fminnaf(float a, float b) {
+    if (isnan(a) || isnan(b)) return isnan(a) ? a : b;
+    return b < a ? b : a;
+}
+
+/* ---- element functors, evaluated per dtype ------------------------------------------ */
+
+static const float kSqrt2F = 1.41421356237309504880f;
+static const double kSqrt2 = 1.41421356237309504880;
+static const float kPiF = 3.14159265358979323846f;
+static const double kPi = 3.14159265358979323846;
+
+/* Float unary ops (run_floating, kernels.inl:382-407) in float precision. */
+static float unary_f32(int op, float x) {
+    switch (op) {
+    case KD_OP_EXP: return expf(x);
+    case KD_OP_LOG: return logf(x);
+    case KD_OP_LOG1P: return log1pf(x);
+    case KD_OP_EXPM1: return expm1f(x);
+    case KD_OP_SQRT: return sqrtf(x);
+    case KD_OP_RSQRT: return 1 / sqrtf(x);
+    case KD_OP_SIN: return sinf(x);
+    case KD_OP_COS: return cosf(x);
+    case KD_OP_TANH: return tanhf(x);
+    case KD_OP_SIGMOID:
+        if (x >= 0) return 1 / (1 + expf(-x));
+        else {
+            const float e = expf(x);
+            return e / (1 + e);
+        }
+    case KD_OP_GELU_EXACT: return 0.5f * x * (1 + erff(x / kSqrt2F));
+    case KD_OP_GELU_TANH: {
+        const float scale = sqrtf(2 / kPiF);
+        return 0.5f * x * (1 + tanhf(scale * (x + 0.044715f * x * x * x)));
+    }
+    }
+    return 0.0f;
+}
+
+static double unary_f64(int op, double x) {
+    switch (op) {
+    case KD_OP_EXP: return exp(x);
+    case KD_OP_LOG: return log(x);
+    case KD_OP_LOG1P: return log1p(x);
+    case KD_OP_EXPM1: return expm1(x);
+    case KD_OP_SQRT: return sqrt(x);
+    case KD_OP_RSQRT: return 1 / sqrt(x);
+    case KD_OP_SIN: return sin(x);
+    case KD_OP_COS: return cos(x);
+    case KD_OP_TANH: return tanh(x);
+    case KD_OP_SIGMOID:
+        if (x >= 0) return 1 / (1 + exp(-x));
+        else {
+            const double e = exp(x);
+            return e / (1 + e);
+        }
+    case KD_OP_GELU_EXACT: return 0.5 * x * (1 + erf(x / kSqrt2));
+    case KD_OP_GELU_TANH: {
+        const double scale = sqrt(2 / kPi);
+        return 0.5 * x * (1 + tanh(scale * (x + 0.044715 * x * x * x)));
+    }
+    }
+    return 0.0;
+}
+
+/* gelu_exact_slope / gelu_tanh_slope: functions_math.cpp:35-46 */
+static float gelu_slope_f32(int tanh_form, float x) {
+    if (!tanh_form) {
+        const float density = expf(-x * x / 2) / sqrtf(2 * kPiF);
+        return 0.5f * (1 + erff(x / kSqrt2F)) + x * density;
+    }
+    const float scale = sqrtf(2 / kPiF);
+    const float c = 0.044715f;
+    const float s = tanhf(scale * (x + c * x * x * x));
+    return 0.5f * (1 + s) + 0.5f * x * (1 - s * s) * scale * (1 + 3 * c * x * x);
+}
+
+static double gelu_slope_f64(int tanh_form, double x) {
+    if (!tanh_form) {
+        const double density = exp(-x * x / 2) / sqrt(2 * kPi);
+        return 0.5 * (1 + erf(x / kSqrt2)) + x * density;
+    }
+    const double scale = sqrt(2 / kPi);
+    const double c = 0.044715;
+    const double s = tanh(scale * (x + c * x * x * x));
+    return 0.5 * (1 + s) + 0.5 * x * (1 - s * s) * scale * (1 + 3 * c * x * x);
+}
+
+static int is_compare(int op) { return op >= KD_OP_EQUAL && op <= KD_OP_LOGICAL_XOR; }
+static int is_floating_only(int op) {
+    return (op >= KD_OP_EXP && op <= KD_OP_SIGMOID) || op == KD_OP_GELU_EXACT ||
+           op == KD_OP_GELU_TANH || op == KD_OP_GELU_EXACT_BACKWARD ||
+           op == KD_OP_GELU_TANH_BACKWARD;
+}
+static int input_count(int op) {
+    if (op <= KD_OP_LOGICAL_XOR) return 2;
+    if (op == KD_OP_WHERE) return 3;
+    if (op == KD_OP_MASKED_FILL || op == KD_OP_GELU_EXACT_BACKWARD ||
+        op == KD_OP_GELU_TANH_BACKWARD)
+        return 2;
+    return 1;
+}
+
+/* Comparison (run_compare, kernels.inl:270-276): the functor returns bool. */
+#define COMPARE_BODY(a, b)                                                                   \
+    switch (op) {                                                                            \
+    case KD_OP_EQUAL: return (a) == (b);                                                     \
+    case KD_OP_NOT_EQUAL: return (a) != (b);                                                 \
+    case KD_OP_LESS: return (a) < (b);                                                       \
+    case KD_OP_LESS_EQUAL: return (a) <= (b);                                                \
+    case KD_OP_GREATER: return (a) > (b);                                                    \
+    case KD_OP_GREATER_EQUAL: return (a) >= (b);                                             \
+    case KD_OP_LOGICAL_AND: return (a) != 0 && (b) != 0;                                     \
+    case KD_OP_LOGICAL_OR: return (a) != 0 || (b) != 0;                                      \
+    case KD_OP_LOGICAL_XOR: return ((a) != 0) != ((b) != 0);                                 \
+    }                                                                                        \
+    return 0;
+
+static u8 compare_f32(int op, float a, float b) { COMPARE_BODY(a, b) }
+static u8 compare_f64(int op, double a, double b) { COMPARE_BODY(a, b) }
+static u8 compare_i64(int op, int64_t a, int64_t b) { COMPARE_BODY(a, b) }
+static u8 compare_u8(int op, u8 a, u8 b) { COMPARE_BODY(a, b) }
+
+/* Same-dtype ops on float (run_same, kernels.inl:254-260 + functors). */
+static float same_f32(int op, const float* in, const kd_element_parameters* p) {
+    const float x = in[0];
+    switch (op) {
+    case KD_OP_PLUS: return in[0] + in[1];
+    case KD_OP_MINUS: return in[0] - in[1];
+    case KD_OP_TIMES: return in[0] * in[1];
+    case KD_OP_DIVIDES: return in[0] / in[1];
+    case KD_OP_POWER: return powf(in[0], in[1]);
+    case KD_OP_MAXIMUM: return fmaxnaf(in[0], in[1]);
+    case KD_OP_MINIMUM: return fminnaf(in[0], in[1]);
+    case KD_OP_IS_ZERO: return x == 0.0f ? 1.0f : 0.0f;
+    case KD_OP_NEGATE: return -x;
+    case KD_OP_ABSOLUTE: return fabsf(x);
+    case KD_OP_SIGN: return (float)(x > 0 ? 1 : (x < 0 ? -1 : 0));
+    case KD_OP_RELU: return x < 0 ? 0.0f : x;
+    case KD_OP_CLAMP: {
+        const float low = (float)p->reals[0], high = (float)p->reals[1];
+        if (isnan(low) || isnan(high)) return NAN;
+        const float raised = x < low ? low : x;
+        return raised > high ? high : raised;
+    }
+    case KD_OP_WHERE: return in[0] != 0 ? in[1] : in[2];
+    case KD_OP_MASKED_FILL: return in[1] != 0 ? (float)p->reals[0] : in[0];
+    case KD_OP_GELU_EXACT_BACKWARD: return in[1] * gelu_slope_f32(0, in[0]);
+    case KD_OP_GELU_TANH_BACKWARD: return in[1] * gelu_slope_f32(1, in[0]);
+    }
+    return unary_f32(op, x);
+}
+
+static double same_f64(int op, const double* in, const kd_element_parameters* p) {
+    const double x = in[0];
+    switch (op) {
+    case KD_OP_PLUS: return in[0] + in[1];
+    case KD_OP_MINUS: return in[0] - in[1];
+    case KD_OP_TIMES: return in[0] * in[1];
+    case KD_OP_DIVIDES: return in[0] / in[1];
+    case KD_OP_POWER: return pow(in[0], in[1]);
+    case KD_OP_MAXIMUM: return fmaxna(in[0], in[1]);
+    case KD_OP_MINIMUM: return fminna(in[0], in[1]);
+    case KD_OP_IS_ZERO: return x == 0.0 ? 1.0 : 0.0;
+    case KD_OP_NEGATE: return -x;
+    case KD_OP_ABSOLUTE: return fabs(x);
+    case KD_OP_SIGN: return (double)(x > 0 ? 1 : (x < 0 ? -1 : 0));
+    case KD_OP_RELU: return x < 0 ? 0.0 : x;
+    case KD_OP_CLAMP: {
+        const double low = p->reals[0], high = p->reals[1];
+        if (isnan(low) || isnan(high)) return NAN;
+        const double raised = x < low ? low : x;
+        return raised > high ? high : raised;
+    }
+    case KD_OP_WHERE: return in[0] != 0 ? in[1] : in[2];
+    case KD_OP_MASKED_FILL: return in[1] != 0 ? p->reals[0] : in[0];
+    case KD_OP_GELU_EXACT_BACKWARD: return in[1] * gelu_slope_f64(0, in[0]);
+    case KD_OP_GELU_TANH_BACKWARD: return in[1] * gelu_slope_f64(1, in[0]);
+    }
+    return unary_f64(op, x);
+}
+
+static int64_t same_i64(int op, const int64_t* in, const kd_element_parameters* p) {
+    const int64_t x = in[0];
+    switch (op) {
+    case KD_OP_PLUS: return wadd(in[0], in[1]);
+    case KD_OP_MINUS: return wsub(in[0], in[1]);
+    case KD_OP_TIMES: return wmul(in[0], in[1]);
+    case KD_OP_DIVIDES: return idiv(in[0], in[1]);
+    case KD_OP_POWER: return ipow(in[0], in[1]);
+    case KD_OP_MAXIMUM: return in[0] < in[1] ? in[1] : in[0];
+    case KD_OP_MINIMUM: return in[1] < in[0] ? in[1] : in[0];
+    case KD_OP_IS_ZERO: return x == 0;
+    case KD_OP_NEGATE: return wsub(0, x);
+    case KD_OP_ABSOLUTE: return x < 0 ? wsub(0, x) : x;
+    case KD_OP_SIGN: return x > 0 ? 1 : (x < 0 ? -1 : 0);
+    case KD_OP_RELU: return x < 0 ? 0 : x;
+    case KD_OP_CLAMP: {
+        const int64_t low = p->integers[0], high = p->integers[1];
+        const int64_t raised = x < low ? low : x;
+        return raised > high ? high : raised;
+    }
+    case KD_OP_WHERE: return in[0] != 0 ? in[1] : in[2];
+    case KD_OP_MASKED_FILL: return in[1] != 0 ? p->integers[0] : in[0];
+    }
+    return 0;
+}
+
+/* bool (uint8) arithmetic: operands promote to int and the result is normalised
+ * by cast_value<uint8_t> (kernels.inl:6-7). */
+static u8 same_u8(int op, const u8* in, const kd_element_parameters* p) {
+    const int a = in[0];
+    int r = 0;
+    switch (op) {
+    case KD_OP_PLUS: r = in[0] + in[1]; break;
+    case KD_OP_MINUS: r = in[0] - in[1]; break;
+    case KD_OP_TIMES: r = in[0] * in[1]; break;
+    case KD_OP_DIVIDES: r = in[1] == 0 ? 0 : in[0] / in[1]; break;
+    case KD_OP_MAXIMUM: r = in[0] < in[1] ? in[1] : in[0]; break;
+    case KD_OP_MINIMUM: r = in[1] < in[0] ? in[1] : in[0]; break;
+    case KD_OP_IS_ZERO: r = a == 0; break;
+    case KD_OP_NEGATE: r = -a; break;
+    case KD_OP_ABSOLUTE: r = a; break;
+    case KD_OP_SIGN: r = a; break;
+    case KD_OP_RELU: r = a; break;
+    case KD_OP_CLAMP: {
+        const u8 low = (u8)p->integers[0], high = (u8)p->integers[1];
+        const u8 raised = in[0] < low ? low : in[0];
+        r = raised > high ? high : raised;
+        break;
+    }
+    case KD_OP_WHERE: r = in[0] != 0 ? in[1] : in[2]; break;
+    case KD_OP_MASKED_FILL: r = in[1] != 0 ? (u8)p->integers[0] : in[0]; break;
+    }
+    return r != 0;
+}
+
+/* ---- layouts -------------------------------------------------------------------------- */
+
+static int64_t dtype_size(int dtype) {
+    switch (dtype) {
+    case KD_F32: return 4;
+    case KD_F64: return 8;
+    case KD_I64: return 8;
+    case KD_BOOL: return 1;
+    }
+    return 0;
+}
+
+/* locate: kernels.inl:15-28 */
+static void locate(const kd_element_layout* l, int64_t element, char** pointers) {
+    int64_t offsets[KD_MAX_OPERANDS] = {0, 0, 0, 0};
+    int64_t remaining = element;
+    for (int dim = l->dims - 1; dim >= 0; --dim) {
+        const int64_t position = remaining % l->shape[dim];
+        remaining /= l->shape[dim];
+        for (int op = 0; op < l->operands; ++op) offsets[op] += position * l->strides[op][dim];
+    }
+    for (int op = 0; op < l->operands; ++op) pointers[op] = (char*)l->base[op] + offsets[op];
+}
+
+static int check_layout(const kd_element_layout* l, int operands) {
+    if (l->dims < 1 || l->dims > KD_MAX_DIMS) return fail("layout dims out of range");
+    if (l->operands != operands) return fail("layout operand count does not match the op");
+    return KD_OK;
+}
+
+static double read_as_double(int dtype, const char* p) {
+    switch (dtype) {
+    case KD_F32: return *(const float*)p;
+    case KD_F64: return *(const double*)p;
+    case KD_I64: return (double)*(const int64_t*)p;
+    default: return *(const u8*)p;
+    }
+}
+
+/* cast_value<Out, In>: kernels.inl:5-13 */
+static void store_cast(int out_dtype, char* dst, int in_dtype, const char* src) {
+    if (out_dtype == KD_BOOL) {
+        *(u8*)dst = read_as_double(in_dtype, src) != 0.0 ||
+                    (in_dtype == KD_I64 && *(const int64_t*)src != 0);
+        return;
+    }
+    if (out_dtype == KD_I64) {
+        if (in_dtype == KD_F32) *(int64_t*)dst = sat_i64(*(const float*)src);
+        else if (in_dtype == KD_F64) *(int64_t*)dst = sat_i64(*(const double*)src);
+        else if (in_dtype == KD_I64) *(int64_t*)dst = *(const int64_t*)src;
+        else *(int64_t*)dst = *(const u8*)src;
+        return;
+    }
+    if (out_dtype == KD_F32) {
+        if (in_dtype == KD_I64) *(float*)dst = (float)*(const int64_t*)src;
+        else if (in_dtype == KD_F64) *(float*)dst = (float)*(const double*)src;
+        else *(float*)dst = (float)read_as_double(in_dtype, src);
+        return;
+    }
+    if (in_dtype == KD_I64) *(double*)dst = (double)*(const int64_t*)src;
+    else *(double*)dst = read_as_double(in_dtype, src);
+}
+
+int oracle_fill(int dtype, void* target, int64_t count, const void* value) {
+    const int64_t size = dtype_size(dtype);
+    if (size == 0) return fail("fill: unknown dtype");
+    for (int64_t i = 0; i < count; ++i) memcpy((char*)target + i * size, value, (size_t)size);
+    return KD_OK;
+}
+
+int oracle_convert(int out_dtype, int in_dtype, const kd_element_layout* l) {
+    if (dtype_size(out_dtype) == 0 || dtype_size(in_dtype) == 0) return fail("convert: dtype");
+    if (l->count == 0) return KD_OK;
+    if (check_layout(l, 2)) return KD_E_INVALID;
+    for (int64_t e = l->count; e-- > 0;) {
+        char* ptr[KD_MAX_OPERANDS];
+        locate(l, e, ptr);
+        store_cast(out_dtype, ptr[0], in_dtype, ptr[1]);
+    }
+    return KD_OK;
+}
+
+int oracle_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout* l,
+                       kd_element_parameters p) {
+    (void)out_dtype; /* implied by the op, as at kernels.inl:335 */
+    const int valid_op = (op >= KD_OP_PLUS && op <= KD_OP_MASKED_FILL) ||
+                         op == KD_OP_GELU_EXACT_BACKWARD || op == KD_OP_GELU_TANH_BACKWARD;
+    if (!valid_op) return fail("elementwise: unknown op");
+    if (dtype_size(in_dtype) == 0) return fail("elementwise: unknown dtype");
+    if (is_floating_only(op) && in_dtype != KD_F32 && in_dtype != KD_F64)
+        return fail("elementwise: floating op on a non-floating dtype");
+    if (op == KD_OP_POWER && in_dtype == KD_BOOL) return KD_OK; /* kernels.inl:345-351 */
+    if (l->count == 0) return KD_OK;
+    const int inputs = input_count(op);
+    if (check_layout(l, inputs + 1)) return KD_E_INVALID;
+    for (int64_t e = l->count; e-- > 0;) {
+        char* ptr[KD_MAX_OPERANDS];
+        locate(l, e, ptr);
+        if (is_compare(op)) {
+            u8 r = 0;
+            switch (in_dtype) {
+            case KD_F32: r = compare_f32(op, *(float*)ptr[1], *(float*)ptr[2]); break;
+            case KD_F64: r = compare_f64(op, *(double*)ptr[1], *(double*)ptr[2]); break;
+            case KD_I64: r = compare_i64(op, *(int64_t*)ptr[1], *(int64_t*)ptr[2]); break;
+            default: r = compare_u8(op, *(u8*)ptr[1], *(u8*)ptr[2]); break;
+            }
+            *(u8*)ptr[0] = r;
+            continue;
+        }
+        switch (in_dtype) {
+        case KD_F32: {
+            float in[3];
+            for (int i = 0; i < inputs; ++i) in[i] = *(float*)ptr[i + 1];
+            *(float*)ptr[0] = same_f32(op, in, &p);
+            break;
+        }
+        case KD_F64: {
+            double in[3];
+            for (int i = 0; i < inputs; ++i) in[i] = *(double*)ptr[i + 1];
+            *(double*)ptr[0] = same_f64(op, in, &p);
+            break;
+        }
+        case KD_I64: {
+            int64_t in[3];
+            for (int i = 0; i < inputs; ++i) in[i] = *(int64_t*)ptr[i + 1];
+            *(int64_t*)ptr[0] = same_i64(op, in, &p);
+            break;
+        }
+        default: {
+            u8 in[3];
+            for (int i = 0; i < inputs; ++i) in[i] = *(u8*)ptr[i + 1];
+            *(u8*)ptr[0] = same_u8(op, in, &p);
+            break;
+        }
+        }
+    }
+    return KD_OK;
+}
+
+/* ---- reduce: kernels.inl:59-134, 278-307, 426-445 ----------------------------------------- */
+
+#define KBLOCK 4096
+
+static double reduce_range_f(int op, int in_dtype, const char* data, int64_t begin, int64_t end) {
+    const int64_t size = dtype_size(in_dtype);
+    if (op == KD_REDUCE_SUM) {
+        double total = 0.0;
+        for (int64_t i = begin; i < end; ++i) total += read_as_double(in_dtype, data + i * size);
+        return total;
+    }
+    if (in_dtype == KD_F32) {
+        const float* d = (const float*)data;
+        float best = d[begin];
+        for (int64_t i = begin + 1; i < end; ++i)
+            best = op == KD_REDUCE_MAX ? fmaxnaf(best, d[i]) : fminnaf(best, d[i]);
+        return best;
+    }
+    const double* d = (const double*)data;
+    double best = d[begin];
+    for (int64_t i = begin + 1; i < end; ++i)
+        best = op == KD_REDUCE_MAX ? fmaxna(best, d[i]) : fminna(best, d[i]);
+    return best;
+}
+
+static int64_t reduce_range_i(int op, int in_dtype, const char* data, int64_t begin, int64_t end) {
+    const int64_t* d64 = (const int64_t*)data;
+    const u8* d8 = (const u8*)data;
+    const int wide = in_dtype == KD_I64;
+    if (op == KD_REDUCE_SUM) {
+        int64_t total = 0;
+        for (int64_t i = begin; i < end; ++i) total = wadd(total, wide ? d64[i] : d8[i]);
+        return total;
+    }
+    int64_t best = wide ? d64[begin] : d8[begin];
+    for (int64_t i = begin + 1; i < end; ++i) {
+        const int64_t v = wide ? d64[i] : d8[i];
+        if (op == KD_REDUCE_MAX) best = best < v ? v : best;
+        else best = v < best ? v : best;
+    }
+    return best;
+}
+
+int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                  int64_t chunk, int64_t rows) {
+    (void)out_dtype;
+    if (op < KD_REDUCE_SUM || op > KD_REDUCE_MIN) return fail("reduce: unknown op");
+    if (dtype_size(in_dtype) == 0) return fail("reduce: unknown dtype");
+    if (rows == 0) return KD_OK;
+    if (chunk == 0 && op != KD_REDUCE_SUM) return fail("reduce: max/min of an empty chunk");
+    const int floating = in_dtype == KD_F32 || in_dtype == KD_F64;
+    const int64_t esize = dtype_size(in_dtype);
+    const int64_t blocks = chunk <= KBLOCK ? 1 : (chunk + KBLOCK - 1) / KBLOCK;
+    double* fpart = (double*)malloc((size_t)(2 * blocks) * sizeof(double));
+    int64_t* ipart = (int64_t*)malloc((size_t)(2 * blocks) * sizeof(int64_t));
+    for (int64_t r = 0; r < rows; ++r) {
+        const char* row = (const char*)data + r * chunk * esize;
+        double fv;
+        int64_t iv;
+        if (chunk <= KBLOCK) {
+            fv = floating ? reduce_range_f(op, in_dtype, row, 0, chunk) : 0;
+            iv = floating ? 0 : reduce_range_i(op, in_dtype, row, 0, chunk);
+        } else {
+            /* ReduceBlocks then the MergePairs tree, kernels.inl:108-128, 286-303 */
+            double* fs = fpart;
+            double* ft = fpart + blocks;
+            int64_t* is = ipart;
+            int64_t* it = ipart + blocks;
+            for (int64_t b = 0; b < blocks; ++b) {
+                const int64_t begin = b * KBLOCK;
+                const int64_t end = begin + KBLOCK < chunk ? begin + KBLOCK : chunk;
+                if (floating) fs[b] = reduce_range_f(op, in_dtype, row, begin, end);
+                else is[b] = reduce_range_i(op, in_dtype, row, begin, end);
+            }
+            for (int64_t width = blocks; width > 1; width = (width + 1) / 2) {
+                for (int64_t i = 0; i < (width + 1) / 2; ++i) {
+                    if (2 * i + 1 < width) {
+                        if (floating) {
+                            const double a = fs[2 * i], b = fs[2 * i + 1];
+                            ft[i] = op == KD_REDUCE_SUM ? a + b
+                                    : op == KD_REDUCE_MAX ? (in_dtype == KD_F32 ? fmaxnaf((float)a, (float)b) : fmaxna(a, b))
+                                                          : (in_dtype == KD_F32 ? fminnaf((float)a, (float)b) : fminna(a, b));
+                        } else {
+                            const int64_t a = is[2 * i], b = is[2 * i + 1];
+                            it[i] = op == KD_REDUCE_SUM ? wadd(a, b)
+                                    : op == KD_REDUCE_MAX ? (a < b ? b : a)
+                                                          : (b < a ? b : a);
+                        }
+                    } else {
+                        if (floating) ft[i] = fs[2 * i];
+                        else it[i] = is[2 * i];
+                    }
+                }
+                double* ftmp = fs; fs = ft; ft = ftmp;
+                int64_t* itmp = is; is = it; it = itmp;
+            }
+            fv = fs[0];
+            iv = is[0];
+        }
+        if (floating) {
+            if (in_dtype == KD_F32) ((float*)results)[r] = (float)fv;
+            else ((double*)results)[r] = fv;
+        } else if (op == KD_REDUCE_SUM || in_dtype == KD_I64) {
+            ((int64_t*)results)[r] = iv;
+        } else {
+            ((u8*)results)[r] = (u8)iv;
+        }
+    }
+    free(fpart);
+    free(ipart);
+    return KD_OK;
+}
+
+/* ---- matmul: kernels.inl:136-177 -------------------------------------------------------------- */
+
+int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,
+                  int exact) {
+    kd_matmul_strides st;
+    st.a[0] = s->rows * s->inner; st.a[1] = s->inner; st.a[2] = 1;
+    st.b[0] = s->inner * s->columns; st.b[1] = s->columns; st.b[2] = 1;
+    st.out[0] = s->rows * s->columns; st.out[1] = s->columns; st.out[2] = 1;
+    if (exact && dtype == KD_F32) {
+        const float* A = (const float*)a;
+        const float* B = (const float*)b;
+        float* C = (float*)out;
+        for (int64_t bt = 0; bt < s->batches; ++bt)
+            for (int64_t i = 0; i < s->rows; ++i)
+                for (int64_t j = 0; j < s->columns; ++j) {
+                    double acc = 0.0;
+                    for (int64_t k = 0; k < s->inner; ++k)
+                        acc += (double)A[bt * st.a[0] + i * s->inner + k] *
+                               (double)B[bt * st.b[0] + k * s->columns + j];
+                    C[bt * st.out[0] + i * s->columns + j] = (float)acc;
+                }
+        return KD_OK;
+    }
+    return oracle_matmul_strided(dtype, a, b, out, s, &st);
+}
+
+int oracle_matmul_strided(int dtype, const void* a, const void* b, void* out,
+                          const kd_matmul_sizes* s, const kd_matmul_strides* t) {
+    if (dtype == KD_BOOL) return fail("matmul does not support dtype bool");
+    if (dtype_size(dtype) == 0) return fail("matmul: unknown dtype");
+    for (int64_t bt = 0; bt < s->batches; ++bt)
+        for (int64_t i = 0; i < s->rows; ++i)
+            for (int64_t j = 0; j < s->columns; ++j) {
+                const int64_t ao = bt * t->a[0] + i * t->a[1];
+                const int64_t bo = bt * t->b[0] + j * t->b[2];
+                const int64_t oo = bt * t->out[0] + i * t->out[1] + j * t->out[2];
+                if (dtype == KD_F32) {
+                    float acc = 0.0f;
+                    for (int64_t k = 0; k < s->inner; ++k)
+                        acc = acc + ((const float*)a)[ao + k * t->a[2]] *
+                                        ((const float*)b)[bo + k * t->b[1]];
+                    ((float*)out)[oo] = acc;
+                } else if (dtype == KD_F64) {
+                    double acc = 0.0;
+                    for (int64_t k = 0; k < s->inner; ++k)
+                        acc = acc + ((const double*)a)[ao + k * t->a[2]] *
+                                        ((const double*)b)[bo + k * t->b[1]];
+                    ((double*)out)[oo] = acc;
+                } else {
+                    int64_t acc = 0;
+                    for (int64_t k = 0; k < s->inner; ++k)
+                        acc = wadd(acc, wmul(((const int64_t*)a)[ao + k * t->a[2]],
+                                             ((const int64_t*)b)[bo + k * t->b[1]]));
+                    ((int64_t*)out)[oo] = acc;
+                }
+            }
+    return KD_OK;
+}
+
+/* ---- gather / scatter_add: kernels.inl:179-221 --------------------------------------------------- */
+
+typedef struct {
+    int64_t data, index, source;
+} position_t;
+
+static position_t locate_index(const kd_index_layout* l, const int64_t* indices, int64_t e) {
+    position_t p = {0, 0, 0};
+    int64_t remaining = e;
+    for (int dim = l->dims - 1; dim >= 0; --dim) {
+        const int64_t c = remaining % l->shape[dim];
+        remaining /= l->shape[dim];
+        p.index += c * l->index_strides[dim];
+        p.source += c * l->source_strides[dim];
+        if (dim != l->axis) p.data += c * l->data_strides[dim];
+    }
+    p.data += indices[p.index] * l->data_strides[l->axis];
+    return p;
+}
+
+int oracle_gather(int dtype, void* out, const void* data, const int64_t* indices,
+                  const kd_index_layout* l) {
+    const int64_t size = dtype_size(dtype);
+    if (size == 0) return fail("gather: unknown dtype");
+    for (int64_t e = l->count; e-- > 0;) {
+        const position_t p = locate_index(l, indices, e);
+        memcpy((char*)out + e * size, (const char*)data + p.data * size, (size_t)size);
+    }
+    return KD_OK;
+}
+
+int oracle_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
+                       const kd_index_layout* l) {
+    if (dtype != KD_F32 && dtype != KD_F64 && dtype != KD_I64)
+        return fail("scatter_add: dtype must be f32, f64 or i64");
+    for (int64_t e = 0; e < l->count; ++e) {
+        const position_t p = locate_index(l, indices, e);
+        if (dtype == KD_F32) ((float*)data)[p.data] += ((const float*)source)[p.source];
+        else if (dtype == KD_F64) ((double*)data)[p.data] += ((const double*)source)[p.source];
+        else ((int64_t*)data)[p.data] = wadd(((int64_t*)data)[p.data], ((const int64_t*)source)[p.source]);
+    }
+    return KD_OK;
+}
+
+/* ---- row kernels: nn.cpp:52-129, 214-240 ------------------------------------------------------ */
+
+#define ROW_KERNELS(T, SUFFIX, EXPF, LOGF, MAXF)                                                     \
+    static T row_max_##SUFFIX(const T* row, int64_t n) {                                        \
+        T largest = row[0];                                                                     \
+        for (int64_t i = 1; i < n; ++i) largest = MAXF(largest, row[i]);                         \
+        return largest;                                                                         \
+    }                                                                                           \
+    static void softmax_row_##SUFFIX(const T* row, T* out, int64_t n) {                          \
+        const T largest = row_max_##SUFFIX(row, n);                                             \
+        double total = 0.0;                                                                     \
+        for (int64_t i = 0; i < n; ++i) {                                                       \
+            out[i] = EXPF(row[i] - largest);                                                    \
+            total += (double)out[i];                                                            \
+        }                                                                                       \
+        const T denominator = (T)total;                                                         \
+        for (int64_t i = 0; i < n; ++i) out[i] /= denominator;                                  \
+    }                                                                                           \
+    static void log_softmax_row_##SUFFIX(const T* row, T* out, int64_t n) {                      \
+        const T largest = row_max_##SUFFIX(row, n);                                             \
+        double total = 0.0;                                                                     \
+        for (int64_t i = 0; i < n; ++i) {                                                       \
+            out[i] = row[i] - largest;                                                          \
+            total += (double)EXPF(out[i]);                                                      \
+        }                                                                                       \
+        const T log_total = LOGF((T)total);                                                     \
+        for (int64_t i = 0; i < n; ++i) out[i] -= log_total;                                    \
+    }                                                                                           \
+    static T cross_entropy_row_##SUFFIX(const T* row, int64_t target, int64_t n) {              \
+        const T largest = row_max_##SUFFIX(row, n);                                             \
+        double total = 0.0;                                                                     \
+        for (int64_t i = 0; i < n; ++i) total += (double)EXPF(row[i] - largest);                \
+        return LOGF((T)total) - (row[target] - largest);                                        \
+    }                                                                                           \
+    static void standardize_row_##SUFFIX(const T* row, T* out, int64_t n, double eps,           \
+                                         const T* w, const T* b) {                              \
+        double total = 0.0;                                                                     \
+        for (int64_t i = 0; i < n; ++i) total += (double)row[i];                                \
+        const double center = total / (double)n;                                                \
+        double squares = 0.0;                                                                   \
+        for (int64_t i = 0; i < n; ++i) {                                                       \
+            const double d = (double)row[i] - center;                                           \
+            squares += d * d;                                                                   \
+        }                                                                                       \
+        const double scale = sqrt(squares / (double)n + eps);                                   \
+        for (int64_t i = 0; i < n; ++i) {                                                       \
+            T y = (T)(((double)row[i] - center) / scale);                                       \
+            if (w) {                                                                            \
+                y = y * w[i];                                                                   \
+                y = y + b[i];                                                                   \
+            }                                                                                   \
+            out[i] = y;                                                                         \
+        }                                                                                       \
+    }
+
+ROW_KERNELS(float, f32, expf, logf, fmaxnaf)
+ROW_KERNELS(double, f64, exp, log, fmaxna)
+
+static int check_floating(int dtype) {
+    return dtype == KD_F32 || dtype == KD_F64 ? KD_OK : fail("row kernel: dtype must be f32 or f64");
+}
+
+int oracle_softmax_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols,
+                        int log_softmax) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    if (cols == 0) return KD_OK;
+    for (int64_t r = 0; r < rows; ++r) {
+        if (dtype == KD_F32) {
+            const float* x = (const float*)in + r * cols;
+            float* y = (float*)out + r * cols;
+            if (log_softmax) log_softmax_row_f32(x, y, cols);
+            else softmax_row_f32(x, y, cols);
+        } else {
+            const double* x = (const double*)in + r * cols;
+            double* y = (double*)out + r * cols;
+            if (log_softmax) log_softmax_row_f64(x, y, cols);
+            else softmax_row_f64(x, y, cols);
+        }
+    }
+    return KD_OK;
+}
+
+int oracle_standardize_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols,
+                            double eps, const void* weight, const void* bias) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    if ((weight == NULL) != (bias == NULL)) return fail("standardize: weight and bias go together");
+    if (cols == 0) return KD_OK;
+    for (int64_t r = 0; r < rows; ++r) {
+        if (dtype == KD_F32)
+            standardize_row_f32((const float*)in + r * cols, (float*)out + r * cols, cols, eps,
+                                (const float*)weight, (const float*)bias);
+        else
+            standardize_row_f64((const double*)in + r * cols, (double*)out + r * cols, cols, eps,
+                                (const double*)weight, (const double*)bias);
+    }
+    return KD_OK;
+}
+
+int oracle_cross_entropy_rows(int dtype, void* losses, const void* logits, const int64_t* targets,
+                              int64_t rows, int64_t cols) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    for (int64_t r = 0; r < rows; ++r) {
+        if (targets[r] < 0 || targets[r] >= cols) return fail("cross_entropy: target out of range");
+        if (dtype == KD_F32)
+            ((float*)losses)[r] = cross_entropy_row_f32((const float*)logits + r * cols, targets[r], cols);
+        else
+            ((double*)losses)[r] = cross_entropy_row_f64((const double*)logits + r * cols, targets[r], cols);
+    }
+    return KD_OK;
+}
+
+int oracle_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
+                              const void* weights, int64_t rows, int64_t cols) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    for (int64_t r = 0; r < rows; ++r) {
+        if (targets[r] < 0 || targets[r] >= cols) return fail("cross_entropy: target out of range");
+        if (dtype == KD_F32) {
+            float* y = (float*)out + r * cols;
+            const float w = ((const float*)weights)[r];
+            softmax_row_f32((const float*)logits + r * cols, y, cols);
+            for (int64_t i = 0; i < cols; ++i) y[i] *= w;
+            y[targets[r]] -= w;
+        } else {
+            double* y = (double*)out + r * cols;
+            const double w = ((const double*)weights)[r];
+            softmax_row_f64((const double*)logits + r * cols, y, cols);
+            for (int64_t i = 0; i < cols; ++i) y[i] *= w;
+            y[targets[r]] -= w;
+        }
+    }
+    return KD_OK;
+}
+
+/* ---- layout planning: iterator.cpp:12-63, 152-172 ------------------------------------------- */
+
+int oracle_layout_build(kd_element_layout* out, int operands, const int* ranks,
+                        const int64_t* shapes, const int64_t* strides, const int* element_sizes,
+                        void* const* bases) {
+    if (operands < 1 || operands > KD_MAX_OPERANDS) return fail("layout: operand count");
+    const int ndim = ranks[0];
+    if (ndim < 0 || ndim > KD_MAX_DIMS) return fail("layout: rank");
+    int64_t shape[KD_MAX_DIMS];
+    int64_t st[KD_MAX_OPERANDS][KD_MAX_DIMS];
+    int64_t count = 1;
+    for (int d = 0; d < ndim; ++d) {
+        shape[d] = shapes[d];
+        count *= shape[d];
+        st[0][d] = strides[d] * element_sizes[0];
+    }
+    /* broadcast_strides: align trailing dims; size-1 or missing dims get stride 0 */
+    for (int op = 1; op < operands; ++op) {
+        const int r = ranks[op];
+        if (r > ndim) return fail("layout: input rank exceeds the output rank");
+        for (int d = 0; d < ndim; ++d) {
+            const int src = d - (ndim - r);
+            if (src < 0) {
+                st[op][d] = 0;
+                continue;
+            }
+            const int64_t size = shapes[op * KD_MAX_DIMS + src];
+            if (size == shape[d]) st[op][d] = strides[op * KD_MAX_DIMS + src] * element_sizes[op];
+            else if (size == 1) st[op][d] = 0;
+            else return fail("layout: shapes do not broadcast");
+        }
+    }
+    /* coalesce_dims: drop size-1 dims, then merge from the innermost outward */
+    int n = 0;
+    int64_t ms[KD_MAX_DIMS];
+    int64_t mst[KD_MAX_OPERANDS][KD_MAX_DIMS];
+    for (int d = 0; d < ndim; ++d) {
+        if (shape[d] == 1) continue;
+        ms[n] = shape[d];
+        for (int op = 0; op < operands; ++op) mst[op][n] = st[op][d];
+        ++n;
+    }
+    for (int inner = n - 1; inner >= 1; --inner) {
+        const int outer = inner - 1;
+        int mergeable = 1;
+        for (int op = 0; op < operands; ++op)
+            if (mst[op][outer] != mst[op][inner] * ms[inner]) mergeable = 0;
+        if (!mergeable) continue;
+        ms[outer] *= ms[inner];
+        for (int k = inner; k < n - 1; ++k) ms[k] = ms[k + 1];
+        for (int op = 0; op < operands; ++op) {
+            mst[op][outer] = mst[op][inner];
+            for (int k = inner; k < n - 1; ++k) mst[op][k] = mst[op][k + 1];
+        }
+        --n;
+    }
+    memset(out, 0, sizeof *out);
+    if (n == 0) {
+        n = 1;
+        ms[0] = 1;
+        for (int op = 0; op < operands; ++op) mst[op][0] = 0;
+    }
+    out->dims = n;
+    out->operands = operands;
+    out->count = count;
+    for (int d = 0; d < n; ++d) {
+        out->shape[d] = ms[d];
+        for (int op = 0; op < operands; ++op) out->strides[op][d] = mst[op][d];
+    }
+    for (int op = 0; op < operands; ++op) out->base[op] = bases ? bases[op] : NULL;
+    return KD_OK;
+}

@@ -1,0 +1,53 @@
+/*
+ * kd_oracle.h - TEST INFRASTRUCTURE ONLY.
+ *
+ * Plain-C CPU restatement of the reference device semantics, with the same entry points
+ * and argument meaning as include/kd_api.h (prefix `oracle_` instead of `kd_`). Pointers
+ * are host memory. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it, and only as the checker. Each function cites the reference lines it
+ * restates.
+ */
+#ifndef KD_ORACLE_H
+#define KD_ORACLE_H
+
+#include "kd_api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* oracle_last_error(void);
+
+int oracle_fill(int dtype, void* target, int64_t count, const void* value);
+int oracle_convert(int out_dtype, int in_dtype, const kd_element_layout* layout);
+int oracle_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout* layout,
+                       kd_element_parameters parameters);
+int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                  int64_t chunk_size, int64_t output_count);
+/* exact == 0: the reference device order (MatmulTiles, sequential k in T);
+ * exact != 0: f32 inputs accumulated in double (error-analysis reference). */
+int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                  int exact);
+int oracle_matmul_strided(int dtype, const void* a, const void* b, void* out,
+                          const kd_matmul_sizes* sizes, const kd_matmul_strides* strides);
+int oracle_gather(int dtype, void* out, const void* data, const int64_t* indices,
+                  const kd_index_layout* layout);
+int oracle_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
+                       const kd_index_layout* layout);
+int oracle_softmax_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols,
+                        int log_softmax);
+int oracle_standardize_rows(int dtype, void* out, const void* in, int64_t rows, int64_t cols,
+                            double eps, const void* weight, const void* bias);
+int oracle_cross_entropy_rows(int dtype, void* losses, const void* logits, const int64_t* targets,
+                              int64_t rows, int64_t cols);
+int oracle_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
+                              const void* row_weights, int64_t rows, int64_t cols);
+int oracle_layout_build(kd_element_layout* out, int operands, const int* ranks,
+                        const int64_t* shapes, const int64_t* strides, const int* element_sizes,
+                        void* const* bases);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

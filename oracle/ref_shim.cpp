@@ -1,0 +1,580 @@
+// ref_shim.cpp - TEST INFRASTRUCTURE ONLY (the checker, never the product).
+//
+// extern "C" entry points over the reference kael C++ core, compiled unmodified from
+// /root/reference/src by oracle/Makefile into oracle/_ref/libkael_ref.so. Two families:
+//
+//  ref_dev_*  the reference's own device tasks (src/cuda/kernels.inl) executed on the host by
+//             the reference's emulation backend src/cuda/backend_fake.cpp. They take the same
+//             kd_* layouts as the HIP backend and pin the C restatement in oracle/kd_oracle.c
+//             at the exact device boundary (include/kael/device_kernels.h:96-116).
+//  ref_*      kael's CPU path through the public tensor API (ops, nn, autograd, optim): the
+//             op-level oracle and the timed CPU baseline.
+//
+// Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kael/device_kernels.h"
+#include "kael/kael.h"
+#include "kael/nn/linear.h"
+#include "kael/nn/loss.h"
+#include "kael/nn/activation.h"
+#include "kael/nn/sequential.h"
+#include "kael/nn/transformer.h"
+#include "kael/optim/adam.h"
+#include "kael/optim/sgd.h"
+
+#include "kd_api.h"
+
+namespace kael::detail {
+// Declared in the reference's autograd sources (defined in src/ops/nn.cpp:214-240).
+Tensor cross_entropy_gradient(const Tensor& logits, const Tensor& targets, const Tensor& scale);
+} // namespace kael::detail
+
+namespace {
+
+thread_local std::string g_error;
+
+template <typename F> int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return -1;
+    }
+}
+
+static_assert(sizeof(kd_element_layout) == sizeof(kael::device::ElementLayout));
+static_assert(sizeof(kd_index_layout) == sizeof(kael::device::IndexLayout));
+static_assert(sizeof(kd_matmul_sizes) == sizeof(kael::device::MatmulSizes));
+
+kael::DType to_dtype(int code) { return static_cast<kael::DType>(code); }
+
+kael::device::ElementLayout to_layout(const kd_element_layout* l) {
+    kael::device::ElementLayout out{};
+    std::memcpy(&out, l, sizeof(out));
+    return out;
+}
+
+kael::device::IndexLayout to_index_layout(const kd_index_layout* l) {
+    kael::device::IndexLayout out{};
+    std::memcpy(&out, l, sizeof(out));
+    return out;
+}
+
+// A CPU tensor holding a copy of `count` elements of `dtype` at `data`.
+kael::Tensor host_tensor(const void* data, const kael::Shape& shape, kael::DType dtype) {
+    kael::Tensor t = kael::empty(shape, dtype);
+    std::memcpy(t.data_ptr_raw(), data,
+                static_cast<std::size_t>(t.numel() * kael::element_size(dtype)));
+    return t;
+}
+
+void copy_out(const kael::Tensor& t, void* out) {
+    const kael::Tensor c = t.contiguous();
+    std::memcpy(out, c.data_ptr_raw(),
+                static_cast<std::size_t>(c.numel() * kael::element_size(c.dtype())));
+}
+
+} // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_error.c_str(); }
+
+void ref_set_threads(int64_t n) { kael::set_num_threads(n); }
+int64_t ref_get_threads(void) { return kael::get_num_threads(); }
+
+// ---- boundary-level: the reference device tasks, run on the host -------------------------
+
+int ref_dev_fill(int dtype, void* target, int64_t count, const void* value) {
+    return guarded([&] {
+        kael::device::fill(to_dtype(dtype), static_cast<std::byte*>(target), count, value);
+    });
+}
+
+int ref_dev_convert(int out, int in, const kd_element_layout* layout) {
+    return guarded([&] { kael::device::convert(to_dtype(out), to_dtype(in), to_layout(layout)); });
+}
+
+int ref_dev_elementwise(int op, int out, int in, const kd_element_layout* layout,
+                        kd_element_parameters p) {
+    return guarded([&] {
+        kael::device::ElementParameters params{};
+        params.reals = {p.reals[0], p.reals[1]};
+        params.integers = {p.integers[0], p.integers[1]};
+        kael::device::elementwise(static_cast<kael::device::ElementOp>(op), to_dtype(out),
+                                  to_dtype(in), to_layout(layout), params);
+    });
+}
+
+int ref_dev_reduce(int op, int out, int in, void* results, const void* data, int64_t chunk,
+                   int64_t rows) {
+    return guarded([&] {
+        kael::device::reduce(static_cast<kael::device::ReduceOp>(op), to_dtype(out), to_dtype(in),
+                             static_cast<std::byte*>(results),
+                             static_cast<const std::byte*>(data), chunk, rows);
+    });
+}
+
+int ref_dev_matmul(int dtype, const void* a, const void* b, void* out,
+                   const kd_matmul_sizes* sizes) {
+    return guarded([&] {
+        kael::device::matmul(to_dtype(dtype), static_cast<const std::byte*>(a),
+                             static_cast<const std::byte*>(b), static_cast<std::byte*>(out),
+                             {sizes->batches, sizes->rows, sizes->inner, sizes->columns});
+    });
+}
+
+int ref_dev_gather(int dtype, void* out, const void* data, const int64_t* indices,
+                   const kd_index_layout* layout) {
+    return guarded([&] {
+        kael::device::gather(to_dtype(dtype), static_cast<std::byte*>(out),
+                             static_cast<const std::byte*>(data), indices,
+                             to_index_layout(layout));
+    });
+}
+
+int ref_dev_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
+                        const kd_index_layout* layout) {
+    return guarded([&] {
+        kael::device::scatter_add(to_dtype(dtype), static_cast<std::byte*>(data), indices,
+                                  static_cast<const std::byte*>(source), to_index_layout(layout));
+    });
+}
+
+// ---- host-side layout planning (TensorIterator) ---------------------------------------------
+
+// Runs kael::coalesce_dims on (shape, byte strides per operand) and writes the merged
+// result. Returns the number of merged dims (or -1).
+int ref_coalesce(int dims, int operands, const int64_t* shape, const int64_t* strides,
+                 int64_t* out_shape, int64_t* out_strides) {
+    int result = -1;
+    const int rc = guarded([&] {
+        kael::LoopDims loop;
+        loop.shape.assign(shape, shape + dims);
+        for (int op = 0; op < operands; ++op) {
+            loop.operand_strides.emplace_back(strides + op * dims, strides + (op + 1) * dims);
+        }
+        const kael::LoopDims merged = kael::coalesce_dims(loop);
+        const int n = static_cast<int>(merged.shape.size());
+        for (int d = 0; d < n; ++d) {
+            out_shape[d] = merged.shape[static_cast<std::size_t>(d)];
+            for (int op = 0; op < operands; ++op) {
+                out_strides[op * 8 + d] =
+                    merged.operand_strides[static_cast<std::size_t>(op)][static_cast<std::size_t>(d)];
+            }
+        }
+        result = n;
+    });
+    return rc == 0 ? result : -1;
+}
+
+// ---- op-level: kael's CPU path ----------------------------------------------------------------
+
+int ref_matmul(int dtype, const void* a, const void* b, void* out, int64_t batches, int64_t m,
+               int64_t k, int64_t n) {
+    return guarded([&] {
+        const kael::DType dt = to_dtype(dtype);
+        const kael::Tensor ta = host_tensor(a, {batches, m, k}, dt);
+        const kael::Tensor tb = host_tensor(b, {batches, k, n}, dt);
+        copy_out(kael::matmul(ta, tb), out);
+    });
+}
+
+int ref_softmax(int dtype, void* out, const void* in, int64_t rows, int64_t cols, int log) {
+    return guarded([&] {
+        const kael::Tensor x = host_tensor(in, {rows, cols}, to_dtype(dtype));
+        copy_out(log ? kael::log_softmax(x, -1) : kael::softmax(x, -1), out);
+    });
+}
+
+int ref_layer_norm(int dtype, void* out, const void* in, int64_t rows, int64_t cols, double eps,
+                   const void* weight, const void* bias) {
+    return guarded([&] {
+        const kael::DType dt = to_dtype(dtype);
+        const kael::Tensor x = host_tensor(in, {rows, cols}, dt);
+        kael::Tensor y = kael::standardize(x, 1, eps);
+        if (weight != nullptr) {
+            y = y * host_tensor(weight, {cols}, dt) + host_tensor(bias, {cols}, dt);
+        }
+        copy_out(y, out);
+    });
+}
+
+int ref_cross_entropy(int dtype, void* losses, const void* logits, const int64_t* targets,
+                      int64_t rows, int64_t cols) {
+    return guarded([&] {
+        const kael::Tensor x = host_tensor(logits, {rows, cols}, to_dtype(dtype));
+        const kael::Tensor t = host_tensor(targets, {rows}, kael::DType::I64);
+        copy_out(kael::cross_entropy_losses(x, t), losses);
+    });
+}
+
+int ref_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
+                           const void* weights, int64_t rows, int64_t cols) {
+    return guarded([&] {
+        const kael::DType dt = to_dtype(dtype);
+        const kael::Tensor x = host_tensor(logits, {rows, cols}, dt);
+        const kael::Tensor t = host_tensor(targets, {rows}, kael::DType::I64);
+        const kael::Tensor w = host_tensor(weights, {rows}, dt);
+        copy_out(kael::detail::cross_entropy_gradient(x, t, w), out);
+    });
+}
+
+// g * gelu'(x) through kael's autograd (GeluBackward, src/autograd/functions_math.cpp:221-231).
+int ref_gelu_backward(int dtype, void* out, const void* x, const void* g, int64_t n,
+                      int approximate) {
+    return guarded([&] {
+        const kael::DType dt = to_dtype(dtype);
+        kael::Tensor tx = host_tensor(x, {n}, dt);
+        tx.requires_grad_();
+        const kael::Tensor y = kael::gelu(tx, approximate != 0);
+        y.backward(host_tensor(g, {n}, dt));
+        copy_out(*tx.grad(), out);
+    });
+}
+
+// ---- workloads (inputs from kael's own RNG, as the benchmark configs specify) ------------------
+
+// rand(shape)*2-1 after manual_seed(seed): the matmul / elementwise config recipe.
+int ref_uniform_pm1(uint64_t seed, int64_t count, float* out) {
+    return guarded([&] {
+        kael::manual_seed(seed);
+        copy_out(kael::rand({count}) * 2 - 1, out);
+    });
+}
+
+// Times `iters` calls of kael::matmul on f32 [m,k]x[k,n] CPU tensors (after one warm-up call)
+// and returns the median seconds per call.
+int ref_time_matmul(int64_t m, int64_t k, int64_t n, int iters, double* median_seconds) {
+    return guarded([&] {
+        kael::manual_seed(0);
+        const kael::Tensor a = kael::rand({m, k}) * 2 - 1;
+        const kael::Tensor b = kael::rand({k, n}) * 2 - 1;
+        (void)kael::matmul(a, b);
+        std::vector<double> times;
+        for (int i = 0; i < iters; ++i) {
+            const auto t0 = std::chrono::steady_clock::now();
+            const kael::Tensor c = kael::matmul(a, b);
+            const auto t1 = std::chrono::steady_clock::now();
+            times.push_back(std::chrono::duration<double>(t1 - t0).count());
+        }
+        std::sort(times.begin(), times.end());
+        *median_seconds = times[times.size() / 2];
+    });
+}
+
+// Times one of the elementwise/reduction ops of the C2 config on CPU tensors; `which`:
+// 0 a+b, 1 a*b, 2 a.T()+b, 3 sum(a,{1}), 4 max(a). Median seconds per call.
+int ref_time_c2(int which, int64_t rows, int64_t cols, int iters, double* median_seconds) {
+    return guarded([&] {
+        kael::manual_seed(1);
+        const kael::Tensor a = kael::rand({rows, cols}) * 2 - 1;
+        const kael::Tensor b = kael::rand({rows, 1}) * 2 - 1;
+        const auto run = [&] {
+            switch (which) {
+            case 0: return a + b;
+            case 1: return a * b;
+            case 2: return a.T() + b;
+            case 3: return kael::sum(a, {1});
+            default: return kael::max(a);
+            }
+        };
+        (void)run();
+        std::vector<double> times;
+        for (int i = 0; i < iters; ++i) {
+            const auto t0 = std::chrono::steady_clock::now();
+            const kael::Tensor c = run();
+            const auto t1 = std::chrono::steady_clock::now();
+            times.push_back(std::chrono::duration<double>(t1 - t0).count());
+        }
+        std::sort(times.begin(), times.end());
+        *median_seconds = times[times.size() / 2];
+    });
+}
+
+// ---- GPT (C5 decode) ----------------------------------------------------------------------------
+
+struct RefGpt {
+    std::unique_ptr<kael::nn::GPT> model;
+    std::vector<kael::nn::NamedTensor> named;
+};
+
+void* ref_gpt_create(int64_t vocab, int64_t positions, int64_t layers, int64_t heads,
+                     int64_t dimension, uint64_t seed, int tanh_gelu) {
+    RefGpt* handle = nullptr;
+    guarded([&] {
+        kael::nn::GptConfig config;
+        config.vocab_size = vocab;
+        config.max_positions = positions;
+        config.layers = layers;
+        config.heads = heads;
+        config.dimension = dimension;
+        config.tanh_gelu = tanh_gelu != 0;
+        kael::manual_seed(seed);
+        auto h = std::make_unique<RefGpt>();
+        h->model = std::make_unique<kael::nn::GPT>(config);
+        h->model->eval();
+        h->named = h->model->named_parameters();
+        handle = h.release();
+    });
+    return handle;
+}
+
+void ref_gpt_destroy(void* handle) { delete static_cast<RefGpt*>(handle); }
+
+int64_t ref_gpt_param_count(void* handle) {
+    return static_cast<int64_t>(static_cast<RefGpt*>(handle)->named.size());
+}
+
+// Name (NUL-terminated into name[len]), rank and shape of parameter i; copies the values into
+// `data` when it is non-NULL.
+int ref_gpt_param(void* handle, int64_t i, char* name, int len, int64_t* shape, int* rank,
+                  float* data) {
+    return guarded([&] {
+        const auto& entry = static_cast<RefGpt*>(handle)->named.at(static_cast<std::size_t>(i));
+        std::snprintf(name, static_cast<std::size_t>(len), "%s", entry.first.c_str());
+        const kael::Tensor& t = entry.second;
+        *rank = static_cast<int>(t.dim());
+        for (int d = 0; d < *rank; ++d) {
+            shape[d] = t.size(d);
+        }
+        if (data != nullptr) {
+            copy_out(t.detach(), data);
+        }
+    });
+}
+
+// Full forward (no cache) of `tokens` [batch, length]; logits [batch, length, vocab].
+int ref_gpt_forward(void* handle, const int64_t* tokens, int64_t batch, int64_t length,
+                    float* logits) {
+    return guarded([&] {
+        const kael::autograd::NoGradGuard guard;
+        const kael::Tensor ids = host_tensor(tokens, {batch, length}, kael::DType::I64);
+        copy_out(static_cast<RefGpt*>(handle)->model->forward(ids), logits);
+    });
+}
+
+// Teacher-forced cached decode: prefill tokens[0..prompt) with a KV cache, then feed
+// tokens[prompt..total) one at a time. Writes the last-position logits of the prefill and of
+// every step: (total - prompt + 1) rows of vocab floats.
+int ref_gpt_cached_logits(void* handle, const int64_t* tokens, int64_t prompt, int64_t total,
+                          float* logits) {
+    return guarded([&] {
+        const kael::autograd::NoGradGuard guard;
+        auto& model = *static_cast<RefGpt*>(handle)->model;
+        const int64_t vocab = model.config().vocab_size;
+        kael::nn::KvCache cache;
+        const kael::Tensor ids = host_tensor(tokens, {1, total}, kael::DType::I64);
+        kael::Tensor out = model.forward(ids.narrow(1, 0, prompt), &cache);
+        copy_out(out.select(1, prompt - 1), logits);
+        for (int64_t t = prompt; t < total; ++t) {
+            out = model.forward(ids.narrow(1, t, 1), &cache);
+            copy_out(out.select(1, 0), logits + (t - prompt + 1) * vocab);
+        }
+    });
+}
+
+// kael::nn::generate (greedy, KV cache) of `new_tokens` after `prompt`; writes the generated
+// ids and the wall seconds of the call.
+int ref_gpt_generate(void* handle, const int64_t* prompt, int64_t length, int64_t new_tokens,
+                     int64_t* out_tokens, double* seconds) {
+    return guarded([&] {
+        auto& model = *static_cast<RefGpt*>(handle)->model;
+        const kael::Tensor ids = host_tensor(prompt, {1, length}, kael::DType::I64);
+        const auto t0 = std::chrono::steady_clock::now();
+        const kael::Tensor seq = kael::nn::generate(
+            model, ids, {.max_new_tokens = new_tokens, .temperature = 0.0});
+        const auto t1 = std::chrono::steady_clock::now();
+        *seconds = std::chrono::duration<double>(t1 - t0).count();
+        copy_out(seq, out_tokens);
+    });
+}
+
+} // extern "C"
+
+// ---- golden cases through kael's public API ---------------------------------------------------
+//
+// Runs one case of the reference's golden suite (tests/golden/manifest.txt; op table of
+// tests/test_golden.cpp:134-232) with the inputs placed on `device` (0 = CPU, 1 = the device
+// backend this library was linked with) after applying the case's view to each input. The
+// result is returned contiguous on the host: dtype code, rank, shape and bytes.
+
+namespace {
+
+std::vector<std::string> split_text(const std::string& text, char separator) {
+    std::vector<std::string> parts;
+    std::string part;
+    for (char ch : text) {
+        if (ch == separator) {
+            parts.push_back(part);
+            part.clear();
+        } else {
+            part.push_back(ch);
+        }
+    }
+    parts.push_back(part);
+    return parts;
+}
+
+std::vector<int64_t> ints_of(const std::vector<std::string>& texts) {
+    std::vector<int64_t> out;
+    for (const auto& t : texts) {
+        if (!t.empty()) out.push_back(std::stoll(t));
+    }
+    return out;
+}
+
+struct CaseArgs {
+    std::vector<std::pair<std::string, std::string>> items;
+    explicit CaseArgs(const std::string& encoded) {
+        if (encoded.empty()) return;
+        for (const auto& item : split_text(encoded, ',')) {
+            const auto colon = item.find(':');
+            items.emplace_back(item.substr(0, colon), colon == std::string::npos ? "" : item.substr(colon + 1));
+        }
+    }
+    const std::string* find(const std::string& key) const {
+        for (const auto& [k, v] : items) {
+            if (k == key) return &v;
+        }
+        return nullptr;
+    }
+    bool has(const std::string& key) const { return find(key) != nullptr; }
+    int64_t integer(const std::string& key) const { return std::stoll(*find(key)); }
+    double real(const std::string& key) const { return std::stod(*find(key)); }
+    bool flag(const std::string& key) const { return has(key) && *find(key) == "1"; }
+    kael::Dims dims(const std::string& key) const {
+        if (!has(key)) return {};
+        const auto v = ints_of(split_text(*find(key), '/'));
+        return kael::Dims(v.begin(), v.end());
+    }
+};
+
+kael::Tensor view_of(const kael::Tensor& t, const std::string& view) {
+    const auto parts = split_text(view, ':');
+    const auto args = ints_of(std::vector<std::string>(parts.begin() + 1, parts.end()));
+    if (parts[0] == "none") return t;
+    if (parts[0] == "transpose") return t.transpose(args[0], args[1]);
+    if (parts[0] == "permute") return t.permute(kael::Dims(args.begin(), args.end()));
+    if (parts[0] == "slice") return t.slice(args[0], args[1], args[2], args[3]);
+    if (parts[0] == "expand") return t.expand(kael::Shape(args.begin(), args.end()));
+    throw kael::Error("unknown golden view " + view);
+}
+
+kael::Tensor run_golden_op(const std::string& op, std::vector<kael::Tensor>& in, const CaseArgs& a) {
+    using kael::Tensor;
+    if (op == "add") return kael::add(in[0], in[1]);
+    if (op == "sub") return kael::sub(in[0], in[1]);
+    if (op == "mul") return kael::mul(in[0], in[1]);
+    if (op == "div") return kael::div(in[0], in[1]);
+    if (op == "floor_divide") return kael::floor_divide(in[0], in[1]);
+    if (op == "pow") return kael::pow(in[0], in[1]);
+    if (op == "maximum") return kael::maximum(in[0], in[1]);
+    if (op == "minimum") return kael::minimum(in[0], in[1]);
+    if (op == "eq") return kael::eq(in[0], in[1]);
+    if (op == "ne") return kael::ne(in[0], in[1]);
+    if (op == "lt") return kael::lt(in[0], in[1]);
+    if (op == "le") return kael::le(in[0], in[1]);
+    if (op == "gt") return kael::gt(in[0], in[1]);
+    if (op == "ge") return kael::ge(in[0], in[1]);
+    if (op == "logical_and") return kael::logical_and(in[0], in[1]);
+    if (op == "logical_or") return kael::logical_or(in[0], in[1]);
+    if (op == "logical_xor") return kael::logical_xor(in[0], in[1]);
+    if (op == "neg") return kael::neg(in[0]);
+    if (op == "abs") return kael::abs(in[0]);
+    if (op == "sign") return kael::sign(in[0]);
+    if (op == "exp") return kael::exp(in[0]);
+    if (op == "log") return kael::log(in[0]);
+    if (op == "log1p") return kael::log1p(in[0]);
+    if (op == "expm1") return kael::expm1(in[0]);
+    if (op == "sqrt") return kael::sqrt(in[0]);
+    if (op == "rsqrt") return kael::rsqrt(in[0]);
+    if (op == "sin") return kael::sin(in[0]);
+    if (op == "cos") return kael::cos(in[0]);
+    if (op == "tanh") return kael::tanh(in[0]);
+    if (op == "sigmoid") return kael::sigmoid(in[0]);
+    if (op == "relu") return kael::relu(in[0]);
+    if (op == "gelu") return kael::gelu(in[0]);
+    if (op == "gelu_tanh") return kael::gelu(in[0], true);
+    if (op == "add_") { Tensor self = in[0]; return self.add_(in[1]); }
+    if (op == "sub_") { Tensor self = in[0]; return self.sub_(in[1]); }
+    if (op == "mul_") { Tensor self = in[0]; return self.mul_(in[1]); }
+    if (op == "div_") { Tensor self = in[0]; return self.div_(in[1]); }
+    if (op == "pow_") { Tensor self = in[0]; return self.pow_(in[1]); }
+    if (op == "copy_") { Tensor self = in[0]; return self.copy_(in[1]); }
+    if (op == "clamp_") { Tensor self = in[0]; return self.clamp_(a.real("min"), a.real("max")); }
+    if (op == "sum") return kael::sum(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "prod") return kael::prod(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "mean") return kael::mean(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "max") return kael::max(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "min") return kael::min(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "all") return kael::all(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "any") return kael::any(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "norm") return kael::norm(in[0], a.dims("dims"), a.flag("keepdim"));
+    if (op == "var") return kael::var(in[0], a.dims("dims"), a.flag("keepdim"), 1);
+    if (op == "std") return kael::std(in[0], a.dims("dims"), a.flag("keepdim"), 1);
+    if (op == "var_correction0") return kael::var(in[0], a.dims("dims"), a.flag("keepdim"), 0);
+    if (op == "argmax")
+        return a.has("dim") ? kael::argmax(in[0], a.integer("dim"), a.flag("keepdim")) : kael::argmax(in[0]);
+    if (op == "argmin")
+        return a.has("dim") ? kael::argmin(in[0], a.integer("dim"), a.flag("keepdim")) : kael::argmin(in[0]);
+    if (op == "matmul") return kael::matmul(in[0], in[1]);
+    if (op == "dot") return kael::dot(in[0], in[1]);
+    if (op == "outer") return kael::outer(in[0], in[1]);
+    if (op == "cat") return kael::cat(in, a.integer("dim"));
+    if (op == "stack") return kael::stack(in, a.integer("dim"));
+    if (op == "where") return kael::where(in[0], in[1], in[2]);
+    if (op == "masked_fill") return kael::masked_fill(in[0], in[1], a.real("value"));
+    if (op == "index_select") return kael::index_select(in[0], a.integer("dim"), in[1]);
+    if (op == "gather") return kael::gather(in[0], a.integer("dim"), in[1]);
+    if (op == "scatter_add_") { Tensor self = in[0]; return self.scatter_add_(a.integer("dim"), in[1], in[2]); }
+    if (op == "logsumexp") return kael::logsumexp(in[0], a.integer("dim"), a.flag("keepdim"));
+    if (op == "softmax") return kael::softmax(in[0], a.integer("dim"));
+    if (op == "log_softmax") return kael::log_softmax(in[0], a.integer("dim"));
+    if (op == "clamp") return kael::clamp(in[0], a.real("min"), a.real("max"));
+    throw kael::Error("no golden op " + op);
+}
+
+} // namespace
+
+extern "C" {
+
+// inputs: `n` base arrays (contiguous host data of dtypes[i], ranks[i], shapes[i*8..]) and a
+// view string per input; `args` is the manifest's args field. Output bytes go to `out`
+// (capacity `out_bytes`); returns the output byte count, or -1 on error (ref_last_error()).
+int64_t ref_golden(const char* op, const char* args, int n, const void* const* datas, const int* dtypes,
+                   const int* ranks, const int64_t* shapes, const char* const* views, int device, void* out,
+                   int64_t out_bytes, int* out_dtype, int* out_rank, int64_t* out_shape) {
+    int64_t written = -1;
+    guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        std::vector<kael::Tensor> inputs;
+        for (int i = 0; i < n; ++i) {
+            kael::Shape shape(shapes + i * 8, shapes + i * 8 + ranks[i]);
+            kael::Tensor base = host_tensor(datas[i], shape, to_dtype(dtypes[i]));
+            inputs.push_back(view_of(base.to(dev), views[i]));
+        }
+        const kael::Tensor result = run_golden_op(op, inputs, CaseArgs(args)).cpu().contiguous();
+        const int64_t bytes = result.numel() * kael::element_size(result.dtype());
+        if (bytes > out_bytes) throw kael::Error("golden output buffer too small");
+        std::memcpy(out, result.data_ptr_raw(), static_cast<std::size_t>(bytes));
+        *out_dtype = static_cast<int>(result.dtype());
+        *out_rank = static_cast<int>(result.dim());
+        for (int d = 0; d < result.dim(); ++d) out_shape[d] = result.size(d);
+        written = bytes;
+    });
+    return written;
+}
+
+int ref_device_available(void) { return kael::cuda_is_available() ? 1 : 0; }
+
+} // extern "C"

@@ -1,0 +1,178 @@
+"""Shared test helpers: library loading, golden-case runner and comparison rules.
+
+Loads (never builds) the backend library and the test oracles:
+  kael.cpp_amd/lib/libkd.so         the MI355X backend (the thing under test)
+  oracle/build/liboracle.so         C restatement of the reference device semantics (checker)
+  oracle/_ref/libkael_*.so          the reference kael core with one of three device backends
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+from ctypes import POINTER, c_char_p, c_double, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT / "kael.cpp_amd"))
+
+import kd  # noqa: E402  (the package directory name is not an identifier)
+
+GOLDEN = ROOT / "tests" / "golden"
+ORACLE_LIB = ROOT / "oracle" / "build" / "liboracle.so"
+REF_DIR = ROOT / "oracle" / "_ref"
+
+
+def cpu_has_avx512() -> bool:
+    try:
+        flags = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return False
+    return " avx512f" in flags and " avx512bw" in flags and " avx512vl" in flags
+
+
+def ref_path(variant: str) -> Path:
+    """variant: 'ref' (reference emulation backend), 'oracle', 'hip'."""
+    if variant == "ref":
+        return REF_DIR / ("libkael_ref-v4.so" if cpu_has_avx512() else "libkael_ref-v3.so")
+    return REF_DIR / f"libkael_{variant}.so"
+
+
+ORACLE_SIGS = dict(kd.SIGNATURES)
+ORACLE_SIGS["matmul"] = (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.MatmulSizes), c_int])
+ORACLE_SIGS["last_error"] = (c_char_p, [])
+
+
+def load_oracle() -> ctypes.CDLL:
+    lib = ctypes.CDLL(str(ORACLE_LIB))
+    kd.bind(lib, "oracle_", ORACLE_SIGS)
+    return lib
+
+
+REF_SIGS = {
+    "last_error": (c_char_p, []),
+    "set_threads": (None, [c_int64]),
+    "get_threads": (c_int64, []),
+    "dev_fill": (c_int, [c_int, c_void_p, c_int64, c_void_p]),
+    "dev_convert": (c_int, [c_int, c_int, POINTER(kd.ElementLayout)]),
+    "dev_elementwise": (c_int, [c_int, c_int, c_int, POINTER(kd.ElementLayout), kd.ElementParameters]),
+    "dev_reduce": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "dev_matmul": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.MatmulSizes)]),
+    "dev_gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.IndexLayout)]),
+    "dev_scatter_add": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.IndexLayout)]),
+    "coalesce": (c_int, [c_int, c_int, POINTER(c_int64), POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)]),
+    "matmul": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64]),
+    "softmax": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int]),
+    "layer_norm": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
+    "cross_entropy": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
+    "cross_entropy_grad": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
+    "gelu_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int]),
+    "uniform_pm1": (c_int, [ctypes.c_uint64, c_int64, c_void_p]),
+    "time_matmul": (c_int, [c_int64, c_int64, c_int64, c_int, POINTER(c_double)]),
+    "time_c2": (c_int, [c_int, c_int64, c_int64, c_int, POINTER(c_double)]),
+    "gpt_create": (c_void_p, [c_int64, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_int]),
+    "gpt_destroy": (None, [c_void_p]),
+    "gpt_param_count": (c_int64, [c_void_p]),
+    "gpt_param": (c_int, [c_void_p, c_int64, c_char_p, c_int, POINTER(c_int64), POINTER(c_int), c_void_p]),
+    "gpt_forward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "gpt_cached_logits": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "gpt_generate": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
+    "golden": (c_int64, [c_char_p, c_char_p, c_int, POINTER(c_void_p), POINTER(c_int), POINTER(c_int),
+                         POINTER(c_int64), POINTER(c_char_p), c_int, c_void_p, c_int64, POINTER(c_int),
+                         POINTER(c_int), POINTER(c_int64)]),
+    "device_available": (c_int, []),
+}
+
+
+def load_ref(variant: str = "ref") -> ctypes.CDLL:
+    path = ref_path(variant)
+    lib = ctypes.CDLL(str(path), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+    kd.bind(lib, "ref_", REF_SIGS)
+    return lib
+
+
+def ref_error(lib) -> str:
+    m = lib.ref_last_error()
+    return m.decode() if m else ""
+
+
+def ptr(a: np.ndarray) -> c_void_p:
+    return a.ctypes.data_as(c_void_p)
+
+
+# ---- golden manifest ----------------------------------------------------------------------
+
+NPY_TO_CODE = {np.dtype(np.float32): kd.F32, np.dtype(np.float64): kd.F64,
+               np.dtype(np.int64): kd.I64, np.dtype(np.bool_): kd.BOOL}
+
+
+def golden_cases():
+    cases = []
+    for line in (GOLDEN / "manifest.txt").read_text().splitlines():
+        if not line.strip():
+            continue
+        fields = dict(tok.split("=", 1) for tok in line.split())
+        cases.append(fields)
+    return cases
+
+
+def run_golden(lib, case: dict, device: int):
+    """Runs one golden case through kael's API in `lib`; returns (array, expected)."""
+    op, name = case["op"], case["case"]
+    inputs = case["inputs"].split(",")
+    arrays = [np.load(GOLDEN / op / f"{name}_{i}.npy") for i in inputs]
+    arrays = [np.require(a.astype(np.uint8) if a.dtype == np.bool_ else a, requirements="C") for a in arrays]
+    n = len(arrays)
+    datas = (c_void_p * n)(*[a.ctypes.data for a in arrays])
+    dtypes = (c_int * n)(*[kd.DTYPE_OF[a.dtype] for a in arrays])
+    ranks = (c_int * n)(*[a.ndim for a in arrays])
+    shapes = (c_int64 * (8 * n))()
+    for i, a in enumerate(arrays):
+        for d, s in enumerate(a.shape):
+            shapes[8 * i + d] = s
+    views = (c_char_p * n)(*[case[f"view_{i}"].encode() for i in inputs])
+    expected = np.load(GOLDEN / op / f"{name}_out.npy")
+    capacity = max(1024, expected.nbytes * 8 + 1024)
+    out = np.zeros(capacity, np.uint8)
+    odt, orank = c_int(), c_int()
+    oshape = (c_int64 * 8)()
+    nbytes = lib.ref_golden(op.encode(), case["args"].encode(), n, datas, dtypes, ranks, shapes, views, device,
+                            ptr(out), capacity, ctypes.byref(odt), ctypes.byref(orank), oshape)
+    if nbytes < 0:
+        raise RuntimeError(f"{op}/{name}: {ref_error(lib)}")
+    dtype = kd.NUMPY_DTYPE[odt.value]
+    shape = tuple(oshape[d] for d in range(orank.value))
+    result = out[:nbytes].view(dtype).reshape(shape)
+    if dtype == np.uint8:
+        result = result.astype(np.bool_)
+    return result, expected
+
+
+def golden_close(actual: np.ndarray, expected: np.ndarray, rtol=None, atol=None) -> tuple[bool, str]:
+    """The reference's allclose (tests/support/allclose.h:21-32) with equal_nan, default
+    tolerances f32 1e-5/1e-6, f64 1e-12/1e-14, exact for int64/bool."""
+    if actual.shape != expected.shape:
+        return False, f"shape {actual.shape} != {expected.shape}"
+    if actual.dtype != expected.dtype:
+        return False, f"dtype {actual.dtype} != {expected.dtype}"
+    if expected.dtype in (np.int64, np.bool_):
+        ok = np.array_equal(actual, expected)
+        return ok, "" if ok else "integer mismatch"
+    if rtol is None:
+        rtol, atol = (1e-5, 1e-6) if expected.dtype == np.float32 else (1e-12, 1e-14)
+    a = actual.astype(np.float64)
+    e = expected.astype(np.float64)
+    nan = np.isnan(a) | np.isnan(e)
+    both_nan = np.isnan(a) & np.isnan(e)
+    inf = np.isinf(a) | np.isinf(e)
+    ok = np.ones(a.shape, bool)
+    ok[nan] = both_nan[nan]
+    fin = ~nan & ~inf
+    ok[inf & ~nan] = a[inf & ~nan] == e[inf & ~nan]
+    ok[fin] = np.abs(a[fin] - e[fin]) <= atol + rtol * np.abs(e[fin])
+    if ok.all():
+        return True, ""
+    idx = np.argwhere(~ok)[0]
+    return False, f"first mismatch at {tuple(idx)}: {a[tuple(idx)]} vs {e[tuple(idx)]} ({(~ok).sum()} bad)"

@@ -1,0 +1,84 @@
+"""kd_gather / kd_scatter_add against the C oracle (reference src/cuda/kernels.inl:179-221).
+
+Covers the embedding lookup of GPT-2 decode ([1]/[64] token ids into [50257,768] and [1024,768]),
+gather along an inner axis with a transposed index tensor (tests/test_cuda.cpp:365-384) and
+i64 scatter_add wrapping (:482-490). Gather is bit-exact; f32 scatter_add with colliding indices
+adds in a different order than the oracle (atomics), so it is checked to 1e-5.
+"""
+import numpy as np
+import pytest
+
+import kd
+import support
+
+pytestmark = pytest.mark.gpu
+
+
+def index_layout(shape, axis, data_strides, index_strides, source_strides):
+    lay = kd.IndexLayout()
+    lay.dims = len(shape)
+    lay.axis = axis
+    lay.count = int(np.prod(shape))
+    for d in range(len(shape)):
+        lay.shape[d] = shape[d]
+        lay.data_strides[d] = data_strides[d]
+        lay.index_strides[d] = index_strides[d]
+        lay.source_strides[d] = source_strides[d]
+    return lay
+
+
+@pytest.mark.parametrize("tokens", [1, 64])
+def test_embedding_gather(kdb, oracle, tokens):
+    rng = np.random.default_rng(tokens)
+    vocab, dim = 50257, 768
+    table = rng.normal(0, 0.02, (vocab, dim)).astype(np.float32)
+    ids = rng.integers(0, vocab, tokens).astype(np.int64)
+    # index_select(weight, 0, ids) -> gather over shape [tokens, dim], axis 0 (indexing.cpp:109-118)
+    lay = index_layout((tokens, dim), 0, (dim, 1), (1, 0), (dim, 1))
+    want = np.empty((tokens, dim), np.float32)
+    assert oracle.oracle_gather(kd.F32, support.ptr(want), support.ptr(table), support.ptr(ids), lay) == 0
+    dt, di, do = kdb.to_device(table), kdb.to_device(ids), kdb.empty((tokens, dim), np.float32)
+    kdb.call("gather", kd.F32, do.ptr, dt.ptr, di.ptr, lay)
+    np.testing.assert_array_equal(do.numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64, kd.BOOL], ids=["f32", "f64", "i64", "bool"])
+def test_gather_inner_axis_transposed_indices(kdb, oracle, dtype):
+    rng = np.random.default_rng(dtype)
+    npd = kd.NUMPY_DTYPE[dtype]
+    data = (rng.normal(size=(6, 5)) * 10).astype(npd)
+    idx = rng.integers(0, 5, (3, 6)).astype(np.int64)  # used transposed: shape [6, 3], strides (1, 6)
+    lay = index_layout((6, 3), 1, (5, 1), (1, 6), (3, 1))
+    want = np.empty((6, 3), npd)
+    assert oracle.oracle_gather(dtype, support.ptr(want), support.ptr(data), support.ptr(idx), lay) == 0
+    dd, di, do = kdb.to_device(data), kdb.to_device(idx), kdb.empty((6, 3), npd)
+    kdb.call("gather", dtype, do.ptr, dd.ptr, di.ptr, lay)
+    np.testing.assert_array_equal(do.numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64], ids=["f32", "f64", "i64"])
+def test_scatter_add(kdb, oracle, dtype):
+    rng = np.random.default_rng(10 + dtype)
+    npd = kd.NUMPY_DTYPE[dtype]
+    rows, dim, n = 96, 256, 4096  # char-GPT embedding gradient: index_add_ of [4096,256] into [96,256]
+    target = np.zeros((rows, dim), npd)
+    ids = rng.integers(0, rows, n).astype(np.int64)
+    src = (rng.normal(size=(n, dim)) * 4).astype(npd) if dtype != kd.I64 else rng.integers(-9, 9, (n, dim)).astype(np.int64)
+    lay = index_layout((n, dim), 0, (dim, 1), (1, 0), (dim, 1))
+    want = target.copy()
+    assert oracle.oracle_scatter_add(dtype, support.ptr(want), support.ptr(ids), support.ptr(src), lay) == 0
+    dtgt, di, ds = kdb.to_device(target), kdb.to_device(ids), kdb.to_device(src)
+    kdb.call("scatter_add", dtype, dtgt.ptr, di.ptr, ds.ptr, lay)
+    got = dtgt.numpy()
+    if dtype == kd.I64:
+        np.testing.assert_array_equal(got, want)
+    else:
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4)
+
+
+def test_int64_scatter_add_wraps(kdb):
+    target = kdb.to_device(np.array([2**63 - 1], np.int64))
+    ids = kdb.to_device(np.array([0], np.int64))
+    src = kdb.to_device(np.array([1], np.int64))
+    kdb.call("scatter_add", kd.I64, target.ptr, ids.ptr, src.ptr, index_layout((1,), 0, (1,), (1,), (1,)))
+    assert target.numpy()[0] == -(2**63)

@@ -1,0 +1,113 @@
+"""kd_matmul / kd_matmul_strided against the C oracle.
+
+Shapes: the reference's CudaMatmul list (tests/test_cuda.cpp:324-341), batched / vector /
+integer / transposed cases (:343-355), BASELINE config C1 (512^3, uniform[-1,1]) and the GPT-2
+decode and char-GPT training shapes. f32 and f64 use the reference device
+tolerance rtol = atol = 1e-4 (tests/test_cuda.cpp:40-43) against a double-accumulated product;
+i64 is exact with wrapping.
+"""
+import numpy as np
+import pytest
+
+import kd
+import support
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1, 1), (4, 4, 4), (5, 3, 9), (8, 16, 7), (33, 20, 65), (64, 1, 64), (1, 64, 1),
+          (512, 512, 512), (1, 768, 2304), (1, 3072, 768), (16, 768, 768), (130, 257, 129),
+          (1000, 768, 1), (300, 64, 3), (64, 784, 128), (256, 128, 768)]
+
+
+def reference_product(a, b):
+    return np.matmul(a.astype(np.float64), b.astype(np.float64))
+
+
+def close(got, want, rtol=1e-4, atol=1e-4):
+    err = np.abs(got.astype(np.float64) - want)
+    bad = err > atol + rtol * np.abs(want)
+    assert not bad.any(), f"{bad.sum()} elements off; worst {err.max()}"
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64], ids=["f32", "f64"])
+@pytest.mark.parametrize("m,k,n", SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in SHAPES])
+def test_matmul_matches(kdb, dtype, m, k, n):
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    npd = kd.NUMPY_DTYPE[dtype]
+    a = rng.uniform(-1, 1, (m, k)).astype(npd)
+    b = rng.uniform(-1, 1, (k, n)).astype(npd)
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((m, n), npd)
+    kdb.call("matmul", dtype, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(1, m, k, n))
+    close(dc.numpy(), reference_product(a, b))
+
+
+def test_c1_config_matches_kael_cpu_order(kdb, oracle):
+    """C1: manual_seed(0)-style uniform[-1,1] 512^3, against the oracle's reference device order."""
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    b = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    want = np.empty((512, 512), np.float32)
+    sizes = kd.MatmulSizes(1, 512, 512, 512)
+    assert oracle.oracle_matmul(kd.F32, support.ptr(a), support.ptr(b), support.ptr(want), sizes, 0) == 0
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((512, 512), np.float32)
+    kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, sizes)
+    close(dc.numpy(), want.astype(np.float64))
+
+
+def test_batched_and_integer(kdb, oracle):
+    rng = np.random.default_rng(3)
+    a = rng.normal(size=(6, 4, 5)).astype(np.float32)
+    b = rng.normal(size=(6, 5, 6)).astype(np.float32)
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((6, 4, 6), np.float32)
+    kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(6, 4, 5, 6))
+    close(dc.numpy(), reference_product(a, b))
+    i = rng.integers(-5, 5, (3, 6, 6)).astype(np.int64)
+    i[0, 0, 0] = 2**62
+    di, do = kdb.to_device(i), kdb.empty((3, 6, 6), np.int64)
+    kdb.call("matmul", kd.I64, di.ptr, di.ptr, do.ptr, kd.MatmulSizes(3, 6, 6, 6))
+    want = np.empty((3, 6, 6), np.int64)
+    assert oracle.oracle_matmul(kd.I64, support.ptr(i), support.ptr(i), support.ptr(want), kd.MatmulSizes(3, 6, 6, 6), 0) == 0
+    np.testing.assert_array_equal(do.numpy(), want)
+
+
+def test_bool_is_rejected_and_empty_is_zero(kdb):
+    x = kdb.to_device(np.ones(4, np.uint8))
+    with pytest.raises(kd.KdError):
+        kdb.call("matmul", kd.BOOL, x.ptr, x.ptr, x.ptr, kd.MatmulSizes(1, 2, 2, 1))
+    out = kdb.to_device(np.full((3, 2), 9.0, np.float32))
+    kdb.call("matmul", kd.F32, out.ptr, out.ptr, out.ptr, kd.MatmulSizes(1, 3, 0, 2))
+    np.testing.assert_array_equal(out.numpy(), np.zeros((3, 2), np.float32))
+
+
+# (batches, M, K, N, a strides, b strides): transposed / batch-broadcast operands read in place.
+STRIDED = [
+    ("wT", 1, 64, 256, 768, (0, 256, 1), (0, 1, 256)),       # x . W^T with W [768, 256] row-major
+    ("aT", 1, 256, 128, 96, (0, 1, 256), (0, 96, 1)),         # X^T . g
+    ("both", 1, 130, 70, 200, (0, 1, 130), (0, 1, 70)),
+    ("bcast", 4, 64, 128, 192, (64 * 128, 128, 1), (0, 1, 128)),  # batch-broadcast W^T
+    ("decode", 1, 1, 768, 2304, (0, 768, 1), (0, 1, 768)),
+    ("generic", 2, 33, 17, 40, (17 * 33 * 2, 1, 33 * 2), (0, 40 * 3, 3)),
+]
+
+
+@pytest.mark.parametrize("case", STRIDED, ids=[c[0] for c in STRIDED])
+def test_strided_operands(kdb, oracle, case):
+    name, batches, m, k, n, sa, sb = case
+    rng = np.random.default_rng(len(name))
+
+    def extent(shape, st):
+        return 1 + sum((s - 1) * t for s, t in zip(shape, st))
+
+    a_store = rng.uniform(-1, 1, extent((batches, m, k), sa)).astype(np.float32)
+    b_store = rng.uniform(-1, 1, extent((batches, k, n), sb)).astype(np.float32)
+    so = (m * n, n, 1)
+    strides = kd.MatmulStrides()
+    for i in range(3):
+        strides.a[i], strides.b[i], strides.out[i] = sa[i], sb[i], so[i]
+    sizes = kd.MatmulSizes(batches, m, k, n)
+    want = np.empty((batches, m, n), np.float32)
+    assert oracle.oracle_matmul_strided(kd.F32, support.ptr(a_store), support.ptr(b_store), support.ptr(want),
+                                        sizes, strides) == 0
+    da, db, dc = kdb.to_device(a_store), kdb.to_device(b_store), kdb.empty((batches, m, n), np.float32)
+    kdb.call("matmul_strided", kd.F32, da.ptr, db.ptr, dc.ptr, sizes, strides)
+    close(dc.numpy(), want.astype(np.float64))
