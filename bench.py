@@ -144,6 +144,18 @@ def bench_rows(backend, steps, warmup):
     return out
 
 
+def bench_copy(backend, steps, warmup, mib=256):
+    """Plain contiguous f32 copy (kd_convert f32->f32) of `mib` MiB: the calibration kernel for
+    HBM byte counters (it must read and write exactly `mib` MiB each)."""
+    n = mib * (1 << 20) // 4
+    src = backend.to_device(np.ones(n, np.float32))
+    dst = backend.empty((n,), np.float32)
+    lay = kd.element_layout((n,), [(4,), (4,)], [dst.ptr, src.ptr])
+    fn = backend.lib.kd_convert
+    ms, _ = time_steps(backend, lambda i: fn(kd.F32, kd.F32, ctypes.byref(lay)), steps, warmup)
+    return {"us": ms * 1e3, "bytes_per_launch": 2 * n * 4, "gbps": 2 * n * 4 / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(n, budget_s=20.0):
     """kael's CPU matmul (reference build, threaded) on a bounded sample of the same workload."""
     sys.path.insert(0, str(ROOT / "tests"))
@@ -171,7 +183,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="")
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "copy", "c2", "rows"],
+                    help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend drives one GPU; multi-GPU runs are out of scope (bench.py --gpus 1)"}))
@@ -181,8 +194,16 @@ def main() -> int:
         raise SystemExit(f"no usable gfx950 device: {backend.error()}")
     info = backend.device_info()
     n = 4096
-    main_run = bench_matmul(backend, n, args.steps, args.warmup)
     extra = {"device": info}
+    if args.only == "copy":
+        extra["copy"] = bench_copy(backend, args.steps, args.warmup)
+        print(json.dumps({"metric": "copy calibration", "extra": extra}))
+        return 0
+    if args.only in ("c2", "rows"):
+        extra[args.only] = (bench_c2 if args.only == "c2" else bench_rows)(backend, args.steps, args.warmup)
+        print(json.dumps({"metric": f"{args.only} only", "extra": extra}))
+        return 0
+    main_run = bench_matmul(backend, n, args.steps, args.warmup)
     if args.only in ("", "all"):
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup)
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)

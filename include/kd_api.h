@@ -171,8 +171,8 @@ int kd_convert(int out_dtype, int in_dtype, const kd_element_layout* layout);
 
 /* reference device_kernels.h:107-108 `elementwise(ElementOp, DType out, DType in,
  * const ElementLayout&, ElementParameters)`. As in the reference, the output dtype
- * is implied by the op (In for arithmetic, Bool for comparisons) and `out_dtype`
- * is only checked for consistency. */
+ * is implied by the op (In for arithmetic, Bool for comparisons) and `out_dtype` is
+ * ignored (kernels.inl:335). */
 int kd_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout* layout,
                    kd_element_parameters parameters);
 
@@ -254,6 +254,42 @@ int kd_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_
  * shapes/strides are [operands][KD_MAX_DIMS] arrays of ELEMENT counts. Host only. */
 int kd_layout_build(kd_element_layout* out, int operands, const int* ranks, const int64_t* shapes,
                     const int64_t* strides, const int* element_sizes, void* const* bases);
+
+/* ---- GPT-2 decode engine (config C5) ---------------------------------------- */
+
+/* The workload of reference examples/gpt2_generate.cpp: kael's GPT (src/nn/transformer.cpp:
+ * 103-237) run by nn::generate with temperature 0 and a KV cache (:256-295), batch 1, f32.
+ * No single reference function corresponds: kael composes it from ~700 device calls per
+ * token. This engine keeps kael's parameter layout and arithmetic (LayerNorm = standardize
+ * then affine, Linear = x.W^T then + bias, tanh GELU, scores / sqrt(head_dim), row softmax
+ * with a double sum, greedy first-maximum argmax) and runs each token as one HIP graph. */
+typedef struct kd_gpt_config {
+    int64_t vocab_size;    /* GptConfig::vocab_size (include/kael/nn/transformer.h:19-30) */
+    int64_t max_positions; /* GptConfig::max_positions */
+    int64_t layers;
+    int64_t heads;
+    int64_t dimension;
+    int32_t tanh_gelu;     /* GptConfig::tanh_gelu */
+    int32_t reserved;
+} kd_gpt_config;
+
+int kd_gpt_create(void** handle, const kd_gpt_config* config);
+void kd_gpt_destroy(void* handle);
+/* Uploads one parameter by its kael name (GPT::named_parameters(), e.g. "blocks.3.attn.qkv.weight")
+ * from host f32 data holding all `count` elements in kael's row-major layout. */
+int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int64_t count);
+/* Runs the prompt (positions 0..length-1) through the cached forward; the last position's
+ * greedy token becomes the first generated token. Clears any previous sequence. */
+int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length);
+/* Generates `count` more tokens greedily, one cached step each (decode). `tokens` (host, may be
+ * NULL) receives the `count` new ids. The total sequence may not exceed max_positions + 1. */
+int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens);
+/* Teacher-forced cached forward over `count` tokens starting at position 0; writes the logits
+ * of every position (count x vocab, host). Used for step-by-step parity. */
+int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, float* logits);
+/* The full sequence so far (prompt + generated), `capacity` entries at most; returns its length
+ * through `length`. */
+int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* length);
 
 /* ---- measurement helpers (no reference counterpart; used by the bench) -- */
 
