@@ -156,6 +156,90 @@ def bench_copy(backend, steps, warmup, mib=256):
     return {"us": ms * 1e3, "bytes_per_launch": 2 * n * 4, "gbps": 2 * n * 4 / (ms * 1e-3) / 1e9}
 
 
+def gpt2_weights(seed=4):
+    """Random-init GPT-2 small in kael's layout: N(0, 0.02) weights, residual projections
+    N(0, 0.02/sqrt(2*layers)), LayerNorm gain 1 / bias 0, Linear biases 0
+    (reference src/nn/transformer.cpp:187-207)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, shape in kd.gpt2_parameter_shapes():
+        if name.endswith("ln1.weight") or name.endswith("ln2.weight") or name == "ln_final.weight":
+            a = np.ones(shape, np.float32)
+        elif name.endswith(".bias"):
+            a = np.zeros(shape, np.float32)
+        else:
+            std = 0.02 / np.sqrt(24.0) if (name.endswith("attn.proj.weight") or name.endswith("mlp.fc2.weight")) else 0.02
+            a = rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+        out.append((name, a))
+    return out
+
+
+def bench_gpt2(backend, prompt_len=64, new_tokens=256, repeats=3, eager=False):
+    """C5: greedy decode with the KV cache. Prefill = the prompt's forward producing token 1;
+    decode = the new_tokens - 1 single-token steps that follow. `eager` launches each step's
+    kernels directly instead of replaying the captured graph (for kernel-level profiling)."""
+    g = kd.Gpt(backend, eager=eager)
+    weights = gpt2_weights()
+    for name, a in weights:
+        g.load(name, a)
+    params = sum(a.size for _, a in weights)
+    prompt = np.random.default_rng(4).integers(0, 50257, prompt_len)
+    g.prefill(prompt)  # warm-up (graph instantiation)
+    g.decode(8)
+    best = None
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        g.prefill(prompt)
+        g.decode(0)
+        t1 = time.perf_counter()
+        g.decode(new_tokens - 1)
+        t2 = time.perf_counter()
+        run = {"prefill_ms": (t1 - t0) * 1e3, "decode_s": t2 - t1}
+        if best is None or run["decode_s"] < best["decode_s"]:
+            best = run
+    steps = new_tokens - 1
+    ms_tok = best["decode_s"] / steps * 1e3
+    # Per decode step: every weight except the position table is read once (the head reuses the
+    # token table), plus the KV cache read by attention (mean over the decode steps).
+    weight_bytes = 4 * (params - 1024 * 768)
+    mean_ctx = prompt_len + steps / 2
+    kv_bytes = 2 * 12 * 4 * 768 * mean_ctx
+    return {"prefill_ms": best["prefill_ms"], "decode_tok_s": steps / best["decode_s"], "ms_per_token": ms_tok,
+            "bytes_per_token": weight_bytes + kv_bytes,
+            "achieved_gbps": (weight_bytes + kv_bytes) / (ms_tok * 1e-3) / 1e9,
+            "frac_hbm": (weight_bytes + kv_bytes) / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "config": f"GPT-2 small f32, prompt {prompt_len}, {new_tokens} new tokens, batch 1, greedy, KV cache; "
+                      "wall clock around kd_gpt_decode (one HIP graph per token)",
+            "sequence_head": g.sequence()[prompt_len:prompt_len + 8].tolist()}
+
+
+def cpu_gpt2_baseline(new_tokens=8):
+    """kael's own nn::generate on the CPU path (reference build), GPT-2 small, seed 4: decode
+    tokens/s from two runs (1 and 1 + new_tokens new tokens) so prefill cancels out."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import support
+
+    lib = support.load_ref("ref")
+    threads = int(os.environ.get("KAEL_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    lib.ref_set_threads(threads)
+    h = lib.ref_gpt_create(50257, 1024, 12, 12, 768, 4, 1)
+    prompt = np.ascontiguousarray(np.random.default_rng(4).integers(0, 50257, 64), np.int64)
+    out = np.zeros(64 + 1 + new_tokens, np.int64)
+    t1, t2 = ctypes.c_double(), ctypes.c_double()
+    try:
+        if lib.ref_gpt_generate(h, prompt.ctypes.data_as(ctypes.c_void_p), 64, 1, out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(t1)):
+            raise RuntimeError(support.ref_error(lib))
+        if lib.ref_gpt_generate(h, prompt.ctypes.data_as(ctypes.c_void_p), 64, 1 + new_tokens,
+                                out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(t2)):
+            raise RuntimeError(support.ref_error(lib))
+    finally:
+        lib.ref_gpt_destroy(h)
+    rate = new_tokens / max(t2.value - t1.value, 1e-9)
+    return {"value": rate, "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"kael nn::generate GPT-2 small f32 (seed 4), prompt 64, decode rate from {new_tokens} extra tokens, "
+                      f"prefill {t1.value:.2f} s", "prefill_s": t1.value}
+
+
 def cpu_baseline(n, budget_s=20.0):
     """kael's CPU matmul (reference build, threaded) on a bounded sample of the same workload."""
     sys.path.insert(0, str(ROOT / "tests"))
@@ -183,7 +267,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", choices=["", "all", "matmul", "copy", "c2", "rows"],
+    ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "copy", "c2", "rows", "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -199,6 +284,10 @@ def main() -> int:
         extra["copy"] = bench_copy(backend, args.steps, args.warmup)
         print(json.dumps({"metric": "copy calibration", "extra": extra}))
         return 0
+    if args.only == "gpt2":
+        extra["gpt2_decode"] = bench_gpt2(backend, eager=args.gpt_eager)
+        print(json.dumps({"metric": "GPT-2-small decode tok/s", "extra": extra}))
+        return 0
     if args.only in ("c2", "rows"):
         extra[args.only] = (bench_c2 if args.only == "c2" else bench_rows)(backend, args.steps, args.warmup)
         print(json.dumps({"metric": f"{args.only} only", "extra": extra}))
@@ -208,12 +297,20 @@ def main() -> int:
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup)
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
         extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
+        extra["gpt2_decode"] = bench_gpt2(backend)
     cpu = None
     if not args.no_cpu:
         try:
             cpu = cpu_baseline(n)
         except Exception as e:  # the baseline is reported, never required
             cpu = {"error": str(e)}
+        if "gpt2_decode" in extra:
+            try:
+                gcpu = cpu_gpt2_baseline()
+                extra["gpt2_decode"]["cpu_baseline"] = gcpu
+                extra["gpt2_decode"]["speedup_vs_cpu"] = extra["gpt2_decode"]["decode_tok_s"] / gcpu["value"]
+            except Exception as e:
+                extra["gpt2_decode"]["cpu_baseline"] = {"error": str(e)}
     achieved = main_run["tflops"]
     line = {
         "metric": "f32 matmul TFLOP/s (% FP32 MFMA peak)",

@@ -270,8 +270,10 @@ typedef struct kd_gpt_config {
     int64_t heads;
     int64_t dimension;
     int32_t tanh_gelu;     /* GptConfig::tanh_gelu */
-    int32_t reserved;
+    int32_t flags;         /* KD_GPT_EAGER: launch each step's kernels directly instead of
+                              replaying the captured graph (for kernel-level profiling) */
 } kd_gpt_config;
+#define KD_GPT_EAGER 1
 
 int kd_gpt_create(void** handle, const kd_gpt_config* config);
 void kd_gpt_destroy(void* handle);

@@ -1,0 +1,790 @@
+// kd_gpt2.hip - GPT-2 greedy decode engine (benchmark config C5) for gfx950.
+//
+// Workload of reference examples/gpt2_generate.cpp: kael's GPT (src/nn/transformer.cpp:103-237)
+// generating greedily with a KV cache (nn::generate, :256-295), batch 1, f32. kael runs it as ~700
+// device calls per token with blocking host syncs (embedding index checks, host argmax). This
+// engine keeps kael's parameters in kael's layout and its arithmetic, and runs one token per
+// replay of a captured HIP graph:
+//
+//   embed       x = wte[token] + wpe[pos]                                      (1 launch)
+//   per layer   qkv GEMV on ln1(x) (+bias; K/V appended to the cache)
+//               -> attention split into 16 key chunks per head (chunk max, double sum of
+//                  exponentials, unnormalised weighted values)
+//               -> proj GEMV on the combined attention output (+bias, +residual into x)
+//               -> fc1 GEMV on ln2(x) (+bias, GELU)
+//               -> fc2 GEMV (+bias, +residual into x)                          (5 launches)
+//   head        ln_final -> logits = wte . h with per-workgroup best rows -> greedy pick of
+//               the first maximum, which writes the next token and advances the position in
+//               device memory                                                 (3 launches)
+// The LayerNorm feeding a GEMV is recomputed by each of its workgroups into LDS (768 values):
+// cheaper than a separate launch. A "last workgroup finishes" epilogue was measured and
+// rejected: same-address device-scope atomics serialise at about 100 ns each on this part.
+//
+// All step-dependent values (position, token) live in device memory, so the graph is static.
+// Weights keep kael's [out, in] row-major layout: every Linear is a row-dot GEMV reading whole
+// rows with 16-byte loads (the decode step is HBM-bound on ~494 MB of weights per token).
+// Rounding follows kael's op sequence: Linear rounds the product and then adds the bias;
+// LayerNorm rounds the standardised value, then multiplies, then adds; attention scores are
+// divided by sqrt(head_dim); softmax sums exponentials in double (src/ops/nn.cpp:60-71).
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct Step {
+    int64_t pos;     // position processed by the next step
+    int64_t forced;  // positions < forced take their token from `seq` (teacher forcing)
+};
+
+// ---- kernels -------------------------------------------------------------------------------
+
+__device__ __forceinline__ double block_sum_d(double v, double* scratch) {
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) v += __shfl_xor(v, m, 64);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int waves = blockDim.x / 64;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    double r = scratch[0];
+    for (int w = 1; w < waves; ++w) r += scratch[w];
+    return r;
+}
+
+// Whole-workgroup LayerNorm of x[0, d) into h: mean and population variance in double, the
+// standardised value rounded to float, then * w and + b, each rounded (reference
+// src/ops/nn.cpp:114-129 then src/nn/layers.cpp:67).
+__device__ void block_layernorm(const float* x, int64_t d, const float* w, const float* b, float* h) {
+    __shared__ double scratch[16];
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) s += static_cast<double>(x[i]);
+    const double mean = block_sum_d(s, scratch) / static_cast<double>(d);
+    double q = 0.0;
+    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
+        const double dv = static_cast<double>(x[i]) - mean;
+        q += dv * dv;
+    }
+    const double scale = std::sqrt(block_sum_d(q, scratch) / static_cast<double>(d) + 1e-5);
+    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
+        const float y = static_cast<float>((static_cast<double>(x[i]) - mean) / scale);
+        h[i] = __fadd_rn(__fmul_rn(y, w[i]), b[i]);
+    }
+}
+
+// x = wte[token] + wpe[pos].
+__global__ __launch_bounds__(kThreads) void embed_kernel(const Step* st, const int64_t* seq, const float* wte,
+                                                         const float* wpe, float* x, int64_t d) {
+    const int64_t pos = st->pos;
+    const int64_t tok = seq[pos];
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < d; i += static_cast<int64_t>(gridDim.x) * kThreads)
+        x[i] = __fadd_rn(wte[tok * d + i], wpe[pos * d + i]);
+}
+
+// h = LayerNorm(x) as one workgroup (the final LayerNorm before the head).
+__global__ __launch_bounds__(kThreads) void layernorm_kernel(const float* x, int64_t d, const float* w, const float* b,
+                                                             float* h) {
+    block_layernorm(x, d, w, b, h);
+}
+
+enum Epilogue { kStore = 0, kGeluTanh = 1, kGeluExact = 2, kResidual = 3, kQkv = 4, kHead = 5 };
+
+struct Best {
+    float v;
+    int64_t i;
+};
+
+// `a` wins over `b` if it is NaN-first, larger, or equal with a smaller index: the first
+// maximum, with the first NaN winning (reference best_position, src/ops/reduce.cpp:236-254).
+__device__ __forceinline__ bool better(const Best& a, const Best& b) {
+    const bool an = isnan(a.v), bn = isnan(b.v);
+    if (an || bn) return an && (!bn || a.i < b.i);
+    return a.v > b.v || (a.v == b.v && a.i < b.i);
+}
+
+__device__ __forceinline__ Best wave_best(Best v) {
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) {
+        Best o{__shfl_xor(v.v, m, 64), __shfl_xor(v.i, m, 64)};
+        if (better(o, v)) v = o;
+    }
+    return v;
+}
+
+constexpr int kAttnChunks = 8;
+
+struct AttnPartials {
+    float* m;      // [heads][chunks]
+    double* l;     // [heads][chunks]
+    float* acc;    // [heads][chunks][head_dim]
+};
+
+// Attention output of every head into h[0, heads * head_dim) from the chunk partials: with M the
+// maximum over a head's non-empty chunks (an empty chunk reports m = -inf, l = 0),
+// out = sum_c exp(m_c - M) acc_c / float(sum_c exp(m_c - M) l_c), the denominator being the
+// float rounding of a double sum as in reference src/ops/nn.cpp:60-71. Per-head factors are
+// staged in LDS, then every element issues its chunk loads together.
+constexpr int kMaxHeads = 64;
+
+__device__ void combine_attention(const AttnPartials& p, int64_t heads, int64_t head_dim, float* h) {
+    __shared__ float factor[kMaxHeads * kAttnChunks];
+    __shared__ float denom[kMaxHeads];
+    const int64_t slots = heads * kAttnChunks;
+    for (int64_t i = threadIdx.x; i < slots; i += blockDim.x) factor[i] = p.m[i];
+    __syncthreads();
+    for (int64_t hd = threadIdx.x; hd < heads; hd += blockDim.x) {
+        float M = -INFINITY;
+        bool any = false;
+        double lsum = 0.0;
+        float w[kAttnChunks];
+        double l[kAttnChunks];
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) l[c] = p.l[hd * kAttnChunks + c];
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) {
+            const float m = factor[hd * kAttnChunks + c];
+            if (!(m == -INFINITY && l[c] == 0.0)) {
+                M = any ? max_na(M, m) : m;
+                any = true;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) {
+            const float m = factor[hd * kAttnChunks + c];
+            const bool empty = m == -INFINITY && l[c] == 0.0;
+            w[c] = empty ? 0.f : std::exp(__fsub_rn(m, M));
+            if (!empty) lsum += static_cast<double>(w[c]) * l[c];
+        }
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) factor[hd * kAttnChunks + c] = w[c];
+        denom[hd] = static_cast<float>(lsum);
+    }
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < heads * head_dim; k += blockDim.x) {
+        const int64_t hd = k / head_dim;
+        const int64_t e = k - hd * head_dim;
+        float acc[kAttnChunks];
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) acc[c] = p.acc[(hd * kAttnChunks + c) * head_dim + e];
+        float num = 0.f;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) num += factor[hd * kAttnChunks + c] * acc[c];
+        h[k] = __fdiv_rn(num, denom[hd]);
+    }
+}
+
+struct GemvArgs {
+    const float* W;        // [N, K] row-major
+    const float* x;        // input vector [K]
+    const float* bias;     // [N] or nullptr
+    float* out;            // [N]
+    int64_t N, K;
+    // When ln_w is non-null the input is LayerNorm(x) with this weight and bias, computed by every
+    // workgroup into LDS (a 768-vector: cheaper than a separate launch).
+    const float* ln_w;
+    const float* ln_b;
+    // When attn.m is non-null the input is the attention output combined from chunk partials.
+    AttnPartials attn;
+    // kQkv: query -> q, key/value rows appended to this layer's cache at the current position
+    float* q;
+    float* kcache;
+    float* vcache;
+    int64_t d, head_dim, max_positions;
+    // kHead: per-workgroup argmax partials (argmax_final_kernel picks the winner)
+    float* best_v;
+    int64_t* best_i;
+    Step* st;
+};
+
+constexpr int kMaxK = 4096;
+
+// out[n] = epilogue(W[n, :] . x) for the rows of this workgroup. The input vector is staged in
+// LDS. Rows: WavesPerRow == 1 -> each wave
+// owns 2 rows (8 rows per workgroup); WavesPerRow == 4 -> the workgroup owns 2 rows and each wave
+// a quarter of K, combined through LDS.
+template <int Epi, int WavesPerRow>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+    __shared__ float4 hs4[kMaxK / 4];
+    __shared__ float part[4][2];
+    __shared__ float bv[kThreads / 64 * 2];
+    __shared__ int64_t bi[kThreads / 64 * 2];
+    float* hs = reinterpret_cast<float*>(hs4);
+    const int64_t K = a.K;
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    constexpr int rows_per_block = WavesPerRow == 1 ? 8 : 2;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * rows_per_block + (WavesPerRow == 1 ? 2 * wave : 0);
+    const int64_t k4 = K / 4;
+    const int64_t kb = WavesPerRow == 1 ? 0 : (k4 * wave) / 4;
+    const int64_t ke = WavesPerRow == 1 ? k4 : (k4 * (wave + 1)) / 4;
+    const bool has0 = n0 < a.N;
+    const bool has1 = n0 + 1 < a.N;
+    const float4* w0 = reinterpret_cast<const float4*>(a.W + (has0 ? n0 : 0) * K);
+    const float4* w1 = reinterpret_cast<const float4*>(a.W + (has1 ? n0 + 1 : (has0 ? n0 : 0)) * K);
+    // Issue this lane's first weight loads before the input prologue so that their HBM latency
+    // overlaps it.
+    constexpr int kPrefetch = 4;
+    float4 pw0[kPrefetch], pw1[kPrefetch];
+#pragma unroll
+    for (int i = 0; i < kPrefetch; ++i) {
+        const int64_t k = kb + lane + 64 * i;
+        if (has0 && k < ke) {
+            pw0[i] = w0[k];
+            pw1[i] = w1[k];
+        }
+    }
+    if (a.ln_w != nullptr) {
+        block_layernorm(a.x, K, a.ln_w, a.ln_b, hs);
+    } else if (a.attn.m != nullptr) {
+        combine_attention(a.attn, K / a.head_dim, a.head_dim, hs);
+    } else {
+        for (int64_t k = threadIdx.x; k < K; k += kThreads) hs[k] = a.x[k];
+    }
+    __syncthreads();
+
+    float a0 = 0.f, a1 = 0.f;
+    if (has0) {
+#pragma unroll
+        for (int i = 0; i < kPrefetch; ++i) {
+            const int64_t k = kb + lane + 64 * i;
+            if (k < ke) {
+                const float4 xx = hs4[k];
+                a0 += pw0[i].x * xx.x + pw0[i].y * xx.y + pw0[i].z * xx.z + pw0[i].w * xx.w;
+                a1 += pw1[i].x * xx.x + pw1[i].y * xx.y + pw1[i].z * xx.z + pw1[i].w * xx.w;
+            }
+        }
+        for (int64_t k = kb + lane + 64 * kPrefetch; k < ke; k += 64) {
+            const float4 xx = hs4[k];
+            const float4 p = w0[k];
+            const float4 r = w1[k];
+            a0 += p.x * xx.x + p.y * xx.y + p.z * xx.z + p.w * xx.w;
+            a1 += r.x * xx.x + r.y * xx.y + r.z * xx.z + r.w * xx.w;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) {
+        a0 += __shfl_xor(a0, m, 64);
+        a1 += __shfl_xor(a1, m, 64);
+    }
+    if constexpr (WavesPerRow == 4) {
+        if (lane == 0) {
+            part[wave][0] = a0;
+            part[wave][1] = a1;
+        }
+        __syncthreads();
+        a0 = ((part[0][0] + part[1][0]) + part[2][0]) + part[3][0];
+        a1 = ((part[0][1] + part[1][1]) + part[2][1]) + part[3][1];
+    }
+    // lanes 0 and 1 of the owning wave finish rows n0 and n0 + 1
+    const bool owner = WavesPerRow == 1 || wave == 0;
+    const bool active = owner && lane < 2 && (lane == 0 ? has0 : has1);
+    const int64_t n = n0 + lane;
+    float y = 0.f;
+    if (active) {
+        const float dot = lane == 0 ? a0 : a1;
+        y = Epi == kHead ? dot : __fadd_rn(dot, a.bias[n]);
+        if constexpr (Epi == kGeluTanh) {
+            const float scale = std::sqrt(2 / MathConst<float>::pi);
+            y = 0.5f * y * (1 + std::tanh(scale * (y + 0.044715f * y * y * y)));
+        } else if constexpr (Epi == kGeluExact) {
+            y = 0.5f * y * (1 + std::erf(y / MathConst<float>::sqrt2));
+        } else if constexpr (Epi == kResidual) {
+            y = __fadd_rn(a.out[n], y);
+        }
+        if constexpr (Epi == kQkv) {
+            const int64_t part_id = n / a.d;
+            const int64_t within = n - part_id * a.d;
+            if (part_id == 0) {
+                a.q[within] = y;
+            } else {
+                const int64_t head = within / a.head_dim;
+                const int64_t dim = within - head * a.head_dim;
+                float* cache = part_id == 1 ? a.kcache : a.vcache;
+                cache[(head * a.max_positions + a.st->pos) * a.head_dim + dim] = y;
+            }
+        } else {
+            a.out[n] = y;
+        }
+    }
+    if constexpr (Epi == kHead) {
+        // Workgroup best of its rows; argmax_final_kernel picks among the workgroups.
+        Best b{-INFINITY, INT64_MAX};
+        if (active) b = Best{y, n};
+        b = wave_best(b);
+        if (lane == 0) {
+            bv[wave] = b.v;
+            bi[wave] = b.i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            Best r{bv[0], bi[0]};
+            for (int w = 1; w < kThreads / 64; ++w) {
+                Best o{bv[w], bi[w]};
+                if (better(o, r)) r = o;
+            }
+            a.best_v[blockIdx.x] = r.v;
+            a.best_i[blockIdx.x] = r.i;
+        }
+    }
+}
+
+// Picks the greedy token among the head's workgroup partials, appends it to the sequence unless
+// the next position is teacher-forced, and advances the position. One workgroup.
+__global__ __launch_bounds__(kThreads) void argmax_final_kernel(Step* st, int64_t* seq, const float* pv,
+                                                                const int64_t* pi, int64_t parts) {
+    __shared__ float bv[kThreads / 64];
+    __shared__ int64_t bi[kThreads / 64];
+    Best r{-INFINITY, INT64_MAX};
+    for (int64_t i = threadIdx.x; i < parts; i += kThreads) {
+        Best o{pv[i], pi[i]};
+        if (better(o, r)) r = o;
+    }
+    r = wave_best(r);
+    if (threadIdx.x % 64 == 0) {
+        bv[threadIdx.x / 64] = r.v;
+        bi[threadIdx.x / 64] = r.i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Best w{bv[0], bi[0]};
+        for (int k = 1; k < kThreads / 64; ++k) {
+            Best o{bv[k], bi[k]};
+            if (better(o, w)) w = o;
+        }
+        const int64_t pos = st->pos;
+        if (pos + 1 >= st->forced) seq[pos + 1] = w.i;
+        st->pos = pos + 1;
+    }
+}
+
+// Split attention over the cached keys of one head: workgroup (h, c) takes chunk c of the
+// L = pos + 1 keys (the decode query sees every cached key, so no mask applies). Scores are
+// q.k / sqrt(head_dim) (16-lane groups, 16-byte loads, group shuffle reduction); the chunk keeps
+// its maximum m_c, the double sum l_c of exp(s - m_c) and the unnormalised weighted values
+// acc_c = sum exp(s - m_c) v. combine_attention() merges the chunks.
+__global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, const float* __restrict__ q,
+                                                             const float* __restrict__ kcache,
+                                                             const float* __restrict__ vcache, AttnPartials part,
+                                                             int64_t head_dim, int64_t max_positions, float divisor) {
+    extern __shared__ float scores[];  // [chunk length]
+    __shared__ float red_f[kThreads / 64];
+    __shared__ double red_d[kThreads / 64];
+    __shared__ float4 acc_part[kThreads / 16][16];
+    const int64_t h = blockIdx.x;
+    const int64_t c = blockIdx.y;
+    const int64_t L = st->pos + 1;
+    const int64_t chunk = (L + kAttnChunks - 1) / kAttnChunks;
+    const int64_t j0 = c * chunk;
+    const int64_t count = j0 < L ? (j0 + chunk < L ? chunk : L - j0) : 0;
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
+    const int sub = tid % 16, group = tid / 16;  // 16 groups of 16 lanes
+    const bool dims_ok = 4 * sub < head_dim;
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (dims_ok) qv = *reinterpret_cast<const float4*>(q + h * head_dim + 4 * sub);
+    const float* K = kcache + (h * max_positions + j0) * head_dim;
+    const float* V = vcache + (h * max_positions + j0) * head_dim;
+    float local_max = -INFINITY;
+    for (int64_t j = group; j < count; j += kThreads / 16) {
+        float sc = 0.f;
+        if (dims_ok) {
+            const float4 k = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
+            sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
+        }
+#pragma unroll
+        for (int m = 8; m > 0; m /= 2) sc += __shfl_xor(sc, m, 64);
+        sc = __fdiv_rn(sc, divisor);
+        if (sub == 0) scores[j] = sc;
+        local_max = max_na(local_max, sc);
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) local_max = max_na(local_max, __shfl_xor(local_max, m, 64));
+    if (lane == 0) red_f[wave] = local_max;
+    __syncthreads();
+    float largest = red_f[0];
+    for (int w = 1; w < kThreads / 64; ++w) largest = max_na(largest, red_f[w]);
+    double total = 0.0;
+    for (int64_t j = tid; j < count; j += kThreads) {
+        const float e = std::exp(__fsub_rn(scores[j], largest));
+        scores[j] = e;
+        total += static_cast<double>(e);
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) total += __shfl_xor(total, m, 64);
+    if (lane == 0) red_d[wave] = total;
+    __syncthreads();
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (dims_ok) {
+        for (int64_t j = group; j < count; j += kThreads / 16) {
+            const float w = scores[j];
+            const float4 v = *reinterpret_cast<const float4*>(V + j * head_dim + 4 * sub);
+            acc.x += w * v.x;
+            acc.y += w * v.y;
+            acc.z += w * v.z;
+            acc.w += w * v.w;
+        }
+    }
+    acc_part[group][sub] = acc;
+    __syncthreads();
+    const int64_t slot = h * kAttnChunks + c;
+    if (tid < head_dim) {
+        const int s4 = tid / 4, e = tid % 4;
+        float r = 0.f;
+        for (int g = 0; g < kThreads / 16; ++g) {
+            const float4 pv = acc_part[g][s4];
+            r += e == 0 ? pv.x : e == 1 ? pv.y : e == 2 ? pv.z : pv.w;
+        }
+        part.acc[slot * head_dim + tid] = r;
+    }
+    if (tid == 0) {
+        double sum = red_d[0];
+        for (int w = 1; w < kThreads / 64; ++w) sum += red_d[w];
+        part.m[slot] = largest;
+        part.l[slot] = sum;
+    }
+}
+
+// ---- engine ----------------------------------------------------------------------------------
+
+struct Engine {
+    kd_gpt_config cfg{};
+    int64_t d = 0, hd = 0, ff = 0;
+    hipStream_t stream = nullptr;
+    float* params = nullptr;  // every parameter, kael names -> offsets
+    std::unordered_map<std::string, std::pair<int64_t, int64_t>> offsets;  // name -> (offset, count)
+    std::vector<bool> loaded;
+    std::vector<std::string> names;
+    float* kcache = nullptr;
+    float* vcache = nullptr;
+    float* x = nullptr;
+    float* h = nullptr;
+    float* q = nullptr;
+    AttnPartials partials{};
+    float* f = nullptr;
+    float* logits = nullptr;
+    float* pv = nullptr;     // head argmax partials, one per workgroup
+    int64_t* pi = nullptr;
+    int64_t* seq = nullptr;
+    Step* st = nullptr;
+    hipGraphExec_t graph = nullptr;
+    int64_t host_pos = 0;     // mirror of st->pos
+    int64_t host_forced = 0;
+
+    const float* p(const std::string& name) const { return params + offsets.at(name).first; }
+
+    GemvArgs base() const {
+        GemvArgs a{};
+        a.d = d;
+        a.head_dim = hd;
+        a.max_positions = cfg.max_positions;
+        a.st = st;
+        return a;
+    }
+
+    static dim3 rows_grid(int64_t n, bool split_k) {
+        return dim3(static_cast<uint32_t>(split_k ? (n + 1) / 2 : (n + 7) / 8));
+    }
+
+    template <int Epi> void gemv(hipStream_t s, const GemvArgs& a) const {
+        // Few rows: split K across the workgroup's waves so that more workgroups stream weights.
+        const bool split = a.N <= 4096;
+        if (split) hipLaunchKernelGGL((gemv_kernel<Epi, 4>), rows_grid(a.N, true), dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((gemv_kernel<Epi, 1>), rows_grid(a.N, false), dim3(kThreads), 0, s, a);
+    }
+
+    int record_step(hipStream_t s) {
+        const int64_t L = cfg.layers;
+        hipLaunchKernelGGL(embed_kernel, dim3(static_cast<uint32_t>((d + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, st,
+                           seq, p("token_embedding.weight"), p("position_embedding.weight"), x, d);
+        const size_t attn_lds = static_cast<size_t>((cfg.max_positions + kAttnChunks - 1) / kAttnChunks) * sizeof(float);
+        const float divisor = static_cast<float>(std::sqrt(static_cast<double>(hd)));
+        for (int64_t l = 0; l < L; ++l) {
+            const std::string b = "blocks." + std::to_string(l) + ".";
+            float* kc = kcache + l * cfg.heads * cfg.max_positions * hd;
+            float* vc = vcache + l * cfg.heads * cfg.max_positions * hd;
+            GemvArgs qkv = base();
+            qkv.W = p(b + "attn.qkv.weight");
+            qkv.bias = p(b + "attn.qkv.bias");
+            qkv.x = x;
+            qkv.N = 3 * d;
+            qkv.K = d;
+            qkv.ln_w = p(b + "ln1.weight");
+            qkv.ln_b = p(b + "ln1.bias");
+            qkv.q = q;
+            qkv.kcache = kc;
+            qkv.vcache = vc;
+            gemv<kQkv>(s, qkv);
+            hipLaunchKernelGGL(attention_kernel, dim3(static_cast<uint32_t>(cfg.heads), kAttnChunks), dim3(kThreads), attn_lds,
+                               s, st, q, kc, vc, partials, hd, cfg.max_positions, divisor);
+            GemvArgs proj = base();
+            proj.W = p(b + "attn.proj.weight");
+            proj.bias = p(b + "attn.proj.bias");
+            proj.x = nullptr;
+            proj.attn = partials;
+            proj.out = x;
+            proj.N = d;
+            proj.K = d;
+            gemv<kResidual>(s, proj);
+            GemvArgs fc1 = base();
+            fc1.W = p(b + "mlp.fc1.weight");
+            fc1.bias = p(b + "mlp.fc1.bias");
+            fc1.x = x;
+            fc1.out = f;
+            fc1.N = ff;
+            fc1.K = d;
+            fc1.ln_w = p(b + "ln2.weight");
+            fc1.ln_b = p(b + "ln2.bias");
+            if (cfg.tanh_gelu) gemv<kGeluTanh>(s, fc1);
+            else gemv<kGeluExact>(s, fc1);
+            GemvArgs fc2 = base();
+            fc2.W = p(b + "mlp.fc2.weight");
+            fc2.bias = p(b + "mlp.fc2.bias");
+            fc2.x = f;
+            fc2.out = x;
+            fc2.N = d;
+            fc2.K = ff;
+            gemv<kResidual>(s, fc2);
+        }
+        hipLaunchKernelGGL(layernorm_kernel, dim3(1), dim3(kThreads), 0, s, x, d, p("ln_final.weight"), p("ln_final.bias"), h);
+        GemvArgs head = base();
+        head.W = p("token_embedding.weight");
+        head.x = h;
+        head.N = cfg.vocab_size;
+        head.K = d;
+        head.out = logits;
+        head.best_v = pv;
+        head.best_i = pi;
+        gemv<kHead>(s, head);
+        const int64_t parts = head.N <= 4096 ? (head.N + 1) / 2 : (head.N + 7) / 8;
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kThreads), 0, s, st, seq, pv, pi, parts);
+        return KD_OK;
+    }
+
+    int build_graph() {
+        if (graph != nullptr || eager()) return KD_OK;
+        hipGraph_t g;
+        KD_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+        record_step(stream);
+        KD_HIP(hipStreamEndCapture(stream, &g));
+        KD_HIP(hipGraphInstantiate(&graph, g, nullptr, nullptr, 0));
+        KD_HIP(hipGraphDestroy(g));
+        return KD_OK;
+    }
+
+    int ready() {
+        for (size_t i = 0; i < loaded.size(); ++i)
+            if (!loaded[i]) return fail(KD_E_INVALID, "kd_gpt: parameter " + names[i] + " was never loaded");
+        return build_graph();
+    }
+
+    int set_state(int64_t pos, int64_t forced) {
+        Step s{pos, forced};
+        KD_HIP(hipMemcpyAsync(st, &s, sizeof s, hipMemcpyHostToDevice, stream));
+        KD_HIP(hipStreamSynchronize(stream));
+        host_pos = pos;
+        host_forced = forced;
+        return KD_OK;
+    }
+
+    bool eager() const { return (cfg.flags & KD_GPT_EAGER) != 0; }
+
+    int steps(int64_t count) {
+        if (host_pos + count > cfg.max_positions)
+            return fail(KD_E_INVALID, "kd_gpt: the sequence would exceed max_positions (the cache-window refill of "
+                                      "nn::generate is not implemented)");
+        for (int64_t i = 0; i < count; ++i) {
+            if (eager()) {
+                record_step(stream);
+                KD_LAUNCH_CHECK();
+            } else {
+                KD_HIP(hipGraphLaunch(graph, stream));
+            }
+        }
+        host_pos += count;
+        return KD_OK;
+    }
+
+    ~Engine() {
+        if (graph) (void)hipGraphExecDestroy(graph);
+        for (void* ptr : {static_cast<void*>(params), static_cast<void*>(kcache), static_cast<void*>(vcache),
+                          static_cast<void*>(x), static_cast<void*>(h), static_cast<void*>(q), static_cast<void*>(partials.m),
+                          static_cast<void*>(partials.l), static_cast<void*>(partials.acc),
+                          static_cast<void*>(f), static_cast<void*>(logits), static_cast<void*>(pv),
+                          static_cast<void*>(pi), static_cast<void*>(seq), static_cast<void*>(st)})
+            if (ptr) (void)hipFree(ptr);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+template <typename T> int alloc(T** out, int64_t count) {
+    void* p = nullptr;
+    KD_HIP(hipMalloc(&p, static_cast<size_t>(count) * sizeof(T)));
+    *out = static_cast<T*>(p);
+    return KD_OK;
+}
+
+int create(Engine& e, const kd_gpt_config& c) {
+    if (c.vocab_size <= 0 || c.max_positions <= 0 || c.layers <= 0 || c.heads <= 0 || c.dimension <= 0)
+        return fail(KD_E_INVALID, "kd_gpt_create: sizes must be positive");
+    if (c.dimension % c.heads != 0) return fail(KD_E_INVALID, "kd_gpt_create: dimension must divide by heads");
+    e.cfg = c;
+    e.d = c.dimension;
+    e.hd = c.dimension / c.heads;
+    e.ff = 4 * c.dimension;
+    if (e.hd > 64) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim above 64 is not supported");
+    if (e.d % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: dimension must be a multiple of 4");
+    if (e.ff > kMaxK) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: 4 * dimension above 4096 is not supported");
+    if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: more than 64 heads is not supported");
+    if (c.max_positions > 8192) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: max_positions above 8192");
+    // kael's parameter order and shapes (GPT::named_parameters)
+    std::vector<std::pair<std::string, int64_t>> shapes;
+    shapes.emplace_back("token_embedding.weight", c.vocab_size * e.d);
+    shapes.emplace_back("position_embedding.weight", c.max_positions * e.d);
+    for (int64_t l = 0; l < c.layers; ++l) {
+        const std::string b = "blocks." + std::to_string(l) + ".";
+        shapes.emplace_back(b + "ln1.weight", e.d);
+        shapes.emplace_back(b + "ln1.bias", e.d);
+        shapes.emplace_back(b + "attn.qkv.weight", 3 * e.d * e.d);
+        shapes.emplace_back(b + "attn.qkv.bias", 3 * e.d);
+        shapes.emplace_back(b + "attn.proj.weight", e.d * e.d);
+        shapes.emplace_back(b + "attn.proj.bias", e.d);
+        shapes.emplace_back(b + "ln2.weight", e.d);
+        shapes.emplace_back(b + "ln2.bias", e.d);
+        shapes.emplace_back(b + "mlp.fc1.weight", e.ff * e.d);
+        shapes.emplace_back(b + "mlp.fc1.bias", e.ff);
+        shapes.emplace_back(b + "mlp.fc2.weight", e.d * e.ff);
+        shapes.emplace_back(b + "mlp.fc2.bias", e.d);
+    }
+    shapes.emplace_back("ln_final.weight", e.d);
+    shapes.emplace_back("ln_final.bias", e.d);
+    int64_t total = 0;
+    for (const auto& [name, count] : shapes) {
+        e.offsets[name] = {total, count};
+        e.names.push_back(name);
+        total += (count + 63) / 64 * 64;  // keep every parameter 256-byte aligned
+    }
+    e.loaded.assign(shapes.size(), false);
+    KD_HIP(hipStreamCreateWithFlags(&e.stream, hipStreamNonBlocking));
+    if (int rc = alloc(&e.params, total)) return rc;
+    const int64_t cache = c.layers * c.heads * c.max_positions * e.hd;
+    if (int rc = alloc(&e.kcache, cache)) return rc;
+    if (int rc = alloc(&e.vcache, cache)) return rc;
+    if (int rc = alloc(&e.x, e.d)) return rc;
+    if (int rc = alloc(&e.h, e.d)) return rc;
+    if (int rc = alloc(&e.q, e.d)) return rc;
+    if (int rc = alloc(&e.partials.m, c.heads * kAttnChunks)) return rc;
+    if (int rc = alloc(&e.partials.l, c.heads * kAttnChunks)) return rc;
+    if (int rc = alloc(&e.partials.acc, c.heads * kAttnChunks * e.hd)) return rc;
+    if (int rc = alloc(&e.f, e.ff)) return rc;
+    if (int rc = alloc(&e.logits, c.vocab_size)) return rc;
+    const int64_t head_groups = (c.vocab_size + 1) / 2 + 1;  // enough for either GEMV row layout
+    if (int rc = alloc(&e.pv, head_groups)) return rc;
+    if (int rc = alloc(&e.pi, head_groups)) return rc;
+
+    if (int rc = alloc(&e.seq, c.max_positions + 1)) return rc;
+    if (int rc = alloc(&e.st, 1)) return rc;
+    return KD_OK;
+}
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" {
+
+int kd_gpt_create(void** handle, const kd_gpt_config* config) {
+    if (handle == nullptr || config == nullptr) return fail(KD_E_INVALID, "kd_gpt_create: null argument");
+    *handle = nullptr;
+    if (int rc = ensure_device()) return rc;
+    auto* e = new Engine();
+    if (int rc = create(*e, *config)) {
+        delete e;
+        return rc;
+    }
+    *handle = e;
+    return KD_OK;
+}
+
+void kd_gpt_destroy(void* handle) { delete static_cast<Engine*>(handle); }
+
+int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int64_t count) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || name == nullptr || data == nullptr) return fail(KD_E_INVALID, "kd_gpt_load_parameter: null argument");
+    const auto it = e->offsets.find(name);
+    if (it == e->offsets.end()) return fail(KD_E_INVALID, std::string("kd_gpt_load_parameter: unknown parameter ") + name);
+    if (it->second.second != count)
+        return fail(KD_E_INVALID, std::string("kd_gpt_load_parameter: wrong element count for ") + name);
+    KD_HIP(hipMemcpy(e->params + it->second.first, data, static_cast<size_t>(count) * sizeof(float), hipMemcpyHostToDevice));
+    for (size_t i = 0; i < e->names.size(); ++i)
+        if (e->names[i] == name) e->loaded[i] = true;
+    return KD_OK;
+}
+
+int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || prompt == nullptr || length <= 0) return fail(KD_E_INVALID, "kd_gpt_prefill: bad arguments");
+    if (length > e->cfg.max_positions) return fail(KD_E_INVALID, "kd_gpt_prefill: prompt longer than max_positions");
+    for (int64_t i = 0; i < length; ++i)
+        if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab_size) return fail(KD_E_INVALID, "kd_gpt_prefill: token id out of range");
+    if (int rc = e->ready()) return rc;
+    KD_HIP(hipMemcpyAsync(e->seq, prompt, static_cast<size_t>(length) * sizeof(int64_t), hipMemcpyHostToDevice, e->stream));
+    if (int rc = e->set_state(0, length)) return rc;
+    return e->steps(length);
+}
+
+int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || count < 0) return fail(KD_E_INVALID, "kd_gpt_decode: bad arguments");
+    if (e->host_pos == 0) return fail(KD_E_INVALID, "kd_gpt_decode: call kd_gpt_prefill first");
+    const int64_t first = e->host_pos + 1;  // index in seq of the first token this call produces
+    if (int rc = e->steps(count)) return rc;
+    if (tokens != nullptr && count > 0) {
+        KD_HIP(hipMemcpyAsync(tokens, e->seq + first, static_cast<size_t>(count) * sizeof(int64_t), hipMemcpyDeviceToHost,
+                              e->stream));
+    }
+    KD_HIP(hipStreamSynchronize(e->stream));
+    return KD_OK;
+}
+
+int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, float* logits) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || tokens == nullptr || logits == nullptr || count <= 0)
+        return fail(KD_E_INVALID, "kd_gpt_forward_logits: bad arguments");
+    if (count > e->cfg.max_positions) return fail(KD_E_INVALID, "kd_gpt_forward_logits: more tokens than max_positions");
+    for (int64_t i = 0; i < count; ++i)
+        if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size) return fail(KD_E_INVALID, "kd_gpt_forward_logits: token id out of range");
+    if (int rc = e->ready()) return rc;
+    KD_HIP(hipMemcpyAsync(e->seq, tokens, static_cast<size_t>(count) * sizeof(int64_t), hipMemcpyHostToDevice, e->stream));
+    if (int rc = e->set_state(0, count)) return rc;
+    const int64_t v = e->cfg.vocab_size;
+    for (int64_t t = 0; t < count; ++t) {
+        if (int rc = e->steps(1)) return rc;
+        KD_HIP(hipMemcpyAsync(logits + t * v, e->logits, static_cast<size_t>(v) * sizeof(float), hipMemcpyDeviceToHost, e->stream));
+    }
+    KD_HIP(hipStreamSynchronize(e->stream));
+    return KD_OK;
+}
+
+int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* length) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || length == nullptr) return fail(KD_E_INVALID, "kd_gpt_sequence: bad arguments");
+    KD_HIP(hipStreamSynchronize(e->stream));
+    const int64_t n = e->host_pos == 0 ? 0 : e->host_pos + 1;
+    *length = n;
+    if (ids != nullptr && capacity > 0 && n > 0) {
+        KD_HIP(hipMemcpy(ids, e->seq, static_cast<size_t>(std::min(n, capacity)) * sizeof(int64_t), hipMemcpyDeviceToHost));
+    }
+    return KD_OK;
+}
+
+} // extern "C"

@@ -81,6 +81,11 @@ class MatmulStrides(Structure):
     _fields_ = [("a", c_int64 * 3), ("b", c_int64 * 3), ("out", c_int64 * 3)]
 
 
+class GptConfig(Structure):
+    _fields_ = [("vocab_size", c_int64), ("max_positions", c_int64), ("layers", c_int64), ("heads", c_int64),
+                ("dimension", c_int64), ("tanh_gelu", c_int32), ("flags", c_int32)]
+
+
 assert ctypes.sizeof(ElementLayout) == 368
 assert ctypes.sizeof(IndexLayout) == 272
 
@@ -125,6 +130,13 @@ BACKEND_ONLY = {
     "event_record": (c_int, [c_void_p]),
     "event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
     "device_info": (c_int, [POINTER(c_int), POINTER(c_int), ctypes.c_char_p, c_int]),
+    "gpt_create": (c_int, [POINTER(c_void_p), POINTER(GptConfig)]),
+    "gpt_destroy": (None, [c_void_p]),
+    "gpt_load_parameter": (c_int, [c_void_p, ctypes.c_char_p, c_void_p, c_int64]),
+    "gpt_prefill": (c_int, [c_void_p, c_void_p, c_int64]),
+    "gpt_decode": (c_int, [c_void_p, c_int64, c_void_p]),
+    "gpt_forward_logits": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "gpt_sequence": (c_int, [c_void_p, c_void_p, c_int64, POINTER(c_int64)]),
 }
 
 # Every symbol include/kd_api.h declares.
@@ -218,6 +230,68 @@ class DeviceArray:
                 self.ptr = 0
         except Exception:
             pass
+
+
+class Gpt:
+    """The GPT-2 decode engine (kd_gpt_*): kael's parameter names and layout, greedy decoding."""
+
+    def __init__(self, backend: Backend, vocab_size=50257, max_positions=1024, layers=12, heads=12, dimension=768,
+                 tanh_gelu=True, eager=False):
+        self.b = backend
+        self.config = GptConfig(vocab_size, max_positions, layers, heads, dimension, int(bool(tanh_gelu)), 1 if eager else 0)
+        h = c_void_p()
+        backend.check(backend.lib.kd_gpt_create(ctypes.byref(h), ctypes.byref(self.config)), "kd_gpt_create")
+        self.handle = h
+
+    def load(self, name: str, array: np.ndarray) -> None:
+        a = np.ascontiguousarray(array, dtype=np.float32)
+        self.b.check(self.b.lib.kd_gpt_load_parameter(self.handle, name.encode(), a.ctypes.data_as(c_void_p), a.size),
+                     f"kd_gpt_load_parameter({name})")
+
+    def prefill(self, prompt) -> None:
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        self.b.check(self.b.lib.kd_gpt_prefill(self.handle, p.ctypes.data_as(c_void_p), p.size), "kd_gpt_prefill")
+
+    def decode(self, count: int) -> np.ndarray:
+        out = np.zeros(max(count, 1), np.int64)
+        self.b.check(self.b.lib.kd_gpt_decode(self.handle, count, out.ctypes.data_as(c_void_p)), "kd_gpt_decode")
+        return out[:count]
+
+    def forward_logits(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int64)
+        out = np.empty((t.size, self.config.vocab_size), np.float32)
+        self.b.check(self.b.lib.kd_gpt_forward_logits(self.handle, t.ctypes.data_as(c_void_p), t.size,
+                                                      out.ctypes.data_as(c_void_p)), "kd_gpt_forward_logits")
+        return out
+
+    def sequence(self) -> np.ndarray:
+        n = c_int64()
+        buf = np.zeros(self.config.max_positions + 1, np.int64)
+        self.b.check(self.b.lib.kd_gpt_sequence(self.handle, buf.ctypes.data_as(c_void_p), buf.size, ctypes.byref(n)),
+                     "kd_gpt_sequence")
+        return buf[:n.value]
+
+    def __del__(self):
+        try:
+            if self.handle:
+                self.b.lib.kd_gpt_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def gpt2_parameter_shapes(vocab_size=50257, max_positions=1024, layers=12, dimension=768):
+    """kael's GPT parameter names and shapes in GPT::named_parameters() order."""
+    d = dimension
+    shapes = [("token_embedding.weight", (vocab_size, d)), ("position_embedding.weight", (max_positions, d))]
+    for l in range(layers):
+        b = f"blocks.{l}."
+        shapes += [(b + "ln1.weight", (d,)), (b + "ln1.bias", (d,)), (b + "attn.qkv.weight", (3 * d, d)),
+                   (b + "attn.qkv.bias", (3 * d,)), (b + "attn.proj.weight", (d, d)), (b + "attn.proj.bias", (d,)),
+                   (b + "ln2.weight", (d,)), (b + "ln2.bias", (d,)), (b + "mlp.fc1.weight", (4 * d, d)),
+                   (b + "mlp.fc1.bias", (4 * d,)), (b + "mlp.fc2.weight", (d, 4 * d)), (b + "mlp.fc2.bias", (d,))]
+    shapes += [("ln_final.weight", (d,)), ("ln_final.bias", (d,))]
+    return shapes
 
 
 _BACKEND: Backend | None = None

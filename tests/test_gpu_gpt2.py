@@ -1,0 +1,102 @@
+"""The GPT-2 decode engine (kd_gpt_*) against kael's own GPT on the CPU path.
+
+Weights come from kael itself (GPT constructor with manual_seed, src/nn/transformer.cpp:171-207),
+exported parameter by parameter, so both sides run the identical model. Checks:
+  - a small model (the config of reference tests/test_cuda.cpp:584-609, in f32): logits of every
+    position with the KV cache, and the greedy generation, token for token;
+  - GPT-2 small (config C5, seed 4): teacher-forced logits over a 64-token prompt plus decode
+    steps, within 1e-4 relative, and identical greedy tokens.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kd
+import support
+
+pytestmark = pytest.mark.gpu
+
+
+def export_params(ref, handle):
+    n = ref.ref_gpt_param_count(handle)
+    name = ctypes.create_string_buffer(256)
+    shape = (ctypes.c_int64 * 8)()
+    rank = ctypes.c_int()
+    out = []
+    for i in range(n):
+        assert ref.ref_gpt_param(handle, i, name, 256, shape, ctypes.byref(rank), None) == 0
+        dims = tuple(shape[d] for d in range(rank.value))
+        data = np.empty(dims, np.float32)
+        assert ref.ref_gpt_param(handle, i, name, 256, shape, ctypes.byref(rank), data.ctypes.data_as(ctypes.c_void_p)) == 0
+        out.append((name.value.decode(), data))
+    return out
+
+
+def build(kdb, ref, vocab, positions, layers, heads, dim, seed):
+    h = ref.ref_gpt_create(vocab, positions, layers, heads, dim, seed, 1)
+    assert h, support.ref_error(ref)
+    params = export_params(ref, h)
+    g = kd.Gpt(kdb, vocab, positions, layers, heads, dim, True)
+    for name, data in params:
+        g.load(name, data)
+    return h, g
+
+
+def cpu_cached_logits(ref, h, tokens, prompt, vocab):
+    t = np.ascontiguousarray(tokens, np.int64)
+    rows = len(t) - prompt + 1
+    out = np.empty((rows, vocab), np.float32)
+    assert ref.ref_gpt_cached_logits(h, t.ctypes.data_as(ctypes.c_void_p), prompt, len(t),
+                                     out.ctypes.data_as(ctypes.c_void_p)) == 0, support.ref_error(ref)
+    return out
+
+
+def cpu_generate(ref, h, prompt, new):
+    p = np.ascontiguousarray(prompt, np.int64)
+    out = np.zeros(len(p) + new, np.int64)
+    secs = ctypes.c_double()
+    assert ref.ref_gpt_generate(h, p.ctypes.data_as(ctypes.c_void_p), len(p), new, out.ctypes.data_as(ctypes.c_void_p),
+                                ctypes.byref(secs)) == 0, support.ref_error(ref)
+    return out, secs.value
+
+
+def test_small_model_logits_and_generation(kdb, refdev):
+    ref = refdev
+    h, g = build(kdb, ref, 11, 16, 2, 2, 8, 31)
+    try:
+        rng = np.random.default_rng(0)
+        tokens = rng.integers(0, 11, 12)
+        want = cpu_cached_logits(ref, h, tokens, 1, 11)  # position 0 alone, then one token at a time
+        got = g.forward_logits(tokens)
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+        prompt = tokens[:6]
+        seq, _ = cpu_generate(ref, h, prompt, 8)
+        g.prefill(prompt)
+        new = g.decode(7)
+        np.testing.assert_array_equal(np.concatenate([g.sequence()]), seq)
+        np.testing.assert_array_equal(new, seq[7:])
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
+def test_gpt2_small_teacher_forced_logits(kdb, refdev):
+    ref = refdev
+    ref.ref_set_threads(min(16, max(1, __import__("os").cpu_count() or 1)))
+    h, g = build(kdb, ref, 50257, 1024, 12, 12, 768, 4)
+    try:
+        rng = np.random.default_rng(4)
+        prompt_len, extra = 64, 6
+        tokens = rng.integers(0, 50257, prompt_len + extra)
+        want = cpu_cached_logits(ref, h, tokens, prompt_len, 50257)  # prefill's last row, then 6 steps
+        got = g.forward_logits(tokens)[prompt_len - 1:]
+        scale = np.abs(want).max()
+        err = np.abs(got - want).max()
+        assert err <= 1e-4 * scale, f"max |dlogit| {err} vs scale {scale}"
+        np.testing.assert_array_equal(got.argmax(axis=1), want.argmax(axis=1))
+        seq, _ = cpu_generate(ref, h, tokens[:prompt_len], 4)
+        g.prefill(tokens[:prompt_len])
+        g.decode(3)
+        np.testing.assert_array_equal(g.sequence(), seq)
+    finally:
+        ref.ref_gpt_destroy(h)
