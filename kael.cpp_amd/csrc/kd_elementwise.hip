@@ -73,7 +73,64 @@ template <typename T, int N> struct alignas(sizeof(T) * N) Vec {
     T v[N];
 };
 
-template <typename F, int VEC>
+// Loads and stores of 1..32-byte aggregates, optionally with the nontemporal hint (streaming
+// data that is touched once: measured ~6.4 TB/s versus ~5.5 TB/s with default caching).
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT, typename T> __device__ __forceinline__ T ld(const T* p) {
+    if constexpr (!NT) {
+        return *p;
+    } else {
+        T out;
+        if constexpr (sizeof(T) == 16) {
+            const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+            __builtin_memcpy(&out, &r, 16);
+        } else if constexpr (sizeof(T) == 32) {
+            const u32x4 r0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+            const u32x4 r1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + 1);
+            __builtin_memcpy(&out, &r0, 16);
+            __builtin_memcpy(reinterpret_cast<char*>(&out) + 16, &r1, 16);
+        } else if constexpr (sizeof(T) == 8) {
+            const u32x2 r = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+            __builtin_memcpy(&out, &r, 8);
+        } else if constexpr (sizeof(T) == 4) {
+            const unsigned r = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p));
+            __builtin_memcpy(&out, &r, 4);
+        } else {
+            out = *p;
+        }
+        return out;
+    }
+}
+
+template <bool NT, typename T> __device__ __forceinline__ void st(T* p, const T& v) {
+    if constexpr (!NT) {
+        *p = v;
+    } else if constexpr (sizeof(T) == 16) {
+        u32x4 r;
+        __builtin_memcpy(&r, &v, 16);
+        __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
+    } else if constexpr (sizeof(T) == 32) {
+        u32x4 r0, r1;
+        __builtin_memcpy(&r0, &v, 16);
+        __builtin_memcpy(&r1, reinterpret_cast<const char*>(&v) + 16, 16);
+        __builtin_nontemporal_store(r0, reinterpret_cast<u32x4*>(p));
+        __builtin_nontemporal_store(r1, reinterpret_cast<u32x4*>(p) + 1);
+    } else if constexpr (sizeof(T) == 8) {
+        u32x2 r;
+        __builtin_memcpy(&r, &v, 8);
+        __builtin_nontemporal_store(r, reinterpret_cast<u32x2*>(p));
+    } else if constexpr (sizeof(T) == 4) {
+        unsigned r;
+        __builtin_memcpy(&r, &v, 4);
+        __builtin_nontemporal_store(r, reinterpret_cast<unsigned*>(p));
+    } else {
+        *p = v;
+    }
+}
+
+template <typename F, int VEC, bool NT>
 __global__ __launch_bounds__(kBlock) void vec_kernel(F f, Bases bases, Decode outer,
                                                      uint32_t inner_vectors, FastDiv inner_div,
                                                      uint32_t total_vectors, uint32_t broadcast_mask) {
@@ -95,7 +152,7 @@ __global__ __launch_bounds__(kBlock) void vec_kernel(F f, Bases bases, Decode ou
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) in[i].v[e] = s;
             } else {
-                in[i] = reinterpret_cast<const Vec<In, VEC>*>(base)[col];
+                in[i] = ld<NT>(reinterpret_cast<const Vec<In, VEC>*>(base) + col);
             }
         }
         Vec<Out, VEC> out;
@@ -103,7 +160,7 @@ __global__ __launch_bounds__(kBlock) void vec_kernel(F f, Bases bases, Decode ou
         for (int e = 0; e < VEC; ++e) {
             out.v[e] = f(in[0].v[e], N > 1 ? in[1].v[e] : In{}, N > 2 ? in[2].v[e] : In{});
         }
-        reinterpret_cast<Vec<Out, VEC>*>(bases.p[0] + off[0])[col] = out;
+        st<NT>(reinterpret_cast<Vec<Out, VEC>*>(bases.p[0] + off[0]) + col, out);
     }
 }
 
@@ -167,6 +224,80 @@ __global__ __launch_bounds__(kBlock) void tile_kernel(F f, Bases bases, Decode o
     }
 }
 
+// Vectorized tile family: 64x64 tiles of (rows = dim d-2, cols = dim d-1). Transposed inputs
+// (contiguous along rows) are loaded with VEC-wide vectors along their contiguous dim and
+// staged in LDS; the output and inner-contiguous inputs move VEC-wide vectors along cols;
+// broadcast inputs (stride 0 along cols) are read once per row. Needs rows % VEC == 0,
+// cols % VEC == 0 and VEC-aligned bases and strides for every vector access (checked on the
+// host). Measured ~5.3 TB/s on a[4096,4096].T() + b[4096,1] (the scalar tile: ~2 TB/s).
+template <typename F, int VEC, bool NT>
+__global__ __launch_bounds__(kBlock) void tile_vec_kernel(F f, Bases bases, Decode outer, int64_t rows, int64_t cols,
+                                                          int64_t rs0, int64_t rs1, int64_t rs2, int64_t rs3, int64_t cs1,
+                                                          int64_t cs2, int64_t cs3, uint32_t transposed_mask,
+                                                          uint32_t broadcast_mask) {
+    using In = typename F::In;
+    using Out = typename F::Out;
+    constexpr int N = F::inputs;
+    // stage[slot][c][r] for the transposed inputs only (slot order = input order)
+    extern __shared__ __align__(16) unsigned char tile_lds[];
+    auto stage = reinterpret_cast<In(*)[kTile][kTile + VEC]>(tile_lds);
+    int slot_of[3] = {0, 0, 0};
+    {
+        int next = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (transposed_mask & (1u << (i + 1))) slot_of[i] = next++;
+    }
+    const int64_t rstride[4] = {rs0, rs1, rs2, rs3};
+    const int64_t cstride[4] = {static_cast<int64_t>(sizeof(Out)), cs1, cs2, cs3};
+    int64_t off[KD_MAX_OPERANDS];
+    decode<N + 1>(outer, blockIdx.z, off);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTile;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kTile;
+    const char* tile_base[3];
+#pragma unroll
+    for (int i = 0; i < N; ++i) tile_base[i] = bases.p[i + 1] + off[i + 1] + r0 * rstride[i + 1] + c0 * cstride[i + 1];
+    char* out_base = bases.p[0] + off[0] + r0 * rstride[0] + c0 * static_cast<int64_t>(sizeof(Out));
+    constexpr int per_line = kTile / VEC;  // vectors along one tile edge
+
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (!(transposed_mask & (1u << (i + 1)))) continue;
+        for (int idx = threadIdx.x; idx < kTile * per_line; idx += kBlock) {
+            const int c = idx / per_line, rv = idx % per_line;
+            if (c0 + c < cols && r0 + VEC * rv < rows) {
+                const Vec<In, VEC> v = ld<NT>(reinterpret_cast<const Vec<In, VEC>*>(
+                    tile_base[i] + c * cstride[i + 1] + static_cast<int64_t>(VEC * rv) * sizeof(In)));
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) stage[slot_of[i]][c][VEC * rv + e] = v.v[e];
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kTile * per_line; idx += kBlock) {
+        const int r = idx / per_line, cv = idx % per_line;
+        if (r0 + r >= rows || c0 + VEC * cv >= cols) continue;
+        Vec<In, VEC> in[3];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if (transposed_mask & (1u << (i + 1))) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) in[i].v[e] = stage[slot_of[i]][VEC * cv + e][r];
+            } else if (broadcast_mask & (1u << (i + 1))) {
+                const In s = *reinterpret_cast<const In*>(tile_base[i] + r * rstride[i + 1]);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) in[i].v[e] = s;
+            } else {
+                in[i] = ld<NT>(reinterpret_cast<const Vec<In, VEC>*>(tile_base[i] + r * rstride[i + 1]) + cv);
+            }
+        }
+        Vec<Out, VEC> o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = f(in[0].v[e], N > 1 ? in[1].v[e] : In{}, N > 2 ? in[2].v[e] : In{});
+        st<NT>(reinterpret_cast<Vec<Out, VEC>*>(out_base + r * rstride[0]) + cv, o);
+    }
+}
+
 // ---- nd family ---------------------------------------------------------------------------------
 
 template <typename F>
@@ -226,6 +357,11 @@ void make_decode(const kd_element_layout& l, int operands, int first, int last, 
     }
 }
 
+// Streaming hint for operands too large to stay in cache between kernels (>= 32 MiB moved).
+bool streaming(const kd_element_layout& l, int64_t out_size, int64_t in_size, int operands) {
+    return l.count * (out_size + in_size * (operands - 1)) >= (int64_t{32} << 20);
+}
+
 template <typename F> int launch(const F& f, const kd_element_layout& l) {
     using In = typename F::In;
     using Out = typename F::Out;
@@ -274,8 +410,12 @@ template <typename F> int launch(const F& f, const kd_element_layout& l) {
             make_decode(l, operands, 0, last, outer);
             const uint32_t inner_vectors = static_cast<uint32_t>(l.shape[last] / VEC);
             const uint32_t total = static_cast<uint32_t>(l.count / VEC);
-            hipLaunchKernelGGL((vec_kernel<F, VEC>), dim3(grid_for(total)), dim3(kBlock), 0, stream(), f,
-                               bases, outer, inner_vectors, FastDiv(inner_vectors), total, broadcast_mask);
+            if (streaming(l, out_size, in_size, operands))
+                hipLaunchKernelGGL((vec_kernel<F, VEC, true>), dim3(grid_for(total)), dim3(kBlock), 0, stream(), f,
+                                   bases, outer, inner_vectors, FastDiv(inner_vectors), total, broadcast_mask);
+            else
+                hipLaunchKernelGGL((vec_kernel<F, VEC, false>), dim3(grid_for(total)), dim3(kBlock), 0, stream(), f,
+                                   bases, outer, inner_vectors, FastDiv(inner_vectors), total, broadcast_mask);
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
@@ -302,6 +442,45 @@ template <typename F> int launch(const F& f, const kd_element_layout& l) {
                 const dim3 grid(static_cast<uint32_t>((l.shape[last] + kTile - 1) / kTile),
                                 static_cast<uint32_t>((l.shape[r] + kTile - 1) / kTile),
                                 static_cast<uint32_t>(outer_count));
+                // Vectorized tile when every vector access is aligned and whole.
+                constexpr int TV = sizeof(In) >= 8 ? 2 : (sizeof(In) == 4 ? 4 : 16);
+                bool tv_ok = grid.y < 65536 && l.shape[r] % TV == 0 && l.shape[last] % TV == 0 &&
+                             sizeof(Out) * TV <= 32;
+                uint32_t bmask = 0;
+                const auto vec_aligned = [&](int op, int64_t esize, bool along_rows) {
+                    const int64_t bytes = esize * TV;
+                    if (reinterpret_cast<uintptr_t>(l.base[op]) % bytes != 0) return false;
+                    for (int dd = 0; dd < l.dims; ++dd) {
+                        if ((along_rows ? dd == r : dd == last)) continue;
+                        if (l.strides[op][dd] % bytes != 0) return false;
+                    }
+                    return true;
+                };
+                if (tv_ok) tv_ok = vec_aligned(0, out_size, false);
+                for (int i = 1; i <= N && tv_ok; ++i) {
+                    if (tmask & (1u << i)) {
+                        tv_ok = vec_aligned(i, in_size, true);
+                    } else if (l.strides[i][last] == 0) {
+                        bmask |= 1u << i;
+                    } else if (l.strides[i][last] == in_size) {
+                        tv_ok = vec_aligned(i, in_size, false);
+                    } else {
+                        tv_ok = false;
+                    }
+                }
+                if (tv_ok) {
+                    const size_t lds = static_cast<size_t>(__builtin_popcount(tmask)) * kTile * (kTile + TV) * sizeof(In);
+                    if (streaming(l, out_size, in_size, operands))
+                        hipLaunchKernelGGL((tile_vec_kernel<F, TV, true>), grid, dim3(kBlock), lds, stream(), f, bases, outer,
+                                           l.shape[r], l.shape[last], rs[0], rs[1], rs[2], rs[3], cs[1], cs[2], cs[3], tmask,
+                                           bmask);
+                    else
+                        hipLaunchKernelGGL((tile_vec_kernel<F, TV, false>), grid, dim3(kBlock), lds, stream(), f, bases, outer,
+                                           l.shape[r], l.shape[last], rs[0], rs[1], rs[2], rs[3], cs[1], cs[2], cs[3], tmask,
+                                           bmask);
+                    KD_LAUNCH_CHECK();
+                    return KD_OK;
+                }
                 if (grid.y < 65536) {
                     hipLaunchKernelGGL((tile_kernel<F>), grid, dim3(kBlock), 0, stream(), f, bases, outer,
                                        l.shape[r], l.shape[last], rs[0], rs[1], rs[2], rs[3], cs[0], cs[1],

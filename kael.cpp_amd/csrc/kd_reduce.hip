@@ -98,6 +98,15 @@ template <typename In> struct alignas(16) Vec16 {
     In v[16 / sizeof(In)];
 };
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename In> __device__ __forceinline__ Vec16<In> nt_load(const Vec16<In>* p) {
+    const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    Vec16<In> out;
+    __builtin_memcpy(&out, &r, 16);
+    return out;
+}
+
 // Reduces data[begin, end) with all lanes of the block; 16-byte loads when `data + begin` is
 // 16-byte aligned. Lane-level order is fixed by the block size.
 template <typename C, typename In>
@@ -115,8 +124,19 @@ __device__ __forceinline__ typename C::Acc block_range(const In* data, int64_t b
     }
     const int64_t vectors = (end - i) / V;
     const Vec16<In>* vp = reinterpret_cast<const Vec16<In>*>(data + i);
-    for (int64_t k = threadIdx.x; k < vectors; k += kBlock) {
-        const Vec16<In> x = vp[k];
+    // Four nontemporal 16-byte loads in flight per lane (the data is read exactly once).
+    int64_t k = threadIdx.x;
+    for (; k + 3 * kBlock < vectors; k += 4 * kBlock) {
+        Vec16<In> x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = nt_load(vp + k + u * kBlock);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x[u].v[e]));
+    }
+    for (; k < vectors; k += kBlock) {
+        const Vec16<In> x = nt_load(vp + k);
 #pragma unroll
         for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x.v[e]));
     }

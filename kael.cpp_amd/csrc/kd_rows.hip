@@ -117,6 +117,150 @@ __global__ __launch_bounds__(kThreads) void softmax_wave_kernel(T* __restrict__ 
     }
 }
 
+template <typename T>
+__device__ __forceinline__ T standardized(T x, double center, double scale, const T* w, const T* b, int64_t c);
+
+// ---- vectorized wave-per-row variants (cols % 4 == 0, cols <= 1024) ----------------------------
+//
+// Same arithmetic as the scalar wave kernels; each lane holds V4 groups of 4 consecutive columns
+// and moves them with 16-byte loads and stores (nontemporal for large tensors).
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Quad {
+    T v[4];
+};
+
+template <bool NT, typename T> __device__ __forceinline__ Quad<T> ld4(const T* p) {
+    Quad<T> q;
+    if constexpr (NT && sizeof(T) == 4) {
+        const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+        __builtin_memcpy(&q, &r, 16);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q.v[e] = p[e];
+    }
+    return q;
+}
+
+template <bool NT, typename T> __device__ __forceinline__ void st4(T* p, const Quad<T>& q) {
+    if constexpr (NT && sizeof(T) == 4) {
+        u32x4 r;
+        __builtin_memcpy(&r, &q, 16);
+        __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = q.v[e];
+    }
+}
+
+template <typename T, int V4, int Op, bool NT>
+__global__ __launch_bounds__(kThreads) void softmax_wave4_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                                 int64_t rows, int64_t cols) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    const T* x = in + row * cols;
+    Quad<T> v[V4];
+    T largest = neg_inf<T>();
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+            v[j] = ld4<NT>(x + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) largest = max_na(largest, v[j].v[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j].v[e] = neg_inf<T>();
+        }
+    }
+    largest = wave_max(largest);
+    double total = 0.0;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const T ex = std::exp(sub_rn(v[j].v[e], largest));
+                if constexpr (Op == kSoftmax) v[j].v[e] = ex;
+                total += static_cast<double>(ex);
+            }
+        }
+    }
+    total = wave_sum(total);
+    const T denominator = static_cast<T>(total);
+    const T log_total = Op == kLogSoftmax ? std::log(denominator) : T(0);
+    T* y = out + row * cols;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+            Quad<T> o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o.v[e] = Op == kSoftmax ? div_rn(v[j].v[e], denominator) : sub_rn(sub_rn(v[j].v[e], largest), log_total);
+            st4<NT>(y + c, o);
+        }
+    }
+}
+
+template <typename T, int V4, bool NT>
+__global__ __launch_bounds__(kThreads) void standardize_wave4_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                                     int64_t rows, int64_t cols, double eps,
+                                                                     const T* __restrict__ w, const T* __restrict__ b) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    const T* x = in + row * cols;
+    Quad<T> v[V4];
+    double total = 0.0;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+            v[j] = ld4<NT>(x + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) total += static_cast<double>(v[j].v[e]);
+        }
+    }
+    const double center = wave_sum(total) / static_cast<double>(cols);
+    double squares = 0.0;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double d = static_cast<double>(v[j].v[e]) - center;
+                squares += d * d;
+            }
+        }
+    }
+    // (x - mean) * (1 / scale) in double: it differs from the reference's division by at most one
+    // double ulp, which the rounding to T that follows absorbs (a per-element double divide made
+    // this kernel compute-bound at a third of HBM bandwidth).
+    const double rscale = 1.0 / std::sqrt(wave_sum(squares) / static_cast<double>(cols) + eps);
+    T* y = out + row * cols;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+            Quad<T> o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o.v[e] = static_cast<T>((static_cast<double>(v[j].v[e]) - center) * rscale);
+            if (w != nullptr) {
+                const Quad<T> wq = ld4<false>(w + c);
+                const Quad<T> bq = ld4<false>(b + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o.v[e] = add_rn(mul_rn(o.v[e], wq.v[e]), bq.v[e]);
+            }
+            st4<NT>(y + c, o);
+        }
+    }
+}
+
 // ---- softmax family, one workgroup per row (long rows) -------------------------------------------
 
 template <typename T> __device__ __forceinline__ T block_max(T v, T* scratch) {
@@ -183,6 +327,21 @@ template <typename T, int Op>
 int softmax_family(T* out, const T* in, const int64_t* targets, const T* weights, int64_t rows, int64_t cols) {
     if (rows == 0 || cols == 0) return KD_OK;
     const dim3 block(kThreads);
+    const bool quads = (Op == kSoftmax || Op == kLogSoftmax) && cols % 4 == 0 && cols <= 1024 &&
+                       reinterpret_cast<uintptr_t>(in) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if (quads) {
+        const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
+        const bool nt = rows * cols * static_cast<int64_t>(sizeof(T)) >= (int64_t{16} << 20);
+#define KD_WAVE4(V4)                                                                                                   \
+    if (nt) hipLaunchKernelGGL((softmax_wave4_kernel<T, V4, Op, true>), grid, block, 0, stream(), out, in, rows, cols); \
+    else hipLaunchKernelGGL((softmax_wave4_kernel<T, V4, Op, false>), grid, block, 0, stream(), out, in, rows, cols);
+        if (cols <= 256) { KD_WAVE4(1) }
+        else if (cols <= 512) { KD_WAVE4(2) }
+        else { KD_WAVE4(4) }
+#undef KD_WAVE4
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
     if (cols <= 1024) {
         const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
         if (rows > int64_t{0xffffffff} * 4) return fail(KD_E_INVALID, "row kernel: too many rows");
@@ -271,6 +430,21 @@ template <typename T>
 int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double eps, const T* w, const T* b) {
     if (rows == 0 || cols == 0) return KD_OK;
     const dim3 block(kThreads);
+    const bool quads = cols % 4 == 0 && cols <= 1024 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if (quads) {
+        const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
+        const bool nt = rows * cols * static_cast<int64_t>(sizeof(T)) >= (int64_t{16} << 20);
+#define KD_WAVE4(V4)                                                                                                    \
+    if (nt) hipLaunchKernelGGL((standardize_wave4_kernel<T, V4, true>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b); \
+    else hipLaunchKernelGGL((standardize_wave4_kernel<T, V4, false>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b);
+        if (cols <= 256) { KD_WAVE4(1) }
+        else if (cols <= 512) { KD_WAVE4(2) }
+        else { KD_WAVE4(4) }
+#undef KD_WAVE4
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
     if (cols <= 1024) {
         const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
 #define KD_WAVE(V) hipLaunchKernelGGL((standardize_wave_kernel<T, V>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b)
