@@ -578,3 +578,103 @@ int64_t ref_golden(const char* op, const char* args, int n, const void* const* d
 int ref_device_available(void) { return kael::cuda_is_available() ? 1 : 0; }
 
 } // extern "C"
+
+// ---- training workloads (configs C3 and C4) through kael's autograd and optimizers ---------------
+
+namespace {
+
+std::vector<float> flat_parameters(const std::vector<kael::Tensor>& params) {
+    std::vector<float> out;
+    for (const kael::Tensor& p : params) {
+        const kael::Tensor c = p.detach().cpu().contiguous();
+        const float* d = c.data_ptr<float>();
+        out.insert(out.end(), d, d + c.numel());
+    }
+    return out;
+}
+
+} // namespace
+
+extern "C" {
+
+// C3: Linear(784,128)-ReLU-Linear(128,10), manual_seed(2) for the Kaiming-uniform init and the
+// inputs x = rand({64,784}), y = randint(0,10,{64}); cross-entropy, backward, SGD lr 0.01.
+// device 0 = CPU, 1 = the linked device backend. Writes the loss of every step, the flattened
+// final parameters (when params_out is non-NULL; 101770 floats) and the wall seconds of the loop.
+int ref_train_mlp(int device, int64_t steps, float* losses, float* params_out, double* seconds) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(2);
+        kael::nn::Sequential model{std::make_shared<kael::nn::Linear>(784, 128), std::make_shared<kael::nn::ReLU>(),
+                                   std::make_shared<kael::nn::Linear>(128, 10)};
+        const kael::Tensor x = kael::rand({64, 784}).to(dev);
+        const kael::Tensor y = kael::randint(0, 10, {64}).to(dev);
+        model.to(dev);
+        kael::optim::SGD optimizer(model.parameters(), kael::optim::SgdOptions{.learning_rate = 0.01});
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int64_t step = 0; step < steps; ++step) {
+            optimizer.zero_grad();
+            const kael::Tensor loss = kael::nn::cross_entropy(model(x), y);
+            loss.backward();
+            optimizer.step();
+            losses[step] = loss.item<float>();
+        }
+        const auto t1 = std::chrono::steady_clock::now();
+        *seconds = std::chrono::duration<double>(t1 - t0).count();
+        if (params_out != nullptr) {
+            const std::vector<float> flat = flat_parameters(model.parameters());
+            std::memcpy(params_out, flat.data(), flat.size() * sizeof(float));
+        }
+    });
+}
+
+// C4: char-GPT {vocab 96, context 128, 4 layers, 4 heads, dim 256} (tanh GELU), manual_seed(3)
+// for the N(0,0.02) init and ids = randint(0,96,{32,128}), targets = randint(0,96,{4096});
+// forward, cross-entropy, backward, Adam (defaults). Writes each step's loss and the seconds.
+int ref_train_chargpt(int device, int64_t steps, float* losses, double* seconds) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(3);
+        kael::nn::GptConfig config;
+        config.vocab_size = 96;
+        config.max_positions = 128;
+        config.layers = 4;
+        config.heads = 4;
+        config.dimension = 256;
+        kael::nn::GPT model(config);
+        const kael::Tensor ids = kael::randint(0, 96, {32, 128}).to(dev);
+        const kael::Tensor targets = kael::randint(0, 96, {4096}).to(dev);
+        model.to(dev);
+        kael::optim::Adam optimizer(model.parameters());
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int64_t step = 0; step < steps; ++step) {
+            optimizer.zero_grad();
+            const kael::Tensor logits = model(ids).reshape({4096, 96});
+            const kael::Tensor loss = kael::nn::cross_entropy(logits, targets);
+            loss.backward();
+            optimizer.step();
+            losses[step] = loss.item<float>();
+        }
+        const auto t1 = std::chrono::steady_clock::now();
+        *seconds = std::chrono::duration<double>(t1 - t0).count();
+    });
+}
+
+// kael's GPT-2 small generate on `device`, timed (the drop-in path end to end).
+int ref_gpt_generate_on(void* handle, int device, const int64_t* prompt, int64_t length, int64_t new_tokens,
+                        int64_t* out_tokens, double* seconds) {
+    return guarded([&] {
+        auto& model = *static_cast<RefGpt*>(handle)->model;
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        model.to(dev);
+        const kael::Tensor ids = host_tensor(prompt, {1, length}, kael::DType::I64).to(dev);
+        const auto t0 = std::chrono::steady_clock::now();
+        const kael::Tensor seq = kael::nn::generate(model, ids, {.max_new_tokens = new_tokens, .temperature = 0.0});
+        const auto t1 = std::chrono::steady_clock::now();
+        *seconds = std::chrono::duration<double>(t1 - t0).count();
+        copy_out(seq.cpu(), out_tokens);
+        model.to(kael::Device::CPU);
+    });
+}
+
+} // extern "C"

@@ -83,12 +83,15 @@ REF_SIGS = {
                          POINTER(c_int64), POINTER(c_char_p), c_int, c_void_p, c_int64, POINTER(c_int),
                          POINTER(c_int), POINTER(c_int64)]),
     "device_available": (c_int, []),
+    "train_mlp": (c_int, [c_int, c_int64, c_void_p, c_void_p, POINTER(c_double)]),
+    "train_chargpt": (c_int, [c_int, c_int64, c_void_p, POINTER(c_double)]),
+    "gpt_generate_on": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
 }
 
 
 def load_ref(variant: str = "ref") -> ctypes.CDLL:
     path = ref_path(variant)
-    lib = ctypes.CDLL(str(path), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+    lib = ctypes.CDLL(str(path), mode=os.RTLD_NOW | os.RTLD_LOCAL)
     kd.bind(lib, "ref_", REF_SIGS)
     return lib
 
