@@ -31,6 +31,10 @@ import kd  # noqa: E402
 
 FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense FP32 matrix (AMD spec)
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+# HBM bytes one 4096^3 mfma_f32_kernel launch moves, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# (347 241 KiB and 65 536 KiB per dispatch), scaled by the factors a plain 256 MiB copy gives the
+# same counters (x2.0 fetch, x1.0 write). The PMC runs and commands are kept in profiles/.
+MATMUL_4096_TRAFFIC_BYTES = (2 * 347241 + 65536) * 1024
 
 
 class Timer:
@@ -328,7 +332,8 @@ def main() -> int:
         "config": {"workload": "f32 matmul C=A.B, M=N=K=4096, contiguous row-major (BASELINE C1 recipe at the north-star size)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": MATMUL_4096_TRAFFIC_BYTES if n == 4096 else None},
         "cpu_baseline": cpu,
         "extra": extra,
     }
