@@ -115,6 +115,29 @@ def test_fill(kdb, dtype, count):
     np.testing.assert_array_equal(got, want)
 
 
+# Tile-family shapes: tile counts off a multiple of 8 (the XCD-grouped tile order has a remainder
+# path), batches of transposes (grid z > 1), vectorized tiles (rows and cols multiples of the
+# vector width) and scalar tiles.
+TILE_SHAPES = [(520, 260), (4, 256, 128), (3, 300, 197), (2, 130, 67), (1000, 64)]
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64, kd.BOOL], ids=["f32", "f64", "i64", "bool"])
+@pytest.mark.parametrize("shape", TILE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_transposed_tiles(kdb, oracle, dtype, shape):
+    rng = np.random.default_rng(len(shape) * 1000 + shape[-1] + dtype)
+    op = kd.OP["PLUS"]
+    cases = {
+        "transposed+transposed": [contiguous(shape), transposed(shape), transposed(shape)],
+        "transposed+contiguous": [contiguous(shape), transposed(shape), contiguous(shape)],
+        "transposed+column": [contiguous(shape), transposed(shape), contiguous(shape[:-1] + (1,))],
+    }
+    for name, views in cases.items():
+        got, want = run_both(kdb, oracle, views, dtype, dtype,
+                             lambda lay: kdb.call("elementwise", op, dtype, dtype, lay, kd.params()),
+                             lambda lay: oracle.oracle_elementwise(op, dtype, dtype, lay, kd.params()), rng, op)
+        assert_same(got, want, True, what=f"{name} {shape}")
+
+
 C2 = (4096, 4096)
 
 
