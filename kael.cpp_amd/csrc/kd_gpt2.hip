@@ -47,36 +47,59 @@ struct Step {
 
 // ---- kernels -------------------------------------------------------------------------------
 
-__device__ __forceinline__ double block_sum_d(double v, double* scratch) {
-#pragma unroll
-    for (int m = 32; m > 0; m /= 2) v += __shfl_xor(v, m, 64);
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const int waves = blockDim.x / 64;
-    __syncthreads();
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    double r = scratch[0];
-    for (int w = 1; w < waves; ++w) r += scratch[w];
-    return r;
-}
+// Whole-workgroup LayerNorm of x[0, d) into h, d <= 4 * kThreads: one read of x into registers,
+// the sums of (x - c) and (x - c)^2 in double around the pivot c = x[0] (one pass; the shift
+// keeps the variance free of cancellation) with a single workgroup reduction, then mean =
+// c + S1/d and the population variance S2/d - (S1/d)^2; each element is standardised in double,
+// rounded to float, then * w and + b, each rounded (reference src/ops/nn.cpp:114-129 then
+// src/nn/layers.cpp:67).
+constexpr int64_t kMaxLnDim = 4 * kThreads;
 
-// Whole-workgroup LayerNorm of x[0, d) into h: mean and population variance in double, the
-// standardised value rounded to float, then * w and + b, each rounded (reference
-// src/ops/nn.cpp:114-129 then src/nn/layers.cpp:67).
 __device__ void block_layernorm(const float* x, int64_t d, const float* w, const float* b, float* h) {
-    __shared__ double scratch[16];
-    double s = 0.0;
-    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) s += static_cast<double>(x[i]);
-    const double mean = block_sum_d(s, scratch) / static_cast<double>(d);
-    double q = 0.0;
-    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
-        const double dv = static_cast<double>(x[i]) - mean;
-        q += dv * dv;
+    __shared__ double sums[2][kThreads / 64];
+    float xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        xv[j] = i < d ? x[i] : 0.f;
     }
-    const double scale = std::sqrt(block_sum_d(q, scratch) / static_cast<double>(d) + 1e-5);
-    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
-        const float y = static_cast<float>((static_cast<double>(x[i]) - mean) / scale);
-        h[i] = __fadd_rn(__fmul_rn(y, w[i]), b[i]);
+    const double c = x[0];
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (threadIdx.x + j * kThreads < d) {
+            const double t = static_cast<double>(xv[j]) - c;
+            s1 += t;
+            s2 += t * t;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) {
+        s1 += __shfl_xor(s1, m, 64);
+        s2 += __shfl_xor(s2, m, 64);
+    }
+    const int wave = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) {
+        sums[0][wave] = s1;
+        sums[1][wave] = s2;
+    }
+    __syncthreads();
+    s1 = sums[0][0];
+    s2 = sums[1][0];
+    for (int v = 1; v < kThreads / 64; ++v) {
+        s1 += sums[0][v];
+        s2 += sums[1][v];
+    }
+    const double m1 = s1 / static_cast<double>(d);
+    const double mean = c + m1;
+    const double scale = std::sqrt(s2 / static_cast<double>(d) - m1 * m1 + 1e-5);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        if (i < d) {
+            const float y = static_cast<float>((static_cast<double>(xv[j]) - mean) / scale);
+            h[i] = __fadd_rn(__fmul_rn(y, w[i]), b[i]);
+        }
     }
 }
 
@@ -187,8 +210,8 @@ struct GemvArgs {
     const float* bias;     // [N] or nullptr
     float* out;            // [N]
     int64_t N, K;
-    // When ln_w is non-null the input is LayerNorm(x) with this weight and bias, computed by every
-    // workgroup into LDS (a 768-vector: cheaper than a separate launch).
+    // With the Ln template flag the input is LayerNorm(x) with this weight and bias, computed by
+    // every workgroup into LDS (a 768-vector: cheaper than a separate launch).
     const float* ln_w;
     const float* ln_b;
     // When attn.m is non-null the input is the attention output combined from chunk partials.
@@ -210,7 +233,7 @@ constexpr int kMaxK = 4096;
 // LDS. Rows: WavesPerRow == 1 -> each wave
 // owns 2 rows (8 rows per workgroup); WavesPerRow == 4 -> the workgroup owns 2 rows and each wave
 // a quarter of K, combined through LDS.
-template <int Epi, int WavesPerRow>
+template <int Epi, int WavesPerRow, bool Ln>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __shared__ float4 hs4[kMaxK / 4];
     __shared__ float part[4][2];
@@ -230,8 +253,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const float4* w0 = reinterpret_cast<const float4*>(a.W + (has0 ? n0 : 0) * K);
     const float4* w1 = reinterpret_cast<const float4*>(a.W + (has1 ? n0 + 1 : (has0 ? n0 : 0)) * K);
     // Issue this lane's first weight loads before the input prologue so that their HBM latency
-    // overlaps it.
-    constexpr int kPrefetch = 4;
+    // overlaps it. A LayerNorm input has K = d <= 1024, so with K split over 4 waves one float4
+    // per row covers a wave's range: the registers this frees hold the LayerNorm row and keep
+    // 6 workgroups per CU resident.
+    constexpr int kPrefetch = Ln && WavesPerRow == 4 ? 1 : 4;
     float4 pw0[kPrefetch], pw1[kPrefetch];
 #pragma unroll
     for (int i = 0; i < kPrefetch; ++i) {
@@ -241,7 +266,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             pw1[i] = w1[k];
         }
     }
-    if (a.ln_w != nullptr) {
+    // Operands of the epilogue, loaded now so that their latency overlaps the prologue and the
+    // dot products instead of following them.
+    const bool owner = WavesPerRow == 1 || wave == 0;
+    const bool active = owner && lane < 2 && (lane == 0 ? has0 : has1);
+    const int64_t n = n0 + lane;
+    float bias = 0.f, resid = 0.f;
+    if (active) {
+        if constexpr (Epi != kHead) bias = a.bias[n];
+        if constexpr (Epi == kResidual) resid = a.out[n];
+    }
+    const int64_t pos = Epi == kQkv ? a.st->pos : 0;
+    if constexpr (Ln) {
         block_layernorm(a.x, K, a.ln_w, a.ln_b, hs);
     } else if (a.attn.m != nullptr) {
         combine_attention(a.attn, K / a.head_dim, a.head_dim, hs);
@@ -284,20 +320,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         a1 = ((part[0][1] + part[1][1]) + part[2][1]) + part[3][1];
     }
     // lanes 0 and 1 of the owning wave finish rows n0 and n0 + 1
-    const bool owner = WavesPerRow == 1 || wave == 0;
-    const bool active = owner && lane < 2 && (lane == 0 ? has0 : has1);
-    const int64_t n = n0 + lane;
     float y = 0.f;
     if (active) {
         const float dot = lane == 0 ? a0 : a1;
-        y = Epi == kHead ? dot : __fadd_rn(dot, a.bias[n]);
+        y = Epi == kHead ? dot : __fadd_rn(dot, bias);
         if constexpr (Epi == kGeluTanh) {
             const float scale = std::sqrt(2 / MathConst<float>::pi);
             y = 0.5f * y * (1 + std::tanh(scale * (y + 0.044715f * y * y * y)));
         } else if constexpr (Epi == kGeluExact) {
             y = 0.5f * y * (1 + std::erf(y / MathConst<float>::sqrt2));
         } else if constexpr (Epi == kResidual) {
-            y = __fadd_rn(a.out[n], y);
+            y = __fadd_rn(resid, y);
         }
         if constexpr (Epi == kQkv) {
             const int64_t part_id = n / a.d;
@@ -308,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 const int64_t head = within / a.head_dim;
                 const int64_t dim = within - head * a.head_dim;
                 float* cache = part_id == 1 ? a.kcache : a.vcache;
-                cache[(head * a.max_positions + a.st->pos) * a.head_dim + dim] = y;
+                cache[(head * a.max_positions + pos) * a.head_dim + dim] = y;
             }
         } else {
             a.out[n] = y;
@@ -337,13 +370,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 }
 
 // Picks the greedy token among the head's workgroup partials, appends it to the sequence unless
-// the next position is teacher-forced, and advances the position. One workgroup.
-__global__ __launch_bounds__(kThreads) void argmax_final_kernel(Step* st, int64_t* seq, const float* pv,
-                                                                const int64_t* pi, int64_t parts) {
-    __shared__ float bv[kThreads / 64];
-    __shared__ int64_t bi[kThreads / 64];
+// the next position is teacher-forced, and advances the position. One workgroup of 1024 lanes:
+// GPT-2's 6283 partials take 7 loads per lane (4.7 us less per token than with 256 lanes).
+constexpr int kPickThreads = 1024;
+
+__global__ __launch_bounds__(kPickThreads) void argmax_final_kernel(Step* st, int64_t* seq, const float* pv,
+                                                                    const int64_t* pi, int64_t parts) {
+    __shared__ float bv[kPickThreads / 64];
+    __shared__ int64_t bi[kPickThreads / 64];
     Best r{-INFINITY, INT64_MAX};
-    for (int64_t i = threadIdx.x; i < parts; i += kThreads) {
+    for (int64_t i = threadIdx.x; i < parts; i += kPickThreads) {
         Best o{pv[i], pi[i]};
         if (better(o, r)) r = o;
     }
@@ -355,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void argmax_final_kernel(Step* st, int64_
     __syncthreads();
     if (threadIdx.x == 0) {
         Best w{bv[0], bi[0]};
-        for (int k = 1; k < kThreads / 64; ++k) {
+        for (int k = 1; k < kPickThreads / 64; ++k) {
             Best o{bv[k], bi[k]};
             if (better(o, w)) w = o;
         }
@@ -493,11 +529,12 @@ struct Engine {
         return dim3(static_cast<uint32_t>(split_k ? (n + 1) / 2 : (n + 7) / 8));
     }
 
-    template <int Epi> void gemv(hipStream_t s, const GemvArgs& a) const {
+    // Ln: the input is LayerNorm(a.x) with weight a.ln_w and bias a.ln_b (K = d).
+    template <int Epi, bool Ln> void gemv(hipStream_t s, const GemvArgs& a) const {
         // Few rows: split K across the workgroup's waves so that more workgroups stream weights.
         const bool split = a.N <= 4096;
-        if (split) hipLaunchKernelGGL((gemv_kernel<Epi, 4>), rows_grid(a.N, true), dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<Epi, 1>), rows_grid(a.N, false), dim3(kThreads), 0, s, a);
+        if (split) hipLaunchKernelGGL((gemv_kernel<Epi, 4, Ln>), rows_grid(a.N, true), dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((gemv_kernel<Epi, 1, Ln>), rows_grid(a.N, false), dim3(kThreads), 0, s, a);
     }
 
     int record_step(hipStream_t s) {
@@ -521,7 +558,7 @@ struct Engine {
             qkv.q = q;
             qkv.kcache = kc;
             qkv.vcache = vc;
-            gemv<kQkv>(s, qkv);
+            gemv<kQkv, true>(s, qkv);
             hipLaunchKernelGGL(attention_kernel, dim3(static_cast<uint32_t>(cfg.heads), kAttnChunks), dim3(kThreads), attn_lds,
                                s, st, q, kc, vc, partials, hd, cfg.max_positions, divisor);
             GemvArgs proj = base();
@@ -532,7 +569,7 @@ struct Engine {
             proj.out = x;
             proj.N = d;
             proj.K = d;
-            gemv<kResidual>(s, proj);
+            gemv<kResidual, false>(s, proj);
             GemvArgs fc1 = base();
             fc1.W = p(b + "mlp.fc1.weight");
             fc1.bias = p(b + "mlp.fc1.bias");
@@ -542,8 +579,8 @@ struct Engine {
             fc1.K = d;
             fc1.ln_w = p(b + "ln2.weight");
             fc1.ln_b = p(b + "ln2.bias");
-            if (cfg.tanh_gelu) gemv<kGeluTanh>(s, fc1);
-            else gemv<kGeluExact>(s, fc1);
+            if (cfg.tanh_gelu) gemv<kGeluTanh, true>(s, fc1);
+            else gemv<kGeluExact, true>(s, fc1);
             GemvArgs fc2 = base();
             fc2.W = p(b + "mlp.fc2.weight");
             fc2.bias = p(b + "mlp.fc2.bias");
@@ -551,7 +588,7 @@ struct Engine {
             fc2.out = x;
             fc2.N = d;
             fc2.K = ff;
-            gemv<kResidual>(s, fc2);
+            gemv<kResidual, false>(s, fc2);
         }
         hipLaunchKernelGGL(layernorm_kernel, dim3(1), dim3(kThreads), 0, s, x, d, p("ln_final.weight"), p("ln_final.bias"), h);
         GemvArgs head = base();
@@ -562,9 +599,9 @@ struct Engine {
         head.out = logits;
         head.best_v = pv;
         head.best_i = pi;
-        gemv<kHead>(s, head);
+        gemv<kHead, false>(s, head);
         const int64_t parts = head.N <= 4096 ? (head.N + 1) / 2 : (head.N + 7) / 8;
-        hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kThreads), 0, s, st, seq, pv, pi, parts);
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kPickThreads), 0, s, st, seq, pv, pi, parts);
         return KD_OK;
     }
 
@@ -642,6 +679,7 @@ int create(Engine& e, const kd_gpt_config& c) {
     if (e.hd > 64) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim above 64 is not supported");
     if (e.d % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: dimension must be a multiple of 4");
     if (e.ff > kMaxK) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: 4 * dimension above 4096 is not supported");
+    static_assert(kMaxK / 4 <= kMaxLnDim, "block_layernorm holds a row of at most kMaxLnDim elements");
     if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: more than 64 heads is not supported");
     if (c.max_positions > 8192) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: max_positions above 8192");
     // kael's parameter order and shapes (GPT::named_parameters)
