@@ -112,13 +112,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const Step* st, const i
         x[i] = __fadd_rn(wte[tok * d + i], wpe[pos * d + i]);
 }
 
-// h = LayerNorm(x) as one workgroup (the final LayerNorm before the head).
-__global__ __launch_bounds__(kThreads) void layernorm_kernel(const float* x, int64_t d, const float* w, const float* b,
-                                                             float* h) {
-    block_layernorm(x, d, w, b, h);
-}
-
-enum Epilogue { kStore = 0, kGeluTanh = 1, kGeluExact = 2, kResidual = 3, kQkv = 4, kHead = 5 };
+enum Epilogue { kStore = 0, kGeluTanh = 1, kGeluExact = 2, kResidual = 3, kQkv = 4 };
 
 struct Best {
     float v;
@@ -143,6 +137,7 @@ __device__ __forceinline__ Best wave_best(Best v) {
 }
 
 constexpr int kAttnChunks = 8;
+constexpr int kAttnRegs = 8;  // keys per 16-lane group whose rows attention_kernel holds in registers
 
 struct AttnPartials {
     float* m;      // [heads][chunks]
@@ -160,6 +155,19 @@ constexpr int kMaxHeads = 64;
 __device__ void combine_attention(const AttnPartials& p, int64_t heads, int64_t head_dim, float* h) {
     __shared__ float factor[kMaxHeads * kAttnChunks];
     __shared__ float denom[kMaxHeads];
+    // The chunk outputs of this thread's elements (heads * head_dim <= kMaxLnDim), loaded first:
+    // they do not depend on the factors.
+    constexpr int kPer = kMaxLnDim / kThreads;
+    float acc[kPer][kAttnChunks];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t k = threadIdx.x + r * kThreads;
+        const int64_t hd = k / head_dim;
+        const int64_t e = k - hd * head_dim;
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c)
+            acc[r][c] = k < heads * head_dim ? p.acc[(hd * kAttnChunks + c) * head_dim + e] : 0.f;
+    }
     const int64_t slots = heads * kAttnChunks;
     for (int64_t i = threadIdx.x; i < slots; i += blockDim.x) factor[i] = p.m[i];
     __syncthreads();
@@ -191,16 +199,16 @@ __device__ void combine_attention(const AttnPartials& p, int64_t heads, int64_t 
         denom[hd] = static_cast<float>(lsum);
     }
     __syncthreads();
-    for (int64_t k = threadIdx.x; k < heads * head_dim; k += blockDim.x) {
-        const int64_t hd = k / head_dim;
-        const int64_t e = k - hd * head_dim;
-        float acc[kAttnChunks];
 #pragma unroll
-        for (int c = 0; c < kAttnChunks; ++c) acc[c] = p.acc[(hd * kAttnChunks + c) * head_dim + e];
-        float num = 0.f;
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t k = threadIdx.x + r * kThreads;
+        if (k < heads * head_dim) {
+            const int64_t hd = k / head_dim;
+            float num = 0.f;
 #pragma unroll
-        for (int c = 0; c < kAttnChunks; ++c) num += factor[hd * kAttnChunks + c] * acc[c];
-        h[k] = __fdiv_rn(num, denom[hd]);
+            for (int c = 0; c < kAttnChunks; ++c) num += factor[hd * kAttnChunks + c] * acc[r][c];
+            h[k] = __fdiv_rn(num, denom[hd]);
+        }
     }
 }
 
@@ -221,7 +229,7 @@ struct GemvArgs {
     float* kcache;
     float* vcache;
     int64_t d, head_dim, max_positions;
-    // kHead: per-workgroup argmax partials (argmax_final_kernel picks the winner)
+    // head_kernel: per-workgroup argmax partials (argmax_final_kernel picks the winner)
     float* best_v;
     int64_t* best_i;
     Step* st;
@@ -237,8 +245,6 @@ template <int Epi, int WavesPerRow, bool Ln>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __shared__ float4 hs4[kMaxK / 4];
     __shared__ float part[4][2];
-    __shared__ float bv[kThreads / 64 * 2];
-    __shared__ int64_t bi[kThreads / 64 * 2];
     float* hs = reinterpret_cast<float*>(hs4);
     const int64_t K = a.K;
     const int lane = threadIdx.x % 64;
@@ -273,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const int64_t n = n0 + lane;
     float bias = 0.f, resid = 0.f;
     if (active) {
-        if constexpr (Epi != kHead) bias = a.bias[n];
+        bias = a.bias[n];
         if constexpr (Epi == kResidual) resid = a.out[n];
     }
     const int64_t pos = Epi == kQkv ? a.st->pos : 0;
@@ -323,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     float y = 0.f;
     if (active) {
         const float dot = lane == 0 ? a0 : a1;
-        y = Epi == kHead ? dot : __fadd_rn(dot, bias);
+        y = __fadd_rn(dot, bias);
         if constexpr (Epi == kGeluTanh) {
             const float scale = std::sqrt(2 / MathConst<float>::pi);
             y = 0.5f * y * (1 + std::tanh(scale * (y + 0.044715f * y * y * y)));
@@ -347,25 +353,101 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             a.out[n] = y;
         }
     }
-    if constexpr (Epi == kHead) {
-        // Workgroup best of its rows; argmax_final_kernel picks among the workgroups.
-        Best b{-INFINITY, INT64_MAX};
-        if (active) b = Best{y, n};
-        b = wave_best(b);
-        if (lane == 0) {
-            bv[wave] = b.v;
-            bi[wave] = b.i;
+}
+
+// Logits of the tied head, logits[n] = wte[n, :] . LayerNorm_f(x), and each workgroup's best
+// row (first maximum, first NaN; reference src/ops/reduce.cpp:236-254) for argmax_final_kernel.
+// A fixed grid of 2 workgroups per CU streams the [vocab, d] table: each wave takes row pairs
+// p, p + stride, ... and issues the next pair's loads before the current pair's dot products,
+// so every wave keeps two pairs in flight. The final LayerNorm is computed once per workgroup
+// into LDS and then held in registers (one launch fewer than a separate LayerNorm, and 512
+// argmax partials instead of one per 8 rows). Needs d <= kMaxLnDim (4 float4 per lane).
+constexpr int kHeadVec = kMaxLnDim / 256;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load with the nontemporal hint (the table is read once per token).
+__device__ __forceinline__ float4 nt_load4(const float4* p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
+    __shared__ float4 hs4[kMaxLnDim / 4];
+    __shared__ float bv[kThreads / 64];
+    __shared__ int64_t bi[kThreads / 64];
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const int64_t N = a.N;
+    const int64_t k4 = a.K / 4;
+    const int64_t pairs = (N + 1) / 2;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
+    const float4* W4 = reinterpret_cast<const float4*>(a.W);
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    const auto load = [&](int64_t pair, float4 (&r0)[kHeadVec], float4 (&r1)[kHeadVec]) {
+        const int64_t n = 2 * pair;
+        const bool second = n + 1 < N;
+#pragma unroll
+        for (int i = 0; i < kHeadVec; ++i) {
+            const int64_t j = lane + 64 * i;
+            r0[i] = j < k4 ? nt_load4(W4 + n * k4 + j) : zero;
+            r1[i] = j < k4 && second ? nt_load4(W4 + (n + 1) * k4 + j) : zero;
         }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            Best r{bv[0], bi[0]};
-            for (int w = 1; w < kThreads / 64; ++w) {
-                Best o{bv[w], bi[w]};
-                if (better(o, r)) r = o;
-            }
-            a.best_v[blockIdx.x] = r.v;
-            a.best_i[blockIdx.x] = r.i;
+    };
+    int64_t p = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave;
+    float4 c0[kHeadVec], c1[kHeadVec];
+    if (p < pairs) load(p, c0, c1);
+    block_layernorm(a.x, a.K, a.ln_w, a.ln_b, reinterpret_cast<float*>(hs4));
+    __syncthreads();
+    float4 h[kHeadVec];
+#pragma unroll
+    for (int i = 0; i < kHeadVec; ++i) {
+        const int64_t j = lane + 64 * i;
+        h[i] = j < k4 ? hs4[j] : zero;
+    }
+    Best best{-INFINITY, INT64_MAX};
+    for (; p < pairs; p += stride) {
+        float4 n0[kHeadVec], n1[kHeadVec];
+        if (p + stride < pairs) load(p + stride, n0, n1);
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < kHeadVec; ++i) {
+            a0 += c0[i].x * h[i].x + c0[i].y * h[i].y + c0[i].z * h[i].z + c0[i].w * h[i].w;
+            a1 += c1[i].x * h[i].x + c1[i].y * h[i].y + c1[i].z * h[i].z + c1[i].w * h[i].w;
         }
+#pragma unroll
+        for (int m = 32; m > 0; m /= 2) {
+            a0 += __shfl_xor(a0, m, 64);
+            a1 += __shfl_xor(a1, m, 64);
+        }
+        const int64_t n = 2 * p;
+        if (lane == 0) a.out[n] = a0;
+        if (lane == 1 && n + 1 < N) a.out[n + 1] = a1;
+        const Best o0{a0, n};
+        if (better(o0, best)) best = o0;
+        if (n + 1 < N) {
+            const Best o1{a1, n + 1};
+            if (better(o1, best)) best = o1;
+        }
+#pragma unroll
+        for (int i = 0; i < kHeadVec; ++i) {
+            c0[i] = n0[i];
+            c1[i] = n1[i];
+        }
+    }
+    if (lane == 0) {
+        bv[wave] = best.v;
+        bi[wave] = best.i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Best r{bv[0], bi[0]};
+        for (int w = 1; w < kThreads / 64; ++w) {
+            const Best o{bv[w], bi[w]};
+            if (better(o, r)) r = o;
+        }
+        a.best_v[blockIdx.x] = r.v;
+        a.best_i[blockIdx.x] = r.i;
     }
 }
 
@@ -428,18 +510,38 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
     if (dims_ok) qv = *reinterpret_cast<const float4*>(q + h * head_dim + 4 * sub);
     const float* K = kcache + (h * max_positions + j0) * head_dim;
     const float* V = vcache + (h * max_positions + j0) * head_dim;
-    float local_max = -INFINITY;
-    for (int64_t j = group; j < count; j += kThreads / 16) {
-        float sc = 0.f;
-        if (dims_ok) {
-            const float4 k = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
-            sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
+    // The first kAttnRegs keys of each 16-lane group: key and value rows issued together up
+    // front (the value loads need only the position, not the scores).
+    float4 kreg[kAttnRegs], vreg[kAttnRegs];
+#pragma unroll
+    for (int u = 0; u < kAttnRegs; ++u) {
+        const int64_t j = group + u * (kThreads / 16);
+        const bool ok = dims_ok && j < count;
+        kreg[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        vreg[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ok) {
+            kreg[u] = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
+            vreg[u] = *reinterpret_cast<const float4*>(V + j * head_dim + 4 * sub);
         }
+    }
+    float local_max = -INFINITY;
+    const auto score = [&](int64_t j, float4 k) {
+        float sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
 #pragma unroll
         for (int m = 8; m > 0; m /= 2) sc += __shfl_xor(sc, m, 64);
         sc = __fdiv_rn(sc, divisor);
         if (sub == 0) scores[j] = sc;
         local_max = max_na(local_max, sc);
+    };
+#pragma unroll
+    for (int u = 0; u < kAttnRegs; ++u) {
+        const int64_t j = group + u * (kThreads / 16);
+        if (j < count) score(j, kreg[u]);
+    }
+    for (int64_t j = group + kAttnRegs * (kThreads / 16); j < count; j += kThreads / 16) {
+        float4 k = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (dims_ok) k = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
+        score(j, k);
     }
 #pragma unroll
     for (int m = 32; m > 0; m /= 2) local_max = max_na(local_max, __shfl_xor(local_max, m, 64));
@@ -459,14 +561,20 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
     __syncthreads();
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (dims_ok) {
-        for (int64_t j = group; j < count; j += kThreads / 16) {
+        const auto accumulate = [&](int64_t j, float4 v) {
             const float w = scores[j];
-            const float4 v = *reinterpret_cast<const float4*>(V + j * head_dim + 4 * sub);
             acc.x += w * v.x;
             acc.y += w * v.y;
             acc.z += w * v.z;
             acc.w += w * v.w;
+        };
+#pragma unroll
+        for (int u = 0; u < kAttnRegs; ++u) {
+            const int64_t j = group + u * (kThreads / 16);
+            if (j < count) accumulate(j, vreg[u]);
         }
+        for (int64_t j = group + kAttnRegs * (kThreads / 16); j < count; j += kThreads / 16)
+            accumulate(j, *reinterpret_cast<const float4*>(V + j * head_dim + 4 * sub));
     }
     acc_part[group][sub] = acc;
     __syncthreads();
@@ -501,7 +609,6 @@ struct Engine {
     float* kcache = nullptr;
     float* vcache = nullptr;
     float* x = nullptr;
-    float* h = nullptr;
     float* q = nullptr;
     AttnPartials partials{};
     float* f = nullptr;
@@ -523,6 +630,13 @@ struct Engine {
         a.max_positions = cfg.max_positions;
         a.st = st;
         return a;
+    }
+
+    // Workgroups of head_kernel: 2 per CU, fewer when the vocabulary has fewer row pairs than
+    // that grid has waves.
+    int64_t head_groups() const {
+        const int64_t waves = (cfg.vocab_size + 1) / 2;
+        return std::max<int64_t>(1, std::min<int64_t>(4 * compute_units(), (waves + 3) / 4));
     }
 
     static dim3 rows_grid(int64_t n, bool split_k) {
@@ -590,17 +704,18 @@ struct Engine {
             fc2.K = ff;
             gemv<kResidual, false>(s, fc2);
         }
-        hipLaunchKernelGGL(layernorm_kernel, dim3(1), dim3(kThreads), 0, s, x, d, p("ln_final.weight"), p("ln_final.bias"), h);
         GemvArgs head = base();
         head.W = p("token_embedding.weight");
-        head.x = h;
+        head.x = x;
+        head.ln_w = p("ln_final.weight");
+        head.ln_b = p("ln_final.bias");
         head.N = cfg.vocab_size;
         head.K = d;
         head.out = logits;
         head.best_v = pv;
         head.best_i = pi;
-        gemv<kHead, false>(s, head);
-        const int64_t parts = head.N <= 4096 ? (head.N + 1) / 2 : (head.N + 7) / 8;
+        const int64_t parts = head_groups();
+        hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
         hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kPickThreads), 0, s, st, seq, pv, pi, parts);
         return KD_OK;
     }
@@ -652,7 +767,7 @@ struct Engine {
     ~Engine() {
         if (graph) (void)hipGraphExecDestroy(graph);
         for (void* ptr : {static_cast<void*>(params), static_cast<void*>(kcache), static_cast<void*>(vcache),
-                          static_cast<void*>(x), static_cast<void*>(h), static_cast<void*>(q), static_cast<void*>(partials.m),
+                          static_cast<void*>(x), static_cast<void*>(q), static_cast<void*>(partials.m),
                           static_cast<void*>(partials.l), static_cast<void*>(partials.acc),
                           static_cast<void*>(f), static_cast<void*>(logits), static_cast<void*>(pv),
                           static_cast<void*>(pi), static_cast<void*>(seq), static_cast<void*>(st)})
@@ -716,16 +831,14 @@ int create(Engine& e, const kd_gpt_config& c) {
     if (int rc = alloc(&e.kcache, cache)) return rc;
     if (int rc = alloc(&e.vcache, cache)) return rc;
     if (int rc = alloc(&e.x, e.d)) return rc;
-    if (int rc = alloc(&e.h, e.d)) return rc;
     if (int rc = alloc(&e.q, e.d)) return rc;
     if (int rc = alloc(&e.partials.m, c.heads * kAttnChunks)) return rc;
     if (int rc = alloc(&e.partials.l, c.heads * kAttnChunks)) return rc;
     if (int rc = alloc(&e.partials.acc, c.heads * kAttnChunks * e.hd)) return rc;
     if (int rc = alloc(&e.f, e.ff)) return rc;
     if (int rc = alloc(&e.logits, c.vocab_size)) return rc;
-    const int64_t head_groups = (c.vocab_size + 1) / 2 + 1;  // enough for either GEMV row layout
-    if (int rc = alloc(&e.pv, head_groups)) return rc;
-    if (int rc = alloc(&e.pi, head_groups)) return rc;
+    if (int rc = alloc(&e.pv, e.head_groups())) return rc;
+    if (int rc = alloc(&e.pi, e.head_groups())) return rc;
 
     if (int rc = alloc(&e.seq, c.max_positions + 1)) return rc;
     if (int rc = alloc(&e.st, 1)) return rc;
