@@ -57,32 +57,10 @@ class Timer:
         self.ms = ms.value
 
 
-class Lead:
-    """Matmuls queued ahead of the start event when a step is shorter than the host's call path.
-
-    A ctypes call into the backend takes ~25 us of host time, longer than a 22 us HBM-bound
-    kernel, so without a lead the GPU would idle between the timed launches and the events would
-    time the Python loop. While the lead runs (~0.14 ms per 2048^3 matmul) the host queues every
-    timed step; the events then bracket the timed kernels back to back."""
-
-    def __init__(self, backend, n=2048):
-        self.b = backend
-        self.n = n
-        self.a = backend.to_device(np.ones((n, n), np.float32))
-        self.c = backend.empty((n, n), np.float32)
-        self.sizes = kd.MatmulSizes(1, n, n, n)
-
-    def queue(self, steps):
-        for _ in range(2 + steps // 3):  # ~50 us of host time per step covered
-            self.b.check(self.b.lib.kd_matmul(kd.F32, self.a.ptr, self.a.ptr, self.c.ptr, self.sizes), "lead")
-
-
-def time_steps(backend, step, steps, warmup, lead=None):
+def time_steps(backend, step, steps, warmup):
     for _ in range(warmup):
         step(0)
     backend.synchronize()
-    if lead is not None:
-        lead.queue(steps)
     t0 = time.perf_counter()
     with Timer(backend) as t:
         for i in range(steps):
@@ -132,17 +110,15 @@ def bench_c2(backend, steps, warmup):
     p = kd.params()
     ew = backend.lib.kd_elementwise
     rd = backend.lib.kd_reduce
-    lead = Lead(backend)
     for name, op in (("add", kd.OP["PLUS"]), ("mul", kd.OP["TIMES"]), ("transposed_add", kd.OP["PLUS"])):
         ls = lays[name]
-        ms, _ = time_steps(backend, lambda i: ew(op, kd.F32, kd.F32, ctypes.byref(ls[i % sets]), p), steps, warmup,
-                           lead)
+        ms, _ = time_steps(backend, lambda i: ew(op, kd.F32, kd.F32, ctypes.byref(ls[i % sets]), p), steps, warmup)
         out[name] = {"us": ms * 1e3, "gbps": algo_bytes[name] / (ms * 1e-3) / 1e9}
     ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_SUM, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr, cols, rows),
-                       steps, warmup, lead)
+                       steps, warmup)
     out["sum_dim1"] = {"us": ms * 1e3, "gbps": algo_bytes["sum_dim1"] / (ms * 1e-3) / 1e9}
     ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_MAX, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr,
-                                             rows * cols, 1), steps, warmup, lead)
+                                             rows * cols, 1), steps, warmup)
     out["max_all"] = {"us": ms * 1e3, "gbps": algo_bytes["max_all"] / (ms * 1e-3) / 1e9}
     for v in out.values():
         v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
@@ -160,19 +136,17 @@ def bench_rows(backend, steps, warmup):
     bb = backend.to_device(np.zeros(cols, np.float32))
     nbytes = 2 * rows * cols * 4
     out = {}
-    lead = Lead(backend)
     sm = backend.lib.kd_softmax_rows
-    ms, _ = time_steps(backend, lambda i: sm(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 0), steps, warmup,
-                       lead)
+    ms, _ = time_steps(backend, lambda i: sm(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 0), steps, warmup)
     out["softmax_1024"] = {"us": ms * 1e3, "gbps": nbytes / (ms * 1e-3) / 1e9}
     st = backend.lib.kd_standardize_rows
     ms, _ = time_steps(backend, lambda i: st(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 1e-5, w.ptr, bb.ptr),
-                       steps, warmup, lead)
+                       steps, warmup)
     out["layernorm_1024"] = {"us": ms * 1e3, "gbps": (nbytes + 2 * cols * 4) / (ms * 1e-3) / 1e9}
     # GELU (tanh form, GPT-2's default) over the same rows: an element op on the vector path.
     gl = [kd.element_layout((rows * cols,), [(4,), (4,)], [y[i].ptr, x[i].ptr]) for i in range(sets)]
     ew, gp, gelu = backend.lib.kd_elementwise, kd.params(), kd.OP["GELU_TANH"]
-    ms, _ = time_steps(backend, lambda i: ew(gelu, kd.F32, kd.F32, ctypes.byref(gl[i % sets]), gp), steps, warmup, lead)
+    ms, _ = time_steps(backend, lambda i: ew(gelu, kd.F32, kd.F32, ctypes.byref(gl[i % sets]), gp), steps, warmup)
     out["gelu_tanh_1024"] = {"us": ms * 1e3, "gbps": nbytes / (ms * 1e-3) / 1e9}
     for v in out.values():
         v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS

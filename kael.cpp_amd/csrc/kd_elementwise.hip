@@ -130,7 +130,10 @@ template <bool NT, typename T> __device__ __forceinline__ void st(T* p, const T&
     }
 }
 
-template <typename F, int VEC, bool NT>
+// Outer1: at most one outer dim (contiguous tensors, row and column broadcasts): the outer
+// strides are loop invariants held in scalar registers, instead of a per-vector decode loop
+// whose dynamically indexed kernel arguments cost a scalar-load round trip per vector.
+template <typename F, int VEC, bool NT, bool Outer1>
 __global__ __launch_bounds__(kBlock) void vec_kernel(F f, Bases bases, Decode outer,
                                                      uint32_t inner_vectors, FastDiv inner_div,
                                                      uint32_t total_vectors, uint32_t broadcast_mask) {
@@ -142,7 +145,12 @@ __global__ __launch_bounds__(kBlock) void vec_kernel(F f, Bases bases, Decode ou
         const uint32_t row = inner_div.div(v);
         const uint32_t col = v - row * inner_vectors;
         int64_t off[KD_MAX_OPERANDS];
-        decode<N + 1>(outer, row, off);
+        if constexpr (Outer1) {
+#pragma unroll
+            for (int op = 0; op <= N; ++op) off[op] = static_cast<int64_t>(row) * outer.stride[op][0];
+        } else {
+            decode<N + 1>(outer, row, off);
+        }
         Vec<In, VEC> in[3];
 #pragma unroll
         for (int i = 0; i < N; ++i) {
@@ -424,16 +432,29 @@ template <typename F> int launch(const F& f, const kd_element_layout& l) {
             }
         }
         if (vec_ok) {
-            Decode outer;
+            Decode outer{};
             make_decode(l, operands, 0, last, outer);
             const uint32_t inner_vectors = static_cast<uint32_t>(l.shape[last] / VEC);
             const uint32_t total = static_cast<uint32_t>(l.count / VEC);
-            if (streaming(l, out_size, in_size, operands))
-                hipLaunchKernelGGL((vec_kernel<F, VEC, true>), dim3(grid_for(total)), dim3(kBlock), 0, stream(), f,
-                                   bases, outer, inner_vectors, FastDiv(inner_vectors), total, broadcast_mask);
-            else
-                hipLaunchKernelGGL((vec_kernel<F, VEC, false>), dim3(grid_for(total)), dim3(kBlock), 0, stream(), f,
-                                   bases, outer, inner_vectors, FastDiv(inner_vectors), total, broadcast_mask);
+            const bool nt = streaming(l, out_size, in_size, operands);
+            const dim3 grid(grid_for(total));
+            const FastDiv inner_div(inner_vectors);
+            // With no outer dim the row is always 0; the zeroed strides make every offset 0.
+            if (outer.dims <= 1) {
+                if (nt)
+                    hipLaunchKernelGGL((vec_kernel<F, VEC, true, true>), grid, dim3(kBlock), 0, stream(), f, bases,
+                                       outer, inner_vectors, inner_div, total, broadcast_mask);
+                else
+                    hipLaunchKernelGGL((vec_kernel<F, VEC, false, true>), grid, dim3(kBlock), 0, stream(), f, bases,
+                                       outer, inner_vectors, inner_div, total, broadcast_mask);
+            } else {
+                if (nt)
+                    hipLaunchKernelGGL((vec_kernel<F, VEC, true, false>), grid, dim3(kBlock), 0, stream(), f, bases,
+                                       outer, inner_vectors, inner_div, total, broadcast_mask);
+                else
+                    hipLaunchKernelGGL((vec_kernel<F, VEC, false, false>), grid, dim3(kBlock), 0, stream(), f, bases,
+                                       outer, inner_vectors, inner_div, total, broadcast_mask);
+            }
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
