@@ -6,7 +6,10 @@ kd_matmul call over inputs already resident in HBM. Secondary figures in "extra"
 (512^3), the C2 elementwise/reduction ops in GB/s, and the fused row kernels.
 
 Timing: W untimed warm-up steps, then K steps bracketed by kd_synchronize(); the kernel time comes
-from HIP events recorded on the backend stream (the stream every kd_* launch uses).
+from HIP events recorded on the backend stream (the stream every kd_* launch uses). The GPU's
+clocks ramp up from idle over tens of milliseconds (the 4096^3 matmul measures ~127 TFLOP/s after
+5 warm-up steps and ~140 after 50), so W defaults to 50 for the headline; the secondary sections,
+whose steps take microseconds, warm up for at least MIN_WARMUP_S of steps.
 The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference sources,
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
@@ -31,10 +34,10 @@ import kd  # noqa: E402
 
 FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense FP32 matrix (AMD spec)
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
-# HBM bytes one 4096^3 mfma_f32_kernel launch moves, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# (347 241 KiB and 65 536 KiB per dispatch), scaled by the factors a plain 256 MiB copy gives the
-# same counters (x2.0 fetch, x1.0 write). The PMC runs and commands are kept in profiles/.
-MATMUL_4096_TRAFFIC_BYTES = (2 * 347241 + 65536) * 1024
+# HBM bytes one 4096^3 mfma_f32_rowmajor_kernel launch moves, from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (197 383 KiB and 65 536 KiB per dispatch), scaled by the factors a plain 256 MiB copy
+# gives the same counters (x2.0 fetch, x1.0 write). The PMC runs and commands are kept in profiles/.
+MATMUL_4096_TRAFFIC_BYTES = (2 * 197383 + 65536) * 1024
 
 
 class Timer:
@@ -57,9 +60,18 @@ class Timer:
         self.ms = ms.value
 
 
-def time_steps(backend, step, steps, warmup):
-    for _ in range(warmup):
-        step(0)
+MIN_WARMUP_S = 0.05
+
+
+def time_steps(backend, step, steps, warmup, min_warmup_s=0.0):
+    """W warm-up steps (continued until `min_warmup_s` of wall time when given), then K timed steps."""
+    t_start = time.perf_counter()
+    done = 0
+    while done < warmup or (min_warmup_s > 0 and time.perf_counter() - t_start < min_warmup_s):
+        step(done)
+        done += 1
+        if done >= warmup and min_warmup_s > 0 and done % 64 == 0:
+            backend.synchronize()
     backend.synchronize()
     t0 = time.perf_counter()
     with Timer(backend) as t:
@@ -70,7 +82,7 @@ def time_steps(backend, step, steps, warmup):
     return t.ms / steps, wall
 
 
-def bench_matmul(backend, n, steps, warmup, seed=0):
+def bench_matmul(backend, n, steps, warmup, seed=0, min_warmup_s=0.0):
     rng = np.random.default_rng(seed)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
     b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
@@ -83,7 +95,7 @@ def bench_matmul(backend, n, steps, warmup, seed=0):
         if rc:
             backend.check(rc, "kd_matmul")
 
-    ms, wall = time_steps(backend, step, steps, warmup)
+    ms, wall = time_steps(backend, step, steps, warmup, min_warmup_s)
     flops = 2.0 * n ** 3
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "wall_s": wall, "flops_per_launch": flops}
 
@@ -112,13 +124,14 @@ def bench_c2(backend, steps, warmup):
     rd = backend.lib.kd_reduce
     for name, op in (("add", kd.OP["PLUS"]), ("mul", kd.OP["TIMES"]), ("transposed_add", kd.OP["PLUS"])):
         ls = lays[name]
-        ms, _ = time_steps(backend, lambda i: ew(op, kd.F32, kd.F32, ctypes.byref(ls[i % sets]), p), steps, warmup)
+        ms, _ = time_steps(backend, lambda i: ew(op, kd.F32, kd.F32, ctypes.byref(ls[i % sets]), p), steps, warmup,
+                           MIN_WARMUP_S)
         out[name] = {"us": ms * 1e3, "gbps": algo_bytes[name] / (ms * 1e-3) / 1e9}
     ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_SUM, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr, cols, rows),
-                       steps, warmup)
+                       steps, warmup, MIN_WARMUP_S)
     out["sum_dim1"] = {"us": ms * 1e3, "gbps": algo_bytes["sum_dim1"] / (ms * 1e-3) / 1e9}
     ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_MAX, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr,
-                                             rows * cols, 1), steps, warmup)
+                                             rows * cols, 1), steps, warmup, MIN_WARMUP_S)
     out["max_all"] = {"us": ms * 1e3, "gbps": algo_bytes["max_all"] / (ms * 1e-3) / 1e9}
     for v in out.values():
         v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
@@ -137,16 +150,18 @@ def bench_rows(backend, steps, warmup):
     nbytes = 2 * rows * cols * 4
     out = {}
     sm = backend.lib.kd_softmax_rows
-    ms, _ = time_steps(backend, lambda i: sm(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 0), steps, warmup)
+    ms, _ = time_steps(backend, lambda i: sm(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 0), steps, warmup,
+                       MIN_WARMUP_S)
     out["softmax_1024"] = {"us": ms * 1e3, "gbps": nbytes / (ms * 1e-3) / 1e9}
     st = backend.lib.kd_standardize_rows
     ms, _ = time_steps(backend, lambda i: st(kd.F32, y[i % sets].ptr, x[i % sets].ptr, rows, cols, 1e-5, w.ptr, bb.ptr),
-                       steps, warmup)
+                       steps, warmup, MIN_WARMUP_S)
     out["layernorm_1024"] = {"us": ms * 1e3, "gbps": (nbytes + 2 * cols * 4) / (ms * 1e-3) / 1e9}
     # GELU (tanh form, GPT-2's default) over the same rows: an element op on the vector path.
     gl = [kd.element_layout((rows * cols,), [(4,), (4,)], [y[i].ptr, x[i].ptr]) for i in range(sets)]
     ew, gp, gelu = backend.lib.kd_elementwise, kd.params(), kd.OP["GELU_TANH"]
-    ms, _ = time_steps(backend, lambda i: ew(gelu, kd.F32, kd.F32, ctypes.byref(gl[i % sets]), gp), steps, warmup)
+    ms, _ = time_steps(backend, lambda i: ew(gelu, kd.F32, kd.F32, ctypes.byref(gl[i % sets]), gp), steps, warmup,
+                       MIN_WARMUP_S)
     out["gelu_tanh_1024"] = {"us": ms * 1e3, "gbps": nbytes / (ms * 1e-3) / 1e9}
     for v in out.values():
         v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
@@ -161,7 +176,7 @@ def bench_copy(backend, steps, warmup, mib=256):
     dst = backend.empty((n,), np.float32)
     lay = kd.element_layout((n,), [(4,), (4,)], [dst.ptr, src.ptr])
     fn = backend.lib.kd_convert
-    ms, _ = time_steps(backend, lambda i: fn(kd.F32, kd.F32, ctypes.byref(lay)), steps, warmup)
+    ms, _ = time_steps(backend, lambda i: fn(kd.F32, kd.F32, ctypes.byref(lay)), steps, warmup, MIN_WARMUP_S)
     return {"us": ms * 1e3, "bytes_per_launch": 2 * n * 4, "gbps": 2 * n * 4 / (ms * 1e-3) / 1e9}
 
 
@@ -274,7 +289,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
     ap.add_argument("--only", default="", choices=["", "all", "matmul", "copy", "c2", "rows", "gpt2"],
@@ -303,7 +318,7 @@ def main() -> int:
         return 0
     main_run = bench_matmul(backend, n, args.steps, args.warmup)
     if args.only in ("", "all"):
-        extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup)
+        extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
         extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
         extra["gpt2_decode"] = bench_gpt2(backend)
