@@ -133,6 +133,14 @@ def bench_c2(backend, steps, warmup):
     ms, _ = time_steps(backend, lambda i: rd(kd.REDUCE_MAX, kd.F32, kd.F32, red[i % sets].ptr, a[i % sets].ptr,
                                              rows * cols, 1), steps, warmup, MIN_WARMUP_S)
     out["max_all"] = {"us": ms * 1e3, "gbps": algo_bytes["max_all"] / (ms * 1e-3) / 1e9}
+    # Reductions kael runs on the host, on the same matrix: argmax along dim 1 and cumsum along dim 1.
+    idx = [backend.empty((rows,), np.int64) for _ in range(sets)]
+    ms, _ = time_steps(backend, lambda i: backend.lib.kd_arg_reduce(1, kd.F32, idx[i % sets].ptr, a[i % sets].ptr,
+                                                                    cols, rows), steps, warmup, MIN_WARMUP_S)
+    out["argmax_dim1"] = {"us": ms * 1e3, "gbps": (rows * cols * 4 + rows * 8) / (ms * 1e-3) / 1e9}
+    ms, _ = time_steps(backend, lambda i: backend.lib.kd_cumsum(kd.F32, o[i % sets].ptr, a[i % sets].ptr, cols, rows),
+                       steps, warmup, MIN_WARMUP_S)
+    out["cumsum_dim1"] = {"us": ms * 1e3, "gbps": 2 * rows * cols * 4 / (ms * 1e-3) / 1e9}
     for v in out.values():
         v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
     return out

@@ -94,8 +94,17 @@ typedef enum kd_element_op {
     KD_OP_GELU_TANH_BACKWARD = 65
 } kd_element_op;
 
-/* `enum class ReduceOp { Sum, Max, Min }` (reference device_kernels.h:54). */
-typedef enum kd_reduce_op { KD_REDUCE_SUM = 0, KD_REDUCE_MAX = 1, KD_REDUCE_MIN = 2 } kd_reduce_op;
+/* `enum class ReduceOp { Sum, Max, Min }` (reference device_kernels.h:54), plus three
+ * extensions for reductions that kael computes on the host today (src/ops/reduce.cpp:362-369
+ * `prod`, :442-469 `all` / `any`); they use the same contiguous-chunk contract. */
+typedef enum kd_reduce_op {
+    KD_REDUCE_SUM = 0,
+    KD_REDUCE_MAX = 1,
+    KD_REDUCE_MIN = 2,
+    KD_REDUCE_PROD = 16, /* f32/f64: double accumulation, stores In; i64/bool: wrapping int64 */
+    KD_REDUCE_ALL = 17,  /* bool: every element nonzero (NaN counts as nonzero); empty -> 1 */
+    KD_REDUCE_ANY = 18   /* bool: some element nonzero; empty -> 0 */
+} kd_reduce_op;
 
 /* Mirror of `struct ElementParameters` (reference device_kernels.h:57-68): integer
  * arguments travel apart from real ones so that every int64 survives. */
@@ -184,6 +193,20 @@ int kd_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout*
  * (reference src/cuda/kernels.inl:426-445). Max/Min of an empty chunk is an error. */
 int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
               int64_t chunk_size, int64_t output_count);
+
+/* Replaces the host round trip of reference src/ops/reduce.cpp:399-421 `argmax` / `argmin`
+ * (`on_host` + `arg_extreme`, :256-268, `best_position`, :236-254): results[r] = the index
+ * in [0, chunk_size) of the first largest (largest != 0) or first smallest element of
+ * data[r*chunk_size .. (r+1)*chunk_size), where the first NaN, if any, wins. An empty chunk
+ * is an error (plan_nonempty_reduction). */
+int kd_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
+                  int64_t output_count);
+
+/* Replaces the host round trip of reference src/ops/sequence.cpp:95-117 `cumsum` along a
+ * contiguous last dim: out[r][i] = in[r][0] + ... + in[r][i] for `rows` rows of `size`
+ * elements. f32/f64 store In (sums accumulated in double here, sequentially in In by the
+ * reference: equal within rounding); i64/bool store wrapping int64 (bit-exact). */
+int kd_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);
 
 /* reference device_kernels.h:111-112 `matmul(DType, const std::byte* a, const std::byte* b,
  * std::byte* out, const MatmulSizes&)`: out[b] = a[b] . b[b] for contiguous row-major

@@ -13,6 +13,11 @@
 //   split  few long rows: each row is cut into S segments reduced by separate workgroups into
 //          a persistent workspace, then combined in a fixed order by a second launch.
 // Every path reduces in an order fixed by (chunk, rows), so results are deterministic.
+//
+// The same machinery serves reductions kael runs on the host today: prod (double / wrapping
+// int64 accumulation, src/ops/reduce.cpp:202-219,362-369), all / any (:285-295,442-469) and
+// argmax / argmin (first extreme, first NaN wins: :236-268,399-421), plus cumsum
+// (src/ops/sequence.cpp:95-117) as a segmented scan.
 #include <algorithm>
 #include <climits>
 #include <cfloat>
@@ -32,12 +37,16 @@ template <typename In> struct SumAcc {
 };
 
 template <int Op, typename In> struct Combiner {
-    using Acc = std::conditional_t<Op == KD_REDUCE_SUM, typename SumAcc<In>::type, In>;
-    using Out = std::conditional_t<Op == KD_REDUCE_SUM,
-                                   std::conditional_t<std::is_floating_point_v<In>, In, int64_t>, In>;
+    static constexpr bool kArith = Op == KD_REDUCE_SUM || Op == KD_REDUCE_PROD;
+    static constexpr bool kLogical = Op == KD_REDUCE_ALL || Op == KD_REDUCE_ANY;
+    using Acc = std::conditional_t<kArith, typename SumAcc<In>::type, std::conditional_t<kLogical, uint8_t, In>>;
+    using Out = std::conditional_t<kArith, std::conditional_t<std::is_floating_point_v<In>, In, int64_t>,
+                                   std::conditional_t<kLogical, uint8_t, In>>;
     __device__ __forceinline__ static Acc identity() {
-        if constexpr (Op == KD_REDUCE_SUM) {
+        if constexpr (Op == KD_REDUCE_SUM || Op == KD_REDUCE_ANY) {
             return Acc(0);
+        } else if constexpr (Op == KD_REDUCE_PROD || Op == KD_REDUCE_ALL) {
+            return Acc(1);
         } else if constexpr (std::is_floating_point_v<In>) {
             return Op == KD_REDUCE_MAX ? static_cast<In>(-INFINITY) : static_cast<In>(INFINITY);
         } else if constexpr (std::is_same_v<In, int64_t>) {
@@ -46,17 +55,62 @@ template <int Op, typename In> struct Combiner {
             return Op == KD_REDUCE_MAX ? uint8_t{0} : uint8_t{255};
         }
     }
-    __device__ __forceinline__ static Acc load(In v) { return static_cast<Acc>(v); }
+    // `index` (the element's position in its chunk) matters only to ArgCombiner.
+    __device__ __forceinline__ static Acc load(In v, int64_t) {
+        if constexpr (kLogical) return v != In(0) ? uint8_t{1} : uint8_t{0};
+        else return static_cast<Acc>(v);
+    }
     __device__ __forceinline__ static Acc combine(Acc a, Acc b) {
         if constexpr (Op == KD_REDUCE_SUM) {
             if constexpr (std::is_same_v<Acc, int64_t>) return wrap_add(a, b);
             else return a + b;
+        } else if constexpr (Op == KD_REDUCE_PROD) {
+            if constexpr (std::is_same_v<Acc, int64_t>) return wrap_mul(a, b);
+            else return a * b;
+        } else if constexpr (Op == KD_REDUCE_ALL) {
+            return a & b;
+        } else if constexpr (Op == KD_REDUCE_ANY) {
+            return a | b;
         } else if constexpr (Op == KD_REDUCE_MAX) {
             return max_na(a, b);
         } else {
             return min_na(a, b);
         }
     }
+    __device__ __forceinline__ static Out finish(Acc a) { return static_cast<Out>(a); }
+};
+
+// (value, position) of the first extreme of a chunk: the first NaN wins, then the larger
+// (Largest) or smaller value, then the smaller position - the rule of reference
+// best_position, which is order independent, so every reduction tree gives the same index.
+template <typename In> struct ArgAcc {
+    In v;
+    int64_t i;
+};
+
+template <bool Largest, typename In> struct ArgCombiner {
+    using Acc = ArgAcc<In>;
+    using Out = int64_t;
+    __device__ __forceinline__ static Acc identity() {
+        if constexpr (std::is_floating_point_v<In>) {
+            return Acc{static_cast<In>(Largest ? -INFINITY : INFINITY), INT64_MAX};
+        } else if constexpr (std::is_same_v<In, int64_t>) {
+            return Acc{Largest ? INT64_MIN : INT64_MAX, INT64_MAX};
+        } else {
+            return Acc{static_cast<In>(Largest ? 0 : 255), INT64_MAX};
+        }
+    }
+    __device__ __forceinline__ static Acc load(In v, int64_t index) { return Acc{v, index}; }
+    __device__ __forceinline__ static Acc combine(Acc a, Acc b) {
+        if constexpr (std::is_floating_point_v<In>) {
+            const bool an = a.v != a.v, bn = b.v != b.v;
+            if (an || bn) return (an && (!bn || a.i < b.i)) ? a : b;
+        }
+        if (Largest ? a.v > b.v : a.v < b.v) return a;
+        if (Largest ? b.v > a.v : b.v < a.v) return b;
+        return a.i < b.i ? a : b;
+    }
+    __device__ __forceinline__ static Out finish(Acc a) { return a.i; }
 };
 
 template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
@@ -65,6 +119,10 @@ template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
     } else {
         return __shfl_xor(v, mask, 64);
     }
+}
+
+template <typename In> __device__ __forceinline__ ArgAcc<In> shfl_xor(ArgAcc<In> v, int mask) {
+    return ArgAcc<In>{shfl_xor(v.v, mask), __shfl_xor(v.i, mask, 64)};
 }
 
 // Reduces within aligned groups of `G` lanes (G a power of two <= 64).
@@ -119,7 +177,7 @@ __device__ __forceinline__ typename C::Acc block_range(const In* data, int64_t b
     const int64_t misalign = (reinterpret_cast<uintptr_t>(data + begin) % 16) / sizeof(In);
     if (misalign != 0) {
         const int64_t head_end = std::min<int64_t>(end, begin + (V - misalign));
-        for (int64_t j = begin + threadIdx.x; j < head_end; j += kBlock) acc = C::combine(acc, C::load(data[j]));
+        for (int64_t j = begin + threadIdx.x; j < head_end; j += kBlock) acc = C::combine(acc, C::load(data[j], j));
         i = head_end;
     }
     const int64_t vectors = (end - i) / V;
@@ -133,14 +191,14 @@ __device__ __forceinline__ typename C::Acc block_range(const In* data, int64_t b
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x[u].v[e]));
+            for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x[u].v[e], i + (k + u * kBlock) * V + e));
     }
     for (; k < vectors; k += kBlock) {
         const Vec16<In> x = nt_load(vp + k);
 #pragma unroll
-        for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x.v[e]));
+        for (int e = 0; e < V; ++e) acc = C::combine(acc, C::load(x.v[e], i + k * V + e));
     }
-    for (int64_t j = i + vectors * V + threadIdx.x; j < end; j += kBlock) acc = C::combine(acc, C::load(data[j]));
+    for (int64_t j = i + vectors * V + threadIdx.x; j < end; j += kBlock) acc = C::combine(acc, C::load(data[j], j));
     return block_reduce<C>(acc);
 }
 
@@ -149,7 +207,7 @@ __global__ __launch_bounds__(kBlock) void block_kernel(typename C::Out* results,
                                                        int64_t rows) {
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const typename C::Acc v = block_range<C, In>(data + r * chunk, 0, chunk);
-        if (threadIdx.x == 0) results[r] = static_cast<typename C::Out>(v);
+        if (threadIdx.x == 0) results[r] = C::finish(v);
     }
 }
 
@@ -165,10 +223,10 @@ __global__ __launch_bounds__(kBlock) void group_kernel(typename C::Out* results,
         typename C::Acc acc = C::identity();
         if (r < rows) {
             const In* row = data + r * chunk;
-            for (int64_t j = lane; j < chunk; j += G) acc = C::combine(acc, C::load(row[j]));
+            for (int64_t j = lane; j < chunk; j += G) acc = C::combine(acc, C::load(row[j], j));
         }
         acc = group_reduce<C, G>(acc);
-        if (lane == 0 && r < rows) results[r] = static_cast<typename C::Out>(acc);
+        if (lane == 0 && r < rows) results[r] = C::finish(acc);
     }
 }
 
@@ -191,11 +249,157 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(typename C::Out* result
     typename C::Acc acc = C::identity();
     for (int64_t s = threadIdx.x; s < segments; s += kBlock) acc = C::combine(acc, partial[r * segments + s]);
     acc = block_reduce<C>(acc);
-    if (threadIdx.x == 0) results[r] = static_cast<typename C::Out>(acc);
+    if (threadIdx.x == 0) results[r] = C::finish(acc);
 }
 
-template <int Op, typename In> int reduce_typed(void* results, const void* data_v, int64_t chunk, int64_t rows) {
-    using C = Combiner<Op, In>;
+// ---- cumsum ------------------------------------------------------------------------------------
+
+constexpr int kScanPer = 8;  // consecutive elements scanned in registers by one lane
+
+template <typename Acc> __device__ __forceinline__ Acc scan_add(Acc a, Acc b) {
+    if constexpr (std::is_same_v<Acc, int64_t>) return wrap_add(a, b);
+    else return a + b;
+}
+
+// Exclusive scan of one value per lane across the workgroup (waves by shuffles, then the wave
+// totals through LDS); `total` receives the workgroup sum.
+template <typename Acc> __device__ __forceinline__ Acc block_exclusive_scan(Acc v, Acc& total) {
+    __shared__ Acc wave_sum[kBlock / 64];
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    Acc x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {
+        const Acc y = __shfl_up(x, d, 64);
+        if (lane >= d) x = scan_add(x, y);
+    }
+    Acc excl = __shfl_up(x, 1, 64);
+    if (lane == 0) excl = Acc(0);
+    if (lane == 63) wave_sum[wave] = x;
+    __syncthreads();
+    Acc before = Acc(0);
+    total = Acc(0);
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) {
+        if (w < wave) before = scan_add(before, wave_sum[w]);
+        total = scan_add(total, wave_sum[w]);
+    }
+    __syncthreads();  // wave_sum is reused by the next tile
+    return scan_add(before, excl);
+}
+
+// Workgroup (s, r) scans segment s of row r (all of it when segments == 1), starting from the
+// sum of the row's earlier segments (their totals come from split_kernel). Tiles of
+// kBlock * kScanPer elements: lane t takes kScanPer consecutive elements, scans them in
+// registers, adds the exclusive scan of the lane totals and the running carry.
+// Vec: every row starts 16-byte aligned for In and Out and segments are whole tiles, so a lane
+// moves its kScanPer elements with 16-byte loads and stores (4x the scalar path's rate).
+template <typename T> struct alignas(16) Group8 {
+    T v[kScanPer];
+};
+
+template <typename In, typename Out, typename Acc, bool Vec>
+__global__ __launch_bounds__(kBlock) void scan_kernel(Out* out, const In* data, int64_t size, int64_t rows,
+                                                      const Acc* seg_totals, int64_t segments, int64_t segment) {
+    __shared__ Acc carry_in;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const int64_t s = blockIdx.x;
+        const int64_t begin = s * segment;
+        const int64_t end = std::min<int64_t>(size, begin + segment);
+        const In* row = data + r * size;
+        Out* orow = out + r * size;
+        if (segments > 1) {
+            Acc c = Acc(0);
+            for (int64_t k = threadIdx.x; k < s; k += kBlock) c = scan_add(c, seg_totals[r * segments + k]);
+            c = block_reduce<Combiner<KD_REDUCE_SUM, In>>(c);
+            if (threadIdx.x == 0) carry_in = c;
+        } else if (threadIdx.x == 0) {
+            carry_in = Acc(0);
+        }
+        __syncthreads();
+        Acc carry = carry_in;
+        for (int64_t base = begin; base < end; base += int64_t{kBlock} * kScanPer) {
+            const int64_t first = base + static_cast<int64_t>(threadIdx.x) * kScanPer;
+            const bool whole = Vec && first + kScanPer <= end;
+            Acc vals[kScanPer];
+            Acc run = Acc(0);
+            if (whole) {
+                const Group8<In> g = *reinterpret_cast<const Group8<In>*>(row + first);
+#pragma unroll
+                for (int e = 0; e < kScanPer; ++e) {
+                    run = scan_add(run, static_cast<Acc>(g.v[e]));
+                    vals[e] = run;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < kScanPer; ++e) {
+                    const int64_t j = first + e;
+                    run = scan_add(run, j < end ? static_cast<Acc>(row[j]) : Acc(0));
+                    vals[e] = run;
+                }
+            }
+            Acc total;
+            const Acc offset = scan_add(carry, block_exclusive_scan(run, total));
+            if (whole) {
+                Group8<Out> g;
+#pragma unroll
+                for (int e = 0; e < kScanPer; ++e) g.v[e] = static_cast<Out>(scan_add(offset, vals[e]));
+                *reinterpret_cast<Group8<Out>*>(orow + first) = g;
+            } else {
+#pragma unroll
+                for (int e = 0; e < kScanPer; ++e) {
+                    const int64_t j = first + e;
+                    if (j < end) orow[j] = static_cast<Out>(scan_add(offset, vals[e]));
+                }
+            }
+            carry = scan_add(carry, total);
+        }
+        __syncthreads();  // carry_in is rewritten for the next row
+    }
+}
+
+template <typename In> int cumsum_typed(void* out_v, const void* data_v, int64_t size, int64_t rows) {
+    using Acc = typename SumAcc<In>::type;
+    using Out = std::conditional_t<std::is_floating_point_v<In>, In, int64_t>;
+    Out* out = static_cast<Out*>(out_v);
+    const In* data = static_cast<const In*>(data_v);
+    const int cus = compute_units();
+    constexpr int64_t kTile = int64_t{kBlock} * kScanPer;
+    // 16-byte groups of kScanPer elements: aligned rows whose length is a whole number of groups.
+    const bool vec = sizeof(In) * kScanPer % 16 == 0 && reinterpret_cast<uintptr_t>(data) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 16 == 0 && size % kScanPer == 0;
+    const auto launch = [&](dim3 grid, const Acc* totals, int64_t segments, int64_t segment) {
+        if (vec)
+            hipLaunchKernelGGL((scan_kernel<In, Out, Acc, true>), grid, dim3(kBlock), 0, stream(), out, data, size, rows,
+                               totals, segments, segment);
+        else
+            hipLaunchKernelGGL((scan_kernel<In, Out, Acc, false>), grid, dim3(kBlock), 0, stream(), out, data, size,
+                               rows, totals, segments, segment);
+    };
+    if (rows >= 2 * cus || size <= 16 * kTile) {
+        launch(dim3(1, static_cast<uint32_t>(std::min<int64_t>(rows, 65535))), nullptr, 1, size);
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    // Few long rows: segment totals first (the sum reduction's split kernel), then every segment
+    // scans from the total of the segments before it.
+    int64_t segments = std::max<int64_t>(1, (int64_t{cus} * 4 + rows - 1) / rows);
+    int64_t segment = (size + segments - 1) / segments;
+    segment = (std::max<int64_t>(segment, 4 * kTile) + kTile - 1) / kTile * kTile;
+    segments = (size + segment - 1) / segment;
+    if (rows > 65535) return fail(KD_E_INVALID, "kd_cumsum: too many rows for the split path");
+    void* ws = nullptr;
+    if (int rc = workspace(&ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
+    const dim3 grid(static_cast<uint32_t>(segments), static_cast<uint32_t>(rows));
+    hipLaunchKernelGGL((split_kernel<Combiner<KD_REDUCE_SUM, In>, In>), grid, dim3(kBlock), 0, stream(),
+                       static_cast<Acc*>(ws), data, size, segments, segment);
+    KD_LAUNCH_CHECK();
+    launch(grid, static_cast<const Acc*>(ws), segments, segment);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <typename C, typename In> int reduce_with(void* results, const void* data_v, int64_t chunk, int64_t rows) {
     using Out = typename C::Out;
     using Acc = typename C::Acc;
     Out* out = static_cast<Out*>(results);
@@ -247,12 +451,22 @@ template <int Op, typename In> int reduce_typed(void* results, const void* data_
 
 template <int Op> int reduce_dtype(int in, void* results, const void* data, int64_t chunk, int64_t rows) {
     switch (in) {
-    case KD_F32: return reduce_typed<Op, float>(results, data, chunk, rows);
-    case KD_F64: return reduce_typed<Op, double>(results, data, chunk, rows);
-    case KD_I64: return reduce_typed<Op, int64_t>(results, data, chunk, rows);
-    case KD_BOOL: return reduce_typed<Op, uint8_t>(results, data, chunk, rows);
+    case KD_F32: return reduce_with<Combiner<Op, float>, float>(results, data, chunk, rows);
+    case KD_F64: return reduce_with<Combiner<Op, double>, double>(results, data, chunk, rows);
+    case KD_I64: return reduce_with<Combiner<Op, int64_t>, int64_t>(results, data, chunk, rows);
+    case KD_BOOL: return reduce_with<Combiner<Op, uint8_t>, uint8_t>(results, data, chunk, rows);
     }
     return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
+}
+
+template <bool Largest> int arg_dtype(int in, int64_t* results, const void* data, int64_t chunk, int64_t rows) {
+    switch (in) {
+    case KD_F32: return reduce_with<ArgCombiner<Largest, float>, float>(results, data, chunk, rows);
+    case KD_F64: return reduce_with<ArgCombiner<Largest, double>, double>(results, data, chunk, rows);
+    case KD_I64: return reduce_with<ArgCombiner<Largest, int64_t>, int64_t>(results, data, chunk, rows);
+    case KD_BOOL: return reduce_with<ArgCombiner<Largest, uint8_t>, uint8_t>(results, data, chunk, rows);
+    }
+    return fail(KD_E_INVALID, "kd_arg_reduce: unknown dtype");
 }
 
 } // namespace
@@ -267,12 +481,40 @@ extern "C" int kd_reduce(int op, int out_dtype, int in_dtype, void* results, con
     if (chunk_size < 0 || output_count < 0) return fail(KD_E_INVALID, "kd_reduce: negative size");
     if (dtype_size(in_dtype) == 0) return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
     if (output_count == 0) return KD_OK;
-    if (chunk_size == 0 && op != KD_REDUCE_SUM) return fail(KD_E_INVALID, "kd_reduce: max/min of an empty chunk");
+    if (chunk_size == 0 && (op == KD_REDUCE_MAX || op == KD_REDUCE_MIN))
+        return fail(KD_E_INVALID, "kd_reduce: max/min of an empty chunk");
     if (int rc = ensure_device()) return rc;
     switch (op) {
     case KD_REDUCE_SUM: return reduce_dtype<KD_REDUCE_SUM>(in_dtype, results, data, chunk_size, output_count);
     case KD_REDUCE_MAX: return reduce_dtype<KD_REDUCE_MAX>(in_dtype, results, data, chunk_size, output_count);
     case KD_REDUCE_MIN: return reduce_dtype<KD_REDUCE_MIN>(in_dtype, results, data, chunk_size, output_count);
+    case KD_REDUCE_PROD: return reduce_dtype<KD_REDUCE_PROD>(in_dtype, results, data, chunk_size, output_count);
+    case KD_REDUCE_ALL: return reduce_dtype<KD_REDUCE_ALL>(in_dtype, results, data, chunk_size, output_count);
+    case KD_REDUCE_ANY: return reduce_dtype<KD_REDUCE_ANY>(in_dtype, results, data, chunk_size, output_count);
     }
     return fail(KD_E_INVALID, "kd_reduce: unknown op");
+}
+
+extern "C" int kd_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
+                             int64_t output_count) {
+    if (chunk_size < 0 || output_count < 0) return fail(KD_E_INVALID, "kd_arg_reduce: negative size");
+    if (dtype_size(in_dtype) == 0) return fail(KD_E_INVALID, "kd_arg_reduce: unknown dtype");
+    if (output_count == 0) return KD_OK;
+    if (chunk_size == 0) return fail(KD_E_INVALID, "kd_arg_reduce: argmax/argmin of an empty chunk");
+    if (int rc = ensure_device()) return rc;
+    return largest ? arg_dtype<true>(in_dtype, results, data, chunk_size, output_count)
+                   : arg_dtype<false>(in_dtype, results, data, chunk_size, output_count);
+}
+
+extern "C" int kd_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows) {
+    if (size < 0 || rows < 0) return fail(KD_E_INVALID, "kd_cumsum: negative size");
+    if (size == 0 || rows == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    switch (in_dtype) {
+    case KD_F32: return cumsum_typed<float>(out, in, size, rows);
+    case KD_F64: return cumsum_typed<double>(out, in, size, rows);
+    case KD_I64: return cumsum_typed<int64_t>(out, in, size, rows);
+    case KD_BOOL: return cumsum_typed<uint8_t>(out, in, size, rows);
+    }
+    return fail(KD_E_INVALID, "kd_cumsum: unknown dtype");
 }

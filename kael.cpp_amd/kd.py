@@ -41,6 +41,7 @@ FLOATING_OPS = {OP[n] for n in ("EXP", "LOG", "LOG1P", "EXPM1", "SQRT", "RSQRT",
                                 "TANH", "SIGMOID", "GELU_EXACT", "GELU_TANH",
                                 "GELU_EXACT_BACKWARD", "GELU_TANH_BACKWARD")}
 REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
+REDUCE_PROD, REDUCE_ALL, REDUCE_ANY = 16, 17, 18  # extensions (kael computes these on the host)
 
 
 def op_inputs(op: int) -> int:
@@ -103,6 +104,8 @@ SIGNATURES = {
     "convert": (c_int, [c_int, c_int, POINTER(ElementLayout)]),
     "elementwise": (c_int, [c_int, c_int, c_int, POINTER(ElementLayout), ElementParameters]),
     "reduce": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "arg_reduce": (c_int, [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "cumsum": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
     "scatter_add": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
     "softmax_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int]),

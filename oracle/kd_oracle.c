@@ -13,6 +13,9 @@
  *   - row kernels            src/ops/nn.cpp:52-129, 214-240; src/nn/layers.cpp:60-68
  *   - GELU slopes            src/autograd/functions_math.cpp:35-46, 221-231
  *   - layout planning        src/iterator.cpp:12-63, 112-132, 152-172
+ *   - host reductions        src/ops/reduce.cpp:24-83 (8 lanes, 16384-element blocks, pairwise
+ *                            merge), :202-219 prod, :236-268 argmax/argmin, :285-295 all/any;
+ *                            src/ops/sequence.cpp:95-117 cumsum (sequential, in the output dtype)
  *
  * Deliberate choices where the reference is undefined: integer division by zero yields 0 and
  * INT64_MIN / -1 yields INT64_MIN (the reference host would trap). Floating ops on integer
@@ -506,9 +509,183 @@ static int64_t reduce_range_i(int op, int in_dtype, const char* data, int64_t be
     return best;
 }
 
+/* ---- reductions kael runs on the host: prod, all / any, argmax / argmin, cumsum --------- */
+
+#define CPU_BLOCK 16384 /* kReductionBlock, reduce.cpp:24 */
+#define CPU_LANES 8     /* kLanes, reduce.cpp:25 */
+
+/* fold_lanes (reduce.cpp:35-56) of the product over [first, last): double for floats. */
+static double prod_lanes_f(int in_dtype, const char* row, int64_t first, int64_t last) {
+    double lanes[CPU_LANES];
+    for (int l = 0; l < CPU_LANES; ++l) lanes[l] = 1.0;
+    int64_t i = first;
+    for (; i + CPU_LANES <= last; i += CPU_LANES)
+        for (int l = 0; l < CPU_LANES; ++l) lanes[l] = lanes[l] * read_as_double(in_dtype, row + (i + l) * dtype_size(in_dtype));
+    double total = 1.0;
+    for (int l = 0; l < CPU_LANES; ++l) total = total * lanes[l];
+    for (; i < last; ++i) total = total * read_as_double(in_dtype, row + i * dtype_size(in_dtype));
+    return total;
+}
+
+static int64_t read_as_i64(int in_dtype, const char* p) {
+    if (in_dtype == KD_I64) {
+        int64_t v;
+        memcpy(&v, p, 8);
+        return v;
+    }
+    return (int64_t)*(const u8*)p;
+}
+
+/* The same for integers: wrapping int64 products (element_functions.h:66-73). */
+static int64_t prod_lanes_i(int in_dtype, const char* row, int64_t first, int64_t last) {
+    int64_t lanes[CPU_LANES];
+    for (int l = 0; l < CPU_LANES; ++l) lanes[l] = 1;
+    int64_t i = first;
+    for (; i + CPU_LANES <= last; i += CPU_LANES)
+        for (int l = 0; l < CPU_LANES; ++l) lanes[l] = wmul(lanes[l], read_as_i64(in_dtype, row + (i + l) * dtype_size(in_dtype)));
+    int64_t total = 1;
+    for (int l = 0; l < CPU_LANES; ++l) total = wmul(total, lanes[l]);
+    for (; i < last; ++i) total = wmul(total, read_as_i64(in_dtype, row + i * dtype_size(in_dtype)));
+    return total;
+}
+
+/* reduce_in_blocks (reduce.cpp:58-83) of the product of one chunk. */
+static int prod_chunk(int in_dtype, const char* row, int64_t size, double* fv, int64_t* iv) {
+    const int floating = in_dtype == KD_F32 || in_dtype == KD_F64;
+    if (size <= CPU_BLOCK) {
+        if (floating) *fv = 1.0 * prod_lanes_f(in_dtype, row, 0, size);
+        else *iv = wmul(1, prod_lanes_i(in_dtype, row, 0, size));
+        return KD_OK;
+    }
+    const int64_t blocks = (size + CPU_BLOCK - 1) / CPU_BLOCK;
+    double* fp = (double*)malloc((size_t)blocks * sizeof(double));
+    int64_t* ip = (int64_t*)malloc((size_t)blocks * sizeof(int64_t));
+    if (!fp || !ip) {
+        free(fp);
+        free(ip);
+        return fail("prod: out of memory");
+    }
+    for (int64_t b = 0; b < blocks; ++b) {
+        const int64_t begin = b * CPU_BLOCK;
+        const int64_t end = begin + CPU_BLOCK < size ? begin + CPU_BLOCK : size;
+        if (floating) fp[b] = prod_lanes_f(in_dtype, row, begin, end);
+        else ip[b] = prod_lanes_i(in_dtype, row, begin, end);
+    }
+    for (int64_t width = blocks; width > 1; width = (width + 1) / 2) {
+        for (int64_t i = 0; i < width / 2; ++i) {
+            if (floating) fp[i] = fp[2 * i] * fp[2 * i + 1];
+            else ip[i] = wmul(ip[2 * i], ip[2 * i + 1]);
+        }
+        if (width % 2 == 1) {
+            if (floating) fp[width / 2] = fp[width - 1];
+            else ip[width / 2] = ip[width - 1];
+        }
+    }
+    if (floating) *fv = 1.0 * fp[0];
+    else *iv = wmul(1, ip[0]);
+    free(fp);
+    free(ip);
+    return KD_OK;
+}
+
+static int host_reduce(int op, int in_dtype, void* results, const void* data, int64_t chunk, int64_t rows) {
+    const int64_t esize = dtype_size(in_dtype);
+    for (int64_t r = 0; r < rows; ++r) {
+        const char* row = (const char*)data + r * chunk * esize;
+        if (op == KD_REDUCE_PROD) {
+            double fv = 0;
+            int64_t iv = 0;
+            if (prod_chunk(in_dtype, row, chunk, &fv, &iv) != KD_OK) return KD_E_INVALID;
+            if (in_dtype == KD_F32) ((float*)results)[r] = (float)fv;
+            else if (in_dtype == KD_F64) ((double*)results)[r] = fv;
+            else ((int64_t*)results)[r] = iv;
+        } else {
+            /* all / any: the first zero (all) or nonzero (any) decides; NaN != 0 (reduce.cpp:295) */
+            u8 v = op == KD_REDUCE_ALL ? 1 : 0;
+            for (int64_t i = 0; i < chunk; ++i) {
+                const int nonzero = read_as_double(in_dtype, row + i * esize) != 0.0 ||
+                                    (in_dtype == KD_I64 && read_as_i64(in_dtype, row + i * esize) != 0);
+                if (op == KD_REDUCE_ALL && !nonzero) {
+                    v = 0;
+                    break;
+                }
+                if (op == KD_REDUCE_ANY && nonzero) {
+                    v = 1;
+                    break;
+                }
+            }
+            ((u8*)results)[r] = v;
+        }
+    }
+    return KD_OK;
+}
+
+/* best_position (reduce.cpp:236-254) with std::greater (argmax) or std::less (argmin). */
+int oracle_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk,
+                      int64_t rows) {
+    if (dtype_size(in_dtype) == 0) return fail("arg_reduce: unknown dtype");
+    if (chunk < 0 || rows < 0) return fail("arg_reduce: negative size");
+    if (rows == 0) return KD_OK;
+    if (chunk == 0) return fail("arg_reduce: argmax/argmin of an empty chunk");
+    const int64_t esize = dtype_size(in_dtype);
+    const int floating = in_dtype == KD_F32 || in_dtype == KD_F64;
+    for (int64_t r = 0; r < rows; ++r) {
+        const char* row = (const char*)data + r * chunk * esize;
+        int64_t best = 0;
+        for (int64_t i = 1; i < chunk; ++i) {
+            if (floating) {
+                const double b = read_as_double(in_dtype, row + best * esize);
+                const double c = read_as_double(in_dtype, row + i * esize);
+                if (b != b) break;
+                if (c != c) {
+                    best = i;
+                    continue;
+                }
+                if (largest ? c > b : c < b) best = i;
+            } else {
+                const int64_t b = read_as_i64(in_dtype, row + best * esize);
+                const int64_t c = read_as_i64(in_dtype, row + i * esize);
+                if (largest ? c > b : c < b) best = i;
+            }
+        }
+        results[r] = best;
+    }
+    return KD_OK;
+}
+
+/* cumsum (sequence.cpp:95-117): the input converted to the output dtype (In for floats, I64
+ * otherwise), then results[i] = results[i-1] + data[i] in that dtype (wrapping for I64). */
+int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows) {
+    if (dtype_size(in_dtype) == 0) return fail("cumsum: unknown dtype");
+    if (size < 0 || rows < 0) return fail("cumsum: negative size");
+    const int64_t esize = dtype_size(in_dtype);
+    for (int64_t r = 0; r < rows; ++r) {
+        const char* row = (const char*)in + r * size * esize;
+        if (in_dtype == KD_F32) {
+            float* o = (float*)out + r * size;
+            for (int64_t i = 0; i < size; ++i) o[i] = i == 0 ? ((const float*)row)[0] : o[i - 1] + ((const float*)row)[i];
+        } else if (in_dtype == KD_F64) {
+            double* o = (double*)out + r * size;
+            for (int64_t i = 0; i < size; ++i) o[i] = i == 0 ? ((const double*)row)[0] : o[i - 1] + ((const double*)row)[i];
+        } else {
+            int64_t* o = (int64_t*)out + r * size;
+            for (int64_t i = 0; i < size; ++i) {
+                const int64_t v = read_as_i64(in_dtype, row + i * esize);
+                o[i] = i == 0 ? v : wadd(o[i - 1], v);
+            }
+        }
+    }
+    return KD_OK;
+}
+
 int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
                   int64_t chunk, int64_t rows) {
     (void)out_dtype;
+    if (op == KD_REDUCE_PROD || op == KD_REDUCE_ALL || op == KD_REDUCE_ANY) {
+        if (dtype_size(in_dtype) == 0) return fail("reduce: unknown dtype");
+        if (chunk < 0 || rows < 0) return fail("reduce: negative size");
+        return host_reduce(op, in_dtype, results, data, chunk, rows);
+    }
     if (op < KD_REDUCE_SUM || op > KD_REDUCE_MIN) return fail("reduce: unknown op");
     if (dtype_size(in_dtype) == 0) return fail("reduce: unknown dtype");
     if (rows == 0) return KD_OK;

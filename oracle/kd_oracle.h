@@ -24,6 +24,9 @@ int oracle_elementwise(int op, int out_dtype, int in_dtype, const kd_element_lay
                        kd_element_parameters parameters);
 int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
                   int64_t chunk_size, int64_t output_count);
+int oracle_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
+                      int64_t output_count);
+int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);
 /* exact == 0: the reference device order (MatmulTiles, sequential k in T);
  * exact != 0: f32 inputs accumulated in double (error-analysis reference). */
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,

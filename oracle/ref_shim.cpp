@@ -17,6 +17,7 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -193,6 +194,23 @@ int ref_softmax(int dtype, void* out, const void* in, int64_t rows, int64_t cols
     return guarded([&] {
         const kael::Tensor x = host_tensor(in, {rows, cols}, to_dtype(dtype));
         copy_out(log ? kael::log_softmax(x, -1) : kael::softmax(x, -1), out);
+    });
+}
+
+// kael's CPU reductions of a [rows, cols] tensor along dim 1: what = 0 prod, 1 all, 2 any,
+// 3 argmax, 4 argmin, 5 cumsum (src/ops/reduce.cpp, src/ops/sequence.cpp).
+int ref_host_reduce(int what, int dtype, void* out, const void* in, int64_t rows, int64_t cols) {
+    return guarded([&] {
+        const kael::Tensor x = host_tensor(in, {rows, cols}, to_dtype(dtype));
+        switch (what) {
+        case 0: copy_out(kael::prod(x, {1}), out); break;
+        case 1: copy_out(kael::all(x, {1}), out); break;
+        case 2: copy_out(kael::any(x, {1}), out); break;
+        case 3: copy_out(kael::argmax(x, 1), out); break;
+        case 4: copy_out(kael::argmin(x, 1), out); break;
+        case 5: copy_out(kael::cumsum(x, 1), out); break;
+        default: throw std::runtime_error("ref_host_reduce: unknown reduction");
+        }
     });
 }
 

@@ -59,6 +59,7 @@ REF_SIGS = {
     "dev_convert": (c_int, [c_int, c_int, POINTER(kd.ElementLayout)]),
     "dev_elementwise": (c_int, [c_int, c_int, c_int, POINTER(kd.ElementLayout), kd.ElementParameters]),
     "dev_reduce": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "host_reduce": (c_int, [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "dev_matmul": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.MatmulSizes)]),
     "dev_gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.IndexLayout)]),
     "dev_scatter_add": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.IndexLayout)]),
