@@ -251,6 +251,20 @@ class Gpt:
         self.b.check(self.b.lib.kd_gpt_load_parameter(self.handle, name.encode(), a.ctypes.data_as(c_void_p), a.size),
                      f"kd_gpt_load_parameter({name})")
 
+    def load_gpt2_safetensors(self, path) -> None:
+        """Loads a Hugging Face GPT-2 checkpoint (`model.safetensors`), as kael's
+        load_gpt2_weights does (reference src/nn/transformer.cpp:297-308): names translated,
+        Conv1D weights transposed, entries kael's GPT does not have ignored, a missing one an
+        error. The file is memory-mapped; f16 tensors are widened to f32."""
+        from safetensors import safe_open
+
+        c = self.config
+        expected = dict(gpt2_parameter_shapes(c.vocab_size, c.max_positions, c.layers, c.dimension))
+        with safe_open(str(path), framework="numpy") as f:
+            state = gpt2_state_from_hf({k: f.get_tensor(k) for k in f.keys()}, expected)
+        for name, array in state.items():
+            self.load(name, array)
+
     def prefill(self, prompt) -> None:
         p = np.ascontiguousarray(prompt, dtype=np.int64)
         self.b.check(self.b.lib.kd_gpt_prefill(self.handle, p.ctypes.data_as(c_void_p), p.size), "kd_gpt_prefill")
@@ -295,6 +309,53 @@ def gpt2_parameter_shapes(vocab_size=50257, max_positions=1024, layers=12, dimen
                    (b + "mlp.fc1.bias", (4 * d,)), (b + "mlp.fc2.weight", (d, 4 * d)), (b + "mlp.fc2.bias", (d,))]
     shapes += [("ln_final.weight", (d,)), ("ln_final.bias", (d,))]
     return shapes
+
+
+def gpt2_name(stored: str) -> str:
+    """kael's name for a Hugging Face GPT-2 tensor (reference translated_gpt2_name,
+    src/nn/transformer.cpp:54-81)."""
+    name = stored[len("transformer."):] if stored.startswith("transformer.") else stored
+    if name.startswith("wte."):
+        return "token_embedding." + name[len("wte."):]
+    if name.startswith("wpe."):
+        return "position_embedding." + name[len("wpe."):]
+    if name.startswith("ln_f."):
+        return "ln_final." + name[len("ln_f."):]
+    if name.startswith("h."):
+        name = "blocks." + name[2:]
+        for old, new in ((".ln_1.", ".ln1."), (".ln_2.", ".ln2."), (".attn.c_attn.", ".attn.qkv."),
+                         (".attn.c_proj.", ".attn.proj."), (".mlp.c_fc.", ".mlp.fc1."), (".mlp.c_proj.", ".mlp.fc2.")):
+            name = name.replace(old, new, 1)
+    return name
+
+
+def gpt2_stored_transposed(name: str) -> bool:
+    """Conv1D weights are stored [in, out] (reference stored_transposed, transformer.cpp:83-89)."""
+    conv1d = any(part in name for part in (".attn.qkv.", ".attn.proj.", ".mlp.fc1.", ".mlp.fc2."))
+    return conv1d and name.endswith(".weight")
+
+
+def gpt2_state_from_hf(tensors: dict, expected: dict) -> dict:
+    """kael parameters (name -> f32 array of the expected shape) from Hugging Face GPT-2 tensors:
+    unknown entries are dropped, a missing or misshapen parameter raises ValueError."""
+    state = {}
+    for stored, array in tensors.items():
+        name = gpt2_name(stored)
+        if name not in expected:
+            continue
+        a = np.asarray(array)
+        if a.dtype not in (np.float32, np.float16, np.float64):
+            raise ValueError(f"GPT-2 weights: {stored} has dtype {a.dtype}, expected a float dtype")
+        if gpt2_stored_transposed(name):
+            a = a.T
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        if a.shape != tuple(expected[name]):
+            raise ValueError(f"GPT-2 weights: {stored} has shape {a.shape}, {name} needs {tuple(expected[name])}")
+        state[name] = a
+    missing = [n for n in expected if n not in state]
+    if missing:
+        raise ValueError(f"GPT-2 weights: missing {len(missing)} entries, e.g. {missing[:3]}")
+    return state
 
 
 _BACKEND: Backend | None = None

@@ -180,3 +180,41 @@ def golden_close(actual: np.ndarray, expected: np.ndarray, rtol=None, atol=None)
         return True, ""
     idx = np.argwhere(~ok)[0]
     return False, f"first mismatch at {tuple(idx)}: {a[tuple(idx)]} vs {e[tuple(idx)]} ({(~ok).sum()} bad)"
+
+
+def export_gpt_params(ref, handle):
+    """kael's GPT parameters (GPT::named_parameters() order) as (name, f32 array) pairs."""
+    n = ref.ref_gpt_param_count(handle)
+    name = ctypes.create_string_buffer(256)
+    shape = (c_int64 * 8)()
+    rank = c_int()
+    out = []
+    for i in range(n):
+        assert ref.ref_gpt_param(handle, i, name, 256, shape, ctypes.byref(rank), None) == 0
+        dims = tuple(shape[d] for d in range(rank.value))
+        data = np.empty(dims, np.float32)
+        assert ref.ref_gpt_param(handle, i, name, 256, shape, ctypes.byref(rank), data.ctypes.data_as(c_void_p)) == 0
+        out.append((name.value.decode(), data))
+    return out
+
+
+def hf_gpt2_tensors(params, prefix_blocks=True):
+    """The same weights under Hugging Face GPT-2 names and layouts (Conv1D weights [in, out]),
+    with the extra entries a checkpoint carries (the tied lm_head, attention mask buffers), as
+    in reference tests/test_transformer.cpp:294-329."""
+    own = dict(params)
+    hf = {"wte.weight": own["token_embedding.weight"], "wpe.weight": own["position_embedding.weight"],
+          "ln_f.weight": own["ln_final.weight"], "ln_f.bias": own["ln_final.bias"],
+          "lm_head.weight": own["token_embedding.weight"]}
+    layers = sum(1 for n in own if n.endswith(".ln1.weight"))
+    for i in range(layers):
+        h = ("transformer.h." if prefix_blocks else "h.") + f"{i}."
+        b = f"blocks.{i}."
+        hf[h + "ln_1.weight"], hf[h + "ln_1.bias"] = own[b + "ln1.weight"], own[b + "ln1.bias"]
+        hf[h + "ln_2.weight"], hf[h + "ln_2.bias"] = own[b + "ln2.weight"], own[b + "ln2.bias"]
+        for hname, kname in (("attn.c_attn", "attn.qkv"), ("attn.c_proj", "attn.proj"), ("mlp.c_fc", "mlp.fc1"),
+                             ("mlp.c_proj", "mlp.fc2")):
+            hf[h + hname + ".weight"] = np.ascontiguousarray(own[b + kname + ".weight"].T)
+            hf[h + hname + ".bias"] = own[b + kname + ".bias"]
+        hf[h + "attn.bias"] = np.zeros((1,), np.float32)
+    return hf

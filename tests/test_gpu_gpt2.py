@@ -19,18 +19,7 @@ pytestmark = pytest.mark.gpu
 
 
 def export_params(ref, handle):
-    n = ref.ref_gpt_param_count(handle)
-    name = ctypes.create_string_buffer(256)
-    shape = (ctypes.c_int64 * 8)()
-    rank = ctypes.c_int()
-    out = []
-    for i in range(n):
-        assert ref.ref_gpt_param(handle, i, name, 256, shape, ctypes.byref(rank), None) == 0
-        dims = tuple(shape[d] for d in range(rank.value))
-        data = np.empty(dims, np.float32)
-        assert ref.ref_gpt_param(handle, i, name, 256, shape, ctypes.byref(rank), data.ctypes.data_as(ctypes.c_void_p)) == 0
-        out.append((name.value.decode(), data))
-    return out
+    return support.export_gpt_params(ref, handle)
 
 
 def build(kdb, ref, vocab, positions, layers, heads, dim, seed):
@@ -97,6 +86,30 @@ def test_gpt2_small_teacher_forced_logits(kdb, refdev):
         seq, _ = cpu_generate(ref, h, tokens[:prompt_len], 4)
         g.prefill(tokens[:prompt_len])
         g.decode(3)
+        np.testing.assert_array_equal(g.sequence(), seq)
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
+def test_hugging_face_checkpoint_loads_into_the_engine(kdb, refdev, tmp_path):
+    """A GPT-2 checkpoint in Hugging Face layout (kael's own weights written as model.safetensors)
+    through Gpt.load_gpt2_safetensors: the engine then computes kael's logits."""
+    from safetensors.numpy import save_file
+
+    ref = refdev
+    h = ref.ref_gpt_create(11, 16, 2, 2, 8, 31, 1)
+    assert h, support.ref_error(ref)
+    try:
+        path = tmp_path / "model.safetensors"
+        save_file(support.hf_gpt2_tensors(support.export_gpt_params(ref, h)), str(path))
+        g = kd.Gpt(kdb, 11, 16, 2, 2, 8, True)
+        g.load_gpt2_safetensors(path)
+        tokens = np.random.default_rng(1).integers(0, 11, 10)
+        want = cpu_cached_logits(ref, h, tokens, 1, 11)
+        np.testing.assert_allclose(g.forward_logits(tokens), want, rtol=1e-5, atol=1e-6)
+        seq, _ = cpu_generate(ref, h, tokens[:4], 6)
+        g.prefill(tokens[:4])
+        g.decode(5)
         np.testing.assert_array_equal(g.sequence(), seq)
     finally:
         ref.ref_gpt_destroy(h)
