@@ -363,11 +363,17 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_kernel(const float* __restr
 // offsets and leading dimensions, and the loop bound in a scalar register: on 4096^3 this runs
 // ~5 % faster than the general kernel's Full path, whose 64-bit index math and argument block
 // cost issue slots around the MFMAs. Results are bitwise those of mfma_f32_kernel.
+//
+// Split K (blockIdx.z = split): workgroup (tile, batch, split) multiplies the K slice that
+// starts split_a columns into A and split_b elements into B (K is the slice length) and writes
+// its partial product split_o floats further into the output, a workspace that
+// split_sum_kernel adds up in split order.
 __global__ __launch_bounds__(kThreads) void mfma_f32_rowmajor_kernel(const float* __restrict__ a,
                                                                      const float* __restrict__ b,
                                                                      float* __restrict__ out, int M, int N, int K,
                                                                      int lda, int ldb, int ldo, int64_t batch_a,
-                                                                     int64_t batch_b, int64_t batch_o) {
+                                                                     int64_t batch_b, int64_t batch_o, int64_t split_a,
+                                                                     int64_t split_b, int64_t split_o) {
     __shared__ float As[2][kAsize];
     __shared__ float Bs[2][kBsize];
     const int tiles_m = M / kBM;
@@ -376,9 +382,9 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_rowmajor_kernel(const float
     tile_of(blockIdx.x, tiles_m, tiles_n, tm64, tn64);
     const int m0 = static_cast<int>(tm64) * kBM;
     const int n0 = static_cast<int>(tn64) * kBN;
-    a += blockIdx.y * batch_a;
-    b += blockIdx.y * batch_b;
-    out += blockIdx.y * batch_o;
+    a += blockIdx.y * batch_a + blockIdx.z * split_a;
+    b += blockIdx.y * batch_b + blockIdx.z * split_b;
+    out += blockIdx.y * batch_o + blockIdx.z * split_o;
 
     const int t = threadIdx.x;
     const int lane = t % 64;
@@ -692,10 +698,38 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
         constexpr int64_t kMax = int64_t{1} << 31;
         const bool small = p.M * p.sa.r < kMax && p.K * p.sb.r < kMax && p.M * p.so.r < kMax && p.so.c == 1;
         if (small && p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0) {
+            // Too few tiles to occupy the device (C1's 512^3 has 16): split K so that about one
+            // workgroup per CU is busy, partial products into the workspace, summed in split order.
+            const int cus = compute_units();
+            int64_t splits = 1;
+            if (tiles * p.batches * 2 <= cus && p.K >= 256 && p.M * p.N * p.batches * (cus / tiles) < kMax) {
+                splits = std::min<int64_t>(p.K / 64, (cus + tiles * p.batches - 1) / (tiles * p.batches));
+                while (splits > 1 && p.K % (splits * kBK) != 0) --splits;
+            }
+            if (splits > 1) {
+                void* ws = nullptr;
+                const int64_t per = p.M * p.N;
+                if (int rc = workspace(&ws, static_cast<size_t>(splits * p.batches * per) * sizeof(float))) return rc;
+                const int64_t kc = p.K / splits;
+                hipLaunchKernelGGL(mfma_f32_rowmajor_kernel,
+                                   dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(p.batches),
+                                        static_cast<uint32_t>(splits)),
+                                   dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws), static_cast<int>(p.M),
+                                   static_cast<int>(p.N), static_cast<int>(kc), static_cast<int>(p.sa.r),
+                                   static_cast<int>(p.sb.r), static_cast<int>(p.N), p.sa.b, p.sb.b, splits * per, kc,
+                                   kc * p.sb.r, per);
+                KD_LAUNCH_CHECK();
+                const int64_t total = p.batches * per;
+                const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{cus} * 16);
+                hipLaunchKernelGGL(split_sum_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream(),
+                                   static_cast<const float*>(ws), out, p, splits);
+                KD_LAUNCH_CHECK();
+                return KD_OK;
+            }
             hipLaunchKernelGGL(mfma_f32_rowmajor_kernel, grid, dim3(kThreads), 0, stream(), a, b, out,
                                static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
                                static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r), p.sa.b,
-                               p.sb.b, p.so.b);
+                               p.sb.b, p.so.b, int64_t{0}, int64_t{0}, int64_t{0});
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
