@@ -20,23 +20,28 @@ def test_c3_mlp_sgd_100_steps_match_cpu(kael_hip):
     lib = kael_hip
     cpu_l, gpu_l = np.zeros(100, np.float32), np.zeros(100, np.float32)
     cpu_p, gpu_p = np.zeros(101770, np.float32), np.zeros(101770, np.float32)
-    tc, tg = ctypes.c_double(), ctypes.c_double()
+    tc, tg, cold = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
     assert lib.ref_train_mlp(0, 100, cpu_l.ctypes.data_as(ctypes.c_void_p), cpu_p.ctypes.data_as(ctypes.c_void_p),
                              ctypes.byref(tc)) == 0
+    # The first device run also loads kernels and fills kael's block cache; the second (same seeds,
+    # same computation) is the one timed and checked.
+    assert lib.ref_train_mlp(1, 100, gpu_l.ctypes.data_as(ctypes.c_void_p), gpu_p.ctypes.data_as(ctypes.c_void_p),
+                             ctypes.byref(cold)) == 0
     assert lib.ref_train_mlp(1, 100, gpu_l.ctypes.data_as(ctypes.c_void_p), gpu_p.ctypes.data_as(ctypes.c_void_p),
                              ctypes.byref(tg)) == 0
     np.testing.assert_allclose(gpu_l, cpu_l, rtol=1e-4)
     np.testing.assert_allclose(gpu_p, cpu_p, rtol=1e-4, atol=1e-5)
     assert gpu_l[-1] < gpu_l[0]
     print(f"\nC3 MLP 100 SGD steps through kael: CPU {tc.value:.3f} s, MI355X {tg.value:.3f} s "
-          f"({100 / tg.value:.0f} steps/s)")
+          f"({100 / tg.value:.0f} steps/s; first run {cold.value:.3f} s)")
 
 
 def test_c4_char_gpt_adam_steps_match_cpu(kael_hip):
     lib = kael_hip
     steps = 3
     cpu_l, gpu_l = np.zeros(steps, np.float32), np.zeros(steps, np.float32)
-    tc, tg = ctypes.c_double(), ctypes.c_double()
+    tc, tg, cold = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    assert lib.ref_train_chargpt(1, steps, gpu_l.ctypes.data_as(ctypes.c_void_p), ctypes.byref(cold)) == 0
     assert lib.ref_train_chargpt(1, steps, gpu_l.ctypes.data_as(ctypes.c_void_p), ctypes.byref(tg)) == 0
     assert lib.ref_train_chargpt(0, steps, cpu_l.ctypes.data_as(ctypes.c_void_p), ctypes.byref(tc)) == 0
     np.testing.assert_allclose(gpu_l, cpu_l, rtol=1e-4)
