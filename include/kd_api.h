@@ -210,7 +210,8 @@ int kd_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t row
 
 /* reference device_kernels.h:111-112 `matmul(DType, const std::byte* a, const std::byte* b,
  * std::byte* out, const MatmulSizes&)`: out[b] = a[b] . b[b] for contiguous row-major
- * batches, overwriting out. f32 and f64 on matrix cores, i64 wrapping, bool rejected. */
+ * batches, overwriting out. f32 on the FP32 matrix cores; f64 and i64 (wrapping) on the
+ * vector ALUs; bool rejected. */
 int kd_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes);
 
 /* Extension of kd_matmul with element strides per operand, so that transposed or
