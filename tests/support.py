@@ -87,6 +87,11 @@ REF_SIGS = {
     "train_mlp": (c_int, [c_int, c_int64, c_void_p, c_void_p, POINTER(c_double)]),
     "train_chargpt": (c_int, [c_int, c_int64, c_void_p, POINTER(c_double)]),
     "gpt_generate_on": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
+    "suite_size": (c_int, []),
+    "suite_name": (c_char_p, [c_int]),
+    "suite_run": (c_int, [c_int]),
+    "suite_message": (c_char_p, []),
+    "suite_self_check": (c_int, []),
 }
 
 
@@ -100,6 +105,23 @@ def load_ref(variant: str = "ref") -> ctypes.CDLL:
 def ref_error(lib) -> str:
     m = lib.ref_last_error()
     return m.decode() if m else ""
+
+
+def suite_cases(lib) -> list[str]:
+    """Names of the device-behaviour cases in oracle/device_suite.cpp."""
+    return [lib.ref_suite_name(i).decode() for i in range(lib.ref_suite_size())]
+
+
+def run_suite_case(lib, name: str) -> None:
+    """Runs one device-behaviour case; fails or skips the calling test as the case does."""
+    import pytest
+
+    index = suite_cases(lib).index(name)
+    status = lib.ref_suite_run(index)
+    message = (lib.ref_suite_message() or b"").decode()
+    if status == 2:
+        pytest.skip(message)
+    assert status == 0, f"{name}: {message}"
 
 
 def ptr(a: np.ndarray) -> c_void_p:

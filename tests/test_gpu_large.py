@@ -1,6 +1,7 @@
-"""Element counts above 2^31 (64-bit index paths): the elementwise nd64 kernel (IS_ZERO of bool is logical not), a reduction
-whose single chunk is longer than 2^31, and argmax positions past 2^31. Bool data (1 byte per
-element) keeps each buffer near 2 GiB; results are exact.
+"""Element counts above 2^31 (64-bit index paths): the elementwise nd64 kernel (IS_ZERO
+of bool is logical not), a reduction whose single chunk is longer than 2^31, and argmax
+positions past 2^31. Bool data (1 byte per element) keeps each buffer near 2 GiB; results
+are exact.
 """
 import numpy as np
 import pytest
