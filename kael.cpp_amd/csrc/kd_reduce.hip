@@ -37,6 +37,7 @@ template <typename In> struct SumAcc {
 };
 
 template <int Op, typename In> struct Combiner {
+    static constexpr bool kDescending = false;  // lanes scan their elements in increasing position
     static constexpr bool kArith = Op == KD_REDUCE_SUM || Op == KD_REDUCE_PROD;
     static constexpr bool kLogical = Op == KD_REDUCE_ALL || Op == KD_REDUCE_ANY;
     using Acc = std::conditional_t<kArith, typename SumAcc<In>::type, std::conditional_t<kLogical, uint8_t, In>>;
@@ -91,6 +92,11 @@ template <typename In> struct ArgAcc {
 template <bool Largest, typename In> struct ArgCombiner {
     using Acc = ArgAcc<In>;
     using Out = int64_t;
+    // Each lane scans its own elements from the highest position down (block_range_down), so
+    // the element being added always lies before everything the accumulator has seen: it wins
+    // ties and every NaN replaces the accumulator, which leaves the first extreme (or first NaN)
+    // in one compare and two selects per element instead of a full combine.
+    static constexpr bool kDescending = true;
     __device__ __forceinline__ static Acc identity() {
         if constexpr (std::is_floating_point_v<In>) {
             return Acc{static_cast<In>(Largest ? -INFINITY : INFINITY), INT64_MAX};
@@ -109,6 +115,13 @@ template <bool Largest, typename In> struct ArgCombiner {
         if (Largest ? a.v > b.v : a.v < b.v) return a;
         if (Largest ? b.v > a.v : b.v < a.v) return b;
         return a.i < b.i ? a : b;
+    }
+    // `a` is the identity or holds an element at a position above `index`.
+    __device__ __forceinline__ static Acc step_down(Acc a, In x, int64_t index) {
+        bool take;
+        if constexpr (std::is_floating_point_v<In>) take = x != x || (Largest ? x >= a.v : x <= a.v);
+        else take = Largest ? x >= a.v : x <= a.v;
+        return take ? Acc{x, index} : a;
     }
     __device__ __forceinline__ static Out finish(Acc a) { return a.i; }
 };
@@ -165,10 +178,48 @@ template <typename In> __device__ __forceinline__ Vec16<In> nt_load(const Vec16<
     return out;
 }
 
+// block_range for combiners with kDescending: the same lanes take the same elements, but every
+// lane visits them from its highest position down - the scalar tail, its 16-byte vectors four
+// at a time from the top, then the scalar head.
+template <typename C, typename In>
+__device__ __forceinline__ typename C::Acc block_range_down(const In* data, int64_t begin, int64_t end) {
+    using Acc = typename C::Acc;
+    constexpr int V = 16 / sizeof(In);
+    Acc acc = C::identity();
+    const int64_t misalign = (reinterpret_cast<uintptr_t>(data + begin) % 16) / sizeof(In);
+    const int64_t head_end = misalign != 0 ? std::min<int64_t>(end, begin + (V - misalign)) : begin;
+    const int64_t i = head_end;
+    const int64_t vectors = (end - i) / V;
+    const int64_t t = threadIdx.x;
+    for (int64_t j = i + vectors * V + t; j < end; j += kBlock) acc = C::step_down(acc, data[j], j);  // <= 1 per lane
+    const Vec16<In>* vp = reinterpret_cast<const Vec16<In>*>(data + i);
+    int64_t m = t < vectors ? (vectors - 1 - t) / kBlock + 1 : 0;  // this lane's vectors: t, t + kBlock, ...
+    for (; m >= 4; m -= 4) {
+        Vec16<In> x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = nt_load(vp + t + (m - 1 - u) * kBlock);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t first = i + (t + (m - 1 - u) * kBlock) * V;
+#pragma unroll
+            for (int e = V - 1; e >= 0; --e) acc = C::step_down(acc, x[u].v[e], first + e);
+        }
+    }
+    for (; m >= 1; --m) {
+        const Vec16<In> x = nt_load(vp + t + (m - 1) * kBlock);
+        const int64_t first = i + (t + (m - 1) * kBlock) * V;
+#pragma unroll
+        for (int e = V - 1; e >= 0; --e) acc = C::step_down(acc, x.v[e], first + e);
+    }
+    for (int64_t j = begin + t; j < head_end; j += kBlock) acc = C::step_down(acc, data[j], j);  // <= 1 per lane
+    return block_reduce<C>(acc);
+}
+
 // Reduces data[begin, end) with all lanes of the block; 16-byte loads when `data + begin` is
 // 16-byte aligned. Lane-level order is fixed by the block size.
 template <typename C, typename In>
 __device__ __forceinline__ typename C::Acc block_range(const In* data, int64_t begin, int64_t end) {
+    if constexpr (C::kDescending) return block_range_down<C, In>(data, begin, end);
     using Acc = typename C::Acc;
     constexpr int V = 16 / sizeof(In);
     Acc acc = C::identity();
@@ -223,7 +274,12 @@ __global__ __launch_bounds__(kBlock) void group_kernel(typename C::Out* results,
         typename C::Acc acc = C::identity();
         if (r < rows) {
             const In* row = data + r * chunk;
-            for (int64_t j = lane; j < chunk; j += G) acc = C::combine(acc, C::load(row[j], j));
+            if constexpr (C::kDescending) {
+                if (lane < chunk)
+                    for (int64_t j = lane + (chunk - 1 - lane) / G * G; j >= 0; j -= G) acc = C::step_down(acc, row[j], j);
+            } else {
+                for (int64_t j = lane; j < chunk; j += G) acc = C::combine(acc, C::load(row[j], j));
+            }
         }
         acc = group_reduce<C, G>(acc);
         if (lane == 0 && r < rows) results[r] = C::finish(acc);

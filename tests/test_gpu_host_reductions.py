@@ -7,7 +7,8 @@ accumulate in double on the device in a different order than kael's host code: f
 within rtol 1e-6 (prod) and, for cumsum, within 1e-6 of the running sum of |x| plus one f32
 ulp; f64 within 1e-12 of the same scales.
 Shapes reach every launch path: groups of lanes per short row, a workgroup per row, rows split
-across workgroups (reductions), one workgroup per row and segmented scans (cumsum).
+across workgroups (reductions), one workgroup per row and segmented scans with 8 or 16 elements
+per lane (cumsum).
 """
 import numpy as np
 import pytest
@@ -21,7 +22,8 @@ NP = {kd.F32: np.float32, kd.F64: np.float64, kd.I64: np.int64, kd.BOOL: np.bool
 DTYPES = [kd.F32, kd.F64, kd.I64, kd.BOOL]
 IDS = ["f32", "f64", "i64", "bool"]
 REDUCE_SHAPES = [(1, 1), (3, 7), (1000, 100), (600, 3000), (3, 100000), (1, 2000003)]
-SCAN_SHAPES = [(1, 1), (3, 7), (700, 130), (2, 30000), (1, 70001), (2, 1000003), (3, 333333)]
+SCAN_SHAPES = [(1, 1), (3, 7), (700, 130), (2, 30000), (1, 70001), (2, 1000003), (3, 333333), (64, 4096),
+               (3, 262144)]
 
 
 def sample(dtype, shape, rng, kind):
