@@ -178,6 +178,12 @@ template <typename In> __device__ __forceinline__ Vec16<In> nt_load(const Vec16<
     return out;
 }
 
+template <typename T> __device__ __forceinline__ void nt_store(Vec16<T>* p, const Vec16<T>& v) {
+    u32x4 r;
+    __builtin_memcpy(&r, &v, 16);
+    __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
+}
+
 // block_range for combiners with kDescending: the same lanes take the same elements, but every
 // lane visits them from its highest position down - the scalar tail, its 16-byte vectors four
 // at a time from the top, then the scalar head.
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(typename C::Out* result
 
 // ---- cumsum ------------------------------------------------------------------------------------
 
-constexpr int kScanPer = 8;  // consecutive elements scanned in registers by one lane
+constexpr int kScanPer = 8;  // elements scanned in registers by one lane per tile
 
 template <typename Acc> __device__ __forceinline__ Acc scan_add(Acc a, Acc b) {
     if constexpr (std::is_same_v<Acc, int64_t>) return wrap_add(a, b);
@@ -344,16 +350,57 @@ template <typename Acc> __device__ __forceinline__ Acc block_exclusive_scan(Acc 
     return scan_add(before, excl);
 }
 
-// Workgroup (s, r) scans segment s of row r (all of it when segments == 1), starting from the
-// sum of the row's earlier segments (their totals come from split_kernel). Tiles of
-// kBlock * kScanPer elements: lane t takes kScanPer consecutive elements, scans them in
-// registers, adds the exclusive scan of the lane totals and the running carry.
-// Vec: every row starts 16-byte aligned for In and Out and segments are whole tiles, so a lane
-// moves its kScanPer elements with 16-byte loads and stores (4x the scalar path's rate).
-template <typename T> struct alignas(16) Group8 {
-    T v[kScanPer];
-};
+// Exclusive scans of C values per lane across the workgroup in one pass (one pair of barriers
+// for all C); total[c] receives the workgroup sum of value c.
+template <typename Acc, int C>
+__device__ __forceinline__ void block_exclusive_scan_n(const Acc (&v)[C], Acc (&excl)[C], Acc (&total)[C]) {
+    __shared__ Acc wave_sum[kBlock / 64][C];
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    Acc x[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) x[c] = v[c];
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const Acc y = __shfl_up(x[c], d, 64);
+            if (lane >= d) x[c] = scan_add(x[c], y);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const Acc e = __shfl_up(x[c], 1, 64);
+        excl[c] = lane == 0 ? Acc(0) : e;
+        if (lane == 63) wave_sum[wave][c] = x[c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        Acc before = Acc(0);
+        Acc sum = Acc(0);
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) {
+            if (w < wave) before = scan_add(before, wave_sum[w][c]);
+            sum = scan_add(sum, wave_sum[w][c]);
+        }
+        excl[c] = scan_add(before, excl[c]);
+        total[c] = sum;
+    }
+    __syncthreads();  // wave_sum is reused by the next tile
+}
 
+// Workgroup (s, r) scans segment s of row r (all of it when segments == 1), starting from the
+// sum of the row's earlier segments (their totals come from split_kernel), in tiles of
+// kBlock * kScanPer elements.
+//  scalar: lane t takes kScanPer consecutive elements, scans them in registers and adds the
+//          exclusive scan of the lane totals and the running carry.
+//  Vec:    rows start 16-byte aligned for In and Out (of equal size) and hold a whole number
+//          of 16-byte vectors (segments are multiples of them). A tile is kScanPer / V chunks of
+//          kBlock vectors (V elements each) and lane t holds vector t of every chunk, so each
+//          load and store instruction moves one contiguous kBlock * 16 bytes; one block scan of
+//          the per-chunk lane totals serves the whole tile. The data is streamed once, with
+//          nontemporal loads and stores.
 template <typename In, typename Out, typename Acc, bool Vec>
 __global__ __launch_bounds__(kBlock) void scan_kernel(Out* out, const In* data, int64_t size, int64_t rows,
                                                       const Acc* seg_totals, int64_t segments, int64_t segment) {
@@ -375,40 +422,61 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Out* out, const In* data, 
         __syncthreads();
         Acc carry = carry_in;
         for (int64_t base = begin; base < end; base += int64_t{kBlock} * kScanPer) {
-            const int64_t first = base + static_cast<int64_t>(threadIdx.x) * kScanPer;
-            const bool whole = Vec && first + kScanPer <= end;
-            Acc vals[kScanPer];
-            Acc run = Acc(0);
-            if (whole) {
-                const Group8<In> g = *reinterpret_cast<const Group8<In>*>(row + first);
+            if constexpr (Vec) {
+                constexpr int V = 16 / sizeof(In);
+                constexpr int kChunks = kScanPer / V;
+                Acc vals[kChunks][V];
+                Acc lane_total[kChunks];
 #pragma unroll
-                for (int e = 0; e < kScanPer; ++e) {
-                    run = scan_add(run, static_cast<Acc>(g.v[e]));
-                    vals[e] = run;
+                for (int c = 0; c < kChunks; ++c) {
+                    const int64_t first = base + (int64_t{c} * kBlock + threadIdx.x) * V;
+                    Acc run = Acc(0);
+                    if (first < end) {  // whole vector: end is a multiple of V
+                        const Vec16<In> g = nt_load(reinterpret_cast<const Vec16<In>*>(row + first));
+#pragma unroll
+                        for (int e = 0; e < V; ++e) {
+                            run = scan_add(run, static_cast<Acc>(g.v[e]));
+                            vals[c][e] = run;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < V; ++e) vals[c][e] = Acc(0);
+                    }
+                    lane_total[c] = run;
+                }
+                Acc excl[kChunks], total[kChunks];
+                block_exclusive_scan_n<Acc, kChunks>(lane_total, excl, total);
+#pragma unroll
+                for (int c = 0; c < kChunks; ++c) {
+                    const int64_t first = base + (int64_t{c} * kBlock + threadIdx.x) * V;
+                    const Acc offset = scan_add(carry, excl[c]);
+                    if (first < end) {
+                        Vec16<Out> g;
+#pragma unroll
+                        for (int e = 0; e < V; ++e) g.v[e] = static_cast<Out>(scan_add(offset, vals[c][e]));
+                        nt_store(reinterpret_cast<Vec16<Out>*>(orow + first), g);
+                    }
+                    carry = scan_add(carry, total[c]);
                 }
             } else {
+                const int64_t first = base + static_cast<int64_t>(threadIdx.x) * kScanPer;
+                Acc vals[kScanPer];
+                Acc run = Acc(0);
 #pragma unroll
                 for (int e = 0; e < kScanPer; ++e) {
                     const int64_t j = first + e;
                     run = scan_add(run, j < end ? static_cast<Acc>(row[j]) : Acc(0));
                     vals[e] = run;
                 }
-            }
-            Acc total;
-            const Acc offset = scan_add(carry, block_exclusive_scan(run, total));
-            if (whole) {
-                Group8<Out> g;
-#pragma unroll
-                for (int e = 0; e < kScanPer; ++e) g.v[e] = static_cast<Out>(scan_add(offset, vals[e]));
-                *reinterpret_cast<Group8<Out>*>(orow + first) = g;
-            } else {
+                Acc total;
+                const Acc offset = scan_add(carry, block_exclusive_scan(run, total));
 #pragma unroll
                 for (int e = 0; e < kScanPer; ++e) {
                     const int64_t j = first + e;
                     if (j < end) orow[j] = static_cast<Out>(scan_add(offset, vals[e]));
                 }
+                carry = scan_add(carry, total);
             }
-            carry = scan_add(carry, total);
         }
         __syncthreads();  // carry_in is rewritten for the next row
     }
@@ -421,16 +489,21 @@ template <typename In> int cumsum_typed(void* out_v, const void* data_v, int64_t
     const In* data = static_cast<const In*>(data_v);
     const int cus = compute_units();
     constexpr int64_t kTile = int64_t{kBlock} * kScanPer;
-    // 16-byte groups of kScanPer elements: aligned rows whose length is a whole number of groups.
-    const bool vec = sizeof(In) * kScanPer % 16 == 0 && reinterpret_cast<uintptr_t>(data) % 16 == 0 &&
-                     reinterpret_cast<uintptr_t>(out) % 16 == 0 && size % kScanPer == 0;
+    // Coalesced 16-byte vectors: aligned rows holding a whole number of them, In and Out of one
+    // size (f32, f64, i64).
+    constexpr bool kVecType = sizeof(In) == sizeof(Out) && kScanPer * sizeof(In) % 16 == 0;
+    const bool vec = kVecType && reinterpret_cast<uintptr_t>(data) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 16 == 0 && size % static_cast<int64_t>(16 / sizeof(In)) == 0;
     const auto launch = [&](dim3 grid, const Acc* totals, int64_t segments, int64_t segment) {
-        if (vec)
-            hipLaunchKernelGGL((scan_kernel<In, Out, Acc, true>), grid, dim3(kBlock), 0, stream(), out, data, size, rows,
-                               totals, segments, segment);
-        else
-            hipLaunchKernelGGL((scan_kernel<In, Out, Acc, false>), grid, dim3(kBlock), 0, stream(), out, data, size,
-                               rows, totals, segments, segment);
+        if constexpr (kVecType) {
+            if (vec) {
+                hipLaunchKernelGGL((scan_kernel<In, Out, Acc, true>), grid, dim3(kBlock), 0, stream(), out, data, size,
+                                   rows, totals, segments, segment);
+                return;
+            }
+        }
+        hipLaunchKernelGGL((scan_kernel<In, Out, Acc, false>), grid, dim3(kBlock), 0, stream(), out, data, size, rows,
+                           totals, segments, segment);
     };
     if (rows >= 2 * cus || size <= 16 * kTile) {
         launch(dim3(1, static_cast<uint32_t>(std::min<int64_t>(rows, 65535))), nullptr, 1, size);
