@@ -53,22 +53,38 @@ struct Step {
 // c + S1/d and the population variance S2/d - (S1/d)^2; each element is standardised in double,
 // rounded to float, then * w and + b, each rounded (reference src/ops/nn.cpp:114-129 then
 // src/nn/layers.cpp:67).
+// Split in two so that a kernel issues the row's loads (ln_load) before its weight loads and
+// computes (ln_finish) after them: a wave waits for its loads in issue order, so a row loaded
+// after the weights could only be used once the weights had arrived too (measured: 0.8 us per
+// LayerNorm GEMV).
 constexpr int64_t kMaxLnDim = 4 * kThreads;
 
-__device__ void block_layernorm(const float* x, int64_t d, const float* w, const float* b, float* h) {
-    __shared__ double sums[2][kThreads / 64];
-    float xv[4];
+struct LnIn {
+    float x[4], w[4], b[4];
+    float c;  // the pivot x[0]
+};
+
+__device__ __forceinline__ LnIn ln_load(const float* x, int64_t d, const float* w, const float* b) {
+    LnIn r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t i = threadIdx.x + j * kThreads;
-        xv[j] = i < d ? x[i] : 0.f;
+        r.x[j] = i < d ? x[i] : 0.f;
+        r.w[j] = i < d ? w[i] : 0.f;
+        r.b[j] = i < d ? b[i] : 0.f;
     }
-    const double c = x[0];
+    r.c = x[0];
+    return r;
+}
+
+__device__ void ln_finish(const LnIn& r, int64_t d, float* h) {
+    __shared__ double sums[2][kThreads / 64];
+    const double c = r.c;
     double s1 = 0.0, s2 = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         if (threadIdx.x + j * kThreads < d) {
-            const double t = static_cast<double>(xv[j]) - c;
+            const double t = static_cast<double>(r.x[j]) - c;
             s1 += t;
             s2 += t * t;
         }
@@ -97,8 +113,8 @@ __device__ void block_layernorm(const float* x, int64_t d, const float* w, const
     for (int j = 0; j < 4; ++j) {
         const int64_t i = threadIdx.x + j * kThreads;
         if (i < d) {
-            const float y = static_cast<float>((static_cast<double>(xv[j]) - mean) / scale);
-            h[i] = __fadd_rn(__fmul_rn(y, w[i]), b[i]);
+            const float y = static_cast<float>((static_cast<double>(r.x[j]) - mean) / scale);
+            h[i] = __fadd_rn(__fmul_rn(y, r.w[j]), r.b[j]);
         }
     }
 }
@@ -148,41 +164,62 @@ struct AttnPartials {
 // Attention output of every head into h[0, heads * head_dim) from the chunk partials: with M the
 // maximum over a head's non-empty chunks (an empty chunk reports m = -inf, l = 0),
 // out = sum_c exp(m_c - M) acc_c / float(sum_c exp(m_c - M) l_c), the denominator being the
-// float rounding of a double sum as in reference src/ops/nn.cpp:60-71. Per-head factors are
-// staged in LDS, then every element issues its chunk loads together.
+// float rounding of a double sum as in reference src/ops/nn.cpp:60-71. attn_load issues every
+// load (this thread's chunk outputs, the chunk maxima, and thread hd's chunk sums for head
+// hd < heads) and attn_finish computes: the split lets a kernel issue its weight loads between
+// the two (see ln_load).
 constexpr int kMaxHeads = 64;
+constexpr int kAttnPer = kMaxLnDim / kThreads;                  // output elements per thread
+constexpr int kAttnSlots = kMaxHeads * kAttnChunks / kThreads;  // chunk maxima per thread
 
-__device__ void combine_attention(const AttnPartials& p, int64_t heads, int64_t head_dim, float* h) {
-    __shared__ float factor[kMaxHeads * kAttnChunks];
-    __shared__ float denom[kMaxHeads];
-    // The chunk outputs of this thread's elements (heads * head_dim <= kMaxLnDim), loaded first:
-    // they do not depend on the factors.
-    constexpr int kPer = kMaxLnDim / kThreads;
-    float acc[kPer][kAttnChunks];
+struct AttnIn {
+    float acc[kAttnPer][kAttnChunks];
+    float m[kAttnSlots];
+    double l[kAttnChunks];
+};
+
+__device__ __forceinline__ void attn_load(const AttnPartials& p, int64_t heads, int64_t head_dim, AttnIn& r) {
 #pragma unroll
-    for (int r = 0; r < kPer; ++r) {
-        const int64_t k = threadIdx.x + r * kThreads;
+    for (int q = 0; q < kAttnPer; ++q) {
+        const int64_t k = threadIdx.x + q * kThreads;
         const int64_t hd = k / head_dim;
         const int64_t e = k - hd * head_dim;
 #pragma unroll
         for (int c = 0; c < kAttnChunks; ++c)
-            acc[r][c] = k < heads * head_dim ? p.acc[(hd * kAttnChunks + c) * head_dim + e] : 0.f;
+            r.acc[q][c] = k < heads * head_dim ? p.acc[(hd * kAttnChunks + c) * head_dim + e] : 0.f;
     }
     const int64_t slots = heads * kAttnChunks;
-    for (int64_t i = threadIdx.x; i < slots; i += blockDim.x) factor[i] = p.m[i];
+#pragma unroll
+    for (int j = 0; j < kAttnSlots; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        r.m[j] = i < slots ? p.m[i] : 0.f;
+    }
+    if (threadIdx.x < heads) {
+#pragma unroll
+        for (int c = 0; c < kAttnChunks; ++c) r.l[c] = p.l[threadIdx.x * kAttnChunks + c];
+    }
+}
+
+__device__ void attn_finish(const AttnIn& r, int64_t heads, int64_t head_dim, float* h) {
+    __shared__ float factor[kMaxHeads * kAttnChunks];
+    __shared__ float denom[kMaxHeads];
+    const int64_t slots = heads * kAttnChunks;
+#pragma unroll
+    for (int j = 0; j < kAttnSlots; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        if (i < slots) factor[i] = r.m[j];
+    }
     __syncthreads();
-    for (int64_t hd = threadIdx.x; hd < heads; hd += blockDim.x) {
+    if (threadIdx.x < heads) {  // heads <= kMaxHeads <= kThreads
+        const int64_t hd = threadIdx.x;
         float M = -INFINITY;
         bool any = false;
         double lsum = 0.0;
         float w[kAttnChunks];
-        double l[kAttnChunks];
-#pragma unroll
-        for (int c = 0; c < kAttnChunks; ++c) l[c] = p.l[hd * kAttnChunks + c];
 #pragma unroll
         for (int c = 0; c < kAttnChunks; ++c) {
             const float m = factor[hd * kAttnChunks + c];
-            if (!(m == -INFINITY && l[c] == 0.0)) {
+            if (!(m == -INFINITY && r.l[c] == 0.0)) {
                 M = any ? max_na(M, m) : m;
                 any = true;
             }
@@ -190,9 +227,9 @@ __device__ void combine_attention(const AttnPartials& p, int64_t heads, int64_t 
 #pragma unroll
         for (int c = 0; c < kAttnChunks; ++c) {
             const float m = factor[hd * kAttnChunks + c];
-            const bool empty = m == -INFINITY && l[c] == 0.0;
+            const bool empty = m == -INFINITY && r.l[c] == 0.0;
             w[c] = empty ? 0.f : std::exp(__fsub_rn(m, M));
-            if (!empty) lsum += static_cast<double>(w[c]) * l[c];
+            if (!empty) lsum += static_cast<double>(w[c]) * r.l[c];
         }
 #pragma unroll
         for (int c = 0; c < kAttnChunks; ++c) factor[hd * kAttnChunks + c] = w[c];
@@ -200,13 +237,13 @@ __device__ void combine_attention(const AttnPartials& p, int64_t heads, int64_t 
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kPer; ++r) {
-        const int64_t k = threadIdx.x + r * kThreads;
+    for (int q = 0; q < kAttnPer; ++q) {
+        const int64_t k = threadIdx.x + q * kThreads;
         if (k < heads * head_dim) {
             const int64_t hd = k / head_dim;
             float num = 0.f;
 #pragma unroll
-            for (int c = 0; c < kAttnChunks; ++c) num += factor[hd * kAttnChunks + c] * acc[r][c];
+            for (int c = 0; c < kAttnChunks; ++c) num += factor[hd * kAttnChunks + c] * r.acc[q][c];
             h[k] = __fdiv_rn(num, denom[hd]);
         }
     }
@@ -218,11 +255,11 @@ struct GemvArgs {
     const float* bias;     // [N] or nullptr
     float* out;            // [N]
     int64_t N, K;
-    // With the Ln template flag the input is LayerNorm(x) with this weight and bias, computed by
+    // With the kLn prologue the input is LayerNorm(x) with this weight and bias, computed by
     // every workgroup into LDS (a 768-vector: cheaper than a separate launch).
     const float* ln_w;
     const float* ln_b;
-    // When attn.m is non-null the input is the attention output combined from chunk partials.
+    // With the kAttn prologue the input is the attention output combined from these chunk partials.
     AttnPartials attn;
     // kQkv: query -> q, key/value rows appended to this layer's cache at the current position
     float* q;
@@ -237,11 +274,16 @@ struct GemvArgs {
 
 constexpr int kMaxK = 4096;
 
+// Input prologues of gemv_kernel: the input vector as is, LayerNorm(x), or the attention output
+// combined from chunk partials.
+enum Prologue { kPlain = 0, kLn = 1, kAttn = 2 };
+
 // out[n] = epilogue(W[n, :] . x) for the rows of this workgroup. The input vector is staged in
-// LDS. Rows: WavesPerRow == 1 -> each wave
-// owns 2 rows (8 rows per workgroup); WavesPerRow == 4 -> the workgroup owns 2 rows and each wave
-// a quarter of K, combined through LDS.
-template <int Epi, int WavesPerRow, bool Ln>
+// LDS. Rows: WavesPerRow == 1 -> each wave owns 2 rows (8 rows per workgroup); WavesPerRow == 4
+// -> the workgroup owns 2 rows and each wave a quarter of K, combined through LDS.
+// Load order: the prologue's inputs first, then this lane's weights, then the epilogue's
+// operands; the prologue's arithmetic runs while the weights are in flight.
+template <int Epi, int WavesPerRow, int Pro>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __shared__ float4 hs4[kMaxK / 4];
     __shared__ float part[4][2];
@@ -256,13 +298,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const int64_t ke = WavesPerRow == 1 ? k4 : (k4 * (wave + 1)) / 4;
     const bool has0 = n0 < a.N;
     const bool has1 = n0 + 1 < a.N;
+    [[maybe_unused]] LnIn ln;
+    [[maybe_unused]] AttnIn attn;
+    [[maybe_unused]] float xr[kMaxK / kThreads];
+    if constexpr (Pro == kLn) {
+        ln = ln_load(a.x, K, a.ln_w, a.ln_b);
+    } else if constexpr (Pro == kAttn) {
+        attn_load(a.attn, K / a.head_dim, a.head_dim, attn);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kMaxK / kThreads; ++j) {
+            const int64_t k = threadIdx.x + j * kThreads;
+            xr[j] = k < K ? a.x[k] : 0.f;
+        }
+    }
     const float4* w0 = reinterpret_cast<const float4*>(a.W + (has0 ? n0 : 0) * K);
     const float4* w1 = reinterpret_cast<const float4*>(a.W + (has1 ? n0 + 1 : (has0 ? n0 : 0)) * K);
-    // Issue this lane's first weight loads before the input prologue so that their HBM latency
-    // overlaps it. A LayerNorm input has K = d <= 1024, so with K split over 4 waves one float4
-    // per row covers a wave's range: the registers this frees hold the LayerNorm row and keep
-    // 6 workgroups per CU resident.
-    constexpr int kPrefetch = Ln && WavesPerRow == 4 ? 1 : 4;
+    // This lane's first weight loads, in flight during the prologue. A LayerNorm input has
+    // K = d <= 1024, so with K split over 4 waves one float4 per row covers a wave's range:
+    // the registers this frees hold the LayerNorm row.
+    constexpr int kPrefetch = Pro == kLn && WavesPerRow == 4 ? 1 : 4;
     float4 pw0[kPrefetch], pw1[kPrefetch];
 #pragma unroll
     for (int i = 0; i < kPrefetch; ++i) {
@@ -283,12 +338,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         if constexpr (Epi == kResidual) resid = a.out[n];
     }
     const int64_t pos = Epi == kQkv ? a.st->pos : 0;
-    if constexpr (Ln) {
-        block_layernorm(a.x, K, a.ln_w, a.ln_b, hs);
-    } else if (a.attn.m != nullptr) {
-        combine_attention(a.attn, K / a.head_dim, a.head_dim, hs);
+    if constexpr (Pro == kLn) {
+        ln_finish(ln, K, hs);
+    } else if constexpr (Pro == kAttn) {
+        attn_finish(attn, K / a.head_dim, a.head_dim, hs);
     } else {
-        for (int64_t k = threadIdx.x; k < K; k += kThreads) hs[k] = a.x[k];
+#pragma unroll
+        for (int j = 0; j < kMaxK / kThreads; ++j) {
+            const int64_t k = threadIdx.x + j * kThreads;
+            if (k < K) hs[k] = xr[j];
+        }
     }
     __syncthreads();
 
@@ -395,9 +454,10 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
         }
     };
     int64_t p = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave;
+    const LnIn ln = ln_load(a.x, a.K, a.ln_w, a.ln_b);
     float4 c0[kHeadVec], c1[kHeadVec];
     if (p < pairs) load(p, c0, c1);
-    block_layernorm(a.x, a.K, a.ln_w, a.ln_b, reinterpret_cast<float*>(hs4));
+    ln_finish(ln, a.K, reinterpret_cast<float*>(hs4));
     __syncthreads();
     float4 h[kHeadVec];
 #pragma unroll
@@ -487,7 +547,7 @@ __global__ __launch_bounds__(kPickThreads) void argmax_final_kernel(Step* st, in
 // L = pos + 1 keys (the decode query sees every cached key, so no mask applies). Scores are
 // q.k / sqrt(head_dim) (16-lane groups, 16-byte loads, group shuffle reduction); the chunk keeps
 // its maximum m_c, the double sum l_c of exp(s - m_c) and the unnormalised weighted values
-// acc_c = sum exp(s - m_c) v. combine_attention() merges the chunks.
+// acc_c = sum exp(s - m_c) v. attn_load() / attn_finish() merge the chunks.
 __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, const float* __restrict__ q,
                                                              const float* __restrict__ kcache,
                                                              const float* __restrict__ vcache, AttnPartials part,
@@ -644,14 +704,14 @@ struct Engine {
     }
 
     // Ln: the input is LayerNorm(a.x) with weight a.ln_w and bias a.ln_b (K = d).
-    template <int Epi, bool Ln> void gemv(hipStream_t s, const GemvArgs& a) const {
+    template <int Epi, int Pro> void gemv(hipStream_t s, const GemvArgs& a) const {
         // Long rows and few of them (fc2: K = 3072, N = 768): split K across the workgroup's waves
         // so that more workgroups stream weights. Rows of K <= 1024 take one wave per row pair:
         // measured 1.5 us faster per LayerNorm GEMV at K = 768 (fewer workgroups repeat the
         // LayerNorm and no cross-wave combine), 0.5 us without a prologue.
         const bool split = a.N <= 4096 && a.K > 1024;
-        if (split) hipLaunchKernelGGL((gemv_kernel<Epi, 4, Ln>), rows_grid(a.N, true), dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<Epi, 1, Ln>), rows_grid(a.N, false), dim3(kThreads), 0, s, a);
+        if (split) hipLaunchKernelGGL((gemv_kernel<Epi, 4, Pro>), rows_grid(a.N, true), dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((gemv_kernel<Epi, 1, Pro>), rows_grid(a.N, false), dim3(kThreads), 0, s, a);
     }
 
     int record_step(hipStream_t s) {
@@ -675,7 +735,7 @@ struct Engine {
             qkv.q = q;
             qkv.kcache = kc;
             qkv.vcache = vc;
-            gemv<kQkv, true>(s, qkv);
+            gemv<kQkv, kLn>(s, qkv);
             hipLaunchKernelGGL(attention_kernel, dim3(static_cast<uint32_t>(cfg.heads), kAttnChunks), dim3(kThreads), attn_lds,
                                s, st, q, kc, vc, partials, hd, cfg.max_positions, divisor);
             GemvArgs proj = base();
@@ -686,7 +746,7 @@ struct Engine {
             proj.out = x;
             proj.N = d;
             proj.K = d;
-            gemv<kResidual, false>(s, proj);
+            gemv<kResidual, kAttn>(s, proj);
             GemvArgs fc1 = base();
             fc1.W = p(b + "mlp.fc1.weight");
             fc1.bias = p(b + "mlp.fc1.bias");
@@ -696,8 +756,8 @@ struct Engine {
             fc1.K = d;
             fc1.ln_w = p(b + "ln2.weight");
             fc1.ln_b = p(b + "ln2.bias");
-            if (cfg.tanh_gelu) gemv<kGeluTanh, true>(s, fc1);
-            else gemv<kGeluExact, true>(s, fc1);
+            if (cfg.tanh_gelu) gemv<kGeluTanh, kLn>(s, fc1);
+            else gemv<kGeluExact, kLn>(s, fc1);
             GemvArgs fc2 = base();
             fc2.W = p(b + "mlp.fc2.weight");
             fc2.bias = p(b + "mlp.fc2.bias");
@@ -705,7 +765,7 @@ struct Engine {
             fc2.out = x;
             fc2.N = d;
             fc2.K = ff;
-            gemv<kResidual, false>(s, fc2);
+            gemv<kResidual, kPlain>(s, fc2);
         }
         GemvArgs head = base();
         head.W = p("token_embedding.weight");
@@ -797,7 +857,7 @@ int create(Engine& e, const kd_gpt_config& c) {
     if (e.hd > 64) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim above 64 is not supported");
     if (e.d % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: dimension must be a multiple of 4");
     if (e.ff > kMaxK) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: 4 * dimension above 4096 is not supported");
-    static_assert(kMaxK / 4 <= kMaxLnDim, "block_layernorm holds a row of at most kMaxLnDim elements");
+    static_assert(kMaxK / 4 <= kMaxLnDim, "ln_load holds a row of at most kMaxLnDim elements");
     if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: more than 64 heads is not supported");
     if (c.max_positions > 8192) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: max_positions above 8192");
     // kael's parameter order and shapes (GPT::named_parameters)
