@@ -295,17 +295,22 @@ typedef struct kd_gpt_config {
     int64_t dimension;
     int32_t tanh_gelu;     /* GptConfig::tanh_gelu */
     int32_t flags;         /* KD_GPT_EAGER: launch each step's kernels directly instead of
-                              replaying the captured graph (for kernel-level profiling) */
+                              replaying the captured graph (for kernel-level profiling);
+                              KD_GPT_STEPWISE_PREFILL: run the prompt one cached step per
+                              position instead of the batched prefill (for comparison) */
 } kd_gpt_config;
 #define KD_GPT_EAGER 1
+#define KD_GPT_STEPWISE_PREFILL 2
 
 int kd_gpt_create(void** handle, const kd_gpt_config* config);
 void kd_gpt_destroy(void* handle);
 /* Uploads one parameter by its kael name (GPT::named_parameters(), e.g. "blocks.3.attn.qkv.weight")
  * from host f32 data holding all `count` elements in kael's row-major layout. */
 int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int64_t count);
-/* Runs the prompt (positions 0..length-1) through the cached forward; the last position's
- * greedy token becomes the first generated token. Clears any previous sequence. */
+/* Runs the prompt (positions 0..length-1) through the model, filling the KV cache; the last
+ * position's greedy token becomes the first generated token. Clears any previous sequence. By
+ * default all positions pass each layer together (GEMMs on the matrix cores, causal attention);
+ * KD_GPT_STEPWISE_PREFILL runs them as cached single-token steps. */
 int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length);
 /* Generates `count` more tokens greedily, one cached step each (decode). `tokens` (host, may be
  * NULL) receives the `count` new ids. The total sequence may not exceed max_positions + 1. */
@@ -316,6 +321,10 @@ int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, fl
 /* The full sequence so far (prompt + generated), `capacity` entries at most; returns its length
  * through `length`. */
 int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* length);
+/* The logits of the most recent position (vocab_size floats, host): the prompt's last position
+ * after kd_gpt_prefill, the last step's after kd_gpt_decode. No reference counterpart (kael's
+ * generate returns tokens only); for parity checks of the prefill paths. */
+int kd_gpt_logits(void* handle, float* logits);
 
 /* ---- measurement helpers (no reference counterpart; used by the bench) -- */
 

@@ -8,7 +8,7 @@
 //
 //   embed       x = wte[token] + wpe[pos]                                      (1 launch)
 //   per layer   qkv GEMV on ln1(x) (+bias; K/V appended to the cache)
-//               -> attention split into 16 key chunks per head (chunk max, double sum of
+//               -> attention split into 8 key chunks per head (chunk max, double sum of
 //                  exponentials, unnormalised weighted values)
 //               -> proj GEMV on the combined attention output (+bias, +residual into x)
 //               -> fc1 GEMV on ln2(x) (+bias, GELU)
@@ -19,6 +19,10 @@
 // The LayerNorm feeding a GEMV is recomputed by each of its workgroups into LDS (768 values):
 // cheaper than a separate launch. A "last workgroup finishes" epilogue was measured and
 // rejected: same-address device-scope atomics serialise at about 100 ns each on this part.
+//
+// The prompt goes through a batched prefill instead: all of its positions pass each layer
+// together (row LayerNorms, GEMMs on the MFMA matmul path, a causal attention kernel), and the
+// last position's logits and greedy token come from the same head and pick kernels.
 //
 // All step-dependent values (position, token) live in device memory, so the graph is static.
 // Weights keep kael's [out, in] row-major layout: every Linear is a row-dot GEMV reading whole
@@ -274,6 +278,16 @@ struct GemvArgs {
 
 constexpr int kMaxK = 4096;
 
+// kael's GELU forms (reference src/internal/element_functions.h:278-288) on a Linear output.
+template <int Epi> __device__ __forceinline__ float gelu_of(float y) {
+    if constexpr (Epi == kGeluTanh) {
+        const float scale = std::sqrt(2 / MathConst<float>::pi);
+        return 0.5f * y * (1 + std::tanh(scale * (y + 0.044715f * y * y * y)));
+    } else {
+        return 0.5f * y * (1 + std::erf(y / MathConst<float>::sqrt2));
+    }
+}
+
 // Input prologues of gemv_kernel: the input vector as is, LayerNorm(x), or the attention output
 // combined from chunk partials.
 enum Prologue { kPlain = 0, kLn = 1, kAttn = 2 };
@@ -389,11 +403,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     if (active) {
         const float dot = lane == 0 ? a0 : a1;
         y = __fadd_rn(dot, bias);
-        if constexpr (Epi == kGeluTanh) {
-            const float scale = std::sqrt(2 / MathConst<float>::pi);
-            y = 0.5f * y * (1 + std::tanh(scale * (y + 0.044715f * y * y * y)));
-        } else if constexpr (Epi == kGeluExact) {
-            y = 0.5f * y * (1 + std::erf(y / MathConst<float>::sqrt2));
+        if constexpr (Epi == kGeluTanh || Epi == kGeluExact) {
+            y = gelu_of<Epi>(y);
         } else if constexpr (Epi == kResidual) {
             y = __fadd_rn(resid, y);
         }
@@ -656,6 +667,142 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
     }
 }
 
+// ---- batched prefill ---------------------------------------------------------------------------
+//
+// The prompt's T positions pass each layer together: row LayerNorms, the four Linear products
+// as GEMMs on the MFMA matmul path (activation rows padded to whole 128-row tiles, weights in
+// [in, out] copies made once so that both operands are row-major and few-tile products get
+// split K), epilogue kernels for the bias, residual, GELU and the K/V rows into the cache, and a
+// causal attention kernel. Same arithmetic as the decode step; only the summation order of the
+// dot products differs.
+
+// X[t] = wte[seq[t]] + wpe[t].
+__global__ __launch_bounds__(kThreads) void prefill_embed_kernel(const int64_t* seq, const float* wte, const float* wpe,
+                                                                 float* X, int64_t d) {
+    const int64_t t = blockIdx.y;
+    const int64_t tok = seq[t];
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < d;
+         i += static_cast<int64_t>(gridDim.x) * kThreads)
+        X[t * d + i] = __fadd_rn(wte[tok * d + i], wpe[t * d + i]);
+}
+
+// H[t] = LayerNorm(X[t]), one workgroup per row.
+__global__ __launch_bounds__(kThreads) void ln_rows_kernel(const float* X, const float* w, const float* b, float* H,
+                                                           int64_t d) {
+    const int64_t t = blockIdx.x;
+    const LnIn r = ln_load(X + t * d, d, w, b);
+    ln_finish(r, d, H + t * d);
+}
+
+// y = P[t, n] + bias[n] for the T x N product P (row stride N), then by epilogue:
+//   kQkv       query part -> Q[t, n]; key and value parts -> the cache rows of position t
+//   kResidual  X[t, n] = X[t, n] + y
+//   kGelu*     F[t, n] = gelu(y)
+template <int Epi>
+__global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float* P, const float* bias, float* out, int64_t T,
+                                                                    int64_t N, int64_t d, int64_t head_dim,
+                                                                    int64_t max_positions, float* kcache, float* vcache) {
+    const int64_t total = T * N;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t t = e / N;
+        const int64_t n = e - t * N;
+        const float y = __fadd_rn(P[e], bias[n]);
+        if constexpr (Epi == kQkv) {
+            const int64_t part = n / d;
+            const int64_t within = n - part * d;
+            if (part == 0) {
+                out[t * d + within] = y;
+            } else {
+                const int64_t head = within / head_dim;
+                const int64_t dim = within - head * head_dim;
+                float* cache = part == 1 ? kcache : vcache;
+                cache[(head * max_positions + t) * head_dim + dim] = y;
+            }
+        } else if constexpr (Epi == kResidual) {
+            out[e] = __fadd_rn(out[e], y);
+        } else {
+            out[e] = gelu_of<Epi>(y);
+        }
+    }
+}
+
+// Causal attention of query t of head h (workgroup (h, t)) over keys 0..t: scores q.k /
+// sqrt(head_dim) by 16-lane groups, the row maximum, exponentials summed in double, the
+// weighted sum of values divided by the float rounding of that sum.
+__global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const float* __restrict__ Q,
+                                                                     const float* __restrict__ kcache,
+                                                                     const float* __restrict__ vcache, float* A,
+                                                                     int64_t d, int64_t head_dim, int64_t max_positions,
+                                                                     float divisor) {
+    extern __shared__ float scores[];  // [t + 1]
+    __shared__ float red_f[kThreads / 64];
+    __shared__ double red_d[kThreads / 64];
+    __shared__ float4 acc_part[kThreads / 16][16];
+    const int64_t h = blockIdx.x;
+    const int64_t t = blockIdx.y;
+    const int64_t count = t + 1;
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
+    const int sub = tid % 16, group = tid / 16;
+    const bool dims_ok = 4 * sub < head_dim;
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (dims_ok) qv = *reinterpret_cast<const float4*>(Q + t * d + h * head_dim + 4 * sub);
+    const float* K = kcache + h * max_positions * head_dim;
+    const float* V = vcache + h * max_positions * head_dim;
+    float local_max = -INFINITY;
+    for (int64_t j = group; j < count; j += kThreads / 16) {
+        float4 k = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (dims_ok) k = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
+        float sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
+#pragma unroll
+        for (int m = 8; m > 0; m /= 2) sc += __shfl_xor(sc, m, 64);
+        sc = __fdiv_rn(sc, divisor);
+        if (sub == 0) scores[j] = sc;
+        local_max = max_na(local_max, sc);
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) local_max = max_na(local_max, __shfl_xor(local_max, m, 64));
+    if (lane == 0) red_f[wave] = local_max;
+    __syncthreads();
+    float largest = red_f[0];
+    for (int w = 1; w < kThreads / 64; ++w) largest = max_na(largest, red_f[w]);
+    double total = 0.0;
+    for (int64_t j = tid; j < count; j += kThreads) {
+        const float e = std::exp(__fsub_rn(scores[j], largest));
+        scores[j] = e;
+        total += static_cast<double>(e);
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m /= 2) total += __shfl_xor(total, m, 64);
+    if (lane == 0) red_d[wave] = total;
+    __syncthreads();
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (dims_ok) {
+        for (int64_t j = group; j < count; j += kThreads / 16) {
+            const float w = scores[j];
+            const float4 v = *reinterpret_cast<const float4*>(V + j * head_dim + 4 * sub);
+            acc.x += w * v.x;
+            acc.y += w * v.y;
+            acc.z += w * v.z;
+            acc.w += w * v.w;
+        }
+    }
+    acc_part[group][sub] = acc;
+    __syncthreads();
+    if (tid < head_dim) {
+        double sum = red_d[0];
+        for (int w = 1; w < kThreads / 64; ++w) sum += red_d[w];
+        const int s4 = tid / 4, e = tid % 4;
+        float r = 0.f;
+        for (int g = 0; g < kThreads / 16; ++g) {
+            const float4 pv = acc_part[g][s4];
+            r += e == 0 ? pv.x : e == 1 ? pv.y : e == 2 ? pv.z : pv.w;
+        }
+        A[t * d + h * head_dim + tid] = __fdiv_rn(r, static_cast<float>(sum));
+    }
+}
+
 // ---- engine ----------------------------------------------------------------------------------
 
 struct Engine {
@@ -680,6 +827,17 @@ struct Engine {
     hipGraphExec_t graph = nullptr;
     int64_t host_pos = 0;     // mirror of st->pos
     int64_t host_forced = 0;
+    // batched prefill (allocated at the first prefill): activations of up to pf_rows positions
+    // (max_positions rounded up to whole 128-row tiles) and the weights as [in, out] copies
+    int64_t pf_rows = 0;
+    float* pf_x = nullptr;    // [pf_rows, d] residual stream
+    float* pf_h = nullptr;    // [pf_rows, d] LayerNorm output
+    float* pf_q = nullptr;    // [pf_rows, d] queries
+    float* pf_a = nullptr;    // [pf_rows, d] attention output
+    float* pf_f = nullptr;    // [pf_rows, ff] GELU output
+    float* pf_p = nullptr;    // [pf_rows, max(3d, ff)] product before its epilogue
+    float* wt = nullptr;      // per layer: qkv^T [d, 3d], proj^T [d, d], fc1^T [d, ff], fc2^T [ff, d]
+    bool wt_valid = false;    // cleared by every parameter upload
 
     const float* p(const std::string& name) const { return params + offsets.at(name).first; }
 
@@ -827,8 +985,131 @@ struct Engine {
         return KD_OK;
     }
 
+    bool stepwise_prefill() const { return (cfg.flags & KD_GPT_STEPWISE_PREFILL) != 0; }
+
+    int64_t layer_t_floats() const { return 12 * d * d; }
+    float* wt_qkv(int64_t l) const { return wt + l * layer_t_floats(); }
+    float* wt_proj(int64_t l) const { return wt_qkv(l) + 3 * d * d; }
+    float* wt_fc1(int64_t l) const { return wt_proj(l) + d * d; }
+    float* wt_fc2(int64_t l) const { return wt_fc1(l) + d * ff; }
+
+    int ensure_prefill_buffers() {
+        if (pf_x != nullptr) return KD_OK;
+        pf_rows = (cfg.max_positions + 127) / 128 * 128;
+        for (auto [ptr, cols] : {std::pair<float**, int64_t>{&pf_x, d}, {&pf_h, d}, {&pf_q, d}, {&pf_a, d}, {&pf_f, ff},
+                                 {&pf_p, std::max(3 * d, ff)}}) {
+            void* mem = nullptr;
+            KD_HIP(hipMalloc(&mem, static_cast<size_t>(pf_rows * cols) * sizeof(float)));
+            *ptr = static_cast<float*>(mem);
+        }
+        void* mem = nullptr;
+        KD_HIP(hipMalloc(&mem, static_cast<size_t>(cfg.layers * layer_t_floats()) * sizeof(float)));
+        wt = static_cast<float*>(mem);
+        return KD_OK;
+    }
+
+    // dst [K, N] row-major = transpose of src [N, K] row-major (kael's Linear weight).
+    static int transpose_into(float* dst, const float* src, int64_t N, int64_t K) {
+        kd_element_layout l{};
+        l.dims = 2;
+        l.operands = 2;
+        l.count = N * K;
+        l.shape[0] = K;
+        l.shape[1] = N;
+        l.strides[0][0] = N * 4;
+        l.strides[0][1] = 4;
+        l.strides[1][0] = 4;
+        l.strides[1][1] = K * 4;
+        l.base[0] = dst;
+        l.base[1] = const_cast<float*>(src);
+        return kd_convert(KD_F32, KD_F32, &l);
+    }
+
+    int refresh_transposed() {
+        if (wt_valid) return KD_OK;
+        for (int64_t l = 0; l < cfg.layers; ++l) {
+            const std::string b = "blocks." + std::to_string(l) + ".";
+            if (int rc = transpose_into(wt_qkv(l), p(b + "attn.qkv.weight"), 3 * d, d)) return rc;
+            if (int rc = transpose_into(wt_proj(l), p(b + "attn.proj.weight"), d, d)) return rc;
+            if (int rc = transpose_into(wt_fc1(l), p(b + "mlp.fc1.weight"), ff, d)) return rc;
+            if (int rc = transpose_into(wt_fc2(l), p(b + "mlp.fc2.weight"), d, ff)) return rc;
+        }
+        wt_valid = true;
+        return KD_OK;
+    }
+
+    // P[rows, N] = A[rows, K] . Wt[K, N] on the backend's matmul path (rows = T rounded up to
+    // 128; the padding rows hold leftovers of earlier rows and their products are ignored).
+    static int product(const float* A, const float* Wt, float* P, int64_t rows, int64_t K, int64_t N) {
+        kd_matmul_sizes sz{1, rows, K, N};
+        return kd_matmul(KD_F32, A, Wt, P, &sz);
+    }
+
+    template <int Epi> void epilogue(const float* bias, float* out, int64_t T, int64_t N, float* kc, float* vc) const {
+        const int64_t total = T * N;
+        const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{compute_units()} * 16);
+        hipLaunchKernelGGL((prefill_epilogue_kernel<Epi>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, kd::stream(),
+                           pf_p, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
+    }
+
+    // Positions 0..T-1 of seq (already on the device) through every layer at once; then the
+    // head and the greedy pick on position T - 1, which write seq[T] and leave st->pos = T.
+    int batched_prefill(int64_t T) {
+        if (int rc = ensure_prefill_buffers()) return rc;
+        if (int rc = refresh_transposed()) return rc;
+        hipStream_t s = kd::stream();
+        const int64_t rows = (T + 127) / 128 * 128;
+        const float divisor = static_cast<float>(std::sqrt(static_cast<double>(hd)));
+        hipLaunchKernelGGL(prefill_embed_kernel, dim3(static_cast<uint32_t>((d + kThreads - 1) / kThreads), static_cast<uint32_t>(T)),
+                           dim3(kThreads), 0, s, seq, p("token_embedding.weight"), p("position_embedding.weight"), pf_x, d);
+        KD_LAUNCH_CHECK();
+        for (int64_t l = 0; l < cfg.layers; ++l) {
+            const std::string b = "blocks." + std::to_string(l) + ".";
+            float* kc = kcache + l * cfg.heads * cfg.max_positions * hd;
+            float* vc = vcache + l * cfg.heads * cfg.max_positions * hd;
+            hipLaunchKernelGGL(ln_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pf_x, p(b + "ln1.weight"),
+                               p(b + "ln1.bias"), pf_h, d);
+            if (int rc = product(pf_h, wt_qkv(l), pf_p, rows, d, 3 * d)) return rc;
+            epilogue<kQkv>(p(b + "attn.qkv.bias"), pf_q, T, 3 * d, kc, vc);
+            hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<uint32_t>(cfg.heads), static_cast<uint32_t>(T)),
+                               dim3(kThreads), static_cast<size_t>(T) * sizeof(float), s, pf_q, kc, vc, pf_a, d, hd,
+                               cfg.max_positions, divisor);
+            if (int rc = product(pf_a, wt_proj(l), pf_p, rows, d, d)) return rc;
+            epilogue<kResidual>(p(b + "attn.proj.bias"), pf_x, T, d, nullptr, nullptr);
+            hipLaunchKernelGGL(ln_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pf_x, p(b + "ln2.weight"),
+                               p(b + "ln2.bias"), pf_h, d);
+            if (int rc = product(pf_h, wt_fc1(l), pf_p, rows, d, ff)) return rc;
+            if (cfg.tanh_gelu) epilogue<kGeluTanh>(p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
+            else epilogue<kGeluExact>(p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
+            if (int rc = product(pf_f, wt_fc2(l), pf_p, rows, ff, d)) return rc;
+            epilogue<kResidual>(p(b + "mlp.fc2.bias"), pf_x, T, d, nullptr, nullptr);
+            KD_LAUNCH_CHECK();
+        }
+        GemvArgs head = base();
+        head.W = p("token_embedding.weight");
+        head.x = pf_x + (T - 1) * d;
+        head.ln_w = p("ln_final.weight");
+        head.ln_b = p("ln_final.bias");
+        head.N = cfg.vocab_size;
+        head.K = d;
+        head.out = logits;
+        head.best_v = pv;
+        head.best_i = pi;
+        const int64_t parts = head_groups();
+        hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kPickThreads), 0, s, st, seq, pv, pi, parts);
+        KD_LAUNCH_CHECK();
+        KD_HIP(hipStreamSynchronize(s));
+        host_pos = T;
+        return KD_OK;
+    }
+
     ~Engine() {
         if (graph) (void)hipGraphExecDestroy(graph);
+        for (void* ptr : {static_cast<void*>(pf_x), static_cast<void*>(pf_h), static_cast<void*>(pf_q),
+                          static_cast<void*>(pf_a), static_cast<void*>(pf_f), static_cast<void*>(pf_p),
+                          static_cast<void*>(wt)})
+            if (ptr) (void)hipFree(ptr);
         for (void* ptr : {static_cast<void*>(params), static_cast<void*>(kcache), static_cast<void*>(vcache),
                           static_cast<void*>(x), static_cast<void*>(q), static_cast<void*>(partials.m),
                           static_cast<void*>(partials.l), static_cast<void*>(partials.acc),
@@ -856,6 +1137,7 @@ int create(Engine& e, const kd_gpt_config& c) {
     e.ff = 4 * c.dimension;
     if (e.hd > 64) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim above 64 is not supported");
     if (e.d % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: dimension must be a multiple of 4");
+    if (e.hd % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim must be a multiple of 4 (16-byte key rows)");
     if (e.ff > kMaxK) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: 4 * dimension above 4096 is not supported");
     static_assert(kMaxK / 4 <= kMaxLnDim, "ln_load holds a row of at most kMaxLnDim elements");
     if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: more than 64 heads is not supported");
@@ -941,6 +1223,7 @@ int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int
     KD_HIP(hipMemcpy(e->params + it->second.first, data, static_cast<size_t>(count) * sizeof(float), hipMemcpyHostToDevice));
     for (size_t i = 0; i < e->names.size(); ++i)
         if (e->names[i] == name) e->loaded[i] = true;
+    e->wt_valid = false;
     return KD_OK;
 }
 
@@ -952,8 +1235,13 @@ int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length) {
         if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab_size) return fail(KD_E_INVALID, "kd_gpt_prefill: token id out of range");
     if (int rc = e->ready()) return rc;
     KD_HIP(hipMemcpyAsync(e->seq, prompt, static_cast<size_t>(length) * sizeof(int64_t), hipMemcpyHostToDevice, e->stream));
-    if (int rc = e->set_state(0, length)) return rc;
-    return e->steps(length);
+    if (e->stepwise_prefill()) {
+        if (int rc = e->set_state(0, length)) return rc;
+        return e->steps(length);
+    }
+    // The pick after the batched layers runs as the step of position length - 1.
+    if (int rc = e->set_state(length - 1, length)) return rc;
+    return e->batched_prefill(length);
 }
 
 int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens) {
@@ -998,6 +1286,15 @@ int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* lengt
     if (ids != nullptr && capacity > 0 && n > 0) {
         KD_HIP(hipMemcpy(ids, e->seq, static_cast<size_t>(std::min(n, capacity)) * sizeof(int64_t), hipMemcpyDeviceToHost));
     }
+    return KD_OK;
+}
+
+int kd_gpt_logits(void* handle, float* logits) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || logits == nullptr) return fail(KD_E_INVALID, "kd_gpt_logits: bad arguments");
+    if (e->host_pos == 0) return fail(KD_E_INVALID, "kd_gpt_logits: no position has been run");
+    KD_HIP(hipStreamSynchronize(e->stream));
+    KD_HIP(hipMemcpy(logits, e->logits, static_cast<size_t>(e->cfg.vocab_size) * sizeof(float), hipMemcpyDeviceToHost));
     return KD_OK;
 }
 

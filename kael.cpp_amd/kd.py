@@ -140,6 +140,7 @@ BACKEND_ONLY = {
     "gpt_decode": (c_int, [c_void_p, c_int64, c_void_p]),
     "gpt_forward_logits": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "gpt_sequence": (c_int, [c_void_p, c_void_p, c_int64, POINTER(c_int64)]),
+    "gpt_logits": (c_int, [c_void_p, c_void_p]),
 }
 
 # Every symbol include/kd_api.h declares.
@@ -238,10 +239,14 @@ class DeviceArray:
 class Gpt:
     """The GPT-2 decode engine (kd_gpt_*): kael's parameter names and layout, greedy decoding."""
 
+    EAGER = 1
+    STEPWISE_PREFILL = 2
+
     def __init__(self, backend: Backend, vocab_size=50257, max_positions=1024, layers=12, heads=12, dimension=768,
-                 tanh_gelu=True, eager=False):
+                 tanh_gelu=True, eager=False, stepwise_prefill=False):
         self.b = backend
-        self.config = GptConfig(vocab_size, max_positions, layers, heads, dimension, int(bool(tanh_gelu)), 1 if eager else 0)
+        flags = (self.EAGER if eager else 0) | (self.STEPWISE_PREFILL if stepwise_prefill else 0)
+        self.config = GptConfig(vocab_size, max_positions, layers, heads, dimension, int(bool(tanh_gelu)), flags)
         h = c_void_p()
         backend.check(backend.lib.kd_gpt_create(ctypes.byref(h), ctypes.byref(self.config)), "kd_gpt_create")
         self.handle = h
@@ -279,6 +284,12 @@ class Gpt:
         out = np.empty((t.size, self.config.vocab_size), np.float32)
         self.b.check(self.b.lib.kd_gpt_forward_logits(self.handle, t.ctypes.data_as(c_void_p), t.size,
                                                       out.ctypes.data_as(c_void_p)), "kd_gpt_forward_logits")
+        return out
+
+    def logits(self) -> np.ndarray:
+        """Logits of the most recent position (the prompt's last after prefill)."""
+        out = np.empty(self.config.vocab_size, np.float32)
+        self.b.check(self.b.lib.kd_gpt_logits(self.handle, out.ctypes.data_as(c_void_p)), "kd_gpt_logits")
         return out
 
     def sequence(self) -> np.ndarray:

@@ -113,3 +113,62 @@ def test_hugging_face_checkpoint_loads_into_the_engine(kdb, refdev, tmp_path):
         np.testing.assert_array_equal(g.sequence(), seq)
     finally:
         ref.ref_gpt_destroy(h)
+
+
+def check_prefill_and_steps(g, ref, h, prompt, steps, vocab, rtol):
+    """Prefill `prompt`, then `steps` greedy decode steps; the logits after the prefill and
+    after every step against kael's cached forward over kael's own greedy sequence."""
+    seq, _ = cpu_generate(ref, h, prompt, steps + 1)
+    want = cpu_cached_logits(ref, h, seq, len(prompt), vocab)  # rows: positions len-1 .. len+steps
+    g.prefill(prompt)
+    got = [g.logits()]
+    for _ in range(steps):
+        g.decode(1)
+        got.append(g.logits())
+    got = np.stack(got)
+    scale = np.abs(want).max()
+    err = np.abs(got - want[:steps + 1]).max()
+    assert err <= rtol * scale, f"max |dlogit| {err} vs scale {scale}"
+    np.testing.assert_array_equal(g.sequence(), seq[:len(prompt) + steps + 1])
+    return got
+
+
+@pytest.mark.parametrize("prompt_len", [1, 5, 16])
+def test_small_model_batched_prefill(kdb, refdev, prompt_len):
+    """head_dim 4, prompts of one position up to the whole context; batched and stepwise prefill
+    both against kael, and against each other."""
+    ref = refdev
+    h = ref.ref_gpt_create(11, 24, 2, 2, 8, 31, 1)
+    assert h, support.ref_error(ref)
+    try:
+        params = export_params(ref, h)
+        prompt = np.random.default_rng(prompt_len).integers(0, 11, prompt_len)
+        steps = min(4, 24 - prompt_len - 1)
+        runs = []
+        for stepwise in (False, True):
+            g = kd.Gpt(kdb, 11, 24, 2, 2, 8, True, stepwise_prefill=stepwise)
+            for name, data in params:
+                g.load(name, data)
+            runs.append(check_prefill_and_steps(g, ref, h, prompt, steps, 11, 1e-5))
+        np.testing.assert_allclose(runs[0], runs[1], rtol=1e-5, atol=1e-6)
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
+def test_gpt2_small_batched_prefill(kdb, refdev):
+    """Config C5 with prompts of 64 and 300 positions (three 128-row tiles): the prompt's last
+    logits and three decode steps within 1e-4 of the largest logit, kael's greedy tokens."""
+    ref = refdev
+    ref.ref_set_threads(min(16, max(1, __import__("os").cpu_count() or 1)))
+    h, g = build(kdb, ref, 50257, 1024, 12, 12, 768, 4)
+    try:
+        rng = np.random.default_rng(5)
+        for prompt_len in (64, 300):
+            check_prefill_and_steps(g, ref, h, rng.integers(0, 50257, prompt_len), 3, 50257, 1e-4)
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
+def test_odd_head_dim_is_rejected(kdb):
+    with pytest.raises(kd.KdError):
+        kd.Gpt(kdb, 11, 16, 1, 4, 24, True)  # head_dim 6
