@@ -111,3 +111,41 @@ def test_strided_operands(kdb, oracle, case):
     da, db, dc = kdb.to_device(a_store), kdb.to_device(b_store), kdb.empty((batches, m, n), np.float32)
     kdb.call("matmul_strided", kd.F32, da.ptr, db.ptr, dc.ptr, sizes, strides)
     close(dc.numpy(), want.astype(np.float64))
+
+
+def test_headline_4096_cubed(kdb, refdev):
+    """The benchmark's headline product (row-major MFMA kernel, whole tiles) at its full size,
+    inputs as bench.py draws them. At K = 4096 an element's f32 rounding error scales with its
+    dot product's sum of |a||b| (~1024 here), not with the element itself, so elements near
+    zero miss the small-shape rule 1e-4 + 1e-4 |y| by a few ulps of that sum in any f32
+    product. Checks: within 1e-4 of the largest |element| of the float64 product (the rule of
+    the GPT-2 logits), and within 8x the worst error of kael's own f32 CPU product of the same
+    inputs (reference matmul_versions v6). Measured: device worst 3.6e-4 (one running f32 MFMA
+    sum over K), kael CPU 6.6e-5 (its K blocking shortens the running sums), scale ~1e2."""
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (4096, 4096)).astype(np.float32)
+    b = rng.uniform(-1, 1, (4096, 4096)).astype(np.float32)
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((4096, 4096), np.float32)
+    kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(1, 4096, 4096, 4096))
+    got = dc.numpy().astype(np.float64)
+    want = reference_product(a, b)
+    refdev.ref_set_threads(min(16, max(1, __import__("os").cpu_count() or 1)))
+    cpu = np.empty((4096, 4096), np.float32)
+    assert refdev.ref_matmul(kd.F32, support.ptr(a), support.ptr(b), support.ptr(cpu), 1, 4096, 4096, 4096) == 0, \
+        support.ref_error(refdev)
+    err = np.abs(got - want)
+    err_cpu = np.abs(cpu.astype(np.float64) - want)
+    assert err.max() <= 1e-4 * np.abs(want).max(), f"worst {err.max()} vs scale {np.abs(want).max()}"
+    assert err.max() <= 8 * err_cpu.max(), f"device worst {err.max()}, kael CPU worst {err_cpu.max()}"
+
+
+@pytest.mark.parametrize("batches,m,k,n", [(2, 384, 256, 512), (3, 128, 1024, 128)])
+def test_batched_whole_tiles_with_split_k(kdb, batches, m, k, n):
+    """Batched row-major products with few tiles: the row-major kernel splits K and sums the
+    partials per batch."""
+    rng = np.random.default_rng(m + k + n)
+    a = rng.uniform(-1, 1, (batches, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (batches, k, n)).astype(np.float32)
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((batches, m, n), np.float32)
+    kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n))
+    close(dc.numpy(), reference_product(a, b))
