@@ -427,11 +427,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 
 // Logits of the tied head, logits[n] = wte[n, :] . LayerNorm_f(x), and each workgroup's best
 // row (first maximum, first NaN; reference src/ops/reduce.cpp:236-254) for argmax_final_kernel.
-// A fixed grid of 2 workgroups per CU streams the [vocab, d] table: each wave takes row pairs
-// p, p + stride, ... and issues the next pair's loads before the current pair's dot products,
-// so every wave keeps two pairs in flight. The final LayerNorm is computed once per workgroup
-// into LDS and then held in registers (one launch fewer than a separate LayerNorm, and 512
-// argmax partials instead of one per 8 rows). Needs d <= kMaxLnDim (4 float4 per lane).
+// A fixed grid of 4 workgroups per CU (its occupancy at 108 VGPRs) streams the [vocab, d] table:
+// each wave takes row pairs p, p + stride, ... and issues the next pair's loads before the
+// current pair's dot products, so every wave keeps two pairs in flight. The final LayerNorm is
+// computed once per workgroup into LDS and then held in registers (one launch fewer than a
+// separate LayerNorm, and one argmax partial per workgroup: 1024 instead of one per 8 rows).
+// Needs d <= kMaxLnDim (4 float4 per lane). Registers sized to d = 768 (5 workgroups per CU)
+// measured no faster (27.4 µs against 27.1).
 constexpr int kHeadVec = kMaxLnDim / 256;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -850,7 +852,7 @@ struct Engine {
         return a;
     }
 
-    // Workgroups of head_kernel: 2 per CU, fewer when the vocabulary has fewer row pairs than
+    // Workgroups of head_kernel: 4 per CU, fewer when the vocabulary has fewer row pairs than
     // that grid has waves.
     int64_t head_groups() const {
         const int64_t waves = (cfg.vocab_size + 1) / 2;
