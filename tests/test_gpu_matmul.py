@@ -149,3 +149,53 @@ def test_batched_whole_tiles_with_split_k(kdb, batches, m, k, n):
     da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((batches, m, n), np.float32)
     kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n))
     close(dc.numpy(), reference_product(a, b))
+
+
+def random_operand_strides(rng, batches, rows, cols, allow_broadcast):
+    """Element strides (batch, row, col) of a random layout for a [batches, rows, cols] operand:
+    row-major, column-major (a transposed view), stepped rows and columns, and, for inputs, a
+    batch stride of 0 (one matrix broadcast to every batch). Returns (strides, storage length)."""
+    kind = rng.integers(0, 4)
+    step_r, step_c = (int(rng.integers(1, 3)), int(rng.integers(1, 3))) if kind == 2 else (1, 1)
+    if kind == 1:  # column-major matrices
+        st = [rows * cols, 1, rows]
+    else:
+        st = [rows * cols * step_r * step_c, cols * step_c * step_r, step_c]
+    if allow_broadcast and batches > 1 and rng.random() < 0.3:
+        st[0] = 0
+    extent = 1 + (batches - 1) * st[0] + (rows - 1) * st[1] + (cols - 1) * st[2]
+    return tuple(st), extent
+
+
+DIMS = [1, 2, 3, 7, 16, 33, 64, 100, 128, 130, 257]
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64], ids=["f32", "f64"])
+@pytest.mark.parametrize("block", range(4))
+def test_random_strided_products(kdb, oracle, dtype, block):
+    """60 seeded random products per dtype: sizes from 1 to 257 (whole and ragged tiles,
+    skinny and row-dot shapes), every operand in a random layout, batch broadcast of either
+    input, row- or column-major output; against the oracle's double-accumulated product."""
+    npd = kd.NUMPY_DTYPE[dtype]
+    for seed in range(block * 15, (block + 1) * 15):
+        rng = np.random.default_rng(seed)
+        batches = int(rng.integers(1, 4))
+        m, k, n = (DIMS[int(rng.integers(0, len(DIMS)))] for _ in range(3))
+        sa, la = random_operand_strides(rng, batches, m, k, True)
+        sb, lb = random_operand_strides(rng, batches, k, n, True)
+        so = (m * n, n, 1) if rng.random() < 0.7 else (m * n, 1, m)
+        a_store = rng.uniform(-1, 1, la).astype(npd)
+        b_store = rng.uniform(-1, 1, lb).astype(npd)
+        strides = kd.MatmulStrides()
+        for i in range(3):
+            strides.a[i], strides.b[i], strides.out[i] = sa[i], sb[i], so[i]
+        sizes = kd.MatmulSizes(batches, m, k, n)
+        want = np.zeros(batches * m * n, npd)
+        assert oracle.oracle_matmul_strided(dtype, support.ptr(a_store), support.ptr(b_store), support.ptr(want),
+                                            sizes, strides) == 0
+        da, db, dc = kdb.to_device(a_store), kdb.to_device(b_store), kdb.empty((batches * m * n,), npd)
+        kdb.call("matmul_strided", dtype, da.ptr, db.ptr, dc.ptr, sizes, strides)
+        try:
+            close(dc.numpy(), want.astype(np.float64))
+        except AssertionError as e:
+            raise AssertionError(f"seed {seed}: {batches}x{m}x{k}x{n} a{sa} b{sb} out{so}: {e}") from None
