@@ -307,13 +307,17 @@ void kd_gpt_destroy(void* handle);
 /* Uploads one parameter by its kael name (GPT::named_parameters(), e.g. "blocks.3.attn.qkv.weight")
  * from host f32 data holding all `count` elements in kael's row-major layout. */
 int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int64_t count);
-/* Runs the prompt (positions 0..length-1) through the model, filling the KV cache; the last
- * position's greedy token becomes the first generated token. Clears any previous sequence. By
- * default all positions pass each layer together (GEMMs on the matrix cores, causal attention);
- * KD_GPT_STEPWISE_PREFILL runs them as cached single-token steps. */
+/* Runs the prompt through the model from position 0 with an empty KV cache; the last position's
+ * greedy token becomes the first generated token. Clears any previous sequence. A prompt longer
+ * than max_positions runs its last max_positions tokens, as nn::generate does (reference
+ * src/nn/transformer.cpp:270-284). By default all positions pass each layer together (GEMMs on
+ * the matrix cores, causal attention); KD_GPT_STEPWISE_PREFILL runs them as cached single-token
+ * steps. */
 int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length);
-/* Generates `count` more tokens greedily, one cached step each (decode). `tokens` (host, may be
- * NULL) receives the `count` new ids. The total sequence may not exceed max_positions + 1. */
+/* Generates `count` more tokens greedily (reference nn::generate with use_cache, temperature 0):
+ * one cached step each while the KV cache has room; once it holds max_positions positions, each
+ * token clears it and reruns the sequence's last max_positions tokens from position 0, as
+ * nn::generate does. `tokens` (host, may be NULL) receives the `count` new ids. */
 int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens);
 /* Teacher-forced cached forward over `count` tokens starting at position 0; writes the logits
  * of every position (count x vocab, host). Used for step-by-step parity. */

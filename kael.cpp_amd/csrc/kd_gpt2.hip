@@ -827,7 +827,8 @@ struct Engine {
     int64_t* seq = nullptr;
     Step* st = nullptr;
     hipGraphExec_t graph = nullptr;
-    int64_t host_pos = 0;     // mirror of st->pos
+    int64_t host_pos = 0;     // mirror of st->pos: positions in the KV cache
+    std::vector<int64_t> history;  // the whole sequence so far (prompt + generated), host copy
     int64_t host_forced = 0;
     // batched prefill (allocated at the first prefill): activations of up to pf_rows positions
     // (max_positions rounded up to whole 128-row tiles) and the weights as [in, out] copies
@@ -1106,6 +1107,53 @@ struct Engine {
         return KD_OK;
     }
 
+    // Runs the last min(history, max_positions) tokens of the history from position 0 with an
+    // empty cache and appends the greedy token they produce: the prompt, and kael's cache refill
+    // once the sequence has outgrown the context (reference src/nn/transformer.cpp:270-284:
+    // with a full cache every step clears it and reruns the window).
+    int run_window() {
+        const int64_t n = static_cast<int64_t>(history.size());
+        const int64_t window = std::min(n, cfg.max_positions);
+        KD_HIP(hipMemcpyAsync(seq, history.data() + (n - window), static_cast<size_t>(window) * sizeof(int64_t),
+                              hipMemcpyHostToDevice, stream));
+        if (stepwise_prefill()) {
+            if (int rc = set_state(0, window)) return rc;
+            if (int rc = steps(window)) return rc;
+        } else {
+            // the pick after the batched layers runs as the step of position window - 1
+            if (int rc = set_state(window - 1, window)) return rc;
+            if (int rc = batched_prefill(window)) return rc;
+        }
+        int64_t next = 0;
+        KD_HIP(hipMemcpyAsync(&next, seq + window, sizeof next, hipMemcpyDeviceToHost, stream));
+        KD_HIP(hipStreamSynchronize(stream));
+        history.push_back(next);
+        return KD_OK;
+    }
+
+    // `count` greedy tokens: cached single-token steps while the cache has room, then one
+    // window rerun per token.
+    int generate(int64_t count) {
+        int64_t produced = 0;
+        while (produced < count) {
+            if (host_pos < cfg.max_positions) {
+                const int64_t n = std::min(count - produced, cfg.max_positions - host_pos);
+                const int64_t first = host_pos + 1;  // index in seq of the first token these steps produce
+                if (int rc = steps(n)) return rc;
+                const size_t old = history.size();
+                history.resize(old + static_cast<size_t>(n));
+                KD_HIP(hipMemcpyAsync(history.data() + old, seq + first, static_cast<size_t>(n) * sizeof(int64_t),
+                                      hipMemcpyDeviceToHost, stream));
+                KD_HIP(hipStreamSynchronize(stream));
+                produced += n;
+            } else {
+                if (int rc = run_window()) return rc;
+                ++produced;
+            }
+        }
+        return KD_OK;
+    }
+
     ~Engine() {
         if (graph) (void)hipGraphExecDestroy(graph);
         for (void* ptr : {static_cast<void*>(pf_x), static_cast<void*>(pf_h), static_cast<void*>(pf_q),
@@ -1232,31 +1280,20 @@ int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int
 int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length) {
     auto* e = static_cast<Engine*>(handle);
     if (e == nullptr || prompt == nullptr || length <= 0) return fail(KD_E_INVALID, "kd_gpt_prefill: bad arguments");
-    if (length > e->cfg.max_positions) return fail(KD_E_INVALID, "kd_gpt_prefill: prompt longer than max_positions");
     for (int64_t i = 0; i < length; ++i)
         if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab_size) return fail(KD_E_INVALID, "kd_gpt_prefill: token id out of range");
     if (int rc = e->ready()) return rc;
-    KD_HIP(hipMemcpyAsync(e->seq, prompt, static_cast<size_t>(length) * sizeof(int64_t), hipMemcpyHostToDevice, e->stream));
-    if (e->stepwise_prefill()) {
-        if (int rc = e->set_state(0, length)) return rc;
-        return e->steps(length);
-    }
-    // The pick after the batched layers runs as the step of position length - 1.
-    if (int rc = e->set_state(length - 1, length)) return rc;
-    return e->batched_prefill(length);
+    e->history.assign(prompt, prompt + length);
+    return e->run_window();
 }
 
 int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens) {
     auto* e = static_cast<Engine*>(handle);
     if (e == nullptr || count < 0) return fail(KD_E_INVALID, "kd_gpt_decode: bad arguments");
-    if (e->host_pos == 0) return fail(KD_E_INVALID, "kd_gpt_decode: call kd_gpt_prefill first");
-    const int64_t first = e->host_pos + 1;  // index in seq of the first token this call produces
-    if (int rc = e->steps(count)) return rc;
-    if (tokens != nullptr && count > 0) {
-        KD_HIP(hipMemcpyAsync(tokens, e->seq + first, static_cast<size_t>(count) * sizeof(int64_t), hipMemcpyDeviceToHost,
-                              e->stream));
-    }
-    KD_HIP(hipStreamSynchronize(e->stream));
+    if (e->history.empty()) return fail(KD_E_INVALID, "kd_gpt_decode: call kd_gpt_prefill first");
+    if (int rc = e->generate(count)) return rc;
+    if (tokens != nullptr && count > 0)
+        std::memcpy(tokens, e->history.data() + e->history.size() - count, static_cast<size_t>(count) * sizeof(int64_t));
     return KD_OK;
 }
 
@@ -1275,6 +1312,10 @@ int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, fl
         if (int rc = e->steps(1)) return rc;
         KD_HIP(hipMemcpyAsync(logits + t * v, e->logits, static_cast<size_t>(v) * sizeof(float), hipMemcpyDeviceToHost, e->stream));
     }
+    // the tokens, then the greedy token the last position produced
+    e->history.assign(tokens, tokens + count);
+    e->history.push_back(0);
+    KD_HIP(hipMemcpyAsync(&e->history.back(), e->seq + count, sizeof(int64_t), hipMemcpyDeviceToHost, e->stream));
     KD_HIP(hipStreamSynchronize(e->stream));
     return KD_OK;
 }
@@ -1282,19 +1323,17 @@ int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, fl
 int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* length) {
     auto* e = static_cast<Engine*>(handle);
     if (e == nullptr || length == nullptr) return fail(KD_E_INVALID, "kd_gpt_sequence: bad arguments");
-    KD_HIP(hipStreamSynchronize(e->stream));
-    const int64_t n = e->host_pos == 0 ? 0 : e->host_pos + 1;
+    const int64_t n = static_cast<int64_t>(e->history.size());
     *length = n;
-    if (ids != nullptr && capacity > 0 && n > 0) {
-        KD_HIP(hipMemcpy(ids, e->seq, static_cast<size_t>(std::min(n, capacity)) * sizeof(int64_t), hipMemcpyDeviceToHost));
-    }
+    if (ids != nullptr && capacity > 0 && n > 0)
+        std::memcpy(ids, e->history.data(), static_cast<size_t>(std::min(n, capacity)) * sizeof(int64_t));
     return KD_OK;
 }
 
 int kd_gpt_logits(void* handle, float* logits) {
     auto* e = static_cast<Engine*>(handle);
     if (e == nullptr || logits == nullptr) return fail(KD_E_INVALID, "kd_gpt_logits: bad arguments");
-    if (e->host_pos == 0) return fail(KD_E_INVALID, "kd_gpt_logits: no position has been run");
+    if (e->history.empty()) return fail(KD_E_INVALID, "kd_gpt_logits: no position has been run");
     KD_HIP(hipStreamSynchronize(e->stream));
     KD_HIP(hipMemcpy(logits, e->logits, static_cast<size_t>(e->cfg.vocab_size) * sizeof(float), hipMemcpyDeviceToHost));
     return KD_OK;

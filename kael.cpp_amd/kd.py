@@ -294,7 +294,8 @@ class Gpt:
 
     def sequence(self) -> np.ndarray:
         n = c_int64()
-        buf = np.zeros(self.config.max_positions + 1, np.int64)
+        self.b.check(self.b.lib.kd_gpt_sequence(self.handle, None, 0, ctypes.byref(n)), "kd_gpt_sequence")
+        buf = np.zeros(max(n.value, 1), np.int64)
         self.b.check(self.b.lib.kd_gpt_sequence(self.handle, buf.ctypes.data_as(c_void_p), buf.size, ctypes.byref(n)),
                      "kd_gpt_sequence")
         return buf[:n.value]

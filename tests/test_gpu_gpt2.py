@@ -173,3 +173,41 @@ def test_gpt2_small_batched_prefill(kdb, refdev):
 def test_odd_head_dim_is_rejected(kdb):
     with pytest.raises(kd.KdError):
         kd.Gpt(kdb, 11, 16, 1, 4, 24, True)  # head_dim 6
+
+
+@pytest.mark.parametrize("prompt_len", [10, 16, 23])
+def test_generation_past_the_context(kdb, refdev, prompt_len):
+    """Greedy generation that outgrows max_positions (16): once the KV cache is full, every token
+    clears it and reruns the last 16 tokens from position 0, as nn::generate does (reference
+    src/nn/transformer.cpp:270-284); a prompt longer than the context runs its last 16 tokens.
+    Tokens identical to kael's generate; the logits of each window rerun against kael's forward
+    over the same window (batched and stepwise prefill)."""
+    ref = refdev
+    h = ref.ref_gpt_create(11, 16, 2, 2, 8, 31, 1)
+    assert h, support.ref_error(ref)
+    try:
+        params = export_params(ref, h)
+        prompt = np.random.default_rng(100 + prompt_len).integers(0, 11, prompt_len)
+        new = 30
+        seq, _ = cpu_generate(ref, h, prompt, new)
+        for stepwise in (False, True):
+            g = kd.Gpt(kdb, 11, 16, 2, 2, 8, True, stepwise_prefill=stepwise)
+            for name, data in params:
+                g.load(name, data)
+            g.prefill(prompt)
+            got = [g.sequence()[-1]]
+            for _ in range(new - 1):
+                got.extend(g.decode(1))
+                total = len(prompt) + len(got) - 1  # tokens that went into the last forward
+                if total > 16:  # a window rerun: its last position's logits
+                    want = cpu_cached_logits(ref, h, seq[total - 16:total], 16, 11)[0]
+                    np.testing.assert_allclose(g.logits(), want, rtol=1e-5, atol=1e-5)
+            np.testing.assert_array_equal(np.array(got), seq[len(prompt):])
+            np.testing.assert_array_equal(g.sequence(), seq)
+        g = kd.Gpt(kdb, 11, 16, 2, 2, 8, True)  # the same in one decode call
+        for name, data in params:
+            g.load(name, data)
+        g.prefill(prompt)
+        np.testing.assert_array_equal(g.decode(new - 1), seq[len(prompt) + 1:])
+    finally:
+        ref.ref_gpt_destroy(h)
