@@ -974,8 +974,7 @@ struct Engine {
 
     int steps(int64_t count) {
         if (host_pos + count > cfg.max_positions)
-            return fail(KD_E_INVALID, "kd_gpt: the sequence would exceed max_positions (the cache-window refill of "
-                                      "nn::generate is not implemented)");
+            return fail(KD_E_INVALID, "kd_gpt: cached steps past max_positions");
         for (int64_t i = 0; i < count; ++i) {
             if (eager()) {
                 record_step(stream);
