@@ -35,9 +35,22 @@ hipStream_t stream();
 int device_ordinal();
 int compute_units();
 
-// Per-device workspace of at least `bytes` (grown on demand, never shrunk, freed at exit).
-// Stream-ordered reuse is safe because every launch goes to the one backend stream.
-int workspace(void** out, size_t bytes);
+// A lease on the per-device workspace (scratch for split reductions and split-K partials,
+// grown on demand, never shrunk). The lease holds the workspace lock from `workspace()` until
+// it is destroyed, so a caller keeps it alive until every kernel that touches `ptr` has been
+// enqueued: calls from several host threads then use the buffer one after another in stream
+// order, and a growth (which frees the old block) never frees a block that a caller is about to
+// hand to a kernel. When the backend stream differs from the one the previous lease used, the
+// previous stream is drained first, so leases on different streams never overlap either.
+struct Workspace {
+    Workspace() = default;
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    ~Workspace();
+    void* ptr = nullptr;
+    bool held = false;
+};
+int workspace(Workspace& lease, size_t bytes);
 
 inline int64_t dtype_size(int dtype) {
     switch (dtype) {

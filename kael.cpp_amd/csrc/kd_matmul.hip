@@ -707,14 +707,14 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                 while (splits > 1 && p.K % (splits * kBK) != 0) --splits;
             }
             if (splits > 1) {
-                void* ws = nullptr;
+                Workspace ws;  // held until split_sum_kernel is enqueued
                 const int64_t per = p.M * p.N;
-                if (int rc = workspace(&ws, static_cast<size_t>(splits * p.batches * per) * sizeof(float))) return rc;
+                if (int rc = workspace(ws, static_cast<size_t>(splits * p.batches * per) * sizeof(float))) return rc;
                 const int64_t kc = p.K / splits;
                 hipLaunchKernelGGL(mfma_f32_rowmajor_kernel,
                                    dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(p.batches),
                                         static_cast<uint32_t>(splits)),
-                                   dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws), static_cast<int>(p.M),
+                                   dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr), static_cast<int>(p.M),
                                    static_cast<int>(p.N), static_cast<int>(kc), static_cast<int>(p.sa.r),
                                    static_cast<int>(p.sb.r), static_cast<int>(p.N), p.sa.b, p.sb.b, splits * per, kc,
                                    kc * p.sb.r, per);
@@ -722,7 +722,7 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                 const int64_t total = p.batches * per;
                 const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{cus} * 16);
                 hipLaunchKernelGGL(split_sum_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream(),
-                                   static_cast<const float*>(ws), out, p, splits);
+                                   static_cast<const float*>(ws.ptr), out, p, splits);
                 KD_LAUNCH_CHECK();
                 return KD_OK;
             }
@@ -778,10 +778,10 @@ int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) 
         splits = (p.K + k_chunk - 1) / k_chunk;
         if (splits < 1) splits = 1;
         float* partial = nullptr;
+        Workspace ws;  // held (when split) until split_sum_kernel is enqueued
         if (splits > 1) {
-            void* ws = nullptr;
-            if (int rc = workspace(&ws, static_cast<size_t>(p.batches * splits * p.M * p.N) * sizeof(float))) return rc;
-            partial = static_cast<float*>(ws);
+            if (int rc = workspace(ws, static_cast<size_t>(p.batches * splits * p.M * p.N) * sizeof(float))) return rc;
+            partial = static_cast<float*>(ws.ptr);
         }
         if (p.batches > 65535 || splits > 65535) return fail(KD_E_INVALID, "kd_matmul: grid too large");
         const dim3 grid(static_cast<uint32_t>(col_blocks), static_cast<uint32_t>(splits), static_cast<uint32_t>(p.batches));

@@ -517,13 +517,13 @@ template <typename In> int cumsum_typed(void* out_v, const void* data_v, int64_t
     segment = (std::max<int64_t>(segment, 4 * kTile) + kTile - 1) / kTile * kTile;
     segments = (size + segment - 1) / segment;
     if (rows > 65535) return fail(KD_E_INVALID, "kd_cumsum: too many rows for the split path");
-    void* ws = nullptr;
-    if (int rc = workspace(&ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
+    Workspace ws;  // held until the scan that reads the segment totals is enqueued
+    if (int rc = workspace(ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
     const dim3 grid(static_cast<uint32_t>(segments), static_cast<uint32_t>(rows));
     hipLaunchKernelGGL((split_kernel<Combiner<KD_REDUCE_SUM, In>, In>), grid, dim3(kBlock), 0, stream(),
-                       static_cast<Acc*>(ws), data, size, segments, segment);
+                       static_cast<Acc*>(ws.ptr), data, size, segments, segment);
     KD_LAUNCH_CHECK();
-    launch(grid, static_cast<const Acc*>(ws), segments, segment);
+    launch(grid, static_cast<const Acc*>(ws.ptr), segments, segment);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }
@@ -567,13 +567,13 @@ template <typename C, typename In> int reduce_with(void* results, const void* da
     segment = (segment + 63) / 64 * 64;
     segments = (chunk + segment - 1) / segment;
     if (rows > 65535) return fail(KD_E_INVALID, "kd_reduce: too many rows for the split path");
-    void* ws = nullptr;
-    if (int rc = workspace(&ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
+    Workspace ws;  // held until combine_kernel is enqueued
+    if (int rc = workspace(ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
     hipLaunchKernelGGL((split_kernel<C, In>), dim3(static_cast<uint32_t>(segments), static_cast<uint32_t>(rows)),
-                       dim3(kBlock), 0, stream(), static_cast<Acc*>(ws), data, chunk, segments, segment);
+                       dim3(kBlock), 0, stream(), static_cast<Acc*>(ws.ptr), data, chunk, segments, segment);
     KD_LAUNCH_CHECK();
     hipLaunchKernelGGL((combine_kernel<C>), dim3(static_cast<uint32_t>(rows)), dim3(kBlock), 0, stream(), out,
-                       static_cast<const Acc*>(ws), segments);
+                       static_cast<const Acc*>(ws.ptr), segments);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }

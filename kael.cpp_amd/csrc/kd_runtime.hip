@@ -3,6 +3,7 @@
 // Replaces the runtime half of the reference backend (src/cuda/backend.cu:17-32, 73-105):
 // same synchronous-at-the-host copy semantics, but every operation is issued on one
 // in-order backend stream (the null stream unless kd_set_stream selects another).
+#include <atomic>
 #include <cstdio>
 #include <mutex>
 #include <string>
@@ -15,15 +16,19 @@ namespace kd {
 namespace {
 
 thread_local std::string g_error;
-hipStream_t g_stream = nullptr;
+std::atomic<hipStream_t> g_stream{nullptr};
 
 struct DeviceState {
-    int checked = 0;  // 0 = not probed, 1 = usable, -1 = unusable
+    std::atomic<int> checked{0};  // 0 = not probed, 1 = usable, -1 = unusable
     int ordinal = 0;
     int cus = 0;
     std::string arch;
+    // Workspace, guarded by g_workspace_mutex: the block, its size, and the stream the last
+    // lease enqueued its kernels on (valid once `workspace_used` is set).
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    hipStream_t workspace_stream = nullptr;
+    bool workspace_used = false;
 };
 
 DeviceState& state() {
@@ -32,6 +37,7 @@ DeviceState& state() {
 }
 
 std::mutex g_mutex;
+std::mutex g_workspace_mutex;
 
 } // namespace
 
@@ -79,17 +85,28 @@ int hip_fail(hipError_t status, const char* call, const char* file, int line) {
     return KD_E_RUNTIME;
 }
 
-hipStream_t stream() { return g_stream; }
+hipStream_t stream() { return g_stream.load(); }
 int device_ordinal() { return state().ordinal; }
 int compute_units() { return state().cus > 0 ? state().cus : 256; }
 
-int workspace(void** out, size_t bytes) {
+Workspace::~Workspace() {
+    if (held) g_workspace_mutex.unlock();
+}
+
+int workspace(Workspace& lease, size_t bytes) {
     DeviceState& s = state();
-    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!lease.held) {
+        g_workspace_mutex.lock();
+        lease.held = true;
+    }
+    const hipStream_t current = g_stream.load();
+    // The previous lease's kernels may still run on another stream: let them finish before this
+    // stream reuses (or this call frees) the block.
+    if (s.workspace_used && s.workspace_stream != current) KD_HIP(hipStreamSynchronize(s.workspace_stream));
     if (s.workspace_bytes < bytes) {
         if (s.workspace != nullptr) {
-            // The old block may still be read by queued kernels: drain before freeing.
-            KD_HIP(hipStreamSynchronize(g_stream));
+            // Kernels queued by earlier leases may still read the old block: drain before freeing.
+            KD_HIP(hipStreamSynchronize(current));
             KD_HIP(hipFree(s.workspace));
             s.workspace = nullptr;
             s.workspace_bytes = 0;
@@ -99,7 +116,9 @@ int workspace(void** out, size_t bytes) {
         KD_HIP(hipMalloc(&s.workspace, size));
         s.workspace_bytes = size;
     }
-    *out = s.workspace;
+    s.workspace_stream = current;
+    s.workspace_used = true;
+    lease.ptr = s.workspace;
     return KD_OK;
 }
 
@@ -115,16 +134,16 @@ int kd_available(void) { return ensure_device() == KD_OK ? 1 : 0; }
 
 int kd_synchronize(void) {
     if (int rc = ensure_device()) return rc;
-    KD_HIP(hipStreamSynchronize(g_stream));
+    KD_HIP(hipStreamSynchronize(g_stream.load()));
     return KD_OK;
 }
 
 int kd_set_stream(void* s) {
-    g_stream = static_cast<hipStream_t>(s);
+    g_stream.store(static_cast<hipStream_t>(s));
     return KD_OK;
 }
 
-void* kd_get_stream(void) { return g_stream; }
+void* kd_get_stream(void) { return g_stream.load(); }
 
 int kd_malloc(void** out, int64_t bytes) {
     if (out == nullptr || bytes < 0) return fail(KD_E_INVALID, "kd_malloc: bad arguments");
@@ -147,8 +166,8 @@ int kd_copy_h2d(void* target, const void* source, int64_t bytes) {
     if (bytes < 0) return fail(KD_E_INVALID, "kd_copy_h2d: negative size");
     if (bytes == 0) return KD_OK;
     if (int rc = ensure_device()) return rc;
-    KD_HIP(hipMemcpyAsync(target, source, static_cast<size_t>(bytes), hipMemcpyHostToDevice, g_stream));
-    KD_HIP(hipStreamSynchronize(g_stream));
+    KD_HIP(hipMemcpyAsync(target, source, static_cast<size_t>(bytes), hipMemcpyHostToDevice, stream()));
+    KD_HIP(hipStreamSynchronize(stream()));
     return KD_OK;
 }
 
@@ -156,8 +175,8 @@ int kd_copy_d2h(void* target, const void* source, int64_t bytes) {
     if (bytes < 0) return fail(KD_E_INVALID, "kd_copy_d2h: negative size");
     if (bytes == 0) return KD_OK;
     if (int rc = ensure_device()) return rc;
-    KD_HIP(hipMemcpyAsync(target, source, static_cast<size_t>(bytes), hipMemcpyDeviceToHost, g_stream));
-    KD_HIP(hipStreamSynchronize(g_stream));
+    KD_HIP(hipMemcpyAsync(target, source, static_cast<size_t>(bytes), hipMemcpyDeviceToHost, stream()));
+    KD_HIP(hipStreamSynchronize(stream()));
     return KD_OK;
 }
 
@@ -165,7 +184,7 @@ int kd_copy_d2d(void* target, const void* source, int64_t bytes) {
     if (bytes < 0) return fail(KD_E_INVALID, "kd_copy_d2d: negative size");
     if (bytes == 0) return KD_OK;
     if (int rc = ensure_device()) return rc;
-    KD_HIP(hipMemcpyAsync(target, source, static_cast<size_t>(bytes), hipMemcpyDeviceToDevice, g_stream));
+    KD_HIP(hipMemcpyAsync(target, source, static_cast<size_t>(bytes), hipMemcpyDeviceToDevice, stream()));
     return KD_OK;
 }
 
@@ -183,7 +202,7 @@ int kd_event_destroy(void* event) {
 }
 
 int kd_event_record(void* event) {
-    KD_HIP(hipEventRecord(static_cast<hipEvent_t>(event), g_stream));
+    KD_HIP(hipEventRecord(static_cast<hipEvent_t>(event), stream()));
     return KD_OK;
 }
 
