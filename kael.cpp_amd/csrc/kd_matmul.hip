@@ -484,6 +484,123 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_rowmajor_kernel(const float
         }
 }
 
+// A read through a transposed view (M contiguous: the weight gradient X^T . g of a Linear layer,
+// reference src/autograd/functions_linalg.cpp:44) with row-major B, whole tiles and 32-bit
+// offsets. The generic kColVec loader stores each 16-byte load of A as four scalars down a
+// column of the [m][k] LDS tile (20-float row stride: 8-way bank conflicts); here waves 0-1 load
+// A as 4(k) x 4(m) blocks - four 16-byte loads along M at four consecutive k, coalesced across
+// lanes - and write each block transposed as four 16-byte [m][k] rows, while waves 2-3 load the
+// B tile as four 16-byte rows each. LDS layout, MFMA order and results are those of
+// mfma_f32_rowmajor_kernel. `lda` is the distance between consecutive k of A (its column
+// stride), `ldb` and `ldo` the row strides of B and the output.
+__global__ __launch_bounds__(kThreads) void mfma_f32_at_kernel(const float* __restrict__ a,
+                                                               const float* __restrict__ b, float* __restrict__ out,
+                                                               int M, int N, int K, int lda, int ldb, int ldo,
+                                                               int64_t batch_a, int64_t batch_b, int64_t batch_o) {
+    __shared__ float As[2][kAsize];
+    __shared__ float Bs[2][kBsize];
+    const int tiles_m = M / kBM;
+    const int tiles_n = N / kBN;
+    int64_t tm64, tn64;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm64, tn64);
+    const int m0 = static_cast<int>(tm64) * kBM;
+    const int n0 = static_cast<int>(tn64) * kBN;
+    a += blockIdx.y * batch_a;
+    b += blockIdx.y * batch_b;
+    out += blockIdx.y * batch_o;
+
+    const int t = threadIdx.x;
+    const int lane = t % 64;
+    const int wave = t / 64;
+    const int wm = wave / 2;
+    const int wn = wave % 2;
+    const int li = lane % 32;
+    const int lh = lane / 32;
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    // Waves 0-1 (u = t): A rows m0 + 4*(u%32) .. +3 at k = 4*(u/32) + j. Waves 2-3 (u = t - 128):
+    // B rows k = 4*(u/32) + j, columns n0 + 4*(u%32) .. +3. j = 0..3 in both.
+    const bool loads_a = t < kThreads / 2;
+    const int u = loads_a ? t : t - kThreads / 2;
+    const int q = u / 32;
+    const int c4 = 4 * (u % 32);
+    const int g_off = loads_a ? 4 * q * lda + m0 + c4 : 4 * q * ldb + n0 + c4;
+    const int g_row = loads_a ? lda : ldb;
+    const int g_step = kBK * g_row;
+    const float* src = loads_a ? a : b;
+    f4 r[4];
+    const auto fetch = [&](int ks) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const f4*>(src + g_off + ks * g_step + j * g_row);
+    };
+    const auto stash = [&](int buf) {
+        if (loads_a) {
+            // r[j][e] = A[m0 + c4 + e][4q + j]: row c4 + e of the [m][k] tile, columns 4q .. 4q+3.
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<f4*>(&As[buf][(c4 + e) * kAld + 4 * q]) = f4{r[0][e], r[1][e], r[2][e], r[3][e]};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(&Bs[buf][(4 * q + j) * kBld + c4]) = r[j];
+        }
+    };
+    fetch(0);
+    stash(0);
+    __syncthreads();
+
+    const int ksteps = K / kBK;
+    for (int ks = 0; ks < ksteps; ++ks) {
+        const int cur = ks & 1;
+        const bool more = ks + 1 < ksteps;
+        if (more) fetch(ks + 1);
+        const float* as = As[cur];
+        const float* bs = Bs[cur];
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int kg = 0; kg < kBK; kg += 8) {
+            f4 af[2];
+            float bf[2][4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = *reinterpret_cast<const f4*>(as + (wm * 64 + i * 32 + li) * kAld + kg + 4 * lh);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4) bf[j][s4] = bs[(kg + 4 * lh + s4) * kBld + wn * 64 + j * 32 + li];
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s4], bf[j][s4], acc[i][j], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        if (more) stash(cur ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn * 64 + j * 32 + li;
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const int row = m0 + wm * 64 + i * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
+                out[row * ldo + col] = acc[i][j][rr];
+            }
+        }
+}
+
 // ---- small family (f32, few output tiles) -----------------------------------------------------
 
 constexpr int kSmallTile = 32;
@@ -816,6 +933,17 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                                static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
                                static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r), p.sa.b,
                                p.sb.b, p.so.b, int64_t{0}, int64_t{0}, int64_t{0});
+            KD_LAUNCH_CHECK();
+            return KD_OK;
+        }
+    }
+    if constexpr (AMode == kColVec && BMode == kRowVec) {
+        constexpr int64_t kMax = int64_t{1} << 31;
+        const bool fits = p.K * p.sa.c + p.M < kMax && p.K * p.sb.r + p.N < kMax && p.M * p.so.r + p.N < kMax;
+        if (fits && p.so.c == 1 && p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0) {
+            hipLaunchKernelGGL(mfma_f32_at_kernel, grid, dim3(kThreads), 0, stream(), a, b, out, static_cast<int>(p.M),
+                               static_cast<int>(p.N), static_cast<int>(p.K), static_cast<int>(p.sa.c),
+                               static_cast<int>(p.sb.r), static_cast<int>(p.so.r), p.sa.b, p.sb.b, p.so.b);
             KD_LAUNCH_CHECK();
             return KD_OK;
         }

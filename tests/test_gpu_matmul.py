@@ -113,6 +113,48 @@ def test_strided_operands(kdb, oracle, case):
     close(dc.numpy(), want.astype(np.float64))
 
 
+def _strided_product(kdb, a_store, b_store, batches, m, k, n, sa, sb):
+    strides = kd.MatmulStrides()
+    so = (m * n, n, 1)
+    for i in range(3):
+        strides.a[i], strides.b[i], strides.out[i] = sa[i], sb[i], so[i]
+    da, db, dc = kdb.to_device(a_store), kdb.to_device(b_store), kdb.empty((batches, m, n), np.float32)
+    kdb.call("matmul_strided", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n), strides)
+    return dc.numpy()
+
+
+def test_transposed_a_whole_tiles_equals_row_major(kdb):
+    """A read in place through a transposed view, whole 128x128 tiles and enough of them to
+    skip the small-product path (3 x 1024x256x1024): the product runs on the kernel that loads
+    A as 4x4 blocks and writes them transposed into the same [m][k] LDS tile the row-major
+    kernel fills, with the same MFMA order, so it must equal bit for bit the row-major product
+    of the materialized A (reference src/autograd/functions_linalg.cpp:44 computes X^T . g)."""
+    batches, m, k, n = 3, 1024, 256, 1024
+    rng = np.random.default_rng(44)
+    a_t = rng.uniform(-1, 1, (batches, k, m)).astype(np.float32)   # A[b] = a_t[b].T
+    b = rng.uniform(-1, 1, (batches, k, n)).astype(np.float32)
+    got = _strided_product(kdb, a_t, b, batches, m, k, n, (k * m, 1, m), (k * n, n, 1))
+    a = np.ascontiguousarray(np.transpose(a_t, (0, 2, 1)))
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((batches, m, n), np.float32)
+    kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n))
+    np.testing.assert_array_equal(got, dc.numpy())
+    close(got, np.matmul(a.astype(np.float64), b.astype(np.float64)))
+
+
+def test_weight_gradient_shape_of_c4(kdb):
+    """C4's Linear weight gradient X^T . g with X [4096 tokens, 256] and g [4096, 768] read in
+    place (M 256, K 4096, N 768: whole tiles, K too long for the small-product path). At K = 4096
+    an element's f32 error scales with its sum of |a||b|, so the check is the GPT-2 logits rule:
+    within 1e-4 of the largest |element| of the float64 product."""
+    m, k, n = 256, 4096, 768
+    rng = np.random.default_rng(45)
+    x = rng.uniform(-1, 1, (k, m)).astype(np.float32)
+    g = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    got = _strided_product(kdb, x, g, 1, m, k, n, (0, 1, m), (0, n, 1))[0]
+    want = np.matmul(x.T.astype(np.float64), g.astype(np.float64))
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+
+
 def test_headline_4096_cubed(kdb, refdev):
     """The benchmark's headline product (row-major MFMA kernel, whole tiles) at its full size,
     inputs as bench.py draws them. At K = 4096 an element's f32 rounding error scales with its
