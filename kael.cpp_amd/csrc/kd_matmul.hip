@@ -484,19 +484,25 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_rowmajor_kernel(const float
         }
 }
 
-// A read through a transposed view (M contiguous: the weight gradient X^T . g of a Linear layer,
-// reference src/autograd/functions_linalg.cpp:44) with row-major B, whole tiles and 32-bit
-// offsets. The generic kColVec loader stores each 16-byte load of A as four scalars down a
-// column of the [m][k] LDS tile (20-float row stride: 8-way bank conflicts); here waves 0-1 load
-// A as 4(k) x 4(m) blocks - four 16-byte loads along M at four consecutive k, coalesced across
-// lanes - and write each block transposed as four 16-byte [m][k] rows, while waves 2-3 load the
-// B tile as four 16-byte rows each. LDS layout, MFMA order and results are those of
-// mfma_f32_rowmajor_kernel. `lda` is the distance between consecutive k of A (its column
-// stride), `ldb` and `ldo` the row strides of B and the output.
-__global__ __launch_bounds__(kThreads) void mfma_f32_at_kernel(const float* __restrict__ a,
-                                                               const float* __restrict__ b, float* __restrict__ out,
-                                                               int M, int N, int K, int lda, int ldb, int ldo,
-                                                               int64_t batch_a, int64_t batch_b, int64_t batch_o) {
+// Whole-tile products with A and/or B read through a transposed view, 32-bit offsets: A
+// M-contiguous (AT: the weight gradient X^T . g of a Linear layer, reference
+// src/autograd/functions_linalg.cpp:44) and/or B K-contiguous (BT: the forward x . W^T,
+// src/nn/layers.cpp:43). The general kernel's transposed loaders store each 16-byte load as four
+// scalars down an LDS column (8-way bank conflicts for A). Here waves 0-1 load the A tile and
+// waves 2-3 the B tile, four 16-byte loads per thread: a transposed operand as a 4 x 4 block
+// (four consecutive rows of its contiguous dim, coalesced across lanes) that the thread writes
+// transposed as four 16-byte rows of the [m][k] / [k][n] LDS tile; a row-major operand as four
+// 16-byte rows. With AT the A tile's 16-byte column groups are XOR-swizzled by (row / 16) % 4,
+// which makes those transposed writes conflict-free; the MFMA reads apply the same swizzle. MFMA
+// order and results are those of mfma_f32_rowmajor_kernel (bit for bit). `lda` / `ldb` / `ldo`
+// are the strides between consecutive rows of the stored operands: of A's k (AT) or m rows, of
+// B's n (BT) or k rows, of the output's m rows.
+template <bool AT, bool BT>
+__global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* __restrict__ a,
+                                                                  const float* __restrict__ b,
+                                                                  float* __restrict__ out, int M, int N, int K,
+                                                                  int lda, int ldb, int ldo, int64_t batch_a,
+                                                                  int64_t batch_b, int64_t batch_o) {
     __shared__ float As[2][kAsize];
     __shared__ float Bs[2][kBsize];
     const int tiles_m = M / kBM;
@@ -526,15 +532,30 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_at_kernel(const float* __re
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     typedef float f4 __attribute__((ext_vector_type(4)));
-    // Waves 0-1 (u = t): A rows m0 + 4*(u%32) .. +3 at k = 4*(u/32) + j. Waves 2-3 (u = t - 128):
-    // B rows k = 4*(u/32) + j, columns n0 + 4*(u%32) .. +3. j = 0..3 in both.
+    // Column (in floats) of 16-byte group `c4` of A tile row `row` after the swizzle.
+    const auto aswz = [](int row, int c4) { return AT ? c4 ^ (4 * ((row / 16) % 4)) : c4; };
     const bool loads_a = t < kThreads / 2;
     const int u = loads_a ? t : t - kThreads / 2;
-    const int q = u / 32;
-    const int c4 = 4 * (u % 32);
-    const int g_off = loads_a ? 4 * q * lda + m0 + c4 : 4 * q * ldb + n0 + c4;
-    const int g_row = loads_a ? lda : ldb;
-    const int g_step = kBK * g_row;
+    // Per-thread source offset (element) of load j = 0..3 at K step 0, and the step per load j.
+    int g_off, g_row;
+    if (loads_a) {
+        if (AT) {  // A^T rows k = 4*(u/32) + j, columns m0 + 4*(u%32) .. +3
+            g_off = 4 * (u / 32) * lda + m0 + 4 * (u % 32);
+            g_row = lda;
+        } else {   // A rows m0 + u/4 + 32*j, columns k = 4*(u%4) .. +3
+            g_off = (m0 + u / 4) * lda + 4 * (u % 4);
+            g_row = 32 * lda;
+        }
+    } else {
+        if (BT) {  // B^T rows n0 + 4*(u/4) + j, columns k = 4*(u%4) .. +3
+            g_off = (n0 + 4 * (u / 4)) * ldb + 4 * (u % 4);
+            g_row = ldb;
+        } else {   // B rows k = 4*(u/32) + j, columns n0 + 4*(u%32) .. +3
+            g_off = 4 * (u / 32) * ldb + n0 + 4 * (u % 32);
+            g_row = ldb;
+        }
+    }
+    const int g_step = loads_a ? (AT ? kBK * lda : kBK) : (BT ? kBK : kBK * ldb);
     const float* src = loads_a ? a : b;
     f4 r[4];
     const auto fetch = [&](int ks) {
@@ -543,15 +564,39 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_at_kernel(const float* __re
     };
     const auto stash = [&](int buf) {
         if (loads_a) {
-            // r[j][e] = A[m0 + c4 + e][4q + j]: row c4 + e of the [m][k] tile, columns 4q .. 4q+3.
+            if (AT) {
+                // r[j][e] = A[m0 + 4*(u%32) + e][4*(u/32) + j]
+                const int c4 = 4 * (u / 32);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                *reinterpret_cast<f4*>(&As[buf][(c4 + e) * kAld + 4 * q]) = f4{r[0][e], r[1][e], r[2][e], r[3][e]};
+                for (int e = 0; e < 4; ++e) {
+                    const int row = 4 * (u % 32) + e;
+                    *reinterpret_cast<f4*>(&As[buf][row * kAld + aswz(row, c4)]) = f4{r[0][e], r[1][e], r[2][e], r[3][e]};
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(&As[buf][(u / 4 + 32 * j) * kAld + 4 * (u % 4)]) = r[j];
+            }
         } else {
+            if (BT) {
+                // r[j][e] = B[4*(u%4) + e][n0 + 4*(u/4) + j]
 #pragma unroll
-            for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(&Bs[buf][(4 * q + j) * kBld + c4]) = r[j];
+                for (int e = 0; e < 4; ++e)
+                    *reinterpret_cast<f4*>(&Bs[buf][(4 * (u % 4) + e) * kBld + 4 * (u / 4)]) = f4{r[0][e], r[1][e], r[2][e], r[3][e]};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(&Bs[buf][(4 * (u / 32) + j) * kBld + 4 * (u % 32)]) = r[j];
+            }
         }
     };
+    // This lane's A tile reads (rows wm*64 + i*32 + li, 16-byte groups kg + 4*lh) as LDS offsets.
+    int a_rd[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = wm * 64 + i * 32 + li;
+            a_rd[i][h] = row * kAld + aswz(row, 8 * h + 4 * lh);
+        }
     fetch(0);
     stash(0);
     __syncthreads();
@@ -569,8 +614,7 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_at_kernel(const float* __re
             f4 af[2];
             float bf[2][4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const f4*>(as + (wm * 64 + i * 32 + li) * kAld + kg + 4 * lh);
+            for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const f4*>(as + a_rd[i][kg / 8]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -937,13 +981,21 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             return KD_OK;
         }
     }
-    if constexpr (AMode == kColVec && BMode == kRowVec) {
+    if constexpr ((AMode == kColVec || BMode == kColVec) && AMode != kGeneric && BMode != kGeneric) {
+        // A transposed and/or B transposed, whole tiles, 32-bit offsets: the conflict-free loaders.
+        constexpr bool at = AMode == kColVec;
+        constexpr bool bt = BMode == kColVec;
         constexpr int64_t kMax = int64_t{1} << 31;
-        const bool fits = p.K * p.sa.c + p.M < kMax && p.K * p.sb.r + p.N < kMax && p.M * p.so.r + p.N < kMax;
-        if (fits && p.so.c == 1 && p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0) {
-            hipLaunchKernelGGL(mfma_f32_at_kernel, grid, dim3(kThreads), 0, stream(), a, b, out, static_cast<int>(p.M),
-                               static_cast<int>(p.N), static_cast<int>(p.K), static_cast<int>(p.sa.c),
-                               static_cast<int>(p.sb.r), static_cast<int>(p.so.r), p.sa.b, p.sb.b, p.so.b);
+        const int64_t lda = at ? p.sa.c : p.sa.r;
+        const int64_t ldb = bt ? p.sb.c : p.sb.r;
+        const int64_t a_extent = at ? p.K * lda + p.M : p.M * lda + p.K;
+        const int64_t b_extent = bt ? p.N * ldb + p.K : p.K * ldb + p.N;
+        if (a_extent < kMax && b_extent < kMax && p.M * p.so.r + p.N < kMax && p.so.c == 1 && p.M % kBM == 0 &&
+            p.N % kBN == 0 && p.K % kBK == 0) {
+            hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>), grid, dim3(kThreads), 0, stream(), a, b, out,
+                               static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
+                               static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r), p.sa.b, p.sb.b,
+                               p.so.b);
             KD_LAUNCH_CHECK();
             return KD_OK;
         }

@@ -123,18 +123,23 @@ def _strided_product(kdb, a_store, b_store, batches, m, k, n, sa, sb):
     return dc.numpy()
 
 
-def test_transposed_a_whole_tiles_equals_row_major(kdb):
-    """A read in place through a transposed view, whole 128x128 tiles and enough of them to
-    skip the small-product path (3 x 1024x256x1024): the product runs on the kernel that loads
-    A as 4x4 blocks and writes them transposed into the same [m][k] LDS tile the row-major
-    kernel fills, with the same MFMA order, so it must equal bit for bit the row-major product
-    of the materialized A (reference src/autograd/functions_linalg.cpp:44 computes X^T . g)."""
+@pytest.mark.parametrize("a_t,b_t", [(True, False), (False, True), (True, True)], ids=["aT", "bT", "both"])
+def test_transposed_whole_tiles_equal_row_major(kdb, a_t, b_t):
+    """A and/or B read in place through transposed views, whole 128x128 tiles and enough of them
+    to skip the small-product path (3 x 1024x256x1024): the product runs on the kernel that loads
+    a transposed operand as 4x4 blocks and writes them transposed into the same LDS tiles the
+    row-major kernel fills, with the same MFMA order, so it must equal bit for bit the row-major
+    product of the materialized operands (reference src/autograd/functions_linalg.cpp:37,44 and
+    src/nn/layers.cpp:43 issue X^T . g and x . W^T)."""
     batches, m, k, n = 3, 1024, 256, 1024
-    rng = np.random.default_rng(44)
-    a_t = rng.uniform(-1, 1, (batches, k, m)).astype(np.float32)   # A[b] = a_t[b].T
+    rng = np.random.default_rng(44 + 2 * a_t + b_t)
+    a = rng.uniform(-1, 1, (batches, m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, (batches, k, n)).astype(np.float32)
-    got = _strided_product(kdb, a_t, b, batches, m, k, n, (k * m, 1, m), (k * n, n, 1))
-    a = np.ascontiguousarray(np.transpose(a_t, (0, 2, 1)))
+    a_store = np.ascontiguousarray(np.transpose(a, (0, 2, 1))) if a_t else a
+    b_store = np.ascontiguousarray(np.transpose(b, (0, 2, 1))) if b_t else b
+    sa = (k * m, 1, m) if a_t else (m * k, k, 1)
+    sb = (k * n, 1, k) if b_t else (k * n, n, 1)
+    got = _strided_product(kdb, a_store, b_store, batches, m, k, n, sa, sb)
     da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((batches, m, n), np.float32)
     kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n))
     np.testing.assert_array_equal(got, dc.numpy())
