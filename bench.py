@@ -13,7 +13,7 @@ whose steps take microseconds, warm up for at least MIN_WARMUP_S of steps.
 The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference sources,
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only matmul]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only matmul|c1|c2|rows|gpt2|copy]
 """
 from __future__ import annotations
 
@@ -306,7 +306,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
-    ap.add_argument("--only", default="", choices=["", "all", "matmul", "copy", "c2", "rows", "gpt2"],
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "copy", "c2", "rows", "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -325,6 +325,10 @@ def main() -> int:
     if args.only == "gpt2":
         extra["gpt2_decode"] = bench_gpt2(backend, eager=args.gpt_eager)
         print(json.dumps({"metric": "GPT-2-small decode tok/s", "extra": extra}))
+        return 0
+    if args.only == "c1":
+        extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
+        print(json.dumps({"metric": "C1 f32 matmul 512^3", "extra": extra}))
         return 0
     if args.only in ("c2", "rows"):
         extra[args.only] = (bench_c2 if args.only == "c2" else bench_rows)(backend, args.steps, args.warmup)
