@@ -5,7 +5,8 @@
 // that kael's build picks (reference CMakeLists.txt:26-36: src/cuda/backend.cu, backend_fake.cpp
 // or backend_none.cpp): compile this file with kael's include directory and link libkd.so.
 // Failures become kael::Error carrying the backend's message (as KAEL_CUDA_CHECK does in
-// reference src/cuda/backend.cu:17-32); release() never throws (backend.cu:88-90).
+// reference src/cuda/backend.cu:17-32); release() never throws (backend.cu:88-90). The fused
+// entry points of kd_kael_extensions.h are defined at the end.
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -14,6 +15,7 @@
 #include "kael/error.h"
 
 #include "kd_api.h"
+#include "kd_kael_extensions.h"
 
 namespace kael::device {
 
@@ -110,6 +112,44 @@ void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, cons
     check(kd_scatter_add(static_cast<int>(dtype), data, indices, source,
                          reinterpret_cast<const kd_index_layout*>(&layout)),
           "scatter_add");
+}
+
+// ---- extensions (kd_kael_extensions.h) ----------------------------------------------------
+
+void softmax_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols, bool log) {
+    check(kd_softmax_rows(static_cast<int>(dtype), out, in, rows, cols, log ? 1 : 0), "softmax_rows");
+}
+
+void standardize_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols,
+                      double eps) {
+    check(kd_standardize_rows(static_cast<int>(dtype), out, in, rows, cols, eps, nullptr, nullptr), "standardize_rows");
+}
+
+void cross_entropy_rows(DType dtype, std::byte* losses, const std::byte* logits, const std::int64_t* targets,
+                        std::int64_t rows, std::int64_t cols) {
+    check(kd_cross_entropy_rows(static_cast<int>(dtype), losses, logits, targets, rows, cols), "cross_entropy_rows");
+}
+
+void cross_entropy_grad(DType dtype, std::byte* out, const std::byte* logits, const std::int64_t* targets,
+                        const std::byte* row_weights, std::int64_t rows, std::int64_t cols) {
+    check(kd_cross_entropy_grad(static_cast<int>(dtype), out, logits, targets, row_weights, rows, cols),
+          "cross_entropy_grad");
+}
+
+ElementOp gelu_backward_op(bool approximate) {
+    return static_cast<ElementOp>(approximate ? KD_OP_GELU_TANH_BACKWARD : KD_OP_GELU_EXACT_BACKWARD);
+}
+
+void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
+                    const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides) {
+    const kd_matmul_sizes s{sizes.batches, sizes.rows, sizes.inner, sizes.columns};
+    kd_matmul_strides st;
+    for (int i = 0; i < 3; ++i) {
+        st.a[i] = a_strides[i];
+        st.b[i] = b_strides[i];
+        st.out[i] = out_strides[i];
+    }
+    check(kd_matmul_strided(static_cast<int>(dtype), a, b, out, &s, &st), "matmul_strided");
 }
 
 } // namespace kael::device

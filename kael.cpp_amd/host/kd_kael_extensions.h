@@ -1,0 +1,46 @@
+// kd_kael_extensions.h - kael::device functions that the MI355X backend adds to kael's device
+// interface (reference include/kael/device_kernels.h:96-116) for the fused paths: row softmax /
+// log-softmax, row standardization, cross-entropy losses and gradient, GELU backward as one
+// element op, and matmul over strided (transposed or batch-broadcast) operands.
+//
+// Defined in backend_hip.cpp. Unmodified kael never calls them; the device branches that do are
+// the optional kael patches listed in INTEGRATION.md (a one-line include of this header at the
+// end of kael/device_kernels.h, and a device branch at each site).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "kael/device_kernels.h"
+
+namespace kael::device {
+
+// Softmax (log = false) or log-softmax (log = true) of `rows` contiguous rows of `cols`
+// elements (reference src/ops/nn.cpp:60-84 row semantics).
+void softmax_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols,
+                  bool log);
+
+// (x - mean) / sqrt(var + eps) over `rows` contiguous rows of `cols` elements, mean and
+// population variance in double (reference src/ops/nn.cpp:114-129).
+void standardize_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols,
+                      double eps);
+
+// losses[r] = log(sum exp(x - max)) - (x[target[r]] - max) (reference src/ops/nn.cpp:105-112);
+// targets are device int64 in [0, cols).
+void cross_entropy_rows(DType dtype, std::byte* losses, const std::byte* logits, const std::int64_t* targets,
+                        std::int64_t rows, std::int64_t cols);
+
+// out = softmax(x) * w[r] with w[r] subtracted at the target (reference src/ops/nn.cpp:214-240).
+void cross_entropy_grad(DType dtype, std::byte* out, const std::byte* logits, const std::int64_t* targets,
+                        const std::byte* row_weights, std::int64_t rows, std::int64_t cols);
+
+// The element op computing grad * d/dx gelu(x) over operands (out, x, grad), tanh form when
+// `approximate` (reference src/autograd/functions_math.cpp:35-46 slopes).
+ElementOp gelu_backward_op(bool approximate);
+
+// out[b] = a[b] . b[b] with per-operand element strides {batch, row, column}; a batch stride of 0
+// broadcasts the operand (reference src/ops/linalg.cpp:56-76 without the operand copies).
+void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
+                    const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides);
+
+} // namespace kael::device

@@ -1,0 +1,192 @@
+"""Writes kael with the optional MI355X device branches into oracle/_ref/fused/ (test build only).
+
+TEST INFRASTRUCTURE: the reference's sources are read where they lie under /root/reference and
+the patched copies are written only to oracle/_ref/fused/ (git-ignored); nothing here ships.
+It applies the kael-side patches that INTEGRATION.md lists, so that the tests can run kael's
+training configs with kael's own host code calling the backend's fused entry points
+(kael.cpp_amd/host/kd_kael_extensions.h):
+
+  include/kael/device_kernels.h      + one include of kd_kael_extensions.h (the declarations)
+  src/ops/nn.cpp                     the device interface include; device branches of softmax and
+                                     log_softmax (reference :147-181), standardize (:244-271),
+                                     cross_entropy_losses (:183-210) and
+                                     detail::cross_entropy_gradient (:214-240)
+  src/autograd/functions_math.cpp    GELU backward without the host round trip (:221-231)
+  src/ops/linalg.cpp                 multiply_batches reads transposed / broadcast operands in
+                                     place (:56-76)
+
+Each edit is anchored on a line of the reference file that must occur exactly once; a missing
+or repeated anchor is an error, so a changed reference fails loudly instead of building
+something else. The inserted code is this repository's own.
+
+Usage: python oracle/kael_fused.py REF_DIR OUT_DIR
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+SOFTMAX_BRANCH = """        if (x.device() != Device::CPU && x.dim() > 0 && x.is_contiguous() &&
+            dim_position(dim, x.dim()) == static_cast<std::size_t>(x.dim() - 1)) {
+            // MI355X: one fused row kernel instead of max, sub, exp, sum and div launches.
+            Tensor out = empty(x.shape(), x.dtype(), x.device());
+            device::softmax_rows(x.dtype(), out.device_data(), x.device_data(), x.numel() / x.size(-1),
+                                 x.size(-1), %s);
+            return out;
+        }
+"""
+
+STANDARDIZE_BRANCH = """        if (x.device() != Device::CPU) {
+            // MI355X: one fused row kernel (mean and population variance in double).
+            const std::int64_t row_size =
+                numel(Shape(x.shape().end() - static_cast<std::ptrdiff_t>(normalized_dims), x.shape().end()));
+            Tensor out = empty(x.shape(), x.dtype(), x.device());
+            device::standardize_rows(x.dtype(), out.device_data(), x.device_data(), x.numel() / row_size, row_size,
+                                     eps);
+            return out;
+        }
+"""
+
+CROSS_ENTROPY_BRANCH = """    if (logits.device() != Device::CPU) {
+        // MI355X: per-row losses in one kernel; the backward is detail::cross_entropy_gradient.
+        Tensor out = autograd::without_grad([&] {
+            const Tensor x = as_floating(logits).contiguous();
+            const Tensor classes = targets.contiguous();
+            Tensor losses = empty({x.size(0)}, x.dtype(), x.device());
+            if (x.numel() > 0) {
+                device::cross_entropy_rows(x.dtype(), losses.device_data(), x.device_data(),
+                                           reinterpret_cast<const std::int64_t*>(classes.device_data()),
+                                           x.size(0), x.size(1));
+            }
+            return losses;
+        });
+        autograd::record_cross_entropy(out, logits, targets);
+        return out;
+    }
+"""
+
+CROSS_ENTROPY_GRAD_BRANCH = """    if (x.device() != Device::CPU) {
+        // MI355X: softmax(x) * w[row] - w[row] * onehot(target) in one kernel.
+        Tensor out = empty(x.shape(), x.dtype(), x.device());
+        if (x.numel() > 0) {
+            device::cross_entropy_grad(x.dtype(), out.device_data(), x.device_data(),
+                                       reinterpret_cast<const std::int64_t*>(classes.device_data()),
+                                       weights.to(x.dtype()).contiguous().device_data(), x.size(0), x.size(1));
+        }
+        return out;
+    }
+"""
+
+GELU_BACKWARD_BRANCH = """                          if (saved.get().device() != Device::CPU) {
+                              // MI355X: g * gelu'(x) as one element kernel, no host round trip.
+                              const NoGradGuard guard;
+                              const Tensor xs = saved.get();
+                              const DType dtype = is_floating_point(xs.dtype()) ? xs.dtype() : DType::F32;
+                              TensorIterator iterator;
+                              iterator.allocate_output(dtype).add_input(xs.to(dtype)).add_input(g.to(dtype)).build();
+                              device::elementwise(device::gelu_backward_op(approximate), dtype, dtype,
+                                                  iterator.device_layout(), {});
+                              return iterator.output();
+                          }
+"""
+
+STRIDES_HELPER = """// MI355X: element strides {batch, row, column} of an expanded operand whose batch dims flatten
+// to one stride (contiguous batch dims, or broadcast ones); false when they do not.
+bool flat_batch_strides(const Tensor& v, std::int64_t* strides) {
+    const std::int64_t d = v.dim();
+    strides[0] = 0;
+    strides[1] = v.stride(d - 2);
+    strides[2] = v.stride(d - 1);
+    bool first = true;
+    std::int64_t span = 0;
+    for (std::int64_t i = d - 3; i >= 0; --i) {
+        if (v.size(i) == 1) {
+            continue;
+        }
+        if (first) {
+            strides[0] = v.stride(i);
+            span = v.stride(i) * v.size(i);
+            first = false;
+        } else if (v.stride(i) == span) {
+            span *= v.size(i);
+        } else {
+            return false;
+        }
+    }
+    return true;
+}
+
+"""
+
+MATMUL_BRANCH = """    if (a.device() != Device::CPU && is_floating_point(dtype)) {
+        // MI355X: transposed and batch-broadcast operands read in place (no expand/reshape copies).
+        const Tensor va = a.to(dtype).expand(with_matrix_dims(batch, rows, inner));
+        const Tensor vb = b.to(dtype).expand(with_matrix_dims(batch, inner, columns));
+        std::int64_t sa[3];
+        std::int64_t sb[3];
+        if (flat_batch_strides(va, sa) && flat_batch_strides(vb, sb)) {
+            Tensor out = empty(with_matrix_dims(batch, rows, columns), dtype, a.device());
+            const std::int64_t so[3] = {rows * columns, columns, 1};
+            device::matmul_strided(dtype, va.device_data(), vb.device_data(), out.device_data(),
+                                   {numel(batch), rows, inner, columns}, sa, sb, so);
+            return out;
+        }
+    }
+"""
+
+# (relative path, anchor line(s), where, text). where: "before", "after", "replace", "append".
+EDITS = [
+    ("include/kael/device_kernels.h", None, "append", '\n#include "kd_kael_extensions.h"\n'),
+    ("src/ops/nn.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/ops/nn.cpp", "        const Tensor exponentials = exp(shifted_by_max(x, dim));\n", "before",
+     SOFTMAX_BRANCH % "false"),
+    ("src/ops/nn.cpp", "        const Tensor shifted = shifted_by_max(x, dim);\n", "before", SOFTMAX_BRANCH % "true"),
+    ("src/ops/nn.cpp", "        if (x.device() != Device::CPU) {\n            Dims dims;\n", "before", STANDARDIZE_BRANCH),
+    ("src/ops/nn.cpp",
+     "    if (logits.device() != Device::CPU) {\n"
+     "        return -gather(log_softmax(logits, 1), 1, targets.unsqueeze(1)).squeeze(1);\n    }\n",
+     "replace", CROSS_ENTROPY_BRANCH),
+    ("src/ops/nn.cpp", "    const Tensor weights = scale.contiguous();\n", "after", CROSS_ENTROPY_GRAD_BRANCH),
+    ("src/autograd/functions_math.cpp",
+     "                      [saved = SavedTensor(x), approximate](const Tensor& g) {\n", "after", GELU_BACKWARD_BRANCH),
+    ("src/ops/linalg.cpp", "Tensor multiply_batches(const Tensor& a, const Tensor& b, const Shape& batch,\n", "before",
+     STRIDES_HELPER),
+    ("src/ops/linalg.cpp", "    const Tensor flat_a = as_batch_of_matrices(a.to(dtype), batch, rows, inner);\n", "before",
+     MATMUL_BRANCH),
+]
+
+
+def apply(ref: Path, out: Path) -> list[Path]:
+    texts: dict[str, str] = {}
+    for rel, anchor, where, text in EDITS:
+        body = texts.get(rel)
+        if body is None:
+            body = (ref / rel).read_text()
+        if where == "append":
+            body = body + text
+        else:
+            count = body.count(anchor)
+            if count != 1:
+                raise SystemExit(f"{rel}: anchor found {count} times (expected 1): {anchor!r}")
+            if where == "before":
+                body = body.replace(anchor, text + anchor)
+            elif where == "after":
+                body = body.replace(anchor, anchor + text)
+            else:
+                body = body.replace(anchor, text)
+        texts[rel] = body
+    written = []
+    for rel, body in texts.items():
+        target = out / rel
+        target.parent.mkdir(parents=True, exist_ok=True)
+        if not target.is_file() or target.read_text() != body:
+            target.write_text(body)
+        written.append(target)
+    return written
+
+
+if __name__ == "__main__":
+    if len(sys.argv) != 3:
+        raise SystemExit(__doc__)
+    for path in apply(Path(sys.argv[1]), Path(sys.argv[2])):
+        print(path)

@@ -4,6 +4,7 @@
 // C restatement in kd_oracle.c, with host memory standing in for device memory. Linked with the
 // unmodified kael core it lets kael's own host code (TensorIterator, reductions planning,
 // autograd, nn) drive the oracle, so the reference's golden suite pins the restatement.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -11,6 +12,7 @@
 #include "kael/device_kernels.h"
 #include "kael/error.h"
 
+#include "kd_kael_extensions.h"
 #include "kd_oracle.h"
 
 namespace kael::device {
@@ -80,4 +82,61 @@ void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, cons
           "scatter_add");
 }
 
+// The fused entry points of kael.cpp_amd/host/kd_kael_extensions.h, over the same restatement.
+// Each call is counted so that tests can check that the patched kael branches ran.
+
+namespace {
+// 0 softmax_rows, 1 standardize_rows, 2 cross_entropy_rows, 3 cross_entropy_grad,
+// 4 gelu_backward_op, 5 matmul_strided.
+std::atomic<long long> g_extension_calls[6];
+} // namespace
+
+void softmax_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols, bool log) {
+    ++g_extension_calls[0];
+    check(oracle_softmax_rows(static_cast<int>(dtype), out, in, rows, cols, log ? 1 : 0), "softmax_rows");
+}
+
+void standardize_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols,
+                      double eps) {
+    ++g_extension_calls[1];
+    check(oracle_standardize_rows(static_cast<int>(dtype), out, in, rows, cols, eps, nullptr, nullptr),
+          "standardize_rows");
+}
+
+void cross_entropy_rows(DType dtype, std::byte* losses, const std::byte* logits, const std::int64_t* targets,
+                        std::int64_t rows, std::int64_t cols) {
+    ++g_extension_calls[2];
+    check(oracle_cross_entropy_rows(static_cast<int>(dtype), losses, logits, targets, rows, cols), "cross_entropy_rows");
+}
+
+void cross_entropy_grad(DType dtype, std::byte* out, const std::byte* logits, const std::int64_t* targets,
+                        const std::byte* row_weights, std::int64_t rows, std::int64_t cols) {
+    ++g_extension_calls[3];
+    check(oracle_cross_entropy_grad(static_cast<int>(dtype), out, logits, targets, row_weights, rows, cols),
+          "cross_entropy_grad");
+}
+
+ElementOp gelu_backward_op(bool approximate) {
+    ++g_extension_calls[4];
+    return static_cast<ElementOp>(approximate ? KD_OP_GELU_TANH_BACKWARD : KD_OP_GELU_EXACT_BACKWARD);
+}
+
+void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& s,
+                    const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides) {
+    ++g_extension_calls[5];
+    const kd_matmul_sizes sizes{s.batches, s.rows, s.inner, s.columns};
+    kd_matmul_strides st;
+    for (int i = 0; i < 3; ++i) {
+        st.a[i] = a_strides[i];
+        st.b[i] = b_strides[i];
+        st.out[i] = out_strides[i];
+    }
+    check(oracle_matmul_strided(static_cast<int>(dtype), a, b, out, &sizes, &st), "matmul_strided");
+}
+
 } // namespace kael::device
+
+// Test hook: how many times extension `which` (numbered as g_extension_calls) has run.
+extern "C" long long ref_extension_calls(int which) {
+    return which >= 0 && which < 6 ? kael::device::g_extension_calls[which].load() : -1;
+}

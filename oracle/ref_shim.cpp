@@ -646,28 +646,30 @@ int ref_train_mlp(int device, int64_t steps, float* losses, float* params_out, d
     });
 }
 
-// C4: char-GPT {vocab 96, context 128, 4 layers, 4 heads, dim 256} (tanh GELU), manual_seed(3)
-// for the N(0,0.02) init and ids = randint(0,96,{32,128}), targets = randint(0,96,{4096});
-// forward, cross-entropy, backward, Adam (defaults). Writes each step's loss and the seconds.
-int ref_train_chargpt(int device, int64_t steps, float* losses, double* seconds) {
+// A char-GPT (tanh GELU) of the given size, manual_seed(3) for the N(0,0.02) init and
+// ids = randint(0,vocab,{batch,context}), targets = randint(0,vocab,{batch*context}); forward,
+// cross-entropy, backward, Adam (defaults). Writes each step's loss and the seconds.
+// ref_train_chargpt is config C4: {vocab 96, context 128, 4 layers, 4 heads, dim 256}, batch 32.
+int ref_train_gpt(int device, int64_t steps, int64_t vocab, int64_t context, int64_t layers, int64_t heads,
+                  int64_t dimension, int64_t batch, float* losses, double* seconds) {
     return guarded([&] {
         const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
         kael::manual_seed(3);
         kael::nn::GptConfig config;
-        config.vocab_size = 96;
-        config.max_positions = 128;
-        config.layers = 4;
-        config.heads = 4;
-        config.dimension = 256;
+        config.vocab_size = vocab;
+        config.max_positions = context;
+        config.layers = layers;
+        config.heads = heads;
+        config.dimension = dimension;
         kael::nn::GPT model(config);
-        const kael::Tensor ids = kael::randint(0, 96, {32, 128}).to(dev);
-        const kael::Tensor targets = kael::randint(0, 96, {4096}).to(dev);
+        const kael::Tensor ids = kael::randint(0, vocab, {batch, context}).to(dev);
+        const kael::Tensor targets = kael::randint(0, vocab, {batch * context}).to(dev);
         model.to(dev);
         kael::optim::Adam optimizer(model.parameters());
         const auto t0 = std::chrono::steady_clock::now();
         for (int64_t step = 0; step < steps; ++step) {
             optimizer.zero_grad();
-            const kael::Tensor logits = model(ids).reshape({4096, 96});
+            const kael::Tensor logits = model(ids).reshape({batch * context, vocab});
             const kael::Tensor loss = kael::nn::cross_entropy(logits, targets);
             loss.backward();
             optimizer.step();
@@ -676,6 +678,10 @@ int ref_train_chargpt(int device, int64_t steps, float* losses, double* seconds)
         const auto t1 = std::chrono::steady_clock::now();
         *seconds = std::chrono::duration<double>(t1 - t0).count();
     });
+}
+
+int ref_train_chargpt(int device, int64_t steps, float* losses, double* seconds) {
+    return ref_train_gpt(device, steps, 96, 128, 4, 4, 256, 32, losses, seconds);
 }
 
 // kael's GPT-2 small generate on `device`, timed (the drop-in path end to end).

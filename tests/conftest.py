@@ -53,3 +53,18 @@ def kdb():
 def kael_hip(kdb):
     """kael core + kael::device implemented by the MI355X backend; GPU tests only."""
     return _ref_or_skip("hip")
+
+
+@pytest.fixture(scope="session")
+def kael_oracle_fused():
+    """kael with its optional device branches (oracle/kael_fused.py) over the C oracle: the
+    patched branches checked on the CPU."""
+    return _ref_or_skip("oracle_fused")
+
+
+@pytest.fixture(scope="session")
+def kael_hip_fused(kdb):
+    """The same with kael's optional device branches applied (oracle/kael_fused.py): softmax,
+    log_softmax, standardize, cross-entropy and GELU backward call the fused entry points and
+    matmul reads strided operands in place; GPU tests only."""
+    return _ref_or_skip("hip_fused")
