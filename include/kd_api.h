@@ -267,6 +267,25 @@ int kd_cross_entropy_rows(int dtype, void* losses, const void* logits, const int
 int kd_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
                           const void* row_weights, int64_t rows, int64_t cols);
 
+/* ---- optimizer steps (extensions replacing composed device paths) ------ */
+
+/* One Adam / AdamW step of a contiguous parameter tensor in place, with its first and second
+ * moments: the element chain of reference src/optim/optimizer.cpp:93-120 (AdamBase::update),
+ * each op rounded as kael's separate device op rounds it, the scalars converted to the element
+ * type as kael's scalar fills convert them, bias corrections 1 - beta^step with the host's pow.
+ * weight_decay > 0 with decoupled == 0 adds p * weight_decay to the gradient (Adam); with
+ * decoupled != 0 it scales p by 1 - lr * weight_decay first (AdamW). `step` >= 1 is the
+ * parameter's step count after the increment. Replaces 14 element launches and 7 fills per
+ * tensor. dtype f32 or f64. */
+int kd_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
+                 double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
+                 int decoupled, int64_t step);
+
+/* One SGD step without momentum: p -= (g (+ p * weight_decay if > 0)) * learning_rate, as
+ * reference src/optim/optimizer.cpp:60-80 computes it. dtype f32 or f64. */
+int kd_sgd_step(int dtype, void* param, const void* grad, int64_t count, double learning_rate,
+                double weight_decay);
+
 /* ---- host-side layout planning ----------------------------------------- */
 
 /* Builds the kd_element_layout that kael's TensorIterator would hand to the device for

@@ -118,7 +118,7 @@ __device__ void ln_finish(const LnIn& r, int64_t d, float* h) {
         const int64_t i = threadIdx.x + j * kThreads;
         if (i < d) {
             const float y = static_cast<float>((static_cast<double>(r.x[j]) - mean) / scale);
-            h[i] = __fadd_rn(__fmul_rn(y, r.w[j]), r.b[j]);
+            h[i] = add_sep(mul_sep(y, r.w[j]), r.b[j]);  // two roundings, as kael's * w and + b
         }
     }
 }

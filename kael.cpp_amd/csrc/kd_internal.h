@@ -62,6 +62,29 @@ inline int64_t dtype_size(int dtype) {
     return 0;
 }
 
+// ---- arithmetic rounded op by op -----------------------------------------------------------
+//
+// The compiler may contract a product and a following sum into one FMA, which rounds once;
+// __fmul_rn / __fadd_rn do not prevent that on this target. Where a result must round as kael's
+// separate element ops round it (each op rounded to the element type), these helpers are used:
+// the pragma leaves their operations without the contraction flag, also after inlining.
+template <typename T> __device__ __forceinline__ T mul_sep(T a, T b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+template <typename T> __device__ __forceinline__ T add_sep(T a, T b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+template <typename T> __device__ __forceinline__ T sub_sep(T a, T b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+template <typename T> __device__ __forceinline__ T div_sep(T a, T b) {
+#pragma clang fp contract(off)
+    return a / b;
+}
+
 // ---- exact integer arithmetic (reference src/internal/element_functions.h:45-119) --------
 
 __host__ __device__ inline int64_t wrap_add(int64_t a, int64_t b) {

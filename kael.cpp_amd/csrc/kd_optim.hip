@@ -1,0 +1,167 @@
+// kd_optim.hip - optimizer steps, one launch per parameter tensor, for gfx950.
+//
+// kael's optimizers (reference src/optim/optimizer.cpp:60-80 SGD, :93-120 Adam / AdamW) update
+// a parameter through a chain of whole-tensor element ops: on the device Adam is 14 element
+// launches and 7 scalar fills per tensor, SGD 3. Here the same chain runs per element in
+// registers. Every step is rounded to the element type as kael's separate op rounds it (the
+// *_sep helpers of kd_internal.h, so nothing is contracted into an FMA), and every scalar operand is
+// the host-computed double converted to the element type, as kael's fill of a 0-d scalar tensor
+// converts it (reference src/factory.cpp:68-79, include/kael/scalar.h:23-25). The bias
+// corrections 1 - beta^step are computed on the host with std::pow, as kael computes them. The
+// result therefore equals kael's composed device path bit for bit.
+//
+// Layout: p, g and the moments are contiguous, 16-byte aligned for the vector path (4 floats or
+// 2 doubles per lane), scalar tail otherwise; HBM-bound (Adam moves 28 bytes per f32 element).
+#include <cmath>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename T> __device__ __forceinline__ T mul_rn(T a, T b) { return mul_sep(a, b); }
+template <typename T> __device__ __forceinline__ T add_rn(T a, T b) { return add_sep(a, b); }
+template <typename T> __device__ __forceinline__ T sub_rn(T a, T b) { return sub_sep(a, b); }
+template <typename T> __device__ __forceinline__ T div_rn(T a, T b) { return div_sep(a, b); }
+// std::sqrt is the correctly rounded square root here (v_sqrt_f32 plus a refinement step); the
+// __fsqrt_rn intrinsic compiles to the bare v_sqrt_f32, which is not correctly rounded.
+template <typename T> __device__ __forceinline__ T sqrt_rn(T a) { return std::sqrt(a); }
+
+// Scalar operands in the element type, in the order kael uses them.
+template <typename T> struct AdamScalars {
+    T weight_decay;  // coupled: g + p * weight_decay
+    T decay;         // decoupled: p * (1 - lr * weight_decay)
+    T beta1, one_minus_beta1, beta2, one_minus_beta2;
+    T first_correction, second_correction, epsilon, learning_rate;
+    int mode;  // 0 no weight decay, 1 coupled (Adam), 2 decoupled (AdamW)
+};
+
+// One element of AdamBase::update (reference src/optim/optimizer.cpp:101-118).
+template <typename T>
+__device__ __forceinline__ void adam_element(T& p, T g, T& m, T& v, const AdamScalars<T>& s) {
+    if (s.mode == 1) g = add_rn(g, mul_rn(p, s.weight_decay));   // gradient + parameter * wd
+    else if (s.mode == 2) p = mul_rn(p, s.decay);                // parameter.mul_(1 - lr * wd)
+    m = add_rn(mul_rn(m, s.beta1), mul_rn(g, s.one_minus_beta1));            // first.mul_(b1).add_(g * (1 - b1))
+    v = add_rn(mul_rn(v, s.beta2), mul_rn(mul_rn(g, g), s.one_minus_beta2));  // second.mul_(b2).add_(g * g * (1 - b2))
+    const T corrected_first = div_rn(m, s.first_correction);
+    const T corrected_second = div_rn(v, s.second_correction);
+    const T denominator = add_rn(sqrt_rn(corrected_second), s.epsilon);
+    p = sub_rn(p, mul_rn(div_rn(corrected_first, denominator), s.learning_rate));
+}
+
+template <typename T> struct alignas(16) Vec {
+    T v[16 / sizeof(T)];
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void adam_kernel(T* __restrict__ p, const T* __restrict__ g,
+                                                        T* __restrict__ m, T* __restrict__ v, int64_t count,
+                                                        bool vec, AdamScalars<T> s) {
+    constexpr int V = 16 / sizeof(T);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    int64_t first_scalar = 0;
+    if (vec) {
+        const int64_t vectors = count / V;
+        Vec<T>* pv = reinterpret_cast<Vec<T>*>(p);
+        const Vec<T>* gv = reinterpret_cast<const Vec<T>*>(g);
+        Vec<T>* mv = reinterpret_cast<Vec<T>*>(m);
+        Vec<T>* vv = reinterpret_cast<Vec<T>*>(v);
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors; i += stride) {
+            Vec<T> a = pv[i], b = gv[i], c = mv[i], d = vv[i];
+#pragma unroll
+            for (int e = 0; e < V; ++e) adam_element(a.v[e], b.v[e], c.v[e], d.v[e], s);
+            pv[i] = a;
+            mv[i] = c;
+            vv[i] = d;
+        }
+        first_scalar = vectors * V;
+    }
+    for (int64_t i = first_scalar + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride)
+        adam_element(p[i], g[i], m[i], v[i], s);
+}
+
+// One element of SGD::update without momentum (reference src/optim/optimizer.cpp:60-80):
+// gradient = g (+ p * weight_decay); parameter.sub_(gradient * lr).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void sgd_kernel(T* __restrict__ p, const T* __restrict__ g, int64_t count,
+                                                       T learning_rate, T weight_decay, bool decay) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride) {
+        T grad = g[i];
+        if (decay) grad = add_rn(grad, mul_rn(p[i], weight_decay));
+        p[i] = sub_rn(p[i], mul_rn(grad, learning_rate));
+    }
+}
+
+bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
+
+dim3 grid_for(int64_t work) {
+    const int64_t blocks = (work + kThreads - 1) / kThreads;
+    return dim3(static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t{compute_units()} * 16))));
+}
+
+template <typename T>
+int adam_typed(void* param, const void* grad, void* first, void* second, int64_t count, double learning_rate,
+               double beta1, double beta2, double epsilon, double weight_decay, int decoupled, int64_t step) {
+    AdamScalars<T> s;
+    s.mode = weight_decay > 0.0 ? (decoupled ? 2 : 1) : 0;
+    s.weight_decay = static_cast<T>(weight_decay);
+    s.decay = static_cast<T>(1.0 - learning_rate * weight_decay);
+    s.beta1 = static_cast<T>(beta1);
+    s.one_minus_beta1 = static_cast<T>(1.0 - beta1);
+    s.beta2 = static_cast<T>(beta2);
+    s.one_minus_beta2 = static_cast<T>(1.0 - beta2);
+    const double step_d = static_cast<double>(step);
+    s.first_correction = static_cast<T>(1.0 - std::pow(beta1, step_d));
+    s.second_correction = static_cast<T>(1.0 - std::pow(beta2, step_d));
+    s.epsilon = static_cast<T>(epsilon);
+    s.learning_rate = static_cast<T>(learning_rate);
+    const bool vec = aligned16(param) && aligned16(grad) && aligned16(first) && aligned16(second);
+    constexpr int V = 16 / sizeof(T);
+    hipLaunchKernelGGL(adam_kernel<T>, grid_for(vec ? (count + V - 1) / V : count), dim3(kThreads), 0, stream(),
+                       static_cast<T*>(param), static_cast<const T*>(grad), static_cast<T*>(first),
+                       static_cast<T*>(second), count, vec, s);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <typename T>
+int sgd_typed(void* param, const void* grad, int64_t count, double learning_rate, double weight_decay) {
+    hipLaunchKernelGGL(sgd_kernel<T>, grid_for(count), dim3(kThreads), 0, stream(), static_cast<T*>(param),
+                       static_cast<const T*>(grad), count, static_cast<T>(learning_rate),
+                       static_cast<T>(weight_decay), weight_decay > 0.0);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" int kd_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
+                            double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
+                            int decoupled, int64_t step) {
+    if (count < 0 || step < 1) return fail(KD_E_INVALID, "kd_adam_step: negative count or step < 1");
+    if (dtype != KD_F32 && dtype != KD_F64) return fail(KD_E_INVALID, "kd_adam_step: dtype must be f32 or f64");
+    if (count == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    return dtype == KD_F32 ? adam_typed<float>(param, grad, first, second, count, learning_rate, beta1, beta2, epsilon,
+                                               weight_decay, decoupled, step)
+                           : adam_typed<double>(param, grad, first, second, count, learning_rate, beta1, beta2,
+                                                epsilon, weight_decay, decoupled, step);
+}
+
+extern "C" int kd_sgd_step(int dtype, void* param, const void* grad, int64_t count, double learning_rate,
+                           double weight_decay) {
+    if (count < 0) return fail(KD_E_INVALID, "kd_sgd_step: negative count");
+    if (dtype != KD_F32 && dtype != KD_F64) return fail(KD_E_INVALID, "kd_sgd_step: dtype must be f32 or f64");
+    if (count == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    return dtype == KD_F32 ? sgd_typed<float>(param, grad, count, learning_rate, weight_decay)
+                           : sgd_typed<double>(param, grad, count, learning_rate, weight_decay);
+}

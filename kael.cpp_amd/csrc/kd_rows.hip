@@ -31,16 +31,12 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// Multiply and add without contraction into FMA, so the LayerNorm affine rounds twice, as the
-// reference's separate `* weight` and `+ bias` kernels do.
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ double mul_rn(double a, double b) { return __dmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ double add_rn(double a, double b) { return __dadd_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
-__device__ __forceinline__ double sub_rn(double a, double b) { return __dsub_rn(a, b); }
-__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
-__device__ __forceinline__ double div_rn(double a, double b) { return __ddiv_rn(a, b); }
+// Multiply and add without contraction into FMA (kd_internal.h *_sep), so the LayerNorm affine
+// rounds twice, as the reference's separate `* weight` and `+ bias` kernels do.
+template <typename T> __device__ __forceinline__ T mul_rn(T a, T b) { return mul_sep(a, b); }
+template <typename T> __device__ __forceinline__ T add_rn(T a, T b) { return add_sep(a, b); }
+template <typename T> __device__ __forceinline__ T sub_rn(T a, T b) { return sub_sep(a, b); }
+template <typename T> __device__ __forceinline__ T div_rn(T a, T b) { return div_sep(a, b); }
 
 template <typename T> __device__ __forceinline__ T neg_inf() { return static_cast<T>(-INFINITY); }
 

@@ -152,4 +152,17 @@ void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::by
     check(kd_matmul_strided(static_cast<int>(dtype), a, b, out, &s, &st), "matmul_strided");
 }
 
+void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* first, std::byte* second,
+               std::int64_t count, double learning_rate, double beta1, double beta2, double epsilon,
+               double weight_decay, bool decoupled, std::int64_t step) {
+    check(kd_adam_step(static_cast<int>(dtype), param, grad, first, second, count, learning_rate, beta1, beta2,
+                       epsilon, weight_decay, decoupled ? 1 : 0, step),
+          "adam_step");
+}
+
+void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
+              double weight_decay) {
+    check(kd_sgd_step(static_cast<int>(dtype), param, grad, count, learning_rate, weight_decay), "sgd_step");
+}
+
 } // namespace kael::device

@@ -1,7 +1,8 @@
 // kd_kael_extensions.h - kael::device functions that the MI355X backend adds to kael's device
 // interface (reference include/kael/device_kernels.h:96-116) for the fused paths: row softmax /
 // log-softmax, row standardization, cross-entropy losses and gradient, GELU backward as one
-// element op, and matmul over strided (transposed or batch-broadcast) operands.
+// element op, matmul over strided (transposed or batch-broadcast) operands, and the Adam / SGD
+// parameter updates as one kernel per tensor.
 //
 // Defined in backend_hip.cpp. Unmodified kael never calls them; the device branches that do are
 // the optional kael patches listed in INTEGRATION.md (a one-line include of this header at the
@@ -42,5 +43,16 @@ ElementOp gelu_backward_op(bool approximate);
 // broadcasts the operand (reference src/ops/linalg.cpp:56-76 without the operand copies).
 void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
                     const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides);
+
+// One Adam / AdamW step of a contiguous parameter with its moments, in place (reference
+// src/optim/optimizer.cpp:93-120): `step` is the parameter's step count after the increment,
+// `decoupled` selects AdamW's weight decay. Same rounding as kael's composed ops.
+void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* first, std::byte* second,
+               std::int64_t count, double learning_rate, double beta1, double beta2, double epsilon,
+               double weight_decay, bool decoupled, std::int64_t step);
+
+// One SGD step without momentum, in place (reference src/optim/optimizer.cpp:60-80).
+void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
+              double weight_decay);
 
 } // namespace kael::device

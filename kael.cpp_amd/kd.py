@@ -112,6 +112,9 @@ SIGNATURES = {
     "standardize_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "cross_entropy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
     "cross_entropy_grad": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
+    "adam_step": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_double, c_double, c_double,
+                          c_double, c_double, c_int, c_int64]),
+    "sgd_step": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_double, c_double]),
     "matmul_strided": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides)]),
     "layout_build": (c_int, [POINTER(ElementLayout), c_int, POINTER(c_int), POINTER(c_int64),
                              POINTER(c_int64), POINTER(c_int), POINTER(c_void_p)]),

@@ -14,6 +14,8 @@ training configs with kael's own host code calling the backend's fused entry poi
   src/autograd/functions_math.cpp    GELU backward without the host round trip (:221-231)
   src/ops/linalg.cpp                 multiply_batches reads transposed / broadcast operands in
                                      place (:56-76)
+  src/optim/optimizer.cpp            SGD (no momentum, :60-80) and Adam / AdamW (:93-120) update a
+                                     contiguous device parameter in one kernel
 
 Each edit is anchored on a line of the reference file that must occur exactly once; a missing
 or repeated anchor is an error, so a changed reference fails loudly instead of building
@@ -134,6 +136,39 @@ MATMUL_BRANCH = """    if (a.device() != Device::CPU && is_floating_point(dtype)
     }
 """
 
+ADAM_BRANCH = """        if (parameter.device() != Device::CPU && is_floating_point(parameter.dtype()) &&
+            parameter.is_contiguous() && stored->dtype() == parameter.dtype() && stored->is_contiguous() &&
+            first_moments_[i].is_contiguous() && second_moments_[i].is_contiguous()) {
+            // MI355X: the whole update in one kernel, rounded as the ops below round it.
+            const bool decoupled = options_.weight_decay > 0.0 && mode_ == WeightDecayMode::Decoupled;
+            device::adam_step(parameter.dtype(), parameter.device_data(), stored->device_data(),
+                              first_moments_[i].device_data(), second_moments_[i].device_data(), parameter.numel(),
+                              learning_rate(), options_.beta1, options_.beta2, options_.epsilon,
+                              options_.weight_decay, decoupled, steps_[i]);
+            // The in-place ops below bump each storage's version once per op.
+            parameter.impl()->storage->bump_version();
+            if (decoupled) {
+                parameter.impl()->storage->bump_version();
+            }
+            for (int bump = 0; bump < 2; ++bump) {
+                first_moments_[i].impl()->storage->bump_version();
+                second_moments_[i].impl()->storage->bump_version();
+            }
+            continue;
+        }
+"""
+
+SGD_BRANCH = """        if (options_.momentum == 0.0 && parameter.device() != Device::CPU &&
+            is_floating_point(parameter.dtype()) && parameter.is_contiguous() &&
+            stored->dtype() == parameter.dtype() && stored->is_contiguous()) {
+            // MI355X: parameter.sub_((g + p * weight_decay) * lr) in one kernel.
+            device::sgd_step(parameter.dtype(), parameter.device_data(), stored->device_data(), parameter.numel(),
+                             learning_rate(), options_.weight_decay);
+            parameter.impl()->storage->bump_version();
+            continue;
+        }
+"""
+
 # (relative path, anchor line(s), where, text). where: "before", "after", "replace", "append".
 EDITS = [
     ("include/kael/device_kernels.h", None, "append", '\n#include "kd_kael_extensions.h"\n'),
@@ -153,6 +188,13 @@ EDITS = [
      STRIDES_HELPER),
     ("src/ops/linalg.cpp", "    const Tensor flat_a = as_batch_of_matrices(a.to(dtype), batch, rows, inner);\n", "before",
      MATMUL_BRANCH),
+    ("src/optim/optimizer.cpp", '#include "kael/ops.h"\n', "after",
+     '#include "kael/device_kernels.h"\n#include "kael/tensor_impl.h"\n'),
+    ("src/optim/optimizer.cpp",
+     "        Tensor gradient =\n            options_.weight_decay > 0.0 ? *stored + parameter * options_.weight_decay : *stored;\n",
+     "before", SGD_BRANCH),
+    ("src/optim/optimizer.cpp",
+     "        const double second_correction = 1.0 - std::pow(options_.beta2, step);\n", "after", ADAM_BRANCH),
 ]
 
 

@@ -16,6 +16,8 @@
  *   - host reductions        src/ops/reduce.cpp:24-83 (8 lanes, 16384-element blocks, pairwise
  *                            merge), :202-219 prod, :236-268 argmax/argmin, :285-295 all/any;
  *                            src/ops/sequence.cpp:95-117 cumsum (sequential, in the output dtype)
+ *   - optimizer steps        src/optim/optimizer.cpp:60-80 SGD, :93-120 Adam / AdamW (the chain of
+ *                            whole-tensor ops, each rounded to the element type)
  *
  * Deliberate choices where the reference is undefined: integer division by zero yields 0 and
  * INT64_MIN / -1 yields INT64_MIN (the reference host would trap). Floating ops on integer
@@ -984,6 +986,86 @@ int oracle_cross_entropy_grad(int dtype, void* out, const void* logits, const in
             softmax_row_f64((const double*)logits + r * cols, y, cols);
             for (int64_t i = 0; i < cols; ++i) y[i] *= w;
             y[targets[r]] -= w;
+        }
+    }
+    return KD_OK;
+}
+
+/* ---- optimizer steps: src/optim/optimizer.cpp:60-80 (SGD), :93-120 (AdamBase::update) ------ */
+
+/* Each statement is one of kael's whole-tensor ops, rounded to the element type (ISO C: no
+ * contraction into FMA); scalars are the doubles kael computes, converted to the element type as
+ * its scalar fill converts them (src/factory.cpp:68-79). */
+#define ADAM_BODY(T, SQRT)                                                                          \
+    do {                                                                                            \
+        T* p = (T*)param;                                                                           \
+        const T* g = (const T*)grad;                                                                \
+        T* m = (T*)first;                                                                           \
+        T* v = (T*)second;                                                                          \
+        const T wd = (T)weight_decay, decay = (T)(1.0 - learning_rate * weight_decay);              \
+        const T b1 = (T)beta1, omb1 = (T)(1.0 - beta1), b2 = (T)beta2, omb2 = (T)(1.0 - beta2);     \
+        const T c1 = (T)(1.0 - pow(beta1, (double)step)), c2 = (T)(1.0 - pow(beta2, (double)step)); \
+        const T eps = (T)epsilon, lr = (T)learning_rate;                                            \
+        for (int64_t i = 0; i < count; ++i) {                                                       \
+            T gi = g[i];                                                                            \
+            if (weight_decay > 0.0 && !decoupled) {                                                 \
+                const T t = p[i] * wd; /* gradient + parameter * weight_decay */                    \
+                gi = gi + t;                                                                        \
+            } else if (weight_decay > 0.0) {                                                        \
+                p[i] = p[i] * decay; /* parameter.mul_(1 - lr * weight_decay) */                    \
+            }                                                                                       \
+            const T m1 = m[i] * b1; /* first.mul_(beta1) */                                         \
+            const T t1 = gi * omb1; /* gradient * (1 - beta1) */                                    \
+            m[i] = m1 + t1;         /* .add_(...) */                                                \
+            const T v1 = v[i] * b2;                                                                 \
+            const T gg = gi * gi;                                                                   \
+            const T t2 = gg * omb2;                                                                 \
+            v[i] = v1 + t2;                                                                         \
+            const T cf = m[i] / c1; /* first / first_correction */                                  \
+            const T cs = v[i] / c2;                                                                 \
+            const T sq = SQRT(cs);                                                                  \
+            const T den = sq + eps;                                                                 \
+            const T q = cf / den;                                                                   \
+            const T u = q * lr;                                                                     \
+            p[i] = p[i] - u; /* parameter.sub_(...) */                                              \
+        }                                                                                           \
+    } while (0)
+
+int oracle_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
+                     double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
+                     int decoupled, int64_t step) {
+    if (count < 0 || step < 1) return fail("adam_step: negative count or step < 1");
+    if (check_floating(dtype)) return KD_E_INVALID;
+    if (dtype == KD_F32) ADAM_BODY(float, sqrtf);
+    else ADAM_BODY(double, sqrt);
+    return KD_OK;
+}
+
+#undef ADAM_BODY
+
+int oracle_sgd_step(int dtype, void* param, const void* grad, int64_t count, double learning_rate,
+                    double weight_decay) {
+    if (count < 0) return fail("sgd_step: negative count");
+    if (check_floating(dtype)) return KD_E_INVALID;
+    for (int64_t i = 0; i < count; ++i) {
+        if (dtype == KD_F32) {
+            float* p = (float*)param;
+            float gi = ((const float*)grad)[i];
+            if (weight_decay > 0.0) {
+                const float t = p[i] * (float)weight_decay;
+                gi = gi + t;
+            }
+            const float u = gi * (float)learning_rate;
+            p[i] = p[i] - u;
+        } else {
+            double* p = (double*)param;
+            double gi = ((const double*)grad)[i];
+            if (weight_decay > 0.0) {
+                const double t = p[i] * weight_decay;
+                gi = gi + t;
+            }
+            const double u = gi * learning_rate;
+            p[i] = p[i] - u;
         }
     }
     return KD_OK;

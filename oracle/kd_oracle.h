@@ -45,6 +45,11 @@ int oracle_cross_entropy_rows(int dtype, void* losses, const void* logits, const
                               int64_t rows, int64_t cols);
 int oracle_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
                               const void* row_weights, int64_t rows, int64_t cols);
+int oracle_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
+                     double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
+                     int decoupled, int64_t step);
+int oracle_sgd_step(int dtype, void* param, const void* grad, int64_t count, double learning_rate,
+                    double weight_decay);
 int oracle_layout_build(kd_element_layout* out, int operands, const int* ranks,
                         const int64_t* shapes, const int64_t* strides, const int* element_sizes,
                         void* const* bases);

@@ -87,8 +87,8 @@ void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, cons
 
 namespace {
 // 0 softmax_rows, 1 standardize_rows, 2 cross_entropy_rows, 3 cross_entropy_grad,
-// 4 gelu_backward_op, 5 matmul_strided.
-std::atomic<long long> g_extension_calls[6];
+// 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step.
+std::atomic<long long> g_extension_calls[8];
 } // namespace
 
 void softmax_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols, bool log) {
@@ -134,9 +134,24 @@ void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::by
     check(oracle_matmul_strided(static_cast<int>(dtype), a, b, out, &sizes, &st), "matmul_strided");
 }
 
+void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* first, std::byte* second,
+               std::int64_t count, double learning_rate, double beta1, double beta2, double epsilon,
+               double weight_decay, bool decoupled, std::int64_t step) {
+    ++g_extension_calls[6];
+    check(oracle_adam_step(static_cast<int>(dtype), param, grad, first, second, count, learning_rate, beta1, beta2,
+                           epsilon, weight_decay, decoupled ? 1 : 0, step),
+          "adam_step");
+}
+
+void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
+              double weight_decay) {
+    ++g_extension_calls[7];
+    check(oracle_sgd_step(static_cast<int>(dtype), param, grad, count, learning_rate, weight_decay), "sgd_step");
+}
+
 } // namespace kael::device
 
 // Test hook: how many times extension `which` (numbered as g_extension_calls) has run.
 extern "C" long long ref_extension_calls(int which) {
-    return which >= 0 && which < 6 ? kael::device::g_extension_calls[which].load() : -1;
+    return which >= 0 && which < 8 ? kael::device::g_extension_calls[which].load() : -1;
 }

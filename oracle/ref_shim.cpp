@@ -646,6 +646,53 @@ int ref_train_mlp(int device, int64_t steps, float* losses, float* params_out, d
     });
 }
 
+// `steps` steps of kael's own optimizer on one parameter of n elements (kind 0 SGD, 1 Adam,
+// 2 AdamW; dtype 0 f32, 1 f64), starting from `init`; the gradient of step s is
+// grads[s*n .. (s+1)*n), produced by backward of sum(p * g), which is exactly g. device 0 = CPU,
+// 1 = the linked device backend. Writes the final parameter.
+int ref_optim_steps(int kind, int device, int dtype, int64_t n, int64_t steps, const void* init, const void* grads,
+                    void* out, double learning_rate, double beta1, double beta2, double epsilon,
+                    double weight_decay) {
+    return guarded([&] {
+        const kael::DType dt = dtype == 0 ? kael::DType::F32 : kael::DType::F64;
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        const std::size_t es = static_cast<std::size_t>(kael::element_size(dt));
+        kael::Tensor p = host_tensor(init, {n}, dt).to(dev);
+        p.requires_grad_(true);
+        std::unique_ptr<kael::optim::Optimizer> optimizer;
+        if (kind == 0) {
+            kael::optim::SgdOptions o;
+            o.learning_rate = learning_rate;
+            o.weight_decay = weight_decay;
+            optimizer = std::make_unique<kael::optim::SGD>(std::vector<kael::Tensor>{p}, o);
+        } else if (kind == 1) {
+            kael::optim::AdamOptions o;
+            o.learning_rate = learning_rate;
+            o.beta1 = beta1;
+            o.beta2 = beta2;
+            o.epsilon = epsilon;
+            o.weight_decay = weight_decay;
+            optimizer = std::make_unique<kael::optim::Adam>(std::vector<kael::Tensor>{p}, o);
+        } else {
+            kael::optim::AdamWOptions o;
+            o.learning_rate = learning_rate;
+            o.beta1 = beta1;
+            o.beta2 = beta2;
+            o.epsilon = epsilon;
+            o.weight_decay = weight_decay;
+            optimizer = std::make_unique<kael::optim::AdamW>(std::vector<kael::Tensor>{p}, o);
+        }
+        for (int64_t s = 0; s < steps; ++s) {
+            optimizer->zero_grad();
+            const kael::Tensor g =
+                host_tensor(static_cast<const std::byte*>(grads) + static_cast<std::size_t>(s * n) * es, {n}, dt).to(dev);
+            kael::sum(p * g).backward();
+            optimizer->step();
+        }
+        copy_out(p.detach().cpu(), out);
+    });
+}
+
 // A char-GPT (tanh GELU) of the given size, manual_seed(3) for the N(0,0.02) init and
 // ids = randint(0,vocab,{batch,context}), targets = randint(0,vocab,{batch*context}); forward,
 // cross-entropy, backward, Adam (defaults). Writes each step's loss and the seconds.

@@ -86,6 +86,8 @@ REF_SIGS = {
     "device_available": (c_int, []),
     "train_mlp": (c_int, [c_int, c_int64, c_void_p, c_void_p, POINTER(c_double)]),
     "train_chargpt": (c_int, [c_int, c_int64, c_void_p, POINTER(c_double)]),
+    "optim_steps": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_double, c_double,
+                            c_double, c_double, c_double]),
     "train_gpt": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                           POINTER(c_double)]),
     "gpt_generate_on": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
