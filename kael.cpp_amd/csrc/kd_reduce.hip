@@ -20,6 +20,7 @@
 // (src/ops/sequence.cpp:95-117) as a segmented scan.
 #include <algorithm>
 #include <climits>
+#include <limits>
 #include <cfloat>
 
 #include "kd_internal.h"
@@ -84,29 +85,34 @@ template <int Op, typename In> struct Combiner {
 // (value, position) of the first extreme of a chunk: the first NaN wins, then the larger
 // (Largest) or smaller value, then the smaller position - the rule of reference
 // best_position, which is order independent, so every reduction tree gives the same index.
-template <typename In> struct ArgAcc {
+template <typename In, typename I> struct ArgAcc {
     In v;
-    int64_t i;
+    I i;
 };
 
-template <bool Largest, typename In> struct ArgCombiner {
-    using Acc = ArgAcc<In>;
+// I: the position type. Positions are relative to the chunk, so int32 serves every chunk below
+// 2^31 elements (cheaper index arithmetic and one select instead of two per element); int64
+// otherwise.
+template <bool Largest, typename In, typename I = int64_t> struct ArgCombiner {
+    using Acc = ArgAcc<In, I>;
+    using Index = I;
     using Out = int64_t;
     // Each lane scans its own elements from the highest position down (block_range_down), so
     // the element being added always lies before everything the accumulator has seen: it wins
     // ties and every NaN replaces the accumulator, which leaves the first extreme (or first NaN)
     // in one compare and two selects per element instead of a full combine.
     static constexpr bool kDescending = true;
+    static constexpr I kNone = std::numeric_limits<I>::max();
     __device__ __forceinline__ static Acc identity() {
         if constexpr (std::is_floating_point_v<In>) {
-            return Acc{static_cast<In>(Largest ? -INFINITY : INFINITY), INT64_MAX};
+            return Acc{static_cast<In>(Largest ? -INFINITY : INFINITY), kNone};
         } else if constexpr (std::is_same_v<In, int64_t>) {
-            return Acc{Largest ? INT64_MIN : INT64_MAX, INT64_MAX};
+            return Acc{Largest ? INT64_MIN : INT64_MAX, kNone};
         } else {
-            return Acc{static_cast<In>(Largest ? 0 : 255), INT64_MAX};
+            return Acc{static_cast<In>(Largest ? 0 : 255), kNone};
         }
     }
-    __device__ __forceinline__ static Acc load(In v, int64_t index) { return Acc{v, index}; }
+    __device__ __forceinline__ static Acc load(In v, int64_t index) { return Acc{v, static_cast<I>(index)}; }
     __device__ __forceinline__ static Acc combine(Acc a, Acc b) {
         if constexpr (std::is_floating_point_v<In>) {
             const bool an = a.v != a.v, bn = b.v != b.v;
@@ -117,13 +123,13 @@ template <bool Largest, typename In> struct ArgCombiner {
         return a.i < b.i ? a : b;
     }
     // `a` is the identity or holds an element at a position above `index`.
-    __device__ __forceinline__ static Acc step_down(Acc a, In x, int64_t index) {
+    __device__ __forceinline__ static Acc step_down(Acc a, In x, I index) {
         bool take;
         if constexpr (std::is_floating_point_v<In>) take = x != x || (Largest ? x >= a.v : x <= a.v);
         else take = Largest ? x >= a.v : x <= a.v;
         return take ? Acc{x, index} : a;
     }
-    __device__ __forceinline__ static Out finish(Acc a) { return a.i; }
+    __device__ __forceinline__ static Out finish(Acc a) { return static_cast<Out>(a.i); }
 };
 
 template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
@@ -134,8 +140,8 @@ template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
     }
 }
 
-template <typename In> __device__ __forceinline__ ArgAcc<In> shfl_xor(ArgAcc<In> v, int mask) {
-    return ArgAcc<In>{shfl_xor(v.v, mask), __shfl_xor(v.i, mask, 64)};
+template <typename In, typename I> __device__ __forceinline__ ArgAcc<In, I> shfl_xor(ArgAcc<In, I> v, int mask) {
+    return ArgAcc<In, I>{shfl_xor(v.v, mask), __shfl_xor(v.i, mask, 64)};
 }
 
 // Reduces within aligned groups of `G` lanes (G a power of two <= 64).
@@ -188,36 +194,39 @@ template <typename T> __device__ __forceinline__ void nt_store(Vec16<T>* p, cons
 // lane visits them from its highest position down - the scalar tail, its 16-byte vectors four
 // at a time from the top, then the scalar head.
 template <typename C, typename In>
-__device__ __forceinline__ typename C::Acc block_range_down(const In* data, int64_t begin, int64_t end) {
+__device__ __forceinline__ typename C::Acc block_range_down(const In* data, int64_t begin64, int64_t end64) {
     using Acc = typename C::Acc;
+    using I = typename C::Index;  // positions within the chunk: the dispatch picks a type that holds them
     constexpr int V = 16 / sizeof(In);
     Acc acc = C::identity();
-    const int64_t misalign = (reinterpret_cast<uintptr_t>(data + begin) % 16) / sizeof(In);
-    const int64_t head_end = misalign != 0 ? std::min<int64_t>(end, begin + (V - misalign)) : begin;
-    const int64_t i = head_end;
-    const int64_t vectors = (end - i) / V;
-    const int64_t t = threadIdx.x;
-    for (int64_t j = i + vectors * V + t; j < end; j += kBlock) acc = C::step_down(acc, data[j], j);  // <= 1 per lane
+    const I begin = static_cast<I>(begin64);
+    const I end = static_cast<I>(end64);
+    const I misalign = static_cast<I>((reinterpret_cast<uintptr_t>(data + begin64) % 16) / sizeof(In));
+    const I head_end = misalign != 0 ? std::min<I>(end, begin + (V - misalign)) : begin;
+    const I i = head_end;
+    const I vectors = (end - i) / V;
+    const I t = static_cast<I>(threadIdx.x);
+    for (I j = i + vectors * V + t; j < end; j += kBlock) acc = C::step_down(acc, data[j], j);  // <= 1 per lane
     const Vec16<In>* vp = reinterpret_cast<const Vec16<In>*>(data + i);
-    int64_t m = t < vectors ? (vectors - 1 - t) / kBlock + 1 : 0;  // this lane's vectors: t, t + kBlock, ...
+    I m = t < vectors ? (vectors - 1 - t) / kBlock + 1 : 0;  // this lane's vectors: t, t + kBlock, ...
     for (; m >= 4; m -= 4) {
         Vec16<In> x[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) x[u] = nt_load(vp + t + (m - 1 - u) * kBlock);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int64_t first = i + (t + (m - 1 - u) * kBlock) * V;
+            const I first = i + (t + (m - 1 - u) * kBlock) * V;
 #pragma unroll
             for (int e = V - 1; e >= 0; --e) acc = C::step_down(acc, x[u].v[e], first + e);
         }
     }
     for (; m >= 1; --m) {
         const Vec16<In> x = nt_load(vp + t + (m - 1) * kBlock);
-        const int64_t first = i + (t + (m - 1) * kBlock) * V;
+        const I first = i + (t + (m - 1) * kBlock) * V;
 #pragma unroll
         for (int e = V - 1; e >= 0; --e) acc = C::step_down(acc, x.v[e], first + e);
     }
-    for (int64_t j = begin + t; j < head_end; j += kBlock) acc = C::step_down(acc, data[j], j);  // <= 1 per lane
+    for (I j = begin + t; j < head_end; j += kBlock) acc = C::step_down(acc, data[j], j);  // <= 1 per lane
     return block_reduce<C>(acc);
 }
 
@@ -281,8 +290,10 @@ __global__ __launch_bounds__(kBlock) void group_kernel(typename C::Out* results,
         if (r < rows) {
             const In* row = data + r * chunk;
             if constexpr (C::kDescending) {
+                using I = typename C::Index;
                 if (lane < chunk)
-                    for (int64_t j = lane + (chunk - 1 - lane) / G * G; j >= 0; j -= G) acc = C::step_down(acc, row[j], j);
+                    for (I j = static_cast<I>(lane + (chunk - 1 - lane) / G * G); j >= 0; j -= G)
+                        acc = C::step_down(acc, row[j], j);
             } else {
                 for (int64_t j = lane; j < chunk; j += G) acc = C::combine(acc, C::load(row[j], j));
             }
@@ -588,14 +599,20 @@ template <int Op> int reduce_dtype(int in, void* results, const void* data, int6
     return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
 }
 
-template <bool Largest> int arg_dtype(int in, int64_t* results, const void* data, int64_t chunk, int64_t rows) {
+template <bool Largest, typename I> int arg_typed(int in, int64_t* results, const void* data, int64_t chunk, int64_t rows) {
     switch (in) {
-    case KD_F32: return reduce_with<ArgCombiner<Largest, float>, float>(results, data, chunk, rows);
-    case KD_F64: return reduce_with<ArgCombiner<Largest, double>, double>(results, data, chunk, rows);
-    case KD_I64: return reduce_with<ArgCombiner<Largest, int64_t>, int64_t>(results, data, chunk, rows);
-    case KD_BOOL: return reduce_with<ArgCombiner<Largest, uint8_t>, uint8_t>(results, data, chunk, rows);
+    case KD_F32: return reduce_with<ArgCombiner<Largest, float, I>, float>(results, data, chunk, rows);
+    case KD_F64: return reduce_with<ArgCombiner<Largest, double, I>, double>(results, data, chunk, rows);
+    case KD_I64: return reduce_with<ArgCombiner<Largest, int64_t, I>, int64_t>(results, data, chunk, rows);
+    case KD_BOOL: return reduce_with<ArgCombiner<Largest, uint8_t, I>, uint8_t>(results, data, chunk, rows);
     }
     return fail(KD_E_INVALID, "kd_arg_reduce: unknown dtype");
+}
+
+// Positions in int32 when the chunk (plus a block of lanes past its end) fits, else int64.
+template <bool Largest> int arg_dtype(int in, int64_t* results, const void* data, int64_t chunk, int64_t rows) {
+    if (chunk < (int64_t{1} << 31) - 4 * kBlock) return arg_typed<Largest, int32_t>(in, results, data, chunk, rows);
+    return arg_typed<Largest, int64_t>(in, results, data, chunk, rows);
 }
 
 } // namespace
