@@ -973,10 +973,14 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                 KD_LAUNCH_CHECK();
                 return KD_OK;
             }
-            hipLaunchKernelGGL(mfma_f32_rowmajor_kernel, grid, dim3(kThreads), 0, stream(), a, b, out,
+            // Whole tiles without split K: the same tiles and MFMA order on the loader of the
+            // transposed-operand family (waves 0-1 load A, waves 2-3 load B, four 16-byte loads
+            // each), which measured ~1 % faster than mfma_f32_rowmajor_kernel at 4096^3 with
+            // bit-identical results. The bounds checked above cover its 32-bit offsets.
+            hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false>), grid, dim3(kThreads), 0, stream(), a, b, out,
                                static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
                                static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r), p.sa.b,
-                               p.sb.b, p.so.b, int64_t{0}, int64_t{0}, int64_t{0});
+                               p.sb.b, p.so.b);
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
