@@ -165,4 +165,20 @@ void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t
     check(kd_sgd_step(static_cast<int>(dtype), param, grad, count, learning_rate, weight_decay), "sgd_step");
 }
 
+void reduce_extra(ExtraReduceOp op, DType in, std::byte* results, const std::byte* data, std::int64_t chunk_size,
+                  std::int64_t output_count) {
+    const int code = op == ExtraReduceOp::Prod ? KD_REDUCE_PROD : op == ExtraReduceOp::All ? KD_REDUCE_ALL : KD_REDUCE_ANY;
+    const int out = op != ExtraReduceOp::Prod ? KD_BOOL : (in == DType::F32 || in == DType::F64) ? static_cast<int>(in) : KD_I64;
+    check(kd_reduce(code, out, static_cast<int>(in), results, data, chunk_size, output_count), "reduce_extra");
+}
+
+void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* data, std::int64_t chunk_size,
+                std::int64_t output_count) {
+    check(kd_arg_reduce(largest ? 1 : 0, static_cast<int>(in), results, data, chunk_size, output_count), "arg_reduce");
+}
+
+void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {
+    check(kd_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
+}
+
 } // namespace kael::device

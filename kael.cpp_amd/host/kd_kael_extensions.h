@@ -1,8 +1,9 @@
 // kd_kael_extensions.h - kael::device functions that the MI355X backend adds to kael's device
 // interface (reference include/kael/device_kernels.h:96-116) for the fused paths: row softmax /
 // log-softmax, row standardization, cross-entropy losses and gradient, GELU backward as one
-// element op, matmul over strided (transposed or batch-broadcast) operands, and the Adam / SGD
-// parameter updates as one kernel per tensor.
+// element op, matmul over strided (transposed or batch-broadcast) operands, the Adam / SGD
+// parameter updates as one kernel per tensor, and the reductions kael otherwise computes on the
+// host (prod, all, any, argmax / argmin, cumsum).
 //
 // Defined in backend_hip.cpp. Unmodified kael never calls them; the device branches that do are
 // the optional kael patches listed in INTEGRATION.md (a one-line include of this header at the
@@ -54,5 +55,26 @@ void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* 
 // One SGD step without momentum, in place (reference src/optim/optimizer.cpp:60-80).
 void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
               double weight_decay);
+
+// The reductions that device::reduce does not cover (reference device_kernels.h:54 has Sum, Max
+// and Min only; kael runs these through a host copy, src/ops/reduce.cpp:362-369,399-451).
+enum class ExtraReduceOp { Prod, All, Any };
+
+// results[r] = op over data[r * chunk_size .. (r + 1) * chunk_size), as device::reduce: Prod of
+// f32 / f64 accumulates in double and stores In, of i64 / bool wrapping int64 stored as I64
+// (reference src/ops/reduce.cpp:202-219,362-369); All / Any store Bool, NaN counting as nonzero,
+// an empty chunk giving true / false (:423-451).
+void reduce_extra(ExtraReduceOp op, DType in, std::byte* results, const std::byte* data, std::int64_t chunk_size,
+                  std::int64_t output_count);
+
+// results[r] = the position in [0, chunk_size) of the first largest (largest = true) or first
+// smallest element of chunk r, the first NaN winning (reference src/ops/reduce.cpp:236-268);
+// chunk_size > 0.
+void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* data, std::int64_t chunk_size,
+                std::int64_t output_count);
+
+// Running sums along `rows` contiguous rows of `size` elements (reference src/ops/sequence.cpp:95-117):
+// f32 / f64 store In, i64 / bool wrapping int64.
+void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows);
 
 } // namespace kael::device

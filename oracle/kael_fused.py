@@ -16,6 +16,11 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      place (:56-76)
   src/optim/optimizer.cpp            SGD (no momentum, :60-80) and Adam / AdamW (:93-120) update a
                                      contiguous device parameter in one kernel
+  src/ops/reduce.cpp                 prod (:362-369), argmax / argmin (:399-421) and all / any
+                                     (:423-451) of a device tensor on the device instead of through
+                                     a host copy (the same planning: plan_reduction's kept-first
+                                     permutation, then one call over contiguous chunks)
+  src/ops/sequence.cpp               cumsum (:95-117) of a device tensor on the device
 
 Each edit is anchored on a line of the reference file that must occur exactly once; a missing
 or repeated anchor is an error, so a changed reference fails loudly instead of building
@@ -169,6 +174,66 @@ SGD_BRANCH = """        if (options_.momentum == 0.0 && parameter.device() != De
         }
 """
 
+REDUCE_HELPERS = """// MI355X: the reductions below run on the device over the same plan as device_reduce.
+Tensor device_prod(const Tensor& t, const Dims& dims, bool keepdim) {
+    const Reduction reduction = plan_reduction(t, dims, keepdim);
+    Tensor out = empty(reduction.output_shape, is_floating_point(t.dtype()) ? t.dtype() : DType::I64, t.device());
+    device::reduce_extra(device::ExtraReduceOp::Prod, reduction.data.dtype(), out.device_data(),
+                         reduction.data.device_data(), reduction.chunk_size, reduction.output_count);
+    return out;
+}
+
+Tensor device_logical(const Tensor& t, const Dims& dims, bool keepdim, device::ExtraReduceOp op) {
+    const Reduction reduction = plan_reduction(t, dims, keepdim);
+    Tensor out = empty(reduction.output_shape, DType::Bool, t.device());
+    device::reduce_extra(op, reduction.data.dtype(), out.device_data(), reduction.data.device_data(),
+                         reduction.chunk_size, reduction.output_count);
+    return out;
+}
+
+Tensor device_arg_extreme(const Tensor& t, const Dims& dims, bool keepdim, bool largest, const char* op) {
+    const Reduction reduction = plan_nonempty_reduction(t, dims, keepdim, op);
+    Tensor out = empty(reduction.output_shape, DType::I64, t.device());
+    device::arg_reduce(largest, reduction.data.dtype(), reinterpret_cast<std::int64_t*>(out.device_data()),
+                       reduction.data.device_data(), reduction.chunk_size, reduction.output_count);
+    return out;
+}
+
+"""
+
+PROD_BRANCH = """    if (on_device(t)) {
+        Tensor out = device_prod(t, dims, keepdim);
+        autograd::record_prod(out, t, dims, keepdim);
+        return out;
+    }
+"""
+
+LOGICAL_BRANCH = """    if (on_device(t)) {
+        return device_logical(t, dims, keepdim, device::ExtraReduceOp::%s);
+    }
+"""
+
+ARG_BRANCH = """    if (on_device(t)) {
+        return device_arg_extreme(%s, %s, %s);
+    }
+"""
+
+CUMSUM_BRANCH = """    if (t.device() != Device::CPU) {
+        // MI355X: running sums on the device instead of through a host copy.
+        Tensor out = autograd::without_grad([&] {
+            const Tensor rows = t.detach().transpose(dim, -1).to(dtype).contiguous();
+            Tensor totals = empty(rows.shape(), dtype, rows.device());
+            if (rows.numel() > 0) {
+                device::cumsum_rows(dtype, totals.device_data(), rows.device_data(), rows.size(-1),
+                                    rows.numel() / rows.size(-1));
+            }
+            return totals.transpose(dim, -1).contiguous();
+        });
+        autograd::record_cumsum(out, t, dim);
+        return out;
+    }
+"""
+
 # (relative path, anchor line(s), where, text). where: "before", "after", "replace", "append".
 EDITS = [
     ("include/kael/device_kernels.h", None, "append", '\n#include "kd_kael_extensions.h"\n'),
@@ -195,6 +260,23 @@ EDITS = [
      "before", SGD_BRANCH),
     ("src/optim/optimizer.cpp",
      "        const double second_correction = 1.0 - std::pow(options_.beta2, step);\n", "after", ADAM_BRANCH),
+    ("src/ops/reduce.cpp", "Tensor device_norm(const Tensor& t, const Dims& dims, bool keepdim) {\n", "before",
+     REDUCE_HELPERS),
+    ("src/ops/reduce.cpp", "Tensor prod(const Tensor& t, const Dims& dims, bool keepdim) {\n", "after", PROD_BRANCH),
+    ("src/ops/reduce.cpp", "Tensor all(const Tensor& t, const Dims& dims, bool keepdim) {\n", "after",
+     LOGICAL_BRANCH % "All"),
+    ("src/ops/reduce.cpp", "Tensor any(const Tensor& t, const Dims& dims, bool keepdim) {\n", "after",
+     LOGICAL_BRANCH % "Any"),
+    ("src/ops/reduce.cpp", "Tensor argmax(const Tensor& t) {\n", "after",
+     ARG_BRANCH % ("t.flatten(), {0}, false", "true", '"argmax"')),
+    ("src/ops/reduce.cpp", "Tensor argmax(const Tensor& t, std::int64_t dim, bool keepdim) {\n", "after",
+     ARG_BRANCH % ("t, {dim}, keepdim", "true", '"argmax"')),
+    ("src/ops/reduce.cpp", "Tensor argmin(const Tensor& t) {\n", "after",
+     ARG_BRANCH % ("t.flatten(), {0}, false", "false", '"argmin"')),
+    ("src/ops/reduce.cpp", "Tensor argmin(const Tensor& t, std::int64_t dim, bool keepdim) {\n", "after",
+     ARG_BRANCH % ("t, {dim}, keepdim", "false", '"argmin"')),
+    ("src/ops/sequence.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/ops/sequence.cpp", "        return t.to(dtype).clone();\n    }\n", "after", CUMSUM_BRANCH),
 ]
 
 

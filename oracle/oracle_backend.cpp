@@ -87,8 +87,10 @@ void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, cons
 
 namespace {
 // 0 softmax_rows, 1 standardize_rows, 2 cross_entropy_rows, 3 cross_entropy_grad,
-// 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step.
-std::atomic<long long> g_extension_calls[8];
+// 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
+// 9 arg_reduce, 10 cumsum_rows.
+constexpr int kExtensions = 11;
+std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
 void softmax_rows(DType dtype, std::byte* out, const std::byte* in, std::int64_t rows, std::int64_t cols, bool log) {
@@ -149,9 +151,29 @@ void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t
     check(oracle_sgd_step(static_cast<int>(dtype), param, grad, count, learning_rate, weight_decay), "sgd_step");
 }
 
+void reduce_extra(ExtraReduceOp op, DType in, std::byte* results, const std::byte* data, std::int64_t chunk_size,
+                  std::int64_t output_count) {
+    ++g_extension_calls[8];
+    const int code = op == ExtraReduceOp::Prod ? KD_REDUCE_PROD : op == ExtraReduceOp::All ? KD_REDUCE_ALL : KD_REDUCE_ANY;
+    const int out = op != ExtraReduceOp::Prod ? KD_BOOL : (in == DType::F32 || in == DType::F64) ? static_cast<int>(in) : KD_I64;
+    check(oracle_reduce(code, out, static_cast<int>(in), results, data, chunk_size, output_count), "reduce_extra");
+}
+
+void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* data, std::int64_t chunk_size,
+                std::int64_t output_count) {
+    ++g_extension_calls[9];
+    check(oracle_arg_reduce(largest ? 1 : 0, static_cast<int>(in), results, data, chunk_size, output_count),
+          "arg_reduce");
+}
+
+void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {
+    ++g_extension_calls[10];
+    check(oracle_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
+}
+
 } // namespace kael::device
 
 // Test hook: how many times extension `which` (numbered as g_extension_calls) has run.
 extern "C" long long ref_extension_calls(int which) {
-    return which >= 0 && which < 8 ? kael::device::g_extension_calls[which].load() : -1;
+    return which >= 0 && which < kael::device::kExtensions ? kael::device::g_extension_calls[which].load() : -1;
 }

@@ -545,6 +545,7 @@ kael::Tensor run_golden_op(const std::string& op, std::vector<kael::Tensor>& in,
         return a.has("dim") ? kael::argmax(in[0], a.integer("dim"), a.flag("keepdim")) : kael::argmax(in[0]);
     if (op == "argmin")
         return a.has("dim") ? kael::argmin(in[0], a.integer("dim"), a.flag("keepdim")) : kael::argmin(in[0]);
+    if (op == "cumsum") return kael::cumsum(in[0], a.integer("dim"));
     if (op == "matmul") return kael::matmul(in[0], in[1]);
     if (op == "dot") return kael::dot(in[0], in[1]);
     if (op == "outer") return kael::outer(in[0], in[1]);

@@ -153,6 +153,15 @@ def run_golden(lib, case: dict, device: int):
     op, name = case["op"], case["case"]
     inputs = case["inputs"].split(",")
     arrays = [np.load(GOLDEN / op / f"{name}_{i}.npy") for i in inputs]
+    expected = np.load(GOLDEN / op / f"{name}_out.npy")
+    views = [case[f"view_{i}"] for i in inputs]
+    return run_op(lib, op, case["args"], arrays, views, device, expected.nbytes), expected
+
+
+def run_op(lib, op: str, args: str, arrays, views, device: int, out_bytes: int):
+    """Runs kael op `op` (the shim's golden op table, arguments as in the golden manifest) on
+    `arrays` with the given input views ("none", "transpose", ...); returns the result array.
+    `out_bytes` bounds the result size."""
     arrays = [np.require(a.astype(np.uint8) if a.dtype == np.bool_ else a, requirements="C") for a in arrays]
     n = len(arrays)
     datas = (c_void_p * n)(*[a.ctypes.data for a in arrays])
@@ -162,22 +171,34 @@ def run_golden(lib, case: dict, device: int):
     for i, a in enumerate(arrays):
         for d, s in enumerate(a.shape):
             shapes[8 * i + d] = s
-    views = (c_char_p * n)(*[case[f"view_{i}"].encode() for i in inputs])
-    expected = np.load(GOLDEN / op / f"{name}_out.npy")
-    capacity = max(1024, expected.nbytes * 8 + 1024)
+    views = (c_char_p * n)(*[v.encode() for v in views])
+    capacity = max(1024, out_bytes * 8 + 1024)
     out = np.zeros(capacity, np.uint8)
     odt, orank = c_int(), c_int()
     oshape = (c_int64 * 8)()
-    nbytes = lib.ref_golden(op.encode(), case["args"].encode(), n, datas, dtypes, ranks, shapes, views, device,
+    nbytes = lib.ref_golden(op.encode(), args.encode(), n, datas, dtypes, ranks, shapes, views, device,
                             ptr(out), capacity, ctypes.byref(odt), ctypes.byref(orank), oshape)
     if nbytes < 0:
-        raise RuntimeError(f"{op}/{name}: {ref_error(lib)}")
+        raise RuntimeError(f"{op} {args}: {ref_error(lib)}")
     dtype = kd.NUMPY_DTYPE[odt.value]
     shape = tuple(oshape[d] for d in range(orank.value))
     result = out[:nbytes].view(dtype).reshape(shape)
     if dtype == np.uint8:
         result = result.astype(np.bool_)
-    return result, expected
+    return result
+
+
+def apply_view(x: np.ndarray, view: str) -> np.ndarray:
+    """numpy's counterpart of the shim's input views "none", "transpose:a:b" and "permute:..."."""
+    name, *args = view.split(":")
+    dims = [int(a) for a in args]
+    if name == "none":
+        return x
+    if name == "transpose":
+        return np.swapaxes(x, dims[0], dims[1])
+    if name == "permute":
+        return np.transpose(x, dims)
+    raise ValueError(view)
 
 
 def golden_close(actual: np.ndarray, expected: np.ndarray, rtol=None, atol=None) -> tuple[bool, str]:

@@ -1,6 +1,8 @@
 """kael's optional device branches (oracle/kael_fused.py: softmax / log_softmax / standardize as
 row kernels, cross-entropy losses and gradient in one call each, GELU backward as one element op,
-matmul over strided operands) checked on the CPU, with the C oracle as kael's device.
+matmul over strided operands, the fused optimizer steps, and prod / all / any / argmax / argmin /
+cumsum on the device instead of through a host copy) checked on the CPU, with the C oracle as
+kael's device.
 
 kael's golden suite (783 PyTorch known answers, reference tests/test_golden.cpp:236-292
 tolerances), its 36 device-behaviour cases (reference tests/test_cuda.cpp) and 100 steps of the C3
@@ -16,8 +18,12 @@ import support
 from test_oracle_device_suite import NAMES
 
 CASES = support.golden_cases()
+# Numbered as the oracle backend counts them (oracle/oracle_backend.cpp).
 EXTENSIONS = ["softmax_rows", "standardize_rows", "cross_entropy_rows", "cross_entropy_grad", "gelu_backward_op",
-              "matmul_strided"]
+              "matmul_strided", "adam_step", "sgd_step", "reduce_extra", "arg_reduce", "cumsum_rows"]
+# The entry points a char-GPT training step reaches (forward, backward, Adam).
+TRAINING = ["softmax_rows", "standardize_rows", "cross_entropy_rows", "cross_entropy_grad", "gelu_backward_op",
+            "matmul_strided", "adam_step"]
 
 
 def calls(lib):
@@ -40,14 +46,18 @@ def test_golden_suite_through_the_fused_branches(kael_oracle_fused):
     assert not failures, f"{len(failures)} of {len(CASES)} cases:\n" + "\n".join(failures[:40])
     after = calls(kael_oracle_fused)
     # The golden manifest holds tensor ops (no layer norm, cross-entropy or gradients): of the fused
-    # branches it reaches softmax / log_softmax and the products.
-    for name in ("softmax_rows", "matmul_strided"):
+    # branches it reaches softmax / log_softmax, the products, and prod / all / any / argmax / argmin
+    # (20 all, 20 any, 14 prod, 8 argmax and 8 argmin cases, every one now computed on the device).
+    for name in ("softmax_rows", "matmul_strided", "reduce_extra", "arg_reduce"):
         assert after[name] > before[name], f"{name} never ran: {after}"
 
 
 @pytest.mark.parametrize("name", NAMES)
 def test_device_case_through_the_fused_branches(kael_oracle_fused, name):
+    before = calls(kael_oracle_fused)
     support.run_suite_case(kael_oracle_fused, name)
+    if name == "sequence_ops_match_cpu":  # cumsum of a device tensor (reference tests/test_cuda.cpp:576)
+        assert calls(kael_oracle_fused)["cumsum_rows"] > before["cumsum_rows"]
 
 
 def test_c3_mlp_through_the_fused_branches_matches_cpu(kael_oracle_fused):
@@ -86,5 +96,5 @@ def test_small_gpt_training_through_every_fused_branch_matches_cpu(kael_oracle_f
     assert lib.ref_train_gpt(1, *args, dev_l.ctypes.data_as(ctypes.c_void_p), ctypes.byref(t)) == 0, support.ref_error(lib)
     after = calls(lib)
     np.testing.assert_allclose(dev_l, cpu_l, rtol=1e-4)
-    ran = {name: after[name] - before[name] for name in EXTENSIONS}
+    ran = {name: after[name] - before[name] for name in TRAINING}
     assert all(n > 0 for n in ran.values()), ran
