@@ -3,7 +3,8 @@
 Headline (BASELINE.json metric): f32 matmul TFLOP/s as a fraction of FP32 MFMA peak, on the
 north-star size 4096^3 (C = A.B, A and B contiguous row-major, uniform[-1,1]); a "step" is one
 kd_matmul call over inputs already resident in HBM. Secondary figures in "extra": the C1 shape
-(512^3), the C2 elementwise/reduction ops in GB/s, and the fused row kernels.
+(512^3), the C2 elementwise/reduction ops in GB/s, the fused row kernels, the index and
+optimizer kernels at GPT-2-small scale, and GPT-2-small decode tokens/s.
 
 Timing: W untimed warm-up steps, then K steps bracketed by kd_synchronize(); the kernel time comes
 from HIP events recorded on the backend stream (the stream every kd_* launch uses). The GPU's
@@ -13,7 +14,7 @@ whose steps take microseconds, warm up for at least MIN_WARMUP_S of steps.
 The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference sources,
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only matmul|c1|c2|rows|gpt2|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only matmul|c1|c2|rows|train|gpt2|copy]
 """
 from __future__ import annotations
 
@@ -183,6 +184,49 @@ def bench_rows(backend, steps, warmup):
     return out
 
 
+def bench_train(backend, steps, warmup):
+    """The index and optimizer kernels at GPT-2-small scale (HBM-bound sizes; C4's own tensors are
+    latency-bound): embedding-row gather and scatter_add of 65 536 token ids against the
+    [50257, 768] table, and one fused Adam / SGD step over 124 439 808 f32 parameters (GPT-2
+    small). Algorithmic bytes: gather reads and writes each row once (+ 8 B per id); scatter_add
+    reads the source once and reads and writes each distinct target row once (+ 8 B per id); Adam
+    reads p, g, m, v and writes p, m, v (28 B per parameter); SGD reads p, g and writes p (12 B)."""
+    rng = np.random.default_rng(5)
+    vocab, dim, tokens = 50257, 768, 65536
+    table = backend.to_device(rng.normal(0, 0.02, (vocab, dim)).astype(np.float32))
+    ids_host = rng.integers(0, vocab, tokens).astype(np.int64)
+    ids = backend.to_device(ids_host)
+    rows = backend.empty((tokens, dim), np.float32)
+    lay = kd.index_layout((tokens, dim), 0, (dim, 1), (1, 0), (dim, 1))
+    out = {}
+    g = backend.lib.kd_gather
+    ms, _ = time_steps(backend, lambda i: g(kd.F32, rows.ptr, table.ptr, ids.ptr, ctypes.byref(lay)), steps, warmup,
+                       MIN_WARMUP_S)
+    out["gather_65536x768"] = {"us": ms * 1e3, "gbps": (2 * tokens * dim * 4 + tokens * 8) / (ms * 1e-3) / 1e9}
+    sa = backend.lib.kd_scatter_add
+    distinct = len(np.unique(ids_host))
+    ms, _ = time_steps(backend, lambda i: sa(kd.F32, table.ptr, ids.ptr, rows.ptr, ctypes.byref(lay)), steps, warmup,
+                       MIN_WARMUP_S)
+    out["scatter_add_65536x768"] = {"us": ms * 1e3, "distinct_rows": distinct,
+                                    "gbps": (tokens * dim * 4 + 2 * distinct * dim * 4 + tokens * 8) / (ms * 1e-3) / 1e9}
+    del rows, table
+    n = 124439808
+    p = backend.to_device(rng.uniform(-0.1, 0.1, n).astype(np.float32))
+    gr = backend.to_device(rng.uniform(-1e-3, 1e-3, n).astype(np.float32))
+    m = backend.to_device(np.zeros(n, np.float32))
+    v = backend.to_device(np.zeros(n, np.float32))
+    adam = backend.lib.kd_adam_step
+    ms, _ = time_steps(backend, lambda i: adam(kd.F32, p.ptr, gr.ptr, m.ptr, v.ptr, n, 3e-4, 0.9, 0.999, 1e-8, 0.01, 1,
+                                               i + 1), steps, warmup, MIN_WARMUP_S)
+    out["adamw_step_124M"] = {"us": ms * 1e3, "gbps": 28 * n / (ms * 1e-3) / 1e9}
+    sgd = backend.lib.kd_sgd_step
+    ms, _ = time_steps(backend, lambda i: sgd(kd.F32, p.ptr, gr.ptr, n, 0.01, 0.0), steps, warmup, MIN_WARMUP_S)
+    out["sgd_step_124M"] = {"us": ms * 1e3, "gbps": 12 * n / (ms * 1e-3) / 1e9}
+    for v_ in out.values():
+        v_["frac_hbm"] = v_["gbps"] / HBM_PEAK_GBPS
+    return out
+
+
 def bench_copy(backend, steps, warmup, mib=256):
     """Plain contiguous f32 copy (kd_convert f32->f32) of `mib` MiB: the calibration kernel for
     HBM byte counters (it must read and write exactly `mib` MiB each)."""
@@ -307,7 +351,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
-    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "copy", "c2", "rows", "gpt2"],
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "copy", "c2", "rows", "train", "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -331,8 +375,9 @@ def main() -> int:
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
         print(json.dumps({"metric": "C1 f32 matmul 512^3", "extra": extra}))
         return 0
-    if args.only in ("c2", "rows"):
-        extra[args.only] = (bench_c2 if args.only == "c2" else bench_rows)(backend, args.steps, args.warmup)
+    if args.only in ("c2", "rows", "train"):
+        fn = {"c2": bench_c2, "rows": bench_rows, "train": bench_train}[args.only]
+        extra[args.only] = fn(backend, args.steps, args.warmup)
         print(json.dumps({"metric": f"{args.only} only", "extra": extra}))
         return 0
     main_run = bench_matmul(backend, n, args.steps, args.warmup)
@@ -340,6 +385,7 @@ def main() -> int:
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
         extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
+        extra["train"] = bench_train(backend, max(args.steps, 20), args.warmup)
         extra["gpt2_decode"] = bench_gpt2(backend)
     cpu = None
     if not args.no_cpu:

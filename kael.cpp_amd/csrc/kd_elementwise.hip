@@ -392,7 +392,7 @@ __global__ __launch_bounds__(kBlock) void nd64_kernel(F f, kd_element_layout lay
 
 int grid_for(int64_t work) {
     const int64_t blocks = (work + kBlock - 1) / kBlock;
-    const int64_t cap = static_cast<int64_t>(compute_units()) * 32;
+    const int64_t cap = int64_t{1} << 20;
     return static_cast<int>(std::max<int64_t>(1, std::min(blocks, cap)));
 }
 

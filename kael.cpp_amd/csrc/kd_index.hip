@@ -8,8 +8,11 @@
 // Indices are range-checked by the host before the call (src/internal/index_checks.h:37-43).
 //
 // Decoding uses multiply-high division per dim. When the innermost dim is not the indexed
-// axis and is contiguous in every role, consecutive lanes touch consecutive elements of the
-// same gathered row, so an embedding lookup reads and writes whole rows coalesced.
+// axis, is contiguous in data and source and the indices do not vary along it (an embedding
+// lookup, index_select, index_add_), the index space is a set of rows: one wave per row decodes
+// the row and loads its index once, then copies (gather, 16-byte vectors when the row starts
+// allow) or atomically adds (scatter) the row's elements, all lanes' loads issued before their
+// stores. Otherwise every element is decoded on its own.
 #include <algorithm>
 
 #include "kd_internal.h"
@@ -49,6 +52,54 @@ __device__ __forceinline__ Position locate(const IndexPlan& p, const int64_t* __
     return pos;
 }
 
+// Row mode: the data and source offsets of the first element of row r (the index space with the
+// innermost dim dropped).
+__device__ __forceinline__ Position locate_row(const IndexPlan& p, const int64_t* __restrict__ indices, uint32_t r) {
+    Position pos{0, 0, 0};
+    for (int k = 1; k < p.dims; ++k) {
+        const uint32_t q = p.div[k].div(r);
+        const int64_t c = static_cast<int64_t>(r - q * p.div[k].divisor);
+        r = q;
+        pos.index += c * p.index_stride[k];
+        pos.source += c * p.source_stride[k];
+        if (k != p.axis_slot) pos.data += c * p.data_stride[k];
+    }
+    pos.data += indices[pos.index] * p.axis_data_stride;
+    return pos;
+}
+
+template <typename T, int N> struct alignas(sizeof(T) * N) Vec {
+    T v[N];
+};
+
+constexpr int kWaves = kThreads / 64;
+constexpr int kUnroll = 4;
+
+// out[r][0 .. inner) = data row of r, in chunks of V elements (V > 1 only when every row start of
+// data and out is 16-byte aligned and inner is a multiple of V).
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(T* __restrict__ out, const T* __restrict__ data,
+                                                               const int64_t* __restrict__ indices, IndexPlan p,
+                                                               uint32_t rows, uint32_t inner) {
+    using Chunk = Vec<T, V>;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t chunks = inner / V;
+    for (uint32_t r = blockIdx.x * kWaves + wave; r < rows; r += gridDim.x * kWaves) {
+        const Chunk* __restrict__ src = reinterpret_cast<const Chunk*>(data + locate_row(p, indices, r).data);
+        Chunk* __restrict__ dst = reinterpret_cast<Chunk*>(out + static_cast<int64_t>(r) * inner);
+        uint32_t c = lane;
+        for (; c + (kUnroll - 1) * 64 < chunks; c += kUnroll * 64) {
+            Chunk x[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) x[u] = src[c + u * 64];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) dst[c + u * 64] = x[u];
+        }
+        for (; c < chunks; c += 64) dst[c] = src[c];
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gather_kernel(T* __restrict__ out, const T* __restrict__ data,
                                                           const int64_t* __restrict__ indices, IndexPlan p,
@@ -71,6 +122,29 @@ __global__ __launch_bounds__(kThreads) void scatter_add_kernel(T* data, const in
     for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < count; e += gridDim.x * kThreads) {
         const Position pos = locate(p, indices, e);
         atomic_add_value(data + pos.data, source[pos.source]);
+    }
+}
+
+// Row mode of scatter_add: data row of r += source row of r, element by element with atomics.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void scatter_rows_kernel(T* data, const int64_t* __restrict__ indices,
+                                                                const T* __restrict__ source, IndexPlan p,
+                                                                uint32_t rows, uint32_t inner) {
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    for (uint32_t r = blockIdx.x * kWaves + wave; r < rows; r += gridDim.x * kWaves) {
+        const Position pos = locate_row(p, indices, r);
+        T* dst = data + pos.data;
+        const T* __restrict__ src = source + pos.source;
+        uint32_t c = lane;
+        for (; c + (kUnroll - 1) * 64 < inner; c += kUnroll * 64) {
+            T x[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) x[u] = src[c + u * 64];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) atomic_add_value(dst + c + u * 64, x[u]);
+        }
+        for (; c < inner; c += 64) atomic_add_value(dst + c, src[c]);
     }
 }
 
@@ -112,6 +186,19 @@ int plan(const kd_index_layout& l, IndexPlan& p) {
     return KD_OK;
 }
 
+// Row mode applies when the innermost dim is not the indexed axis, is contiguous in data (and,
+// for scatter, in source), the indices are constant along it, and rows are long enough to keep
+// a wave busy.
+bool row_mode(const IndexPlan& p, bool scatter) {
+    return p.dims >= 2 && p.axis_slot != 0 && p.index_stride[0] == 0 && p.data_stride[0] == 1 &&
+           (!scatter || p.source_stride[0] == 1) && p.div[0].divisor >= 64;
+}
+
+int row_grid(uint32_t rows) {
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((int64_t{rows} + kWaves - 1) / kWaves,
+                                                                    int64_t{compute_units()} * 32)));
+}
+
 int grid_for(int64_t count) {
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((count + kThreads - 1) / kThreads,
                                                                     int64_t{compute_units()} * 32)));
@@ -121,6 +208,21 @@ template <typename T> int gather_typed(void* out, const void* data, const int64_
     if (l.count < (int64_t{1} << 31)) {
         IndexPlan p;
         if (int rc = plan(l, p)) return rc;
+        if (row_mode(p, false)) {
+            constexpr int V = 16 / sizeof(T);
+            const uint32_t inner = p.div[0].divisor, rows = static_cast<uint32_t>(l.count / inner);
+            bool vec = inner % V == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(data) % 16 == 0;
+            for (int k = 1; k < p.dims; ++k) vec = vec && p.data_stride[k] % V == 0;
+            if (vec)
+                hipLaunchKernelGGL((gather_rows_kernel<T, V>), dim3(row_grid(rows)), dim3(kThreads), 0, stream(),
+                                   static_cast<T*>(out), static_cast<const T*>(data), indices, p, rows, inner);
+            else
+                hipLaunchKernelGGL((gather_rows_kernel<T, 1>), dim3(row_grid(rows)), dim3(kThreads), 0, stream(),
+                                   static_cast<T*>(out), static_cast<const T*>(data), indices, p, rows, inner);
+            KD_LAUNCH_CHECK();
+            return KD_OK;
+        }
         hipLaunchKernelGGL((gather_kernel<T>), dim3(grid_for(l.count)), dim3(kThreads), 0, stream(), static_cast<T*>(out),
                            static_cast<const T*>(data), indices, p, static_cast<uint32_t>(l.count));
     } else {
@@ -135,6 +237,13 @@ template <typename T> int scatter_typed(void* data, const int64_t* indices, cons
     if (l.count < (int64_t{1} << 31)) {
         IndexPlan p;
         if (int rc = plan(l, p)) return rc;
+        if (row_mode(p, true)) {
+            const uint32_t inner = p.div[0].divisor, rows = static_cast<uint32_t>(l.count / inner);
+            hipLaunchKernelGGL((scatter_rows_kernel<T>), dim3(row_grid(rows)), dim3(kThreads), 0, stream(),
+                               static_cast<T*>(data), indices, static_cast<const T*>(source), p, rows, inner);
+            KD_LAUNCH_CHECK();
+            return KD_OK;
+        }
         hipLaunchKernelGGL((scatter_add_kernel<T>), dim3(grid_for(l.count)), dim3(kThreads), 0, stream(),
                            static_cast<T*>(data), indices, static_cast<const T*>(source), p, static_cast<uint32_t>(l.count));
     } else {

@@ -11,7 +11,9 @@
 // result therefore equals kael's composed device path bit for bit.
 //
 // Layout: p, g and the moments are contiguous, 16-byte aligned for the vector path (4 floats or
-// 2 doubles per lane), scalar tail otherwise; HBM-bound (Adam moves 28 bytes per f32 element).
+// 2 doubles per lane), scalar tail otherwise; HBM-bound (Adam moves 28 bytes per f32 element,
+// SGD 12). Tensors of 32 MiB or more stream with nontemporal loads and stores: they are touched
+// once per step and would only evict other data from the caches.
 #include <cmath>
 
 #include "kd_internal.h"
@@ -56,7 +58,30 @@ template <typename T> struct alignas(16) Vec {
     T v[16 / sizeof(T)];
 };
 
-template <typename T>
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT, typename T> __device__ __forceinline__ Vec<T> ld(const Vec<T>* p) {
+    if constexpr (!NT) {
+        return *p;
+    } else {
+        const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+        Vec<T> out;
+        __builtin_memcpy(&out, &r, 16);
+        return out;
+    }
+}
+
+template <bool NT, typename T> __device__ __forceinline__ void st(Vec<T>* p, const Vec<T>& x) {
+    if constexpr (!NT) {
+        *p = x;
+    } else {
+        u32x4 r;
+        __builtin_memcpy(&r, &x, 16);
+        __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
+    }
+}
+
+template <typename T, bool NT>
 __global__ __launch_bounds__(kThreads) void adam_kernel(T* __restrict__ p, const T* __restrict__ g,
                                                         T* __restrict__ m, T* __restrict__ v, int64_t count,
                                                         bool vec, AdamScalars<T> s) {
@@ -70,12 +95,12 @@ __global__ __launch_bounds__(kThreads) void adam_kernel(T* __restrict__ p, const
         Vec<T>* mv = reinterpret_cast<Vec<T>*>(m);
         Vec<T>* vv = reinterpret_cast<Vec<T>*>(v);
         for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors; i += stride) {
-            Vec<T> a = pv[i], b = gv[i], c = mv[i], d = vv[i];
+            Vec<T> a = ld<NT>(pv + i), b = ld<NT>(gv + i), c = ld<NT>(mv + i), d = ld<NT>(vv + i);
 #pragma unroll
             for (int e = 0; e < V; ++e) adam_element(a.v[e], b.v[e], c.v[e], d.v[e], s);
-            pv[i] = a;
-            mv[i] = c;
-            vv[i] = d;
+            st<NT>(pv + i, a);
+            st<NT>(mv + i, c);
+            st<NT>(vv + i, d);
         }
         first_scalar = vectors * V;
     }
@@ -86,21 +111,43 @@ __global__ __launch_bounds__(kThreads) void adam_kernel(T* __restrict__ p, const
 // One element of SGD::update without momentum (reference src/optim/optimizer.cpp:60-80):
 // gradient = g (+ p * weight_decay); parameter.sub_(gradient * lr).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void sgd_kernel(T* __restrict__ p, const T* __restrict__ g, int64_t count,
-                                                       T learning_rate, T weight_decay, bool decay) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride) {
-        T grad = g[i];
-        if (decay) grad = add_rn(grad, mul_rn(p[i], weight_decay));
-        p[i] = sub_rn(p[i], mul_rn(grad, learning_rate));
-    }
+__device__ __forceinline__ T sgd_element(T p, T g, T learning_rate, T weight_decay, bool decay) {
+    if (decay) g = add_rn(g, mul_rn(p, weight_decay));
+    return sub_rn(p, mul_rn(g, learning_rate));
 }
+
+template <typename T, bool NT>
+__global__ __launch_bounds__(kThreads) void sgd_kernel(T* __restrict__ p, const T* __restrict__ g, int64_t count,
+                                                       bool vec, T learning_rate, T weight_decay, bool decay) {
+    constexpr int V = 16 / sizeof(T);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    int64_t first_scalar = 0;
+    if (vec) {
+        const int64_t vectors = count / V;
+        Vec<T>* pv = reinterpret_cast<Vec<T>*>(p);
+        const Vec<T>* gv = reinterpret_cast<const Vec<T>*>(g);
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors; i += stride) {
+            Vec<T> a = ld<NT>(pv + i);
+            const Vec<T> b = ld<NT>(gv + i);
+#pragma unroll
+            for (int e = 0; e < V; ++e) a.v[e] = sgd_element(a.v[e], b.v[e], learning_rate, weight_decay, decay);
+            st<NT>(pv + i, a);
+        }
+        first_scalar = vectors * V;
+    }
+    for (int64_t i = first_scalar + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride)
+        p[i] = sgd_element(p[i], g[i], learning_rate, weight_decay, decay);
+}
+
+// Streaming threshold of the nontemporal variants (bytes of the parameter tensor).
+constexpr int64_t kStreamBytes = int64_t{32} << 20;
 
 bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
 
+// One work item per thread up to 2^20 workgroups (the grid-stride loops cover larger tensors).
 dim3 grid_for(int64_t work) {
     const int64_t blocks = (work + kThreads - 1) / kThreads;
-    return dim3(static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t{compute_units()} * 16))));
+    return dim3(static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t{1} << 20))));
 }
 
 template <typename T>
@@ -121,18 +168,29 @@ int adam_typed(void* param, const void* grad, void* first, void* second, int64_t
     s.learning_rate = static_cast<T>(learning_rate);
     const bool vec = aligned16(param) && aligned16(grad) && aligned16(first) && aligned16(second);
     constexpr int V = 16 / sizeof(T);
-    hipLaunchKernelGGL(adam_kernel<T>, grid_for(vec ? (count + V - 1) / V : count), dim3(kThreads), 0, stream(),
-                       static_cast<T*>(param), static_cast<const T*>(grad), static_cast<T*>(first),
-                       static_cast<T*>(second), count, vec, s);
+    const dim3 grid = grid_for(vec ? (count + V - 1) / V : count);
+    if (count * static_cast<int64_t>(sizeof(T)) >= kStreamBytes)
+        hipLaunchKernelGGL((adam_kernel<T, true>), grid, dim3(kThreads), 0, stream(), static_cast<T*>(param),
+                           static_cast<const T*>(grad), static_cast<T*>(first), static_cast<T*>(second), count, vec, s);
+    else
+        hipLaunchKernelGGL((adam_kernel<T, false>), grid, dim3(kThreads), 0, stream(), static_cast<T*>(param),
+                           static_cast<const T*>(grad), static_cast<T*>(first), static_cast<T*>(second), count, vec, s);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }
 
 template <typename T>
 int sgd_typed(void* param, const void* grad, int64_t count, double learning_rate, double weight_decay) {
-    hipLaunchKernelGGL(sgd_kernel<T>, grid_for(count), dim3(kThreads), 0, stream(), static_cast<T*>(param),
-                       static_cast<const T*>(grad), count, static_cast<T>(learning_rate),
-                       static_cast<T>(weight_decay), weight_decay > 0.0);
+    const bool vec = aligned16(param) && aligned16(grad);
+    constexpr int V = 16 / sizeof(T);
+    const dim3 grid = grid_for(vec ? (count + V - 1) / V : count);
+    const T lr = static_cast<T>(learning_rate), wd = static_cast<T>(weight_decay);
+    if (count * static_cast<int64_t>(sizeof(T)) >= kStreamBytes)
+        hipLaunchKernelGGL((sgd_kernel<T, true>), grid, dim3(kThreads), 0, stream(), static_cast<T*>(param),
+                           static_cast<const T*>(grad), count, vec, lr, wd, weight_decay > 0.0);
+    else
+        hipLaunchKernelGGL((sgd_kernel<T, false>), grid, dim3(kThreads), 0, stream(), static_cast<T*>(param),
+                           static_cast<const T*>(grad), count, vec, lr, wd, weight_decay > 0.0);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }

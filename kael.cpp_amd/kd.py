@@ -383,6 +383,21 @@ def load() -> Backend:
     return _BACKEND
 
 
+def index_layout(shape, axis, data_strides, index_strides, source_strides) -> IndexLayout:
+    """kd_index_layout for an iteration `shape` with the gathered / scattered `axis` and element
+    strides of the data, index and source (or output) tensors per dim."""
+    lay = IndexLayout()
+    lay.dims = len(shape)
+    lay.axis = axis
+    lay.count = int(np.prod(shape)) if len(shape) else 1
+    for d in range(len(shape)):
+        lay.shape[d] = shape[d]
+        lay.data_strides[d] = data_strides[d]
+        lay.index_strides[d] = index_strides[d]
+        lay.source_strides[d] = source_strides[d]
+    return lay
+
+
 def element_layout(shape, strides_bytes, bases) -> ElementLayout:
     """An ElementLayout from explicit dims: shape (d), per-operand byte strides [ops][d]."""
     lay = ElementLayout()

@@ -14,17 +14,7 @@ import support
 pytestmark = pytest.mark.gpu
 
 
-def index_layout(shape, axis, data_strides, index_strides, source_strides):
-    lay = kd.IndexLayout()
-    lay.dims = len(shape)
-    lay.axis = axis
-    lay.count = int(np.prod(shape))
-    for d in range(len(shape)):
-        lay.shape[d] = shape[d]
-        lay.data_strides[d] = data_strides[d]
-        lay.index_strides[d] = index_strides[d]
-        lay.source_strides[d] = source_strides[d]
-    return lay
+index_layout = kd.index_layout
 
 
 @pytest.mark.parametrize("tokens", [1, 64])
@@ -82,3 +72,68 @@ def test_int64_scatter_add_wraps(kdb):
     src = kdb.to_device(np.array([1], np.int64))
     kdb.call("scatter_add", kd.I64, target.ptr, ids.ptr, src.ptr, index_layout((1,), 0, (1,), (1,), (1,)))
     assert target.numpy()[0] == -(2**63)
+
+
+# Row mode (one wave per row, the index loaded once per row): embedding-shaped layouts whose
+# innermost dim is contiguous and not indexed, with 16-byte vectors where every row start allows
+# them, single elements otherwise (odd row lengths, a data pointer one element off alignment),
+# an indexed middle axis, and the element path for rows shorter than a wave.
+ROW_LAYOUTS = [
+    # (data shape, index count, axis, row length, data offset in elements)
+    ((300, 256), 1000, 0, 256, 0),
+    ((300, 67), 1000, 0, 67, 0),
+    ((300, 256), 517, 0, 256, 1),
+    ((5, 40, 96), 33, 1, 96, 0),
+    ((300, 40), 1000, 0, 40, 0),
+]
+
+
+def _row_case(dtype, data_shape, n_idx, axis, offset, seed):
+    rng = np.random.default_rng(seed)
+    npd = kd.NUMPY_DTYPE[dtype]
+    flat = (rng.normal(size=int(np.prod(data_shape)) + offset) * 8).astype(npd)
+    data = flat[offset:].reshape(data_shape)
+    ids = rng.integers(0, data_shape[axis], n_idx).astype(np.int64)
+    shape = list(data_shape)
+    shape[axis] = n_idx
+    dstr = [int(np.prod(data_shape[d + 1:])) for d in range(len(data_shape))]
+    istr = [0] * len(shape)
+    istr[axis] = 1
+    sstr = [int(np.prod(shape[d + 1:])) for d in range(len(shape))]
+    return flat, data, ids, shape, kd.index_layout(tuple(shape), axis, dstr, istr, sstr)
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64, kd.BOOL], ids=["f32", "f64", "i64", "bool"])
+@pytest.mark.parametrize("case", range(len(ROW_LAYOUTS)))
+def test_gather_rows(kdb, oracle, dtype, case):
+    data_shape, n_idx, axis, _, offset = ROW_LAYOUTS[case]
+    flat, data, ids, shape, lay = _row_case(dtype, data_shape, n_idx, axis, offset, case)
+    npd = kd.NUMPY_DTYPE[dtype]
+    want = np.empty(shape, npd)
+    assert oracle.oracle_gather(dtype, support.ptr(want), support.ptr(np.ascontiguousarray(data)), support.ptr(ids),
+                                lay) == 0
+    np.testing.assert_array_equal(want, np.take(data, ids, axis=axis))
+    dflat, di, do = kdb.to_device(flat), kdb.to_device(ids), kdb.empty(tuple(shape), npd)
+    size = np.dtype(npd).itemsize
+    kdb.call("gather", dtype, do.ptr, dflat.ptr + offset * size, di.ptr, lay)
+    np.testing.assert_array_equal(do.numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64], ids=["f32", "f64", "i64"])
+@pytest.mark.parametrize("case", range(len(ROW_LAYOUTS)))
+def test_scatter_add_rows(kdb, oracle, dtype, case):
+    data_shape, n_idx, axis, _, offset = ROW_LAYOUTS[case]
+    flat, data, ids, shape, lay = _row_case(dtype, data_shape, n_idx, axis, offset, 50 + case)
+    npd = kd.NUMPY_DTYPE[dtype]
+    rng = np.random.default_rng(case)
+    src = (rng.normal(size=shape) * 4).astype(npd) if dtype != kd.I64 else rng.integers(-9, 9, shape).astype(np.int64)
+    want = np.ascontiguousarray(data).copy()
+    assert oracle.oracle_scatter_add(dtype, support.ptr(want), support.ptr(ids), support.ptr(src), lay) == 0
+    dflat, di, ds = kdb.to_device(flat), kdb.to_device(ids), kdb.to_device(src)
+    size = np.dtype(npd).itemsize
+    kdb.call("scatter_add", dtype, dflat.ptr + offset * size, di.ptr, ds.ptr, lay)
+    got = dflat.numpy()[offset:].reshape(data_shape)
+    if dtype == kd.I64:
+        np.testing.assert_array_equal(got, want)
+    else:
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4)
