@@ -317,10 +317,26 @@ __global__ __launch_bounds__(kBlock) void split_kernel(typename C::Acc* partial,
 template <typename C>
 __global__ __launch_bounds__(kBlock) void combine_kernel(typename C::Out* results, const typename C::Acc* partial,
                                                          int64_t segments) {
-    // One workgroup per row: a fixed tree over the segment partials.
+    // One workgroup per row: a fixed tree over the segment partials. Lane t combines partials
+    // t, t + kBlock, t + 2 kBlock, ... in that order; the loads of a batch are all issued before
+    // the first combine, so the partials (just written by other XCDs, read from memory) cost one
+    // round trip per batch instead of one per partial.
+    constexpr int kBatch = 16;
+    using Acc = typename C::Acc;
+    const Acc* row = partial + static_cast<int64_t>(blockIdx.x) * segments;
+    Acc acc = C::identity();
+    for (int64_t s0 = threadIdx.x; s0 < segments; s0 += int64_t{kBlock} * kBatch) {
+        Acc v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int64_t s = s0 + int64_t{u} * kBlock;
+            if (s < segments) v[u] = row[s];
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (s0 + int64_t{u} * kBlock < segments) acc = C::combine(acc, v[u]);
+    }
     const int64_t r = blockIdx.x;
-    typename C::Acc acc = C::identity();
-    for (int64_t s = threadIdx.x; s < segments; s += kBlock) acc = C::combine(acc, partial[r * segments + s]);
     acc = block_reduce<C>(acc);
     if (threadIdx.x == 0) results[r] = C::finish(acc);
 }
