@@ -22,8 +22,9 @@ NP = {kd.F32: np.float32, kd.F64: np.float64, kd.I64: np.int64, kd.BOOL: np.bool
 DTYPES = [kd.F32, kd.F64, kd.I64, kd.BOOL]
 IDS = ["f32", "f64", "i64", "bool"]
 REDUCE_SHAPES = [(1, 1), (3, 7), (1000, 100), (600, 3000), (3, 100000), (1, 2000003)]
+# Includes many short rows ((513, 4), (520, 1000), (600, 2048)) and C2's (4096, 4096).
 SCAN_SHAPES = [(1, 1), (3, 7), (700, 130), (2, 30000), (1, 70001), (2, 1000003), (3, 333333), (64, 4096),
-               (3, 262144)]
+               (3, 262144), (513, 4), (520, 1000), (600, 2048), (4096, 4096)]
 
 
 def sample(dtype, shape, rng, kind):
