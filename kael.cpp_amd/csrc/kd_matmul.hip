@@ -996,6 +996,44 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
         const int64_t b_extent = bt ? p.N * ldb + p.K : p.K * ldb + p.N;
         if (a_extent < kMax && b_extent < kMax && p.M * p.so.r + p.N < kMax && p.so.c == 1 && p.M % kBM == 0 &&
             p.N % kBN == 0 && p.K % kBK == 0) {
+            // Too few tiles to occupy the device, for one product (C4's weight gradient X^T . g:
+            // 256 x 768 outputs, 12 tiles, K = 4096) or for x . W^T over a batch with one shared
+            // weight (kael's Linear: B broadcast, A and the output batches back to back; C4's
+            // 4096 x 256 outputs have 64), whose batch folds into M: K is split, the splits
+            // taking the kernel's batch slot (their K offsets as batch strides) and writing
+            // partial products that split_sum_kernel adds in split order.
+            const int cus = compute_units();
+            const int64_t rows = p.M * p.batches;
+            const int64_t flat_tiles = (rows / kBM) * (p.N / kBN);
+            const bool fold = !at && p.sb.b == 0 && p.sa.b == p.M * lda && p.so.b == p.M * p.so.r;
+            {
+                if ((p.batches == 1 || fold) && flat_tiles * 2 <= cus && p.K >= 256 &&
+                    (at || rows * lda < kMax) && rows * p.so.r < kMax) {
+                    int64_t splits = std::min<int64_t>(p.K / 64, (cus + flat_tiles - 1) / flat_tiles);
+                    while (splits > 1 && p.K % (splits * kBK) != 0) --splits;
+                    const int64_t per = rows * p.N;
+                    if (splits > 1 && splits * per < kMax) {
+                        Workspace ws;  // held until split_sum_kernel is enqueued
+                        if (int rc = workspace(ws, static_cast<size_t>(splits * per) * sizeof(float))) return rc;
+                        const int64_t kc = p.K / splits;
+                        hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>),
+                                           dim3(static_cast<uint32_t>(flat_tiles), static_cast<uint32_t>(splits)),
+                                           dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr),
+                                           static_cast<int>(rows), static_cast<int>(p.N), static_cast<int>(kc),
+                                           static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.N),
+                                           at ? kc * lda : kc, bt ? kc : kc * ldb, per);
+                        KD_LAUNCH_CHECK();
+                        MatmulArgs flat = p;
+                        flat.batches = 1;
+                        flat.M = rows;
+                        const int64_t blocks = std::min<int64_t>((per + kThreads - 1) / kThreads, int64_t{cus} * 16);
+                        hipLaunchKernelGGL(split_sum_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                                           stream(), static_cast<const float*>(ws.ptr), out, flat, splits);
+                        KD_LAUNCH_CHECK();
+                        return KD_OK;
+                    }
+                }
+            }
             hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>), grid, dim3(kThreads), 0, stream(), a, b, out,
                                static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
                                static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r), p.sa.b, p.sb.b,

@@ -12,6 +12,10 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      cross_entropy_losses (:183-210) and
                                      detail::cross_entropy_gradient (:214-240)
   src/autograd/functions_math.cpp    GELU backward without the host round trip (:221-231)
+  src/autograd/functions_linalg.cpp  the gradient of a 2-D weight shared by every batch item of
+                                     the left operand (kael's Linear) as one product over the
+                                     folded batch, X^T . g with K = all tokens, instead of one
+                                     product per batch item and a sum over the batch (:37-44)
   src/ops/linalg.cpp                 multiply_batches reads transposed / broadcast operands in
                                      place (:56-76)
   src/optim/optimizer.cpp            SGD (no momentum, :60-80) and Adam / AdamW (:93-120) update a
@@ -174,6 +178,17 @@ SGD_BRANCH = """        if (options_.momentum == 0.0 && parameter.device() != De
         }
 """
 
+WEIGHT_GRADIENT_BRANCH = """                     if (g.device() != Device::CPU && !layout.left_is_vector && !layout.right_is_vector &&
+                         shape.size() == 2 && left.get().dim() > 2) {
+                         // MI355X: the weight is shared by every batch item, so its gradient is one
+                         // product over the folded batch (K = every row of every item).
+                         const Tensor x = left.get();
+                         const Tensor flat_x = x.reshape({x.numel() / x.size(-1), x.size(-1)});
+                         const Tensor flat_g = g.reshape({g.numel() / g.size(-1), g.size(-1)});
+                         return matmul(flat_x.mT(), flat_g).to(dtype);
+                     }
+"""
+
 REDUCE_HELPERS = """// MI355X: the reductions below run on the device over the same plan as device_reduce.
 Tensor device_prod(const Tensor& t, const Dims& dims, bool keepdim) {
     const Reduction reduction = plan_reduction(t, dims, keepdim);
@@ -260,6 +275,9 @@ EDITS = [
      "before", SGD_BRANCH),
     ("src/optim/optimizer.cpp",
      "        const double second_correction = 1.0 - std::pow(options_.beta2, step);\n", "after", ADAM_BRANCH),
+    ("src/autograd/functions_linalg.cpp",
+     "                     const Tensor gradient = matmul(left.get().mT(), layout.matrix_gradient(g));\n", "before",
+     WEIGHT_GRADIENT_BRANCH),
     ("src/ops/reduce.cpp", "Tensor device_norm(const Tensor& t, const Dims& dims, bool keepdim) {\n", "before",
      REDUCE_HELPERS),
     ("src/ops/reduce.cpp", "Tensor prod(const Tensor& t, const Dims& dims, bool keepdim) {\n", "after", PROD_BRANCH),

@@ -160,6 +160,27 @@ def test_weight_gradient_shape_of_c4(kdb):
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
 
 
+@pytest.mark.parametrize("batches,k,b_t", [(32, 256, True), (32, 1024, True), (32, 1024, False), (1, 512, True)],
+                         ids=["proj-WT", "fc2-WT", "fc2-W", "flat-WT"])
+def test_linear_forward_shapes_of_c4(kdb, batches, k, b_t):
+    """kael's Linear forward x . W^T at C4's narrow outputs (x [32, 128, K], W [256, K] shared by
+    every batch item, reference src/nn/layers.cpp:43): 64 output tiles, so the batch folds into M
+    and K is split over the device, the partial products added in split order. Checked against the
+    float64 product within 1e-4 of its largest |element| (the GPT-2 logits rule), and run twice to
+    check that the result is deterministic."""
+    m, n = 128 * 32 // batches, 256
+    rng = np.random.default_rng(46 + k + b_t)
+    x = rng.uniform(-1, 1, (batches, m, k)).astype(np.float32)
+    w = rng.uniform(-1, 1, (n, k)).astype(np.float32)  # W^T is [k, n]
+    b_store = w if b_t else np.ascontiguousarray(w.T)
+    sb = (0, 1, k) if b_t else (0, n, 1)
+    got = _strided_product(kdb, x, b_store, batches, m, k, n, (m * k, k, 1), sb)
+    again = _strided_product(kdb, x, b_store, batches, m, k, n, (m * k, k, 1), sb)
+    np.testing.assert_array_equal(got, again)
+    want = np.matmul(x.astype(np.float64), w.T.astype(np.float64))
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+
+
 def test_headline_4096_cubed(kdb, refdev):
     """The benchmark's headline product (row-major MFMA kernel, whole tiles) at its full size,
     inputs as bench.py draws them. At K = 4096 an element's f32 rounding error scales with its
