@@ -805,8 +805,19 @@ __global__ __launch_bounds__(kThreads) void split_sum_kernel(const float* __rest
          idx += static_cast<int64_t>(gridDim.x) * kThreads) {
         const int64_t batch = idx / per_batch;
         const int64_t mn = idx % per_batch;
+        // The partials come from memory (written by other XCDs): a batch of them is loaded before
+        // the first add, one round trip per batch; they are added in split order.
+        constexpr int kBatch = 8;
         float v = 0.f;
-        for (int64_t s = 0; s < splits; ++s) v += partial[(batch * splits + s) * per_batch + mn];
+        for (int64_t s0 = 0; s0 < splits; s0 += kBatch) {
+            float x[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s0 + u < splits) x[u] = partial[(batch * splits + s0 + u) * per_batch + mn];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s0 + u < splits) v += x[u];
+        }
         const int64_t m = mn / p.N;
         const int64_t n = mn % p.N;
         out[batch * p.so.b + m * p.so.r + n * p.so.c] = v;
