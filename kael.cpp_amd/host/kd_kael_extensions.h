@@ -6,8 +6,8 @@
 // host (prod, all, any, argmax / argmin, cumsum).
 //
 // Defined in backend_hip.cpp. Unmodified kael never calls them; the device branches that do are
-// the optional kael patches listed in INTEGRATION.md (a one-line include of this header at the
-// end of kael/device_kernels.h, and a device branch at each site).
+// optional kael patches (a one-line include of this header at the end of kael/device_kernels.h,
+// and a device branch at each site; oracle/kael_fused.py holds them as anchored insertions).
 #pragma once
 
 #include <cstddef>

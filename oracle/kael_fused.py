@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE: the reference's sources are read where they lie under /root/reference and
 the patched copies are written only to oracle/_ref/fused/ (git-ignored); nothing here ships.
-It applies the kael-side patches that INTEGRATION.md lists, so that the tests can run kael's
+It applies the optional kael-side patches (one device branch per site), so that the tests can run kael's
 training configs with kael's own host code calling the backend's fused entry points
 (kael.cpp_amd/host/kd_kael_extensions.h):
 
