@@ -179,9 +179,11 @@ SGD_BRANCH = """        if (options_.momentum == 0.0 && parameter.device() != De
 """
 
 WEIGHT_GRADIENT_BRANCH = """                     if (g.device() != Device::CPU && !layout.left_is_vector && !layout.right_is_vector &&
-                         shape.size() == 2 && left.get().dim() > 2) {
+                         shape.size() == 2 && left.get().dim() > 2 && left.get().size(-1) > 0 &&
+                         g.size(-1) > 0) {
                          // MI355X: the weight is shared by every batch item, so its gradient is one
-                         // product over the folded batch (K = every row of every item).
+                         // product over the folded batch (K = every row of every item). An empty
+                         // last dim keeps kael's per-item path (the fold would divide by zero).
                          const Tensor x = left.get();
                          const Tensor flat_x = x.reshape({x.numel() / x.size(-1), x.size(-1)});
                          const Tensor flat_g = g.reshape({g.numel() / g.size(-1), g.size(-1)});
