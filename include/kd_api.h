@@ -194,6 +194,7 @@ int kd_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout*
 int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
               int64_t chunk_size, int64_t output_count);
 
+
 /* Replaces the host round trip of reference src/ops/reduce.cpp:399-421 `argmax` / `argmin`
  * (`on_host` + `arg_extreme`, :256-268, `best_position`, :236-254): results[r] = the index
  * in [0, chunk_size) of the first largest (largest != 0) or first smallest element of
@@ -266,6 +267,25 @@ int kd_cross_entropy_rows(int dtype, void* losses, const void* logits, const int
  * Follows reference src/ops/nn.cpp:214-240 (CPU only in the reference). */
 int kd_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
                           const void* row_weights, int64_t rows, int64_t cols);
+
+/* Backward of kd_softmax_rows over `rows` contiguous rows of `cols`: from the forward output y and
+ * the incoming gradient g, out = y * (g - sum(g * y)) (softmax) or out = g - exp(y) * sum(g)
+ * (log_softmax != 0), each element op rounded to the element type and each row sum accumulated in
+ * double and rounded, as kael's composed device ops round them. Replaces SoftmaxBackward and
+ * LogSoftmaxBackward of reference src/autograd/functions_reduce.cpp:150-164 (3-4 launches each
+ * plus temporaries). dtype f32 or f64; out may not alias y or g. */
+int kd_softmax_rows_backward(int dtype, void* out, const void* y, const void* grad, int64_t rows,
+                             int64_t cols, int log_softmax);
+
+/* Backward of kd_standardize_rows (without the affine step) over `rows` contiguous rows of `cols`:
+ * from the input x, the forward output y and the incoming gradient g,
+ * out = ((g - mean(g)) - y * mean(g * y)) / sqrt(var(x) + eps), with mean = sum / n and the
+ * population variance sum((x - mean(x))^2) / n, every element op rounded to the element type and
+ * every sum accumulated in double and rounded, as kael's composed device ops round them. Replaces
+ * StandardizeBackward of reference src/autograd/functions_reduce.cpp:176-192 (~12 launches).
+ * dtype f32 or f64; out may not alias x, y or g. */
+int kd_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,
+                                 int64_t rows, int64_t cols, double eps);
 
 /* ---- optimizer steps (extensions replacing composed device paths) ------ */
 

@@ -459,6 +459,185 @@ int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double ep
     return KD_OK;
 }
 
+// ---- backward passes of softmax, log_softmax and standardize ----------------------------------------
+//
+// kael composes each backward from whole-tensor device ops (reference
+// src/autograd/functions_reduce.cpp:150-192), every op rounded to T and every row sum accumulated
+// in double and rounded to T (src/ops/reduce.cpp:308-342):
+//   softmax      y * (g - sum(g * y))
+//   log_softmax  g - exp(y) * sum(g)
+//   standardize  ((g - mean(g)) - y * mean(g * y)) / sqrt(var(x) + eps), mean = sum / T(n),
+//                var = sum((x - mean(x))^2) / T(n) (population variance; each square rounded to T)
+// These kernels keep that rounding sequence and fuse it into one pass over the row (plus a second
+// pass over x in registers for the variance): only the order of the double sums differs.
+enum BackOp { kSoftmaxBack = 0, kLogSoftmaxBack = 1, kStandardizeBack = 2 };
+
+template <typename T> struct BackSums {
+    double s1 = 0.0, s2 = 0.0, s3 = 0.0;  // softmax: sum(g*y); log_softmax: sum(g); standardize: sum(x), sum(g), sum(g*y)
+};
+
+template <int Op, typename T> __device__ __forceinline__ void back_accumulate(BackSums<T>& s, T x, T y, T g) {
+    if constexpr (Op == kSoftmaxBack) {
+        s.s1 += static_cast<double>(mul_rn(g, y));
+    } else if constexpr (Op == kLogSoftmaxBack) {
+        s.s1 += static_cast<double>(g);
+    } else {
+        s.s1 += static_cast<double>(x);
+        s.s2 += static_cast<double>(g);
+        s.s3 += static_cast<double>(mul_rn(g, y));
+    }
+}
+
+// The per-row scalars of the output formula once the sums are complete.
+template <typename T> struct BackScalars {
+    T s;      // softmax: sum(g*y); log_softmax: sum(g); standardize: mean(x)
+    T mg;     // standardize: mean(g)
+    T mgy;    // standardize: mean(g*y)
+    T scale;  // standardize: sqrt(var(x) + eps), set after the variance pass
+};
+
+template <int Op, typename T> __device__ __forceinline__ T back_output(const BackScalars<T>& k, T y, T g) {
+    if constexpr (Op == kSoftmaxBack) {
+        return mul_rn(y, sub_rn(g, k.s));
+    } else if constexpr (Op == kLogSoftmaxBack) {
+        return sub_rn(g, mul_rn(static_cast<T>(std::exp(y)), k.s));
+    } else {
+        return div_rn(sub_rn(sub_rn(g, k.mg), mul_rn(y, k.mgy)), k.scale);
+    }
+}
+
+template <int Op, typename T> __device__ __forceinline__ BackScalars<T> back_scalars(const BackSums<T>& s, int64_t cols) {
+    BackScalars<T> k{};
+    k.s = static_cast<T>(s.s1);
+    if constexpr (Op == kStandardizeBack) {
+        const T n = static_cast<T>(cols);
+        k.s = div_rn(static_cast<T>(s.s1), n);
+        k.mg = div_rn(static_cast<T>(s.s2), n);
+        k.mgy = div_rn(static_cast<T>(s.s3), n);
+    }
+    return k;
+}
+
+template <typename T> __device__ __forceinline__ T back_scale(double squares, int64_t cols, double eps) {
+    const T var = div_rn(static_cast<T>(squares), static_cast<T>(cols));
+    return static_cast<T>(std::sqrt(add_rn(var, static_cast<T>(eps))));
+}
+
+// One wave per row of cols <= 1024 (cols % 4 == 0, 16-byte aligned rows): the row's y, g (and x)
+// are held in registers; one read of each input, one write.
+template <typename T, int V4, int Op, bool NT>
+__global__ __launch_bounds__(kThreads) void row_backward_wave4_kernel(T* __restrict__ out, const T* __restrict__ xin,
+                                                                      const T* __restrict__ yin,
+                                                                      const T* __restrict__ gin, int64_t rows,
+                                                                      int64_t cols, double eps) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    const int64_t base = row * cols;
+    Quad<T> y[V4], g[V4], x[V4];
+    BackSums<T> s;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+            y[j] = ld4<NT>(yin + base + c);
+            g[j] = ld4<NT>(gin + base + c);
+            if constexpr (Op == kStandardizeBack) x[j] = ld4<NT>(xin + base + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) back_accumulate<Op>(s, Op == kStandardizeBack ? x[j].v[e] : T(0), y[j].v[e], g[j].v[e]);
+        }
+    }
+    s.s1 = wave_sum(s.s1);
+    if constexpr (Op == kStandardizeBack) {
+        s.s2 = wave_sum(s.s2);
+        s.s3 = wave_sum(s.s3);
+    }
+    BackScalars<T> k = back_scalars<Op>(s, cols);
+    if constexpr (Op == kStandardizeBack) {
+        double squares = 0.0;
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+            const int64_t c = 4 * (lane + 64 * j);
+            if (c < cols) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const T d = sub_rn(x[j].v[e], k.s);
+                    squares += static_cast<double>(mul_rn(d, d));
+                }
+            }
+        }
+        k.scale = back_scale<T>(wave_sum(squares), cols, eps);
+    }
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
+            Quad<T> o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o.v[e] = back_output<Op>(k, y[j].v[e], g[j].v[e]);
+            st4<NT>(out + base + c, o);
+        }
+    }
+}
+
+// Any row length and alignment: a workgroup per row, the row read from memory once per pass
+// (later passes hit the L2 for rows that fit).
+template <typename T, int Op>
+__global__ __launch_bounds__(kThreads) void row_backward_block_kernel(T* __restrict__ out, const T* __restrict__ xin,
+                                                                      const T* __restrict__ yin,
+                                                                      const T* __restrict__ gin, int64_t rows,
+                                                                      int64_t cols, double eps) {
+    __shared__ double tsum[kThreads / 64];
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const int64_t base = row * cols;
+        BackSums<T> s;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads)
+            back_accumulate<Op>(s, Op == kStandardizeBack ? xin[base + c] : T(0), yin[base + c], gin[base + c]);
+        s.s1 = block_sum(s.s1, tsum);
+        if constexpr (Op == kStandardizeBack) {
+            s.s2 = block_sum(s.s2, tsum);
+            s.s3 = block_sum(s.s3, tsum);
+        }
+        BackScalars<T> k = back_scalars<Op>(s, cols);
+        if constexpr (Op == kStandardizeBack) {
+            double squares = 0.0;
+            for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+                const T d = sub_rn(xin[base + c], k.s);
+                squares += static_cast<double>(mul_rn(d, d));
+            }
+            k.scale = back_scale<T>(block_sum(squares, tsum), cols, eps);
+        }
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) out[base + c] = back_output<Op>(k, yin[base + c], gin[base + c]);
+    }
+}
+
+template <typename T, int Op>
+int row_backward_typed(T* out, const T* x, const T* y, const T* g, int64_t rows, int64_t cols, double eps) {
+    if (rows == 0 || cols == 0) return KD_OK;
+    const dim3 block(kThreads);
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool quads = cols % 4 == 0 && cols <= 1024 && aligned(out) && aligned(y) && aligned(g) &&
+                       (Op != kStandardizeBack || aligned(x));
+    if (quads) {
+        if ((rows + 3) / 4 > int64_t{0xffffffff}) return fail(KD_E_INVALID, "row backward: too many rows");
+        const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
+        const bool nt = rows * cols * static_cast<int64_t>(sizeof(T)) >= (int64_t{16} << 20);
+#define KD_BACK4(V4)                                                                                                  \
+    if (nt) hipLaunchKernelGGL((row_backward_wave4_kernel<T, V4, Op, true>), grid, block, 0, stream(), out, x, y, g, rows, cols, eps); \
+    else hipLaunchKernelGGL((row_backward_wave4_kernel<T, V4, Op, false>), grid, block, 0, stream(), out, x, y, g, rows, cols, eps);
+        if (cols <= 256) { KD_BACK4(1) }
+        else if (cols <= 512) { KD_BACK4(2) }
+        else { KD_BACK4(4) }
+#undef KD_BACK4
+    } else {
+        const int64_t blocks = std::min<int64_t>(rows, int64_t{compute_units()} * 32);
+        hipLaunchKernelGGL((row_backward_block_kernel<T, Op>), dim3(static_cast<uint32_t>(blocks)), block, 0, stream(), out,
+                           x, y, g, rows, cols, eps);
+    }
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
 int check_rows(int dtype, int64_t rows, int64_t cols) {
     if (dtype != KD_F32 && dtype != KD_F64) return fail(KD_E_INVALID, "row kernel: dtype must be f32 or f64");
     if (rows < 0 || cols < 0) return fail(KD_E_INVALID, "row kernel: negative size");
@@ -518,4 +697,37 @@ extern "C" int kd_cross_entropy_grad(int dtype, void* out, const void* logits, c
                                                         static_cast<const float*>(row_weights), rows, cols);
     return softmax_family<double, kCrossEntropyGrad>(static_cast<double*>(out), static_cast<const double*>(logits), targets,
                                                      static_cast<const double*>(row_weights), rows, cols);
+}
+
+extern "C" int kd_softmax_rows_backward(int dtype, void* out, const void* y, const void* grad, int64_t rows,
+                                        int64_t cols, int log_softmax) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (rows == 0 || cols == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32) {
+        auto* o = static_cast<float*>(out);
+        const auto* yy = static_cast<const float*>(y);
+        const auto* gg = static_cast<const float*>(grad);
+        return log_softmax ? row_backward_typed<float, kLogSoftmaxBack>(o, nullptr, yy, gg, rows, cols, 0.0)
+                           : row_backward_typed<float, kSoftmaxBack>(o, nullptr, yy, gg, rows, cols, 0.0);
+    }
+    auto* o = static_cast<double*>(out);
+    const auto* yy = static_cast<const double*>(y);
+    const auto* gg = static_cast<const double*>(grad);
+    return log_softmax ? row_backward_typed<double, kLogSoftmaxBack>(o, nullptr, yy, gg, rows, cols, 0.0)
+                       : row_backward_typed<double, kSoftmaxBack>(o, nullptr, yy, gg, rows, cols, 0.0);
+}
+
+extern "C" int kd_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,
+                                            int64_t rows, int64_t cols, double eps) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (rows == 0 || cols == 0) return KD_OK;
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32)
+        return row_backward_typed<float, kStandardizeBack>(static_cast<float*>(out), static_cast<const float*>(x),
+                                                          static_cast<const float*>(y), static_cast<const float*>(grad),
+                                                          rows, cols, eps);
+    return row_backward_typed<double, kStandardizeBack>(static_cast<double*>(out), static_cast<const double*>(x),
+                                                       static_cast<const double*>(y), static_cast<const double*>(grad),
+                                                       rows, cols, eps);
 }

@@ -136,6 +136,18 @@ void cross_entropy_grad(DType dtype, std::byte* out, const std::byte* logits, co
           "cross_entropy_grad");
 }
 
+void softmax_rows_backward(DType dtype, std::byte* out, const std::byte* y, const std::byte* grad, std::int64_t rows,
+                           std::int64_t cols, bool log) {
+    check(kd_softmax_rows_backward(static_cast<int>(dtype), out, y, grad, rows, cols, log ? 1 : 0),
+          "softmax_rows_backward");
+}
+
+void standardize_rows_backward(DType dtype, std::byte* out, const std::byte* x, const std::byte* y,
+                               const std::byte* grad, std::int64_t rows, std::int64_t cols, double eps) {
+    check(kd_standardize_rows_backward(static_cast<int>(dtype), out, x, y, grad, rows, cols, eps),
+          "standardize_rows_backward");
+}
+
 ElementOp gelu_backward_op(bool approximate) {
     return static_cast<ElementOp>(approximate ? KD_OP_GELU_TANH_BACKWARD : KD_OP_GELU_EXACT_BACKWARD);
 }

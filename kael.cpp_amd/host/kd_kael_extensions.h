@@ -36,6 +36,17 @@ void cross_entropy_rows(DType dtype, std::byte* losses, const std::byte* logits,
 void cross_entropy_grad(DType dtype, std::byte* out, const std::byte* logits, const std::int64_t* targets,
                         const std::byte* row_weights, std::int64_t rows, std::int64_t cols);
 
+// Backward of softmax_rows from its output y and the incoming gradient: y * (g - sum(g * y)), or
+// g - exp(y) * sum(g) when `log` (reference src/autograd/functions_reduce.cpp:150-164).
+void softmax_rows_backward(DType dtype, std::byte* out, const std::byte* y, const std::byte* grad, std::int64_t rows,
+                           std::int64_t cols, bool log);
+
+// Backward of standardize_rows from its input x, output y and the incoming gradient:
+// ((g - mean(g)) - y * mean(g * y)) / sqrt(var(x) + eps) (reference
+// src/autograd/functions_reduce.cpp:176-192).
+void standardize_rows_backward(DType dtype, std::byte* out, const std::byte* x, const std::byte* y,
+                               const std::byte* grad, std::int64_t rows, std::int64_t cols, double eps);
+
 // The element op computing grad * d/dx gelu(x) over operands (out, x, grad), tanh form when
 // `approximate` (reference src/autograd/functions_math.cpp:35-46 slopes).
 ElementOp gelu_backward_op(bool approximate);

@@ -112,6 +112,9 @@ SIGNATURES = {
     "standardize_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "cross_entropy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
     "cross_entropy_grad": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),
+    "softmax_rows_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int]),
+    "standardize_rows_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                          c_double]),
     "adam_step": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_double, c_double, c_double,
                           c_double, c_double, c_int, c_int64]),
     "sgd_step": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_double, c_double]),

@@ -12,6 +12,9 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      cross_entropy_losses (:183-210) and
                                      detail::cross_entropy_gradient (:214-240)
   src/autograd/functions_math.cpp    GELU backward without the host round trip (:221-231)
+  src/autograd/functions_reduce.cpp  SoftmaxBackward / LogSoftmaxBackward along the last dim
+                                     (:150-164) and StandardizeBackward (:176-192) as one row
+                                     kernel each
   src/autograd/functions_linalg.cpp  the gradient of a 2-D weight shared by every batch item of
                                      the left operand (kael's Linear) as one product over the
                                      folded batch, X^T . g with K = all tokens, instead of one
@@ -251,6 +254,52 @@ CUMSUM_BRANCH = """    if (t.device() != Device::CPU) {
     }
 """
 
+ROW_BACKWARD_HELPERS = """// MI355X: the backward passes of softmax / log_softmax along the last dim and of standardize as
+// one row kernel each; no value when the operands do not fit (kael's composed path runs then).
+std::optional<Tensor> fused_softmax_backward(const Tensor& y, const Tensor& g, std::int64_t dim, bool log) {
+    if (y.device() == Device::CPU || !is_floating_point(y.dtype()) || g.dtype() != y.dtype() || y.dim() == 0 ||
+        y.numel() == 0 || g.shape() != y.shape() || wrap_dim(dim, y.dim()) != y.dim() - 1) {
+        return std::nullopt;
+    }
+    const Tensor ys = y.contiguous();
+    const Tensor gs = g.contiguous();
+    Tensor out = empty(y.shape(), y.dtype(), y.device());
+    device::softmax_rows_backward(y.dtype(), out.device_data(), ys.device_data(), gs.device_data(),
+                                  y.numel() / y.size(-1), y.size(-1), log);
+    return out;
+}
+
+std::optional<Tensor> fused_standardize_backward(const Tensor& x, const Tensor& y, const Tensor& g,
+                                                 std::int64_t normalized_dims, double eps) {
+    if (y.device() == Device::CPU || !is_floating_point(y.dtype()) || x.dtype() != y.dtype() ||
+        g.dtype() != y.dtype() || y.numel() == 0 || x.shape() != y.shape() || g.shape() != y.shape()) {
+        return std::nullopt;
+    }
+    std::int64_t row_size = 1;
+    for (std::int64_t i = 1; i <= normalized_dims; ++i) {
+        row_size *= y.size(-i);
+    }
+    const Tensor xs = x.contiguous();
+    const Tensor ys = y.contiguous();
+    const Tensor gs = g.contiguous();
+    Tensor out = empty(y.shape(), y.dtype(), y.device());
+    device::standardize_rows_backward(y.dtype(), out.device_data(), xs.device_data(), ys.device_data(),
+                                      gs.device_data(), y.numel() / row_size, row_size, eps);
+    return out;
+}
+
+"""
+
+SOFTMAX_BACKWARD_BRANCH = """                        if (auto fused = fused_softmax_backward(y.get(), g, dim, %s)) {
+                            return *fused;
+                        }
+"""
+
+STANDARDIZE_BACKWARD_BRANCH = """                if (auto fused = fused_standardize_backward(saved.get(), y.get(), g, normalized_dims, eps)) {
+                    return *fused;
+                }
+"""
+
 # (relative path, anchor line(s), where, text). where: "before", "after", "replace", "append".
 EDITS = [
     ("include/kael/device_kernels.h", None, "append", '\n#include "kd_kael_extensions.h"\n'),
@@ -295,6 +344,19 @@ EDITS = [
      ARG_BRANCH % ("t.flatten(), {0}, false", "false", '"argmin"')),
     ("src/ops/reduce.cpp", "Tensor argmin(const Tensor& t, std::int64_t dim, bool keepdim) {\n", "after",
      ARG_BRANCH % ("t, {dim}, keepdim", "false", '"argmin"')),
+    ("src/autograd/functions_reduce.cpp", "#include <algorithm>\n", "after", "#include <optional>\n"),
+    ("src/autograd/functions_reduce.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/autograd/functions_reduce.cpp", "Dims resolved_dims(const Shape& shape, const Dims& dims) {\n", "before",
+     ROW_BACKWARD_HELPERS),
+    ("src/autograd/functions_reduce.cpp",
+     "                        return y.get() * (g - kael::sum(g * y.get(), {dim}, true));\n", "before",
+     SOFTMAX_BACKWARD_BRANCH % "false"),
+    ("src/autograd/functions_reduce.cpp",
+     "                        return g - kael::exp(y.get()) * kael::sum(g, {dim}, true);\n", "before",
+     SOFTMAX_BACKWARD_BRANCH % "true"),
+    ("src/autograd/functions_reduce.cpp",
+     "                const Tensor scale = kael::sqrt(kael::var(saved.get(), dims, true, 0) + eps);\n", "before",
+     STANDARDIZE_BACKWARD_BRANCH),
     ("src/ops/sequence.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/ops/sequence.cpp", "        return t.to(dtype).clone();\n    }\n", "after", CUMSUM_BRANCH),
 ]

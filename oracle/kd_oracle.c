@@ -991,6 +991,118 @@ int oracle_cross_entropy_grad(int dtype, void* out, const void* logits, const in
     return KD_OK;
 }
 
+/* ---- row backward passes: src/autograd/functions_reduce.cpp:150-192 ----------------------------
+ *
+ * kael composes them from whole-tensor device ops; each element op rounds to T (ISO C: no
+ * contraction), each row sum is device::reduce Sum: double accumulation in the order of
+ * kernels.inl:278-307 (sequential for rows of <= 4096 elements, else sequential 4096-element
+ * blocks merged pairwise), rounded to T. mean = sum / T(n) (src/ops/reduce.cpp:330-335);
+ * var = sum((x - mean)^2) / T(n) with correction 0 (:337-343). */
+
+#define ROW_BACKWARD(T, SUFFIX, EXPF, SQRTF)                                                        \
+    static double device_row_sum_##SUFFIX(const T* v, int64_t n) {                               \
+        if (n <= 4096) {                                                                         \
+            double total = 0.0;                                                                  \
+            for (int64_t i = 0; i < n; ++i) total += (double)v[i];                               \
+            return total;                                                                        \
+        }                                                                                        \
+        const int64_t blocks = (n + 4095) / 4096;                                                \
+        double* partial = (double*)malloc((size_t)blocks * sizeof(double));                      \
+        for (int64_t b = 0; b < blocks; ++b) {                                                   \
+            const int64_t end = (b + 1) * 4096 < n ? (b + 1) * 4096 : n;                         \
+            double total = 0.0;                                                                  \
+            for (int64_t i = b * 4096; i < end; ++i) total += (double)v[i];                      \
+            partial[b] = total;                                                                  \
+        }                                                                                        \
+        for (int64_t width = blocks; width > 1; width = (width + 1) / 2)                         \
+            for (int64_t i = 0; i < (width + 1) / 2; ++i)                                        \
+                partial[i] = 2 * i + 1 < width ? partial[2 * i] + partial[2 * i + 1] : partial[2 * i]; \
+        const double total = partial[0];                                                         \
+        free(partial);                                                                           \
+        return total;                                                                            \
+    }                                                                                            \
+    /* y * (g - sum(g * y)) or g - exp(y) * sum(g); `tmp` holds n elements */                    \
+    static void softmax_backward_row_##SUFFIX(const T* y, const T* g, T* out, T* tmp, int64_t n, \
+                                              int log_softmax) {                                 \
+        if (log_softmax) {                                                                       \
+            const T s = (T)device_row_sum_##SUFFIX(g, n);                                        \
+            for (int64_t i = 0; i < n; ++i) {                                                    \
+                const T t = EXPF(y[i]) * s;                                                      \
+                out[i] = g[i] - t;                                                               \
+            }                                                                                    \
+        } else {                                                                                 \
+            for (int64_t i = 0; i < n; ++i) tmp[i] = g[i] * y[i];                                \
+            const T s = (T)device_row_sum_##SUFFIX(tmp, n);                                      \
+            for (int64_t i = 0; i < n; ++i) {                                                    \
+                const T d = g[i] - s;                                                            \
+                out[i] = y[i] * d;                                                               \
+            }                                                                                    \
+        }                                                                                        \
+    }                                                                                            \
+    /* ((g - mean(g)) - y * mean(g * y)) / sqrt(var(x) + eps) */                                 \
+    static void standardize_backward_row_##SUFFIX(const T* x, const T* y, const T* g, T* out,    \
+                                                  T* tmp, int64_t n, double eps) {               \
+        const T count = (T)n;                                                                    \
+        const T mean = (T)device_row_sum_##SUFFIX(x, n) / count;                                 \
+        for (int64_t i = 0; i < n; ++i) {                                                        \
+            const T d = x[i] - mean;                                                             \
+            tmp[i] = d * d;                                                                      \
+        }                                                                                        \
+        const T var = (T)device_row_sum_##SUFFIX(tmp, n) / count;                                \
+        const T shifted = var + (T)eps;                                                          \
+        const T scale = SQRTF(shifted);                                                          \
+        const T mg = (T)device_row_sum_##SUFFIX(g, n) / count;                                   \
+        for (int64_t i = 0; i < n; ++i) tmp[i] = g[i] * y[i];                                    \
+        const T mgy = (T)device_row_sum_##SUFFIX(tmp, n) / count;                                \
+        for (int64_t i = 0; i < n; ++i) {                                                        \
+            const T centered = g[i] - mg;                                                        \
+            const T along = y[i] * mgy;                                                          \
+            const T diff = centered - along;                                                     \
+            out[i] = diff / scale;                                                               \
+        }                                                                                        \
+    }
+
+ROW_BACKWARD(float, f32, expf, sqrtf)
+ROW_BACKWARD(double, f64, exp, sqrt)
+
+int oracle_softmax_rows_backward(int dtype, void* out, const void* y, const void* grad, int64_t rows,
+                                 int64_t cols, int log_softmax) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    if (rows < 0 || cols < 0) return fail("softmax backward: negative size");
+    if (rows == 0 || cols == 0) return KD_OK;
+    void* tmp = malloc((size_t)cols * 8);
+    for (int64_t r = 0; r < rows; ++r) {
+        if (dtype == KD_F32)
+            softmax_backward_row_f32((const float*)y + r * cols, (const float*)grad + r * cols,
+                                     (float*)out + r * cols, (float*)tmp, cols, log_softmax);
+        else
+            softmax_backward_row_f64((const double*)y + r * cols, (const double*)grad + r * cols,
+                                     (double*)out + r * cols, (double*)tmp, cols, log_softmax);
+    }
+    free(tmp);
+    return KD_OK;
+}
+
+int oracle_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,
+                                     int64_t rows, int64_t cols, double eps) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    if (rows < 0 || cols < 0) return fail("standardize backward: negative size");
+    if (rows == 0 || cols == 0) return KD_OK;
+    void* tmp = malloc((size_t)cols * 8);
+    for (int64_t r = 0; r < rows; ++r) {
+        if (dtype == KD_F32)
+            standardize_backward_row_f32((const float*)x + r * cols, (const float*)y + r * cols,
+                                         (const float*)grad + r * cols, (float*)out + r * cols, (float*)tmp,
+                                         cols, eps);
+        else
+            standardize_backward_row_f64((const double*)x + r * cols, (const double*)y + r * cols,
+                                         (const double*)grad + r * cols, (double*)out + r * cols,
+                                         (double*)tmp, cols, eps);
+    }
+    free(tmp);
+    return KD_OK;
+}
+
 /* ---- optimizer steps: src/optim/optimizer.cpp:60-80 (SGD), :93-120 (AdamBase::update) ------ */
 
 /* Each statement is one of kael's whole-tensor ops, rounded to the element type (ISO C: no

@@ -45,6 +45,10 @@ int oracle_cross_entropy_rows(int dtype, void* losses, const void* logits, const
                               int64_t rows, int64_t cols);
 int oracle_cross_entropy_grad(int dtype, void* out, const void* logits, const int64_t* targets,
                               const void* row_weights, int64_t rows, int64_t cols);
+int oracle_softmax_rows_backward(int dtype, void* out, const void* y, const void* grad, int64_t rows,
+                                 int64_t cols, int log_softmax);
+int oracle_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,
+                                     int64_t rows, int64_t cols, double eps);
 int oracle_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
                      double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
                      int decoupled, int64_t step);

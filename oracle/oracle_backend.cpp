@@ -88,8 +88,8 @@ void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, cons
 namespace {
 // 0 softmax_rows, 1 standardize_rows, 2 cross_entropy_rows, 3 cross_entropy_grad,
 // 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
-// 9 arg_reduce, 10 cumsum_rows.
-constexpr int kExtensions = 11;
+// 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward.
+constexpr int kExtensions = 13;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -116,6 +116,20 @@ void cross_entropy_grad(DType dtype, std::byte* out, const std::byte* logits, co
     ++g_extension_calls[3];
     check(oracle_cross_entropy_grad(static_cast<int>(dtype), out, logits, targets, row_weights, rows, cols),
           "cross_entropy_grad");
+}
+
+void softmax_rows_backward(DType dtype, std::byte* out, const std::byte* y, const std::byte* grad, std::int64_t rows,
+                           std::int64_t cols, bool log) {
+    ++g_extension_calls[11];
+    check(oracle_softmax_rows_backward(static_cast<int>(dtype), out, y, grad, rows, cols, log ? 1 : 0),
+          "softmax_rows_backward");
+}
+
+void standardize_rows_backward(DType dtype, std::byte* out, const std::byte* x, const std::byte* y,
+                               const std::byte* grad, std::int64_t rows, std::int64_t cols, double eps) {
+    ++g_extension_calls[12];
+    check(oracle_standardize_rows_backward(static_cast<int>(dtype), out, x, y, grad, rows, cols, eps),
+          "standardize_rows_backward");
 }
 
 ElementOp gelu_backward_op(bool approximate) {

@@ -371,6 +371,17 @@ int ref_gpt_param(void* handle, int64_t i, char* name, int len, int64_t* shape, 
     });
 }
 
+// Overwrites parameter i (the model on the CPU) with `data`, all of its elements in row-major
+// order: a model with weights from elsewhere (the benchmark's own random init).
+int ref_gpt_set_param(void* handle, int64_t i, const float* data) {
+    return guarded([&] {
+        kael::Tensor t = static_cast<RefGpt*>(handle)->named.at(static_cast<std::size_t>(i)).second;
+        if (t.device() != kael::Device::CPU || !t.is_contiguous() || t.dtype() != kael::DType::F32)
+            throw std::runtime_error("ref_gpt_set_param: the parameter is not a contiguous f32 CPU tensor");
+        std::memcpy(t.data_ptr_raw(), data, static_cast<std::size_t>(t.numel()) * sizeof(float));
+    });
+}
+
 // Full forward (no cache) of `tokens` [batch, length]; logits [batch, length, vocab].
 int ref_gpt_forward(void* handle, const int64_t* tokens, int64_t batch, int64_t length,
                     float* logits) {
@@ -698,8 +709,19 @@ int ref_optim_steps(int kind, int device, int dtype, int64_t n, int64_t steps, c
 // ids = randint(0,vocab,{batch,context}), targets = randint(0,vocab,{batch*context}); forward,
 // cross-entropy, backward, Adam (defaults). Writes each step's loss and the seconds.
 // ref_train_chargpt is config C4: {vocab 96, context 128, 4 layers, 4 heads, dim 256}, batch 32.
+int ref_train_gpt_params(int device, int64_t steps, int64_t vocab, int64_t context, int64_t layers, int64_t heads,
+                         int64_t dimension, int64_t batch, float* losses, float* params_out, double* seconds);
+
 int ref_train_gpt(int device, int64_t steps, int64_t vocab, int64_t context, int64_t layers, int64_t heads,
                   int64_t dimension, int64_t batch, float* losses, double* seconds) {
+    return ref_train_gpt_params(device, steps, vocab, context, layers, heads, dimension, batch, losses, nullptr,
+                                seconds);
+}
+
+// ref_train_gpt that also writes the flattened final parameters (GPT::parameters() order) when
+// params_out is non-NULL.
+int ref_train_gpt_params(int device, int64_t steps, int64_t vocab, int64_t context, int64_t layers, int64_t heads,
+                         int64_t dimension, int64_t batch, float* losses, float* params_out, double* seconds) {
     return guarded([&] {
         const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
         kael::manual_seed(3);
@@ -725,6 +747,68 @@ int ref_train_gpt(int device, int64_t steps, int64_t vocab, int64_t context, int
         }
         const auto t1 = std::chrono::steady_clock::now();
         *seconds = std::chrono::duration<double>(t1 - t0).count();
+        if (params_out != nullptr) {
+            const std::vector<float> flat = flat_parameters(model.parameters());
+            std::memcpy(params_out, flat.data(), flat.size() * sizeof(float));
+        }
+    });
+}
+
+// Number of parameters of the GPT that ref_train_gpt_params builds (the size of params_out).
+int64_t ref_gpt_param_total(int64_t vocab, int64_t context, int64_t layers, int64_t heads, int64_t dimension) {
+    int64_t total = -1;
+    guarded([&] {
+        kael::nn::GptConfig config;
+        config.vocab_size = vocab;
+        config.max_positions = context;
+        config.layers = layers;
+        config.heads = heads;
+        config.dimension = dimension;
+        kael::nn::GPT model(config);
+        total = 0;
+        for (const kael::Tensor& p : model.parameters()) total += p.numel();
+    });
+    return total;
+}
+
+// The gradient of a row op through kael's autograd on `device` (0 CPU, 1 the linked device
+// backend): x [rows, cols] (dtype 0 f32, 1 f64) requires grad, y = softmax(x, -1) (kind 0),
+// log_softmax(x, -1) (kind 1) or standardize(x, 1, eps) (kind 2), and sum(y * g).backward() hands
+// exactly g to y's backward; writes x.grad, and y when y_out is non-NULL.
+int ref_row_grad(int kind, int device, int dtype, const void* x, const void* g, int64_t rows, int64_t cols, double eps,
+                 void* grad_out, void* y_out) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        const kael::DType dt = dtype == 0 ? kael::DType::F32 : kael::DType::F64;
+        kael::Tensor xt = host_tensor(x, {rows, cols}, dt).to(dev);
+        xt.requires_grad_(true);
+        const kael::Tensor gt = host_tensor(g, {rows, cols}, dt).to(dev);
+        const kael::Tensor y = kind == 0   ? kael::softmax(xt, -1)
+                               : kind == 1 ? kael::log_softmax(xt, -1)
+                                           : kael::standardize(xt, 1, eps);
+        kael::sum(y * gt).backward();
+        copy_out(xt.grad()->cpu(), grad_out);
+        if (y_out != nullptr) copy_out(y.detach().cpu(), y_out);
+    });
+}
+
+// Gradients of a Linear-shaped product through kael's autograd on `device`: manual_seed(seed);
+// x = rand({batch, m, k}) * 2 - 1, w = (rand({n, k}) * 2 - 1) * 0.05, gout = rand({batch, m, n}) * 2 - 1;
+// y = matmul(x, w.T()) (kael's Linear, src/nn/layers.cpp:42-43); sum(y * gout).backward(). Writes
+// w.grad [n, k] and x.grad [batch, m, k].
+int ref_linear_grads(int device, int64_t batch, int64_t m, int64_t k, int64_t n, uint64_t seed, float* w_grad,
+                     float* x_grad) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(seed);
+        kael::Tensor x = (kael::rand({batch, m, k}) * 2 - 1).to(dev);
+        kael::Tensor w = ((kael::rand({n, k}) * 2 - 1) * 0.05).to(dev);
+        const kael::Tensor gout = (kael::rand({batch, m, n}) * 2 - 1).to(dev);
+        x.requires_grad_(true);
+        w.requires_grad_(true);
+        kael::sum(kael::matmul(x, w.T()) * gout).backward();
+        copy_out(w.grad()->cpu(), w_grad);
+        copy_out(x.grad()->cpu(), x_grad);
     });
 }
 

@@ -80,6 +80,7 @@ REF_SIGS = {
     "gpt_forward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "gpt_cached_logits": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "gpt_generate": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
+    "gpt_set_param": (c_int, [c_void_p, c_int64, c_void_p]),
     "golden": (c_int64, [c_char_p, c_char_p, c_int, POINTER(c_void_p), POINTER(c_int), POINTER(c_int),
                          POINTER(c_int64), POINTER(c_char_p), c_int, c_void_p, c_int64, POINTER(c_int),
                          POINTER(c_int), POINTER(c_int64)]),
@@ -91,6 +92,11 @@ REF_SIGS = {
     "train_gpt": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                           POINTER(c_double)]),
     "gpt_generate_on": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
+    "train_gpt_params": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
+                                 c_void_p, POINTER(c_double)]),
+    "gpt_param_total": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "row_grad": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
+    "linear_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
     "suite_size": (c_int, []),
     "suite_name": (c_char_p, [c_int]),
     "suite_run": (c_int, [c_int]),

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import kd
+import support
 from views import View, assert_same, contiguous, run_both, stepped, transposed
 
 pytestmark = pytest.mark.gpu
@@ -142,9 +143,13 @@ C2 = (4096, 4096)
 
 
 @pytest.mark.parametrize("case", ["add", "mul", "transposed_add"])
-def test_c2_config_full_size(kdb, oracle, case):
-    """BASELINE config C2 at its full size: a[4096,4096] (+|*) b[4096,1] and a.T() + b."""
+def test_c2_config_full_size(kdb, oracle, refdev, case):
+    """BASELINE config C2 at its full size and from its recipe (manual_seed(1);
+    a = rand({4096,4096}) * 2 - 1, b = rand({4096,1}) * 2 - 1): a (+|*) b and a.T() + b."""
     rng = np.random.default_rng(1)
+    flat = np.empty(C2[0] * C2[1] + C2[0], np.float32)
+    assert refdev.ref_uniform_pm1(1, flat.size, support.ptr(flat)) == 0, support.ref_error(refdev)
+    a, b = flat[:C2[0] * C2[1]], flat[C2[0] * C2[1]:]
     if case == "transposed_add":
         views = [contiguous(C2), transposed(C2), contiguous((C2[0], 1))]
     else:
@@ -152,7 +157,8 @@ def test_c2_config_full_size(kdb, oracle, case):
     op = kd.OP["TIMES"] if case == "mul" else kd.OP["PLUS"]
     got, want = run_both(kdb, oracle, views, kd.F32, kd.F32,
                          lambda lay: kdb.call("elementwise", op, kd.F32, kd.F32, lay, kd.params()),
-                         lambda lay: oracle.oracle_elementwise(op, kd.F32, kd.F32, lay, kd.params()), rng)
+                         lambda lay: oracle.oracle_elementwise(op, kd.F32, kd.F32, lay, kd.params()), rng,
+                         inputs=[a, b])
     assert_same(got, want, True, what=case)
 
 

@@ -1,0 +1,82 @@
+"""Gradients and trained parameters through kael's autograd on the MI355X against kael's CPU path.
+
+  - Linear-shaped products y = x . W^T with x [B, M, K] and a 2-D weight W [N, K] (kael's Linear,
+    reference src/nn/layers.cpp:42-43; MatmulBackward src/autograd/functions_linalg.cpp:29-49):
+    W.grad and x.grad element by element, at C4's four Linear shapes and ragged ones, through
+    unmodified kael (libkael_hip.so: one product per batch item, then sum_to_shape) and through
+    kael's optional device branches (libkael_hip_fused.so: the weight gradient as one product over
+    the folded batch, X_flat^T . g_flat, on the split-K path).
+  - C4 (char-GPT, Adam): every one of the 3 216 896 parameters after 5 Adam steps, for both builds.
+
+Tolerance: the reference's f32 device tolerance, |dev - cpu| <= 1e-4 + 1e-4 |cpu|
+(tests/test_cuda.cpp:40-43), elementwise. For trained parameters, Adam's first updates are
+lr * g / (|g| + eps): an element whose CPU gradient is within rounding of zero can take an update
+of different sign on the two sides (at most 2 lr per step), so at most 1 element in 10^5 may exceed
+the tolerance, each by no more than 2 * lr * steps.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import support
+
+pytestmark = pytest.mark.gpu
+
+P = support.ptr
+# (batch, m, k, n): C4's qkv, proj, fc1 (K 256) and fc2 (K 1024) weights over 32 x 128 tokens,
+# then ragged shapes (no whole tiles, K not a multiple of 16, a single token).
+SHAPES = [(32, 128, 256, 768), (32, 128, 256, 256), (32, 128, 256, 1024), (32, 128, 1024, 256),
+          (3, 37, 53, 29), (5, 1, 7, 3), (2, 130, 200, 96)]
+
+
+def linear_grads(lib, device, shape, seed=7):
+    b, m, k, n = shape
+    wg, xg = np.empty((n, k), np.float32), np.empty((b, m, k), np.float32)
+    assert lib.ref_linear_grads(device, b, m, k, n, seed, P(wg), P(xg)) == 0, support.ref_error(lib)
+    return wg, xg
+
+
+def assert_reference_close(got, want, what):
+    bad = np.abs(got.astype(np.float64) - want) > 1e-4 + 1e-4 * np.abs(want)
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} elements beyond 1e-4 + 1e-4|cpu|"
+
+
+@pytest.mark.parametrize("variant", ["hip", "hip_fused"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["x".join(map(str, s)) for s in SHAPES])
+def test_linear_gradients_match_cpu(request, variant, shape):
+    lib = request.getfixturevalue("kael_" + variant)
+    cpu_w, cpu_x = linear_grads(lib, 0, shape)
+    dev_w, dev_x = linear_grads(lib, 1, shape)
+    assert_reference_close(dev_w, cpu_w, "W.grad")
+    assert_reference_close(dev_x, cpu_x, "x.grad")
+
+
+C4 = (96, 128, 4, 4, 256, 32)  # vocab, context, layers, heads, dimension, batch
+LR = 1e-3  # kael's Adam default (include/kael/optim/adam.h:11-17)
+
+
+def chargpt(lib, device, steps):
+    total = lib.ref_gpt_param_total(*C4[:5])
+    losses, params, secs = np.zeros(steps, np.float32), np.zeros(total, np.float32), ctypes.c_double()
+    assert lib.ref_train_gpt_params(device, steps, *C4, P(losses), P(params), ctypes.byref(secs)) == 0, \
+        support.ref_error(lib)
+    return losses, params
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("variant", ["hip", "hip_fused"])
+def test_c4_every_parameter_after_five_adam_steps(request, variant):
+    lib = request.getfixturevalue("kael_" + variant)
+    steps = 5
+    cpu_l, cpu_p = chargpt(lib, 0, steps)
+    dev_l, dev_p = chargpt(lib, 1, steps)
+    assert cpu_p.size == 3216896
+    np.testing.assert_allclose(dev_l, cpu_l, rtol=1e-4)
+    diff = np.abs(dev_p.astype(np.float64) - cpu_p)
+    bad = diff > 1e-4 + 1e-4 * np.abs(cpu_p)
+    assert bad.sum() <= cpu_p.size // 100000, f"{bad.sum()} parameters beyond the reference tolerance"
+    assert diff.max() <= 2 * LR * steps, f"largest parameter difference {diff.max():.3e}"
+    moved = np.abs(dev_p - cpu_p).max()
+    print(f"\nC4 {variant}: {cpu_p.size} parameters after {steps} Adam steps, {bad.sum()} beyond 1e-4 + 1e-4|p|, "
+          f"max |dp| = {moved:.2e}; losses {dev_l.tolist()}")

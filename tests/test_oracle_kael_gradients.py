@@ -1,0 +1,39 @@
+"""The gradients of Linear-shaped products (y = x . W^T, x [B, M, K], W [N, K]; reference
+src/nn/layers.cpp:42-43, MatmulBackward src/autograd/functions_linalg.cpp:29-49) through kael's
+optional device branches with the C oracle as the device: the weight gradient's fold over the batch
+(one product X_flat^T . g_flat) and the strided products, element by element against kael's CPU
+path (the reference's f32 device tolerance 1e-4 + 1e-4 |cpu|, tests/test_cuda.cpp:40-43). The
+fold branch must run (the strided-product counter moves) and an empty last dim must fall back to
+kael's own path.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import support
+from test_gpu_kael_gradients import assert_reference_close, linear_grads
+
+SHAPES = [(3, 37, 53, 29), (5, 1, 7, 3), (2, 30, 64, 48), (4, 16, 32, 24)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=["x".join(map(str, s)) for s in SHAPES])
+def test_linear_gradients_through_the_fused_branches(kael_oracle_fused, shape):
+    lib = kael_oracle_fused
+    fn = lib.ref_extension_calls
+    fn.restype, fn.argtypes = ctypes.c_longlong, [ctypes.c_int]
+    cpu_w, cpu_x = linear_grads(lib, 0, shape)
+    before = fn(5)  # matmul_strided
+    dev_w, dev_x = linear_grads(lib, 1, shape)
+    assert fn(5) > before
+    assert_reference_close(dev_w, cpu_w, "W.grad")
+    assert_reference_close(dev_x, cpu_x, "x.grad")
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 0, 4), (2, 3, 5, 0)], ids=["k0", "n0"])
+def test_empty_last_dim_keeps_kaels_path(kael_oracle_fused, shape):
+    b, m, k, n = shape
+    wg, xg = np.ones((n, k), np.float32), np.ones((b, m, k), np.float32)
+    assert kael_oracle_fused.ref_linear_grads(1, b, m, k, n, 3, support.ptr(wg), support.ptr(xg)) == 0, \
+        support.ref_error(kael_oracle_fused)
+    assert not wg.any() and not xg.any()

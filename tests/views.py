@@ -92,14 +92,18 @@ def random_values(rng, dtype, n, op=None):
     return v
 
 
-def run_both(kdb, oracle, views, in_dtype, out_dtype, call_kd, call_oracle, rng, op=None):
-    """views[0] is the output. Returns (device output storage, oracle output storage)."""
+def run_both(kdb, oracle, views, in_dtype, out_dtype, call_kd, call_oracle, rng, op=None, inputs=None):
+    """views[0] is the output. Returns (device output storage, oracle output storage). `inputs`
+    (optional) gives the input storages instead of values drawn from `rng`."""
     in_np = kd.NUMPY_DTYPE[in_dtype]
     out_np = kd.NUMPY_DTYPE[out_dtype]
     storages = []
     for i, v in enumerate(views):
         if i == 0:
             s = np.full(v.storage_len, 7, out_np) if out_np != np.float32 else np.full(v.storage_len, -7.5, out_np)
+        elif inputs is not None:
+            s = np.ascontiguousarray(inputs[i - 1], in_np).reshape(-1)
+            assert s.size == v.storage_len
         else:
             s = random_values(rng, in_np, v.storage_len, op)
             if op == kd.OP["POWER"] and i == 2 and in_np != np.int64:
