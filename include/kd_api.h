@@ -342,10 +342,18 @@ typedef struct kd_gpt_config {
 #define KD_GPT_STEPWISE_PREFILL 2
 
 int kd_gpt_create(void** handle, const kd_gpt_config* config);
+/* KD_OK when kd_gpt_create would accept `config` on this device (sizes, head_dim a multiple of 4 up
+ * to 64, 4 * dimension <= 4096, at most 64 heads and 8192 positions); otherwise the status and
+ * message kd_gpt_create would give. Allocates nothing. */
+int kd_gpt_supported(const kd_gpt_config* config);
 void kd_gpt_destroy(void* handle);
 /* Uploads one parameter by its kael name (GPT::named_parameters(), e.g. "blocks.3.attn.qkv.weight")
  * from host f32 data holding all `count` elements in kael's row-major layout. */
 int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int64_t count);
+/* The same from device memory (`data` is a device pointer to `count` contiguous f32 elements, e.g.
+ * the storage of kael's parameter tensor on this device); the copy is complete on return. No
+ * reference counterpart: it serves the optional kael branch that runs nn::generate on this engine. */
+int kd_gpt_load_parameter_device(void* handle, const char* name, const float* data, int64_t count);
 /* Runs the prompt through the model from position 0 with an empty KV cache; the last position's
  * greedy token becomes the first generated token. Clears any previous sequence. A prompt longer
  * than max_positions runs its last max_positions tokens, as nn::generate does (reference

@@ -1176,21 +1176,28 @@ template <typename T> int alloc(T** out, int64_t count) {
     return KD_OK;
 }
 
-int create(Engine& e, const kd_gpt_config& c) {
+// The shapes this engine's kernels handle (KD_OK) or the reason they do not.
+int check_config(const kd_gpt_config& c) {
     if (c.vocab_size <= 0 || c.max_positions <= 0 || c.layers <= 0 || c.heads <= 0 || c.dimension <= 0)
-        return fail(KD_E_INVALID, "kd_gpt_create: sizes must be positive");
-    if (c.dimension % c.heads != 0) return fail(KD_E_INVALID, "kd_gpt_create: dimension must divide by heads");
+        return fail(KD_E_INVALID, "kd_gpt: sizes must be positive");
+    if (c.dimension % c.heads != 0) return fail(KD_E_INVALID, "kd_gpt: dimension must divide by heads");
+    const int64_t hd = c.dimension / c.heads;
+    if (hd > 64) return fail(KD_E_UNSUPPORTED, "kd_gpt: head_dim above 64 is not supported");
+    if (c.dimension % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt: dimension must be a multiple of 4");
+    if (hd % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt: head_dim must be a multiple of 4 (16-byte key rows)");
+    if (4 * c.dimension > kMaxK) return fail(KD_E_UNSUPPORTED, "kd_gpt: 4 * dimension above 4096 is not supported");
+    static_assert(kMaxK / 4 <= kMaxLnDim, "ln_load holds a row of at most kMaxLnDim elements");
+    if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt: more than 64 heads is not supported");
+    if (c.max_positions > 8192) return fail(KD_E_UNSUPPORTED, "kd_gpt: max_positions above 8192");
+    return KD_OK;
+}
+
+int create(Engine& e, const kd_gpt_config& c) {
+    if (int rc = check_config(c)) return rc;
     e.cfg = c;
     e.d = c.dimension;
     e.hd = c.dimension / c.heads;
     e.ff = 4 * c.dimension;
-    if (e.hd > 64) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim above 64 is not supported");
-    if (e.d % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: dimension must be a multiple of 4");
-    if (e.hd % 4 != 0) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: head_dim must be a multiple of 4 (16-byte key rows)");
-    if (e.ff > kMaxK) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: 4 * dimension above 4096 is not supported");
-    static_assert(kMaxK / 4 <= kMaxLnDim, "ln_load holds a row of at most kMaxLnDim elements");
-    if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: more than 64 heads is not supported");
-    if (c.max_positions > 8192) return fail(KD_E_UNSUPPORTED, "kd_gpt_create: max_positions above 8192");
     // kael's parameter order and shapes (GPT::named_parameters)
     std::vector<std::pair<std::string, int64_t>> shapes;
     shapes.emplace_back("token_embedding.weight", c.vocab_size * e.d);
@@ -1239,6 +1246,28 @@ int create(Engine& e, const kd_gpt_config& c) {
     return KD_OK;
 }
 
+// Copies one parameter into the engine from host or device memory.
+int load_parameter(const char* what, void* handle, const char* name, const float* data, int64_t count, bool on_device) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || name == nullptr || data == nullptr) return fail(KD_E_INVALID, std::string(what) + ": null argument");
+    const auto it = e->offsets.find(name);
+    if (it == e->offsets.end()) return fail(KD_E_INVALID, std::string(what) + ": unknown parameter " + name);
+    if (it->second.second != count) return fail(KD_E_INVALID, std::string(what) + ": wrong element count for " + name);
+    const size_t bytes = static_cast<size_t>(count) * sizeof(float);
+    if (on_device) {
+        // Ordered after the work already queued on the backend stream (which produced `data`).
+        KD_HIP(hipStreamSynchronize(kd::stream()));
+        KD_HIP(hipMemcpyAsync(e->params + it->second.first, data, bytes, hipMemcpyDeviceToDevice, e->stream));
+        KD_HIP(hipStreamSynchronize(e->stream));
+    } else {
+        KD_HIP(hipMemcpy(e->params + it->second.first, data, bytes, hipMemcpyHostToDevice));
+    }
+    for (size_t i = 0; i < e->names.size(); ++i)
+        if (e->names[i] == name) e->loaded[i] = true;
+    e->wt_valid = false;
+    return KD_OK;
+}
+
 } // namespace
 
 } // namespace kd
@@ -1260,20 +1289,20 @@ int kd_gpt_create(void** handle, const kd_gpt_config* config) {
     return KD_OK;
 }
 
+int kd_gpt_supported(const kd_gpt_config* config) {
+    if (config == nullptr) return fail(KD_E_INVALID, "kd_gpt_supported: null argument");
+    if (int rc = ensure_device()) return rc;
+    return check_config(*config);
+}
+
 void kd_gpt_destroy(void* handle) { delete static_cast<Engine*>(handle); }
 
 int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int64_t count) {
-    auto* e = static_cast<Engine*>(handle);
-    if (e == nullptr || name == nullptr || data == nullptr) return fail(KD_E_INVALID, "kd_gpt_load_parameter: null argument");
-    const auto it = e->offsets.find(name);
-    if (it == e->offsets.end()) return fail(KD_E_INVALID, std::string("kd_gpt_load_parameter: unknown parameter ") + name);
-    if (it->second.second != count)
-        return fail(KD_E_INVALID, std::string("kd_gpt_load_parameter: wrong element count for ") + name);
-    KD_HIP(hipMemcpy(e->params + it->second.first, data, static_cast<size_t>(count) * sizeof(float), hipMemcpyHostToDevice));
-    for (size_t i = 0; i < e->names.size(); ++i)
-        if (e->names[i] == name) e->loaded[i] = true;
-    e->wt_valid = false;
-    return KD_OK;
+    return load_parameter("kd_gpt_load_parameter", handle, name, data, count, false);
+}
+
+int kd_gpt_load_parameter_device(void* handle, const char* name, const float* data, int64_t count) {
+    return load_parameter("kd_gpt_load_parameter_device", handle, name, data, count, true);
 }
 
 int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length) {

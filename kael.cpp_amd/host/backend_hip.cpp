@@ -10,6 +10,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "kael/device_kernels.h"
 #include "kael/error.h"
@@ -191,6 +192,54 @@ void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* 
 
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {
     check(kd_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
+}
+
+namespace {
+
+kd_gpt_config engine_config(const GptEngineShape& s) {
+    kd_gpt_config c{};
+    c.vocab_size = s.vocab_size;
+    c.max_positions = s.max_positions;
+    c.layers = s.layers;
+    c.heads = s.heads;
+    c.dimension = s.dimension;
+    c.tanh_gelu = s.tanh_gelu ? 1 : 0;
+    c.flags = 0;
+    return c;
+}
+
+} // namespace
+
+bool gpt_engine_supported(const GptEngineShape& shape) {
+    const kd_gpt_config c = engine_config(shape);
+    return kd_gpt_supported(&c) == KD_OK;
+}
+
+void* gpt_engine_create(const GptEngineShape& shape) {
+    const kd_gpt_config c = engine_config(shape);
+    void* engine = nullptr;
+    check(kd_gpt_create(&engine, &c), "gpt_engine_create");
+    return engine;
+}
+
+void gpt_engine_destroy(void* engine) noexcept { kd_gpt_destroy(engine); }
+
+void gpt_engine_load(void* engine, const char* name, const std::byte* device_data, std::int64_t count) {
+    check(kd_gpt_load_parameter_device(engine, name, reinterpret_cast<const float*>(device_data), count),
+          "gpt_engine_load");
+}
+
+std::int64_t gpt_engine_prefill(void* engine, const std::int64_t* prompt, std::int64_t length) {
+    check(kd_gpt_prefill(engine, prompt, length), "gpt_engine_prefill");
+    std::int64_t total = 0;
+    check(kd_gpt_sequence(engine, nullptr, 0, &total), "gpt_engine_prefill");
+    std::vector<std::int64_t> ids(static_cast<std::size_t>(total));
+    check(kd_gpt_sequence(engine, ids.data(), total, &total), "gpt_engine_prefill");
+    return ids.back();
+}
+
+void gpt_engine_decode(void* engine, std::int64_t count, std::int64_t* tokens) {
+    check(kd_gpt_decode(engine, count, tokens), "gpt_engine_decode");
 }
 
 } // namespace kael::device

@@ -88,4 +88,26 @@ void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* 
 // f32 / f64 store In, i64 / bool wrapping int64.
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows);
 
+// The GPT decode engine (kd_gpt_*), for the optional branch of nn::generate (reference
+// src/nn/transformer.cpp:256-295) that runs greedy generation with a KV cache on the device.
+struct GptEngineShape {
+    std::int64_t vocab_size;
+    std::int64_t max_positions;
+    std::int64_t layers;
+    std::int64_t heads;
+    std::int64_t dimension;
+    bool tanh_gelu;
+};
+
+// Whether the engine runs a model of this shape on this device (false: kael's own path runs).
+bool gpt_engine_supported(const GptEngineShape& shape);
+void* gpt_engine_create(const GptEngineShape& shape);
+void gpt_engine_destroy(void* engine) noexcept;
+// Copies parameter `name` (a GPT::named_parameters() name) from `count` contiguous f32 device elements.
+void gpt_engine_load(void* engine, const char* name, const std::byte* device_data, std::int64_t count);
+// Runs the prompt (host ids; its last max_positions when longer) and returns the first greedy token.
+std::int64_t gpt_engine_prefill(void* engine, const std::int64_t* prompt, std::int64_t length);
+// The next `count` greedy tokens into `tokens` (host).
+void gpt_engine_decode(void* engine, std::int64_t count, std::int64_t* tokens);
+
 } // namespace kael::device

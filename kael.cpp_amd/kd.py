@@ -142,6 +142,8 @@ BACKEND_ONLY = {
     "gpt_create": (c_int, [POINTER(c_void_p), POINTER(GptConfig)]),
     "gpt_destroy": (None, [c_void_p]),
     "gpt_load_parameter": (c_int, [c_void_p, ctypes.c_char_p, c_void_p, c_int64]),
+    "gpt_load_parameter_device": (c_int, [c_void_p, ctypes.c_char_p, c_void_p, c_int64]),
+    "gpt_supported": (c_int, [POINTER(GptConfig)]),
     "gpt_prefill": (c_int, [c_void_p, c_void_p, c_int64]),
     "gpt_decode": (c_int, [c_void_p, c_int64, c_void_p]),
     "gpt_forward_logits": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),

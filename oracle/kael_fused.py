@@ -28,6 +28,9 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      a host copy (the same planning: plan_reduction's kept-first
                                      permutation, then one call over contiguous chunks)
   src/ops/sequence.cpp               cumsum (:95-117) of a device tensor on the device
+  src/nn/transformer.cpp             nn::generate (:256-295) with temperature 0, the KV cache and a
+                                     batch-1 prompt on the device runs on the decode engine
+                                     (kd_gpt_*), token for token the greedy sequence of the loop
 
 Each edit is anchored on a line of the reference file that must occur exactly once; a missing
 or repeated anchor is an error, so a changed reference fails loudly instead of building
@@ -300,6 +303,66 @@ STANDARDIZE_BACKWARD_BRANCH = """                if (auto fused = fused_standard
                 }
 """
 
+GENERATE_HELPER = """// MI355X: greedy generation with a KV cache of a batch-1 prompt on the device runs on the backend's
+// decode engine (one captured step per token, the greedy pick on the device) when the engine
+// takes the model's shape; no value otherwise, and the loop of generate() runs.
+std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const GenerateOptions& options) {
+    const GptConfig& config = model.config();
+    if (prompt.device() == Device::CPU || options.temperature != 0.0 || !options.use_cache || prompt.size(0) != 1 ||
+        options.max_new_tokens == 0 || config.dtype != DType::F32 || prompt.dtype() != DType::I64) {
+        return std::nullopt;
+    }
+    const device::GptEngineShape shape{config.vocab_size, config.max_positions, config.layers,
+                                       config.heads,      config.dimension,     config.tanh_gelu};
+    if (!device::gpt_engine_supported(shape)) {
+        return std::nullopt;
+    }
+    const std::vector<NamedTensor> named = model.named_parameters();
+    for (const auto& entry : named) {
+        const Tensor& p = entry.second;
+        if (p.device() != prompt.device() || p.dtype() != DType::F32 || !p.is_contiguous()) {
+            return std::nullopt;
+        }
+    }
+    struct Engine {
+        void* handle;
+        ~Engine() { device::gpt_engine_destroy(handle); }
+    } engine{device::gpt_engine_create(shape)};
+    for (const auto& entry : named) {
+        device::gpt_engine_load(engine.handle, entry.first.c_str(), entry.second.device_data(), entry.second.numel());
+    }
+    const Tensor host_prompt = prompt.cpu().contiguous();
+    const std::int64_t length = host_prompt.size(1);
+    const std::int64_t* ids = host_prompt.data_ptr<std::int64_t>();
+    std::vector<std::int64_t> generated{device::gpt_engine_prefill(engine.handle, ids, length)};
+    // on_token sees each token as sample_next returns it: a [1, 1] int64 tensor on the device.
+    const auto emit = [&](std::int64_t token) {
+        return !options.on_token || options.on_token(from_vector<std::int64_t>({token}, {1, 1}).to(prompt.device()));
+    };
+    if (options.on_token) {
+        bool more = emit(generated.back());
+        while (more && static_cast<std::int64_t>(generated.size()) < options.max_new_tokens) {
+            std::int64_t token = 0;
+            device::gpt_engine_decode(engine.handle, 1, &token);
+            generated.push_back(token);
+            more = emit(token);
+        }
+    } else {
+        generated.resize(static_cast<std::size_t>(options.max_new_tokens));
+        device::gpt_engine_decode(engine.handle, options.max_new_tokens - 1, generated.data() + 1);
+    }
+    const Tensor tail =
+        from_vector<std::int64_t>(generated, {1, static_cast<std::int64_t>(generated.size())}).to(prompt.device());
+    return cat({prompt, tail}, 1);
+}
+
+"""
+
+GENERATE_BRANCH = """    if (auto out = device_generate(model, prompt, options)) {
+        return *out;
+    }
+"""
+
 # (relative path, anchor line(s), where, text). where: "before", "after", "replace", "append".
 EDITS = [
     ("include/kael/device_kernels.h", None, "append", '\n#include "kd_kael_extensions.h"\n'),
@@ -357,6 +420,11 @@ EDITS = [
     ("src/autograd/functions_reduce.cpp",
      "                const Tensor scale = kael::sqrt(kael::var(saved.get(), dims, true, 0) + eps);\n", "before",
      STANDARDIZE_BACKWARD_BRANCH),
+    ("src/nn/transformer.cpp", "#include <map>\n", "after", "#include <optional>\n#include <vector>\n"),
+    ("src/nn/transformer.cpp", '#include "kael/autograd/grad_mode.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/nn/transformer.cpp", "class TrainingModeRestorer {\n", "before", GENERATE_HELPER),
+    ("src/nn/transformer.cpp", "    const std::int64_t context = model.config().max_positions;\n", "after",
+     GENERATE_BRANCH),
     ("src/ops/sequence.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/ops/sequence.cpp", "        return t.to(dtype).clone();\n    }\n", "after", CUMSUM_BRANCH),
 ]

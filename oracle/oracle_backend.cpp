@@ -185,6 +185,19 @@ void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t s
     check(oracle_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
 }
 
+// The C oracle has no GPT decode engine: nn::generate's optional branch sees an unsupported
+// shape and keeps kael's own loop.
+bool gpt_engine_supported(const GptEngineShape&) { return false; }
+void* gpt_engine_create(const GptEngineShape&) { throw Error("oracle backend: no GPT decode engine"); }
+void gpt_engine_destroy(void*) noexcept {}
+void gpt_engine_load(void*, const char*, const std::byte*, std::int64_t) {
+    throw Error("oracle backend: no GPT decode engine");
+}
+std::int64_t gpt_engine_prefill(void*, const std::int64_t*, std::int64_t) {
+    throw Error("oracle backend: no GPT decode engine");
+}
+void gpt_engine_decode(void*, std::int64_t, std::int64_t*) { throw Error("oracle backend: no GPT decode engine"); }
+
 } // namespace kael::device
 
 // Test hook: how many times extension `which` (numbered as g_extension_calls) has run.

@@ -812,6 +812,35 @@ int ref_linear_grads(int device, int64_t batch, int64_t m, int64_t k, int64_t n,
     });
 }
 
+// nn::generate (greedy, KV cache) on `device` with an on_token callback, as
+// examples/gpt2_generate.cpp:80-92 passes one: it records every token it is handed (reading each
+// [1, 1] tensor with item(), as the example's printer does) and stops the generation once it has
+// seen `stop_after` tokens. Writes the returned sequence (prompt + generated; its length through
+// `total`) and the tokens the callback saw (their count through `seen`).
+int ref_gpt_generate_streamed(void* handle, int device, const int64_t* prompt, int64_t length, int64_t new_tokens,
+                              int64_t stop_after, int64_t* out_tokens, int64_t* total, int64_t* seen_tokens,
+                              int64_t* seen) {
+    return guarded([&] {
+        auto& model = *static_cast<RefGpt*>(handle)->model;
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        model.to(dev);
+        const kael::Tensor ids = host_tensor(prompt, {1, length}, kael::DType::I64).to(dev);
+        int64_t count = 0;
+        const auto printer = [&](const kael::Tensor& token) {
+            if (token.dim() != 2 || token.size(0) != 1 || token.size(1) != 1 || token.device() != dev)
+                throw std::runtime_error("on_token got a tensor of another shape or device");
+            seen_tokens[count++] = token.item<std::int64_t>();
+            return count < stop_after;
+        };
+        const kael::Tensor seq = kael::nn::generate(
+            model, ids, {.max_new_tokens = new_tokens, .temperature = 0.0, .on_token = printer});
+        *total = seq.size(1);
+        *seen = count;
+        copy_out(seq.cpu(), out_tokens);
+        model.to(kael::Device::CPU);
+    });
+}
+
 int ref_train_chargpt(int device, int64_t steps, float* losses, double* seconds) {
     return ref_train_gpt(device, steps, 96, 128, 4, 4, 256, 32, losses, seconds);
 }

@@ -81,6 +81,8 @@ REF_SIGS = {
     "gpt_cached_logits": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "gpt_generate": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
     "gpt_set_param": (c_int, [c_void_p, c_int64, c_void_p]),
+    "gpt_generate_streamed": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_int64, c_void_p,
+                                      POINTER(c_int64), c_void_p, POINTER(c_int64)]),
     "golden": (c_int64, [c_char_p, c_char_p, c_int, POINTER(c_void_p), POINTER(c_int), POINTER(c_int),
                          POINTER(c_int64), POINTER(c_char_p), c_int, c_void_p, c_int64, POINTER(c_int),
                          POINTER(c_int), POINTER(c_int64)]),

@@ -188,3 +188,34 @@ def test_kael_generate_unchanged_on_the_device(request, kael_cpu_tokens, variant
     np.testing.assert_array_equal(out, seq)
     print(f"\nkael nn::generate on the MI355X ({variant}): {NEW} tokens in {secs.value:.2f} s = "
           f"{NEW / secs.value:.1f} tokens/s (prefill included); kael CPU {NEW / cpu_secs:.2f} tokens/s")
+
+
+def streamed(lib, device, prompt, new, stop_after):
+    h = kael_model(lib)
+    out, seen = np.zeros(len(prompt) + new, np.int64), np.zeros(new, np.int64)
+    total, count = ctypes.c_int64(), ctypes.c_int64()
+    p = np.ascontiguousarray(prompt, np.int64)
+    try:
+        assert lib.ref_gpt_generate_streamed(h, device, p.ctypes.data_as(ctypes.c_void_p), len(p), new, stop_after,
+                                             out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(total),
+                                             seen.ctypes.data_as(ctypes.c_void_p), ctypes.byref(count)) == 0, \
+            support.ref_error(lib)
+    finally:
+        lib.ref_gpt_destroy(h)
+    return out[:total.value], seen[:count.value]
+
+
+@pytest.mark.timeout(300)
+def test_generate_with_on_token_on_the_engine(kael_hip_fused):
+    """examples/gpt2_generate.cpp hands generate an on_token printer: through kael's branch the
+    engine calls it once per token with a [1, 1] device tensor and stops when it returns false,
+    exactly as kael's CPU loop does (here after 9 of 40 tokens, then to the end)."""
+    lib = kael_hip_fused
+    lib.ref_set_threads(threads())
+    prompt = np.random.default_rng(8).integers(0, VOCAB, 12)
+    for stop_after in (9, 40):
+        cpu_seq, cpu_seen = streamed(lib, 0, prompt, 40, stop_after)
+        dev_seq, dev_seen = streamed(lib, 1, prompt, 40, stop_after)
+        np.testing.assert_array_equal(dev_seq, cpu_seq)
+        np.testing.assert_array_equal(dev_seen, cpu_seen)
+        assert len(cpu_seen) == stop_after and len(cpu_seq) == 12 + stop_after
