@@ -194,6 +194,16 @@ int kd_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout*
 int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
               int64_t chunk_size, int64_t output_count);
 
+/* kd_reduce without any allocation: no reference counterpart. For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels and results as kd_reduce (bit for bit); the segment
+ * partials of its split path (few long rows) go to a static 64 KiB device buffer that each GPU
+ * holds until the process ends, instead of the backend's growable workspace. A call whose
+ * partials would not fit fails with KD_E_INVALID (on 256 CUs they take at most 12 KiB). Every
+ * call on one GPU shares that buffer: calls that overlap on one GPU (different streams or host
+ * threads at once) race; calls in one stream's order do not. */
+int kd_reduce_noalloc(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                      int64_t chunk_size, int64_t output_count);
 
 /* Replaces the host round trip of reference src/ops/reduce.cpp:399-421 `argmax` / `argmin`
  * (`on_host` + `arg_extreme`, :256-268, `best_position`, :236-254): results[r] = the index

@@ -22,6 +22,8 @@
 #include <climits>
 #include <limits>
 #include <cfloat>
+#include <mutex>
+#include <string>
 
 #include "kd_internal.h"
 
@@ -555,7 +557,11 @@ template <typename In> int cumsum_typed(void* out_v, const void* data_v, int64_t
     return KD_OK;
 }
 
-template <typename C, typename In> int reduce_with(void* results, const void* data_v, int64_t chunk, int64_t rows) {
+// `fixed` (non-null): the split path's partials go there, up to `fixed_bytes`, instead of the
+// workspace lease (kd_reduce_noalloc); a larger need is an error.
+template <typename C, typename In>
+int reduce_with(void* results, const void* data_v, int64_t chunk, int64_t rows, void* fixed = nullptr,
+                size_t fixed_bytes = 0) {
     using Out = typename C::Out;
     using Acc = typename C::Acc;
     Out* out = static_cast<Out*>(results);
@@ -594,25 +600,55 @@ template <typename C, typename In> int reduce_with(void* results, const void* da
     segment = (segment + 63) / 64 * 64;
     segments = (chunk + segment - 1) / segment;
     if (rows > 65535) return fail(KD_E_INVALID, "kd_reduce: too many rows for the split path");
+    const size_t partial_bytes = static_cast<size_t>(rows * segments) * sizeof(Acc);
     Workspace ws;  // held until combine_kernel is enqueued
-    if (int rc = workspace(ws, static_cast<size_t>(rows * segments) * sizeof(Acc))) return rc;
+    Acc* partial = static_cast<Acc*>(fixed);
+    if (fixed != nullptr) {
+        if (partial_bytes > fixed_bytes)
+            return fail(KD_E_INVALID, "kd_reduce_noalloc: the split path needs " + std::to_string(partial_bytes) +
+                                          " bytes of scratch, above the " + std::to_string(fixed_bytes) +
+                                          "-byte static buffer");
+    } else {
+        if (int rc = workspace(ws, partial_bytes)) return rc;
+        partial = static_cast<Acc*>(ws.ptr);
+    }
     hipLaunchKernelGGL((split_kernel<C, In>), dim3(static_cast<uint32_t>(segments), static_cast<uint32_t>(rows)),
-                       dim3(kBlock), 0, stream(), static_cast<Acc*>(ws.ptr), data, chunk, segments, segment);
+                       dim3(kBlock), 0, stream(), partial, data, chunk, segments, segment);
     KD_LAUNCH_CHECK();
     hipLaunchKernelGGL((combine_kernel<C>), dim3(static_cast<uint32_t>(rows)), dim3(kBlock), 0, stream(), out,
-                       static_cast<const Acc*>(ws.ptr), segments);
+                       static_cast<const Acc*>(partial), segments);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }
 
-template <int Op> int reduce_dtype(int in, void* results, const void* data, int64_t chunk, int64_t rows) {
+template <int Op>
+int reduce_dtype(int in, void* results, const void* data, int64_t chunk, int64_t rows, void* fixed = nullptr,
+                 size_t fixed_bytes = 0) {
     switch (in) {
-    case KD_F32: return reduce_with<Combiner<Op, float>, float>(results, data, chunk, rows);
-    case KD_F64: return reduce_with<Combiner<Op, double>, double>(results, data, chunk, rows);
-    case KD_I64: return reduce_with<Combiner<Op, int64_t>, int64_t>(results, data, chunk, rows);
-    case KD_BOOL: return reduce_with<Combiner<Op, uint8_t>, uint8_t>(results, data, chunk, rows);
+    case KD_F32: return reduce_with<Combiner<Op, float>, float>(results, data, chunk, rows, fixed, fixed_bytes);
+    case KD_F64: return reduce_with<Combiner<Op, double>, double>(results, data, chunk, rows, fixed, fixed_bytes);
+    case KD_I64: return reduce_with<Combiner<Op, int64_t>, int64_t>(results, data, chunk, rows, fixed, fixed_bytes);
+    case KD_BOOL: return reduce_with<Combiner<Op, uint8_t>, uint8_t>(results, data, chunk, rows, fixed, fixed_bytes);
     }
     return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
+}
+
+// Entry body shared by kd_reduce and kd_reduce_noalloc.
+int reduce_entry(const char* name, int op, int in_dtype, void* results, const void* data, int64_t chunk_size,
+                 int64_t output_count, void* fixed, size_t fixed_bytes) {
+    if (chunk_size < 0 || output_count < 0) return fail(KD_E_INVALID, std::string(name) + ": negative size");
+    if (dtype_size(in_dtype) == 0) return fail(KD_E_INVALID, std::string(name) + ": unknown dtype");
+    if (output_count == 0) return KD_OK;
+    if (chunk_size == 0 && (op == KD_REDUCE_MAX || op == KD_REDUCE_MIN))
+        return fail(KD_E_INVALID, std::string(name) + ": max/min of an empty chunk");
+    switch (op) {
+#define KD_REDUCE_CASE(OP) \
+    case OP: return reduce_dtype<OP>(in_dtype, results, data, chunk_size, output_count, fixed, fixed_bytes);
+        KD_REDUCE_CASE(KD_REDUCE_SUM) KD_REDUCE_CASE(KD_REDUCE_MAX) KD_REDUCE_CASE(KD_REDUCE_MIN)
+        KD_REDUCE_CASE(KD_REDUCE_PROD) KD_REDUCE_CASE(KD_REDUCE_ALL) KD_REDUCE_CASE(KD_REDUCE_ANY)
+#undef KD_REDUCE_CASE
+    }
+    return fail(KD_E_INVALID, std::string(name) + ": unknown op");
 }
 
 template <bool Largest, typename I> int arg_typed(int in, int64_t* results, const void* data, int64_t chunk, int64_t rows) {
@@ -635,26 +671,66 @@ template <bool Largest> int arg_dtype(int in, int64_t* results, const void* data
 
 } // namespace kd
 
+// Scratch of kd_reduce_noalloc: the split path's segment partials (at most rows * segments <
+// 4 * CUs + 2 * CUs values of at most 8 bytes: 12 KiB on 256 CUs). Every GPU the library runs on
+// holds its own copy until the process ends. Host code never passes `scratch` itself to a kernel
+// (in host code its name is only a stand-in): it uses the device address that
+// hipGetSymbolAddress returns for the current device (static_scratch below).
+constexpr size_t kStaticScratchBytes = size_t{64} << 10;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace kd {
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (with that
+// device current) and kept.
+int static_scratch(void** out) {
+    int dev = 0;
+    KD_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(KD_E_UNSUPPORTED, "kd_reduce_noalloc: device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        KD_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (ptr == nullptr) return fail(KD_E_RUNTIME, "kd_reduce_noalloc: no device address for the static scratch");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return KD_OK;
+}
+
+} // namespace
+
+} // namespace kd
+
 using namespace kd;
 
 extern "C" int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data, int64_t chunk_size,
                          int64_t output_count) {
     (void)out_dtype;  // implied by op and input dtype, as in the reference (kernels.inl:444)
-    if (chunk_size < 0 || output_count < 0) return fail(KD_E_INVALID, "kd_reduce: negative size");
-    if (dtype_size(in_dtype) == 0) return fail(KD_E_INVALID, "kd_reduce: unknown dtype");
-    if (output_count == 0) return KD_OK;
-    if (chunk_size == 0 && (op == KD_REDUCE_MAX || op == KD_REDUCE_MIN))
-        return fail(KD_E_INVALID, "kd_reduce: max/min of an empty chunk");
-    if (int rc = ensure_device()) return rc;
-    switch (op) {
-    case KD_REDUCE_SUM: return reduce_dtype<KD_REDUCE_SUM>(in_dtype, results, data, chunk_size, output_count);
-    case KD_REDUCE_MAX: return reduce_dtype<KD_REDUCE_MAX>(in_dtype, results, data, chunk_size, output_count);
-    case KD_REDUCE_MIN: return reduce_dtype<KD_REDUCE_MIN>(in_dtype, results, data, chunk_size, output_count);
-    case KD_REDUCE_PROD: return reduce_dtype<KD_REDUCE_PROD>(in_dtype, results, data, chunk_size, output_count);
-    case KD_REDUCE_ALL: return reduce_dtype<KD_REDUCE_ALL>(in_dtype, results, data, chunk_size, output_count);
-    case KD_REDUCE_ANY: return reduce_dtype<KD_REDUCE_ANY>(in_dtype, results, data, chunk_size, output_count);
+    if (output_count > 0) {
+        if (int rc = ensure_device()) return rc;
     }
-    return fail(KD_E_INVALID, "kd_reduce: unknown op");
+    return reduce_entry("kd_reduce", op, in_dtype, results, data, chunk_size, output_count, nullptr, 0);
+}
+
+extern "C" int kd_reduce_noalloc(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                                 int64_t chunk_size, int64_t output_count) {
+    (void)out_dtype;
+    // Sizes that launch nothing (no output, a negative size) return from reduce_entry before any
+    // scratch is used; every other call takes the static scratch, never the workspace lease.
+    void* ptr = nullptr;
+    if (output_count > 0 && chunk_size >= 0) {
+        if (int rc = ensure_device()) return rc;
+        if (int rc = static_scratch(&ptr)) return rc;
+    }
+    return reduce_entry("kd_reduce_noalloc", op, in_dtype, results, data, chunk_size, output_count, ptr,
+                        kStaticScratchBytes);
 }
 
 extern "C" int kd_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,

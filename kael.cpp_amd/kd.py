@@ -134,6 +134,7 @@ BACKEND_ONLY = {
     "copy_d2h": (c_int, [c_void_p, c_void_p, c_int64]),
     "copy_d2d": (c_int, [c_void_p, c_void_p, c_int64]),
     "matmul": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes)]),
+    "reduce_noalloc": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "event_create": (c_int, [POINTER(c_void_p)]),
     "event_destroy": (c_int, [c_void_p]),
     "event_record": (c_int, [c_void_p]),
