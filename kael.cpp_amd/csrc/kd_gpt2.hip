@@ -438,11 +438,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             a1 += r.x * xx.x + r.y * xx.y + r.z * xx.z + r.w * xx.w;
         }
     }
-#pragma unroll
-    for (int m = 32; m > 0; m /= 2) {
-        a0 += __shfl_xor(a0, m, 64);
-        a1 += __shfl_xor(a1, m, 64);
-    }
+    a0 = wave_sum(a0);
+    a1 = wave_sum(a1);
     if constexpr (WavesPerRow == 4) {
         if (lane == 0) {
             part[wave][0] = a0;
@@ -559,11 +556,8 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
             a0 += c0[i].x * h[i].x + c0[i].y * h[i].y + c0[i].z * h[i].z + c0[i].w * h[i].w;
             a1 += c1[i].x * h[i].x + c1[i].y * h[i].y + c1[i].z * h[i].z + c1[i].w * h[i].w;
         }
-#pragma unroll
-        for (int m = 32; m > 0; m /= 2) {
-            a0 += __shfl_xor(a0, m, 64);
-            a1 += __shfl_xor(a1, m, 64);
-        }
+        a0 = wave_sum(a0);
+        a1 = wave_sum(a1);
         const int64_t n = 2 * p;
         if (lane == 0) a.out[n] = a0;
         if (lane == 1 && n + 1 < N) a.out[n + 1] = a1;
@@ -671,8 +665,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
     float local_max = -INFINITY;
     const auto score = [&](int64_t j, float4 k) {
         float sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
-#pragma unroll
-        for (int m = 8; m > 0; m /= 2) sc += __shfl_xor(sc, m, 64);
+        sc = row16_sum(sc);
         sc = __fdiv_rn(sc, divisor);
         if (sub == 0) scores[j] = sc;
         local_max = max_na(local_max, sc);
@@ -687,8 +680,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
         if (dims_ok) k = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
         score(j, k);
     }
-#pragma unroll
-    for (int m = 32; m > 0; m /= 2) local_max = max_na(local_max, __shfl_xor(local_max, m, 64));
+    local_max = wave_max(local_max);
     if (lane == 0) red_f[wave] = local_max;
     __syncthreads();
     float largest = red_f[0];
@@ -699,8 +691,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
         scores[j] = e;
         total += static_cast<double>(e);
     }
-#pragma unroll
-    for (int m = 32; m > 0; m /= 2) total += __shfl_xor(total, m, 64);
+    total = wave_sum(total);
     if (lane == 0) red_d[wave] = total;
     __syncthreads();
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1588,14 +1579,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const float
         float4 k = make_float4(0.f, 0.f, 0.f, 0.f);
         if (dims_ok) k = *reinterpret_cast<const float4*>(K + j * head_dim + 4 * sub);
         float sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
-#pragma unroll
-        for (int m = 8; m > 0; m /= 2) sc += __shfl_xor(sc, m, 64);
+        sc = row16_sum(sc);
         sc = __fdiv_rn(sc, divisor);
         if (sub == 0) scores[j] = sc;
         local_max = max_na(local_max, sc);
     }
-#pragma unroll
-    for (int m = 32; m > 0; m /= 2) local_max = max_na(local_max, __shfl_xor(local_max, m, 64));
+    local_max = wave_max(local_max);
     if (lane == 0) red_f[wave] = local_max;
     __syncthreads();
     float largest = red_f[0];
@@ -1606,8 +1595,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const float
         scores[j] = e;
         total += static_cast<double>(e);
     }
-#pragma unroll
-    for (int m = 32; m > 0; m /= 2) total += __shfl_xor(total, m, 64);
+    total = wave_sum(total);
     if (lane == 0) red_d[wave] = total;
     __syncthreads();
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
