@@ -369,6 +369,23 @@ int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int
  * the storage of kael's parameter tensor on this device); the copy is complete on return. No
  * reference counterpart: it serves the optional kael branch that runs nn::generate on this engine. */
 int kd_gpt_load_parameter_device(void* handle, const char* name, const float* data, int64_t count);
+/* reference src/nn/transformer.cpp:297-308 `load_gpt2_weights(GPT&, path)` over
+ * src/io/safetensors.cpp:258-318 `read_safetensors`: loads a Hugging Face GPT-2 checkpoint
+ * (model.safetensors) into the engine. The file is memory-mapped and checked as the reference checks
+ * it (header size, entry dtype / shape / offsets, entries tiling the data, bool bytes); names are
+ * translated to kael's (transformer. prefix dropped, h.N. -> blocks.N., c_attn -> qkv, ...), the
+ * Conv1D weights of qkv / proj / fc1 / fc2 transposed from [in, out], entries kael's GPT does not
+ * have ignored; a missing parameter or a wrong shape is KD_E_INVALID before anything is copied
+ * (Module::load_state_dict). Values convert to f32 as kael's copy_ converts F64 / I64 / BOOL; F16
+ * and BF16, which the reference rejects, are widened; other dtypes are KD_E_UNSUPPORTED. */
+int kd_gpt_load_safetensors(void* handle, const char* path);
+/* One tensor of a safetensors file as f32 on the host (no device needed), the file checked as
+ * kd_gpt_load_safetensors checks it: *dims = its rank, shape[0..rank) its sizes (shape may be NULL);
+ * with out == NULL only the rank and shape are returned, else `capacity` (elements) must hold it.
+ * The reference's counterpart is src/io/safetensors.cpp:320-322 `load_safetensors` (a map of every
+ * tensor); this returns one tensor per call so that a plain C caller needs no map type. */
+int kd_safetensors_tensor(const char* path, const char* name, float* out, int64_t capacity, int64_t* shape,
+                          int32_t* dims);
 /* Runs the prompt through the model from position 0 with an empty KV cache; the last position's
  * greedy token becomes the first generated token. Clears any previous sequence. A prompt longer
  * than max_positions runs its last max_positions tokens, as nn::generate does (reference

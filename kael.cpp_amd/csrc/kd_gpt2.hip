@@ -37,6 +37,7 @@
 #include <vector>
 
 #include "kd_internal.h"
+#include "../host/kd_safetensors.h"
 
 namespace kd {
 
@@ -1634,6 +1635,7 @@ struct Engine {
     std::unordered_map<std::string, std::pair<int64_t, int64_t>> offsets;  // name -> (offset, count)
     std::vector<bool> loaded;
     std::vector<std::string> names;
+    std::unordered_map<std::string, std::vector<int64_t>> shape_of;  // name -> kael's shape
     float* kcache = nullptr;
     float* vcache = nullptr;
     float* x = nullptr;
@@ -2145,30 +2147,33 @@ int create(Engine& e, const kd_gpt_config& c) {
     e.d = c.dimension;
     e.hd = c.dimension / c.heads;
     e.ff = 4 * c.dimension;
-    // kael's parameter order and shapes (GPT::named_parameters)
-    std::vector<std::pair<std::string, int64_t>> shapes;
-    shapes.emplace_back("token_embedding.weight", c.vocab_size * e.d);
-    shapes.emplace_back("position_embedding.weight", c.max_positions * e.d);
+    // kael's parameter order and shapes (GPT::named_parameters; Linear weights [out, in])
+    std::vector<std::pair<std::string, std::vector<int64_t>>> shapes;
+    shapes.emplace_back("token_embedding.weight", std::vector<int64_t>{c.vocab_size, e.d});
+    shapes.emplace_back("position_embedding.weight", std::vector<int64_t>{c.max_positions, e.d});
     for (int64_t l = 0; l < c.layers; ++l) {
         const std::string b = "blocks." + std::to_string(l) + ".";
-        shapes.emplace_back(b + "ln1.weight", e.d);
-        shapes.emplace_back(b + "ln1.bias", e.d);
-        shapes.emplace_back(b + "attn.qkv.weight", 3 * e.d * e.d);
-        shapes.emplace_back(b + "attn.qkv.bias", 3 * e.d);
-        shapes.emplace_back(b + "attn.proj.weight", e.d * e.d);
-        shapes.emplace_back(b + "attn.proj.bias", e.d);
-        shapes.emplace_back(b + "ln2.weight", e.d);
-        shapes.emplace_back(b + "ln2.bias", e.d);
-        shapes.emplace_back(b + "mlp.fc1.weight", e.ff * e.d);
-        shapes.emplace_back(b + "mlp.fc1.bias", e.ff);
-        shapes.emplace_back(b + "mlp.fc2.weight", e.d * e.ff);
-        shapes.emplace_back(b + "mlp.fc2.bias", e.d);
+        shapes.emplace_back(b + "ln1.weight", std::vector<int64_t>{e.d});
+        shapes.emplace_back(b + "ln1.bias", std::vector<int64_t>{e.d});
+        shapes.emplace_back(b + "attn.qkv.weight", std::vector<int64_t>{3 * e.d, e.d});
+        shapes.emplace_back(b + "attn.qkv.bias", std::vector<int64_t>{3 * e.d});
+        shapes.emplace_back(b + "attn.proj.weight", std::vector<int64_t>{e.d, e.d});
+        shapes.emplace_back(b + "attn.proj.bias", std::vector<int64_t>{e.d});
+        shapes.emplace_back(b + "ln2.weight", std::vector<int64_t>{e.d});
+        shapes.emplace_back(b + "ln2.bias", std::vector<int64_t>{e.d});
+        shapes.emplace_back(b + "mlp.fc1.weight", std::vector<int64_t>{e.ff, e.d});
+        shapes.emplace_back(b + "mlp.fc1.bias", std::vector<int64_t>{e.ff});
+        shapes.emplace_back(b + "mlp.fc2.weight", std::vector<int64_t>{e.d, e.ff});
+        shapes.emplace_back(b + "mlp.fc2.bias", std::vector<int64_t>{e.d});
     }
-    shapes.emplace_back("ln_final.weight", e.d);
-    shapes.emplace_back("ln_final.bias", e.d);
+    shapes.emplace_back("ln_final.weight", std::vector<int64_t>{e.d});
+    shapes.emplace_back("ln_final.bias", std::vector<int64_t>{e.d});
     int64_t total = 0;
-    for (const auto& [name, count] : shapes) {
+    for (const auto& [name, shape] : shapes) {
+        int64_t count = 1;
+        for (const int64_t s : shape) count *= s;
         e.offsets[name] = {total, count};
+        e.shape_of[name] = shape;
         e.names.push_back(name);
         total += (count + 63) / 64 * 64;  // keep every parameter 256-byte aligned
     }
@@ -2250,6 +2255,67 @@ int kd_gpt_load_parameter(void* handle, const char* name, const float* data, int
 
 int kd_gpt_load_parameter_device(void* handle, const char* name, const float* data, int64_t count) {
     return load_parameter("kd_gpt_load_parameter_device", handle, name, data, count, true);
+}
+
+int kd_gpt_load_safetensors(void* handle, const char* path) {
+    namespace st = kd::safetensors;
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || path == nullptr) return fail(KD_E_INVALID, "kd_gpt_load_safetensors: null argument");
+    std::string error;
+    bool unsupported = false;
+    const auto file = st::File::open(path, &error, &unsupported);
+    if (!file) return fail(unsupported ? KD_E_UNSUPPORTED : KD_E_INVALID, "kd_gpt_load_safetensors: " + error);
+    // kael's name of each stored tensor; entries kael's GPT does not have are ignored, and of two
+    // that translate to one name the first in name order is kept (load_gpt2_weights' emplace)
+    std::unordered_map<std::string, const st::Entry*> found;
+    for (const st::Entry& entry : file->entries()) {
+        const std::string name = st::translated_gpt2_name(entry.name);
+        if (e->offsets.count(name) != 0) found.emplace(name, &entry);
+    }
+    const auto shape_text = [](const std::vector<int64_t>& s) {
+        std::string t = "[";
+        for (size_t i = 0; i < s.size(); ++i) t += (i ? ", " : "") + std::to_string(s[i]);
+        return t + "]";
+    };
+    // every parameter present with kael's shape before any is copied (Module::load_state_dict)
+    for (const std::string& name : e->names) {
+        const auto it = found.find(name);
+        if (it == found.end()) return fail(KD_E_INVALID, "kd_gpt_load_safetensors: state dict is missing parameter " + name);
+        std::vector<int64_t> shape = it->second->shape;
+        if (st::stored_transposed(name) && shape.size() == 2) std::swap(shape[0], shape[1]);
+        if (shape != e->shape_of.at(name))
+            return fail(KD_E_INVALID, "kd_gpt_load_safetensors: parameter " + name + " has shape " +
+                                          shape_text(e->shape_of.at(name)) + " but the state dict has " + shape_text(shape));
+    }
+    std::vector<float> values;
+    for (const std::string& name : e->names) {
+        const st::Entry& entry = *found.at(name);
+        values.resize(static_cast<size_t>(entry.numel()));
+        file->to_f32(entry, values.data(), st::stored_transposed(name) && entry.shape.size() == 2);
+        if (int rc = load_parameter("kd_gpt_load_safetensors", handle, name.c_str(), values.data(), entry.numel(), false))
+            return rc;
+    }
+    return KD_OK;
+}
+
+int kd_safetensors_tensor(const char* path, const char* name, float* out, int64_t capacity, int64_t* shape,
+                          int32_t* dims) {
+    namespace st = kd::safetensors;
+    if (path == nullptr || name == nullptr || dims == nullptr) return fail(KD_E_INVALID, "kd_safetensors_tensor: null argument");
+    std::string error;
+    bool unsupported = false;
+    const auto file = st::File::open(path, &error, &unsupported);
+    if (!file) return fail(unsupported ? KD_E_UNSUPPORTED : KD_E_INVALID, "kd_safetensors_tensor: " + error);
+    const st::Entry* entry = file->find(name);
+    if (entry == nullptr) return fail(KD_E_INVALID, std::string("kd_safetensors_tensor: no tensor named ") + name);
+    if (entry->shape.size() > KD_MAX_DIMS) return fail(KD_E_UNSUPPORTED, "kd_safetensors_tensor: more than 8 dims");
+    *dims = static_cast<int32_t>(entry->shape.size());
+    if (shape != nullptr)
+        for (size_t i = 0; i < entry->shape.size(); ++i) shape[i] = entry->shape[i];
+    if (out == nullptr) return KD_OK;  // size query
+    if (capacity < entry->numel()) return fail(KD_E_INVALID, "kd_safetensors_tensor: output holds fewer elements than the tensor");
+    file->to_f32(*entry, out, false);
+    return KD_OK;
 }
 
 int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length) {

@@ -144,6 +144,9 @@ BACKEND_ONLY = {
     "gpt_destroy": (None, [c_void_p]),
     "gpt_load_parameter": (c_int, [c_void_p, ctypes.c_char_p, c_void_p, c_int64]),
     "gpt_load_parameter_device": (c_int, [c_void_p, ctypes.c_char_p, c_void_p, c_int64]),
+    "gpt_load_safetensors": (c_int, [c_void_p, ctypes.c_char_p]),
+    "safetensors_tensor": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int64, POINTER(c_int64),
+                                   POINTER(c_int32)]),
     "gpt_supported": (c_int, [POINTER(GptConfig)]),
     "gpt_prefill": (c_int, [c_void_p, c_void_p, c_int64]),
     "gpt_decode": (c_int, [c_void_p, c_int64, c_void_p]),
@@ -268,18 +271,13 @@ class Gpt:
                      f"kd_gpt_load_parameter({name})")
 
     def load_gpt2_safetensors(self, path) -> None:
-        """Loads a Hugging Face GPT-2 checkpoint (`model.safetensors`), as kael's
-        load_gpt2_weights does (reference src/nn/transformer.cpp:297-308): names translated,
+        """Loads a Hugging Face GPT-2 checkpoint (`model.safetensors`) through the library's own
+        reader (kd_gpt_load_safetensors), as kael's load_gpt2_weights does (reference
+        src/nn/transformer.cpp:297-308): the file memory-mapped and checked, names translated,
         Conv1D weights transposed, entries kael's GPT does not have ignored, a missing one an
-        error. The file is memory-mapped; f16 tensors are widened to f32."""
-        from safetensors import safe_open
-
-        c = self.config
-        expected = dict(gpt2_parameter_shapes(c.vocab_size, c.max_positions, c.layers, c.dimension))
-        with safe_open(str(path), framework="numpy") as f:
-            state = gpt2_state_from_hf({k: f.get_tensor(k) for k in f.keys()}, expected)
-        for name, array in state.items():
-            self.load(name, array)
+        error."""
+        self.b.check(self.b.lib.kd_gpt_load_safetensors(self.handle, os.fsencode(str(path))),
+                     "kd_gpt_load_safetensors")
 
     def prefill(self, prompt) -> None:
         p = np.ascontiguousarray(prompt, dtype=np.int64)
@@ -334,53 +332,6 @@ def gpt2_parameter_shapes(vocab_size=50257, max_positions=1024, layers=12, dimen
     return shapes
 
 
-def gpt2_name(stored: str) -> str:
-    """kael's name for a Hugging Face GPT-2 tensor (reference translated_gpt2_name,
-    src/nn/transformer.cpp:54-81)."""
-    name = stored[len("transformer."):] if stored.startswith("transformer.") else stored
-    if name.startswith("wte."):
-        return "token_embedding." + name[len("wte."):]
-    if name.startswith("wpe."):
-        return "position_embedding." + name[len("wpe."):]
-    if name.startswith("ln_f."):
-        return "ln_final." + name[len("ln_f."):]
-    if name.startswith("h."):
-        name = "blocks." + name[2:]
-        for old, new in ((".ln_1.", ".ln1."), (".ln_2.", ".ln2."), (".attn.c_attn.", ".attn.qkv."),
-                         (".attn.c_proj.", ".attn.proj."), (".mlp.c_fc.", ".mlp.fc1."), (".mlp.c_proj.", ".mlp.fc2.")):
-            name = name.replace(old, new, 1)
-    return name
-
-
-def gpt2_stored_transposed(name: str) -> bool:
-    """Conv1D weights are stored [in, out] (reference stored_transposed, transformer.cpp:83-89)."""
-    conv1d = any(part in name for part in (".attn.qkv.", ".attn.proj.", ".mlp.fc1.", ".mlp.fc2."))
-    return conv1d and name.endswith(".weight")
-
-
-def gpt2_state_from_hf(tensors: dict, expected: dict) -> dict:
-    """kael parameters (name -> f32 array of the expected shape) from Hugging Face GPT-2 tensors:
-    unknown entries are dropped, a missing or misshapen parameter raises ValueError."""
-    state = {}
-    for stored, array in tensors.items():
-        name = gpt2_name(stored)
-        if name not in expected:
-            continue
-        a = np.asarray(array)
-        if a.dtype not in (np.float32, np.float16, np.float64):
-            raise ValueError(f"GPT-2 weights: {stored} has dtype {a.dtype}, expected a float dtype")
-        if gpt2_stored_transposed(name):
-            a = a.T
-        a = np.ascontiguousarray(a, dtype=np.float32)
-        if a.shape != tuple(expected[name]):
-            raise ValueError(f"GPT-2 weights: {stored} has shape {a.shape}, {name} needs {tuple(expected[name])}")
-        state[name] = a
-    missing = [n for n in expected if n not in state]
-    if missing:
-        raise ValueError(f"GPT-2 weights: missing {len(missing)} entries, e.g. {missing[:3]}")
-    return state
-
-
 _BACKEND: Backend | None = None
 
 
@@ -420,3 +371,16 @@ def element_layout(shape, strides_bytes, bases) -> ElementLayout:
     for op, b in enumerate(bases):
         lay.base[op] = b
     return lay
+
+
+def safetensors_tensor(backend: Backend, path, name: str) -> np.ndarray:
+    """One tensor of a safetensors file as float32, read by the library on the host
+    (kd_safetensors_tensor): no device is needed."""
+    dims = c_int32()
+    shape = (c_int64 * MAX_DIMS)()
+    p, n = os.fsencode(str(path)), name.encode()
+    backend.check(backend.lib.kd_safetensors_tensor(p, n, None, 0, shape, ctypes.byref(dims)), "kd_safetensors_tensor")
+    out = np.empty(tuple(shape[i] for i in range(dims.value)), np.float32)
+    backend.check(backend.lib.kd_safetensors_tensor(p, n, out.ctypes.data_as(c_void_p), out.size, shape,
+                                                    ctypes.byref(dims)), "kd_safetensors_tensor")
+    return out

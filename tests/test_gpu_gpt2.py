@@ -115,6 +115,52 @@ def test_hugging_face_checkpoint_loads_into_the_engine(kdb, refdev, tmp_path):
         ref.ref_gpt_destroy(h)
 
 
+@pytest.mark.parametrize("prefix", [True, False], ids=["transformer_prefix", "bare"])
+def test_checkpoint_load_rules(kdb, refdev, tmp_path, prefix):
+    """kd_gpt_load_safetensors as kael's load_gpt2_weights + load_state_dict (reference
+    src/nn/transformer.cpp:297-308, src/nn/module.cpp:94-109): with or without the `transformer.`
+    prefix it loads; a missing parameter or a weight in the wrong layout is an error before anything
+    is copied; an F16 checkpoint loads widened, giving kael's logits for the f16-rounded weights."""
+    from safetensors.numpy import save_file
+
+    ref = refdev
+    h = ref.ref_gpt_create(11, 16, 2, 2, 8, 31, 1)
+    assert h, support.ref_error(ref)
+    try:
+        params = support.export_gpt_params(ref, h)
+        tokens = np.random.default_rng(2).integers(0, 11, 8)
+        hf = support.hf_gpt2_tensors(params, prefix_blocks=prefix)
+        path = tmp_path / "model.safetensors"
+        save_file(hf, str(path))
+        g = kd.Gpt(kdb, 11, 16, 2, 2, 8, True)
+        g.load_gpt2_safetensors(path)
+        np.testing.assert_allclose(g.forward_logits(tokens), cpu_cached_logits(ref, h, tokens, 1, 11), rtol=1e-5, atol=1e-6)
+
+        block = "transformer.h.1." if prefix else "h.1."
+        missing = dict(hf)
+        del missing[block + "mlp.c_fc.bias"]
+        save_file(missing, str(tmp_path / "missing.safetensors"))
+        with pytest.raises(kd.KdError, match="missing parameter blocks.1.mlp.fc1.bias"):
+            kd.Gpt(kdb, 11, 16, 2, 2, 8, True).load_gpt2_safetensors(tmp_path / "missing.safetensors")
+        wrong = dict(hf)
+        wrong[block + "attn.c_attn.weight"] = np.ascontiguousarray(wrong[block + "attn.c_attn.weight"].T)
+        save_file(wrong, str(tmp_path / "wrong.safetensors"))
+        with pytest.raises(kd.KdError, match="shape"):
+            kd.Gpt(kdb, 11, 16, 2, 2, 8, True).load_gpt2_safetensors(tmp_path / "wrong.safetensors")
+
+        half = {k: v.astype(np.float16) for k, v in hf.items()}
+        save_file(half, str(tmp_path / "half.safetensors"))
+        g16 = kd.Gpt(kdb, 11, 16, 2, 2, 8, True)
+        g16.load_gpt2_safetensors(tmp_path / "half.safetensors")
+        for i, (name, data) in enumerate(params):  # kael with the same rounded weights
+            rounded = np.ascontiguousarray(data.astype(np.float16).astype(np.float32))
+            assert ref.ref_gpt_set_param(h, i, rounded.ctypes.data_as(ctypes.c_void_p)) == 0, support.ref_error(ref)
+        np.testing.assert_allclose(g16.forward_logits(tokens), cpu_cached_logits(ref, h, tokens, 1, 11), rtol=1e-5,
+                                   atol=1e-6)
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
 def check_prefill_and_steps(g, ref, h, prompt, steps, vocab, rtol):
     """Prefill `prompt`, then `steps` greedy decode steps; the logits after the prefill and
     after every step against kael's cached forward over kael's own greedy sequence."""
