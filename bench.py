@@ -4,7 +4,9 @@ Headline (BASELINE.json metric): f32 matmul TFLOP/s as a fraction of FP32 MFMA p
 north-star size 4096^3 (C = A.B, A and B contiguous row-major, uniform[-1,1]); a "step" is one
 kd_matmul call over inputs already resident in HBM. Secondary figures in "extra": the C1 shape
 (512^3), the C2 elementwise/reduction ops in GB/s, the fused row kernels, the index and
-optimizer kernels at GPT-2-small scale, and GPT-2-small decode tokens/s.
+optimizer kernels at GPT-2-small scale, a C3 and a C4 training step (replayed from the recorded
+device calls of kael's own loop, see bench_replay), and GPT-2-small decode tokens/s. Each
+section carries kael's CPU path on the same workload as its cpu_baseline.
 
 Timing: W untimed warm-up steps, then K steps bracketed by kd_synchronize(); the kernel time comes
 from HIP events recorded on the backend stream (the stream every kd_* launch uses). The GPU's
@@ -14,7 +16,8 @@ whose steps take microseconds, warm up for at least MIN_WARMUP_S of steps.
 The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference sources,
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only matmul|c1|c2|rows|train|gpt2|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--only matmul|c1|c2|rows|train|c3|c4|gpt2|copy]
 """
 from __future__ import annotations
 
@@ -297,6 +300,124 @@ def bench_gpt2(backend, prompt_len=64, new_tokens=256, repeats=3, eager=False):
             "sequence_head": g.sequence()[prompt_len:prompt_len + 8].tolist()}
 
 
+def bench_replay(backend, name, steps):
+    """Configs C3 / C4: one training step of kael on this backend. bench.py does not run kael (its
+    host code is built only from the reference sources, under oracle/, for the tests); instead it
+    replays the step's recorded device calls (tests/golden/<name>_step_calls.jsonl.gz, written by
+    tests/golden/make_step_traces.py from kael's own training loop with the optional device
+    branches) against the C ABI: the same calls, shapes, strides and order as kael issues them,
+    including the blocking loss read. Parameters upload as zeros in C4 (only token ids and targets
+    are recorded); C3 records every upload, so its replay reproduces kael's losses.
+
+    step_ms: HIP-event time per replayed step (K repetitions of the last traced step, Python issuing
+    the calls); kernel_ms: the sum of per-call event times, one pass with events around every call;
+    matmul: the per-call times of the step's products and their FLOPs."""
+    import replay
+
+    recs = replay.load(ROOT / "tests" / "golden" / f"{name}_step_calls.jsonl.gz")
+    setup, step_recs = replay.split_steps(recs)
+    rp = replay.Replay(backend, recs)
+    rp.run(setup)
+    for s in step_recs:
+        rp.run(s)  # the traced steps, with their index operands checked
+    backend.synchronize()
+    losses = list(rp.losses)
+    last = step_recs[-1]
+    for _ in range(3):
+        rp.run(last, checked=False)
+    backend.synchronize()
+    t0 = time.perf_counter()
+    with Timer(backend) as t:
+        for _ in range(steps):
+            rp.run(last, checked=False)
+    backend.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms = t.ms / steps
+    # one pass with an event pair around every call
+    lib = backend.lib
+    pairs = []
+
+    def timed(r, call):
+        e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+        backend.check(lib.kd_event_create(ctypes.byref(e0)), "event")
+        backend.check(lib.kd_event_create(ctypes.byref(e1)), "event")
+        backend.check(lib.kd_event_record(e0), "record")
+        call()
+        backend.check(lib.kd_event_record(e1), "record")
+        pairs.append((r, e0, e1))
+
+    rp.run(last, checked=False, on_call=timed)
+    backend.synchronize()
+    per_call = []
+    for r, e0, e1 in pairs:
+        ms = ctypes.c_float()
+        backend.check(lib.kd_event_elapsed_ms(ctypes.byref(ms), e0, e1), "elapsed")
+        per_call.append((r, ms.value))
+        lib.kd_event_destroy(e0)
+        lib.kd_event_destroy(e1)
+    mm = [(r, ms) for r, ms in per_call if r["op"] in ("matmul", "matmul_strided")]
+    mm_ms = sum(ms for _, ms in mm)
+    flops = replay.matmul_flops(last)
+    counts = {}
+    for r in last:
+        counts[r["op"]] = counts.get(r["op"], 0) + 1
+    return {"step_ms": step_ms, "wall_ms": wall_ms, "kernel_ms": sum(ms for _, ms in per_call),
+            "calls_per_step": len(last), "calls": counts,
+            "matmul": {"count": len(mm), "ms": mm_ms, "gflop": flops / 1e9,
+                       "tflops": flops / (mm_ms * 1e-3) / 1e12 if mm_ms else None,
+                       "frac_peak": flops / (mm_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if mm_ms else None},
+            "replay_losses": losses, "kael_losses": replay.traced_losses(recs),
+            "data": "C3: kael's recorded inputs and initial parameters; C4: recorded token ids and targets, "
+                    "parameters zero"}
+
+
+def cpu_train_baseline(name):
+    """kael's own training step on the CPU path (reference build, threaded), same config and loop
+    as the traced one: C3 100 SGD steps, C4 3 Adam steps (each ~0.7 s); seconds per step."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import support
+
+    lib = support.load_ref("ref")
+    threads = int(os.environ.get("KAEL_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    lib.ref_set_threads(threads)
+    secs = ctypes.c_double()
+    if name == "c3":
+        steps = 100
+        losses = np.zeros(steps, np.float32)
+        rc = lib.ref_train_mlp(0, steps, losses.ctypes.data_as(ctypes.c_void_p), None, ctypes.byref(secs))
+    else:
+        steps = 3
+        losses = np.zeros(steps, np.float32)
+        rc = lib.ref_train_chargpt(0, steps, losses.ctypes.data_as(ctypes.c_void_p), ctypes.byref(secs))
+    if rc != 0:
+        raise RuntimeError(support.ref_error(lib))
+    return {"value": secs.value / steps * 1e3, "unit": "ms/step", "cores": threads, "kind": "reference",
+            "sample": f"kael {'ref_train_mlp' if name == 'c3' else 'ref_train_chargpt'} on the CPU path, {steps} steps "
+                      f"(forward, cross-entropy, backward, {'SGD' if name == 'c3' else 'Adam'}, loss read)"}
+
+
+def cpu_c2_baseline(iters=5):
+    """kael's C2 ops on the CPU path (reference build, threaded): median of `iters` calls each."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import support
+
+    lib = support.load_ref("ref")
+    threads = int(os.environ.get("KAEL_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    lib.ref_set_threads(threads)
+    rows = cols = 4096
+    algo_bytes = {"add": 2 * rows * cols * 4 + rows * 4, "mul": 2 * rows * cols * 4 + rows * 4,
+                  "transposed_add": 2 * rows * cols * 4 + rows * 4, "sum_dim1": rows * cols * 4 + rows * 4,
+                  "max_all": rows * cols * 4 + 4}
+    out = {}
+    for which, op in enumerate(("add", "mul", "transposed_add", "sum_dim1", "max_all")):
+        t = ctypes.c_double()
+        if lib.ref_time_c2(which, rows, cols, iters, ctypes.byref(t)) != 0:
+            raise RuntimeError(support.ref_error(lib))
+        out[op] = {"us": t.value * 1e6, "gbps": algo_bytes[op] / t.value / 1e9}
+    return {"ops": out, "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"kael CPU path, [4096,4096] f32 (manual_seed(1) inputs), median of {iters} calls per op"}
+
+
 def cpu_gpt2_baseline(new_tokens=8):
     """kael's own nn::generate on the CPU path (reference build), GPT-2 small, seed 4: decode
     tokens/s from two runs (1 and 1 + new_tokens new tokens) so prefill cancels out."""
@@ -345,6 +466,14 @@ def cpu_baseline(n, budget_s=20.0):
                       f"KAEL_NUM_THREADS={threads}", "median_s": t.value}
 
 
+def guarded_cpu(fn, *args):
+    """A CPU-baseline leg: its result, or the error it raised (a baseline is reported, never required)."""
+    try:
+        return fn(*args)
+    except Exception as e:
+        return {"error": str(e)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -352,7 +481,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
-    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "copy", "c2", "rows", "train", "gpt2"],
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "copy", "c2", "rows", "train", "c3", "c4",
+                                                  "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -374,11 +504,21 @@ def main() -> int:
         return 0
     if args.only == "c1":
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
+        if not args.no_cpu:
+            extra["matmul_512"]["cpu_baseline"] = guarded_cpu(cpu_baseline, 512, 5.0)
         print(json.dumps({"metric": "C1 f32 matmul 512^3", "extra": extra}))
+        return 0
+    if args.only in ("c3", "c4"):
+        extra[args.only] = bench_replay(backend, args.only, max(args.steps, 10))
+        if not args.no_cpu:
+            extra[args.only]["cpu_baseline"] = guarded_cpu(cpu_train_baseline, args.only)
+        print(json.dumps({"metric": f"{args.only} training step (replayed kael device calls)", "extra": extra}))
         return 0
     if args.only in ("c2", "rows", "train"):
         fn = {"c2": bench_c2, "rows": bench_rows, "train": bench_train}[args.only]
         extra[args.only] = fn(backend, args.steps, args.warmup)
+        if args.only == "c2" and not args.no_cpu:
+            extra["c2"]["cpu_baseline"] = guarded_cpu(cpu_c2_baseline)
         print(json.dumps({"metric": f"{args.only} only", "extra": extra}))
         return 0
     # The headline warms up like every other section: W steps, then steps for at least
@@ -390,6 +530,8 @@ def main() -> int:
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
         extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
         extra["train"] = bench_train(backend, max(args.steps, 20), args.warmup)
+        extra["c3"] = bench_replay(backend, "c3", max(args.steps, 20))
+        extra["c4"] = bench_replay(backend, "c4", max(args.steps, 10))
         extra["gpt2_decode"] = bench_gpt2(backend)
     cpu = None
     if not args.no_cpu:
@@ -397,6 +539,13 @@ def main() -> int:
             cpu = cpu_baseline(n)
         except Exception as e:  # the baseline is reported, never required
             cpu = {"error": str(e)}
+        if "matmul_512" in extra:
+            extra["matmul_512"]["cpu_baseline"] = guarded_cpu(cpu_baseline, 512, 5.0)
+        if "c2" in extra:
+            extra["c2"]["cpu_baseline"] = guarded_cpu(cpu_c2_baseline)
+        for name in ("c3", "c4"):
+            if name in extra:
+                extra[name]["cpu_baseline"] = guarded_cpu(cpu_train_baseline, name)
         if "gpt2_decode" in extra:
             try:
                 gcpu = cpu_gpt2_baseline()

@@ -1,0 +1,315 @@
+"""Replays a recorded sequence of kael device calls against the C ABI (libkd.so).
+
+A trace is one JSON object per line, as the oracle backend's call trace writes it (KD_ORACLE_TRACE,
+oracle/oracle_backend.cpp): every `kael::device` call of a kael run with its arguments, device
+pointers as [allocation id, byte offset], host-to-device copies with their bytes when the recording
+kept them, and "mark" records at the start of each training step. Replaying it issues exactly the
+backend calls that kael's host code made, in the same order, without kael itself: bench.py times a
+C3 / C4 training step this way.
+
+Every allocation of the trace gets its own device buffer, zero-filled first; copies whose bytes
+were not recorded upload zeros. The first run of the records checks every call that reads indices
+(gather, scatter_add, cross-entropy targets) against the bytes of what it indexes, reading the
+indices back, so that no replayed kernel can address memory outside its buffers; `run(checked=False)`
+then replays the same records without those reads.
+"""
+from __future__ import annotations
+
+import gzip
+import json
+from ctypes import byref, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+import kd
+
+ELEMENT_BYTES = {kd.F32: 4, kd.F64: 8, kd.I64: 8, kd.BOOL: 1}
+
+
+class ReplayError(RuntimeError):
+    pass
+
+
+def load(path) -> list[dict]:
+    opener = gzip.open if str(path).endswith(".gz") else open
+    with opener(path, "rt") as f:
+        return [json.loads(line) for line in f if line.strip()]
+
+
+def split_steps(records: list[dict]) -> tuple[list[dict], list[list[dict]]]:
+    """(the records before the first step mark, the records of each step)."""
+    setup: list[dict] = []
+    steps: list[list[dict]] = []
+    for r in records:
+        if r["op"] == "mark":
+            if r.get("name") == "step":
+                steps.append([])
+            continue
+        if r["op"] != "result":
+            (steps[-1] if steps else setup).append(r)
+    return setup, steps
+
+
+def traced_losses(records: list[dict]) -> list[float]:
+    """kael's loss of each traced step (the trace's "result" record), if recorded."""
+    for r in records:
+        if r["op"] == "result":
+            return list(r["losses"])
+    return []
+
+
+def matmul_flops(records: list[dict]) -> int:
+    return sum(2 * r["sizes"][0] * r["sizes"][1] * r["sizes"][2] * r["sizes"][3]
+               for r in records if r["op"] in ("matmul", "matmul_strided"))
+
+
+# pointer fields of each record kind (the layout bases of convert / elementwise are checked apart)
+POINTERS = {
+    "h2d": ("t",), "d2h": ("s",), "d2d": ("t", "s"), "fill": ("t",), "convert": (), "elementwise": (),
+    "reduce": ("results", "data"), "arg_reduce": ("results", "data"), "cumsum": ("out", "data"),
+    "matmul": ("a", "b", "c"), "matmul_strided": ("a", "b", "c"), "gather": ("out", "data", "indices"),
+    "scatter_add": ("data", "indices", "source"), "softmax_rows": ("out", "x"), "standardize_rows": ("out", "x"),
+    "cross_entropy_rows": ("losses", "logits", "targets"), "cross_entropy_grad": ("out", "logits", "targets", "weights"),
+    "softmax_rows_backward": ("out", "y", "grad"), "standardize_rows_backward": ("out", "x", "y", "grad"),
+    "adam_step": ("p", "g", "m", "v"), "sgd_step": ("p", "g"),
+}
+
+
+def validate(records: list[dict]) -> None:
+    """Checks a trace without a device: known record kinds, every device pointer inside an
+    allocation that is live at that record (allocated before, not yet freed), copies inside their
+    allocations."""
+    size: dict[int, int] = {}
+    live: set[int] = set()
+
+    def check(p, what, need=0):
+        if p is None:
+            return
+        i, off = p
+        if i not in live:
+            raise ReplayError(f"{what}: allocation {i} is not live")
+        if off < 0 or off + need > size[i]:
+            raise ReplayError(f"{what}: [{off}, {off + need}) outside allocation {i} ({size[i]} bytes)")
+
+    for n, r in enumerate(records):
+        op = r["op"]
+        if op == "alloc":
+            size[r["id"]] = r["bytes"]
+            live.add(r["id"])
+        elif op == "free":
+            live.discard(r["id"])
+        elif op in ("mark", "result"):
+            continue
+        elif op not in POINTERS:
+            raise ReplayError(f"record {n}: unknown kind {op!r}")
+        else:
+            for key in POINTERS[op]:
+                need = r["bytes"] if op in ("h2d", "d2h", "d2d") else 0
+                if key == "weights" and r.get(key) is None:
+                    continue
+                check(r[key], f"record {n} {op}.{key}", need)
+            if op in ("convert", "elementwise"):
+                for o, p in enumerate(r["layout"]["base"]):
+                    check(p, f"record {n} {op}.base[{o}]")
+            if op == "h2d" and "data" in r and len(r["data"]) != 2 * r["bytes"]:
+                raise ReplayError(f"record {n}: h2d payload of {len(r['data']) // 2} bytes for {r['bytes']}")
+
+
+def element_layout(j: dict, resolve) -> kd.ElementLayout:
+    out = kd.ElementLayout()
+    out.dims, out.operands, out.count = j["dims"], j["operands"], j["count"]
+    for d, v in enumerate(j["shape"]):
+        out.shape[d] = v
+    for o, row in enumerate(j["strides"]):
+        for d, v in enumerate(row):
+            out.strides[o][d] = v
+    for o, p in enumerate(j["base"]):
+        out.base[o] = resolve(p)
+    return out
+
+
+def index_layout(j: dict) -> kd.IndexLayout:
+    out = kd.IndexLayout()
+    out.dims, out.axis, out.count = j["dims"], j["axis"], j["count"]
+    for name in ("shape", "data_strides", "index_strides", "source_strides"):
+        arr = getattr(out, name)
+        for d, v in enumerate(j[name]):
+            arr[d] = v
+    return out
+
+
+def index_span(layout: dict, skip_axis: bool) -> int:
+    """Largest element offset the non-indexed dims of an index layout reach in the indexed tensor."""
+    return sum((n - 1) * abs(s) for d, (n, s) in enumerate(zip(layout["shape"], layout["data_strides"]))
+               if not (skip_axis and d == layout["axis"]) and n > 0)
+
+
+class Replay:
+    """The calls of one trace bound to device buffers of their allocations."""
+
+    def __init__(self, backend: kd.Backend, records: list[dict]):
+        self.b = backend
+        self.records = records
+        sizes = {r["id"]: r["bytes"] for r in records if r["op"] == "alloc"}
+        self.buffers = {i: backend.empty((max(n, 1),), np.uint8) for i, n in sizes.items()}
+        zero = np.zeros(1, np.uint8)
+        for buf in self.buffers.values():
+            backend.check(backend.lib.kd_fill(kd.BOOL, c_void_p(buf.ptr), buf.nbytes, zero.ctypes.data_as(c_void_p)),
+                          "kd_fill")
+        backend.synchronize()
+        self.bound = [self._bind(r) for r in records]
+        self.losses: list[float] = []  # f32 scalars the replay read back (kael's loss.item())
+
+    # -- pointers --
+    def ptr(self, p):
+        if p is None:
+            return None
+        i, off = p
+        if i not in self.buffers:
+            raise ReplayError(f"pointer into allocation {i}, which the trace never made")
+        if not 0 <= off <= self.buffers[i].nbytes:
+            raise ReplayError(f"offset {off} outside allocation {i} ({self.buffers[i].nbytes} bytes)")
+        return self.buffers[i].ptr + off
+
+    def room(self, p) -> int:
+        """Bytes from pointer p to the end of its allocation."""
+        i, off = p
+        return self.buffers[i].nbytes - off
+
+    def read_i64(self, p, count: int) -> np.ndarray:
+        if count * 8 > self.room(p):
+            raise ReplayError("index array runs past its allocation")
+        out = np.empty(count, np.int64)
+        if count:
+            self.b.check(self.b.lib.kd_copy_d2h(out.ctypes.data_as(c_void_p), c_void_p(self.ptr(p)), count * 8),
+                         "kd_copy_d2h")
+        return out
+
+    # -- binding --
+    def _bind(self, r: dict):
+        """(call, check): `call()` issues the record's backend call; `check()` (or None) validates its
+        index operands first."""
+        lib, chk, P = self.b.lib, self.b.check, self.ptr
+        op = r["op"]
+        if op in ("alloc", "free", "mark", "result"):
+            return None, None
+        if op == "h2d":
+            data = np.frombuffer(bytes.fromhex(r["data"]), np.uint8).copy() if "data" in r else np.zeros(r["bytes"], np.uint8)
+            t, n = c_void_p(P(r["t"])), r["bytes"]
+            return (lambda: chk(lib.kd_copy_h2d(t, data.ctypes.data_as(c_void_p), n), "kd_copy_h2d")), None
+        if op == "d2h":
+            host = np.empty(max(r["bytes"], 1), np.uint8)
+            s, n = c_void_p(P(r["s"])), r["bytes"]
+
+            def d2h():
+                chk(lib.kd_copy_d2h(host.ctypes.data_as(c_void_p), s, n), "kd_copy_d2h")
+                if n == 4:
+                    self.losses.append(float(host[:4].view(np.float32)[0]))
+            return d2h, None
+        if op == "d2d":
+            t, s, n = c_void_p(P(r["t"])), c_void_p(P(r["s"])), r["bytes"]
+            return (lambda: chk(lib.kd_copy_d2d(t, s, n), "kd_copy_d2d")), None
+        if op == "fill":
+            value = np.frombuffer(bytes.fromhex(r["value"]), np.uint8).copy()
+            t = c_void_p(P(r["t"]))
+            return (lambda: chk(lib.kd_fill(r["dtype"], t, r["count"], value.ctypes.data_as(c_void_p)), "kd_fill")), None
+        if op == "convert":
+            lay = element_layout(r["layout"], P)
+            return (lambda: chk(lib.kd_convert(r["out"], r["in"], byref(lay)), "kd_convert")), None
+        if op == "elementwise":
+            lay = element_layout(r["layout"], P)
+            par = kd.params(r["reals"], r["ints"])
+            return (lambda: chk(lib.kd_elementwise(r["eop"], r["out"], r["in"], byref(lay), par), "kd_elementwise")), None
+        if op == "reduce":
+            a = (r["rop"], r["out"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["chunk"], r["rows"])
+            return (lambda: chk(lib.kd_reduce(*a), "kd_reduce")), None
+        if op == "arg_reduce":
+            a = (r["largest"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["chunk"], r["rows"])
+            return (lambda: chk(lib.kd_arg_reduce(*a), "kd_arg_reduce")), None
+        if op == "cumsum":
+            a = (r["in"], c_void_p(P(r["out"])), c_void_p(P(r["data"])), r["size"], r["rows"])
+            return (lambda: chk(lib.kd_cumsum(*a), "kd_cumsum")), None
+        if op in ("matmul", "matmul_strided"):
+            sizes = kd.MatmulSizes(*r["sizes"])
+            a, b, c = c_void_p(P(r["a"])), c_void_p(P(r["b"])), c_void_p(P(r["c"]))
+            if op == "matmul":
+                return (lambda: chk(lib.kd_matmul(r["dtype"], a, b, c, byref(sizes)), "kd_matmul")), None
+            st = kd.MatmulStrides()
+            for i in range(3):
+                st.a[i], st.b[i], st.out[i] = r["sa"][i], r["sb"][i], r["sc"][i]
+            return (lambda: chk(lib.kd_matmul_strided(r["dtype"], a, b, c, byref(sizes), byref(st)),
+                                "kd_matmul_strided")), None
+        if op in ("gather", "scatter_add"):
+            lay = index_layout(r["layout"])
+            es = ELEMENT_BYTES[r["dtype"]]
+            idx_count = r["layout"]["count"]
+            target = r["data"]  # the tensor the indices address
+
+            def check_indices():
+                # every index of the iteration (the index tensor's own strides, as the kernel reads
+                # it) must keep the addressed element inside the data allocation
+                L = r["layout"]
+                reach = 1 + sum((n - 1) * abs(s) for n, s in zip(L["shape"], L["index_strides"]) if n > 0)
+                ids = self.read_i64(r["indices"], reach) if idx_count else np.zeros(0, np.int64)
+                if ids.size == 0:
+                    return
+                axis_stride = abs(L["data_strides"][L["axis"]])
+                last = index_span(L, skip_axis=True) + int(ids.max()) * axis_stride
+                if ids.min() < 0 or (last + 1) * es > self.room(target):
+                    raise ReplayError(f"{op}: indices [{ids.min()}, {ids.max()}] leave the indexed allocation")
+            if op == "gather":
+                a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["data"])), c_void_p(P(r["indices"])), byref(lay))
+                return (lambda: chk(lib.kd_gather(*a), "kd_gather")), check_indices
+            a = (r["dtype"], c_void_p(P(r["data"])), c_void_p(P(r["indices"])), c_void_p(P(r["source"])), byref(lay))
+            return (lambda: chk(lib.kd_scatter_add(*a), "kd_scatter_add")), check_indices
+        if op == "softmax_rows":
+            a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["x"])), r["rows"], r["cols"], r["log"])
+            return (lambda: chk(lib.kd_softmax_rows(*a), "kd_softmax_rows")), None
+        if op == "standardize_rows":
+            a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["x"])), r["rows"], r["cols"], r["eps"], None, None)
+            return (lambda: chk(lib.kd_standardize_rows(*a), "kd_standardize_rows")), None
+        if op in ("cross_entropy_rows", "cross_entropy_grad"):
+            def check_targets():
+                t = self.read_i64(r["targets"], r["rows"])
+                if t.size and (t.min() < 0 or t.max() >= r["cols"]):
+                    raise ReplayError(f"{op}: targets [{t.min()}, {t.max()}] outside [0, {r['cols']})")
+            if op == "cross_entropy_rows":
+                a = (r["dtype"], c_void_p(P(r["losses"])), c_void_p(P(r["logits"])), c_void_p(P(r["targets"])),
+                     r["rows"], r["cols"])
+                return (lambda: chk(lib.kd_cross_entropy_rows(*a), "kd_cross_entropy_rows")), check_targets
+            a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["logits"])), c_void_p(P(r["targets"])),
+                 c_void_p(P(r["weights"])), r["rows"], r["cols"])
+            return (lambda: chk(lib.kd_cross_entropy_grad(*a), "kd_cross_entropy_grad")), check_targets
+        if op == "softmax_rows_backward":
+            a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["y"])), c_void_p(P(r["grad"])), r["rows"], r["cols"],
+                 r["log"])
+            return (lambda: chk(lib.kd_softmax_rows_backward(*a), "kd_softmax_rows_backward")), None
+        if op == "standardize_rows_backward":
+            a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["x"])), c_void_p(P(r["y"])), c_void_p(P(r["grad"])),
+                 r["rows"], r["cols"], r["eps"])
+            return (lambda: chk(lib.kd_standardize_rows_backward(*a), "kd_standardize_rows_backward")), None
+        if op == "adam_step":
+            a = (r["dtype"], c_void_p(P(r["p"])), c_void_p(P(r["g"])), c_void_p(P(r["m"])), c_void_p(P(r["v"])),
+                 r["count"], r["lr"], r["b1"], r["b2"], r["eps"], r["wd"], r["decoupled"], r["step"])
+            return (lambda: chk(lib.kd_adam_step(*a), "kd_adam_step")), None
+        if op == "sgd_step":
+            a = (r["dtype"], c_void_p(P(r["p"])), c_void_p(P(r["g"])), r["count"], r["lr"], r["wd"])
+            return (lambda: chk(lib.kd_sgd_step(*a), "kd_sgd_step")), None
+        raise ReplayError(f"unknown trace record {op!r}")
+
+    def run(self, records: list[dict] | None = None, checked: bool = True, on_call=None) -> None:
+        """Issues the calls of `records` (a slice of the trace this replay was built from, by
+        identity; all of it by default). `on_call(record, call)` may wrap each call (timing)."""
+        index = {id(r): i for i, r in enumerate(self.records)}
+        for r in self.records if records is None else records:
+            call, check = self.bound[index[id(r)]]
+            if call is None:
+                continue
+            if checked and check is not None:
+                self.b.synchronize()
+                check()
+            if on_call is None:
+                call()
+            else:
+                on_call(r, call)

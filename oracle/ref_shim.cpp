@@ -42,6 +42,13 @@ namespace {
 
 thread_local std::string g_error;
 
+// Marks a point of the oracle backend's call trace; defined only in the builds that link
+// oracle_backend.cpp (weak: null elsewhere).
+extern "C" void oracle_trace_mark(const char* name) __attribute__((weak));
+void trace_mark(const char* name) {
+    if (oracle_trace_mark != nullptr) oracle_trace_mark(name);
+}
+
 template <typename F> int guarded(F&& f) {
     try {
         f();
@@ -643,6 +650,7 @@ int ref_train_mlp(int device, int64_t steps, float* losses, float* params_out, d
         kael::optim::SGD optimizer(model.parameters(), kael::optim::SgdOptions{.learning_rate = 0.01});
         const auto t0 = std::chrono::steady_clock::now();
         for (int64_t step = 0; step < steps; ++step) {
+            trace_mark("step");
             optimizer.zero_grad();
             const kael::Tensor loss = kael::nn::cross_entropy(model(x), y);
             loss.backward();
@@ -738,6 +746,7 @@ int ref_train_gpt_params(int device, int64_t steps, int64_t vocab, int64_t conte
         kael::optim::Adam optimizer(model.parameters());
         const auto t0 = std::chrono::steady_clock::now();
         for (int64_t step = 0; step < steps; ++step) {
+            trace_mark("step");
             optimizer.zero_grad();
             const kael::Tensor logits = model(ids).reshape({batch * context, vocab});
             const kael::Tensor loss = kael::nn::cross_entropy(logits, targets);

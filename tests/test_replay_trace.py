@@ -1,0 +1,84 @@
+"""The recorded C3 / C4 step traces that bench.py replays (tests/golden/*_step_calls.jsonl.gz,
+written by tests/golden/make_step_traces.py from kael's own training loops): well-formed without
+a device. Every record is a known backend call, every device pointer lies inside an allocation
+that is live at that point, the trace holds the setup and two steps, and the steps issue the
+calls that C3 (MLP, SGD) and C4 (char-GPT, Adam) need."""
+from pathlib import Path
+
+import pytest
+
+import replay
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_trace_is_well_formed(name):
+    recs = replay.load(GOLDEN / f"{name}_step_calls.jsonl.gz")
+    replay.validate(recs)
+    setup, steps = replay.split_steps(recs)
+    assert len(steps) == 2 and setup
+    losses = replay.traced_losses(recs)
+    assert len(losses) == 2 and all(0 < x < 10 for x in losses)
+    ops = {r["op"] for r in steps[-1]}
+    assert {"matmul_strided", "cross_entropy_rows", "cross_entropy_grad", "d2h"} <= ops
+    assert ("sgd_step" if name == "c3" else "adam_step") in ops
+    if name == "c4":
+        # the fused row kernels and their backward passes are in the step
+        assert {"softmax_rows", "standardize_rows", "softmax_rows_backward", "standardize_rows_backward",
+                "gather", "scatter_add"} <= ops
+    # the step's products: C3 has 3 (forward 2, backward 3 minus the input gradient), C4 dozens
+    assert replay.matmul_flops(steps[-1]) > (1e7 if name == "c3" else 1e10)
+
+
+def test_validate_rejects_pointer_outside_allocation():
+    recs = [{"op": "alloc", "id": 0, "bytes": 16},
+            {"op": "d2d", "t": [0, 8], "s": [0, 0], "bytes": 16}]
+    with pytest.raises(replay.ReplayError):
+        replay.validate(recs)
+    recs[1]["bytes"] = 8
+    replay.validate(recs)
+    recs.append({"op": "free", "id": 0})
+    recs.append({"op": "fill", "dtype": 0, "t": [0, 0], "count": 1, "value": "00000000"})
+    with pytest.raises(replay.ReplayError):
+        replay.validate(recs)
+
+
+class _HostBuffer:
+    def __init__(self, n):
+        self.data = bytearray(n)
+        self.nbytes = n
+        self.ptr = id(self.data)
+
+
+class _StandIn:
+    """Enough of kd.Backend to bind a trace without a device: allocations are host bytes, the
+    library's calls are never made (binding only builds the argument structures)."""
+
+    class _Lib:
+        def __getattr__(self, name):
+            return lambda *a: 0
+
+    def __init__(self):
+        self.lib = self._Lib()
+
+    def empty(self, shape, dtype):
+        return _HostBuffer(int(shape[0]))
+
+    def check(self, rc, what=""):
+        assert rc == 0, what
+
+    def synchronize(self):
+        pass
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_every_record_binds(name):
+    """Every record of the trace turns into a bound C-ABI call (no kind left unknown), so a GPU replay
+    cannot stop half way on a record it does not know."""
+    recs = replay.load(GOLDEN / f"{name}_step_calls.jsonl.gz")
+    rp = replay.Replay(_StandIn(), recs)
+    kinds = {r["op"] for r, (call, _) in zip(recs, rp.bound) if call is not None}
+    assert "alloc" not in kinds and "mark" not in kinds
+    assert len([1 for call, _ in rp.bound if call is not None]) == \
+        len([r for r in recs if r["op"] not in ("alloc", "free", "mark", "result")])
