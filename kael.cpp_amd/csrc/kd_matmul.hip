@@ -645,6 +645,146 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* _
         }
 }
 
+// ---- 64x64 tiles (f32, grids too small for 128x128 tiles) ---------------------------------------
+
+constexpr int kT64 = 64;
+constexpr int kT64K = 32;           // K per LDS stage
+constexpr int kT64Ald = kT64K + 4;  // A tile [m][k], row stride 36 floats
+constexpr int kT64Bld = kT64 + 4;   // B tile [k][n], row stride 68 floats
+
+// Whole 64x64 output tiles for products whose 128x128 grid would not give every CU a workgroup:
+// attention-sized batched products (128 x 128 x 64 per head), x . W^T with N = 256 over a folded
+// batch, split-K weight gradients. Four waves, each one 32x32 v_mfma_f32_32x32x2f32 accumulator of
+// the 2x2 wave grid; K advances 32 at a time through double-buffered LDS. Waves 0-1 load the A
+// tile and waves 2-3 the B tile, four 16-byte loads per thread, coalesced along each operand's
+// contiguous dim; a transposed operand (A^T: M contiguous, B^T: K contiguous) is written
+// transposed into the [m][k] / [k][n] LDS tile, A^T's 16-byte column groups XOR-swizzled by
+// (row / 4) % 8 so that those writes do not collide. Each output element accumulates K in the same
+// (k, k + 4) MFMA pairs and order as the 128x128 kernels, so without split K the results are
+// theirs bit for bit. Batches (or K splits: their offsets as batch strides) take blockIdx.y.
+template <bool AT, bool BT>
+__global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                                float* __restrict__ out, int M, int N, int K, int lda,
+                                                                int ldb, int ldo, int64_t batch_a, int64_t batch_b,
+                                                                int64_t batch_o) {
+    __shared__ float As[2][kT64 * kT64Ald];
+    __shared__ float Bs[2][kT64K * kT64Bld];
+    const int tiles_m = M / kT64;
+    const int tiles_n = N / kT64;
+    int64_t tm64, tn64;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm64, tn64);
+    const int m0 = static_cast<int>(tm64) * kT64;
+    const int n0 = static_cast<int>(tn64) * kT64;
+    a += blockIdx.y * batch_a;
+    b += blockIdx.y * batch_b;
+    out += blockIdx.y * batch_o;
+
+    const int t = threadIdx.x;
+    const int lane = t % 64;
+    const int wave = t / 64;
+    const int wm = wave / 2;
+    const int wn = wave % 2;
+    const int li = lane % 32;
+    const int lh = lane / 32;
+
+    v16f acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    // Column (in floats) of 16-byte group `c4` of A tile row `row` after the swizzle.
+    const auto aswz = [](int row, int c4) { return AT ? c4 ^ (4 * ((row / 4) % 8)) : c4; };
+    const bool loads_a = t < kThreads / 2;
+    const int u = loads_a ? t : t - kThreads / 2;
+    // Per-thread source offset (element) of load j = 0..3 at K step 0, and the step per load j.
+    int g_off, g_row;
+    if (loads_a) {
+        if (AT) {  // A^T rows k = 4*(u/16) + j, columns m0 + 4*(u%16) .. +3
+            g_off = 4 * (u / 16) * lda + m0 + 4 * (u % 16);
+            g_row = lda;
+        } else {   // A rows m0 + u/8 + 16*j, columns k = 4*(u%8) .. +3
+            g_off = (m0 + u / 8) * lda + 4 * (u % 8);
+            g_row = 16 * lda;
+        }
+    } else {
+        if (BT) {  // B^T rows n0 + 4*(u/8) + j, columns k = 4*(u%8) .. +3
+            g_off = (n0 + 4 * (u / 8)) * ldb + 4 * (u % 8);
+            g_row = ldb;
+        } else {   // B rows k = 4*(u/16) + j, columns n0 + 4*(u%16) .. +3
+            g_off = 4 * (u / 16) * ldb + n0 + 4 * (u % 16);
+            g_row = ldb;
+        }
+    }
+    const int g_step = loads_a ? (AT ? kT64K * lda : kT64K) : (BT ? kT64K : kT64K * ldb);
+    const float* src = loads_a ? a : b;
+    f4 r[4];
+    const auto fetch = [&](int ks) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const f4*>(src + g_off + ks * g_step + j * g_row);
+    };
+    const auto stash = [&](int buf) {
+        if (loads_a) {
+            if (AT) {
+                // r[j][e] = A[m0 + 4*(u%16) + e][4*(u/16) + j]
+                const int c4 = 4 * (u / 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = 4 * (u % 16) + e;
+                    *reinterpret_cast<f4*>(&As[buf][row * kT64Ald + aswz(row, c4)]) = f4{r[0][e], r[1][e], r[2][e], r[3][e]};
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(&As[buf][(u / 8 + 16 * j) * kT64Ald + 4 * (u % 8)]) = r[j];
+            }
+        } else {
+            if (BT) {
+                // r[j][e] = B[4*(u%8) + e][n0 + 4*(u/8) + j]
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    *reinterpret_cast<f4*>(&Bs[buf][(4 * (u % 8) + e) * kT64Bld + 4 * (u / 8)]) = f4{r[0][e], r[1][e], r[2][e], r[3][e]};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(&Bs[buf][(4 * (u / 16) + j) * kT64Bld + 4 * (u % 16)]) = r[j];
+            }
+        }
+    };
+    // This lane's A tile reads (row wm*32 + li, 16-byte groups kg + 4*lh) as LDS offsets.
+    const int arow = wm * 32 + li;
+    int a_rd[kT64K / 8];
+#pragma unroll
+    for (int h = 0; h < kT64K / 8; ++h) a_rd[h] = arow * kT64Ald + aswz(arow, 8 * h + 4 * lh);
+    fetch(0);
+    stash(0);
+    __syncthreads();
+
+    const int ksteps = K / kT64K;
+    for (int ks = 0; ks < ksteps; ++ks) {
+        const int cur = ks & 1;
+        const bool more = ks + 1 < ksteps;
+        if (more) fetch(ks + 1);
+        const float* as = As[cur];
+        const float* bs = Bs[cur];
+#pragma unroll
+        for (int kg = 0; kg < kT64K; kg += 8) {
+            const f4 af = *reinterpret_cast<const f4*>(as + a_rd[kg / 8]);
+            float bf[4];
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) bf[s4] = bs[(kg + 4 * lh + s4) * kT64Bld + wn * 32 + li];
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s4], bf[s4], acc, 0, 0, 0);
+        }
+        if (more) stash(cur ^ 1);
+        __syncthreads();
+    }
+
+    const int col = n0 + wn * 32 + li;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+        const int row = m0 + wm * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
+        out[row * ldo + col] = acc[rr];
+    }
+}
+
 // ---- small family (f32, few output tiles) -----------------------------------------------------
 
 constexpr int kSmallTile = 32;
@@ -948,10 +1088,83 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(const T* __restrict__ a
 
 bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
 
+// Status of the launch just issued (KD_LAUNCH_CHECK for callers that report through a pointer).
+int launch_status() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? KD_OK : ::kd::hip_fail(e, "kernel launch", __FILE__, __LINE__);
+}
+
+// 64x64 tiles (mfma_f32_t64_kernel) for whole-tile products (M, N multiples of 64, K of 32,
+// 32-bit offsets) whose 128x128 grid, batch included, would not give every CU a workgroup, or whose
+// M or N is not a multiple of 128 (the alternative is the bounds-checked general kernel). Measured
+// on C4's products: the attention batches (128 x 128 x 128 x 64) 6.5 us against 16.2 on the general
+// kernel, x . W^T over the folded batch with N = 256 22-29 us against 27-31 with split K. When
+// even the 64x64 grid fills at most half the CUs and K >= 512, K is split over the kernel's batch
+// slot into a workspace that split_sum_kernel adds in split order. Returns false when the product
+// does not take this path.
+template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, float* out, const MatmulArgs& p, int* rc) {
+    constexpr int64_t kMax = int64_t{1} << 31;
+    const int64_t lda = AT ? p.sa.c : p.sa.r;
+    const int64_t ldb = BT ? p.sb.c : p.sb.r;
+    const int64_t a_extent = AT ? p.K * lda + p.M : p.M * lda + p.K;
+    const int64_t b_extent = BT ? p.N * ldb + p.K : p.K * ldb + p.N;
+    if (p.M % kT64 != 0 || p.N % kT64 != 0 || p.K % kT64K != 0 || p.K == 0 || p.so.c != 1 || a_extent >= kMax ||
+        b_extent >= kMax || p.M * p.so.r + p.N >= kMax)
+        return false;
+    const int cus = compute_units();
+    const bool whole128 = p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0;
+    // the batch folds into M when the batches share B and lie back to back in A and the output
+    const bool fold = !AT && p.sb.b == 0 && p.sa.b == p.M * lda && p.so.b == p.M * p.so.r;
+    const int64_t rows = fold ? p.M * p.batches : p.M;
+    const int64_t batches = fold ? 1 : p.batches;
+    if (fold && (rows * lda >= kMax || rows * p.so.r >= kMax)) return false;
+    const int64_t tiles128 = (rows / kBM) * (p.N / kBN);
+    if (whole128 && tiles128 * batches >= cus) return false;
+    // One product with 5 or more 128x128 tiles splits K on them (C4's 256 x 4096 x 768 weight
+    // gradient: 28.7 us against 32.1 on 64x64 tiles split 4 ways); with at most 4 the 64x64 grid
+    // wins (256 x 4096 x 256: 13 us against 21).
+    if (whole128 && p.batches == 1 && tiles128 > 4) return false;
+    const int64_t tiles = (rows / kT64) * (p.N / kT64);
+    if (batches > 65535) return false;
+    if (batches == 1 && tiles * 2 <= cus && p.K >= 512) {
+        int64_t splits = std::min<int64_t>(p.K / 256, (cus + tiles - 1) / tiles);
+        while (splits > 1 && p.K % (splits * kT64K) != 0) --splits;
+        const int64_t per = rows * p.N;
+        if (splits > 1 && splits * per < kMax) {
+            Workspace ws;  // held until split_sum_kernel is enqueued
+            if ((*rc = workspace(ws, static_cast<size_t>(splits * per) * sizeof(float)))) return true;
+            const int64_t kc = p.K / splits;
+            hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
+                               dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr), static_cast<int>(rows),
+                               static_cast<int>(p.N), static_cast<int>(kc), static_cast<int>(lda), static_cast<int>(ldb),
+                               static_cast<int>(p.N), AT ? kc * lda : kc, BT ? kc : kc * ldb, per);
+            if ((*rc = launch_status())) return true;
+            MatmulArgs flat = p;
+            flat.batches = 1;
+            flat.M = rows;
+            const int64_t blocks = std::min<int64_t>((per + kThreads - 1) / kThreads, int64_t{cus} * 16);
+            hipLaunchKernelGGL(split_sum_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream(),
+                               static_cast<const float*>(ws.ptr), out, flat, splits);
+            *rc = launch_status();
+            return true;
+        }
+    }
+    hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(batches)),
+                       dim3(kThreads), 0, stream(), a, b, out, static_cast<int>(rows), static_cast<int>(p.N),
+                       static_cast<int>(p.K), static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
+                       p.sa.b, p.sb.b, p.so.b);
+    *rc = launch_status();
+    return true;
+}
+
 template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, float* out, const MatmulArgs& p) {
     const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN);
     if (p.batches > 65535) return fail(KD_E_INVALID, "kd_matmul: too many batches");
     const dim3 grid(static_cast<uint32_t>(tiles), static_cast<uint32_t>(p.batches));
+    if constexpr (AMode != kGeneric && BMode != kGeneric) {
+        int rc = KD_OK;
+        if (launch_t64<AMode == kColVec, BMode == kColVec>(a, b, out, p, &rc)) return rc;
+    }
     if constexpr (AMode == kRowVec && BMode == kRowVec) {
         constexpr int64_t kMax = int64_t{1} << 31;
         const bool small = p.M * p.sa.r < kMax && p.K * p.sb.r < kMax && p.M * p.so.r < kMax && p.so.c == 1;

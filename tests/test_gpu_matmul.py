@@ -193,6 +193,77 @@ def test_linear_forward_shapes_of_c4(kdb, batches, k, b_t):
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
 
 
+def test_64_tiles_equal_128_tiles(kdb):
+    """3 batches of 1024 x 256 x 1024 have 192 128x128 tiles, fewer than the 256 CUs, and run on
+    64x64 tiles; 4 batches have 256 and stay on 128x128 tiles. Each batch item's product is the same
+    computation either way: the same (k, k + 4) MFMA pairs in the same K order, so the first three
+    items must agree bit for bit."""
+    m, k, n = 1024, 256, 1024
+    rng = np.random.default_rng(51)
+    a = rng.uniform(-1, 1, (4, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (4, k, n)).astype(np.float32)
+    outs = []
+    for batches in (3, 4):
+        da, db = kdb.to_device(a[:batches]), kdb.to_device(b[:batches])
+        dc = kdb.empty((batches, m, n), np.float32)
+        kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n))
+        outs.append(dc.numpy())
+    np.testing.assert_array_equal(outs[0], outs[1][:3])
+    close(outs[0], np.matmul(a[:3].astype(np.float64), b[:3].astype(np.float64)))
+
+
+ATTENTION = [(128, 128, 128, 64), (128, 128, 64, 128), (128, 64, 128, 128), (8, 64, 32, 64)]
+
+
+@pytest.mark.parametrize("batches,m,k,n", ATTENTION, ids=[f"{b}x{m}x{k}x{n}" for b, m, k, n in ATTENTION])
+def test_attention_shaped_batches(kdb, batches, m, k, n):
+    """The batched products of C4's attention (32 x 4 heads: Q.K^T with K = head_dim 64, P.V with
+    N = 64, and their gradients, reference src/nn/transformer.cpp:103-139) on 64x64 tiles, and the
+    smallest whole case (64 x 32 x 64)."""
+    rng = np.random.default_rng(52 + m + k + n)
+    a = rng.uniform(-1, 1, (batches, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (batches, k, n)).astype(np.float32)
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((batches, m, n), np.float32)
+    kdb.call("matmul", kd.F32, da.ptr, db.ptr, dc.ptr, kd.MatmulSizes(batches, m, k, n))
+    close(dc.numpy(), np.matmul(a.astype(np.float64), b.astype(np.float64)))
+
+
+@pytest.mark.parametrize("a_t,b_t", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["rows", "aT", "bT", "both"])
+def test_64_tiles_with_transposed_operands(kdb, a_t, b_t):
+    """M and N multiples of 64 but not of 128 (192 x 96 x 320, 4 batches), every operand layout:
+    the 64x64 kernel's loaders (coalesced along each stored operand's contiguous dim, A^T written
+    transposed into a swizzled tile) against the float64 product; all four layouts equal bit for
+    bit (the same tiles, MFMA pairs and order)."""
+    batches, m, k, n = 4, 192, 96, 320
+    rng = np.random.default_rng(53)
+    a = rng.uniform(-1, 1, (batches, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (batches, k, n)).astype(np.float32)
+    a_store = np.ascontiguousarray(np.transpose(a, (0, 2, 1))) if a_t else a
+    b_store = np.ascontiguousarray(np.transpose(b, (0, 2, 1))) if b_t else b
+    sa = (k * m, 1, m) if a_t else (m * k, k, 1)
+    sb = (k * n, 1, k) if b_t else (k * n, n, 1)
+    got = _strided_product(kdb, a_store, b_store, batches, m, k, n, sa, sb)
+    plain = _strided_product(kdb, a, b, batches, m, k, n, (m * k, k, 1), (k * n, n, 1))
+    np.testing.assert_array_equal(got, plain)
+    close(got, np.matmul(a.astype(np.float64), b.astype(np.float64)))
+
+
+def test_split_k_on_64_tiles(kdb):
+    """C4's narrowest weight gradient X^T . g (M = N = 256, K = 4096: 16 tiles of 64x64) splits K
+    16 ways over the device and adds the partial products in split order: within 1e-4 of the
+    largest |element| of the float64 product, and the same bits on a second run."""
+    m, k, n = 256, 4096, 256
+    rng = np.random.default_rng(54)
+    x = rng.uniform(-1, 1, (k, m)).astype(np.float32)
+    g = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    got = _strided_product(kdb, x, g, 1, m, k, n, (0, 1, m), (0, n, 1))[0]
+    again = _strided_product(kdb, x, g, 1, m, k, n, (0, 1, m), (0, n, 1))[0]
+    np.testing.assert_array_equal(got, again)
+    want = np.matmul(x.T.astype(np.float64), g.astype(np.float64))
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+
+
 def test_headline_4096_cubed(kdb, refdev, oracle):
     """The benchmark's headline product (row-major MFMA kernel, whole tiles) at its full size,
     inputs as bench.py draws them. At K = 4096 an element's f32 rounding error scales with its
