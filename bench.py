@@ -355,8 +355,14 @@ def bench_replay(backend, name, steps):
         per_call.append((r, ms.value))
         lib.kd_event_destroy(e0)
         lib.kd_event_destroy(e1)
-    mm = [(r, ms) for r, ms in per_call if r["op"] in ("matmul", "matmul_strided")]
+    mm = [(r, ms) for r, ms in per_call if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads")]
     mm_ms = sum(ms for _, ms in mm)
+    # row kernels: algorithmic bytes = the row arrays each one reads and writes once
+    arrays = {"softmax_rows": 2, "standardize_rows": 2, "softmax_rows_backward": 3, "standardize_rows_backward": 4,
+              "cross_entropy_rows": 1, "cross_entropy_grad": 2}
+    rows = [(r, ms) for r, ms in per_call if r["op"] in arrays]
+    row_bytes = sum(arrays[r["op"]] * r["rows"] * r["cols"] * (4 if r["dtype"] == 0 else 8) for r, _ in rows)
+    row_ms = sum(ms for _, ms in rows)
     flops = replay.matmul_flops(last)
     counts = {}
     for r in last:
@@ -366,6 +372,8 @@ def bench_replay(backend, name, steps):
             "matmul": {"count": len(mm), "ms": mm_ms, "gflop": flops / 1e9,
                        "tflops": flops / (mm_ms * 1e-3) / 1e12 if mm_ms else None,
                        "frac_peak": flops / (mm_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if mm_ms else None},
+            "row_kernels": {"count": len(rows), "ms": row_ms, "gbytes": row_bytes / 1e9,
+                            "tb_s": row_bytes / (row_ms * 1e-3) / 1e12 if row_ms else None},
             "replay_losses": losses, "kael_losses": replay.traced_losses(recs),
             "data": "C3: kael's recorded inputs and initial parameters; C4: recorded token ids and targets, "
                     "parameters zero"}

@@ -194,6 +194,17 @@ int kd_elementwise(int op, int out_dtype, int in_dtype, const kd_element_layout*
 int kd_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
               int64_t chunk_size, int64_t output_count);
 
+/* Column reductions: results[j] = op over i < outer of data[i * inner + j] (j < inner), i.e. a
+ * contiguous tensor reduced over its leading dims, with kd_reduce's ops, accumulators and
+ * output dtypes. It replaces, for that case, kael's device reduction plan (reference
+ * src/ops/reduce.cpp:118-153 plan_reduction + :309-314 device_reduce), which first copies the
+ * tensor with the reduced dims moved last and then calls kd_reduce with chunk = outer and
+ * rows = inner: the result is the one that copy and kd_reduce give (max / min and integer sums
+ * bit for bit; floating sums accumulate in double in a different order). Max/Min of an empty
+ * column is an error. */
+int kd_reduce_columns(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                      int64_t outer, int64_t inner);
+
 /* kd_reduce without any allocation: no reference counterpart. For callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same arguments, kernels and results as kd_reduce (bit for bit); the segment
@@ -237,6 +248,20 @@ typedef struct kd_matmul_strides {
 } kd_matmul_strides;
 int kd_matmul_strided(int dtype, const void* a, const void* b, void* out,
                       const kd_matmul_sizes* sizes, const kd_matmul_strides* strides);
+
+/* kd_matmul_strided over a two-level batch: batch index i = o * heads + h (sizes->batches a
+ * multiple of heads) addresses each operand at o * strides->X[0] + h * heads->X elements. This is
+ * how the per-head views of attention (reference src/nn/transformer.cpp:115-136: the [batch,
+ * head, token, dim] transposes of the fused qkv projection, of keys.mT() and of the output
+ * gradient) are read in place: their batch dims collapse to no single stride, so kael's
+ * matmul copies them (src/ops/linalg.cpp:56-76) before the product. heads = 1 is
+ * kd_matmul_strided. */
+typedef struct kd_matmul_heads {
+    int64_t heads;
+    int64_t a, b, out;
+} kd_matmul_heads;
+int kd_matmul_strided_heads(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                            const kd_matmul_strides* strides, const kd_matmul_heads* heads);
 
 /* reference device_kernels.h:113-114 `gather(DType, std::byte* out, const std::byte* data,
  * const int64* indices, const IndexLayout&)`; indices must already be range-checked
@@ -310,6 +335,25 @@ int kd_standardize_rows_backward(int dtype, void* out, const void* x, const void
 int kd_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
                  double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
                  int decoupled, int64_t step);
+
+/* One parameter tensor of kd_adam_step_many: contiguous param, grad and moments of `count`
+ * elements; `step` >= 1 is the tensor's own step count after the increment. */
+typedef struct kd_adam_tensor {
+    void* param;
+    const void* grad;
+    void* first;
+    void* second;
+    int64_t count;
+    int64_t step;
+} kd_adam_tensor;
+
+/* kd_adam_step over `n` tensors, the same bits as n kd_adam_step calls in table order, in one
+ * launch per 32 tensors: the loop of reference src/optim/optimizer.cpp:93-120 (AdamBase::update)
+ * over every parameter with a gradient, 52 launches per step for the char-GPT config. The table
+ * is read on the host during the call. Tensors whose memory overlaps memory another of them
+ * writes (param, first or second) are rejected with KD_E_INVALID before anything runs. */
+int kd_adam_step_many(int dtype, const kd_adam_tensor* tensors, int64_t n, double learning_rate, double beta1,
+                      double beta2, double epsilon, double weight_decay, int decoupled);
 
 /* One SGD step without momentum: p -= (g (+ p * weight_decay if > 0)) * learning_rate, as
  * reference src/optim/optimizer.cpp:60-80 computes it. dtype f32 or f64. */

@@ -33,10 +33,53 @@ struct Strides3 {
     int64_t b, r, c;
 };
 
+// Batches address the operands on one level (batch b at b * sa.b) or, with heads > 1, on two:
+// b = o * heads + h at o * sa.b + h * ha (attention's [batch, head] views of a [batch, token,
+// head, dim] tensor, which no single batch stride describes).
 struct MatmulArgs {
     int64_t batches, M, K, N;
     Strides3 sa, sb, so;
+    int64_t heads = 1;
+    int64_t ha = 0, hb = 0, ho = 0;
 };
+
+// Element offset of batch `batch` in an operand with outer / head strides `outer` / `inner`.
+__host__ __device__ __forceinline__ int64_t batch_offset(const MatmulArgs& p, int64_t batch, int64_t outer,
+                                                         int64_t inner) {
+    if (p.heads == 1) return batch * outer;
+    const int64_t o = static_cast<uint32_t>(batch) / static_cast<uint32_t>(p.heads);
+    return o * outer + (batch - o * p.heads) * inner;
+}
+
+// Batch addressing of the kernels with 32-bit tile offsets: blockIdx.y = o * heads + h starts
+// o * a + h * ha elements into A (likewise B and the output). heads = 1 is a plain batch stride,
+// also how split K passes each split's offsets.
+struct BatchStrides {
+    int64_t a, b, o;
+    int64_t ha, hb, ho;
+    uint32_t heads;
+};
+
+BatchStrides batch_strides(int64_t a, int64_t b, int64_t o) { return {a, b, o, 0, 0, 0, 1u}; }
+BatchStrides batch_strides(const MatmulArgs& p) {
+    return {p.sa.b, p.sb.b, p.so.b, p.ha, p.hb, p.ho, static_cast<uint32_t>(p.heads)};
+}
+
+// Offsets of this workgroup's batch (blockIdx.y) in A, B and the output.
+__device__ __forceinline__ void batch_offsets(const BatchStrides& s, int64_t& oa, int64_t& ob, int64_t& oo) {
+    const uint32_t y = blockIdx.y;
+    if (s.heads == 1) {
+        oa = y * s.a;
+        ob = y * s.b;
+        oo = y * s.o;
+        return;
+    }
+    const uint32_t o = y / s.heads;
+    const uint32_t h = y - o * s.heads;
+    oa = o * s.a + h * s.ha;
+    ob = o * s.b + h * s.hb;
+    oo = o * s.o + h * s.ho;
+}
 
 constexpr int kThreads = 256;
 
@@ -257,9 +300,9 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_kernel(const float* __restr
     const int64_t batch = blockIdx.y;
     const int64_t m0 = tm * kBM;
     const int64_t n0 = tn * kBN;
-    a += batch * p.sa.b;
-    b += batch * p.sb.b;
-    out += batch * p.so.b;
+    a += batch_offset(p, batch, p.sa.b, p.ha);
+    b += batch_offset(p, batch, p.sb.b, p.hb);
+    out += batch_offset(p, batch, p.so.b, p.ho);
 
     const int lane = threadIdx.x % 64;
     const int wave = threadIdx.x / 64;
@@ -501,8 +544,7 @@ template <bool AT, bool BT>
 __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* __restrict__ a,
                                                                   const float* __restrict__ b,
                                                                   float* __restrict__ out, int M, int N, int K,
-                                                                  int lda, int ldb, int ldo, int64_t batch_a,
-                                                                  int64_t batch_b, int64_t batch_o) {
+                                                                  int lda, int ldb, int ldo, BatchStrides bs) {
     __shared__ float As[2][kAsize];
     __shared__ float Bs[2][kBsize];
     const int tiles_m = M / kBM;
@@ -511,9 +553,13 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* _
     tile_of(blockIdx.x, tiles_m, tiles_n, tm64, tn64);
     const int m0 = static_cast<int>(tm64) * kBM;
     const int n0 = static_cast<int>(tn64) * kBN;
-    a += blockIdx.y * batch_a;
-    b += blockIdx.y * batch_b;
-    out += blockIdx.y * batch_o;
+    {
+        int64_t oa, ob, oo;
+        batch_offsets(bs, oa, ob, oo);
+        a += oa;
+        b += ob;
+        out += oo;
+    }
 
     const int t = threadIdx.x;
     const int lane = t % 64;
@@ -665,8 +711,7 @@ constexpr int kT64Bld = kT64 + 4;   // B tile [k][n], row stride 68 floats
 template <bool AT, bool BT>
 __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                                 float* __restrict__ out, int M, int N, int K, int lda,
-                                                                int ldb, int ldo, int64_t batch_a, int64_t batch_b,
-                                                                int64_t batch_o) {
+                                                                int ldb, int ldo, BatchStrides bs) {
     __shared__ float As[2][kT64 * kT64Ald];
     __shared__ float Bs[2][kT64K * kT64Bld];
     const int tiles_m = M / kT64;
@@ -675,9 +720,13 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
     tile_of(blockIdx.x, tiles_m, tiles_n, tm64, tn64);
     const int m0 = static_cast<int>(tm64) * kT64;
     const int n0 = static_cast<int>(tn64) * kT64;
-    a += blockIdx.y * batch_a;
-    b += blockIdx.y * batch_b;
-    out += blockIdx.y * batch_o;
+    {
+        int64_t oa, ob, oo;
+        batch_offsets(bs, oa, ob, oo);
+        a += oa;
+        b += ob;
+        out += oo;
+    }
 
     const int t = threadIdx.x;
     const int lane = t % 64;
@@ -821,8 +870,8 @@ __global__ __launch_bounds__(kSmallWaves * 64) void small_kernel(const float* __
     const int64_t n = n0 + li;
     const bool mok = m < p.M;
     const bool nok = n < p.N;
-    const float* arow = a + batch * p.sa.b + (mok ? m : 0) * p.sa.r;
-    const float* bcol = b + batch * p.sb.b + (nok ? n : 0) * p.sb.c;
+    const float* arow = a + batch_offset(p, batch, p.sa.b, p.ha) + (mok ? m : 0) * p.sa.r;
+    const float* bcol = b + batch_offset(p, batch, p.sb.b, p.hb) + (nok ? n : 0) * p.sb.c;
     // Group g's operands, zero past the edges of A, B and K.
     const auto load = [&](int g, f4& av, f4& bv) {
         av = f4{0.f, 0.f, 0.f, 0.f};
@@ -864,7 +913,7 @@ __global__ __launch_bounds__(kSmallWaves * 64) void small_kernel(const float* __
         const int l = e % 64;
         const int64_t row = m0 + 8 * (r / 4) + 4 * (l / 32) + (r % 4);
         const int64_t col = n0 + l % 32;
-        if (row < p.M && col < p.N) out[batch * p.so.b + row * p.so.r + col * p.so.c] = v;
+        if (row < p.M && col < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + row * p.so.r + col * p.so.c] = v;
     }
 }
 
@@ -887,8 +936,8 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const float* __restric
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kSkinnyCols + lane * 4;
     const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * k_chunk;
     const int64_t k_end = std::min<int64_t>(p.K, k_begin + k_chunk);
-    a += batch * p.sa.b;
-    b += batch * p.sb.b;
+    a += batch_offset(p, batch, p.sa.b, p.ha);
+    b += batch_offset(p, batch, p.sb.b, p.hb);
 
     float acc[MT][4];
 #pragma unroll
@@ -931,7 +980,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const float* __restric
         if (partial != nullptr) {
             partial[((batch * gridDim.y + blockIdx.y) * p.M + m) * p.N + n] = v;
         } else {
-            out[batch * p.so.b + m * p.so.r + n * p.so.c] = v;
+            out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = v;
         }
     }
 }
@@ -960,7 +1009,7 @@ __global__ __launch_bounds__(kThreads) void split_sum_kernel(const float* __rest
         }
         const int64_t m = mn / p.N;
         const int64_t n = mn % p.N;
-        out[batch * p.so.b + m * p.so.r + n * p.so.c] = v;
+        out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = v;
     }
 }
 
@@ -977,8 +1026,8 @@ __global__ __launch_bounds__(kThreads) void rowdot_kernel(const float* __restric
     if (row_id >= p.batches * p.M) return;
     const int64_t batch = row_id / p.M;
     const int64_t m = row_id % p.M;
-    const float* arow = a + batch * p.sa.b + m * p.sa.r;
-    const float* bb = b + batch * p.sb.b;
+    const float* arow = a + batch_offset(p, batch, p.sa.b, p.ha) + m * p.sa.r;
+    const float* bb = b + batch_offset(p, batch, p.sb.b, p.hb);
     float acc[kRowdotMaxN] = {0.f, 0.f, 0.f, 0.f};
     if (AVec) {
         const int64_t vecs = p.K / 4;
@@ -1015,7 +1064,7 @@ __global__ __launch_bounds__(kThreads) void rowdot_kernel(const float* __restric
     if (lane == 0) {
 #pragma unroll
         for (int n = 0; n < kRowdotMaxN; ++n)
-            if (n < p.N) out[batch * p.so.b + m * p.so.r + n * p.so.c] = acc[n];
+            if (n < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = acc[n];
     }
 }
 
@@ -1037,8 +1086,8 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(const T* __restrict__ a
     const int64_t batch = blockIdx.z;
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTT;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTT;
-    a += batch * p.sa.b;
-    b += batch * p.sb.b;
+    a += batch_offset(p, batch, p.sa.b, p.ha);
+    b += batch_offset(p, batch, p.sb.b, p.hb);
     const int tr = threadIdx.x / 16;  // 0..15 -> rows tr*4 .. +3
     const int tc = threadIdx.x % 16;  // cols tc + 16*j
     T acc[4][4];
@@ -1079,7 +1128,7 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(const T* __restrict__ a
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t n = n0 + tc + 16 * j;
-            if (n < p.N) out[batch * p.so.b + m * p.so.r + n * p.so.c] = acc[i][j];
+            if (n < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = acc[i][j];
         }
     }
 }
@@ -1114,7 +1163,7 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
     const int cus = compute_units();
     const bool whole128 = p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0;
     // the batch folds into M when the batches share B and lie back to back in A and the output
-    const bool fold = !AT && p.sb.b == 0 && p.sa.b == p.M * lda && p.so.b == p.M * p.so.r;
+    const bool fold = !AT && p.heads == 1 && p.sb.b == 0 && p.sa.b == p.M * lda && p.so.b == p.M * p.so.r;
     const int64_t rows = fold ? p.M * p.batches : p.M;
     const int64_t batches = fold ? 1 : p.batches;
     if (fold && (rows * lda >= kMax || rows * p.so.r >= kMax)) return false;
@@ -1137,7 +1186,7 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
             hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
                                dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr), static_cast<int>(rows),
                                static_cast<int>(p.N), static_cast<int>(kc), static_cast<int>(lda), static_cast<int>(ldb),
-                               static_cast<int>(p.N), AT ? kc * lda : kc, BT ? kc : kc * ldb, per);
+                               static_cast<int>(p.N), batch_strides(AT ? kc * lda : kc, BT ? kc : kc * ldb, per));
             if ((*rc = launch_status())) return true;
             MatmulArgs flat = p;
             flat.batches = 1;
@@ -1152,7 +1201,7 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
     hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(batches)),
                        dim3(kThreads), 0, stream(), a, b, out, static_cast<int>(rows), static_cast<int>(p.N),
                        static_cast<int>(p.K), static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
-                       p.sa.b, p.sb.b, p.so.b);
+                       batch_strides(p));
     *rc = launch_status();
     return true;
 }
@@ -1173,7 +1222,8 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             // workgroup per CU is busy, partial products into the workspace, summed in split order.
             const int cus = compute_units();
             int64_t splits = 1;
-            if (tiles * p.batches * 2 <= cus && p.K >= 256 && p.M * p.N * p.batches * (cus / tiles) < kMax) {
+            if (p.heads == 1 && tiles * p.batches * 2 <= cus && p.K >= 256 &&
+                p.M * p.N * p.batches * (cus / tiles) < kMax) {
                 splits = std::min<int64_t>(p.K / 64, (cus + tiles * p.batches - 1) / (tiles * p.batches));
                 while (splits > 1 && p.K % (splits * kBK) != 0) --splits;
             }
@@ -1203,8 +1253,8 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             // bit-identical results. The bounds checked above cover its 32-bit offsets.
             hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false>), grid, dim3(kThreads), 0, stream(), a, b, out,
                                static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                               static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r), p.sa.b,
-                               p.sb.b, p.so.b);
+                               static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r),
+                               batch_strides(p));
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
@@ -1229,7 +1279,7 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             const int cus = compute_units();
             const int64_t rows = p.M * p.batches;
             const int64_t flat_tiles = (rows / kBM) * (p.N / kBN);
-            const bool fold = !at && p.sb.b == 0 && p.sa.b == p.M * lda && p.so.b == p.M * p.so.r;
+            const bool fold = !at && p.heads == 1 && p.sb.b == 0 && p.sa.b == p.M * lda && p.so.b == p.M * p.so.r;
             {
                 if ((p.batches == 1 || fold) && flat_tiles * 2 <= cus && p.K >= 256 &&
                     (at || rows * lda < kMax) && rows * p.so.r < kMax) {
@@ -1245,7 +1295,7 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                                            dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr),
                                            static_cast<int>(rows), static_cast<int>(p.N), static_cast<int>(kc),
                                            static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.N),
-                                           at ? kc * lda : kc, bt ? kc : kc * ldb, per);
+                                           batch_strides(at ? kc * lda : kc, bt ? kc : kc * ldb, per));
                         KD_LAUNCH_CHECK();
                         MatmulArgs flat = p;
                         flat.batches = 1;
@@ -1260,8 +1310,8 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             }
             hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>), grid, dim3(kThreads), 0, stream(), a, b, out,
                                static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                               static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r), p.sa.b, p.sb.b,
-                               p.so.b);
+                               static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
+                               batch_strides(p));
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
@@ -1289,7 +1339,7 @@ template <int AMode> int launch_mfma_b(const float* a, const float* b, float* ou
 int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) {
     const int cus = compute_units();
     if (p.N <= kRowdotMaxN) {
-        const bool avec = p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && aligned16(a);
+        const bool avec = p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && p.ha % 4 == 0 && aligned16(a);
         const int64_t waves = p.batches * p.M;
         const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
         if (avec) hipLaunchKernelGGL((rowdot_kernel<true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
@@ -1298,7 +1348,7 @@ int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) 
         return KD_OK;
     }
     if (p.M <= kSkinnyMaxM) {
-        const bool bvec = p.sb.c == 1 && p.sb.r % 4 == 0 && p.sb.b % 4 == 0 && aligned16(b);
+        const bool bvec = p.sb.c == 1 && p.sb.r % 4 == 0 && p.sb.b % 4 == 0 && p.hb % 4 == 0 && aligned16(b);
         const int64_t col_blocks = (p.N + kSkinnyCols - 1) / kSkinnyCols;
         int64_t splits = 1;
         const int64_t want = 2 * int64_t{cus};
@@ -1347,7 +1397,7 @@ int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) 
         if (big * 2 <= cus && gm * gn * p.batches <= 2 * int64_t{cus} && p.K <= 2048 && fits32) {
             if (p.batches > 65535 || gm > 65535) return fail(KD_E_INVALID, "kd_matmul: grid too large");
             const dim3 grid(static_cast<uint32_t>(gn), static_cast<uint32_t>(gm), static_cast<uint32_t>(p.batches));
-            const bool avec = p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && aligned16(a);
+            const bool avec = p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && p.ha % 4 == 0 && aligned16(a);
             if (avec) hipLaunchKernelGGL(small_kernel<true>, grid, dim3(kSmallWaves * 64), 0, stream(), a, b, out, p);
             else hipLaunchKernelGGL(small_kernel<false>, grid, dim3(kSmallWaves * 64), 0, stream(), a, b, out, p);
             KD_LAUNCH_CHECK();
@@ -1355,10 +1405,10 @@ int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) 
         }
     }
     int amode = kGeneric, bmode = kGeneric;
-    if (p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && p.K % 4 == 0 && aligned16(a)) amode = kRowVec;
-    else if (p.sa.r == 1 && p.sa.c % 4 == 0 && p.sa.b % 4 == 0 && p.M % 4 == 0 && aligned16(a)) amode = kColVec;
-    if (p.sb.c == 1 && p.sb.r % 4 == 0 && p.sb.b % 4 == 0 && p.N % 4 == 0 && aligned16(b)) bmode = kRowVec;
-    else if (p.sb.r == 1 && p.sb.c % 4 == 0 && p.sb.b % 4 == 0 && p.K % 4 == 0 && aligned16(b)) bmode = kColVec;
+    if (p.sa.c == 1 && p.sa.r % 4 == 0 && p.sa.b % 4 == 0 && p.ha % 4 == 0 && p.K % 4 == 0 && aligned16(a)) amode = kRowVec;
+    else if (p.sa.r == 1 && p.sa.c % 4 == 0 && p.sa.b % 4 == 0 && p.ha % 4 == 0 && p.M % 4 == 0 && aligned16(a)) amode = kColVec;
+    if (p.sb.c == 1 && p.sb.r % 4 == 0 && p.sb.b % 4 == 0 && p.hb % 4 == 0 && p.N % 4 == 0 && aligned16(b)) bmode = kRowVec;
+    else if (p.sb.r == 1 && p.sb.c % 4 == 0 && p.sb.b % 4 == 0 && p.hb % 4 == 0 && p.K % 4 == 0 && aligned16(b)) bmode = kColVec;
     switch (amode) {
     case kRowVec: return launch_mfma_b<kRowVec>(a, b, out, p, bmode);
     case kColVec: return launch_mfma_b<kColVec>(a, b, out, p, bmode);
@@ -1384,7 +1434,7 @@ __global__ __launch_bounds__(kThreads) void zero_kernel(T* out, MatmulArgs p) {
         const int64_t batch = idx / (p.M * p.N);
         const int64_t m = (idx / p.N) % p.M;
         const int64_t n = idx % p.N;
-        out[batch * p.so.b + m * p.so.r + n * p.so.c] = T(0);
+        out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = T(0);
     }
 }
 
@@ -1442,5 +1492,30 @@ extern "C" int kd_matmul_strided(int dtype, const void* a, const void* b, void* 
     p.sa = {strides->a[0], strides->a[1], strides->a[2]};
     p.sb = {strides->b[0], strides->b[1], strides->b[2]};
     p.so = {strides->out[0], strides->out[1], strides->out[2]};
+    return dispatch(dtype, a, b, out, p);
+}
+
+extern "C" int kd_matmul_strided_heads(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                                       const kd_matmul_strides* strides, const kd_matmul_heads* heads) {
+    if (sizes == nullptr || strides == nullptr || heads == nullptr)
+        return fail(KD_E_INVALID, "kd_matmul_strided_heads: null argument");
+    if (heads->heads < 1) return fail(KD_E_INVALID, "kd_matmul_strided_heads: heads must be >= 1");
+    if (sizes->batches > 0 && sizes->batches % heads->heads != 0)
+        return fail(KD_E_INVALID, "kd_matmul_strided_heads: batches is not a multiple of heads");
+    if (sizes->batches > (int64_t{1} << 31)) return fail(KD_E_INVALID, "kd_matmul_strided_heads: too many batches");
+    MatmulArgs p;
+    p.batches = sizes->batches;
+    p.M = sizes->rows;
+    p.K = sizes->inner;
+    p.N = sizes->columns;
+    p.sa = {strides->a[0], strides->a[1], strides->a[2]};
+    p.sb = {strides->b[0], strides->b[1], strides->b[2]};
+    p.so = {strides->out[0], strides->out[1], strides->out[2]};
+    if (heads->heads > 1) {
+        p.heads = heads->heads;
+        p.ha = heads->a;
+        p.hb = heads->b;
+        p.ho = heads->out;
+    }
     return dispatch(dtype, a, b, out, p);
 }

@@ -343,6 +343,137 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(typename C::Out* result
     if (threadIdx.x == 0) results[r] = C::finish(acc);
 }
 
+// ---- column reductions ------------------------------------------------------------------------
+//
+// results[j] = op over i < outer of data[i * inner + j] for j < inner: a contiguous tensor reduced
+// over its leading dims, read in place (kael's plan_reduction moves the reduced dims last with a
+// transposed copy, src/ops/reduce.cpp:118-153). Workgroup (cb, s): the 64 columns [64 cb, 64 cb + 64),
+// one per lane (each row read coalesced), over the segment's rows [r0, r1); wave w scans the
+// contiguous rows [r0 + w q, r0 + w q + q) in increasing order, 16 loads in flight, and the four
+// wave partials combine in wave order, so every column is reduced in increasing row order in
+// contiguous runs (max / min keep the first NaN and the first extreme). One segment writes the
+// result; several write partial[s * inner + j], which column_combine_kernel combines in segment
+// order. Sums accumulate in double for f32 / f64, as kd_reduce's do.
+template <typename C, typename In>
+__global__ __launch_bounds__(kBlock) void column_kernel(typename C::Out* results, typename C::Acc* partial,
+                                                        const In* data, int64_t outer, int64_t inner,
+                                                        int64_t seg_rows, int64_t segments) {
+    using Acc = typename C::Acc;
+    constexpr int kWaves = kBlock / 64;
+    __shared__ Acc waves[kWaves][64];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int64_t s = blockIdx.y;
+    const int64_t r0 = s * seg_rows;
+    const int64_t r1 = std::min<int64_t>(outer, r0 + seg_rows);
+    const int64_t q = (r1 - r0 + kWaves - 1) / kWaves;
+    const int64_t w0 = std::min<int64_t>(r1, r0 + wave * q);
+    const int64_t w1 = std::min<int64_t>(r1, w0 + q);
+    Acc acc = C::identity();
+    if (j < inner) {
+        constexpr int kRows = 16;  // loads in flight per lane
+        const In* col = data + j;
+        for (int64_t i0 = w0; i0 < w1; i0 += kRows) {
+            In v[kRows];
+#pragma unroll
+            for (int u = 0; u < kRows; ++u)
+                if (i0 + u < w1) v[u] = col[(i0 + u) * inner];
+#pragma unroll
+            for (int u = 0; u < kRows; ++u)
+                if (i0 + u < w1) acc = C::combine(acc, C::load(v[u], i0 + u));
+        }
+    }
+    waves[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && j < inner) {
+        Acc v = waves[0][lane];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) v = C::combine(v, waves[w][lane]);
+        if (segments == 1) results[j] = C::finish(v);
+        else partial[s * inner + j] = v;
+    }
+}
+
+// Combines the segment partials of 64 columns per workgroup: wave w takes the contiguous segments
+// [w q, w q + q) with up to 16 loads in flight per lane (the partials were just written by other
+// XCDs, so each round of loads costs a trip past the L2), and the four wave results combine in
+// wave order: every column in segment order.
+template <typename C>
+__global__ __launch_bounds__(kBlock) void column_combine_kernel(typename C::Out* results, const typename C::Acc* partial,
+                                                                int64_t segments, int64_t inner) {
+    constexpr int kBatch = 16;
+    constexpr int kWaves = kBlock / 64;
+    using Acc = typename C::Acc;
+    __shared__ Acc waves[kWaves][64];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int64_t q = (segments + kWaves - 1) / kWaves;
+    const int64_t s_begin = std::min<int64_t>(segments, wave * q);
+    const int64_t s_end = std::min<int64_t>(segments, s_begin + q);
+    Acc v = C::identity();
+    if (j < inner) {
+        for (int64_t s0 = s_begin; s0 < s_end; s0 += kBatch) {
+            Acc x[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s0 + u < s_end) x[u] = partial[(s0 + u) * inner + j];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s0 + u < s_end) v = C::combine(v, x[u]);
+        }
+    }
+    waves[wave][lane] = v;
+    __syncthreads();
+    if (wave == 0 && j < inner) {
+        Acc r = waves[0][lane];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) r = C::combine(r, waves[w][lane]);
+        results[j] = C::finish(r);
+    }
+}
+
+template <typename C, typename In>
+int columns_with(void* results, const void* data_v, int64_t outer, int64_t inner) {
+    using Acc = typename C::Acc;
+    auto* out = static_cast<typename C::Out*>(results);
+    const In* data = static_cast<const In*>(data_v);
+    const int cus = compute_units();
+    const int64_t col_blocks = (inner + 63) / 64;
+    // about 4 workgroups per CU, segments of at least 64 rows
+    int64_t segments = std::max<int64_t>(1, (int64_t{cus} * 4 + col_blocks - 1) / col_blocks);
+    segments = std::min<int64_t>(segments, std::max<int64_t>(1, outer / 64));
+    const int64_t seg_rows = std::max<int64_t>(1, (outer + segments - 1) / segments);
+    segments = outer == 0 ? 1 : (outer + seg_rows - 1) / seg_rows;
+    if (col_blocks > int64_t{1} << 31 || segments > 65535) return fail(KD_E_INVALID, "kd_reduce_columns: too large");
+    const dim3 grid(static_cast<uint32_t>(col_blocks), static_cast<uint32_t>(segments));
+    if (segments == 1) {
+        hipLaunchKernelGGL((column_kernel<C, In>), grid, dim3(kBlock), 0, stream(), out, static_cast<Acc*>(nullptr), data,
+                           outer, inner, seg_rows, segments);
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    Workspace ws;  // held until column_combine_kernel is enqueued
+    if (int rc = workspace(ws, static_cast<size_t>(segments * inner) * sizeof(Acc))) return rc;
+    Acc* partial = static_cast<Acc*>(ws.ptr);
+    hipLaunchKernelGGL((column_kernel<C, In>), grid, dim3(kBlock), 0, stream(), out, partial, data, outer, inner, seg_rows,
+                       segments);
+    KD_LAUNCH_CHECK();
+    hipLaunchKernelGGL((column_combine_kernel<C>), dim3(static_cast<uint32_t>(col_blocks)), dim3(kBlock), 0, stream(), out,
+                       static_cast<const Acc*>(partial), segments, inner);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+template <int Op> int columns_dtype(int in, void* results, const void* data, int64_t outer, int64_t inner) {
+    switch (in) {
+    case KD_F32: return columns_with<Combiner<Op, float>, float>(results, data, outer, inner);
+    case KD_F64: return columns_with<Combiner<Op, double>, double>(results, data, outer, inner);
+    case KD_I64: return columns_with<Combiner<Op, int64_t>, int64_t>(results, data, outer, inner);
+    case KD_BOOL: return columns_with<Combiner<Op, uint8_t>, uint8_t>(results, data, outer, inner);
+    }
+    return fail(KD_E_INVALID, "kd_reduce_columns: unknown dtype");
+}
+
 // ---- cumsum ------------------------------------------------------------------------------------
 
 constexpr int kScanPer = 8;  // elements scanned in registers by one lane per tile
@@ -755,4 +886,23 @@ extern "C" int kd_cumsum(int in_dtype, void* out, const void* in, int64_t size, 
     case KD_BOOL: return cumsum_typed<uint8_t>(out, in, size, rows);
     }
     return fail(KD_E_INVALID, "kd_cumsum: unknown dtype");
+}
+
+extern "C" int kd_reduce_columns(int op, int out_dtype, int in_dtype, void* results, const void* data, int64_t outer,
+                                 int64_t inner) {
+    (void)out_dtype;  // implied by op and input dtype, as for kd_reduce
+    if (outer < 0 || inner < 0) return fail(KD_E_INVALID, "kd_reduce_columns: negative size");
+    if (dtype_size(in_dtype) == 0) return fail(KD_E_INVALID, "kd_reduce_columns: unknown dtype");
+    if (inner == 0) return KD_OK;
+    if (outer == 0 && (op == KD_REDUCE_MAX || op == KD_REDUCE_MIN))
+        return fail(KD_E_INVALID, "kd_reduce_columns: max/min of an empty chunk");
+    if (int rc = ensure_device()) return rc;
+    switch (op) {
+#define KD_COLUMNS_CASE(OP) \
+    case OP: return columns_dtype<OP>(in_dtype, results, data, outer, inner);
+        KD_COLUMNS_CASE(KD_REDUCE_SUM) KD_COLUMNS_CASE(KD_REDUCE_MAX) KD_COLUMNS_CASE(KD_REDUCE_MIN)
+        KD_COLUMNS_CASE(KD_REDUCE_PROD) KD_COLUMNS_CASE(KD_REDUCE_ALL) KD_COLUMNS_CASE(KD_REDUCE_ANY)
+#undef KD_COLUMNS_CASE
+    }
+    return fail(KD_E_INVALID, "kd_reduce_columns: unknown op");
 }

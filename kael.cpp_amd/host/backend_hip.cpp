@@ -165,12 +165,36 @@ void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::by
     check(kd_matmul_strided(static_cast<int>(dtype), a, b, out, &s, &st), "matmul_strided");
 }
 
+void matmul_strided_heads(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
+                          const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
+                          std::int64_t heads, const std::int64_t* head_strides) {
+    const kd_matmul_sizes s{sizes.batches, sizes.rows, sizes.inner, sizes.columns};
+    kd_matmul_strides st;
+    for (int i = 0; i < 3; ++i) {
+        st.a[i] = a_strides[i];
+        st.b[i] = b_strides[i];
+        st.out[i] = out_strides[i];
+    }
+    const kd_matmul_heads h{heads, head_strides[0], head_strides[1], head_strides[2]};
+    check(kd_matmul_strided_heads(static_cast<int>(dtype), a, b, out, &s, &st, &h), "matmul_strided_heads");
+}
+
 void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* first, std::byte* second,
                std::int64_t count, double learning_rate, double beta1, double beta2, double epsilon,
                double weight_decay, bool decoupled, std::int64_t step) {
     check(kd_adam_step(static_cast<int>(dtype), param, grad, first, second, count, learning_rate, beta1, beta2,
                        epsilon, weight_decay, decoupled ? 1 : 0, step),
           "adam_step");
+}
+
+void adam_step_many(DType dtype, const std::vector<AdamTensor>& tensors, double learning_rate, double beta1,
+                    double beta2, double epsilon, double weight_decay, bool decoupled) {
+    thread_local std::vector<kd_adam_tensor> table;
+    table.clear();
+    for (const AdamTensor& t : tensors) table.push_back({t.param, t.grad, t.first, t.second, t.count, t.step});
+    check(kd_adam_step_many(static_cast<int>(dtype), table.data(), static_cast<std::int64_t>(table.size()),
+                            learning_rate, beta1, beta2, epsilon, weight_decay, decoupled ? 1 : 0),
+          "adam_step_many");
 }
 
 void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
@@ -192,6 +216,13 @@ void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* 
 
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {
     check(kd_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
+}
+
+void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const std::byte* data, std::int64_t outer,
+                    std::int64_t inner) {
+    check(kd_reduce_columns(static_cast<int>(op), static_cast<int>(out), static_cast<int>(in), results, data, outer,
+                            inner),
+          "reduce_columns");
 }
 
 namespace {

@@ -2,7 +2,7 @@
 // interface (reference include/kael/device_kernels.h:96-116) for the fused paths: row softmax /
 // log-softmax, row standardization, cross-entropy losses and gradient, GELU backward as one
 // element op, matmul over strided (transposed or batch-broadcast) operands, the Adam / SGD
-// parameter updates as one kernel per tensor, and the reductions kael otherwise computes on the
+// parameter updates as one kernel per tensor (Adam also over a list of tensors), and the reductions kael otherwise computes on the
 // host (prod, all, any, argmax / argmin, cumsum).
 //
 // Defined in backend_hip.cpp. Unmodified kael never calls them; the device branches that do are
@@ -12,6 +12,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "kael/device_kernels.h"
 
@@ -56,12 +57,36 @@ ElementOp gelu_backward_op(bool approximate);
 void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
                     const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides);
 
+// matmul_strided over a two-level batch: batch i = o * heads + h reads operand X at
+// o * X_strides[0] + h * head_strides[X] (X = a, b, out), for the per-head attention views whose
+// batch dims collapse to no single stride (reference src/nn/transformer.cpp:115-136).
+void matmul_strided_heads(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
+                          const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
+                          std::int64_t heads, const std::int64_t* head_strides);
+
 // One Adam / AdamW step of a contiguous parameter with its moments, in place (reference
 // src/optim/optimizer.cpp:93-120): `step` is the parameter's step count after the increment,
 // `decoupled` selects AdamW's weight decay. Same rounding as kael's composed ops.
 void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* first, std::byte* second,
                std::int64_t count, double learning_rate, double beta1, double beta2, double epsilon,
                double weight_decay, bool decoupled, std::int64_t step);
+
+// One parameter of adam_step_many: contiguous tensors of `count` elements and the parameter's
+// step count after the increment.
+struct AdamTensor {
+    std::byte* param;
+    const std::byte* grad;
+    std::byte* first;
+    std::byte* second;
+    std::int64_t count;
+    std::int64_t step;
+};
+
+// adam_step over every tensor of the list, the same results as one adam_step per tensor in list
+// order (reference src/optim/optimizer.cpp:93-120 loop), in one launch per 32 tensors. The tensors
+// must not share memory that any of them writes.
+void adam_step_many(DType dtype, const std::vector<AdamTensor>& tensors, double learning_rate, double beta1,
+                    double beta2, double epsilon, double weight_decay, bool decoupled);
 
 // One SGD step without momentum, in place (reference src/optim/optimizer.cpp:60-80).
 void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
@@ -83,6 +108,12 @@ void reduce_extra(ExtraReduceOp op, DType in, std::byte* results, const std::byt
 // chunk_size > 0.
 void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* data, std::int64_t chunk_size,
                 std::int64_t output_count);
+
+// results[j] = op over i < outer of data[i * inner + j] for j < inner: device::reduce (Sum, Max,
+// Min; same accumulators and output dtype `out`) of a contiguous tensor over its leading dims, read
+// in place instead of through plan_reduction's transposed copy (reference src/ops/reduce.cpp:118-153).
+void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const std::byte* data, std::int64_t outer,
+                    std::int64_t inner);
 
 // Running sums along `rows` contiguous rows of `size` elements (reference src/ops/sequence.cpp:95-117):
 // f32 / f64 store In, i64 / bool wrapping int64.

@@ -82,6 +82,15 @@ class MatmulStrides(Structure):
     _fields_ = [("a", c_int64 * 3), ("b", c_int64 * 3), ("out", c_int64 * 3)]
 
 
+class MatmulHeads(Structure):
+    _fields_ = [("heads", c_int64), ("a", c_int64), ("b", c_int64), ("out", c_int64)]
+
+
+class AdamTensor(Structure):
+    _fields_ = [("param", c_void_p), ("grad", c_void_p), ("first", c_void_p), ("second", c_void_p),
+                ("count", c_int64), ("step", c_int64)]
+
+
 class GptConfig(Structure):
     _fields_ = [("vocab_size", c_int64), ("max_positions", c_int64), ("layers", c_int64), ("heads", c_int64),
                 ("dimension", c_int64), ("tanh_gelu", c_int32), ("flags", c_int32)]
@@ -104,6 +113,7 @@ SIGNATURES = {
     "convert": (c_int, [c_int, c_int, POINTER(ElementLayout)]),
     "elementwise": (c_int, [c_int, c_int, c_int, POINTER(ElementLayout), ElementParameters]),
     "reduce": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "reduce_columns": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "arg_reduce": (c_int, [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "cumsum": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
@@ -117,8 +127,12 @@ SIGNATURES = {
                                           c_double]),
     "adam_step": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_double, c_double, c_double,
                           c_double, c_double, c_int, c_int64]),
+    "adam_step_many": (c_int, [c_int, POINTER(AdamTensor), c_int64, c_double, c_double, c_double, c_double, c_double,
+                               c_int]),
     "sgd_step": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_double, c_double]),
     "matmul_strided": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides)]),
+    "matmul_strided_heads": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides),
+                                     POINTER(MatmulHeads)]),
     "layout_build": (c_int, [POINTER(ElementLayout), c_int, POINTER(c_int), POINTER(c_int64),
                              POINTER(c_int64), POINTER(c_int), POINTER(c_void_p)]),
 }

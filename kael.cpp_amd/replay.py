@@ -61,18 +61,20 @@ def traced_losses(records: list[dict]) -> list[float]:
 
 def matmul_flops(records: list[dict]) -> int:
     return sum(2 * r["sizes"][0] * r["sizes"][1] * r["sizes"][2] * r["sizes"][3]
-               for r in records if r["op"] in ("matmul", "matmul_strided"))
+               for r in records if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads"))
 
 
 # pointer fields of each record kind (the layout bases of convert / elementwise are checked apart)
 POINTERS = {
     "h2d": ("t",), "d2h": ("s",), "d2d": ("t", "s"), "fill": ("t",), "convert": (), "elementwise": (),
-    "reduce": ("results", "data"), "arg_reduce": ("results", "data"), "cumsum": ("out", "data"),
-    "matmul": ("a", "b", "c"), "matmul_strided": ("a", "b", "c"), "gather": ("out", "data", "indices"),
+    "reduce": ("results", "data"), "reduce_columns": ("results", "data"), "arg_reduce": ("results", "data"),
+    "cumsum": ("out", "data"),
+    "matmul": ("a", "b", "c"), "matmul_strided": ("a", "b", "c"), "matmul_strided_heads": ("a", "b", "c"),
+    "gather": ("out", "data", "indices"),
     "scatter_add": ("data", "indices", "source"), "softmax_rows": ("out", "x"), "standardize_rows": ("out", "x"),
     "cross_entropy_rows": ("losses", "logits", "targets"), "cross_entropy_grad": ("out", "logits", "targets", "weights"),
     "softmax_rows_backward": ("out", "y", "grad"), "standardize_rows_backward": ("out", "x", "y", "grad"),
-    "adam_step": ("p", "g", "m", "v"), "sgd_step": ("p", "g"),
+    "adam_step": ("p", "g", "m", "v"), "sgd_step": ("p", "g"), "adam_step_many": (),
 }
 
 
@@ -112,6 +114,11 @@ def validate(records: list[dict]) -> None:
             if op in ("convert", "elementwise"):
                 for o, p in enumerate(r["layout"]["base"]):
                     check(p, f"record {n} {op}.base[{o}]")
+            if op == "adam_step_many":
+                esize = 4 if r["dtype"] == kd.F32 else 8
+                for t, x in enumerate(r["tensors"]):
+                    for key in ("p", "g", "m", "v"):
+                        check(x[key], f"record {n} {op}.tensors[{t}].{key}", x["count"] * esize)
             if op == "h2d" and "data" in r and len(r["data"]) != 2 * r["bytes"]:
                 raise ReplayError(f"record {n}: h2d payload of {len(r['data']) // 2} bytes for {r['bytes']}")
 
@@ -224,13 +231,16 @@ class Replay:
         if op == "reduce":
             a = (r["rop"], r["out"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["chunk"], r["rows"])
             return (lambda: chk(lib.kd_reduce(*a), "kd_reduce")), None
+        if op == "reduce_columns":
+            a = (r["rop"], r["out"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["outer"], r["inner"])
+            return (lambda: chk(lib.kd_reduce_columns(*a), "kd_reduce_columns")), None
         if op == "arg_reduce":
             a = (r["largest"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["chunk"], r["rows"])
             return (lambda: chk(lib.kd_arg_reduce(*a), "kd_arg_reduce")), None
         if op == "cumsum":
             a = (r["in"], c_void_p(P(r["out"])), c_void_p(P(r["data"])), r["size"], r["rows"])
             return (lambda: chk(lib.kd_cumsum(*a), "kd_cumsum")), None
-        if op in ("matmul", "matmul_strided"):
+        if op in ("matmul", "matmul_strided", "matmul_strided_heads"):
             sizes = kd.MatmulSizes(*r["sizes"])
             a, b, c = c_void_p(P(r["a"])), c_void_p(P(r["b"])), c_void_p(P(r["c"]))
             if op == "matmul":
@@ -238,6 +248,10 @@ class Replay:
             st = kd.MatmulStrides()
             for i in range(3):
                 st.a[i], st.b[i], st.out[i] = r["sa"][i], r["sb"][i], r["sc"][i]
+            if op == "matmul_strided_heads":
+                h = kd.MatmulHeads(*r["heads"])
+                return (lambda: chk(lib.kd_matmul_strided_heads(r["dtype"], a, b, c, byref(sizes), byref(st), byref(h)),
+                                    "kd_matmul_strided_heads")), None
             return (lambda: chk(lib.kd_matmul_strided(r["dtype"], a, b, c, byref(sizes), byref(st)),
                                 "kd_matmul_strided")), None
         if op in ("gather", "scatter_add"):
@@ -293,6 +307,12 @@ class Replay:
             a = (r["dtype"], c_void_p(P(r["p"])), c_void_p(P(r["g"])), c_void_p(P(r["m"])), c_void_p(P(r["v"])),
                  r["count"], r["lr"], r["b1"], r["b2"], r["eps"], r["wd"], r["decoupled"], r["step"])
             return (lambda: chk(lib.kd_adam_step(*a), "kd_adam_step")), None
+        if op == "adam_step_many":
+            table = (kd.AdamTensor * max(1, len(r["tensors"])))()
+            for t, x in enumerate(r["tensors"]):
+                table[t] = kd.AdamTensor(P(x["p"]), P(x["g"]), P(x["m"]), P(x["v"]), x["count"], x["step"])
+            a = (r["dtype"], table, len(r["tensors"]), r["lr"], r["b1"], r["b2"], r["eps"], r["wd"], r["decoupled"])
+            return (lambda: chk(lib.kd_adam_step_many(*a), "kd_adam_step_many")), None
         if op == "sgd_step":
             a = (r["dtype"], c_void_p(P(r["p"])), c_void_p(P(r["g"])), r["count"], r["lr"], r["wd"])
             return (lambda: chk(lib.kd_sgd_step(*a), "kd_sgd_step")), None

@@ -21,12 +21,15 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      product per batch item and a sum over the batch (:37-44)
   src/ops/linalg.cpp                 multiply_batches reads transposed / broadcast operands in
                                      place (:56-76)
-  src/optim/optimizer.cpp            SGD (no momentum, :60-80) and Adam / AdamW (:93-120) update a
-                                     contiguous device parameter in one kernel
+  src/optim/optimizer.cpp            SGD (no momentum, :60-80) updates a contiguous device
+                                     parameter in one kernel; Adam / AdamW (:93-120) collects the
+                                     contiguous device parameters and updates them in one call
   src/ops/reduce.cpp                 prod (:362-369), argmax / argmin (:399-421) and all / any
                                      (:423-451) of a device tensor on the device instead of through
                                      a host copy (the same planning: plan_reduction's kept-first
-                                     permutation, then one call over contiguous chunks)
+                                     permutation, then one call over contiguous chunks); sum
+                                     over the leading dims of a contiguous tensor (:316-319)
+                                     read in place, without plan_reduction's transposed copy
   src/ops/sequence.cpp               cumsum (:95-117) of a device tensor on the device
   src/nn/transformer.cpp             nn::generate (:256-295) with temperature 0, the KV cache and a
                                      batch-1 prompt on the device runs on the decode engine
@@ -107,21 +110,18 @@ GELU_BACKWARD_BRANCH = """                          if (saved.get().device() != 
                           }
 """
 
-STRIDES_HELPER = """// MI355X: element strides {batch, row, column} of an expanded operand whose batch dims flatten
-// to one stride (contiguous batch dims, or broadcast ones); false when they do not.
-bool flat_batch_strides(const Tensor& v, std::int64_t* strides) {
-    const std::int64_t d = v.dim();
-    strides[0] = 0;
-    strides[1] = v.stride(d - 2);
-    strides[2] = v.stride(d - 1);
+STRIDES_HELPER = """// MI355X: the element stride of dims [lo, hi) of an expanded operand when they flatten to one
+// (contiguous or broadcast dims; size-1 dims skipped, 0 when all have size 1); false otherwise.
+bool flat_group_stride(const Tensor& v, std::int64_t lo, std::int64_t hi, std::int64_t& stride) {
+    stride = 0;
     bool first = true;
     std::int64_t span = 0;
-    for (std::int64_t i = d - 3; i >= 0; --i) {
+    for (std::int64_t i = hi - 1; i >= lo; --i) {
         if (v.size(i) == 1) {
             continue;
         }
         if (first) {
-            strides[0] = v.stride(i);
+            stride = v.stride(i);
             span = v.stride(i) * v.size(i);
             first = false;
         } else if (v.stride(i) == span) {
@@ -131,6 +131,15 @@ bool flat_batch_strides(const Tensor& v, std::int64_t* strides) {
         }
     }
     return true;
+}
+
+// MI355X: element strides {batch, row, column} of an expanded operand whose batch dims flatten
+// to one stride; false when they do not.
+bool flat_batch_strides(const Tensor& v, std::int64_t* strides) {
+    const std::int64_t d = v.dim();
+    strides[1] = v.stride(d - 2);
+    strides[2] = v.stride(d - 1);
+    return flat_group_stride(v, 0, d - 2, strides[0]);
 }
 
 """
@@ -148,18 +157,69 @@ MATMUL_BRANCH = """    if (a.device() != Device::CPU && is_floating_point(dtype)
                                    {numel(batch), rows, inner, columns}, sa, sb, so);
             return out;
         }
+        // Batch dims that flatten in two groups, [0, cut) and [cut, end) (attention's per-head
+        // views: [batch, head] over a [batch, token, head, dim] tensor): one product over both.
+        const std::int64_t batch_dims = va.dim() - 2;
+        for (std::int64_t cut = 1; cut < batch_dims; ++cut) {
+            std::int64_t heads = 1;
+            for (std::int64_t i = cut; i < batch_dims; ++i) {
+                heads *= va.size(i);
+            }
+            std::int64_t head_strides[3];
+            if (heads < 1 || !flat_group_stride(va, 0, cut, sa[0]) || !flat_group_stride(va, cut, batch_dims, head_strides[0]) ||
+                !flat_group_stride(vb, 0, cut, sb[0]) || !flat_group_stride(vb, cut, batch_dims, head_strides[1])) {
+                continue;
+            }
+            sa[1] = va.stride(-2);
+            sa[2] = va.stride(-1);
+            sb[1] = vb.stride(-2);
+            sb[2] = vb.stride(-1);
+            head_strides[2] = rows * columns;
+            Tensor out = empty(with_matrix_dims(batch, rows, columns), dtype, a.device());
+            const std::int64_t so[3] = {heads * rows * columns, columns, 1};
+            device::matmul_strided_heads(dtype, va.device_data(), vb.device_data(), out.device_data(),
+                                         {numel(batch), rows, inner, columns}, sa, sb, so, heads, head_strides);
+            return out;
+        }
     }
+"""
+
+ADAM_PENDING = """    // MI355X: the updates of device parameters are collected and run as one device call over the
+    // list (a launch per 32 tensors instead of one per tensor). The list is flushed before
+    // anything that must see its updates: a parameter on kael's composed path, a change of dtype,
+    // or a tensor sharing storage with one already listed; so the results are those of the
+    // sequential loop.
+    std::vector<device::AdamTensor> pending;
+    std::unordered_set<const void*> pending_storages;
+    DType pending_dtype = DType::F32;
+    const bool decoupled = options_.weight_decay > 0.0 && mode_ == WeightDecayMode::Decoupled;
+    const auto flush = [&] {
+        if (!pending.empty()) {
+            device::adam_step_many(pending_dtype, pending, learning_rate(), options_.beta1, options_.beta2,
+                                   options_.epsilon, options_.weight_decay, decoupled);
+        }
+        pending.clear();
+        pending_storages.clear();
+    };
 """
 
 ADAM_BRANCH = """        if (parameter.device() != Device::CPU && is_floating_point(parameter.dtype()) &&
             parameter.is_contiguous() && stored->dtype() == parameter.dtype() && stored->is_contiguous() &&
             first_moments_[i].is_contiguous() && second_moments_[i].is_contiguous()) {
-            // MI355X: the whole update in one kernel, rounded as the ops below round it.
-            const bool decoupled = options_.weight_decay > 0.0 && mode_ == WeightDecayMode::Decoupled;
-            device::adam_step(parameter.dtype(), parameter.device_data(), stored->device_data(),
-                              first_moments_[i].device_data(), second_moments_[i].device_data(), parameter.numel(),
-                              learning_rate(), options_.beta1, options_.beta2, options_.epsilon,
-                              options_.weight_decay, decoupled, steps_[i]);
+            const void* storages[4] = {parameter.impl()->storage.get(), stored->impl()->storage.get(),
+                                       first_moments_[i].impl()->storage.get(),
+                                       second_moments_[i].impl()->storage.get()};
+            bool flush_first = !pending.empty() && parameter.dtype() != pending_dtype;
+            for (const void* storage : storages) {
+                flush_first = flush_first || pending_storages.count(storage) != 0;
+            }
+            if (flush_first) {
+                flush();
+            }
+            pending_dtype = parameter.dtype();
+            pending.push_back({parameter.device_data(), stored->device_data(), first_moments_[i].device_data(),
+                               second_moments_[i].device_data(), parameter.numel(), steps_[i]});
+            pending_storages.insert(std::begin(storages), std::end(storages));
             // The in-place ops below bump each storage's version once per op.
             parameter.impl()->storage->bump_version();
             if (decoupled) {
@@ -171,6 +231,7 @@ ADAM_BRANCH = """        if (parameter.device() != Device::CPU && is_floating_po
             }
             continue;
         }
+        flush();
 """
 
 SGD_BRANCH = """        if (options_.momentum == 0.0 && parameter.device() != Device::CPU &&
@@ -190,11 +251,95 @@ WEIGHT_GRADIENT_BRANCH = """                     if (g.device() != Device::CPU &
                          // MI355X: the weight is shared by every batch item, so its gradient is one
                          // product over the folded batch (K = every row of every item). An empty
                          // last dim keeps kael's per-item path (the fold would divide by zero).
+                         // Computed as (g^T . X)^T: the product lands in the layout of the weight
+                         // behind the transposed view (Linear's weight.T()), so that view's backward
+                         // hands the weight a contiguous gradient and no transposing copy is made.
                          const Tensor x = left.get();
                          const Tensor flat_x = x.reshape({x.numel() / x.size(-1), x.size(-1)});
                          const Tensor flat_g = g.reshape({g.numel() / g.size(-1), g.size(-1)});
-                         return matmul(flat_x.mT(), flat_g).to(dtype);
+                         return matmul(flat_g.mT(), flat_x).mT().to(dtype);
                      }
+"""
+
+MASKED_FILL_BRANCH = """    if (t.device() != Device::CPU && mask.dtype() == DType::Bool &&
+        broadcast_shapes(t.shape(), mask.shape()) == t.shape()) {
+        // MI355X: one pass out = mask ? value : t into a fresh tensor, instead of a clone of t that
+        // masked_fill_ then rewrites (the same element function and operands as masked_fill_).
+        Tensor out = autograd::without_grad([&] {
+            Tensor filled = empty(t.shape(), t.dtype(), t.device());
+            TensorIterator iterator;
+            iterator.add_output(filled).add_input(t).add_input(mask.to(t.dtype())).build();
+            dispatch(t.dtype(), [&]<typename T>() {
+                functions::MaskedFill<T> fill{value.as<T>()};
+                detail::run_typed<T, T, 2>(iterator, fill);
+            });
+            return filled;
+        });
+        autograd::record_masked_fill(out, t, mask);
+        return out;
+    }
+"""
+
+ACCUMULATE_BRANCH = """    // MI355X: a device gradient that nothing else references (the engine's buffer holds its only
+    // handle, and it spans its whole storage contiguously) becomes the leaf's first gradient as
+    // is, instead of through clone(), which would copy it: the values are the clone's and nothing
+    // else can observe the difference.
+    if (gradient.device() != Device::CPU && leaf_->autograd && !leaf_->autograd->grad &&
+        gradient.impl().use_count() == 1 && gradient.impl()->storage.use_count() == 1 &&
+        !gradient.impl()->autograd && gradient.is_contiguous() && gradient.impl()->offset == 0 &&
+        gradient.nbytes() == gradient.impl()->storage->nbytes()) {
+        leaf_->autograd->grad = gradient;
+        return {};
+    }
+"""
+
+LEADING_REDUCE_HELPER = """// MI355X: a contiguous tensor reduced over its leading dims (an [outer, inner] matrix reduced
+// over its rows: bias and LayerNorm gradients summed over every token) as one
+// device::reduce_columns call that reads it in place; nullopt for any other case, which keeps
+// plan_reduction's transposed copy.
+std::optional<Tensor> device_leading_reduce(const Tensor& t, const Dims& dims, bool keepdim, device::ReduceOp op,
+                                            DType dtype) {
+    if (t.dim() < 2 || !t.is_contiguous() || t.numel() == 0) {
+        return std::nullopt;
+    }
+    const std::vector<bool> reduced = reduced_positions(t, dims);
+    std::size_t lead = 0;
+    while (lead < reduced.size() && reduced[lead]) {
+        ++lead;
+    }
+    if (lead == 0 || lead == reduced.size()) {
+        return std::nullopt;
+    }
+    for (std::size_t i = lead; i < reduced.size(); ++i) {
+        if (reduced[i]) {
+            return std::nullopt;
+        }
+    }
+    Shape output_shape;
+    std::int64_t outer = 1;
+    std::int64_t inner = 1;
+    for (std::size_t i = 0; i < reduced.size(); ++i) {
+        if (i < lead) {
+            outer *= t.shape()[i];
+            if (keepdim) {
+                output_shape.push_back(1);
+            }
+        } else {
+            inner *= t.shape()[i];
+            output_shape.push_back(t.shape()[i]);
+        }
+    }
+    Tensor out = empty(output_shape, dtype, t.device());
+    device::reduce_columns(op, dtype, t.dtype(), out.device_data(), t.device_data(), outer, inner);
+    return out;
+}
+
+"""
+
+LEADING_SUM_BRANCH = """    if (std::optional<Tensor> columns = device_leading_reduce(
+            t, dims, keepdim, device::ReduceOp::Sum, is_floating_point(t.dtype()) ? t.dtype() : DType::I64)) {
+        return *columns;
+    }
 """
 
 REDUCE_HELPERS = """// MI355X: the reductions below run on the device over the same plan as device_reduce.
@@ -387,11 +532,24 @@ EDITS = [
     ("src/optim/optimizer.cpp",
      "        Tensor gradient =\n            options_.weight_decay > 0.0 ? *stored + parameter * options_.weight_decay : *stored;\n",
      "before", SGD_BRANCH),
+    ("src/optim/optimizer.cpp", "#include <utility>\n", "after", "#include <unordered_set>\n#include <vector>\n"),
+    ("src/optim/optimizer.cpp", "void AdamBase::update() {\n", "after", ADAM_PENDING),
     ("src/optim/optimizer.cpp",
      "        const double second_correction = 1.0 - std::pow(options_.beta2, step);\n", "after", ADAM_BRANCH),
+    ("src/optim/optimizer.cpp", "                       learning_rate());\n    }\n", "after", "    flush();\n"),
     ("src/autograd/functions_linalg.cpp",
      "                     const Tensor gradient = matmul(left.get().mT(), layout.matrix_gradient(g));\n", "before",
      WEIGHT_GRADIENT_BRANCH),
+    ("src/ops/indexing.cpp", "Tensor masked_fill(const Tensor& t, const Tensor& mask, Scalar value) {\n", "after",
+     MASKED_FILL_BRANCH),
+    ("src/autograd/node.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/tensor_impl.h"\n'),
+    ("src/autograd/node.cpp", "GradientList AccumulateGrad::apply(const Tensor& gradient) {\n", "after",
+     ACCUMULATE_BRANCH),
+    ("src/ops/reduce.cpp", "#include <functional>\n", "after", "#include <optional>\n"),
+    ("src/ops/reduce.cpp", "Tensor device_reduce(const Reduction& reduction, device::ReduceOp op, DType dtype) {\n",
+     "before", LEADING_REDUCE_HELPER),
+    ("src/ops/reduce.cpp", "Tensor device_sum(const Tensor& t, const Dims& dims, bool keepdim) {\n", "after",
+     LEADING_SUM_BRANCH),
     ("src/ops/reduce.cpp", "Tensor device_norm(const Tensor& t, const Dims& dims, bool keepdim) {\n", "before",
      REDUCE_HELPERS),
     ("src/ops/reduce.cpp", "Tensor prod(const Tensor& t, const Dims& dims, bool keepdim) {\n", "after", PROD_BRANCH),

@@ -755,6 +755,29 @@ int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void
     return KD_OK;
 }
 
+/* kd_reduce_columns: column j of the [outer, inner] matrix copied out and reduced as one chunk by
+ * oracle_reduce, exactly as kael's plan_reduction copy followed by device::reduce computes it
+ * (reference src/ops/reduce.cpp:118-153, 309-314). */
+int oracle_reduce_columns(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                          int64_t outer, int64_t inner) {
+    if (outer < 0 || inner < 0) return fail("reduce_columns: negative size");
+    const int64_t esize = dtype_size(in_dtype);
+    if (esize == 0) return fail("reduce_columns: unknown dtype");
+    if (inner == 0) return KD_OK;
+    const int64_t osize = dtype_size(op == KD_REDUCE_ALL || op == KD_REDUCE_ANY ? KD_BOOL
+                                     : (op == KD_REDUCE_SUM || op == KD_REDUCE_PROD) && in_dtype != KD_F32 && in_dtype != KD_F64
+                                         ? KD_I64 : in_dtype);
+    char* column = (char*)malloc((size_t)(outer > 0 ? outer : 1) * (size_t)esize);
+    int rc = KD_OK;
+    for (int64_t j = 0; j < inner && rc == KD_OK; ++j) {
+        for (int64_t i = 0; i < outer; ++i)
+            memcpy(column + i * esize, (const char*)data + (i * inner + j) * esize, (size_t)esize);
+        rc = oracle_reduce(op, out_dtype, in_dtype, (char*)results + j * osize, column, outer, 1);
+    }
+    free(column);
+    return rc;
+}
+
 /* ---- matmul: kernels.inl:136-177 -------------------------------------------------------------- */
 
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,
@@ -811,6 +834,29 @@ int oracle_matmul_strided(int dtype, const void* a, const void* b, void* out,
                     ((int64_t*)out)[oo] = acc;
                 }
             }
+    return KD_OK;
+}
+
+/* kd_matmul_strided_heads: batch i = o * heads + h at o * strides->X[0] + h * heads->X, i.e.
+ * oracle_matmul_strided over the `heads` batches of each outer index o. */
+int oracle_matmul_strided_heads(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,
+                                const kd_matmul_strides* t, const kd_matmul_heads* h) {
+    if (h->heads < 1) return fail("matmul_strided_heads: heads must be >= 1");
+    if (s->batches % h->heads != 0) return fail("matmul_strided_heads: batches is not a multiple of heads");
+    const int64_t esize = dtype_size(dtype);
+    if (esize == 0) return fail("matmul: unknown dtype");
+    kd_matmul_sizes inner = *s;
+    inner.batches = h->heads;
+    kd_matmul_strides st = *t;
+    st.a[0] = h->a;
+    st.b[0] = h->b;
+    st.out[0] = h->out;
+    for (int64_t o = 0; o < s->batches / h->heads; ++o) {
+        const int rc = oracle_matmul_strided(dtype, (const char*)a + o * t->a[0] * esize,
+                                             (const char*)b + o * t->b[0] * esize, (char*)out + o * t->out[0] * esize,
+                                             &inner, &st);
+        if (rc != KD_OK) return rc;
+    }
     return KD_OK;
 }
 
@@ -1154,6 +1200,20 @@ int oracle_adam_step(int dtype, void* param, const void* grad, void* first, void
 }
 
 #undef ADAM_BODY
+
+/* kd_adam_step_many: oracle_adam_step over the table in order, as the loop of AdamBase::update
+ * (reference src/optim/optimizer.cpp:93-120) visits the parameters. */
+int oracle_adam_step_many(int dtype, const kd_adam_tensor* tensors, int64_t n, double learning_rate, double beta1,
+                          double beta2, double epsilon, double weight_decay, int decoupled) {
+    if (n < 0 || (n > 0 && tensors == NULL)) return fail("adam_step_many: negative count or no table");
+    for (int64_t i = 0; i < n; ++i) {
+        const kd_adam_tensor* x = &tensors[i];
+        const int rc = oracle_adam_step(dtype, x->param, x->grad, x->first, x->second, x->count, learning_rate, beta1,
+                                        beta2, epsilon, weight_decay, decoupled, x->step);
+        if (rc != KD_OK) return rc;
+    }
+    return KD_OK;
+}
 
 int oracle_sgd_step(int dtype, void* param, const void* grad, int64_t count, double learning_rate,
                     double weight_decay) {

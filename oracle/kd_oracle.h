@@ -24,6 +24,8 @@ int oracle_elementwise(int op, int out_dtype, int in_dtype, const kd_element_lay
                        kd_element_parameters parameters);
 int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void* data,
                   int64_t chunk_size, int64_t output_count);
+int oracle_reduce_columns(int op, int out_dtype, int in_dtype, void* results, const void* data,
+                          int64_t outer, int64_t inner);
 int oracle_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
                       int64_t output_count);
 int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);
@@ -33,6 +35,8 @@ int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_m
                   int exact);
 int oracle_matmul_strided(int dtype, const void* a, const void* b, void* out,
                           const kd_matmul_sizes* sizes, const kd_matmul_strides* strides);
+int oracle_matmul_strided_heads(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                                const kd_matmul_strides* strides, const kd_matmul_heads* heads);
 int oracle_gather(int dtype, void* out, const void* data, const int64_t* indices,
                   const kd_index_layout* layout);
 int oracle_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
@@ -52,6 +56,8 @@ int oracle_standardize_rows_backward(int dtype, void* out, const void* x, const 
 int oracle_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
                      double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
                      int decoupled, int64_t step);
+int oracle_adam_step_many(int dtype, const kd_adam_tensor* tensors, int64_t n, double learning_rate, double beta1,
+                          double beta2, double epsilon, double weight_decay, int decoupled);
 int oracle_sgd_step(int dtype, void* param, const void* grad, int64_t count, double learning_rate,
                     double weight_decay);
 int oracle_layout_build(kd_element_layout* out, int operands, const int* ranks,

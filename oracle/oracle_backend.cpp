@@ -242,8 +242,9 @@ void scatter_add(DType dtype, std::byte* data, const std::int64_t* indices, cons
 namespace {
 // 0 softmax_rows, 1 standardize_rows, 2 cross_entropy_rows, 3 cross_entropy_grad,
 // 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
-// 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward.
-constexpr int kExtensions = 13;
+// 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
+// 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads.
+constexpr int kExtensions = 16;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -323,6 +324,25 @@ void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::by
     check(oracle_matmul_strided(static_cast<int>(dtype), a, b, out, &sizes, &st), "matmul_strided");
 }
 
+void matmul_strided_heads(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& s,
+                          const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
+                          std::int64_t heads, const std::int64_t* head_strides) {
+    ++g_extension_calls[15];
+    const kd_matmul_sizes sizes{s.batches, s.rows, s.inner, s.columns};
+    kd_matmul_strides st;
+    for (int i = 0; i < 3; ++i) {
+        st.a[i] = a_strides[i];
+        st.b[i] = b_strides[i];
+        st.out[i] = out_strides[i];
+    }
+    const kd_matmul_heads h{heads, head_strides[0], head_strides[1], head_strides[2]};
+    KD_TRACE("matmul_strided_heads", kv("dtype", static_cast<int>(dtype)) + "," + kv("a", tp(a)) + "," + kv("b", tp(b)) +
+                                         "," + kv("c", tp(out)) + "," + kv("sizes", ints(&sizes.batches, 4)) + "," +
+                                         kv("sa", ints(st.a, 3)) + "," + kv("sb", ints(st.b, 3)) + "," +
+                                         kv("sc", ints(st.out, 3)) + "," + kv("heads", ints(&h.heads, 4)));
+    check(oracle_matmul_strided_heads(static_cast<int>(dtype), a, b, out, &sizes, &st, &h), "matmul_strided_heads");
+}
+
 void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* first, std::byte* second,
                std::int64_t count, double learning_rate, double beta1, double beta2, double epsilon,
                double weight_decay, bool decoupled, std::int64_t step) {
@@ -335,6 +355,28 @@ void adam_step(DType dtype, std::byte* param, const std::byte* grad, std::byte* 
     check(oracle_adam_step(static_cast<int>(dtype), param, grad, first, second, count, learning_rate, beta1, beta2,
                            epsilon, weight_decay, decoupled ? 1 : 0, step),
           "adam_step");
+}
+
+void adam_step_many(DType dtype, const std::vector<AdamTensor>& tensors, double learning_rate, double beta1,
+                    double beta2, double epsilon, double weight_decay, bool decoupled) {
+    ++g_extension_calls[14];
+    std::vector<kd_adam_tensor> table;
+    for (const AdamTensor& t : tensors) table.push_back({t.param, t.grad, t.first, t.second, t.count, t.step});
+    const auto list = [&] {  // evaluated under the trace lock
+        std::string s;
+        for (const AdamTensor& t : tensors)
+            s += std::string(s.empty() ? "" : ",") + "{" + kv("p", tp(t.param)) + "," + kv("g", tp(t.grad)) + "," +
+                 kv("m", tp(t.first)) + "," + kv("v", tp(t.second)) + "," + kv("count", t.count) + "," +
+                 kv("step", t.step) + "}";
+        return s;
+    };
+    KD_TRACE("adam_step_many", kv("dtype", static_cast<int>(dtype)) + ",\"tensors\":[" + list() + "]," +
+                                   kv("lr", real(learning_rate)) + "," + kv("b1", real(beta1)) + "," + kv("b2", real(beta2)) +
+                                   "," + kv("eps", real(epsilon)) + "," + kv("wd", real(weight_decay)) + "," +
+                                   kv("decoupled", decoupled ? 1 : 0));
+    check(oracle_adam_step_many(static_cast<int>(dtype), table.data(), static_cast<std::int64_t>(table.size()),
+                                learning_rate, beta1, beta2, epsilon, weight_decay, decoupled ? 1 : 0),
+          "adam_step_many");
 }
 
 void sgd_step(DType dtype, std::byte* param, const std::byte* grad, std::int64_t count, double learning_rate,
@@ -364,6 +406,17 @@ void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* 
                                kv("rows", output_count));
     check(oracle_arg_reduce(largest ? 1 : 0, static_cast<int>(in), results, data, chunk_size, output_count),
           "arg_reduce");
+}
+
+void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const std::byte* data, std::int64_t outer,
+                    std::int64_t inner) {
+    ++g_extension_calls[13];
+    KD_TRACE("reduce_columns", kv("rop", static_cast<int>(op)) + "," + kv("out", static_cast<int>(out)) + "," +
+                                   kv("in", static_cast<int>(in)) + "," + kv("results", tp(results)) + "," +
+                                   kv("data", tp(data)) + "," + kv("outer", outer) + "," + kv("inner", inner));
+    check(oracle_reduce_columns(static_cast<int>(op), static_cast<int>(out), static_cast<int>(in), results, data, outer,
+                                inner),
+          "reduce_columns");
 }
 
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {

@@ -365,3 +365,105 @@ def test_random_strided_products(kdb, oracle, dtype, block):
             close(dc.numpy(), want.astype(np.float64))
         except AssertionError as e:
             raise AssertionError(f"seed {seed}: {batches}x{m}x{k}x{n} a{sa} b{sb} out{so}: {e}") from None
+
+
+def heads_call(kdb, dtype, a_store, b_store, out_len, sizes, sa, sb, so, heads, ha, hb, ho):
+    strides = kd.MatmulStrides()
+    for i in range(3):
+        strides.a[i], strides.b[i], strides.out[i] = sa[i], sb[i], so[i]
+    h = kd.MatmulHeads(heads, ha, hb, ho)
+    npd = kd.NUMPY_DTYPE[dtype]
+    da, db, dc = kdb.to_device(a_store), kdb.to_device(b_store), kdb.empty((out_len,), npd)
+    kdb.call("matmul_strided_heads", dtype, da.ptr, db.ptr, dc.ptr, sizes, strides, h)
+    return dc.numpy(), strides, h
+
+
+def test_attention_head_views_equal_copied_operands(kdb, oracle):
+    """C4's attention products over views of the fused qkv projection [B, T, 3, H, D] and of the
+    output gradient [B, T, H, D] (B 32, T 128, H 4, D 64): Q.K^T, P.V, dY.V^T, P^T.dY and dS.K,
+    read in place through two-level batch strides, against the same products of the views copied
+    to contiguous tensors (the path kael takes without these strides): the same bits, and the
+    oracle within the device tolerance."""
+    B, T, H, D = 32, 128, 4, 64
+    C = H * D
+    rng = np.random.default_rng(11)
+    qkv = rng.uniform(-1, 1, (B, T, 3, H, D)).astype(np.float32)
+    dy = rng.uniform(-1, 1, (B, T, H, D)).astype(np.float32)
+    p = rng.uniform(0, 1, (B, H, T, T)).astype(np.float32)
+    q_v = (T * 3 * C, D, 3 * C, 1)          # outer, head, row, column strides of q[b, h] = qkv[b, :, 0, h, :]
+    kT = (T * 3 * C, D, 1, 3 * C)           # k[b, h]^T
+    k_v = (T * 3 * C, D, 3 * C, 1)
+    dy_v = (T * C, D, C, 1)
+    p_v, pT = (H * T * T, T * T, T, 1), (H * T * T, T * T, 1, T)
+    views = {"q": (qkv, 0, q_v, (T, D)), "kT": (qkv, C, kT, (D, T)), "k": (qkv, C, k_v, (T, D)),
+             "v": (qkv, 2 * C, k_v, (T, D)), "vT": (qkv, 2 * C, kT, (D, T)), "dy": (dy, 0, dy_v, (T, D)),
+             "p": (p, 0, p_v, (T, T)), "pT": (p, 0, pT, (T, T))}
+
+    def dense(name):
+        store, off, (so_, sh, sr, sc), (r, c) = views[name]
+        flat = store.ravel()[off:]
+        return np.lib.stride_tricks.as_strided(flat, (B, H, r, c), tuple(4 * x for x in (so_, sh, sr, sc))).copy()
+
+    for left, right in [("q", "kT"), ("p", "v"), ("dy", "vT"), ("pT", "dy"), ("p", "k")]:
+        la, lb = views[left], views[right]
+        m, k = la[3]
+        n = lb[3][1]
+        sizes = kd.MatmulSizes(B * H, m, k, n)
+        so = (H * m * n, n, 1)
+        a_store, b_store = la[0].ravel()[la[1]:].copy(), lb[0].ravel()[lb[1]:].copy()
+        got, strides, h = heads_call(kdb, kd.F32, a_store, b_store, B * H * m * n, sizes, (la[2][0], la[2][2], la[2][3]),
+                                     (lb[2][0], lb[2][2], lb[2][3]), so, H, la[2][1], lb[2][1], m * n)
+        copied = _strided_product(kdb, dense(left).ravel(), dense(right).ravel(), B * H, m, k, n, (m * k, k, 1), (k * n, n, 1))
+        np.testing.assert_array_equal(got, copied.ravel(), err_msg=f"{left}.{right}")
+        want = np.empty(B * H * m * n, np.float32)
+        assert oracle.oracle_matmul_strided_heads(kd.F32, support.ptr(a_store), support.ptr(b_store), support.ptr(want),
+                                                  sizes, strides, h) == 0
+        close(got, want.astype(np.float64))
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64], ids=["f32", "f64"])
+def test_random_two_level_batches(kdb, oracle, dtype):
+    """30 seeded products over random [outer, heads] batches: random row / column / head / outer
+    strides (head dims interleaved with the rows, as attention's are, or blocked), ragged and whole
+    tiles, f32 on every kernel family; against oracle_matmul_strided_heads."""
+    npd = kd.NUMPY_DTYPE[dtype]
+    for seed in range(30):
+        rng = np.random.default_rng(1000 + seed)
+        outer, heads = int(rng.integers(1, 4)), int(rng.integers(2, 5))
+        m, k, n = (DIMS[int(rng.integers(0, len(DIMS)))] for _ in range(3))
+
+        def operand(rows, cols):
+            gap = int(rng.integers(0, 3))
+            if rng.random() < 0.5:   # heads interleaved: [rows][heads][cols] (+ gap)
+                st = (rows * (heads * cols + gap), cols, heads * cols + gap, 1)
+            else:                    # transposed within the head: [heads][cols][rows]
+                st = (heads * cols * (rows + gap), cols * (rows + gap), 1, rows + gap)
+            extent = 1 + (outer - 1) * st[0] + (heads - 1) * st[1] + (rows - 1) * st[2] + (cols - 1) * st[3]
+            return st, extent
+
+        sa, la = operand(m, k)
+        sb, lb = operand(k, n)
+        a_store = rng.uniform(-1, 1, la).astype(npd)
+        b_store = rng.uniform(-1, 1, lb).astype(npd)
+        sizes = kd.MatmulSizes(outer * heads, m, k, n)
+        so = (heads * m * n, n, 1)
+        got, strides, h = heads_call(kdb, dtype, a_store, b_store, outer * heads * m * n, sizes, (sa[0], sa[2], sa[3]),
+                                     (sb[0], sb[2], sb[3]), so, heads, sa[1], sb[1], m * n)
+        want = np.zeros(outer * heads * m * n, npd)
+        assert oracle.oracle_matmul_strided_heads(dtype, support.ptr(a_store), support.ptr(b_store), support.ptr(want),
+                                                  sizes, strides, h) == 0
+        try:
+            close(got, want.astype(np.float64))
+        except AssertionError as e:
+            raise AssertionError(f"seed {seed}: {outer}x{heads} {m}x{k}x{n} a{sa} b{sb}: {e}") from None
+
+
+def test_two_level_batches_reject_bad_heads(kdb):
+    x = kdb.to_device(np.zeros(64, np.float32))
+    strides = kd.MatmulStrides()
+    for i, v in enumerate((16, 4, 1)):
+        strides.a[i] = strides.b[i] = strides.out[i] = v
+    for heads, batches in ((0, 2), (3, 4)):
+        with pytest.raises(kd.KdError):
+            kdb.call("matmul_strided_heads", kd.F32, x.ptr, x.ptr, x.ptr, kd.MatmulSizes(batches, 2, 2, 2), strides,
+                     kd.MatmulHeads(heads, 8, 8, 8))

@@ -93,3 +93,45 @@ def test_empty_chunks(kdb):
     np.testing.assert_array_equal(out.numpy(), [0, 0, 0])
     with pytest.raises(kd.KdError):
         kdb.call("reduce", kd.REDUCE_MAX, 0, kd.F32, out.ptr, out.ptr, 0, 3)
+
+
+COLUMN_SHAPES = [(1, 1), (13, 7), (64, 3), (700, 513), (4096, 256), (4096, 768), (100000, 3), (3, 100000), (4097, 1)]
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64, kd.BOOL], ids=["f32", "f64", "i64", "bool"])
+@pytest.mark.parametrize("op", [kd.REDUCE_SUM, kd.REDUCE_MAX, kd.REDUCE_MIN], ids=["sum", "max", "min"])
+@pytest.mark.parametrize("outer,inner", COLUMN_SHAPES, ids=[f"{o}x{i}" for o, i in COLUMN_SHAPES])
+def test_reduce_columns_matches_oracle(kdb, oracle, op, dtype, outer, inner):
+    """kd_reduce_columns (leading dim of a contiguous [outer, inner] tensor, read in place) against
+    oracle_reduce_columns, which the CPU suite pins bit for bit to the reference's reduce tasks over
+    the transposed copy kael makes today. Same tolerance rule as kd_reduce."""
+    rng = np.random.default_rng(outer * 17 + inner + op * 5 + dtype)
+    x = values(rng, dtype, outer * inner)
+    out_np = np.int64 if (op == kd.REDUCE_SUM and dtype in (kd.I64, kd.BOOL)) else kd.NUMPY_DTYPE[dtype]
+    want = np.zeros(inner, out_np)
+    assert oracle.oracle_reduce_columns(op, 0, dtype, support.ptr(want), support.ptr(x), outer, inner) == 0
+    dx = kdb.to_device(x)
+    out = kdb.empty((inner,), out_np)
+    kdb.call("reduce_columns", op, 0, dtype, out.ptr, dx.ptr, outer, inner)
+    got = out.numpy()
+    if dtype == kd.F64 and op == kd.REDUCE_SUM:
+        scale = np.abs(x.reshape(outer, inner)).sum(axis=0) + 1e-300
+        assert np.all(np.abs(got - want) <= 1e-12 * scale)
+    else:
+        np.testing.assert_array_equal(got, want)
+
+
+def test_reduce_columns_non_finite_and_empty(kdb, oracle):
+    x = np.array([[1, np.inf, np.nan], [2, -np.inf, 0.0], [-0.0, 1, 3]], np.float32).ravel()
+    for op in (kd.REDUCE_SUM, kd.REDUCE_MAX, kd.REDUCE_MIN):
+        want = np.zeros(3, np.float32)
+        assert oracle.oracle_reduce_columns(op, 0, kd.F32, support.ptr(want), support.ptr(x), 3, 3) == 0
+        dx = kdb.to_device(x)
+        out = kdb.empty((3,), np.float32)
+        kdb.call("reduce_columns", op, 0, kd.F32, out.ptr, dx.ptr, 3, 3)
+        got = out.numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want)) and np.array_equal(got[~np.isnan(want)], want[~np.isnan(want)])
+    out = kdb.empty((4,), np.float32)
+    kdb.call("reduce_columns", kd.REDUCE_SUM, 0, kd.F32, out.ptr, None, 0, 4)  # no rows: sum identity
+    np.testing.assert_array_equal(out.numpy(), np.zeros(4, np.float32))
+    kdb.call("reduce_columns", kd.REDUCE_SUM, 0, kd.F32, None, None, 5, 0)  # no columns: nothing to write

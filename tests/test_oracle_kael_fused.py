@@ -20,10 +20,15 @@ from test_oracle_device_suite import NAMES
 CASES = support.golden_cases()
 # Numbered as the oracle backend counts them (oracle/oracle_backend.cpp).
 EXTENSIONS = ["softmax_rows", "standardize_rows", "cross_entropy_rows", "cross_entropy_grad", "gelu_backward_op",
-              "matmul_strided", "adam_step", "sgd_step", "reduce_extra", "arg_reduce", "cumsum_rows"]
-# The entry points a char-GPT training step reaches (forward, backward, Adam).
+              "matmul_strided", "adam_step", "sgd_step", "reduce_extra", "arg_reduce", "cumsum_rows",
+              "softmax_rows_backward", "standardize_rows_backward", "reduce_columns", "adam_step_many",
+              "matmul_strided_heads"]
+# The entry points a char-GPT training step reaches (forward, backward, Adam over the parameter list;
+# reduce_columns: the bias and LayerNorm gradients summed over every token; matmul_strided_heads:
+# the attention products over per-head views).
 TRAINING = ["softmax_rows", "standardize_rows", "cross_entropy_rows", "cross_entropy_grad", "gelu_backward_op",
-            "matmul_strided", "adam_step"]
+            "matmul_strided", "adam_step_many", "softmax_rows_backward", "standardize_rows_backward", "reduce_columns",
+            "matmul_strided_heads"]
 
 
 def calls(lib):

@@ -160,3 +160,33 @@ def test_row_kernels_match_kael_cpu(oracle, refdev, dtype):
     assert refdev.ref_cross_entropy_grad(dtype, P(gb), P(x), P(t), P(rw), 40, 96) == 0
     ok, msg = support.golden_close(ga, gb, 2e-6, 1e-7)
     assert ok, msg
+
+
+def test_matmul_two_level_batches_against_numpy_views(oracle):
+    """oracle_matmul_strided_heads on attention-shaped views (q[b, h] and k[b, h]^T of a
+    [B, T, 3, H, D] store, the output [B, H, T, T]) against numpy's product of the same views:
+    exact in wrapping int64 with small values, and a mistaken head / outer stride or batch order
+    changes the result."""
+    B, T, H, D = 2, 5, 3, 4
+    C = H * D
+    rng = np.random.default_rng(8)
+    qkv = rng.integers(-9, 10, (B, T, 3, H, D)).astype(np.int64)
+    q = qkv[:, :, 0].transpose(0, 2, 1, 3)            # [B, H, T, D]
+    k = qkv[:, :, 1].transpose(0, 2, 1, 3)
+    want = q @ k.transpose(0, 1, 3, 2)                # [B, H, T, T]
+    st = kd.MatmulStrides()
+    st.a[:] = [T * 3 * C, 3 * C, 1]
+    st.b[:] = [T * 3 * C, 1, 3 * C]
+    st.out[:] = [H * T * T, T, 1]
+    heads = kd.MatmulHeads(H, D, D, T * T)
+    flat = qkv.ravel()
+    out = np.zeros(B * H * T * T, np.int64)
+    assert oracle.oracle_matmul_strided_heads(kd.I64, P(flat), P(flat[C:].copy()), P(out), kd.MatmulSizes(B * H, T, D, T),
+                                              st, heads) == 0
+    np.testing.assert_array_equal(out.reshape(B, H, T, T), want)
+    swapped = kd.MatmulHeads(H, D, D, T * T)
+    swapped.a = 3 * C  # the head stride mistaken for the row stride
+    assert oracle.oracle_matmul_strided_heads(kd.I64, P(flat), P(flat[C:].copy()), P(out), kd.MatmulSizes(B * H, T, D, T),
+                                              st, swapped) == 0
+    assert not np.array_equal(out.reshape(B, H, T, T), want)
+    assert oracle.oracle_matmul_strided_heads(kd.I64, P(flat), P(flat), P(out), kd.MatmulSizes(5, T, D, T), st, heads) != 0

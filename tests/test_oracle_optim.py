@@ -71,9 +71,9 @@ def test_fused_branch_takes_the_entry_point_and_keeps_the_bits(oracle, kael_orac
     fn.restype, fn.argtypes = ctypes.c_longlong, [ctypes.c_int]
     for kind, dtype, wd, n in CASES:
         p0, grads, hyper = case_inputs(kind, dtype, wd, n)
-        before = fn(6) + fn(7)
+        before = fn(7) + fn(14)  # sgd_step, adam_step_many (one call per step for the one parameter)
         got = kael_steps(kael_oracle_fused, kind, 1, dtype, p0, grads, *hyper)
-        assert fn(6) + fn(7) - before == len(grads), (kind, dtype, wd, n)
+        assert fn(7) + fn(14) - before == len(grads), (kind, dtype, wd, n)
         np.testing.assert_array_equal(got, oracle_steps(oracle, kind, dtype, p0, grads, *hyper))
 
 

@@ -113,6 +113,23 @@ def test_reduce_matches_reference_tasks_bit_exact(oracle, refdev, op, dtype, row
     same(a, b, True, "reduce")
 
 
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64, kd.BOOL])
+@pytest.mark.parametrize("op", [kd.REDUCE_SUM, kd.REDUCE_MAX, kd.REDUCE_MIN])
+@pytest.mark.parametrize("outer,inner", [(1, 1), (13, 7), (4096, 5), (4097, 3), (9000, 2), (2, 300)])
+def test_reduce_columns_match_reference_tasks_over_the_transposed_copy(oracle, refdev, op, dtype, outer, inner):
+    """oracle_reduce_columns (kd_reduce_columns' restatement) against what kael does today for a
+    contiguous [outer, inner] tensor reduced over its leading dim: plan_reduction's copy with that
+    dim moved last, then the reference's device reduce tasks with chunk = outer, rows = inner."""
+    rng = np.random.default_rng(outer * 31 + inner + op + dtype)
+    x = random_values(rng, kd.NUMPY_DTYPE[dtype], outer * inner)
+    out_np = np.int64 if (op == kd.REDUCE_SUM and dtype in (kd.I64, kd.BOOL)) else kd.NUMPY_DTYPE[dtype]
+    a, b = np.zeros(inner, out_np), np.zeros(inner, out_np)
+    assert oracle.oracle_reduce_columns(op, 0, dtype, support.ptr(a), support.ptr(x), outer, inner) == 0
+    xt = np.ascontiguousarray(x.reshape(outer, inner).T)
+    assert refdev.ref_dev_reduce(op, 0, dtype, support.ptr(b), support.ptr(xt), outer, inner) == 0
+    same(a, b, True, "reduce_columns")
+
+
 @pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64])
 @pytest.mark.parametrize("b,m,k,n", [(1, 1, 1, 1), (1, 5, 3, 9), (2, 33, 20, 65), (3, 4, 0, 2), (1, 64, 128, 7)])
 def test_matmul_matches_reference_tasks(oracle, refdev, dtype, b, m, k, n):

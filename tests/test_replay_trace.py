@@ -22,7 +22,7 @@ def test_trace_is_well_formed(name):
     assert len(losses) == 2 and all(0 < x < 10 for x in losses)
     ops = {r["op"] for r in steps[-1]}
     assert {"matmul_strided", "cross_entropy_rows", "cross_entropy_grad", "d2h"} <= ops
-    assert ("sgd_step" if name == "c3" else "adam_step") in ops
+    assert ("sgd_step" if name == "c3" else "adam_step_many") in ops
     if name == "c4":
         # the fused row kernels and their backward passes are in the step
         assert {"softmax_rows", "standardize_rows", "softmax_rows_backward", "standardize_rows_backward",
