@@ -359,7 +359,7 @@ def bench_replay(backend, name, steps):
     mm_ms = sum(ms for _, ms in mm)
     # row kernels: algorithmic bytes = the row arrays each one reads and writes once
     arrays = {"softmax_rows": 2, "standardize_rows": 2, "softmax_rows_backward": 3, "standardize_rows_backward": 4,
-              "cross_entropy_rows": 1, "cross_entropy_grad": 2}
+              "cross_entropy_rows": 1, "cross_entropy_grad": 2, "layer_norm_rows": 3, "layer_norm_rows_backward": 4}
     rows = [(r, ms) for r, ms in per_call if r["op"] in arrays]
     row_bytes = sum(arrays[r["op"]] * r["rows"] * r["cols"] * (4 if r["dtype"] == 0 else 8) for r, _ in rows)
     row_ms = sum(ms for _, ms in rows)

@@ -322,6 +322,25 @@ int kd_softmax_rows_backward(int dtype, void* out, const void* y, const void* gr
 int kd_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,
                                  int64_t rows, int64_t cols, double eps);
 
+/* kael's LayerNorm::forward, standardize(x) * weight + bias (reference src/nn/layers.cpp:60-68),
+ * in one launch: `out` as kd_standardize_rows with the affine step, and `standardized` the rows
+ * before it (what kael's standardize returns, which the backward reads). dtype f32 or f64; weight
+ * and bias of length cols. */
+int kd_layer_norm_rows(int dtype, void* out, void* standardized, const void* in, int64_t rows, int64_t cols,
+                       double eps, const void* weight, const void* bias);
+
+/* The backward of kd_layer_norm_rows as kael composes it from AddBackward, MulBackward and
+ * StandardizeBackward (reference src/autograd/functions_math.cpp:54-72,
+ * functions_reduce.cpp:176-192) for the gradient g of `out`, with y the standardized rows:
+ * grad_in = kd_standardize_rows_backward(x, y, g * weight) (each product rounded),
+ * grad_weight[c] = sum over rows of g * y (products rounded, summed in double),
+ * grad_bias[c] = sum over rows of g (in double). Two launches for rows of <= 1024 elements
+ * (cols % 4 == 0, 16-byte aligned) instead of ~9. grad_weight / grad_bias may be NULL (not
+ * computed). dtype f32 or f64; outputs may not alias inputs. */
+int kd_layer_norm_rows_backward(int dtype, void* grad_in, void* grad_weight, void* grad_bias, const void* x,
+                                const void* standardized, const void* grad, const void* weight, int64_t rows,
+                                int64_t cols, double eps);
+
 /* ---- optimizer steps (extensions replacing composed device paths) ------ */
 
 /* One Adam / AdamW step of a contiguous parameter tensor in place, with its first and second

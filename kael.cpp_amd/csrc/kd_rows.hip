@@ -113,8 +113,7 @@ __global__ __launch_bounds__(kThreads) void softmax_wave_kernel(T* __restrict__ 
     }
 }
 
-template <typename T>
-__device__ __forceinline__ T standardized(T x, double center, double scale, const T* w, const T* b, int64_t c);
+template <typename T> __device__ __forceinline__ T affine(T y, const T* w, const T* b, int64_t c);
 
 // ---- vectorized wave-per-row variants (cols % 4 == 0, cols <= 1024) ----------------------------
 //
@@ -205,7 +204,8 @@ __global__ __launch_bounds__(kThreads) void softmax_wave4_kernel(T* __restrict__
 template <typename T, int V4, bool NT>
 __global__ __launch_bounds__(kThreads) void standardize_wave4_kernel(T* __restrict__ out, const T* __restrict__ in,
                                                                      int64_t rows, int64_t cols, double eps,
-                                                                     const T* __restrict__ w, const T* __restrict__ b) {
+                                                                     const T* __restrict__ w, const T* __restrict__ b,
+                                                                     T* __restrict__ yhat) {
     const int lane = threadIdx.x % 64;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
     if (row >= rows) return;
@@ -246,6 +246,7 @@ __global__ __launch_bounds__(kThreads) void standardize_wave4_kernel(T* __restri
             Quad<T> o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) o.v[e] = static_cast<T>((static_cast<double>(v[j].v[e]) - center) * rscale);
+            if (yhat != nullptr) st4<NT>(yhat + row * cols + c, o);
             if (w != nullptr) {
                 const Quad<T> wq = ld4<false>(w + c);
                 const Quad<T> bq = ld4<false>(b + c);
@@ -359,17 +360,16 @@ int softmax_family(T* out, const T* in, const int64_t* targets, const T* weights
 
 // ---- standardize -------------------------------------------------------------------------------------
 
-template <typename T>
-__device__ __forceinline__ T standardized(T x, double center, double scale, const T* w, const T* b, int64_t c) {
-    T y = static_cast<T>((static_cast<double>(x) - center) / scale);
-    if (w != nullptr) y = add_rn(mul_rn(y, w[c]), b[c]);
-    return y;
+// The LayerNorm affine step of a standardized value: y * w[c] + b[c], each op rounded.
+template <typename T> __device__ __forceinline__ T affine(T y, const T* w, const T* b, int64_t c) {
+    return w != nullptr ? add_rn(mul_rn(y, w[c]), b[c]) : y;
 }
 
 template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void standardize_wave_kernel(T* __restrict__ out, const T* __restrict__ in,
                                                                     int64_t rows, int64_t cols, double eps,
-                                                                    const T* __restrict__ w, const T* __restrict__ b) {
+                                                                    const T* __restrict__ w, const T* __restrict__ b,
+                                                                    T* __restrict__ yhat) {
     const int lane = threadIdx.x % 64;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
     if (row >= rows) return;
@@ -397,14 +397,19 @@ __global__ __launch_bounds__(kThreads) void standardize_wave_kernel(T* __restric
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int64_t c = lane + 64 * j;
-        if (c < cols) y[c] = standardized(v[j], center, scale, w, b, c);
+        if (c < cols) {
+            const T s = static_cast<T>((static_cast<double>(v[j]) - center) / scale);
+            if (yhat != nullptr) yhat[row * cols + c] = s;
+            y[c] = affine(s, w, b, c);
+        }
     }
 }
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void standardize_block_kernel(T* __restrict__ out, const T* __restrict__ in,
                                                                      int64_t rows, int64_t cols, double eps,
-                                                                     const T* __restrict__ w, const T* __restrict__ b) {
+                                                                     const T* __restrict__ w, const T* __restrict__ b,
+                                                                     T* __restrict__ yhat) {
     __shared__ double tsum[kThreads / 64];
     for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
         const T* x = in + row * cols;
@@ -418,22 +423,27 @@ __global__ __launch_bounds__(kThreads) void standardize_block_kernel(T* __restri
         }
         const double scale = std::sqrt(block_sum(squares, tsum) / static_cast<double>(cols) + eps);
         T* y = out + row * cols;
-        for (int64_t c = threadIdx.x; c < cols; c += kThreads) y[c] = standardized(x[c], center, scale, w, b, c);
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+            const T s = static_cast<T>((static_cast<double>(x[c]) - center) / scale);
+            if (yhat != nullptr) yhat[row * cols + c] = s;
+            y[c] = affine(s, w, b, c);
+        }
     }
 }
 
 template <typename T>
-int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double eps, const T* w, const T* b) {
+int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double eps, const T* w, const T* b,
+                      T* yhat = nullptr) {
     if (rows == 0 || cols == 0) return KD_OK;
     const dim3 block(kThreads);
     const bool quads = cols % 4 == 0 && cols <= 1024 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
-                       reinterpret_cast<uintptr_t>(out) % 16 == 0;
+                       reinterpret_cast<uintptr_t>(out) % 16 == 0 && reinterpret_cast<uintptr_t>(yhat) % 16 == 0;
     if (quads) {
         const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
         const bool nt = rows * cols * static_cast<int64_t>(sizeof(T)) >= (int64_t{16} << 20);
 #define KD_WAVE4(V4)                                                                                                    \
-    if (nt) hipLaunchKernelGGL((standardize_wave4_kernel<T, V4, true>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b); \
-    else hipLaunchKernelGGL((standardize_wave4_kernel<T, V4, false>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b);
+    if (nt) hipLaunchKernelGGL((standardize_wave4_kernel<T, V4, true>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b, yhat); \
+    else hipLaunchKernelGGL((standardize_wave4_kernel<T, V4, false>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b, yhat);
         if (cols <= 256) { KD_WAVE4(1) }
         else if (cols <= 512) { KD_WAVE4(2) }
         else { KD_WAVE4(4) }
@@ -443,7 +453,7 @@ int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double ep
     }
     if (cols <= 1024) {
         const dim3 grid(static_cast<uint32_t>((rows + 3) / 4));
-#define KD_WAVE(V) hipLaunchKernelGGL((standardize_wave_kernel<T, V>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b)
+#define KD_WAVE(V) hipLaunchKernelGGL((standardize_wave_kernel<T, V>), grid, block, 0, stream(), out, in, rows, cols, eps, w, b, yhat)
         if (cols <= 64) KD_WAVE(1);
         else if (cols <= 128) KD_WAVE(2);
         else if (cols <= 256) KD_WAVE(4);
@@ -453,7 +463,7 @@ int standardize_typed(T* out, const T* in, int64_t rows, int64_t cols, double ep
     } else {
         const int64_t blocks = std::min<int64_t>(rows, int64_t{compute_units()} * 32);
         hipLaunchKernelGGL((standardize_block_kernel<T>), dim3(static_cast<uint32_t>(blocks)), block, 0, stream(), out, in,
-                           rows, cols, eps, w, b);
+                           rows, cols, eps, w, b, yhat);
     }
     KD_LAUNCH_CHECK();
     return KD_OK;
@@ -638,6 +648,295 @@ int row_backward_typed(T* out, const T* x, const T* y, const T* g, int64_t rows,
     return KD_OK;
 }
 
+// ---- LayerNorm backward ---------------------------------------------------------------------------
+//
+// kael's LayerNorm::forward is standardize(x) * w + b (reference src/nn/layers.cpp:60-68); its
+// backward is composed from AddBackward, MulBackward and StandardizeBackward
+// (src/autograd/functions_math.cpp:54-72, functions_reduce.cpp:176-192). With y the standardized
+// rows and g the gradient of the output:
+//   grad_in     = the standardize backward (above) of gy = g * w (each product rounded),
+//   grad_weight = sum over rows of g * y (each product rounded, summed in double),
+//   grad_bias   = sum over rows of g (in double).
+// ln_backward_wave4_kernel does all three in one pass for rows of <= 1024 (cols % 4 == 0): workgroup
+// s takes the rows [s * rs, s * rs + rs), wave w the rows s * rs + w + 4 i in increasing order;
+// each lane keeps the column sums of its columns in registers, the four waves add theirs in LDS in
+// wave order, and the workgroup writes its partials (double) for ln_combine_kernel, which adds the
+// segments in order. Other shapes: ln_backward_block_kernel (a workgroup per row) for grad_in and
+// ln_columns_kernel for the column partials.
+template <typename T, int V4, bool NT>
+__global__ __launch_bounds__(kThreads) void ln_backward_wave4_kernel(T* __restrict__ grad_in, double* __restrict__ pw,
+                                                                     double* __restrict__ pb, const T* __restrict__ xin,
+                                                                     const T* __restrict__ yin, const T* __restrict__ gin,
+                                                                     const T* __restrict__ w, int64_t rows, int64_t cols,
+                                                                     int64_t rows_per_segment, double eps) {
+    constexpr int kWaves = kThreads / 64;
+    __shared__ double lds[kWaves][2][V4 * 4][64];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_segment;
+    const int64_t r1 = std::min<int64_t>(rows, r0 + rows_per_segment);
+    Quad<T> wq[V4];
+    double cw[V4][4], cb[V4][4];
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) wq[j] = ld4<false>(w + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cw[j][e] = cb[j][e] = 0.0;
+    }
+    for (int64_t row = r0 + wave; row < r1; row += kWaves) {
+        const int64_t base = row * cols;
+        Quad<T> x[V4], y[V4], gy[V4];
+        BackSums<T> s;
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+            const int64_t c = 4 * (lane + 64 * j);
+            if (c < cols) {
+                x[j] = ld4<NT>(xin + base + c);
+                y[j] = ld4<NT>(yin + base + c);
+                const Quad<T> g = ld4<NT>(gin + base + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    cw[j][e] += static_cast<double>(mul_rn(g.v[e], y[j].v[e]));
+                    cb[j][e] += static_cast<double>(g.v[e]);
+                    gy[j].v[e] = mul_rn(g.v[e], wq[j].v[e]);
+                    back_accumulate<kStandardizeBack>(s, x[j].v[e], y[j].v[e], gy[j].v[e]);
+                }
+            }
+        }
+        s.s1 = wave_sum(s.s1);
+        s.s2 = wave_sum(s.s2);
+        s.s3 = wave_sum(s.s3);
+        BackScalars<T> k = back_scalars<kStandardizeBack>(s, cols);
+        double squares = 0.0;
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+            const int64_t c = 4 * (lane + 64 * j);
+            if (c < cols) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const T d = sub_rn(x[j].v[e], k.s);
+                    squares += static_cast<double>(mul_rn(d, d));
+                }
+            }
+        }
+        k.scale = back_scale<T>(wave_sum(squares), cols, eps);
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+            const int64_t c = 4 * (lane + 64 * j);
+            if (c < cols) {
+                Quad<T> o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o.v[e] = back_output<kStandardizeBack>(k, y[j].v[e], gy[j].v[e]);
+                st4<NT>(grad_in + base + c, o);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < V4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lds[wave][0][j * 4 + e][lane] = cw[j][e];
+            lds[wave][1][j * 4 + e][lane] = cb[j][e];
+        }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+            const int64_t c = 4 * (lane + 64 * j);
+            if (c < cols) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    double sw = lds[0][0][j * 4 + e][lane], sb = lds[0][1][j * 4 + e][lane];
+#pragma unroll
+                    for (int v = 1; v < kWaves; ++v) {
+                        sw += lds[v][0][j * 4 + e][lane];
+                        sb += lds[v][1][j * 4 + e][lane];
+                    }
+                    pw[blockIdx.x * cols + c + e] = sw;
+                    pb[blockIdx.x * cols + c + e] = sb;
+                }
+            }
+        }
+    }
+}
+
+// grad_in for any row length: a workgroup per row, gy = g * w recomputed in each pass.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_backward_block_kernel(T* __restrict__ grad_in, const T* __restrict__ xin,
+                                                                     const T* __restrict__ yin, const T* __restrict__ gin,
+                                                                     const T* __restrict__ w, int64_t rows, int64_t cols,
+                                                                     double eps) {
+    __shared__ double tsum[kThreads / 64];
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const int64_t base = row * cols;
+        BackSums<T> s;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads)
+            back_accumulate<kStandardizeBack>(s, xin[base + c], yin[base + c], mul_rn(gin[base + c], w[c]));
+        s.s1 = block_sum(s.s1, tsum);
+        s.s2 = block_sum(s.s2, tsum);
+        s.s3 = block_sum(s.s3, tsum);
+        BackScalars<T> k = back_scalars<kStandardizeBack>(s, cols);
+        double squares = 0.0;
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+            const T d = sub_rn(xin[base + c], k.s);
+            squares += static_cast<double>(mul_rn(d, d));
+        }
+        k.scale = back_scale<T>(block_sum(squares, tsum), cols, eps);
+        for (int64_t c = threadIdx.x; c < cols; c += kThreads)
+            grad_in[base + c] = back_output<kStandardizeBack>(k, yin[base + c], mul_rn(gin[base + c], w[c]));
+    }
+}
+
+// Column partials for any shape: workgroup (cb, s) sums the 64 columns [64 cb, 64 cb + 64) over the
+// segment's rows, wave w the contiguous quarter [r0 + w q, r0 + w q + q), the waves in order.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_columns_kernel(double* __restrict__ pw, double* __restrict__ pb,
+                                                              const T* __restrict__ yin, const T* __restrict__ gin,
+                                                              int64_t rows, int64_t cols, int64_t rows_per_segment) {
+    constexpr int kWaves = kThreads / 64;
+    __shared__ double lds[kWaves][2][64];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_segment;
+    const int64_t r1 = std::min<int64_t>(rows, r0 + rows_per_segment);
+    const int64_t q = (r1 - r0 + kWaves - 1) / kWaves;
+    const int64_t w0 = std::min<int64_t>(r1, r0 + wave * q);
+    const int64_t w1 = std::min<int64_t>(r1, w0 + q);
+    double sw = 0.0, sb = 0.0;
+    if (c < cols) {
+        for (int64_t r = w0; r < w1; ++r) {
+            const T g = gin[r * cols + c];
+            sw += static_cast<double>(mul_rn(g, yin[r * cols + c]));
+            sb += static_cast<double>(g);
+        }
+    }
+    lds[wave][0][lane] = sw;
+    lds[wave][1][lane] = sb;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        for (int v = 1; v < kWaves; ++v) {
+            sw += lds[v][0][lane];
+            sb += lds[v][1][lane];
+        }
+        pw[blockIdx.y * cols + c] = sw;
+        pb[blockIdx.y * cols + c] = sb;
+    }
+}
+
+// The weight and bias gradients from the segment partials: 16 waves per 64 columns, wave v adding
+// the contiguous segments [v q, v q + q) (8 loads of each array in flight per lane), the waves in
+// order in LDS, so every column sums its segments in order.
+constexpr int kCombineThreads = 1024;
+template <typename T>
+__global__ __launch_bounds__(kCombineThreads) void ln_combine_kernel(T* __restrict__ grad_w, T* __restrict__ grad_b,
+                                                                     const double* __restrict__ pw,
+                                                                     const double* __restrict__ pb, int64_t segments,
+                                                                     int64_t cols) {
+    constexpr int kWaves = kCombineThreads / 64;
+    constexpr int kBatch = 8;
+    __shared__ double lds[kWaves][2][64];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int64_t q = (segments + kWaves - 1) / kWaves;
+    const int64_t s0 = std::min<int64_t>(segments, wave * q);
+    const int64_t s1 = std::min<int64_t>(segments, s0 + q);
+    double sw = 0.0, sb = 0.0;
+    if (c < cols) {
+        for (int64_t s = s0; s < s1; s += kBatch) {
+            double a[kBatch], b[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s + u < s1) {
+                    a[u] = pw[(s + u) * cols + c];
+                    b[u] = pb[(s + u) * cols + c];
+                }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s + u < s1) {
+                    sw += a[u];
+                    sb += b[u];
+                }
+        }
+    }
+    lds[wave][0][lane] = sw;
+    lds[wave][1][lane] = sb;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        for (int v = 1; v < kWaves; ++v) {
+            sw += lds[v][0][lane];
+            sb += lds[v][1][lane];
+        }
+        if (grad_w != nullptr) grad_w[c] = static_cast<T>(sw);
+        if (grad_b != nullptr) grad_b[c] = static_cast<T>(sb);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void zero_pair_kernel(T* a, T* b, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        if (a != nullptr) a[i] = T(0);
+        if (b != nullptr) b[i] = T(0);
+    }
+}
+
+template <typename T>
+int ln_backward_typed(T* grad_in, T* grad_w, T* grad_b, const T* x, const T* y, const T* g, const T* w, int64_t rows,
+                      int64_t cols, double eps) {
+    const dim3 block(kThreads);
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool quads = cols % 4 == 0 && cols <= 1024 && aligned(grad_in) && aligned(x) && aligned(y) && aligned(g) &&
+                       aligned(w);
+    const bool columns = grad_w != nullptr || grad_b != nullptr;
+    // segments of at least 16 rows, at most 4 per CU
+    const int64_t segments = std::max<int64_t>(1, std::min<int64_t>((rows + 15) / 16, int64_t{compute_units()} * 4));
+    const int64_t rows_per_segment = (rows + segments - 1) / segments;
+    if (segments > 65535) return fail(KD_E_INVALID, "layer norm backward: too many rows");
+    Workspace ws;  // the column partials, held until ln_combine_kernel is enqueued
+    double* pw = nullptr;
+    double* pb = nullptr;
+    if (columns || quads) {
+        if (int rc = workspace(ws, static_cast<size_t>(2 * segments * cols) * sizeof(double))) return rc;
+        pw = static_cast<double*>(ws.ptr);
+        pb = pw + segments * cols;
+    }
+    if (quads) {
+        const bool nt = rows * cols * static_cast<int64_t>(sizeof(T)) >= (int64_t{16} << 20);
+        const dim3 grid(static_cast<uint32_t>(segments));
+#define KD_LN4(V4)                                                                                                      \
+    if (nt) hipLaunchKernelGGL((ln_backward_wave4_kernel<T, V4, true>), grid, block, 0, stream(), grad_in, pw, pb, x, y, g, w, \
+                               rows, cols, rows_per_segment, eps);                                                      \
+    else hipLaunchKernelGGL((ln_backward_wave4_kernel<T, V4, false>), grid, block, 0, stream(), grad_in, pw, pb, x, y, g, w, \
+                            rows, cols, rows_per_segment, eps);
+        if (cols <= 256) { KD_LN4(1) }
+        else if (cols <= 512) { KD_LN4(2) }
+        else { KD_LN4(4) }
+#undef KD_LN4
+        KD_LAUNCH_CHECK();
+    } else {
+        const int64_t blocks = std::min<int64_t>(rows, int64_t{compute_units()} * 32);
+        hipLaunchKernelGGL((ln_backward_block_kernel<T>), dim3(static_cast<uint32_t>(blocks)), block, 0, stream(), grad_in,
+                           x, y, g, w, rows, cols, eps);
+        KD_LAUNCH_CHECK();
+        if (columns) {
+            const int64_t col_blocks = (cols + 63) / 64;
+            if (col_blocks > int64_t{0xffffffff}) return fail(KD_E_INVALID, "layer norm backward: too many columns");
+            hipLaunchKernelGGL((ln_columns_kernel<T>), dim3(static_cast<uint32_t>(col_blocks), static_cast<uint32_t>(segments)),
+                               block, 0, stream(), pw, pb, y, g, rows, cols, rows_per_segment);
+            KD_LAUNCH_CHECK();
+        }
+    }
+    if (columns) {
+        const int64_t col_blocks = (cols + 63) / 64;
+        if (col_blocks > int64_t{0xffffffff}) return fail(KD_E_INVALID, "layer norm backward: too many columns");
+        hipLaunchKernelGGL((ln_combine_kernel<T>), dim3(static_cast<uint32_t>(col_blocks)), dim3(kCombineThreads), 0,
+                           stream(), grad_w, grad_b, static_cast<const double*>(pw), static_cast<const double*>(pb),
+                           segments, cols);
+        KD_LAUNCH_CHECK();
+    }
+    return KD_OK;
+}
+
 int check_rows(int dtype, int64_t rows, int64_t cols) {
     if (dtype != KD_F32 && dtype != KD_F64) return fail(KD_E_INVALID, "row kernel: dtype must be f32 or f64");
     if (rows < 0 || cols < 0) return fail(KD_E_INVALID, "row kernel: negative size");
@@ -716,6 +1015,53 @@ extern "C" int kd_softmax_rows_backward(int dtype, void* out, const void* y, con
     const auto* gg = static_cast<const double*>(grad);
     return log_softmax ? row_backward_typed<double, kLogSoftmaxBack>(o, nullptr, yy, gg, rows, cols, 0.0)
                        : row_backward_typed<double, kSoftmaxBack>(o, nullptr, yy, gg, rows, cols, 0.0);
+}
+
+extern "C" int kd_layer_norm_rows(int dtype, void* out, void* standardized, const void* in, int64_t rows, int64_t cols,
+                                  double eps, const void* weight, const void* bias) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (rows == 0 || cols == 0) return KD_OK;
+    if (out == nullptr || standardized == nullptr || in == nullptr || weight == nullptr || bias == nullptr)
+        return fail(KD_E_INVALID, "kd_layer_norm_rows: null pointer");
+    if (int rc = ensure_device()) return rc;
+    if (dtype == KD_F32)
+        return standardize_typed<float>(static_cast<float*>(out), static_cast<const float*>(in), rows, cols, eps,
+                                        static_cast<const float*>(weight), static_cast<const float*>(bias),
+                                        static_cast<float*>(standardized));
+    return standardize_typed<double>(static_cast<double*>(out), static_cast<const double*>(in), rows, cols, eps,
+                                     static_cast<const double*>(weight), static_cast<const double*>(bias),
+                                     static_cast<double*>(standardized));
+}
+
+extern "C" int kd_layer_norm_rows_backward(int dtype, void* grad_in, void* grad_weight, void* grad_bias, const void* x,
+                                           const void* standardized, const void* grad, const void* weight, int64_t rows,
+                                           int64_t cols, double eps) {
+    if (int rc = check_rows(dtype, rows, cols)) return rc;
+    if (cols == 0) return KD_OK;
+    if (grad_in == nullptr && rows > 0) return fail(KD_E_INVALID, "kd_layer_norm_rows_backward: null grad_in");
+    if (rows > 0 && (x == nullptr || standardized == nullptr || grad == nullptr || weight == nullptr))
+        return fail(KD_E_INVALID, "kd_layer_norm_rows_backward: null input");
+    if (int rc = ensure_device()) return rc;
+    if (rows == 0) {  // the column sums of no rows are zero (a kernel, not a memset: callers may capture this)
+        const dim3 grid(static_cast<uint32_t>(std::min<int64_t>((cols + kThreads - 1) / kThreads, 65535)));
+        if (dtype == KD_F32)
+            hipLaunchKernelGGL((zero_pair_kernel<float>), grid, dim3(kThreads), 0, stream(), static_cast<float*>(grad_weight),
+                               static_cast<float*>(grad_bias), cols);
+        else
+            hipLaunchKernelGGL((zero_pair_kernel<double>), grid, dim3(kThreads), 0, stream(),
+                               static_cast<double*>(grad_weight), static_cast<double*>(grad_bias), cols);
+        KD_LAUNCH_CHECK();
+        return KD_OK;
+    }
+    if (dtype == KD_F32)
+        return ln_backward_typed<float>(static_cast<float*>(grad_in), static_cast<float*>(grad_weight),
+                                        static_cast<float*>(grad_bias), static_cast<const float*>(x),
+                                        static_cast<const float*>(standardized), static_cast<const float*>(grad),
+                                        static_cast<const float*>(weight), rows, cols, eps);
+    return ln_backward_typed<double>(static_cast<double*>(grad_in), static_cast<double*>(grad_weight),
+                                     static_cast<double*>(grad_bias), static_cast<const double*>(x),
+                                     static_cast<const double*>(standardized), static_cast<const double*>(grad),
+                                     static_cast<const double*>(weight), rows, cols, eps);
 }
 
 extern "C" int kd_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,

@@ -149,6 +149,20 @@ void standardize_rows_backward(DType dtype, std::byte* out, const std::byte* x, 
           "standardize_rows_backward");
 }
 
+void layer_norm_rows(DType dtype, std::byte* out, std::byte* standardized, const std::byte* in, std::int64_t rows,
+                     std::int64_t cols, double eps, const std::byte* weight, const std::byte* bias) {
+    check(kd_layer_norm_rows(static_cast<int>(dtype), out, standardized, in, rows, cols, eps, weight, bias),
+          "layer_norm_rows");
+}
+
+void layer_norm_rows_backward(DType dtype, std::byte* grad_in, std::byte* grad_weight, std::byte* grad_bias,
+                              const std::byte* x, const std::byte* standardized, const std::byte* grad,
+                              const std::byte* weight, std::int64_t rows, std::int64_t cols, double eps) {
+    check(kd_layer_norm_rows_backward(static_cast<int>(dtype), grad_in, grad_weight, grad_bias, x, standardized, grad,
+                                      weight, rows, cols, eps),
+          "layer_norm_rows_backward");
+}
+
 ElementOp gelu_backward_op(bool approximate) {
     return static_cast<ElementOp>(approximate ? KD_OP_GELU_TANH_BACKWARD : KD_OP_GELU_EXACT_BACKWARD);
 }

@@ -48,6 +48,18 @@ void softmax_rows_backward(DType dtype, std::byte* out, const std::byte* y, cons
 void standardize_rows_backward(DType dtype, std::byte* out, const std::byte* x, const std::byte* y,
                                const std::byte* grad, std::int64_t rows, std::int64_t cols, double eps);
 
+// LayerNorm::forward in one pass (reference src/nn/layers.cpp:60-68): out = standardized * w + b
+// and the standardized rows themselves, over `rows` contiguous rows of `cols`.
+void layer_norm_rows(DType dtype, std::byte* out, std::byte* standardized, const std::byte* in, std::int64_t rows,
+                     std::int64_t cols, double eps, const std::byte* weight, const std::byte* bias);
+
+// Its backward as kael composes it (AddBackward, MulBackward, StandardizeBackward): grad_in from
+// g * w; grad_weight = column sums of g * standardized, grad_bias = column sums of g (either may be
+// null).
+void layer_norm_rows_backward(DType dtype, std::byte* grad_in, std::byte* grad_weight, std::byte* grad_bias,
+                              const std::byte* x, const std::byte* standardized, const std::byte* grad,
+                              const std::byte* weight, std::int64_t rows, std::int64_t cols, double eps);
+
 // The element op computing grad * d/dx gelu(x) over operands (out, x, grad), tanh form when
 // `approximate` (reference src/autograd/functions_math.cpp:35-46 slopes).
 ElementOp gelu_backward_op(bool approximate);

@@ -125,6 +125,9 @@ SIGNATURES = {
     "softmax_rows_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int]),
     "standardize_rows_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                           c_double]),
+    "layer_norm_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
+    "layer_norm_rows_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                         c_int64, c_int64, c_double]),
     "adam_step": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_double, c_double, c_double,
                           c_double, c_double, c_int, c_int64]),
     "adam_step_many": (c_int, [c_int, POINTER(AdamTensor), c_int64, c_double, c_double, c_double, c_double, c_double,

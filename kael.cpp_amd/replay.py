@@ -75,6 +75,7 @@ POINTERS = {
     "cross_entropy_rows": ("losses", "logits", "targets"), "cross_entropy_grad": ("out", "logits", "targets", "weights"),
     "softmax_rows_backward": ("out", "y", "grad"), "standardize_rows_backward": ("out", "x", "y", "grad"),
     "adam_step": ("p", "g", "m", "v"), "sgd_step": ("p", "g"), "adam_step_many": (),
+    "layer_norm_rows": ("out", "y", "x", "w", "b"), "layer_norm_rows_backward": ("gx", "gw", "gb", "x", "y", "grad", "w"),
 }
 
 
@@ -303,6 +304,14 @@ class Replay:
             a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["x"])), c_void_p(P(r["y"])), c_void_p(P(r["grad"])),
                  r["rows"], r["cols"], r["eps"])
             return (lambda: chk(lib.kd_standardize_rows_backward(*a), "kd_standardize_rows_backward")), None
+        if op == "layer_norm_rows":
+            a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["y"])), c_void_p(P(r["x"])), r["rows"], r["cols"],
+                 r["eps"], c_void_p(P(r["w"])), c_void_p(P(r["b"])))
+            return (lambda: chk(lib.kd_layer_norm_rows(*a), "kd_layer_norm_rows")), None
+        if op == "layer_norm_rows_backward":
+            a = (r["dtype"], c_void_p(P(r["gx"])), c_void_p(P(r["gw"])), c_void_p(P(r["gb"])), c_void_p(P(r["x"])),
+                 c_void_p(P(r["y"])), c_void_p(P(r["grad"])), c_void_p(P(r["w"])), r["rows"], r["cols"], r["eps"])
+            return (lambda: chk(lib.kd_layer_norm_rows_backward(*a), "kd_layer_norm_rows_backward")), None
         if op == "adam_step":
             a = (r["dtype"], c_void_p(P(r["p"])), c_void_p(P(r["g"])), c_void_p(P(r["m"])), c_void_p(P(r["v"])),
                  r["count"], r["lr"], r["b1"], r["b2"], r["eps"], r["wd"], r["decoupled"], r["step"])

@@ -261,6 +261,60 @@ WEIGHT_GRADIENT_BRANCH = """                     if (g.device() != Device::CPU &
                      }
 """
 
+LAYER_NORM_BRANCH = """    if (input.device() != Device::CPU && input.numel() > 0 && is_floating_point(input.dtype()) &&
+        weight_.dtype() == input.dtype() && bias_.dtype() == input.dtype() && weight_.device() == input.device() &&
+        bias_.device() == input.device() && weight_.is_contiguous() && bias_.is_contiguous()) {
+        // MI355X: standardize, * weight and + bias in one launch that also keeps the standardized
+        // rows; one node for the backward of all three (grad_in, and the weight and bias column
+        // sums, in two launches), computed once for the node's three inputs.
+        const std::int64_t cols = numel(normalized_shape_);
+        const std::int64_t rows = input.numel() / cols;
+        const DType dtype = input.dtype();
+        const Tensor x = autograd::without_grad([&] { return input.contiguous(); });
+        const Tensor standardized = empty(input.shape(), dtype, input.device());
+        Tensor out = empty(input.shape(), dtype, input.device());
+        device::layer_norm_rows(dtype, out.device_data(), standardized.device_data(), x.device_data(), rows, cols, eps_,
+                                weight_.device_data(), bias_.device_data());
+        if (autograd::should_record(out, {&input, &weight_, &bias_})) {
+            struct Gradients {
+                std::optional<Tensor> input, weight, bias;
+                int pending = 0;  // node inputs that still have to take their gradient
+                int needed = 0;
+            };
+            auto state = std::make_shared<Gradients>();
+            state->needed = int{input.requires_grad()} + int{weight_.requires_grad()} + int{bias_.requires_grad()};
+            auto take = [state, saved_x = autograd::SavedTensor(x), saved_y = autograd::SavedTensor(standardized),
+                         saved_w = autograd::SavedTensor(weight_), rows, cols, dtype, eps = eps_,
+                         shape = input.shape(), parameter_shape = weight_.shape()](const Tensor& g, int which) {
+                if (state->pending == 0) {
+                    const Tensor gc = g.contiguous();
+                    Tensor grad_in = empty(shape, dtype, g.device());
+                    Tensor grad_w = empty(parameter_shape, dtype, g.device());
+                    Tensor grad_b = empty(parameter_shape, dtype, g.device());
+                    device::layer_norm_rows_backward(dtype, grad_in.device_data(), grad_w.device_data(),
+                                                     grad_b.device_data(), saved_x.get().device_data(),
+                                                     saved_y.get().device_data(), gc.device_data(),
+                                                     saved_w.get().device_data(), rows, cols, eps);
+                    state->input = std::move(grad_in);
+                    state->weight = std::move(grad_w);
+                    state->bias = std::move(grad_b);
+                    state->pending = state->needed;
+                }
+                std::optional<Tensor>& slot = which == 0 ? state->input : which == 1 ? state->weight : state->bias;
+                Tensor result = std::move(*slot);
+                slot.reset();
+                --state->pending;
+                return result;
+            };
+            autograd::set_history(out, "LayerNormBackward", {input, weight_, bias_},
+                                  {[take](const Tensor& g) { return take(g, 0); },
+                                   [take](const Tensor& g) { return take(g, 1); },
+                                   [take](const Tensor& g) { return take(g, 2); }});
+        }
+        return out;
+    }
+"""
+
 MASKED_FILL_BRANCH = """    if (t.device() != Device::CPU && mask.dtype() == DType::Bool &&
         broadcast_shapes(t.shape(), mask.shape()) == t.shape()) {
         // MI355X: one pass out = mask ? value : t into a fresh tensor, instead of a clone of t that
@@ -542,6 +596,12 @@ EDITS = [
      WEIGHT_GRADIENT_BRANCH),
     ("src/ops/indexing.cpp", "Tensor masked_fill(const Tensor& t, const Tensor& mask, Scalar value) {\n", "after",
      MASKED_FILL_BRANCH),
+    ("src/nn/layers.cpp", '#include "kael/ops.h"\n', "after",
+     '#include "kael/autograd/grad_mode.h"\n#include "kael/device_kernels.h"\n\n#include <memory>\n#include <optional>\n\n'
+     '#include "recording.h"\n'),
+    ("src/nn/layers.cpp",
+     "    return kael::standardize(input, static_cast<std::int64_t>(count), eps_) * weight_ + bias_;\n", "before",
+     LAYER_NORM_BRANCH),
     ("src/autograd/node.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/tensor_impl.h"\n'),
     ("src/autograd/node.cpp", "GradientList AccumulateGrad::apply(const Tensor& gradient) {\n", "after",
      ACCUMULATE_BRANCH),

@@ -1149,6 +1149,61 @@ int oracle_standardize_rows_backward(int dtype, void* out, const void* x, const 
     return KD_OK;
 }
 
+/* kd_layer_norm_rows: LayerNorm::forward (src/nn/layers.cpp:60-68), standardize(x) * w + b:
+ * oracle_standardize_rows, then the product and the sum each rounded (kael's two element ops). */
+int oracle_layer_norm_rows(int dtype, void* out, void* standardized, const void* in, int64_t rows, int64_t cols,
+                           double eps, const void* weight, const void* bias) {
+    if (weight == NULL || bias == NULL) return fail("layer norm: weight and bias are required");
+    const int rc = oracle_standardize_rows(dtype, standardized, in, rows, cols, eps, NULL, NULL);
+    if (rc != KD_OK) return rc;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) {
+            if (dtype == KD_F32) {
+                const float t = ((const float*)standardized)[r * cols + c] * ((const float*)weight)[c];
+                ((float*)out)[r * cols + c] = t + ((const float*)bias)[c];
+            } else {
+                const double t = ((const double*)standardized)[r * cols + c] * ((const double*)weight)[c];
+                ((double*)out)[r * cols + c] = t + ((const double*)bias)[c];
+            }
+        }
+    return KD_OK;
+}
+
+/* kd_layer_norm_rows_backward: the backward of LayerNorm::forward as kael composes it from
+ * AddBackward and MulBackward (src/autograd/functions_math.cpp:54-72: the bias gradient is g summed
+ * over the rows, the weight gradient (g * y) summed over the rows, the standardized rows' gradient
+ * g * w) and StandardizeBackward (functions_reduce.cpp:176-192) of g * w; the row sums are
+ * sum_to_shape's device sums (oracle_reduce_columns: the reference's reduce over the transposed
+ * copy). */
+int oracle_layer_norm_rows_backward(int dtype, void* grad_in, void* grad_weight, void* grad_bias, const void* x,
+                                    const void* standardized, const void* grad, const void* weight, int64_t rows,
+                                    int64_t cols, double eps) {
+    if (check_floating(dtype)) return KD_E_INVALID;
+    if (rows < 0 || cols < 0) return fail("layer norm backward: negative size");
+    const size_t n = (size_t)(rows * cols > 0 ? rows * cols : 1);
+    char* gy = (char*)malloc(n * 8);
+    char* gyy = (char*)malloc(n * 8);
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) {
+            const int64_t i = r * cols + c;
+            if (dtype == KD_F32) {
+                ((float*)gy)[i] = ((const float*)grad)[i] * ((const float*)weight)[c];
+                ((float*)gyy)[i] = ((const float*)grad)[i] * ((const float*)standardized)[i];
+            } else {
+                ((double*)gy)[i] = ((const double*)grad)[i] * ((const double*)weight)[c];
+                ((double*)gyy)[i] = ((const double*)grad)[i] * ((const double*)standardized)[i];
+            }
+        }
+    int rc = oracle_standardize_rows_backward(dtype, grad_in, x, standardized, gy, rows, cols, eps);
+    if (rc == KD_OK && grad_weight != NULL)
+        rc = oracle_reduce_columns(KD_REDUCE_SUM, dtype, dtype, grad_weight, gyy, rows, cols);
+    if (rc == KD_OK && grad_bias != NULL)
+        rc = oracle_reduce_columns(KD_REDUCE_SUM, dtype, dtype, grad_bias, grad, rows, cols);
+    free(gy);
+    free(gyy);
+    return rc;
+}
+
 /* ---- optimizer steps: src/optim/optimizer.cpp:60-80 (SGD), :93-120 (AdamBase::update) ------ */
 
 /* Each statement is one of kael's whole-tensor ops, rounded to the element type (ISO C: no

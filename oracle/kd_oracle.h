@@ -53,6 +53,11 @@ int oracle_softmax_rows_backward(int dtype, void* out, const void* y, const void
                                  int64_t cols, int log_softmax);
 int oracle_standardize_rows_backward(int dtype, void* out, const void* x, const void* y, const void* grad,
                                      int64_t rows, int64_t cols, double eps);
+int oracle_layer_norm_rows(int dtype, void* out, void* standardized, const void* in, int64_t rows, int64_t cols,
+                           double eps, const void* weight, const void* bias);
+int oracle_layer_norm_rows_backward(int dtype, void* grad_in, void* grad_weight, void* grad_bias, const void* x,
+                                    const void* standardized, const void* grad, const void* weight, int64_t rows,
+                                    int64_t cols, double eps);
 int oracle_adam_step(int dtype, void* param, const void* grad, void* first, void* second, int64_t count,
                      double learning_rate, double beta1, double beta2, double epsilon, double weight_decay,
                      int decoupled, int64_t step);

@@ -243,8 +243,9 @@ namespace {
 // 0 softmax_rows, 1 standardize_rows, 2 cross_entropy_rows, 3 cross_entropy_grad,
 // 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
 // 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
-// 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads.
-constexpr int kExtensions = 16;
+// 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads, 16 layer_norm_rows,
+// 17 layer_norm_rows_backward.
+constexpr int kExtensions = 18;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -301,6 +302,31 @@ void standardize_rows_backward(DType dtype, std::byte* out, const std::byte* x, 
                                               kv("rows", rows) + "," + kv("cols", cols) + "," + kv("eps", real(eps)));
     check(oracle_standardize_rows_backward(static_cast<int>(dtype), out, x, y, grad, rows, cols, eps),
           "standardize_rows_backward");
+}
+
+void layer_norm_rows(DType dtype, std::byte* out, std::byte* standardized, const std::byte* in, std::int64_t rows,
+                     std::int64_t cols, double eps, const std::byte* weight, const std::byte* bias) {
+    ++g_extension_calls[16];
+    KD_TRACE("layer_norm_rows", kv("dtype", static_cast<int>(dtype)) + "," + kv("out", tp(out)) + "," +
+                                    kv("y", tp(standardized)) + "," + kv("x", tp(in)) + "," + kv("rows", rows) + "," +
+                                    kv("cols", cols) + "," + kv("eps", real(eps)) + "," + kv("w", tp(weight)) + "," +
+                                    kv("b", tp(bias)));
+    check(oracle_layer_norm_rows(static_cast<int>(dtype), out, standardized, in, rows, cols, eps, weight, bias),
+          "layer_norm_rows");
+}
+
+void layer_norm_rows_backward(DType dtype, std::byte* grad_in, std::byte* grad_weight, std::byte* grad_bias,
+                              const std::byte* x, const std::byte* standardized, const std::byte* grad,
+                              const std::byte* weight, std::int64_t rows, std::int64_t cols, double eps) {
+    ++g_extension_calls[17];
+    KD_TRACE("layer_norm_rows_backward", kv("dtype", static_cast<int>(dtype)) + "," + kv("gx", tp(grad_in)) + "," +
+                                             kv("gw", tp(grad_weight)) + "," + kv("gb", tp(grad_bias)) + "," +
+                                             kv("x", tp(x)) + "," + kv("y", tp(standardized)) + "," +
+                                             kv("grad", tp(grad)) + "," + kv("w", tp(weight)) + "," + kv("rows", rows) +
+                                             "," + kv("cols", cols) + "," + kv("eps", real(eps)));
+    check(oracle_layer_norm_rows_backward(static_cast<int>(dtype), grad_in, grad_weight, grad_bias, x, standardized,
+                                          grad, weight, rows, cols, eps),
+          "layer_norm_rows_backward");
 }
 
 ElementOp gelu_backward_op(bool approximate) {

@@ -23,6 +23,7 @@
 
 #include "kael/device_kernels.h"
 #include "kael/kael.h"
+#include "kael/nn/layernorm.h"
 #include "kael/nn/linear.h"
 #include "kael/nn/loss.h"
 #include "kael/nn/activation.h"
@@ -798,6 +799,34 @@ int ref_row_grad(int kind, int device, int dtype, const void* x, const void* g, 
         kael::sum(y * gt).backward();
         copy_out(xt.grad()->cpu(), grad_out);
         if (y_out != nullptr) copy_out(y.detach().cpu(), y_out);
+    });
+}
+
+// kael's LayerNorm module (reference src/nn/layers.cpp:55-68) through its autograd on `device` (0
+// CPU, 1 the linked device backend): weight and bias set from w / b, x [rows, cols] (dtype 0 f32,
+// 1 f64) requires grad, sum(LayerNorm(x) * g).backward(). Writes the output, kael's standardize(x)
+// on the same device (the rows the backward reads), x.grad, weight.grad and bias.grad.
+int ref_layer_norm_grads(int device, int dtype, const void* x, const void* w, const void* b, const void* g, int64_t rows,
+                         int64_t cols, double eps, void* out, void* standardized, void* grad_x, void* grad_w,
+                         void* grad_b) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        const kael::DType dt = dtype == 0 ? kael::DType::F32 : kael::DType::F64;
+        kael::nn::LayerNorm norm({cols}, eps, dt);
+        {
+            const kael::autograd::NoGradGuard guard;
+            for (auto& [name, p] : norm.named_parameters()) p.copy_(host_tensor(name == "weight" ? w : b, {cols}, dt));
+        }
+        norm.to(dev);
+        kael::Tensor xt = host_tensor(x, {rows, cols}, dt).to(dev);
+        xt.requires_grad_(true);
+        const kael::Tensor gt = host_tensor(g, {rows, cols}, dt).to(dev);
+        const kael::Tensor y = norm.forward(xt);
+        kael::sum(y * gt).backward();
+        copy_out(y.detach().cpu(), out);
+        copy_out(kael::autograd::without_grad([&] { return kael::standardize(xt.detach(), 1, eps); }).cpu(), standardized);
+        copy_out(xt.grad()->cpu(), grad_x);
+        for (const auto& [name, p] : norm.named_parameters()) copy_out(p.grad()->cpu(), name == "weight" ? grad_w : grad_b);
     });
 }
 
