@@ -355,7 +355,8 @@ def bench_replay(backend, name, steps):
         per_call.append((r, ms.value))
         lib.kd_event_destroy(e0)
         lib.kd_event_destroy(e1)
-    mm = [(r, ms) for r, ms in per_call if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads")]
+    mm = [(r, ms) for r, ms in per_call
+          if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads", "matmul_strided_bias")]
     mm_ms = sum(ms for _, ms in mm)
     # row kernels: algorithmic bytes = the row arrays each one reads and writes once
     arrays = {"softmax_rows": 2, "standardize_rows": 2, "softmax_rows_backward": 3, "standardize_rows_backward": 4,

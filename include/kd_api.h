@@ -249,6 +249,14 @@ typedef struct kd_matmul_strides {
 int kd_matmul_strided(int dtype, const void* a, const void* b, void* out,
                       const kd_matmul_sizes* sizes, const kd_matmul_strides* strides);
 
+/* kd_matmul_strided followed by kael's Linear bias add (reference src/nn/layers.cpp:42-44:
+ * product + bias, the bias broadcast over the rows): out[b][m][n] = product + bias[n], the sum
+ * rounded once as kael's separate add rounds it (wrapping for i64), in the product's epilogue
+ * instead of a second launch that reads and writes the product again. bias: `columns` contiguous
+ * elements of dtype. */
+int kd_matmul_strided_bias(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                           const kd_matmul_strides* strides, const void* bias);
+
 /* kd_matmul_strided over a two-level batch: batch index i = o * heads + h (sizes->batches a
  * multiple of heads) addresses each operand at o * strides->X[0] + h * heads->X elements. This is
  * how the per-head views of attention (reference src/nn/transformer.cpp:115-136: the [batch,

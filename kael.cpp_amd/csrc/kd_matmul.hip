@@ -22,6 +22,7 @@
 // Every kernel takes per-operand element strides (batch, row, column), which is how
 // kd_matmul_strided reads transposed or batch-broadcast operands in place.
 #include <algorithm>
+#include <type_traits>
 
 #include "kd_internal.h"
 
@@ -41,7 +42,17 @@ struct MatmulArgs {
     Strides3 sa, sb, so;
     int64_t heads = 1;
     int64_t ha = 0, hb = 0, ho = 0;
+    const void* bias = nullptr;  // element n added to column n of every output row (element type)
 };
+
+// out = v, or v + bias[col] rounded once (wrapping for i64): the bias add of kael's Linear
+// (product + bias) as the epilogue of the product that precedes it.
+template <typename T> __device__ __forceinline__ T plus_bias(T v, const void* bias, int64_t col) {
+    if (bias == nullptr) return v;
+    const T b = static_cast<const T*>(bias)[col];
+    if constexpr (std::is_same_v<T, int64_t>) return wrap_add(v, b);
+    else return add_sep(v, b);
+}
 
 // Element offset of batch `batch` in an operand with outer / head strides `outer` / `inner`.
 __host__ __device__ __forceinline__ int64_t batch_offset(const MatmulArgs& p, int64_t batch, int64_t outer,
@@ -58,11 +69,12 @@ struct BatchStrides {
     int64_t a, b, o;
     int64_t ha, hb, ho;
     uint32_t heads;
+    const float* bias;  // the epilogue's bias (null: none; split-K partials never take it)
 };
 
-BatchStrides batch_strides(int64_t a, int64_t b, int64_t o) { return {a, b, o, 0, 0, 0, 1u}; }
+BatchStrides batch_strides(int64_t a, int64_t b, int64_t o) { return {a, b, o, 0, 0, 0, 1u, nullptr}; }
 BatchStrides batch_strides(const MatmulArgs& p) {
-    return {p.sa.b, p.sb.b, p.so.b, p.ha, p.hb, p.ho, static_cast<uint32_t>(p.heads)};
+    return {p.sa.b, p.sb.b, p.so.b, p.ha, p.hb, p.ho, static_cast<uint32_t>(p.heads), static_cast<const float*>(p.bias)};
 }
 
 // Offsets of this workgroup's batch (blockIdx.y) in A, B and the output.
@@ -287,7 +299,7 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t tiles_m, int64_t til
     tn = in_group / rows_in_group;
 }
 
-template <int AMode, int BMode, bool Full>
+template <int AMode, int BMode, bool Full, bool Bias = false>
 __global__ __launch_bounds__(kThreads) void mfma_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                             float* __restrict__ out, MatmulArgs p) {
     __shared__ float As[2][kAsize];
@@ -395,6 +407,11 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_kernel(const float* __restr
         for (int j = 0; j < 2; ++j) {
             const int64_t col = n0 + wn * 64 + j * 32 + li;
             if (!Full && col >= p.N) continue;
+            if constexpr (Bias) {
+                const float bv = static_cast<const float*>(p.bias)[col];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = add_sep(acc[i][j][r], bv);
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * lh + (r % 4);
@@ -540,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_rowmajor_kernel(const float
 // order and results are those of mfma_f32_rowmajor_kernel (bit for bit). `lda` / `ldb` / `ldo`
 // are the strides between consecutive rows of the stored operands: of A's k (AT) or m rows, of
 // B's n (BT) or k rows, of the output's m rows.
-template <bool AT, bool BT>
+template <bool AT, bool BT, bool Bias = false>
 __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* __restrict__ a,
                                                                   const float* __restrict__ b,
                                                                   float* __restrict__ out, int M, int N, int K,
@@ -683,10 +700,14 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* _
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int col = n0 + wn * 64 + j * 32 + li;
+            // the bias variant is its own instantiation: a runtime test here costs the
+            // headline kernel registers (116 -> 164 VGPRs, one wave per SIMD less)
+            const float bv = Bias ? bs.bias[col] : 0.f;
 #pragma unroll
             for (int rr = 0; rr < 16; ++rr) {
                 const int row = m0 + wm * 64 + i * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
-                out[row * ldo + col] = acc[i][j][rr];
+                if constexpr (Bias) out[row * ldo + col] = add_sep(acc[i][j][rr], bv);
+                else out[row * ldo + col] = acc[i][j][rr];
             }
         }
 }
@@ -827,10 +848,19 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
     }
 
     const int col = n0 + wn * 32 + li;
+    if (bs.bias == nullptr) {
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-        const int row = m0 + wm * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
-        out[row * ldo + col] = acc[rr];
+        for (int rr = 0; rr < 16; ++rr) {
+            const int row = m0 + wm * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
+            out[row * ldo + col] = acc[rr];
+        }
+    } else {
+        const float bv = bs.bias[col];
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+            const int row = m0 + wm * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
+            out[row * ldo + col] = add_sep(acc[rr], bv);
+        }
     }
 }
 
@@ -913,7 +943,8 @@ __global__ __launch_bounds__(kSmallWaves * 64) void small_kernel(const float* __
         const int l = e % 64;
         const int64_t row = m0 + 8 * (r / 4) + 4 * (l / 32) + (r % 4);
         const int64_t col = n0 + l % 32;
-        if (row < p.M && col < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + row * p.so.r + col * p.so.c] = v;
+        if (row < p.M && col < p.N)
+            out[batch_offset(p, batch, p.so.b, p.ho) + row * p.so.r + col * p.so.c] = plus_bias(v, p.bias, col);
     }
 }
 
@@ -980,7 +1011,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const float* __restric
         if (partial != nullptr) {
             partial[((batch * gridDim.y + blockIdx.y) * p.M + m) * p.N + n] = v;
         } else {
-            out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = v;
+            out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = plus_bias(v, p.bias, n);
         }
     }
 }
@@ -1009,7 +1040,7 @@ __global__ __launch_bounds__(kThreads) void split_sum_kernel(const float* __rest
         }
         const int64_t m = mn / p.N;
         const int64_t n = mn % p.N;
-        out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = v;
+        out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = plus_bias(v, p.bias, n);
     }
 }
 
@@ -1064,7 +1095,7 @@ __global__ __launch_bounds__(kThreads) void rowdot_kernel(const float* __restric
     if (lane == 0) {
 #pragma unroll
         for (int n = 0; n < kRowdotMaxN; ++n)
-            if (n < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = acc[n];
+            if (n < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = plus_bias(acc[n], p.bias, n);
     }
 }
 
@@ -1128,7 +1159,7 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(const T* __restrict__ a
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t n = n0 + tc + 16 * j;
-            if (n < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = acc[i][j];
+            if (n < p.N) out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = plus_bias(acc[i][j], p.bias, n);
         }
     }
 }
@@ -1251,10 +1282,16 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             // transposed-operand family (waves 0-1 load A, waves 2-3 load B, four 16-byte loads
             // each), which measured ~1 % faster than mfma_f32_rowmajor_kernel at 4096^3 with
             // bit-identical results. The bounds checked above cover its 32-bit offsets.
-            hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false>), grid, dim3(kThreads), 0, stream(), a, b, out,
-                               static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                               static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r),
-                               batch_strides(p));
+            if (p.bias != nullptr)
+                hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false, true>), grid, dim3(kThreads), 0, stream(), a, b,
+                                   out, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
+                                   static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r),
+                                   batch_strides(p));
+            else
+                hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false>), grid, dim3(kThreads), 0, stream(), a, b, out,
+                                   static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
+                                   static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r),
+                                   batch_strides(p));
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
@@ -1308,21 +1345,31 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                     }
                 }
             }
-            hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>), grid, dim3(kThreads), 0, stream(), a, b, out,
-                               static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                               static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
-                               batch_strides(p));
+            if (p.bias != nullptr)
+                hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt, true>), grid, dim3(kThreads), 0, stream(), a, b, out,
+                                   static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
+                                   static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
+                                   batch_strides(p));
+            else
+                hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>), grid, dim3(kThreads), 0, stream(), a, b, out,
+                                   static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
+                                   static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
+                                   batch_strides(p));
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
     }
     bool full = false;
     if constexpr (AMode != kGeneric && BMode != kGeneric) full = p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0;
+    const bool bias = p.bias != nullptr;
     if (full) {
-        if constexpr (AMode != kGeneric && BMode != kGeneric)
-            hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+        if constexpr (AMode != kGeneric && BMode != kGeneric) {
+            if (bias) hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, true, true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+            else hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+        }
     } else {
-        hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, false>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+        if (bias) hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, false, true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+        else hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, false>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
     }
     KD_LAUNCH_CHECK();
     return KD_OK;
@@ -1434,7 +1481,7 @@ __global__ __launch_bounds__(kThreads) void zero_kernel(T* out, MatmulArgs p) {
         const int64_t batch = idx / (p.M * p.N);
         const int64_t m = (idx / p.N) % p.M;
         const int64_t n = idx % p.N;
-        out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = T(0);
+        out[batch_offset(p, batch, p.so.b, p.ho) + m * p.so.r + n * p.so.c] = plus_bias(T(0), p.bias, n);
     }
 }
 
@@ -1492,6 +1539,23 @@ extern "C" int kd_matmul_strided(int dtype, const void* a, const void* b, void* 
     p.sa = {strides->a[0], strides->a[1], strides->a[2]};
     p.sb = {strides->b[0], strides->b[1], strides->b[2]};
     p.so = {strides->out[0], strides->out[1], strides->out[2]};
+    return dispatch(dtype, a, b, out, p);
+}
+
+extern "C" int kd_matmul_strided_bias(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                                      const kd_matmul_strides* strides, const void* bias) {
+    if (sizes == nullptr || strides == nullptr) return fail(KD_E_INVALID, "kd_matmul_strided_bias: null argument");
+    if (bias == nullptr && sizes->batches > 0 && sizes->rows > 0 && sizes->columns > 0)
+        return fail(KD_E_INVALID, "kd_matmul_strided_bias: null bias");
+    MatmulArgs p;
+    p.batches = sizes->batches;
+    p.M = sizes->rows;
+    p.K = sizes->inner;
+    p.N = sizes->columns;
+    p.sa = {strides->a[0], strides->a[1], strides->a[2]};
+    p.sb = {strides->b[0], strides->b[1], strides->b[2]};
+    p.so = {strides->out[0], strides->out[1], strides->out[2]};
+    p.bias = bias;
     return dispatch(dtype, a, b, out, p);
 }
 

@@ -179,6 +179,19 @@ void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::by
     check(kd_matmul_strided(static_cast<int>(dtype), a, b, out, &s, &st), "matmul_strided");
 }
 
+void matmul_strided_bias(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
+                         const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
+                         const std::byte* bias) {
+    const kd_matmul_sizes s{sizes.batches, sizes.rows, sizes.inner, sizes.columns};
+    kd_matmul_strides st;
+    for (int i = 0; i < 3; ++i) {
+        st.a[i] = a_strides[i];
+        st.b[i] = b_strides[i];
+        st.out[i] = out_strides[i];
+    }
+    check(kd_matmul_strided_bias(static_cast<int>(dtype), a, b, out, &s, &st, bias), "matmul_strided_bias");
+}
+
 void matmul_strided_heads(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
                           const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
                           std::int64_t heads, const std::int64_t* head_strides) {

@@ -69,6 +69,12 @@ ElementOp gelu_backward_op(bool approximate);
 void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
                     const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides);
 
+// matmul_strided with kael's Linear bias add in the product's epilogue: out = product + bias[n]
+// (reference src/nn/layers.cpp:42-44), the sum rounded once.
+void matmul_strided_bias(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& sizes,
+                         const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
+                         const std::byte* bias);
+
 // matmul_strided over a two-level batch: batch i = o * heads + h reads operand X at
 // o * X_strides[0] + h * head_strides[X] (X = a, b, out), for the per-head attention views whose
 // batch dims collapse to no single stride (reference src/nn/transformer.cpp:115-136).

@@ -134,6 +134,8 @@ SIGNATURES = {
                                c_int]),
     "sgd_step": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_double, c_double]),
     "matmul_strided": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides)]),
+    "matmul_strided_bias": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides),
+                                    c_void_p]),
     "matmul_strided_heads": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(MatmulSizes), POINTER(MatmulStrides),
                                      POINTER(MatmulHeads)]),
     "layout_build": (c_int, [POINTER(ElementLayout), c_int, POINTER(c_int), POINTER(c_int64),

@@ -61,7 +61,7 @@ def traced_losses(records: list[dict]) -> list[float]:
 
 def matmul_flops(records: list[dict]) -> int:
     return sum(2 * r["sizes"][0] * r["sizes"][1] * r["sizes"][2] * r["sizes"][3]
-               for r in records if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads"))
+               for r in records if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads", "matmul_strided_bias"))
 
 
 # pointer fields of each record kind (the layout bases of convert / elementwise are checked apart)
@@ -70,6 +70,7 @@ POINTERS = {
     "reduce": ("results", "data"), "reduce_columns": ("results", "data"), "arg_reduce": ("results", "data"),
     "cumsum": ("out", "data"),
     "matmul": ("a", "b", "c"), "matmul_strided": ("a", "b", "c"), "matmul_strided_heads": ("a", "b", "c"),
+    "matmul_strided_bias": ("a", "b", "c", "bias"),
     "gather": ("out", "data", "indices"),
     "scatter_add": ("data", "indices", "source"), "softmax_rows": ("out", "x"), "standardize_rows": ("out", "x"),
     "cross_entropy_rows": ("losses", "logits", "targets"), "cross_entropy_grad": ("out", "logits", "targets", "weights"),
@@ -241,7 +242,7 @@ class Replay:
         if op == "cumsum":
             a = (r["in"], c_void_p(P(r["out"])), c_void_p(P(r["data"])), r["size"], r["rows"])
             return (lambda: chk(lib.kd_cumsum(*a), "kd_cumsum")), None
-        if op in ("matmul", "matmul_strided", "matmul_strided_heads"):
+        if op in ("matmul", "matmul_strided", "matmul_strided_heads", "matmul_strided_bias"):
             sizes = kd.MatmulSizes(*r["sizes"])
             a, b, c = c_void_p(P(r["a"])), c_void_p(P(r["b"])), c_void_p(P(r["c"]))
             if op == "matmul":
@@ -249,6 +250,10 @@ class Replay:
             st = kd.MatmulStrides()
             for i in range(3):
                 st.a[i], st.b[i], st.out[i] = r["sa"][i], r["sb"][i], r["sc"][i]
+            if op == "matmul_strided_bias":
+                bias = c_void_p(P(r["bias"]))
+                return (lambda: chk(lib.kd_matmul_strided_bias(r["dtype"], a, b, c, byref(sizes), byref(st), bias),
+                                    "kd_matmul_strided_bias")), None
             if op == "matmul_strided_heads":
                 h = kd.MatmulHeads(*r["heads"])
                 return (lambda: chk(lib.kd_matmul_strided_heads(r["dtype"], a, b, c, byref(sizes), byref(st), byref(h)),

@@ -261,6 +261,36 @@ WEIGHT_GRADIENT_BRANCH = """                     if (g.device() != Device::CPU &
                      }
 """
 
+LINEAR_BRANCH = """    if (bias_ && input.device() != Device::CPU && input.dim() >= 2 && is_floating_point(input.dtype()) &&
+        input.is_contiguous() && weight_.dim() == 2 && weight_.is_contiguous() && input.size(-1) == weight_.size(1) &&
+        weight_.dtype() == input.dtype() && bias_->dtype() == input.dtype() && bias_->is_contiguous() &&
+        weight_.device() == input.device() && bias_->device() == input.device()) {
+        // MI355X: matmul(input, weight.T()) + bias with the add as the product's epilogue, over the
+        // same batched operands as the matmul device branch (so the same kernel and the same
+        // product bits), one launch instead of two. The graph is the composed one: a stand-in for
+        // the product (MatmulBackward and AddBackward read neither the product nor the sum).
+        const Tensor weight_t = weight_.T();
+        const std::int64_t inner = input.size(-1);
+        const std::int64_t rows = input.size(-2);
+        const std::int64_t columns = weight_.size(0);
+        Shape shape(input.shape().begin(), input.shape().end() - 1);
+        shape.push_back(columns);
+        const std::int64_t batches = input.numel() / std::max<std::int64_t>(1, rows * inner);
+        Tensor out = empty(shape, input.dtype(), input.device());
+        const std::int64_t sa[3] = {rows * inner, inner, 1};
+        const std::int64_t sb[3] = {0, 1, inner};
+        const std::int64_t so[3] = {rows * columns, columns, 1};
+        device::matmul_strided_bias(input.dtype(), input.device_data(), weight_t.device_data(), out.device_data(),
+                                    {batches, rows, inner, columns}, sa, sb, so, bias_->device_data());
+        if (autograd::should_record(out, {&input, &weight_t, &*bias_})) {
+            const Tensor product = out.detach();
+            autograd::record_matmul(product, input, weight_t);
+            autograd::record_add(out, product, *bias_);
+        }
+        return out;
+    }
+"""
+
 LAYER_NORM_BRANCH = """    if (input.device() != Device::CPU && input.numel() > 0 && is_floating_point(input.dtype()) &&
         weight_.dtype() == input.dtype() && bias_.dtype() == input.dtype() && weight_.device() == input.device() &&
         bias_.device() == input.device() && weight_.is_contiguous() && bias_.is_contiguous()) {
@@ -598,7 +628,8 @@ EDITS = [
      MASKED_FILL_BRANCH),
     ("src/nn/layers.cpp", '#include "kael/ops.h"\n', "after",
      '#include "kael/autograd/grad_mode.h"\n#include "kael/device_kernels.h"\n\n#include <memory>\n#include <optional>\n\n'
-     '#include "recording.h"\n'),
+     '#include "record.h"\n#include "recording.h"\n'),
+    ("src/nn/layers.cpp", "    const Tensor product = matmul(input, weight_.T());\n", "before", LINEAR_BRANCH),
     ("src/nn/layers.cpp",
      "    return kael::standardize(input, static_cast<std::int64_t>(count), eps_) * weight_ + bias_;\n", "before",
      LAYER_NORM_BRANCH),

@@ -837,6 +837,23 @@ int oracle_matmul_strided(int dtype, const void* a, const void* b, void* out,
     return KD_OK;
 }
 
+/* kd_matmul_strided_bias: oracle_matmul_strided, then kael's `product + bias` (src/nn/layers.cpp:42-44)
+ * as a separate rounded add per element (wrapping for i64). */
+int oracle_matmul_strided_bias(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,
+                               const kd_matmul_strides* t, const void* bias) {
+    const int rc = oracle_matmul_strided(dtype, a, b, out, s, t);
+    if (rc != KD_OK) return rc;
+    for (int64_t bt = 0; bt < s->batches; ++bt)
+        for (int64_t i = 0; i < s->rows; ++i)
+            for (int64_t j = 0; j < s->columns; ++j) {
+                const int64_t o = bt * t->out[0] + i * t->out[1] + j * t->out[2];
+                if (dtype == KD_F32) ((float*)out)[o] = ((float*)out)[o] + ((const float*)bias)[j];
+                else if (dtype == KD_F64) ((double*)out)[o] = ((double*)out)[o] + ((const double*)bias)[j];
+                else ((int64_t*)out)[o] = wadd(((int64_t*)out)[o], ((const int64_t*)bias)[j]);
+            }
+    return KD_OK;
+}
+
 /* kd_matmul_strided_heads: batch i = o * heads + h at o * strides->X[0] + h * heads->X, i.e.
  * oracle_matmul_strided over the `heads` batches of each outer index o. */
 int oracle_matmul_strided_heads(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,

@@ -35,6 +35,8 @@ int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_m
                   int exact);
 int oracle_matmul_strided(int dtype, const void* a, const void* b, void* out,
                           const kd_matmul_sizes* sizes, const kd_matmul_strides* strides);
+int oracle_matmul_strided_bias(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
+                               const kd_matmul_strides* strides, const void* bias);
 int oracle_matmul_strided_heads(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,
                                 const kd_matmul_strides* strides, const kd_matmul_heads* heads);
 int oracle_gather(int dtype, void* out, const void* data, const int64_t* indices,

@@ -244,8 +244,8 @@ namespace {
 // 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
 // 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
 // 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads, 16 layer_norm_rows,
-// 17 layer_norm_rows_backward.
-constexpr int kExtensions = 18;
+// 17 layer_norm_rows_backward, 18 matmul_strided_bias.
+constexpr int kExtensions = 19;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -348,6 +348,24 @@ void matmul_strided(DType dtype, const std::byte* a, const std::byte* b, std::by
                                    kv("c", tp(out)) + "," + kv("sizes", ints(&sizes.batches, 4)) + "," + kv("sa", ints(st.a, 3)) +
                                    "," + kv("sb", ints(st.b, 3)) + "," + kv("sc", ints(st.out, 3)));
     check(oracle_matmul_strided(static_cast<int>(dtype), a, b, out, &sizes, &st), "matmul_strided");
+}
+
+void matmul_strided_bias(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& s,
+                         const std::int64_t* a_strides, const std::int64_t* b_strides, const std::int64_t* out_strides,
+                         const std::byte* bias) {
+    ++g_extension_calls[18];
+    const kd_matmul_sizes sizes{s.batches, s.rows, s.inner, s.columns};
+    kd_matmul_strides st;
+    for (int i = 0; i < 3; ++i) {
+        st.a[i] = a_strides[i];
+        st.b[i] = b_strides[i];
+        st.out[i] = out_strides[i];
+    }
+    KD_TRACE("matmul_strided_bias", kv("dtype", static_cast<int>(dtype)) + "," + kv("a", tp(a)) + "," + kv("b", tp(b)) +
+                                        "," + kv("c", tp(out)) + "," + kv("sizes", ints(&sizes.batches, 4)) + "," +
+                                        kv("sa", ints(st.a, 3)) + "," + kv("sb", ints(st.b, 3)) + "," +
+                                        kv("sc", ints(st.out, 3)) + "," + kv("bias", tp(bias)));
+    check(oracle_matmul_strided_bias(static_cast<int>(dtype), a, b, out, &sizes, &st, bias), "matmul_strided_bias");
 }
 
 void matmul_strided_heads(DType dtype, const std::byte* a, const std::byte* b, std::byte* out, const MatmulSizes& s,

@@ -467,3 +467,65 @@ def test_two_level_batches_reject_bad_heads(kdb):
         with pytest.raises(kd.KdError):
             kdb.call("matmul_strided_heads", kd.F32, x.ptr, x.ptr, x.ptr, kd.MatmulSizes(batches, 2, 2, 2), strides,
                      kd.MatmulHeads(heads, 8, 8, 8))
+
+
+BIAS_CASES = [  # batches, m, k, n, a strides, b strides: kael's x . W^T shapes and every kernel family
+    (32, 128, 256, 768, (128 * 256, 256, 1), (0, 1, 256)),      # t64 folded (C4 qkv)
+    (32, 128, 256, 1024, (128 * 256, 256, 1), (0, 1, 256)),     # 128x128 transposed-B kernel (C4 fc1)
+    (1, 4096, 4096, 256, (0, 4096, 1), (0, 1, 4096)),           # split K
+    (1, 512, 512, 512, (0, 512, 1), (0, 512, 1)),               # row-major whole tiles / small kernel
+    (1, 3, 768, 2304, (0, 768, 1), (0, 1, 768)),                # skinny (decode-shaped)
+    (1, 64, 784, 128, (0, 784, 1), (0, 1, 784)),                # C3's first Linear
+    (2, 33, 17, 3, (17 * 33, 17, 1), (0, 1, 17)),               # row-dot
+    (2, 130, 70, 200, (130 * 70, 70, 1), (0, 1, 70)),           # ragged tiles, general kernel
+]
+
+
+@pytest.mark.parametrize("dtype", [kd.F32, kd.F64, kd.I64], ids=["f32", "f64", "i64"])
+@pytest.mark.parametrize("case", BIAS_CASES, ids=[f"{c[0]}x{c[1]}x{c[2]}x{c[3]}" for c in BIAS_CASES])
+def test_bias_epilogue_equals_product_then_add(kdb, oracle, dtype, case):
+    """kd_matmul_strided_bias against kd_matmul_strided followed by a separate add of the bias
+    broadcast over the rows (kael's product + bias): the same bits, since the product is the same
+    kernel and the epilogue rounds the sum once; against the oracle within the device tolerance
+    (exact for i64)."""
+    batches, m, k, n, sa, sb = case
+    if dtype != kd.F32 and m * n * k * batches > (1 << 28):
+        pytest.skip("large shapes run for f32 only")
+    npd = kd.NUMPY_DTYPE[dtype]
+    rng = np.random.default_rng(batches * 3 + m + n)
+
+    def extent(shape, st):
+        return 1 + sum((s - 1) * t for s, t in zip(shape, st))
+
+    if dtype == kd.I64:
+        a_store = rng.integers(-9, 10, extent((batches, m, k), sa)).astype(npd)
+        b_store = rng.integers(-9, 10, extent((batches, k, n), sb)).astype(npd)
+        bias = rng.integers(-50, 50, n).astype(npd)
+    else:
+        a_store = rng.uniform(-1, 1, extent((batches, m, k), sa)).astype(npd)
+        b_store = rng.uniform(-1, 1, extent((batches, k, n), sb)).astype(npd)
+        bias = rng.uniform(-1, 1, n).astype(npd)
+        bias[0] = -0.0
+    so = (m * n, n, 1)
+    strides = kd.MatmulStrides()
+    for i in range(3):
+        strides.a[i], strides.b[i], strides.out[i] = sa[i], sb[i], so[i]
+    sizes = kd.MatmulSizes(batches, m, k, n)
+    da, db, dbias = kdb.to_device(a_store), kdb.to_device(b_store), kdb.to_device(bias)
+    fused, plain = kdb.empty((batches, m, n), npd), kdb.empty((batches, m, n), npd)
+    kdb.call("matmul_strided_bias", dtype, da.ptr, db.ptr, fused.ptr, sizes, strides, dbias.ptr)
+    kdb.call("matmul_strided", dtype, da.ptr, db.ptr, plain.ptr, sizes, strides)
+    p = plain.numpy()
+    if dtype == kd.I64:
+        want_sum = (p.view(np.uint64) + bias.view(np.uint64)).view(np.int64)
+    else:
+        want_sum = p + bias  # one rounded add per element, as kael's add kernel
+    got = fused.numpy()
+    np.testing.assert_array_equal(got, want_sum)
+    want = np.empty((batches, m, n), npd)
+    assert oracle.oracle_matmul_strided_bias(dtype, support.ptr(a_store), support.ptr(b_store), support.ptr(want), sizes,
+                                             strides, support.ptr(bias)) == 0
+    if dtype == kd.I64:
+        np.testing.assert_array_equal(got, want)
+    else:
+        close(got, want.astype(np.float64))
