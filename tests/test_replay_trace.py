@@ -24,9 +24,10 @@ def test_trace_is_well_formed(name):
     assert {"matmul_strided", "cross_entropy_rows", "cross_entropy_grad", "d2h"} <= ops
     assert ("sgd_step" if name == "c3" else "adam_step_many") in ops
     if name == "c4":
-        # the fused row kernels and their backward passes are in the step
-        assert {"softmax_rows", "standardize_rows", "softmax_rows_backward", "standardize_rows_backward",
-                "gather", "scatter_add"} <= ops
+        # the fused row kernels and their backward passes, the per-head attention products, the
+        # Linear products with their bias and the column sums are in the step
+        assert {"softmax_rows", "layer_norm_rows", "softmax_rows_backward", "layer_norm_rows_backward",
+                "matmul_strided_heads", "matmul_strided_bias", "reduce_columns", "gather", "scatter_add"} <= ops
     # the step's products: C3 has 3 (forward 2, backward 3 minus the input gradient), C4 dozens
     assert replay.matmul_flops(steps[-1]) > (1e7 if name == "c3" else 1e10)
 
