@@ -17,7 +17,7 @@ The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only matmul|c1|c2|rows|train|c3|c4|gpt2|copy]
+                       [--only matmul|c1|f64|c2|rows|train|c3|c4|gpt2|copy]
 """
 from __future__ import annotations
 
@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT / "kael.cpp_amd"))
 import kd  # noqa: E402
 
 FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense FP32 matrix (AMD spec)
+FP64_MFMA_PEAK_TFLOPS = 78.6    # MI355X dense FP64 matrix (AMD spec)
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
 # HBM bytes one 4096^3 launch of the headline kernel (mfma_f32_trans_kernel<false,false>) moves,
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (199 435 KiB and 65 536 KiB per dispatch), scaled
@@ -94,16 +95,17 @@ def time_steps(backend, step, steps, warmup, min_warmup_s=0.0):
     return t.ms / steps, wall
 
 
-def bench_matmul(backend, n, steps, warmup, seed=0, min_warmup_s=0.0):
+def bench_matmul(backend, n, steps, warmup, seed=0, min_warmup_s=0.0, dtype=kd.F32):
     rng = np.random.default_rng(seed)
-    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
-    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
-    da, db, dc = backend.to_device(a), backend.to_device(b), backend.empty((n, n), np.float32)
+    npd = kd.NUMPY_DTYPE[dtype]
+    a = rng.uniform(-1, 1, (n, n)).astype(npd)
+    b = rng.uniform(-1, 1, (n, n)).astype(npd)
+    da, db, dc = backend.to_device(a), backend.to_device(b), backend.empty((n, n), npd)
     sizes = kd.MatmulSizes(1, n, n, n)
     fn = backend.lib.kd_matmul
 
     def step(_):
-        rc = fn(kd.F32, da.ptr, db.ptr, dc.ptr, sizes)
+        rc = fn(dtype, da.ptr, db.ptr, dc.ptr, sizes)
         if rc:
             backend.check(rc, "kd_matmul")
 
@@ -490,7 +492,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
-    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "copy", "c2", "rows", "train", "c3", "c4",
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "f64", "copy", "c2", "rows", "train", "c3", "c4",
                                                   "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
@@ -510,6 +512,12 @@ def main() -> int:
     if args.only == "gpt2":
         extra["gpt2_decode"] = bench_gpt2(backend, eager=args.gpt_eager)
         print(json.dumps({"metric": "GPT-2-small decode tok/s", "extra": extra}))
+        return 0
+    if args.only == "f64":
+        f64 = bench_matmul(backend, n, max(args.steps, 10), args.warmup, min_warmup_s=MIN_WARMUP_S, dtype=kd.F64)
+        f64["frac_of_fp64_matrix_peak"] = f64["tflops"] / FP64_MFMA_PEAK_TFLOPS
+        extra[f"matmul_f64_{n}"] = f64
+        print(json.dumps({"metric": "f64 matmul 4096^3", "extra": extra}))
         return 0
     if args.only == "c1":
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
@@ -536,6 +544,9 @@ def main() -> int:
     main_run = bench_matmul(backend, n, args.steps, args.warmup, min_warmup_s=HEADLINE_WARMUP_S)
     if args.only in ("", "all"):
         extra["matmul_512"] = bench_matmul(backend, 512, max(args.steps, 50), args.warmup, min_warmup_s=MIN_WARMUP_S)
+        f64 = bench_matmul(backend, n, max(args.steps, 10), args.warmup, min_warmup_s=MIN_WARMUP_S, dtype=kd.F64)
+        f64["frac_of_fp64_matrix_peak"] = f64["tflops"] / FP64_MFMA_PEAK_TFLOPS
+        extra[f"matmul_f64_{n}"] = f64
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
         extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
         extra["train"] = bench_train(backend, max(args.steps, 20), args.warmup)

@@ -1463,6 +1463,121 @@ int matmul_f32(const float* a, const float* b, float* out, const MatmulArgs& p) 
     }
 }
 
+// ---- f64 on the FP64 matrix cores ------------------------------------------------------------
+//
+// 64x64 output tiles, four waves each a 2x2 grid of 16x16 v_mfma_f64_16x16x4f64 accumulators;
+// K advances 16 at a time through double-buffered LDS, the next stage's elements in registers
+// while the current one multiplies. Any operand strides (each thread loads 4 elements of A and 4
+// of B per stage, one at a time), batches with one or two stride levels, the bias epilogue; Full
+// drops the bounds checks for whole tiles. Lane layout of the 16x16x4 f64 MFMA (measured with
+// random operands on gfx950): A[i][k] and B[k][j] come from lane i + 16 k (j + 16 k), and
+// register r of lane l holds D[l / 16 + 4 r][l % 16].
+constexpr int kD = 64;
+constexpr int kDK = 16;
+constexpr int kDAld = kDK + 1;  // A tile [m][k]: odd stride, the 16 rows a wave reads spread over the banks
+constexpr int kDBld = kD + 1;   // B tile [k][n]
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+template <bool Full>
+__global__ __launch_bounds__(kThreads) void mfma_f64_kernel(const double* __restrict__ a, const double* __restrict__ b,
+                                                            double* __restrict__ out, MatmulArgs p) {
+    __shared__ double As[2][kD * kDAld];
+    __shared__ double Bs[2][kDK * kDBld];
+    const int64_t tiles_m = (p.M + kD - 1) / kD;
+    const int64_t tiles_n = (p.N + kD - 1) / kD;
+    int64_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t batch = blockIdx.y;
+    const int64_t m0 = tm * kD;
+    const int64_t n0 = tn * kD;
+    a += batch_offset(p, batch, p.sa.b, p.ha);
+    b += batch_offset(p, batch, p.sb.b, p.hb);
+    out += batch_offset(p, batch, p.so.b, p.ho);
+
+    const int t = threadIdx.x;
+    const int lane = t % 64;
+    const int wave = t / 64;
+    const int wm = wave / 2;
+    const int wn = wave % 2;
+    const int li = lane % 16;
+    const int lk = lane / 16;
+
+    v4d acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+
+    double ra[4], rb[4];
+    const auto fetch = [&](int64_t k0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = t + kThreads * e;
+            const int64_t m = m0 + idx / kDK, ka = k0 + idx % kDK;
+            ra[e] = (Full || (m < p.M && ka < p.K)) ? a[m * p.sa.r + ka * p.sa.c] : 0.0;
+            const int64_t kb = k0 + idx / kD, n = n0 + idx % kD;
+            rb[e] = (Full || (kb < p.K && n < p.N)) ? b[kb * p.sb.r + n * p.sb.c] : 0.0;
+        }
+    };
+    const auto stash = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = t + kThreads * e;
+            As[buf][(idx / kDK) * kDAld + idx % kDK] = ra[e];
+            Bs[buf][(idx / kD) * kDBld + idx % kD] = rb[e];
+        }
+    };
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    const int64_t ksteps = (p.K + kDK - 1) / kDK;
+    for (int64_t ks = 0; ks < ksteps; ++ks) {
+        const int cur = static_cast<int>(ks & 1);
+        const bool more = ks + 1 < ksteps;
+        if (more) fetch((ks + 1) * kDK);
+        const double* as = As[cur];
+        const double* bs = Bs[cur];
+#pragma unroll
+        for (int kk = 0; kk < kDK; kk += 4) {
+            double av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) av[i] = as[(wm * 32 + i * 16 + li) * kDAld + kk + lk];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bv[j] = bs[(kk + lk) * kDBld + wn * 32 + j * 16 + li];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) stash(cur ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t col = n0 + wn * 32 + j * 16 + li;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm * 32 + i * 16 + lk + 4 * r;
+                if (Full || (row < p.M && col < p.N))
+                    out[row * p.so.r + col * p.so.c] = plus_bias(acc[i][j][r], p.bias, col);
+            }
+        }
+}
+
+int matmul_f64(const double* a, const double* b, double* out, const MatmulArgs& p) {
+    if (p.batches > 65535) return fail(KD_E_INVALID, "kd_matmul: too many batches");
+    const int64_t tiles = ((p.M + kD - 1) / kD) * ((p.N + kD - 1) / kD);
+    if (tiles > (int64_t{1} << 31) - 1) return fail(KD_E_INVALID, "kd_matmul: too many tiles");
+    const dim3 grid(static_cast<uint32_t>(tiles), static_cast<uint32_t>(p.batches));
+    const bool full = p.M % kD == 0 && p.N % kD == 0 && p.K % kDK == 0;
+    if (full) hipLaunchKernelGGL((mfma_f64_kernel<true>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+    else hipLaunchKernelGGL((mfma_f64_kernel<false>), grid, dim3(kThreads), 0, stream(), a, b, out, p);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
 template <typename T> int matmul_tiled(const T* a, const T* b, T* out, const MatmulArgs& p) {
     if (p.batches > 65535) return fail(KD_E_INVALID, "kd_matmul: too many batches");
     const int64_t gm = (p.M + kTT - 1) / kTT, gn = (p.N + kTT - 1) / kTT;
@@ -1504,7 +1619,7 @@ int dispatch(int dtype, const void* a, const void* b, void* out, const MatmulArg
     }
     switch (dtype) {
     case KD_F32: return matmul_f32(static_cast<const float*>(a), static_cast<const float*>(b), static_cast<float*>(out), p);
-    case KD_F64: return matmul_tiled<double>(static_cast<const double*>(a), static_cast<const double*>(b), static_cast<double*>(out), p);
+    case KD_F64: return matmul_f64(static_cast<const double*>(a), static_cast<const double*>(b), static_cast<double*>(out), p);
     default: return matmul_tiled<int64_t>(static_cast<const int64_t*>(a), static_cast<const int64_t*>(b), static_cast<int64_t*>(out), p);
     }
 }

@@ -529,3 +529,36 @@ def test_bias_epilogue_equals_product_then_add(kdb, oracle, dtype, case):
         np.testing.assert_array_equal(got, want)
     else:
         close(got, want.astype(np.float64))
+
+
+F64_CASES = [(1, 64, 16, 64), (1, 128, 256, 192), (3, 70, 33, 130), (2, 1, 5, 1), (1, 257, 1000, 65), (4, 64, 64, 64)]
+
+
+@pytest.mark.parametrize("case", F64_CASES, ids=[f"{b}x{m}x{k}x{n}" for b, m, k, n in F64_CASES])
+@pytest.mark.parametrize("layout", ["rowmajor", "transposed"])
+def test_f64_on_the_matrix_cores(kdb, oracle, case, layout):
+    """f64 products on v_mfma_f64_16x16x4f64 (whole and ragged tiles, batches, A and B read
+    through transposed strides) against the oracle's sequential double sums: within 1e-13 of
+    sum |a| |b| per element (the matrix cores accumulate four products per step in their own
+    order). Also pins the instruction's lane layout: a wrong row / column assignment is far off."""
+    batches, m, k, n = case
+    rng = np.random.default_rng(m * 11 + n + k)
+    if layout == "rowmajor":
+        sa, sb = (m * k, k, 1), (k * n, n, 1)
+    else:
+        sa, sb = (m * k, 1, m), (k * n, 1, k)
+    a = rng.uniform(-1, 1, batches * m * k)
+    b = rng.uniform(-1, 1, batches * k * n)
+    strides = kd.MatmulStrides()
+    so = (m * n, n, 1)
+    for i in range(3):
+        strides.a[i], strides.b[i], strides.out[i] = sa[i], sb[i], so[i]
+    sizes = kd.MatmulSizes(batches, m, k, n)
+    want = np.empty(batches * m * n)
+    assert oracle.oracle_matmul_strided(kd.F64, support.ptr(a), support.ptr(b), support.ptr(want), sizes, strides) == 0
+    da, db, dc = kdb.to_device(a), kdb.to_device(b), kdb.empty((batches * m * n,), np.float64)
+    kdb.call("matmul_strided", kd.F64, da.ptr, db.ptr, dc.ptr, sizes, strides)
+    av = np.lib.stride_tricks.as_strided(a, (batches, m, k), tuple(8 * s for s in sa))
+    bv = np.lib.stride_tricks.as_strided(b, (batches, k, n), tuple(8 * s for s in sb))
+    scale = (np.abs(av) @ np.abs(bv)).ravel()
+    assert np.all(np.abs(dc.numpy() - want) <= 1e-13 * scale + 1e-300)
