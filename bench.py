@@ -429,9 +429,11 @@ def cpu_c2_baseline(iters=5):
             "sample": f"kael CPU path, [4096,4096] f32 (manual_seed(1) inputs), median of {iters} calls per op"}
 
 
-def cpu_gpt2_baseline(new_tokens=8):
+def cpu_gpt2_baseline(new_tokens=8, context=192):
     """kael's own nn::generate on the CPU path (reference build), GPT-2 small, seed 4: decode
-    tokens/s from two runs (1 and 1 + new_tokens new tokens) so prefill cancels out."""
+    tokens/s from two runs (1 and 1 + new_tokens new tokens) so prefill cancels out. The prompt
+    is `context` tokens long so that the sampled steps attend over the mean context of the GPU
+    run (a 64-token prompt and 255 new tokens: positions 65-319, mean ~192)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import support
 
@@ -439,21 +441,22 @@ def cpu_gpt2_baseline(new_tokens=8):
     threads = int(os.environ.get("KAEL_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
     lib.ref_set_threads(threads)
     h = lib.ref_gpt_create(50257, 1024, 12, 12, 768, 4, 1)
-    prompt = np.ascontiguousarray(np.random.default_rng(4).integers(0, 50257, 64), np.int64)
-    out = np.zeros(64 + 1 + new_tokens, np.int64)
+    prompt = np.ascontiguousarray(np.random.default_rng(4).integers(0, 50257, context), np.int64)
+    out = np.zeros(context + 1 + new_tokens, np.int64)
     t1, t2 = ctypes.c_double(), ctypes.c_double()
     try:
-        if lib.ref_gpt_generate(h, prompt.ctypes.data_as(ctypes.c_void_p), 64, 1, out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(t1)):
+        if lib.ref_gpt_generate(h, prompt.ctypes.data_as(ctypes.c_void_p), context, 1, out.ctypes.data_as(ctypes.c_void_p),
+                                ctypes.byref(t1)):
             raise RuntimeError(support.ref_error(lib))
-        if lib.ref_gpt_generate(h, prompt.ctypes.data_as(ctypes.c_void_p), 64, 1 + new_tokens,
+        if lib.ref_gpt_generate(h, prompt.ctypes.data_as(ctypes.c_void_p), context, 1 + new_tokens,
                                 out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(t2)):
             raise RuntimeError(support.ref_error(lib))
     finally:
         lib.ref_gpt_destroy(h)
     rate = new_tokens / max(t2.value - t1.value, 1e-9)
     return {"value": rate, "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"kael nn::generate GPT-2 small f32 (seed 4), prompt 64, decode rate from {new_tokens} extra tokens, "
-                      f"prefill {t1.value:.2f} s", "prefill_s": t1.value}
+            "sample": f"kael nn::generate GPT-2 small f32 (seed 4), prompt {context} (the GPU run's mean context), "
+                      f"decode rate from {new_tokens} extra tokens, prefill {t1.value:.2f} s", "prefill_s": t1.value}
 
 
 def cpu_baseline(n, budget_s=20.0):
