@@ -377,6 +377,23 @@ ACCUMULATE_BRANCH = """    // MI355X: a device gradient that nothing else refere
     }
 """
 
+LEFT_WEIGHT_GRADIENT_BRANCH = """                     if (g.device() != Device::CPU && !layout.left_is_vector && !layout.right_is_vector &&
+                         shape.size() == 2 && right.get().dim() > 2 && g.size(-1) > 0 && g.size(-2) > 0 &&
+                         right.get().size(-2) > 0) {
+                         // MI355X: a 2-D left operand shared by every batch item (kael's tied LM head,
+                         // weight . h^T): its gradient is one product over the folded batch,
+                         // (g^T)_flat^T . (right^T)_flat with K = every batch item's columns, instead
+                         // of one product per item and a sum over the batch. The reshapes are views
+                         // when the batch and column dims flatten (the head's gradient is a
+                         // transposed view of a contiguous tensor, so they do).
+                         const Tensor gt = g.transpose(-2, -1);
+                         const Tensor rt = right.get().transpose(-2, -1);
+                         const Tensor flat_g = gt.reshape({gt.numel() / gt.size(-1), gt.size(-1)});
+                         const Tensor flat_r = rt.reshape({rt.numel() / rt.size(-1), rt.size(-1)});
+                         return matmul(flat_g.mT(), flat_r).to(dtype);
+                     }
+"""
+
 LEADING_REDUCE_HELPER = """// MI355X: a contiguous tensor reduced over its leading dims (an [outer, inner] matrix reduced
 // over its rows: bias and LayerNorm gradients summed over every token) as one
 // device::reduce_columns call that reads it in place; nullopt for any other case, which keeps
@@ -624,6 +641,9 @@ EDITS = [
     ("src/autograd/functions_linalg.cpp",
      "                     const Tensor gradient = matmul(left.get().mT(), layout.matrix_gradient(g));\n", "before",
      WEIGHT_GRADIENT_BRANCH),
+    ("src/autograd/functions_linalg.cpp",
+     "                     const Tensor gradient = matmul(layout.matrix_gradient(g), right.get().mT());\n", "before",
+     LEFT_WEIGHT_GRADIENT_BRANCH),
     ("src/ops/indexing.cpp", "Tensor masked_fill(const Tensor& t, const Tensor& mask, Scalar value) {\n", "after",
      MASKED_FILL_BRANCH),
     ("src/nn/layers.cpp", '#include "kael/ops.h"\n', "after",

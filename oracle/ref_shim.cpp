@@ -802,6 +802,26 @@ int ref_row_grad(int kind, int device, int dtype, const void* x, const void* g, 
     });
 }
 
+// Gradients of kael's tied LM-head product through its autograd on `device`
+// (reference src/nn/transformer.cpp:235-236: matmul(weight, h.mT()).mT()): manual_seed(seed);
+// w = (rand({n, k}) * 2 - 1) * 0.05, h = rand({batch, m, k}) * 2 - 1, gout = rand({batch, m, n}) * 2 - 1;
+// sum(matmul(w, h.mT()).mT() * gout).backward(). Writes w.grad [n, k] and h.grad [batch, m, k].
+int ref_head_grads(int device, int64_t batch, int64_t m, int64_t k, int64_t n, uint64_t seed, float* w_grad,
+                   float* h_grad) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(seed);
+        kael::Tensor w = ((kael::rand({n, k}) * 2 - 1) * 0.05).to(dev);
+        kael::Tensor h = (kael::rand({batch, m, k}) * 2 - 1).to(dev);
+        const kael::Tensor gout = (kael::rand({batch, m, n}) * 2 - 1).to(dev);
+        w.requires_grad_(true);
+        h.requires_grad_(true);
+        kael::sum(kael::matmul(w, h.mT()).mT() * gout).backward();
+        copy_out(w.grad()->cpu(), w_grad);
+        copy_out(h.grad()->cpu(), h_grad);
+    });
+}
+
 // kael's LayerNorm module (reference src/nn/layers.cpp:55-68) through its autograd on `device` (0
 // CPU, 1 the linked device backend): weight and bias set from w / b, x [rows, cols] (dtype 0 f32,
 // 1 f64) requires grad, sum(LayerNorm(x) * g).backward(). Writes the output, kael's standardize(x)

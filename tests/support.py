@@ -99,6 +99,7 @@ REF_SIGS = {
     "gpt_param_total": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "row_grad": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "linear_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
+    "head_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
     "layer_norm_grads": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_double,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "suite_size": (c_int, []),

@@ -52,6 +52,30 @@ def test_linear_gradients_match_cpu(request, variant, shape):
     assert_reference_close(dev_x, cpu_x, "x.grad")
 
 
+# (batch, m, k, n) of the tied LM head's product weight . h^T: C4's (32 x 128 tokens, d 256, vocab
+# 96), then ragged shapes.
+HEAD_SHAPES = [(32, 128, 256, 96), (3, 37, 53, 29), (2, 1, 7, 3)]
+
+
+def head_grads(lib, device, shape, seed=9):
+    b, m, k, n = shape
+    wg, hg = np.empty((n, k), np.float32), np.empty((b, m, k), np.float32)
+    assert lib.ref_head_grads(device, b, m, k, n, seed, P(wg), P(hg)) == 0, support.ref_error(lib)
+    return wg, hg
+
+
+@pytest.mark.parametrize("variant", ["hip", "hip_fused"])
+@pytest.mark.parametrize("shape", HEAD_SHAPES, ids=["x".join(map(str, s)) for s in HEAD_SHAPES])
+def test_head_gradients_match_cpu(request, variant, shape):
+    """The tied head's weight gradient: per batch item and a batch sum (unmodified kael), one
+    product over the folded batch (the device branch); both against kael's CPU path."""
+    lib = request.getfixturevalue("kael_" + variant)
+    cpu_w, cpu_h = head_grads(lib, 0, shape)
+    dev_w, dev_h = head_grads(lib, 1, shape)
+    assert_reference_close(dev_w, cpu_w, "W.grad")
+    assert_reference_close(dev_h, cpu_h, "h.grad")
+
+
 C4 = (96, 128, 4, 4, 256, 32)  # vocab, context, layers, heads, dimension, batch
 LR = 1e-3  # kael's Adam default (include/kael/optim/adam.h:11-17)
 

@@ -37,3 +37,25 @@ def test_empty_last_dim_keeps_kaels_path(kael_oracle_fused, shape):
     assert kael_oracle_fused.ref_linear_grads(1, b, m, k, n, 3, support.ptr(wg), support.ptr(xg)) == 0, \
         support.ref_error(kael_oracle_fused)
     assert not wg.any() and not xg.any()
+
+
+@pytest.mark.parametrize("shape", [(3, 37, 53, 29), (2, 1, 7, 3), (4, 16, 32, 24)], ids=["3x37x53x29", "2x1x7x3", "4x16x32x24"])
+def test_head_gradients_through_the_fused_branches(kael_oracle_fused, shape):
+    """The tied head's weight . h^T with the left-operand gradient folded over the batch (one
+    product) against kael's CPU path, on the oracle device."""
+    from test_gpu_kael_gradients import head_grads
+
+    lib = kael_oracle_fused
+    cpu_w, cpu_h = head_grads(lib, 0, shape)
+    dev_w, dev_h = head_grads(lib, 1, shape)
+    assert_reference_close(dev_w, cpu_w, "W.grad")
+    assert_reference_close(dev_h, cpu_h, "h.grad")
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 0, 4), (2, 0, 5, 4), (2, 3, 5, 0)], ids=["k0", "m0", "n0"])
+def test_head_empty_dims_keep_kaels_path(kael_oracle_fused, shape):
+    b, m, k, n = shape
+    wg, hg = np.ones((n, k), np.float32), np.ones((b, m, k), np.float32)
+    assert kael_oracle_fused.ref_head_grads(1, b, m, k, n, 3, support.ptr(wg), support.ptr(hg)) == 0, \
+        support.ref_error(kael_oracle_fused)
+    assert not wg.any() and not hg.any()
