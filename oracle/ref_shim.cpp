@@ -17,10 +17,12 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
+#include "kael/debug.h"
 #include "kael/device_kernels.h"
 #include "kael/kael.h"
 #include "kael/nn/layernorm.h"
@@ -819,6 +821,70 @@ int ref_head_grads(int device, int64_t batch, int64_t m, int64_t k, int64_t n, u
         kael::sum(kael::matmul(w, h.mT()).mT() * gout).backward();
         copy_out(w.grad()->cpu(), w_grad);
         copy_out(h.grad()->cpu(), h_grad);
+    });
+}
+
+// Gradients through kael's select (reference src/autograd/functions_view.cpp:77-88) on `device` (0
+// CPU, 1 the linked device backend) for the graph shapes a backward pass can give its select
+// gradients: x [2, 3, 3, 4] (seeded uniform) requires grad and `which` picks the loss:
+//   0  the attention split: parts = x * 1, q / k / v = parts.select(2, i) (q read transposed);
+//   1  two of three indices selected from the leaf (the third slice stays zero);
+//   2  the same index twice (once as dim -2) and a second index;
+//   3  selects mixed with a gradient of the whole tensor (x * x);
+//   4  selects along two different dims;
+//   5  the split of case 0 on an intermediate that retains its gradient (also written to p_grad);
+//   6  case 0 with anomaly detection on;
+//   7  a select of a select, and a select along the last dim.
+// Writes x.grad (72 values) and, for case 5, the intermediate's gradient (else zeros).
+int ref_select_grads(int device, int which, uint64_t seed, float* x_grad, float* p_grad) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(seed);
+        kael::Tensor x = (kael::rand({2, 3, 3, 4}) * 2 - 1).to(dev);
+        const kael::Tensor wq = (kael::rand({3, 2, 4}) * 2 - 1).to(dev);
+        const kael::Tensor wk = (kael::rand({2, 3, 4}) * 2 - 1).to(dev);
+        const kael::Tensor wv = (kael::rand({2, 3, 4}) * 2 - 1).to(dev);
+        const kael::Tensor wa = (kael::rand({3, 3, 4}) * 2 - 1).to(dev);
+        x.requires_grad_(true);
+        std::optional<kael::Tensor> retained;
+        auto split = [&](const kael::Tensor& parts) {
+            return kael::sum(parts.select(2, 0).transpose(0, 1) * wq) + kael::sum(parts.select(2, 1) * wk) +
+                   kael::sum(parts.select(2, 2) * wv);
+        };
+        auto make_loss = [&]() -> kael::Tensor {
+            switch (which) {
+            case 0: case 6: return split(x * 1.0);
+            case 1: return kael::sum(x.select(2, 0) * wk) + kael::sum(x.select(2, -1) * wv);
+            case 2:
+                return kael::sum(x.select(-2, 1) * wk) + kael::sum(x.select(2, 1) * wv) +
+                       kael::sum(x.select(2, 0) * wq.transpose(0, 1));
+            case 3: return kael::sum(x.select(2, 0) * wk) + kael::sum(x * x) + kael::sum(x.select(2, 1) * wv);
+            case 4: return kael::sum(x.select(0, 1) * wa) + kael::sum(x.select(2, 2) * wv);
+            case 5: {
+                kael::Tensor p = x * 2.0;
+                p.retain_grad();
+                retained = p;
+                return split(p);
+            }
+            case 7: return kael::sum(x.select(0, 1).select(1, 2) * wa.select(1, 0)) + kael::sum(x.select(3, 1));
+            default: throw std::invalid_argument("unknown select case");
+            }
+        };
+        const kael::Tensor loss = make_loss();
+        if (which == 6) kael::set_anomaly_detection(true);
+        try {
+            loss.backward();
+        } catch (...) {
+            if (which == 6) kael::set_anomaly_detection(false);
+            throw;
+        }
+        if (which == 6) kael::set_anomaly_detection(false);
+        copy_out(x.grad()->cpu(), x_grad);
+        if (retained) {
+            copy_out(retained->grad()->cpu(), p_grad);
+        } else {
+            std::fill(p_grad, p_grad + 72, 0.0f);
+        }
     });
 }
 

@@ -80,6 +80,28 @@ C4 = (96, 128, 4, 4, 256, 32)  # vocab, context, layers, heads, dimension, batch
 LR = 1e-3  # kael's Adam default (include/kael/optim/adam.h:11-17)
 
 
+SELECT_CASES = ["attention_split", "two_of_three", "same_index_twice", "mixed_with_whole", "two_dims",
+                "retained_intermediate", "anomaly_detection", "select_of_select"]
+
+
+def select_grads(lib, device, which, seed=11):
+    xg, pg = np.empty(72, np.float32), np.empty(72, np.float32)
+    assert lib.ref_select_grads(device, which, seed, P(xg), P(pg)) == 0, support.ref_error(lib)
+    return xg, pg
+
+
+@pytest.mark.parametrize("variant", ["hip", "hip_fused"])
+@pytest.mark.parametrize("which", range(len(SELECT_CASES)), ids=SELECT_CASES)
+def test_select_gradients_match_cpu(request, variant, which):
+    """Select gradients (deferred by the device branch and written once per receiving node, or
+    kael's zero fill, copy and sum): every value equal to kael's CPU path."""
+    lib = request.getfixturevalue("kael_" + variant)
+    cpu_x, cpu_p = select_grads(lib, 0, which)
+    dev_x, dev_p = select_grads(lib, 1, which)
+    assert np.array_equal(dev_x, cpu_x) and np.array_equal(dev_p, cpu_p)
+    assert (cpu_p != 0).any() == (SELECT_CASES[which] == "retained_intermediate")
+
+
 def chargpt(lib, device, steps):
     total = lib.ref_gpt_param_total(*C4[:5])
     losses, params, secs = np.zeros(steps, np.float32), np.zeros(total, np.float32), ctypes.c_double()

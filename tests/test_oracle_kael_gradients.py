@@ -7,12 +7,13 @@ fold branch must run (the strided-product counter moves) and an empty last dim m
 kael's own path.
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
 
 import support
-from test_gpu_kael_gradients import assert_reference_close, linear_grads
+from test_gpu_kael_gradients import SELECT_CASES, assert_reference_close, linear_grads, select_grads
 
 SHAPES = [(3, 37, 53, 29), (5, 1, 7, 3), (2, 30, 64, 48), (4, 16, 32, 24)]
 
@@ -59,3 +60,52 @@ def test_head_empty_dims_keep_kaels_path(kael_oracle_fused, shape):
     assert kael_oracle_fused.ref_head_grads(1, b, m, k, n, 3, support.ptr(wg), support.ptr(hg)) == 0, \
         support.ref_error(kael_oracle_fused)
     assert not wg.any() and not hg.any()
+
+
+@pytest.mark.parametrize("which", range(len(SELECT_CASES)), ids=SELECT_CASES)
+def test_select_gradients_through_the_fused_branches(kael_oracle_fused, which):
+    """Deferred select gradients on the oracle device equal kael's CPU path value for value,
+    including the slices no select reached (zeros), repeated indices (summed), gradients of the
+    whole tensor mixed in, a retained intermediate and anomaly detection (deferral off)."""
+    cpu_x, cpu_p = select_grads(kael_oracle_fused, 0, which)
+    dev_x, dev_p = select_grads(kael_oracle_fused, 1, which)
+    assert np.array_equal(dev_x, cpu_x) and np.array_equal(dev_p, cpu_p)
+    if SELECT_CASES[which] in ("two_of_three", "same_index_twice"):
+        # one slice of dim 2 has no select: its gradient is zero
+        assert not cpu_x.reshape(2, 3, 3, 4)[:, :, 1 if which == 1 else 2].any()
+
+
+def test_select_gradients_reject_unknown_case(kael_oracle_fused):
+    xg, pg = np.empty(72, np.float32), np.empty(72, np.float32)
+    assert kael_oracle_fused.ref_select_grads(1, 99, 1, support.ptr(xg), support.ptr(pg)) != 0
+
+
+_TRACE_SELECT = """
+import ctypes, sys
+import numpy as np
+lib = ctypes.CDLL(sys.argv[1])
+xg, pg = np.empty(72, np.float32), np.empty(72, np.float32)
+sys.exit(lib.ref_select_grads(1, int(sys.argv[2]), ctypes.c_uint64(11), xg.ctypes.data_as(ctypes.c_void_p),
+                              pg.ctypes.data_as(ctypes.c_void_p)))
+"""
+
+
+@pytest.mark.parametrize("which, unmodified, fused", [(0, 3, 0), (1, 2, 1), (2, 3, 1)],
+                         ids=["attention_split", "two_of_three", "same_index_twice"])
+def test_select_gradients_skip_the_zero_fills(tmp_path, which, unmodified, fused):
+    """The device calls of one backward pass (the oracle backend's call trace): kael fills a
+    zero tensor of the full shape [2, 3, 3, 4] per select; with the select gradients deferred,
+    only a full tensor that some slice of the selected dim never reaches is filled (once)."""
+    import json
+    import subprocess
+    import sys
+
+    fills = {}
+    for name in ("libkael_oracle.so", "libkael_oracle_fused.so"):
+        trace = tmp_path / f"{name}.jsonl"
+        env = dict(os.environ, KD_ORACLE_TRACE=str(trace))
+        subprocess.run([sys.executable, "-c", _TRACE_SELECT, str(support.REF_DIR / name), str(which)],
+                       env=env, check=True, timeout=120)
+        recs = [json.loads(line) for line in trace.read_text().splitlines() if line.strip()]
+        fills[name] = sum(1 for r in recs if r["op"] == "fill" and r["count"] == 72)
+    assert fills == {"libkael_oracle.so": unmodified, "libkael_oracle_fused.so": fused}
