@@ -283,6 +283,14 @@ int kd_gather(int dtype, void* out, const void* data, const int64_t* indices,
 int kd_scatter_add(int dtype, void* data, const int64_t* indices, const void* source,
                    const kd_index_layout* layout);
 
+/* The smallest and largest of `count` > 0 indices indices[i * stride], written to the host pair
+ * bounds[0] (min), bounds[1] (max) before the call returns (one stream sync). Replaces the range
+ * check kael runs before a device gather / scatter_add (reference src/internal/index_checks.h:
+ * 37-43, max(indices).item() then min(indices).item(): two reductions and two blocking reads of
+ * a contiguous copy of the broadcast indices) and on cross-entropy targets (src/ops/nn.cpp:97-98,
+ * src/nn/loss.cpp:27-28); the caller checks the pair in the same order, max first. */
+int kd_index_bounds(const int64_t* indices, int64_t count, int64_t stride, int64_t* bounds);
+
 /* ---- fused row kernels (extensions replacing composed device paths) ---- */
 
 /* Row softmax over `rows` contiguous rows of `cols`: max, exp(x-max), sum in double,

@@ -13,7 +13,15 @@
 // the row and loads its index once, then copies (gather, 16-byte vectors when the row starts
 // allow) or atomically adds (scatter) the row's elements, all lanes' loads issued before their
 // stores. Otherwise every element is decoded on its own.
+//
+// kd_index_bounds returns the smallest and largest of a strided run of indices in one call (the
+// range check kael makes before a device gather or scatter, and on cross-entropy targets): one
+// or more workgroups fold their share, a second launch combines the workgroups' pairs, and the
+// last launch writes the pair into a pinned host slot that is read after one stream sync.
 #include <algorithm>
+#include <climits>
+#include <mutex>
+#include <vector>
 
 #include "kd_internal.h"
 
@@ -254,11 +262,135 @@ template <typename T> int scatter_typed(void* data, const int64_t* indices, cons
     return KD_OK;
 }
 
+// ---- index bounds ------------------------------------------------------------------------
+
+constexpr int kBoundsThreads = 1024;
+constexpr int64_t kBoundsPerBlock = int64_t{kBoundsThreads} * 16;  // elements one workgroup folds
+constexpr int kBoundsMaxBlocks = 512;
+
+__device__ __forceinline__ void fold_bounds(int64_t& lo, int64_t& hi, int64_t v) {
+    lo = v < lo ? v : lo;
+    hi = v > hi ? v : hi;
+}
+
+// Folds another (min, max) pair; an empty pair is (INT64_MAX, INT64_MIN) and changes nothing.
+__device__ __forceinline__ void fold_pair(int64_t& lo, int64_t& hi, int64_t other_lo, int64_t other_hi) {
+    lo = other_lo < lo ? other_lo : lo;
+    hi = other_hi > hi ? other_hi : hi;
+}
+
+// The workgroup's (min, max) over its values (lo / hi per thread) into out[0..1].
+__device__ void write_bounds(int64_t lo, int64_t hi, int64_t* out) {
+    __shared__ int64_t slo[kBoundsThreads / 64], shi[kBoundsThreads / 64];
+#pragma unroll
+    for (int off = 32; off > 0; off /= 2) {
+        const int64_t other_lo = __shfl_xor(lo, off);
+        const int64_t other_hi = __shfl_xor(hi, off);
+        fold_pair(lo, hi, other_lo, other_hi);
+    }
+    const int wave = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) {
+        slo[wave] = lo;
+        shi[wave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kBoundsThreads / 64; ++w) fold_pair(lo, hi, slo[w], shi[w]);
+        out[0] = lo;
+        out[1] = hi;
+    }
+}
+
+// Workgroup b folds elements [b * per, min(count, (b + 1) * per)) of indices[i * stride].
+__global__ __launch_bounds__(kBoundsThreads) void bounds_kernel(const int64_t* __restrict__ indices, int64_t count,
+                                                                int64_t stride, int64_t per, int64_t* out) {
+    int64_t lo = INT64_MAX, hi = INT64_MIN;
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * per;
+    const int64_t end = begin + per < count ? begin + per : count;
+    for (int64_t i = begin + threadIdx.x; i < end; i += kBoundsThreads) fold_bounds(lo, hi, indices[i * stride]);
+    write_bounds(lo, hi, out + 2 * blockIdx.x);
+}
+
+// One workgroup: the (min, max) of `pairs` workgroup pairs.
+__global__ __launch_bounds__(kBoundsThreads) void bounds_combine_kernel(const int64_t* __restrict__ partial, int64_t pairs,
+                                                                        int64_t* out) {
+    int64_t lo = INT64_MAX, hi = INT64_MIN;
+    for (int64_t i = threadIdx.x; i < pairs; i += kBoundsThreads) fold_pair(lo, hi, partial[2 * i], partial[2 * i + 1]);
+    write_bounds(lo, hi, out);
+}
+
+// Pinned host slots for the bounds pairs: each call holds one from its launch until it has read
+// the pair, so calls from several host threads never share a slot. Allocated in pages on first
+// need and kept for the life of the process.
+class BoundsSlots {
+public:
+    int take(int64_t** slot) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        if (free_.empty()) {
+            void* page = nullptr;
+            KD_HIP(hipHostMalloc(&page, kPage * 2 * sizeof(int64_t), hipHostMallocCoherent));
+            for (int i = kPage - 1; i >= 0; --i) free_.push_back(static_cast<int64_t*>(page) + 2 * i);
+        }
+        *slot = free_.back();
+        free_.pop_back();
+        return KD_OK;
+    }
+    void give(int64_t* slot) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        free_.push_back(slot);
+    }
+
+private:
+    static constexpr int kPage = 256;
+    std::mutex mutex_;
+    std::vector<int64_t*> free_;
+};
+
+BoundsSlots& bounds_slots() {
+    static BoundsSlots* slots = new BoundsSlots();  // never destroyed: outlives every caller
+    return *slots;
+}
+
+int index_bounds(const int64_t* indices, int64_t count, int64_t stride, int64_t* bounds) {
+    const int64_t blocks = std::min<int64_t>((count + kBoundsPerBlock - 1) / kBoundsPerBlock, kBoundsMaxBlocks);
+    const int64_t per = (count + blocks - 1) / blocks;
+    int64_t* slot = nullptr;
+    if (int rc = bounds_slots().take(&slot)) return rc;
+    struct Release {
+        int64_t* slot;
+        ~Release() { bounds_slots().give(slot); }
+    } release{slot};
+    if (blocks == 1) {
+        hipLaunchKernelGGL(bounds_kernel, dim3(1), dim3(kBoundsThreads), 0, stream(), indices, count, stride, per, slot);
+        KD_LAUNCH_CHECK();
+    } else {
+        Workspace ws;  // held until bounds_combine_kernel is enqueued
+        if (int rc = workspace(ws, static_cast<size_t>(blocks) * 2 * sizeof(int64_t))) return rc;
+        hipLaunchKernelGGL(bounds_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBoundsThreads), 0, stream(), indices,
+                           count, stride, per, static_cast<int64_t*>(ws.ptr));
+        KD_LAUNCH_CHECK();
+        hipLaunchKernelGGL(bounds_combine_kernel, dim3(1), dim3(kBoundsThreads), 0, stream(),
+                           static_cast<const int64_t*>(ws.ptr), blocks, slot);
+        KD_LAUNCH_CHECK();
+    }
+    KD_HIP(hipStreamSynchronize(stream()));
+    bounds[0] = slot[0];
+    bounds[1] = slot[1];
+    return KD_OK;
+}
+
 } // namespace
 
 } // namespace kd
 
 using namespace kd;
+
+extern "C" int kd_index_bounds(const int64_t* indices, int64_t count, int64_t stride, int64_t* bounds) {
+    if (indices == nullptr || bounds == nullptr || count <= 0)
+        return fail(KD_E_INVALID, "kd_index_bounds: needs indices, a bounds pair and count > 0");
+    if (int rc = ensure_device()) return rc;
+    return index_bounds(indices, count, stride, bounds);
+}
 
 extern "C" int kd_gather(int dtype, void* out, const void* data, const int64_t* indices, const kd_index_layout* layout) {
     if (layout == nullptr) return fail(KD_E_INVALID, "kd_gather: null layout");

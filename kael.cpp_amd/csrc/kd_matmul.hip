@@ -1359,6 +1359,39 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             return KD_OK;
         }
     }
+    {
+        // Few tiles and a long K on the general kernel (a ragged M or N, any strides; C4's tied
+        // LM-head weight gradient, 96 x 256 outputs over K = 4096 tokens, is 2 tiles): K is split so
+        // that about one workgroup per CU is busy, the splits taking the kernel's batch slot (their
+        // K offsets as batch strides) and writing partial products that split_sum_kernel adds in
+        // split order, bias included.
+        const int cus = compute_units();
+        const int64_t per = p.M * p.N;
+        if (p.batches == 1 && p.heads == 1 && tiles * 2 <= cus && p.K >= 1024) {
+            int64_t splits = std::min<int64_t>(p.K / 64, cus / tiles);
+            while (splits > 1 && p.K % (splits * kBK) != 0) --splits;
+            if (splits > 1 && splits * per < (int64_t{1} << 31)) {
+                Workspace ws;  // held until split_sum_kernel is enqueued
+                if (int rc = workspace(ws, static_cast<size_t>(splits * per) * sizeof(float))) return rc;
+                MatmulArgs part = p;
+                part.batches = splits;
+                part.K = p.K / splits;
+                part.sa.b = part.K * p.sa.c;
+                part.sb.b = part.K * p.sb.r;
+                part.so = Strides3{per, p.N, 1};
+                part.bias = nullptr;
+                hipLaunchKernelGGL((mfma_f32_kernel<AMode, BMode, false>),
+                                   dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)), dim3(kThreads), 0,
+                                   stream(), a, b, static_cast<float*>(ws.ptr), part);
+                KD_LAUNCH_CHECK();
+                const int64_t blocks = std::min<int64_t>((per + kThreads - 1) / kThreads, int64_t{cus} * 16);
+                hipLaunchKernelGGL(split_sum_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream(),
+                                   static_cast<const float*>(ws.ptr), out, p, splits);
+                KD_LAUNCH_CHECK();
+                return KD_OK;
+            }
+        }
+    }
     bool full = false;
     if constexpr (AMode != kGeneric && BMode != kGeneric) full = p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0;
     const bool bias = p.bias != nullptr;

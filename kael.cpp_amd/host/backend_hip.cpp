@@ -252,6 +252,10 @@ void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const 
           "reduce_columns");
 }
 
+void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t stride, std::int64_t bounds[2]) {
+    check(kd_index_bounds(indices, count, stride, bounds), "index_bounds");
+}
+
 namespace {
 
 kd_gpt_config engine_config(const GptEngineShape& s) {

@@ -133,6 +133,12 @@ void arg_reduce(bool largest, DType in, std::int64_t* results, const std::byte* 
 void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const std::byte* data, std::int64_t outer,
                     std::int64_t inner);
 
+// bounds[0] = min, bounds[1] = max of the `count` > 0 device indices indices[i * stride], on the
+// host when the call returns: kael's range check of device indices (reference
+// src/internal/index_checks.h:37-43) and of cross-entropy targets (src/ops/nn.cpp:97-98) in one
+// call and one sync instead of two reductions read back one at a time.
+void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t stride, std::int64_t bounds[2]);
+
 // Running sums along `rows` contiguous rows of `size` elements (reference src/ops/sequence.cpp:95-117):
 // f32 / f64 store In, i64 / bool wrapping int64.
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows);

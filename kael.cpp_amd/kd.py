@@ -118,6 +118,7 @@ SIGNATURES = {
     "cumsum": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
     "scatter_add": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
+    "index_bounds": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
     "softmax_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int]),
     "standardize_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "cross_entropy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),

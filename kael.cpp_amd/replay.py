@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import gzip
 import json
-from ctypes import byref, c_void_p
+from ctypes import byref, c_int64, c_void_p
 from pathlib import Path
 
 import numpy as np
@@ -72,7 +72,8 @@ POINTERS = {
     "matmul": ("a", "b", "c"), "matmul_strided": ("a", "b", "c"), "matmul_strided_heads": ("a", "b", "c"),
     "matmul_strided_bias": ("a", "b", "c", "bias"),
     "gather": ("out", "data", "indices"),
-    "scatter_add": ("data", "indices", "source"), "softmax_rows": ("out", "x"), "standardize_rows": ("out", "x"),
+    "scatter_add": ("data", "indices", "source"), "index_bounds": ("indices",),
+    "softmax_rows": ("out", "x"), "standardize_rows": ("out", "x"),
     "cross_entropy_rows": ("losses", "logits", "targets"), "cross_entropy_grad": ("out", "logits", "targets", "weights"),
     "softmax_rows_backward": ("out", "y", "grad"), "standardize_rows_backward": ("out", "x", "y", "grad"),
     "adam_step": ("p", "g", "m", "v"), "sgd_step": ("p", "g"), "adam_step_many": (),
@@ -236,6 +237,10 @@ class Replay:
         if op == "reduce_columns":
             a = (r["rop"], r["out"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["outer"], r["inner"])
             return (lambda: chk(lib.kd_reduce_columns(*a), "kd_reduce_columns")), None
+        if op == "index_bounds":
+            pair = (c_int64 * 2)()
+            a = (c_void_p(P(r["indices"])), r["count"], r["stride"], pair)
+            return (lambda: chk(lib.kd_index_bounds(*a), "kd_index_bounds")), None
         if op == "arg_reduce":
             a = (r["largest"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["chunk"], r["rows"])
             return (lambda: chk(lib.kd_arg_reduce(*a), "kd_arg_reduce")), None

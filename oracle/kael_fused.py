@@ -36,6 +36,12 @@ training configs with kael's own host code calling the backend's fused entry poi
   src/autograd/engine.cpp            backward (:107-153): deferred select gradients of one tensor
                                      merged in add_to_buffer (:83-88) and written once, slices as
                                      copies and the rest as zeros, before the receiving node runs
+  src/ops/indexing.cpp, inplace.cpp  gather (:143-156) and scatter_add_ (:160-178) with broadcast 1-D
+                                     indices (index_select, index_add_): one range check of the
+                                     line (kd_index_bounds) and the indices read in place, instead
+                                     of a contiguous copy checked by two reductions and two reads
+  src/ops/nn.cpp, src/nn/loss.cpp    the cross-entropy targets' range check (:97-98, :27-28) in one
+                                     call
   src/nn/transformer.cpp             nn::generate (:256-295) with temperature 0, the KV cache and a
                                      batch-1 prompt on the device runs on the decode engine
                                      (kd_gpt_*), token for token the greedy sequence of the loop
@@ -751,6 +757,62 @@ DEFER_SELECT_BRANCH = """                        if (std::optional<Tensor> defer
                         }
 """
 
+INDEX_LINE_HELPER = """// MI355X: indices that are one line broadcast over the other dims (every stride 0 but the
+// indexed dim's: index_select's and index_add_'s expanded 1-D indices) are range-checked on the
+// line itself, min and max in one device call and one sync, and handed to the kernel in place
+// (broadcast strides and all), instead of as a contiguous copy of the broadcast whose max and
+// min are read back one at a time. The line holds every value the broadcast does (the broadcast
+// is not empty), so the check passes and fails as kael's, max first. Returns the indices' first
+// element, or nullptr for any other indices (kael's path).
+const std::int64_t* checked_index_line(const Tensor& indices, std::size_t position, std::int64_t size,
+                                       const char* op) {
+    if (indices.device() == Device::CPU || indices.dtype() != DType::I64 || indices.numel() == 0) {
+        return nullptr;
+    }
+    for (std::size_t d = 0; d < indices.shape().size(); ++d) {
+        if (d != position && indices.shape()[d] != 1 && indices.strides()[d] != 0) {
+            return nullptr;
+        }
+    }
+    const auto* line = reinterpret_cast<const std::int64_t*>(indices.device_data());
+    std::int64_t bounds[2];
+    device::index_bounds(line, indices.shape()[position], indices.strides()[position], bounds);
+    detail::checked_index(bounds[1], size, op);
+    detail::checked_index(bounds[0], size, op);
+    return line;
+}
+
+"""
+
+GATHER_LINE_BRANCH = """        if (const std::int64_t* line = checked_index_line(indices, position, t.shape()[position], "gather")) {
+            device::gather(t.dtype(), gathered.device_data(), t.device_data(), line,
+                           detail::index_layout(t, indices, gathered, position));
+            autograd::record_gather(gathered, t, dim, indices);
+            return gathered;
+        }
+"""
+
+SCATTER_LINE_BRANCH = """        if (const std::int64_t* line = checked_index_line(indices, position, shape()[position], "scatter_add_")) {
+            device::scatter_add(dtype(), device_data(), line, source.device_data(),
+                                detail::index_layout(*this, indices, source, position));
+            impl_->storage->bump_version();
+            return *this;
+        }
+"""
+
+TARGET_BOUNDS = """    // MI355X: the targets' max and min of a device tensor in one call and one sync.
+    std::int64_t bounds[2];
+    if (targets.device() != Device::CPU && (targets.is_contiguous() || targets.dim() == 1)) {
+        device::index_bounds(reinterpret_cast<const std::int64_t*>(targets.device_data()), targets.numel(),
+                             targets.is_contiguous() ? 1 : targets.strides()[0], bounds);
+    } else {
+        bounds[1] = %(ns)smax(targets).item<std::int64_t>();
+        bounds[0] = %(ns)smin(targets).item<std::int64_t>();
+    }
+    const auto largest = bounds[1];
+    const auto smallest = bounds[0];
+"""
+
 GENERATE_BRANCH = """    if (auto out = device_generate(model, prompt, options)) {
         return *out;
     }
@@ -856,6 +918,21 @@ EDITS = [
     ("src/autograd/engine.cpp", "    const NoGradGuard guard;\n", "after", "    const DeferredSelectScope deferred_selects;\n"),
     ("src/autograd/engine.cpp", "            buffers.erase(buffered);\n", "after", "            write_if_deferred(incoming);\n"),
     ("src/autograd/functions_view.cpp", '#include "kael/ops.h"\n', "after", "\n#include <optional>\n"),
+    ("src/ops/indexing.cpp", '#include "kael/kernels.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/ops/indexing.cpp", "namespace kael {\n\nnamespace {\n", "after", INDEX_LINE_HELPER),
+    ("src/ops/indexing.cpp",
+     "        const Tensor flat = autograd::without_grad([&] { return indices.contiguous(); });\n"
+     "        detail::check_device_indices(flat, t.shape()[position], \"gather\");\n", "before", GATHER_LINE_BRANCH),
+    ("src/ops/inplace.cpp", '#include "kael/kernels.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/ops/inplace.cpp", "namespace kael {\n\nnamespace {\n", "after", INDEX_LINE_HELPER),
+    ("src/ops/inplace.cpp", "        const Tensor contiguous_indices = indices.contiguous();\n"
+     "        detail::check_device_indices(contiguous_indices, shape()[position], \"scatter_add_\");\n", "before",
+     SCATTER_LINE_BRANCH),
+    ("src/ops/nn.cpp", "    const auto largest = max(targets).item<std::int64_t>();\n"
+     "    const auto smallest = min(targets).item<std::int64_t>();\n", "replace", TARGET_BOUNDS % {"ns": ""}),
+    ("src/nn/loss.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
+    ("src/nn/loss.cpp", "    const auto largest = kael::max(targets).item<std::int64_t>();\n"
+     "    const auto smallest = kael::min(targets).item<std::int64_t>();\n", "replace", TARGET_BOUNDS % {"ns": "kael::"}),
     ("src/autograd/functions_view.cpp", "namespace kael::autograd {\n\n", "after", DEFER_SELECT_DECLARATION),
     ("src/autograd/functions_view.cpp",
      "                        Tensor full_gradient = zeros(shape, dtype, device);\n"

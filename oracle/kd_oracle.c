@@ -778,6 +778,23 @@ int oracle_reduce_columns(int op, int out_dtype, int in_dtype, void* results, co
     return rc;
 }
 
+/* kd_index_bounds: bounds[0] = min, bounds[1] = max of indices[i * stride], i < count: the two
+ * reductions kael reads back before a device gather / scatter_add (reference
+ * src/internal/index_checks.h:37-43: max(indices).item(), min(indices).item()) and on
+ * cross-entropy targets (src/ops/nn.cpp:97-98, src/nn/loss.cpp:27-28). */
+int oracle_index_bounds(const int64_t* indices, int64_t count, int64_t stride, int64_t* bounds) {
+    if (indices == NULL || bounds == NULL || count <= 0) return fail("index_bounds: needs indices and count > 0");
+    int64_t lo = indices[0], hi = indices[0];
+    for (int64_t i = 1; i < count; ++i) {
+        const int64_t v = indices[i * stride];
+        if (v < lo) lo = v;
+        if (v > hi) hi = v;
+    }
+    bounds[0] = lo;
+    bounds[1] = hi;
+    return KD_OK;
+}
+
 /* ---- matmul: kernels.inl:136-177 -------------------------------------------------------------- */
 
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,

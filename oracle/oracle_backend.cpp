@@ -244,8 +244,8 @@ namespace {
 // 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
 // 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
 // 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads, 16 layer_norm_rows,
-// 17 layer_norm_rows_backward, 18 matmul_strided_bias.
-constexpr int kExtensions = 19;
+// 17 layer_norm_rows_backward, 18 matmul_strided_bias, 19 index_bounds.
+constexpr int kExtensions = 20;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -461,6 +461,12 @@ void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const 
     check(oracle_reduce_columns(static_cast<int>(op), static_cast<int>(out), static_cast<int>(in), results, data, outer,
                                 inner),
           "reduce_columns");
+}
+
+void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t stride, std::int64_t bounds[2]) {
+    ++g_extension_calls[19];
+    KD_TRACE("index_bounds", kv("indices", tp(indices)) + "," + kv("count", count) + "," + kv("stride", stride));
+    check(oracle_index_bounds(indices, count, stride, bounds), "index_bounds");
 }
 
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {

@@ -5,6 +5,8 @@ gather along an inner axis with a transposed index tensor (tests/test_cuda.cpp:3
 i64 scatter_add wrapping (:482-490). Gather is bit-exact; f32 scatter_add with colliding indices
 adds in a different order than the oracle (atomics), so it is checked to 1e-5.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -137,3 +139,41 @@ def test_scatter_add_rows(kdb, oracle, dtype, case):
         np.testing.assert_array_equal(got, want)
     else:
         np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4)
+
+
+BOUNDS_CASES = [  # count, stride
+    (1, 1), (7, 1), (4096, 1), (16384, 1), (16385, 1), (1 << 20, 1), (9_000_001, 1), (1000, 3), (5000, 0), (3000, -2),
+]
+
+
+@pytest.mark.parametrize("count, stride", BOUNDS_CASES, ids=[f"{c}x{s}" for c, s in BOUNDS_CASES])
+def test_index_bounds(kdb, oracle, count, stride):
+    """kd_index_bounds (the min and max kael reads back before a device gather / scatter_add, one
+    call) against numpy's min / max of the same strided run and the oracle: exact, with the
+    int64 extremes planted at random positions for the larger runs; one workgroup up to 16384
+    elements, partial pairs and a combine launch above."""
+    rng = np.random.default_rng(count + stride)
+    span = (count - 1) * abs(stride) + 1
+    store = rng.integers(-(1 << 40), 1 << 40, span).astype(np.int64)
+    if count > 2 and stride != 0:
+        run = np.arange(count) * abs(stride)
+        lo, hi = rng.choice(count, 2, replace=False)
+        store[run[lo]], store[run[hi]] = np.iinfo(np.int64).min, np.iinfo(np.int64).max
+    first = 0 if stride >= 0 else (count - 1) * abs(stride)
+    values = store[first + np.arange(count) * stride]
+    want = np.array([values.min(), values.max()], np.int64)
+    dev = kdb.to_device(store)
+    got = np.zeros(2, np.int64)
+    kdb.call("index_bounds", dev.ptr + first * 8, count, stride, support.ptr(got))
+    np.testing.assert_array_equal(got, want)
+    orc = np.zeros(2, np.int64)
+    assert oracle.oracle_index_bounds(ctypes.c_void_p(store.ctypes.data + first * 8), count, stride,
+                                      support.ptr(orc)) == 0
+    np.testing.assert_array_equal(orc, want)
+
+
+def test_index_bounds_rejects_an_empty_run(kdb):
+    dev = kdb.to_device(np.zeros(4, np.int64))
+    got = np.zeros(2, np.int64)
+    with pytest.raises(kd.KdError):
+        kdb.call("index_bounds", dev.ptr, 0, 1, support.ptr(got))

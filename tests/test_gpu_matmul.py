@@ -264,6 +264,31 @@ def test_split_k_on_64_tiles(kdb):
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
 
 
+@pytest.mark.parametrize("m, k, n, sa, sb", [
+    (96, 4096, 256, (0, 1, 96), (0, 256, 1)),       # kael's tied LM-head weight gradient (A read transposed)
+    (130, 3072, 70, (0, 3072, 1), (0, 1, 3072)),    # ragged M and N, B read transposed
+    (33, 2560, 200, (0, 2, 67), (0, 200, 1)),       # generic A strides
+], ids=["head_96x4096x256", "ragged_130x3072x70", "generic_33x2560x200"])
+def test_split_k_on_the_general_kernel(kdb, m, k, n, sa, sb):
+    """Few ragged tiles with a long K: the general kernel splits K over the device (the splits in its
+    batch slot) and split_sum_kernel adds the partials in split order: within 1e-4 of the largest
+    |element| of the float64 product, and the same bits on a second run."""
+    rng = np.random.default_rng(m + k + n)
+
+    def extent(shape, st):
+        return 1 + sum((s - 1) * t for s, t in zip(shape, st))
+
+    a_store = rng.uniform(-1, 1, extent((1, m, k), sa)).astype(np.float32)
+    b_store = rng.uniform(-1, 1, extent((1, k, n), sb)).astype(np.float32)
+    got = _strided_product(kdb, a_store, b_store, 1, m, k, n, sa, sb)[0]
+    again = _strided_product(kdb, a_store, b_store, 1, m, k, n, sa, sb)[0]
+    np.testing.assert_array_equal(got, again)
+    a = np.lib.stride_tricks.as_strided(a_store, (m, k), (sa[1] * 4, sa[2] * 4)).astype(np.float64)
+    b = np.lib.stride_tricks.as_strided(b_store, (k, n), (sb[1] * 4, sb[2] * 4)).astype(np.float64)
+    want = a @ b
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+
+
 def test_headline_4096_cubed(kdb, refdev, oracle):
     """The benchmark's headline product (row-major MFMA kernel, whole tiles) at its full size,
     inputs as bench.py draws them. At K = 4096 an element's f32 rounding error scales with its
@@ -478,6 +503,7 @@ BIAS_CASES = [  # batches, m, k, n, a strides, b strides: kael's x . W^T shapes 
     (1, 64, 784, 128, (0, 784, 1), (0, 1, 784)),                # C3's first Linear
     (2, 33, 17, 3, (17 * 33, 17, 1), (0, 1, 17)),               # row-dot
     (2, 130, 70, 200, (130 * 70, 70, 1), (0, 1, 70)),           # ragged tiles, general kernel
+    (1, 96, 4096, 256, (0, 1, 96), (0, 256, 1)),                # ragged tiles, general kernel split K
 ]
 
 

@@ -190,3 +190,22 @@ def test_matmul_two_level_batches_against_numpy_views(oracle):
                                               st, swapped) == 0
     assert not np.array_equal(out.reshape(B, H, T, T), want)
     assert oracle.oracle_matmul_strided_heads(kd.I64, P(flat), P(flat), P(out), kd.MatmulSizes(5, T, D, T), st, heads) != 0
+
+
+@pytest.mark.parametrize("count, stride", [(1, 1), (9, 1), (50, 3), (40, 0), (30, -2)])
+def test_index_bounds_is_min_and_max(oracle, count, stride):
+    """oracle_index_bounds (kael's range check: max and min of the indices) against numpy's
+    min / max of the same strided run, with int64's extremes in the run."""
+    rng = np.random.default_rng(count)
+    span = (count - 1) * abs(stride) + 1
+    store = rng.integers(-1000, 1000, span).astype(np.int64)
+    if count > 2 and stride != 0:
+        store[abs(stride)] = np.iinfo(np.int64).min
+        store[2 * abs(stride)] = np.iinfo(np.int64).max
+    first = 0 if stride >= 0 else (count - 1) * abs(stride)
+    values = store[first + np.arange(count) * stride]
+    got = np.zeros(2, np.int64)
+    assert oracle.oracle_index_bounds(ctypes.c_void_p(store.ctypes.data + first * 8), count, stride,
+                                      support.ptr(got)) == 0
+    assert got.tolist() == [values.min(), values.max()]
+    assert oracle.oracle_index_bounds(ctypes.c_void_p(store.ctypes.data), 0, 1, support.ptr(got)) != 0
