@@ -291,6 +291,23 @@ int kd_scatter_add(int dtype, void* data, const int64_t* indices, const void* so
  * src/nn/loss.cpp:27-28); the caller checks the pair in the same order, max first. */
 int kd_index_bounds(const int64_t* indices, int64_t count, int64_t stride, int64_t* bounds);
 
+/* kael's causal self-attention without a KV cache or dropout (reference
+ * src/nn/transformer.cpp:114-136: the fused projection viewed [B, T, 3, H, D], q / k / v selected
+ * and transposed per head, softmax(masked_fill(q . k^T / sqrt(D), triu mask, -inf)) . v, the heads
+ * merged with transpose(1, 2).contiguous()) in one launch instead of the two products, the scale,
+ * the mask, the row softmax and the merge copy. qkv [B, T, 3, H, D] and out [B, T, H * D] are
+ * contiguous and 16-byte aligned; lse [B, H, T] receives each row's log-sum-exp (scaled, masked
+ * scores) for the backward. f32 and D = 64 only (KD_E_UNSUPPORTED otherwise). */
+int kd_causal_attention(int dtype, void* out, void* lse, const void* qkv, int64_t batch, int64_t length,
+                        int64_t heads, int64_t head_dim);
+
+/* Its backward (kael's autograd for the same chain: the two products' MatmulBackward,
+ * SoftmaxBackward, MaskedFillBackward, the division's backward and the select / transpose
+ * backward into one tensor): dqkv [B, T, 3, H, D], every element written, from dout
+ * [B, T, H * D] and the forward's qkv, out and lse, in two launches. */
+int kd_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
+                                 const void* lse, int64_t batch, int64_t length, int64_t heads, int64_t head_dim);
+
 /* ---- fused row kernels (extensions replacing composed device paths) ---- */
 
 /* Row softmax over `rows` contiguous rows of `cols`: max, exp(x-max), sum in double,

@@ -1,0 +1,383 @@
+// kd_attention.hip - kael's causal self-attention (reference src/nn/transformer.cpp:103-138: the
+// fused projection's output viewed [B, T, 3, H, D], q / k / v selected and transposed per head,
+// softmax(mask(q . k^T / sqrt(D))) . v, the heads merged back to [B, T, H * D]) as one kernel
+// forward and two backward, for f32 and D = 64, without a KV cache or dropout.
+//
+// Forward: one wave per (batch, head, block of 32 queries). The wave walks the key blocks of 32
+// up to its diagonal: S^T = K_J . Q_I^T on v_mfma_f32_32x32x2f32 (each lane then holds 16 scores
+// of one query: lane (li, lh), register r is key 8 (r / 4) + 4 lh + r % 4 of query li), the
+// scale and the causal mask, an online softmax per query (running max and sum, the output
+// rescaled when the max grows), and O^T += V_J^T . P^T, whose B operand is the score register
+// itself. The output is written in the merged-head layout and the row's log-sum-exp m + log(l)
+// is kept for the backward.
+//
+// Backward (the gradient of every op of kael's chain: the products, the scale, the mask and
+// softmax backward y (g - sum(g y))): with delta_i = sum_d dO[i][d] O[i][d] (= sum_j P dP over
+// the row) and P recomputed from the log-sum-exp, dS = P (dP - delta) / sqrt(D);
+//   dq kernel, one wave per (batch, head, query block): delta (kept for the next launch), then
+//     for each key block S^T, dP^T = V_J . dO_I^T, dS^T, and dQ += dS . K_J;
+//   dkv kernel, one wave per (batch, head, key block): for each query block at or after it S,
+//     dP = dO_I . V_J^T, dS, dV += P^T . dO_I and dK += dS^T . Q_I.
+// Every MFMA sums over 64 features (or 32 keys / queries) with the operands' features split as
+// k-pairs (s, 32 + s), which is a reordering of the same sum.
+#include <algorithm>
+#include <cmath>
+
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 64;      // head dim
+constexpr int kBlock = 32;  // queries / keys per block
+
+__device__ __forceinline__ v16f mfma(float a, float b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v16f zero16() {
+    v16f z;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) z[r] = 0.f;
+    return z;
+}
+
+// Row `t` (features 32 * lh .. 32 * lh + 31) of a [T, D] head matrix with row stride `ld`, or
+// zeros past the last row: the lane-per-row operand of a product that sums over features.
+__device__ __forceinline__ void load_half_row(float (&reg)[32], const float* __restrict__ base, int t, int length,
+                                              int64_t ld, int lh) {
+    if (t < length) {
+        const v4f* src = reinterpret_cast<const v4f*>(base + t * ld + 32 * lh);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const v4f v = src[q];
+            reg[4 * q] = v[0];
+            reg[4 * q + 1] = v[1];
+            reg[4 * q + 2] = v[2];
+            reg[4 * q + 3] = v[3];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 32; ++s) reg[s] = 0.f;
+    }
+}
+
+// Row of block position 8 (s / 4) + 4 lh + s % 4: the k index of MFMA step s in the products
+// whose k runs over a block of 32 (the score registers' layout).
+__device__ __forceinline__ int block_row(int s, int lh) { return 8 * (s / 4) + 4 * lh + (s % 4); }
+
+struct AttentionShape {
+    int batch, length, heads;
+    int64_t row;  // qkv elements per token: 3 * heads * D
+    int64_t out_row;  // merged-head elements per token: heads * D
+    float scale;  // sqrt(D) rounded to float: kael divides the scores by it
+};
+
+// ---- forward -----------------------------------------------------------------------------
+
+__global__ __launch_bounds__(64) void attention_forward_kernel(float* __restrict__ out, float* __restrict__ lse,
+                                                               const float* __restrict__ qkv, AttentionShape sh) {
+    const int blocks = (sh.length + kBlock - 1) / kBlock;
+    const int bh = blockIdx.x / blocks;
+    const int qb = blocks - 1 - static_cast<int>(blockIdx.x % blocks);  // longest rows first
+    const int b = bh / sh.heads, h = bh % sh.heads;
+    const int lane = threadIdx.x, li = lane % 32, lh = lane / 32;
+    const float* q = qkv + static_cast<int64_t>(b) * sh.length * sh.row + h * kD;
+    const float* k = q + sh.heads * kD;
+    const float* v = k + sh.heads * kD;
+    const int i0 = qb * kBlock;
+    const int query = i0 + li;
+
+    float qreg[32];
+    load_half_row(qreg, q, query, sh.length, sh.row, lh);
+
+    v16f o[2] = {zero16(), zero16()};
+    float m = -INFINITY, l = 0.f;
+    for (int kb = 0; kb <= qb; ++kb) {
+        const int j0 = kb * kBlock;
+        float kreg[32];
+        load_half_row(kreg, k, j0 + li, sh.length, sh.row, lh);
+        v16f s = zero16();
+#pragma unroll
+        for (int t = 0; t < 32; ++t) s = mfma(kreg[t], qreg[t], s);
+        // scale, mask, block max of this query's scores (16 here, 16 in lane li + 32)
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = j0 + block_row(r, lh);
+            const float x = (key > query || key >= sh.length) ? -INFINITY : s[r] / sh.scale;
+            s[r] = x;
+            bmax = fmaxf(bmax, x);
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float mnew = fmaxf(m, bmax);
+        const float alpha = mnew == -INFINITY ? 1.f : expf(m - mnew);
+        float bsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = s[r] == -INFINITY ? 0.f : expf(s[r] - mnew);
+            s[r] = p;
+            bsum += p;
+        }
+        bsum += __shfl_xor(bsum, 32);
+        l = l * alpha + bsum;
+        m = mnew;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        }
+        // O^T[d][i] += sum_j V[j][d] P[i][j]: A = V^T (lane li: feature 32 dt + li), B = P^T
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int key = j0 + block_row(t, lh);
+                const float vv = key < sh.length ? v[key * sh.row + 32 * dt + li] : 0.f;
+                o[dt] = mfma(vv, s[t], o[dt]);
+            }
+        }
+    }
+    // o[dt][r] = O^T[32 dt + block_row(r, lh)][query li]: this lane's query, 4 consecutive
+    // features per register quad
+    if (query < sh.length) {
+        const float inv = 1.f / l;
+        float* dst = out + (static_cast<int64_t>(b) * sh.length + query) * sh.out_row + h * kD;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                v4f w;
+                w[0] = o[dt][4 * qd] * inv;
+                w[1] = o[dt][4 * qd + 1] * inv;
+                w[2] = o[dt][4 * qd + 2] * inv;
+                w[3] = o[dt][4 * qd + 3] * inv;
+                *reinterpret_cast<v4f*>(dst + 32 * dt + 8 * qd + 4 * lh) = w;
+            }
+        }
+        if (lh == 0) lse[static_cast<int64_t>(bh) * sh.length + query] = m + logf(l);
+    }
+}
+
+// ---- backward: delta and dQ ---------------------------------------------------------------
+
+__global__ __launch_bounds__(64) void attention_dq_kernel(float* __restrict__ dqkv, float* __restrict__ delta,
+                                                          const float* __restrict__ dout, const float* __restrict__ qkv,
+                                                          const float* __restrict__ out, const float* __restrict__ lse,
+                                                          AttentionShape sh) {
+    const int blocks = (sh.length + kBlock - 1) / kBlock;
+    const int bh = blockIdx.x / blocks;
+    const int qb = blocks - 1 - static_cast<int>(blockIdx.x % blocks);
+    const int b = bh / sh.heads, h = bh % sh.heads;
+    const int lane = threadIdx.x, li = lane % 32, lh = lane / 32;
+    const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
+    const float* q = qkv + tok0 * sh.row + h * kD;
+    const float* k = q + sh.heads * kD;
+    const float* v = k + sh.heads * kD;
+    const float* go = dout + tok0 * sh.out_row + h * kD;
+    const float* o = out + tok0 * sh.out_row + h * kD;
+    const int i0 = qb * kBlock;
+    const int query = i0 + li;
+
+    float qreg[32], doreg[32];
+    load_half_row(qreg, q, query, sh.length, sh.row, lh);
+    load_half_row(doreg, go, query, sh.length, sh.out_row, lh);
+    float dl;
+    {
+        float oreg[32];
+        load_half_row(oreg, o, query, sh.length, sh.out_row, lh);
+        float part = 0.f;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) part += doreg[t] * oreg[t];
+        dl = part + __shfl_xor(part, 32);
+    }
+    const float row_lse = query < sh.length ? lse[static_cast<int64_t>(bh) * sh.length + query] : 0.f;
+    if (query < sh.length && lh == 0) delta[static_cast<int64_t>(bh) * sh.length + query] = dl;
+
+    v16f dq[2] = {zero16(), zero16()};
+    for (int kb = 0; kb <= qb; ++kb) {
+        const int j0 = kb * kBlock;
+        float kreg[32], vreg[32];
+        load_half_row(kreg, k, j0 + li, sh.length, sh.row, lh);
+        load_half_row(vreg, v, j0 + li, sh.length, sh.row, lh);
+        v16f s = zero16(), dp = zero16();
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            s = mfma(kreg[t], qreg[t], s);
+            dp = mfma(vreg[t], doreg[t], dp);
+        }
+        // s[r] = S[query][key], dp[r] = dP[query][key] for key j0 + block_row(r, lh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = j0 + block_row(r, lh);
+            const bool live = key <= query && key < sh.length && query < sh.length;
+            const float p = live ? expf(s[r] / sh.scale - row_lse) : 0.f;
+            s[r] = p * (dp[r] - dl) / sh.scale;
+        }
+        // dQ[i][d] += sum_j dS[i][j] K[j][d]: A = dS (lane li: query li), B = K (feature 32 dt + li)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int key = j0 + block_row(t, lh);
+                const float kk = key < sh.length ? k[key * sh.row + 32 * dt + li] : 0.f;
+                dq[dt] = mfma(s[t], kk, dq[dt]);
+            }
+        }
+    }
+    // dq[dt][r] = dQ[i0 + block_row(r, lh)][32 dt + li]
+    float* dst = dqkv + tok0 * sh.row + h * kD;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = i0 + block_row(r, lh);
+        if (row < sh.length) {
+            dst[row * sh.row + li] = dq[0][r];
+            dst[row * sh.row + 32 + li] = dq[1][r];
+        }
+    }
+}
+
+// ---- backward: dK and dV ------------------------------------------------------------------
+
+__global__ __launch_bounds__(64) void attention_dkv_kernel(float* __restrict__ dqkv, const float* __restrict__ delta,
+                                                           const float* __restrict__ dout, const float* __restrict__ qkv,
+                                                           const float* __restrict__ lse, AttentionShape sh) {
+    const int blocks = (sh.length + kBlock - 1) / kBlock;
+    const int bh = blockIdx.x / blocks;
+    const int kb = static_cast<int>(blockIdx.x % blocks);  // key block 0 has the most query blocks
+    const int b = bh / sh.heads, h = bh % sh.heads;
+    const int lane = threadIdx.x, li = lane % 32, lh = lane / 32;
+    const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
+    const float* q = qkv + tok0 * sh.row + h * kD;
+    const float* k = q + sh.heads * kD;
+    const float* v = k + sh.heads * kD;
+    const float* go = dout + tok0 * sh.out_row + h * kD;
+    const float* row_lse = lse + static_cast<int64_t>(bh) * sh.length;
+    const float* row_delta = delta + static_cast<int64_t>(bh) * sh.length;
+    const int j0 = kb * kBlock;
+    const int key = j0 + li;
+
+    float kreg[32], vreg[32];
+    load_half_row(kreg, k, key, sh.length, sh.row, lh);
+    load_half_row(vreg, v, key, sh.length, sh.row, lh);
+
+    v16f dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
+    for (int qb = kb; qb < blocks; ++qb) {
+        const int i0 = qb * kBlock;
+        float qreg[32], doreg[32];
+        load_half_row(qreg, q, i0 + li, sh.length, sh.row, lh);
+        load_half_row(doreg, go, i0 + li, sh.length, sh.out_row, lh);
+        v16f s = zero16(), dp = zero16();
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            s = mfma(qreg[t], kreg[t], s);
+            dp = mfma(doreg[t], vreg[t], dp);
+        }
+        // s[r] = S[query][key], dp[r] = dP[query][key] for query i0 + block_row(r, lh), key li
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int query = i0 + block_row(r, lh);
+            const bool live = key <= query && query < sh.length && key < sh.length;
+            const float lq = query < sh.length ? row_lse[query] : 0.f;
+            const float dq = query < sh.length ? row_delta[query] : 0.f;
+            p[r] = live ? expf(s[r] / sh.scale - lq) : 0.f;
+            s[r] = p[r] * (dp[r] - dq) / sh.scale;
+        }
+        // dV[j][d] += sum_i P[i][j] dO[i][d], dK[j][d] += sum_i dS[i][j] Q[i][d]:
+        // A = P^T / dS^T (lane li: key li), B = dO / Q (feature 32 dt + li)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int query = i0 + block_row(t, lh);
+                const bool in = query < sh.length;
+                const float gov = in ? go[query * sh.out_row + 32 * dt + li] : 0.f;
+                const float qv = in ? q[query * sh.row + 32 * dt + li] : 0.f;
+                dv[dt] = mfma(p[t], gov, dv[dt]);
+                dk[dt] = mfma(s[t], qv, dk[dt]);
+            }
+        }
+    }
+    // dk[dt][r] = dK[j0 + block_row(r, lh)][32 dt + li]
+    float* dstk = dqkv + tok0 * sh.row + sh.heads * kD + h * kD;
+    float* dstv = dstk + sh.heads * kD;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = j0 + block_row(r, lh);
+        if (row < sh.length) {
+            dstk[row * sh.row + li] = dk[0][r];
+            dstk[row * sh.row + 32 + li] = dk[1][r];
+            dstv[row * sh.row + li] = dv[0][r];
+            dstv[row * sh.row + 32 + li] = dv[1][r];
+        }
+    }
+}
+
+int check_shape(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t head_dim, AttentionShape& sh,
+                const char* what) {
+    if (dtype != KD_F32) return fail(KD_E_UNSUPPORTED, std::string(what) + ": dtype must be f32");
+    if (head_dim != kD) return fail(KD_E_UNSUPPORTED, std::string(what) + ": head dim must be 64");
+    if (batch < 1 || length < 1 || heads < 1) return fail(KD_E_INVALID, std::string(what) + ": empty shape");
+    const int64_t blocks = (length + kBlock - 1) / kBlock;
+    const int64_t row = 3 * heads * kD;
+    if (batch * heads * blocks >= (int64_t{1} << 31) || length * row >= (int64_t{1} << 31) || batch > INT32_MAX)
+        return fail(KD_E_INVALID, std::string(what) + ": shape too large");
+    sh.batch = static_cast<int>(batch);
+    sh.length = static_cast<int>(length);
+    sh.heads = static_cast<int>(heads);
+    sh.row = row;
+    sh.out_row = heads * kD;
+    sh.scale = static_cast<float>(std::sqrt(static_cast<double>(head_dim)));
+    return KD_OK;
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+} // namespace
+
+} // namespace kd
+
+using namespace kd;
+
+extern "C" int kd_causal_attention(int dtype, void* out, void* lse, const void* qkv, int64_t batch, int64_t length,
+                                   int64_t heads, int64_t head_dim) {
+    AttentionShape sh;
+    if (int rc = check_shape(dtype, batch, length, heads, head_dim, sh, "kd_causal_attention")) return rc;
+    if (!aligned16(out) || !aligned16(qkv) || lse == nullptr)
+        return fail(KD_E_INVALID, "kd_causal_attention: out and qkv must be 16-byte aligned, lse given");
+    if (int rc = ensure_device()) return rc;
+    const int64_t blocks = (length + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(attention_forward_kernel, dim3(static_cast<uint32_t>(batch * heads * blocks)), dim3(64), 0,
+                       stream(), static_cast<float*>(out), static_cast<float*>(lse), static_cast<const float*>(qkv), sh);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+extern "C" int kd_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
+                                            const void* lse, int64_t batch, int64_t length, int64_t heads,
+                                            int64_t head_dim) {
+    AttentionShape sh;
+    if (int rc = check_shape(dtype, batch, length, heads, head_dim, sh, "kd_causal_attention_backward")) return rc;
+    if (!aligned16(dqkv) || !aligned16(dout) || !aligned16(qkv) || !aligned16(out) || lse == nullptr)
+        return fail(KD_E_INVALID, "kd_causal_attention_backward: operands must be 16-byte aligned, lse given");
+    if (int rc = ensure_device()) return rc;
+    const int64_t blocks = (length + kBlock - 1) / kBlock;
+    Workspace ws;  // delta, held until the dkv kernel is enqueued
+    if (int rc = workspace(ws, static_cast<size_t>(batch * heads * length) * sizeof(float))) return rc;
+    float* delta = static_cast<float*>(ws.ptr);
+    const dim3 grid(static_cast<uint32_t>(batch * heads * blocks));
+    hipLaunchKernelGGL(attention_dq_kernel, grid, dim3(64), 0, stream(), static_cast<float*>(dqkv), delta,
+                       static_cast<const float*>(dout), static_cast<const float*>(qkv), static_cast<const float*>(out),
+                       static_cast<const float*>(lse), sh);
+    KD_LAUNCH_CHECK();
+    hipLaunchKernelGGL(attention_dkv_kernel, grid, dim3(64), 0, stream(), static_cast<float*>(dqkv),
+                       static_cast<const float*>(delta), static_cast<const float*>(dout), static_cast<const float*>(qkv),
+                       static_cast<const float*>(lse), sh);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}

@@ -252,6 +252,20 @@ void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const 
           "reduce_columns");
 }
 
+void causal_attention(DType dtype, std::byte* out, std::byte* lse, const std::byte* qkv, std::int64_t batch,
+                      std::int64_t length, std::int64_t heads, std::int64_t head_dim) {
+    check(kd_causal_attention(static_cast<int>(dtype), out, lse, qkv, batch, length, heads, head_dim),
+          "causal_attention");
+}
+
+void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* dout, const std::byte* qkv,
+                               const std::byte* out, const std::byte* lse, std::int64_t batch, std::int64_t length,
+                               std::int64_t heads, std::int64_t head_dim) {
+    check(kd_causal_attention_backward(static_cast<int>(dtype), dqkv, dout, qkv, out, lse, batch, length, heads,
+                                       head_dim),
+          "causal_attention_backward");
+}
+
 void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t stride, std::int64_t bounds[2]) {
     check(kd_index_bounds(indices, count, stride, bounds), "index_bounds");
 }

@@ -139,6 +139,18 @@ void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const 
 // call and one sync instead of two reductions read back one at a time.
 void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t stride, std::int64_t bounds[2]);
 
+// kael's causal self-attention without a KV cache or dropout (reference src/nn/transformer.cpp:
+// 114-136) over the fused projection's output qkv [B, T, 3, H, D] (contiguous): out [B, T, H * D]
+// with the heads merged, lse [B, H, T] the rows' log-sum-exp for the backward. f32, D = 64.
+void causal_attention(DType dtype, std::byte* out, std::byte* lse, const std::byte* qkv, std::int64_t batch,
+                      std::int64_t length, std::int64_t heads, std::int64_t head_dim);
+
+// Its backward: dqkv [B, T, 3, H, D] (every element written) from dout [B, T, H * D] (contiguous)
+// and the forward's qkv, out and lse.
+void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* dout, const std::byte* qkv,
+                               const std::byte* out, const std::byte* lse, std::int64_t batch, std::int64_t length,
+                               std::int64_t heads, std::int64_t head_dim);
+
 // Running sums along `rows` contiguous rows of `size` elements (reference src/ops/sequence.cpp:95-117):
 // f32 / f64 store In, i64 / bool wrapping int64.
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows);

@@ -73,6 +73,7 @@ POINTERS = {
     "matmul_strided_bias": ("a", "b", "c", "bias"),
     "gather": ("out", "data", "indices"),
     "scatter_add": ("data", "indices", "source"), "index_bounds": ("indices",),
+    "causal_attention": ("out", "lse", "qkv"), "causal_attention_backward": ("dqkv", "dout", "qkv", "out", "lse"),
     "softmax_rows": ("out", "x"), "standardize_rows": ("out", "x"),
     "cross_entropy_rows": ("losses", "logits", "targets"), "cross_entropy_grad": ("out", "logits", "targets", "weights"),
     "softmax_rows_backward": ("out", "y", "grad"), "standardize_rows_backward": ("out", "x", "y", "grad"),
@@ -237,6 +238,14 @@ class Replay:
         if op == "reduce_columns":
             a = (r["rop"], r["out"], r["in"], c_void_p(P(r["results"])), c_void_p(P(r["data"])), r["outer"], r["inner"])
             return (lambda: chk(lib.kd_reduce_columns(*a), "kd_reduce_columns")), None
+        if op in ("causal_attention", "causal_attention_backward"):
+            shape = (r["batch"], r["length"], r["heads"], r["head_dim"])
+            if op == "causal_attention":
+                a = (r["dtype"], c_void_p(P(r["out"])), c_void_p(P(r["lse"])), c_void_p(P(r["qkv"]))) + shape
+                return (lambda: chk(lib.kd_causal_attention(*a), "kd_causal_attention")), None
+            a = (r["dtype"], c_void_p(P(r["dqkv"])), c_void_p(P(r["dout"])), c_void_p(P(r["qkv"])), c_void_p(P(r["out"])),
+                 c_void_p(P(r["lse"]))) + shape
+            return (lambda: chk(lib.kd_causal_attention_backward(*a), "kd_causal_attention_backward")), None
         if op == "index_bounds":
             pair = (c_int64 * 2)()
             a = (c_void_p(P(r["indices"])), r["count"], r["stride"], pair)

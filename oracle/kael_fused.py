@@ -42,7 +42,10 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      of a contiguous copy checked by two reductions and two reads
   src/ops/nn.cpp, src/nn/loss.cpp    the cross-entropy targets' range check (:97-98, :27-28) in one
                                      call
-  src/nn/transformer.cpp             nn::generate (:256-295) with temperature 0, the KV cache and a
+  src/nn/transformer.cpp             CausalSelfAttention::forward (:103-138) without a cache or
+                                     dropout, f32 heads of 64: one device call forward and one node
+                                     (two launches) backward (kd_causal_attention);
+                                     nn::generate (:256-295) with temperature 0, the KV cache and a
                                      batch-1 prompt on the device runs on the decode engine
                                      (kd_gpt_*), token for token the greedy sequence of the loop
 
@@ -813,6 +816,53 @@ TARGET_BOUNDS = """    // MI355X: the targets' max and min of a device tensor in
     const auto smallest = bounds[0];
 """
 
+ATTENTION_HELPER = """
+// MI355X: the attention of CausalSelfAttention::forward without a KV cache or dropout, for f32
+// heads of 64, as one device call over the fused projection's output parts [B, T, 3, H, D]
+// (contiguous): the output comes back with the heads merged ([B, T, H * D], what
+// transpose(1, 2).contiguous() gives), and one node takes the whole chain's backward (two
+// launches writing the q, k and v gradients into one [B, T, 3, H, D] tensor) instead of the
+// products, scale, mask, softmax, merge copy and three select gradients. nullopt for any other
+// case, which keeps kael's ops.
+std::optional<Tensor> device_causal_attention(const Tensor& parts, std::int64_t heads, std::int64_t head_dim) {
+    if (parts.device() == Device::CPU || parts.dtype() != DType::F32 || head_dim != 64 || parts.numel() == 0 ||
+        !parts.is_contiguous() || reinterpret_cast<std::uintptr_t>(parts.device_data()) % 16 != 0) {
+        return std::nullopt;
+    }
+    const std::int64_t batch = parts.size(0);
+    const std::int64_t length = parts.size(1);
+    Tensor out = empty({batch, length, heads * head_dim}, DType::F32, parts.device());
+    const Tensor lse = empty({batch, heads, length}, DType::F32, parts.device());
+    device::causal_attention(DType::F32, out.device_data(), lse.device_data(), parts.device_data(), batch, length,
+                             heads, head_dim);
+    if (autograd::should_record(out, {&parts})) {
+        autograd::set_history(
+            out, "CausalAttentionBackward", {parts},
+            {[saved_qkv = autograd::SavedTensor(parts), saved_out = autograd::SavedTensor(out), lse,
+              shape = parts.shape(), batch, length, heads, head_dim](const Tensor& g) {
+                Tensor gc = g.contiguous();
+                if (reinterpret_cast<std::uintptr_t>(gc.device_data()) % 16 != 0) {
+                    gc = g.clone();
+                }
+                Tensor dqkv = empty(shape, DType::F32, g.device());
+                device::causal_attention_backward(DType::F32, dqkv.device_data(), gc.device_data(),
+                                                  saved_qkv.get().device_data(), saved_out.get().device_data(),
+                                                  lse.device_data(), batch, length, heads, head_dim);
+                return dqkv;
+            }});
+    }
+    return out;
+}
+"""
+
+ATTENTION_BRANCH = """    if (cache == nullptr && (dropout_ == 0.0 || !is_training())) {
+        if (std::optional<Tensor> mixed = device_causal_attention(parts, heads_, head_dimension_)) {
+            const Tensor output = projection_->forward(mixed->view({batch, length, dimension_}));
+            return functional::dropout(output, dropout_, is_training());
+        }
+    }
+"""
+
 GENERATE_BRANCH = """    if (auto out = device_generate(model, prompt, options)) {
         return *out;
     }
@@ -901,6 +951,11 @@ EDITS = [
     ("src/nn/transformer.cpp", "#include <map>\n", "after", "#include <optional>\n#include <vector>\n"),
     ("src/nn/transformer.cpp", '#include "kael/autograd/grad_mode.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/nn/transformer.cpp", "class TrainingModeRestorer {\n", "before", GENERATE_HELPER),
+    ("src/nn/transformer.cpp", '#include "kael/random.h"\n', "after", '\n#include "recording.h"\n'),
+    ("src/nn/transformer.cpp", "constexpr double kInitialStd = 0.02;\n", "after", ATTENTION_HELPER),
+    ("src/nn/transformer.cpp",
+     "        query_key_value_->forward(input).view({batch, length, 3, heads_, head_dimension_});\n", "after",
+     ATTENTION_BRANCH),
     ("src/nn/transformer.cpp", "    const std::int64_t context = model.config().max_positions;\n", "after",
      GENERATE_BRANCH),
     ("src/ops/sequence.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),

@@ -795,6 +795,165 @@ int oracle_index_bounds(const int64_t* indices, int64_t count, int64_t stride, i
     return KD_OK;
 }
 
+/* ---- causal self-attention: kael's composed chain -------------------------------------------
+ *
+ * kael's CausalSelfAttention::forward without a cache or dropout (reference
+ * src/nn/transformer.cpp:114-136), each op as kael's device path computes it, per (batch, head):
+ * Q, K, V = the head's rows of the fused projection qkv [B, T, 3, H, D] (select + transpose);
+ * S = Q . K^T (oracle_matmul, the device kernel's order); S / sqrt(D) rounded to f32 (the scalar
+ * division); masked_fill of key > query with -inf (the triu(ones, 1) mask, :25-27); softmax rows
+ * (oracle_softmax_rows); O = P . V; out[b, t, h, :] = O[t] (transpose(1, 2).contiguous()). lse
+ * is the log-sum-exp of each scaled, masked row in double (not a kael value: the input of the
+ * fused backward, which recomputes P from it). The backward restates kael's autograd for the
+ * same chain: MatmulBackward of O = P . V (dP = dO . V^T, dV = P^T . dO), SoftmaxBackward
+ * (oracle_softmax_rows_backward), MaskedFillBackward (masked -> 0), the division's backward
+ * (dS / sqrt(D)), MatmulBackward of S = Q . K^T (dQ = dS . K, dK = dS^T . Q), and the select /
+ * transpose backward into dqkv. f32 only. */
+static int64_t attention_index(int64_t b, int64_t t, int64_t part, int64_t h, int64_t d, int64_t length,
+                               int64_t heads, int64_t head_dim) {
+    return (((b * length + t) * 3 + part) * heads + h) * head_dim + d;
+}
+
+static int attention_args(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t head_dim) {
+    if (dtype != KD_F32) return fail("causal_attention: f32 only");
+    if (batch < 1 || length < 1 || heads < 1 || head_dim < 1) return fail("causal_attention: empty shape");
+    return KD_OK;
+}
+
+/* a [rows, cols] row-major copy of the head's `part` (0 q, 1 k, 2 v) rows, or its transpose */
+static void head_matrix(float* dst, const float* qkv, int64_t b, int64_t part, int64_t h, int64_t length,
+                        int64_t heads, int64_t head_dim, int transposed) {
+    for (int64_t t = 0; t < length; ++t)
+        for (int64_t d = 0; d < head_dim; ++d) {
+            const float v = qkv[attention_index(b, t, part, h, d, length, heads, head_dim)];
+            if (transposed) dst[d * length + t] = v;
+            else dst[t * head_dim + d] = v;
+        }
+}
+
+static void transpose_f32(float* dst, const float* src, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) dst[c * rows + r] = src[r * cols + c];
+}
+
+/* P (the softmax of the scaled, masked scores) of one head and, when lse != NULL, its rows' lse */
+static int attention_weights(float* p, float* scores, double* lse, const float* q, const float* kt, int64_t length,
+                             int64_t head_dim) {
+    kd_matmul_sizes s = {1, length, head_dim, length};
+    int rc = oracle_matmul(KD_F32, q, kt, scores, &s, 0);
+    if (rc != KD_OK) return rc;
+    const float scale = (float)sqrt((double)head_dim);
+    for (int64_t i = 0; i < length; ++i)
+        for (int64_t j = 0; j < length; ++j) {
+            const float x = scores[i * length + j] / scale;
+            scores[i * length + j] = j > i ? -INFINITY : x;
+        }
+    if (lse != NULL)
+        for (int64_t i = 0; i < length; ++i) {
+            double m = -INFINITY, sum = 0.0;
+            for (int64_t j = 0; j <= i; ++j) m = fmax(m, (double)scores[i * length + j]);
+            for (int64_t j = 0; j <= i; ++j) sum += exp((double)scores[i * length + j] - m);
+            lse[i] = m + log(sum);
+        }
+    return oracle_softmax_rows(KD_F32, p, scores, length, length, 0);
+}
+
+int oracle_causal_attention(int dtype, void* out, void* lse, const void* qkv, int64_t batch, int64_t length,
+                            int64_t heads, int64_t head_dim) {
+    int rc = attention_args(dtype, batch, length, heads, head_dim);
+    if (rc != KD_OK) return rc;
+    const float* x = (const float*)qkv;
+    const size_t tt = (size_t)(length * length), td = (size_t)(length * head_dim);
+    float* q = (float*)malloc(td * 4);
+    float* kt = (float*)malloc(td * 4);
+    float* v = (float*)malloc(td * 4);
+    float* scores = (float*)malloc(tt * 4);
+    float* p = (float*)malloc(tt * 4);
+    float* o = (float*)malloc(td * 4);
+    double* row_lse = (double*)malloc((size_t)length * 8);
+    for (int64_t b = 0; b < batch && rc == KD_OK; ++b)
+        for (int64_t h = 0; h < heads && rc == KD_OK; ++h) {
+            head_matrix(q, x, b, 0, h, length, heads, head_dim, 0);
+            head_matrix(kt, x, b, 1, h, length, heads, head_dim, 1);
+            head_matrix(v, x, b, 2, h, length, heads, head_dim, 0);
+            rc = attention_weights(p, scores, row_lse, q, kt, length, head_dim);
+            if (rc != KD_OK) break;
+            kd_matmul_sizes s = {1, length, length, head_dim};
+            rc = oracle_matmul(KD_F32, p, v, o, &s, 0);
+            for (int64_t t = 0; t < length; ++t) {
+                for (int64_t d = 0; d < head_dim; ++d)
+                    ((float*)out)[((b * length + t) * heads + h) * head_dim + d] = o[t * head_dim + d];
+                ((float*)lse)[(b * heads + h) * length + t] = (float)row_lse[t];
+            }
+        }
+    free(q); free(kt); free(v); free(scores); free(p); free(o); free(row_lse);
+    return rc;
+}
+
+int oracle_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
+                                     const void* lse, int64_t batch, int64_t length, int64_t heads, int64_t head_dim) {
+    (void)out;
+    (void)lse;
+    int rc = attention_args(dtype, batch, length, heads, head_dim);
+    if (rc != KD_OK) return rc;
+    const float* x = (const float*)qkv;
+    const size_t tt = (size_t)(length * length), td = (size_t)(length * head_dim);
+    float* q = (float*)malloc(td * 4);
+    float* k = (float*)malloc(td * 4);
+    float* kt = (float*)malloc(td * 4);
+    float* v = (float*)malloc(td * 4);
+    float* vt = (float*)malloc(td * 4);
+    float* go = (float*)malloc(td * 4);
+    float* scores = (float*)malloc(tt * 4);
+    float* p = (float*)malloc(tt * 4);
+    float* pt = (float*)malloc(tt * 4);
+    float* dp = (float*)malloc(tt * 4);
+    float* ds = (float*)malloc(tt * 4);
+    float* dst = (float*)malloc(tt * 4);
+    float* grad = (float*)malloc(td * 4);
+    const float scale = (float)sqrt((double)head_dim);
+    for (int64_t b = 0; b < batch && rc == KD_OK; ++b)
+        for (int64_t h = 0; h < heads && rc == KD_OK; ++h) {
+            head_matrix(q, x, b, 0, h, length, heads, head_dim, 0);
+            head_matrix(k, x, b, 1, h, length, heads, head_dim, 0);
+            head_matrix(kt, x, b, 1, h, length, heads, head_dim, 1);
+            head_matrix(v, x, b, 2, h, length, heads, head_dim, 0);
+            head_matrix(vt, x, b, 2, h, length, heads, head_dim, 1);
+            for (int64_t t = 0; t < length; ++t)
+                for (int64_t d = 0; d < head_dim; ++d)
+                    go[t * head_dim + d] = ((const float*)dout)[((b * length + t) * heads + h) * head_dim + d];
+            rc = attention_weights(p, scores, NULL, q, kt, length, head_dim);
+            if (rc != KD_OK) break;
+            kd_matmul_sizes s_dp = {1, length, head_dim, length};  /* dP = dO . V^T */
+            rc = oracle_matmul(KD_F32, go, vt, dp, &s_dp, 0);
+            transpose_f32(pt, p, length, length);
+            kd_matmul_sizes s_dv = {1, length, length, head_dim};  /* dV = P^T . dO */
+            if (rc == KD_OK) rc = oracle_matmul(KD_F32, pt, go, grad, &s_dv, 0);
+            for (int64_t t = 0; t < length; ++t)
+                for (int64_t d = 0; d < head_dim; ++d)
+                    ((float*)dqkv)[attention_index(b, t, 2, h, d, length, heads, head_dim)] = grad[t * head_dim + d];
+            if (rc == KD_OK) rc = oracle_softmax_rows_backward(KD_F32, ds, p, dp, length, length, 0);
+            for (int64_t i = 0; i < length; ++i)
+                for (int64_t j = 0; j < length; ++j) {
+                    const float g = j > i ? 0.0f : ds[i * length + j];
+                    ds[i * length + j] = g / scale;
+                }
+            kd_matmul_sizes s_dq = {1, length, length, head_dim};  /* dQ = dS . K, dK = dS^T . Q */
+            if (rc == KD_OK) rc = oracle_matmul(KD_F32, ds, k, grad, &s_dq, 0);
+            for (int64_t t = 0; t < length; ++t)
+                for (int64_t d = 0; d < head_dim; ++d)
+                    ((float*)dqkv)[attention_index(b, t, 0, h, d, length, heads, head_dim)] = grad[t * head_dim + d];
+            transpose_f32(dst, ds, length, length);
+            if (rc == KD_OK) rc = oracle_matmul(KD_F32, dst, q, grad, &s_dq, 0);
+            for (int64_t t = 0; t < length; ++t)
+                for (int64_t d = 0; d < head_dim; ++d)
+                    ((float*)dqkv)[attention_index(b, t, 1, h, d, length, heads, head_dim)] = grad[t * head_dim + d];
+        }
+    free(q); free(k); free(kt); free(v); free(vt); free(go); free(scores); free(p); free(pt); free(dp); free(ds);
+    free(dst); free(grad);
+    return rc;
+}
+
 /* ---- matmul: kernels.inl:136-177 -------------------------------------------------------------- */
 
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,

@@ -27,6 +27,10 @@ int oracle_reduce(int op, int out_dtype, int in_dtype, void* results, const void
 int oracle_reduce_columns(int op, int out_dtype, int in_dtype, void* results, const void* data,
                           int64_t outer, int64_t inner);
 int oracle_index_bounds(const int64_t* indices, int64_t count, int64_t stride, int64_t* bounds);
+int oracle_causal_attention(int dtype, void* out, void* lse, const void* qkv, int64_t batch, int64_t length,
+                            int64_t heads, int64_t head_dim);
+int oracle_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
+                                     const void* lse, int64_t batch, int64_t length, int64_t heads, int64_t head_dim);
 int oracle_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
                       int64_t output_count);
 int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);

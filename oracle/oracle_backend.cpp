@@ -244,8 +244,9 @@ namespace {
 // 4 gelu_backward_op, 5 matmul_strided, 6 adam_step, 7 sgd_step, 8 reduce_extra,
 // 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
 // 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads, 16 layer_norm_rows,
-// 17 layer_norm_rows_backward, 18 matmul_strided_bias, 19 index_bounds.
-constexpr int kExtensions = 20;
+// 17 layer_norm_rows_backward, 18 matmul_strided_bias, 19 index_bounds, 20 causal_attention,
+// 21 causal_attention_backward.
+constexpr int kExtensions = 22;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -467,6 +468,29 @@ void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t 
     ++g_extension_calls[19];
     KD_TRACE("index_bounds", kv("indices", tp(indices)) + "," + kv("count", count) + "," + kv("stride", stride));
     check(oracle_index_bounds(indices, count, stride, bounds), "index_bounds");
+}
+
+void causal_attention(DType dtype, std::byte* out, std::byte* lse, const std::byte* qkv, std::int64_t batch,
+                      std::int64_t length, std::int64_t heads, std::int64_t head_dim) {
+    ++g_extension_calls[20];
+    KD_TRACE("causal_attention", kv("dtype", static_cast<int>(dtype)) + "," + kv("out", tp(out)) + "," +
+                                     kv("lse", tp(lse)) + "," + kv("qkv", tp(qkv)) + "," + kv("batch", batch) + "," +
+                                     kv("length", length) + "," + kv("heads", heads) + "," + kv("head_dim", head_dim));
+    check(oracle_causal_attention(static_cast<int>(dtype), out, lse, qkv, batch, length, heads, head_dim),
+          "causal_attention");
+}
+
+void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* dout, const std::byte* qkv,
+                               const std::byte* out, const std::byte* lse, std::int64_t batch, std::int64_t length,
+                               std::int64_t heads, std::int64_t head_dim) {
+    ++g_extension_calls[21];
+    KD_TRACE("causal_attention_backward",
+             kv("dtype", static_cast<int>(dtype)) + "," + kv("dqkv", tp(dqkv)) + "," + kv("dout", tp(dout)) + "," +
+                 kv("qkv", tp(qkv)) + "," + kv("out", tp(out)) + "," + kv("lse", tp(lse)) + "," + kv("batch", batch) +
+                 "," + kv("length", length) + "," + kv("heads", heads) + "," + kv("head_dim", head_dim));
+    check(oracle_causal_attention_backward(static_cast<int>(dtype), dqkv, dout, qkv, out, lse, batch, length, heads,
+                                           head_dim),
+          "causal_attention_backward");
 }
 
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {

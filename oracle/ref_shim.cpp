@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <limits>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -884,6 +885,62 @@ int ref_select_grads(int device, int which, uint64_t seed, float* x_grad, float*
             copy_out(retained->grad()->cpu(), p_grad);
         } else {
             std::fill(p_grad, p_grad + 72, 0.0f);
+        }
+    });
+}
+
+// kael's attention chain as CausalSelfAttention::forward composes it (reference
+// src/nn/transformer.cpp:114-136, no cache, no dropout), op by op through kael's tensor API on
+// `device` (0 CPU, 1 the linked device backend): qkv [B, T, 3 H D] (host f32) requires grad, the
+// view / selects / transposes, q . k^T / sqrt(D), masked_fill with triu(ones, 1), softmax, . v,
+// transpose(1, 2).contiguous(); then sum(out * dout).backward(). Writes out [B, T, H D] and
+// qkv.grad.
+int ref_attention_chain(int device, const float* qkv, const float* dout, int64_t batch, int64_t length,
+                        int64_t heads, int64_t head_dim, float* out, float* dqkv) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        const int64_t dim = heads * head_dim;
+        kael::Tensor x = host_tensor(qkv, {batch, length, 3 * dim}, kael::DType::F32).to(dev);
+        x.requires_grad_(true);
+        const kael::Tensor g = host_tensor(dout, {batch, length, dim}, kael::DType::F32).to(dev);
+        const kael::Tensor parts = x.view({batch, length, 3, heads, head_dim});
+        const kael::Tensor q = parts.select(2, 0).transpose(1, 2);
+        const kael::Tensor k = parts.select(2, 1).transpose(1, 2);
+        const kael::Tensor v = parts.select(2, 2).transpose(1, 2);
+        const kael::Tensor mask = kael::triu(kael::ones({length, length}, kael::DType::Bool), 1).to(dev);
+        const kael::Tensor scores = kael::matmul(q, k.mT()) / std::sqrt(static_cast<double>(head_dim));
+        const kael::Tensor masked = kael::masked_fill(scores, mask, -std::numeric_limits<double>::infinity());
+        const kael::Tensor mixed = kael::matmul(kael::softmax(masked, -1), v).transpose(1, 2).contiguous();
+        const kael::Tensor y = mixed.view({batch, length, dim});
+        kael::sum(y * g).backward();
+        copy_out(y.detach().cpu(), out);
+        copy_out(x.grad()->cpu(), dqkv);
+    });
+}
+
+// kael's CausalSelfAttention module (its qkv and proj Linears and the attention; reference
+// src/nn/transformer.cpp:92-138) on `device`: seeded parameters (kael's init) and input x
+// [B, T, C] uniform in [-1, 1), sum(module(x) * g).backward() with g uniform. Writes the output
+// (B T C), x.grad (B T C) and the parameter gradients in named_parameters() order into grads
+// (3 C C + 3 C + C C + C values).
+int ref_attention_module(int device, int64_t batch, int64_t length, int64_t dim, int64_t heads, uint64_t seed,
+                         float* out, float* x_grad, float* grads) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(seed);
+        kael::nn::CausalSelfAttention attention(dim, heads, length);
+        kael::Tensor x = (kael::rand({batch, length, dim}) * 2 - 1).to(dev);
+        const kael::Tensor g = (kael::rand({batch, length, dim}) * 2 - 1).to(dev);
+        attention.to(dev);
+        x.requires_grad_(true);
+        const kael::Tensor y = attention.forward(x);
+        kael::sum(y * g).backward();
+        copy_out(y.detach().cpu(), out);
+        copy_out(x.grad()->cpu(), x_grad);
+        int64_t at = 0;
+        for (auto& [name, p] : attention.named_parameters()) {
+            copy_out(p.grad()->cpu(), grads + at);
+            at += p.numel();
         }
     });
 }

@@ -101,6 +101,9 @@ REF_SIGS = {
     "linear_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
     "head_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
     "select_grads": (c_int, [c_int, c_int, ctypes.c_uint64, c_void_p, c_void_p]),
+    "attention_chain": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "attention_module": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p,
+                                 c_void_p]),
     "layer_norm_grads": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_double,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "suite_size": (c_int, []),
