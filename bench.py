@@ -17,7 +17,7 @@ The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only matmul|c1|f64|c2|rows|train|c3|c4|gpt2|copy]
+                       [--only matmul|c1|f64|c2|rows|attention|train|c3|c4|gpt2|copy]
 """
 from __future__ import annotations
 
@@ -187,6 +187,33 @@ def bench_rows(backend, steps, warmup):
     out["gelu_tanh_1024"] = {"us": ms * 1e3, "gbps": nbytes / (ms * 1e-3) / 1e9}
     for v in out.values():
         v["frac_hbm"] = v["gbps"] / HBM_PEAK_GBPS
+    return out
+
+
+def bench_attention(backend, steps, warmup):
+    """kd_causal_attention (forward) and kd_causal_attention_backward on C4's attention (32 x 128
+    tokens, 4 heads of 64) and a GPT-2-small-shaped one (8 x 1024 tokens, 12 heads). FLOPs are the
+    products' over the unmasked (query, key) pairs, T (T + 1) / 2 per head: forward q . k^T and
+    P . v (4 D each pair), backward the four products of kael's chain (8 D each pair; the kernels
+    also recompute the scores and dP once more, not counted)."""
+    out = {}
+    for name, (b, t, h) in {"c4_32x128x4": (32, 128, 4), "gpt2_8x1024x12": (8, 1024, 12)}.items():
+        rng = np.random.default_rng(b + t + h)
+        qkv = backend.to_device(rng.uniform(-1, 1, (b, t, 3 * h * 64)).astype(np.float32))
+        dout = backend.to_device(rng.uniform(-1, 1, (b, t, h * 64)).astype(np.float32))
+        o = backend.empty((b, t, h * 64), np.float32)
+        lse = backend.empty((b, h, t), np.float32)
+        dq = backend.empty((b, t, 3 * h * 64), np.float32)
+        fwd, bwd = backend.lib.kd_causal_attention, backend.lib.kd_causal_attention_backward
+        pairs = b * h * t * (t + 1) // 2
+        ms_f, _ = time_steps(backend, lambda i: fwd(kd.F32, o.ptr, lse.ptr, qkv.ptr, b, t, h, 64), steps, warmup,
+                             MIN_WARMUP_S)
+        ms_b, _ = time_steps(backend, lambda i: bwd(kd.F32, dq.ptr, dout.ptr, qkv.ptr, o.ptr, lse.ptr, b, t, h, 64),
+                             steps, warmup, MIN_WARMUP_S)
+        out[name] = {"forward_us": ms_f * 1e3, "forward_tflops": 4 * 64 * pairs / (ms_f * 1e-3) / 1e12,
+                     "backward_us": ms_b * 1e3, "backward_tflops": 8 * 64 * pairs / (ms_b * 1e-3) / 1e12}
+        out[name]["frac_fp32_mfma"] = (out[name]["forward_tflops"] * ms_f + out[name]["backward_tflops"] * ms_b) / \
+            (ms_f + ms_b) / FP32_MFMA_PEAK_TFLOPS
     return out
 
 
@@ -495,8 +522,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
-    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "f64", "copy", "c2", "rows", "train", "c3", "c4",
-                                                  "gpt2"],
+    ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "f64", "copy", "c2", "rows", "attention",
+                                                  "train", "c3", "c4", "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -534,6 +561,8 @@ def main() -> int:
             extra[args.only]["cpu_baseline"] = guarded_cpu(cpu_train_baseline, args.only)
         print(json.dumps({"metric": f"{args.only} training step (replayed kael device calls)", "extra": extra}))
         return 0
+    if args.only == "attention":
+        extra["attention"] = bench_attention(backend, max(args.steps, 20), args.warmup)
     if args.only in ("c2", "rows", "train"):
         fn = {"c2": bench_c2, "rows": bench_rows, "train": bench_train}[args.only]
         extra[args.only] = fn(backend, args.steps, args.warmup)
@@ -552,6 +581,7 @@ def main() -> int:
         extra[f"matmul_f64_{n}"] = f64
         extra["c2"] = bench_c2(backend, max(args.steps, 50), args.warmup)
         extra["rows"] = bench_rows(backend, max(args.steps, 20), args.warmup)
+        extra["attention"] = bench_attention(backend, max(args.steps, 20), args.warmup)
         extra["train"] = bench_train(backend, max(args.steps, 20), args.warmup)
         extra["c3"] = bench_replay(backend, "c3", max(args.steps, 20))
         extra["c4"] = bench_replay(backend, "c4", max(args.steps, 10))

@@ -3,21 +3,23 @@
 // softmax(mask(q . k^T / sqrt(D))) . v, the heads merged back to [B, T, H * D]) as one kernel
 // forward and two backward, for f32 and D = 64, without a KV cache or dropout.
 //
-// Forward: one wave per (batch, head, block of 32 queries). The wave walks the key blocks of 32
-// up to its diagonal: S^T = K_J . Q_I^T on v_mfma_f32_32x32x2f32 (each lane then holds 16 scores
+// Forward: one workgroup of four waves per (batch, head, block of 32 queries); wave w walks key
+// blocks w, w + 4, ... up to the diagonal: S^T = K_J . Q_I^T on v_mfma_f32_32x32x2f32 (each lane then holds 16 scores
 // of one query: lane (li, lh), register r is key 8 (r / 4) + 4 lh + r % 4 of query li), the
 // scale and the causal mask, an online softmax per query (running max and sum, the output
 // rescaled when the max grows), and O^T += V_J^T . P^T, whose B operand is the score register
-// itself. The output is written in the merged-head layout and the row's log-sum-exp m + log(l)
-// is kept for the backward.
+// itself. The waves' (max, sum, output) meet in LDS and merge as the online softmax would; the
+// output is written in the merged-head layout and the row's log-sum-exp m + log(l) is kept for
+// the backward.
 //
 // Backward (the gradient of every op of kael's chain: the products, the scale, the mask and
 // softmax backward y (g - sum(g y))): with delta_i = sum_d dO[i][d] O[i][d] (= sum_j P dP over
 // the row) and P recomputed from the log-sum-exp, dS = P (dP - delta) / sqrt(D);
-//   dq kernel, one wave per (batch, head, query block): delta (kept for the next launch), then
-//     for each key block S^T, dP^T = V_J . dO_I^T, dS^T, and dQ += dS . K_J;
-//   dkv kernel, one wave per (batch, head, key block): for each query block at or after it S,
-//     dP = dO_I . V_J^T, dS, dV += P^T . dO_I and dK += dS^T . Q_I.
+//   dq kernel, a workgroup per (batch, head, query block): delta (kept for the next launch),
+//     then for each key block S^T, dP^T = V_J . dO_I^T, dS^T, and dQ += dS . K_J;
+//   dkv kernel, a workgroup per (batch, head, key block): for each query block at or after it
+//     S, dP = dO_I . V_J^T, dS, dV += P^T . dO_I and dK += dS^T . Q_I;
+//   the four waves split the blocks they walk and add their partial sums in wave order.
 // Every MFMA sums over 64 features (or 32 keys / queries) with the operands' features split as
 // k-pairs (s, 32 + s), which is a reordering of the same sum.
 #include <algorithm>
@@ -74,30 +76,105 @@ struct AttentionShape {
     int batch, length, heads;
     int64_t row;  // qkv elements per token: 3 * heads * D
     int64_t out_row;  // merged-head elements per token: heads * D
-    float scale;  // sqrt(D) rounded to float: kael divides the scores by it
+    float inv_scale;  // 1 / sqrt(D) = 1 / 8: kael divides by sqrt(D) = 8, and x * 0.125 equals x / 8 exactly
 };
+
+// ---- work split and LDS tiles --------------------------------------------------------------
+//
+// A workgroup is 4 waves on one block of 32 rows: the forward and dq kernels on a query block,
+// wave w taking key blocks w, w + 4, ... up to the diagonal; the dkv kernel on a key block, wave w
+// taking query blocks kb + w, kb + w + 4, ... Each wave stages the blocks whose elements it reads
+// one per lane along a row (the operand of a product over rows) in an LDS tile of its own, with
+// coalesced 16-byte loads (zeros past the last row) and rows padded to 68 floats. At the end the
+// waves' partial results meet in LDS and are combined in wave order: the forward's (max, sum,
+// output) triples as an online-softmax merge, the gradients as sums.
+
+constexpr int kWaves = 4;
+constexpr int kLd = kD + 4;           // padded LDS row
+constexpr int kTile = kBlock * kLd;   // one 32-row tile
+
+// A wave stages rows t0 .. t0 + 31 of a [T, D] head matrix (row stride ld) into `tile`.
+__device__ __forceinline__ void stage_tile(float* __restrict__ tile, const float* __restrict__ base, int t0, int length,
+                                           int64_t ld, int lane) {
+#pragma unroll
+    for (int q = 0; q < kBlock * kD / 4 / 64; ++q) {
+        const int idx = lane + 64 * q;
+        const int row = idx / (kD / 4), c4 = idx % (kD / 4);
+        v4f v = {0.f, 0.f, 0.f, 0.f};
+        if (t0 + row < length) v = *reinterpret_cast<const v4f*>(base + static_cast<int64_t>(t0 + row) * ld + 4 * c4);
+        *reinterpret_cast<v4f*>(tile + row * kLd + 4 * c4) = v;
+    }
+}
+
+__device__ __forceinline__ void lds_half_row(float (&reg)[32], const float* __restrict__ tile, int row, int lh) {
+    const v4f* src = reinterpret_cast<const v4f*>(tile + row * kLd + 32 * lh);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const v4f v = src[q];
+        reg[4 * q] = v[0];
+        reg[4 * q + 1] = v[1];
+        reg[4 * q + 2] = v[2];
+        reg[4 * q + 3] = v[3];
+    }
+}
+
+// A 32 x 64 accumulator pair acc[dt][r] = X[block_row(r, lh)][32 dt + li] into an LDS tile.
+__device__ __forceinline__ void spill_pair(float* __restrict__ tile, const v16f (&acc)[2], int li, int lh) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        tile[block_row(r, lh) * kLd + li] = acc[0][r];
+        tile[block_row(r, lh) * kLd + 32 + li] = acc[1][r];
+    }
+}
+
+// Rows 8 w .. 8 w + 7 of the sum of the 4 waves' tiles (in wave order) stored to dst rows r0 + row
+// (row stride ld) below `length`: each lane 8 consecutive elements of one row.
+__device__ __forceinline__ void store_tile_sum(float* __restrict__ dst, const float* __restrict__ tiles, int r0,
+                                               int length, int64_t ld, int wave, int lane) {
+    const int row = 8 * wave + lane / 8, c0 = 8 * (lane % 8);
+    if (r0 + row >= length) return;
+    float acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = tiles[row * kLd + c0 + c];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] += tiles[w * kTile + row * kLd + c0 + c];
+    float* out = dst + static_cast<int64_t>(r0 + row) * ld + c0;
+    *reinterpret_cast<v4f*>(out) = v4f{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<v4f*>(out + 4) = v4f{acc[4], acc[5], acc[6], acc[7]};
+}
 
 // ---- forward -----------------------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void attention_forward_kernel(float* __restrict__ out, float* __restrict__ lse,
-                                                               const float* __restrict__ qkv, AttentionShape sh) {
+__global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* __restrict__ out, float* __restrict__ lse,
+                                                                        const float* __restrict__ qkv, AttentionShape sh) {
+    __shared__ float tiles[kWaves * kTile];
+    __shared__ float ms[kWaves][kBlock], ls[kWaves][kBlock];
     const int blocks = (sh.length + kBlock - 1) / kBlock;
     const int bh = blockIdx.x / blocks;
     const int qb = blocks - 1 - static_cast<int>(blockIdx.x % blocks);  // longest rows first
     const int b = bh / sh.heads, h = bh % sh.heads;
-    const int lane = threadIdx.x, li = lane % 32, lh = lane / 32;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const float* q = qkv + static_cast<int64_t>(b) * sh.length * sh.row + h * kD;
     const float* k = q + sh.heads * kD;
     const float* v = k + sh.heads * kD;
-    const int i0 = qb * kBlock;
-    const int query = i0 + li;
+    float* tile = tiles + wave * kTile;
+    const int query = qb * kBlock + li;
 
     float qreg[32];
     load_half_row(qreg, q, query, sh.length, sh.row, lh);
 
     v16f o[2] = {zero16(), zero16()};
     float m = -INFINITY, l = 0.f;
-    for (int kb = 0; kb <= qb; ++kb) {
+    const int rounds = (qb + kWaves) / kWaves;  // ceil((qb + 1) / 4), the same for every wave
+    for (int it = 0; it < rounds; ++it) {
+        const int kb = it * kWaves + wave;
+        const bool mine = kb <= qb;
+        __syncthreads();  // the tile's previous block is consumed
+        if (mine) stage_tile(tile, v, kb * kBlock, sh.length, sh.row, lane);
+        __syncthreads();
+        if (!mine) continue;
         const int j0 = kb * kBlock;
         float kreg[32];
         load_half_row(kreg, k, j0 + li, sh.length, sh.row, lh);
@@ -109,7 +186,7 @@ __global__ __launch_bounds__(64) void attention_forward_kernel(float* __restrict
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int key = j0 + block_row(r, lh);
-            const float x = (key > query || key >= sh.length) ? -INFINITY : s[r] / sh.scale;
+            const float x = (key > query || key >= sh.length) ? -INFINITY : s[r] * sh.inv_scale;
             s[r] = x;
             bmax = fmaxf(bmax, x);
         }
@@ -133,53 +210,67 @@ __global__ __launch_bounds__(64) void attention_forward_kernel(float* __restrict
         }
         // O^T[d][i] += sum_j V[j][d] P[i][j]: A = V^T (lane li: feature 32 dt + li), B = P^T
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int key = j0 + block_row(t, lh);
-                const float vv = key < sh.length ? v[key * sh.row + 32 * dt + li] : 0.f;
-                o[dt] = mfma(vv, s[t], o[dt]);
-            }
+        for (int t = 0; t < 16; ++t) {
+            const float* vr = tile + block_row(t, lh) * kLd + li;
+            o[0] = mfma(vr[0], s[t], o[0]);
+            o[1] = mfma(vr[32], s[t], o[1]);
         }
     }
-    // o[dt][r] = O^T[32 dt + block_row(r, lh)][query li]: this lane's query, 4 consecutive
-    // features per register quad
-    if (query < sh.length) {
-        const float inv = 1.f / l;
-        float* dst = out + (static_cast<int64_t>(b) * sh.length + query) * sh.out_row + h * kD;
+    // merge: o[dt][r] = O^T[32 dt + block_row(r, lh)][query li] of this wave's key blocks
+    __syncthreads();
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
+    for (int r = 0; r < 16; ++r) {
+        tile[li * kLd + 32 * 0 + block_row(r, lh)] = o[0][r];
+        tile[li * kLd + 32 * 1 + block_row(r, lh)] = o[1][r];
+    }
+    if (lh == 0) {
+        ms[wave][li] = m;
+        ls[wave][li] = l;
+    }
+    __syncthreads();
+    // wave w finishes queries 8 w .. 8 w + 7, each lane 8 features of one of them
+    const int row = 8 * wave + lane / 8, c0 = 8 * (lane % 8);
+    const int t = qb * kBlock + row;
+    if (t < sh.length) {
+        float mx = ms[0][row];
 #pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-                v4f w;
-                w[0] = o[dt][4 * qd] * inv;
-                w[1] = o[dt][4 * qd + 1] * inv;
-                w[2] = o[dt][4 * qd + 2] * inv;
-                w[3] = o[dt][4 * qd + 3] * inv;
-                *reinterpret_cast<v4f*>(dst + 32 * dt + 8 * qd + 4 * lh) = w;
-            }
+        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, ms[w][row]);
+        float total = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float f = ms[w][row] == -INFINITY ? 0.f : expf(ms[w][row] - mx);
+            total += f * ls[w][row];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] += f * tiles[w * kTile + row * kLd + c0 + c];
         }
-        if (lh == 0) lse[static_cast<int64_t>(bh) * sh.length + query] = m + logf(l);
+        const float inv = 1.f / total;
+        float* dst = out + (static_cast<int64_t>(b) * sh.length + t) * sh.out_row + h * kD + c0;
+        *reinterpret_cast<v4f*>(dst) = v4f{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        *reinterpret_cast<v4f*>(dst + 4) = v4f{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+        if (lane % 8 == 0) lse[static_cast<int64_t>(bh) * sh.length + t] = mx + logf(total);
     }
 }
 
 // ---- backward: delta and dQ ---------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void attention_dq_kernel(float* __restrict__ dqkv, float* __restrict__ delta,
-                                                          const float* __restrict__ dout, const float* __restrict__ qkv,
-                                                          const float* __restrict__ out, const float* __restrict__ lse,
-                                                          AttentionShape sh) {
+__global__ __launch_bounds__(kWaves * 64) void attention_dq_kernel(float* __restrict__ dqkv, float* __restrict__ delta,
+                                                                   const float* __restrict__ dout,
+                                                                   const float* __restrict__ qkv,
+                                                                   const float* __restrict__ out,
+                                                                   const float* __restrict__ lse, AttentionShape sh) {
+    __shared__ float tiles[kWaves * kTile];
     const int blocks = (sh.length + kBlock - 1) / kBlock;
     const int bh = blockIdx.x / blocks;
     const int qb = blocks - 1 - static_cast<int>(blockIdx.x % blocks);
     const int b = bh / sh.heads, h = bh % sh.heads;
-    const int lane = threadIdx.x, li = lane % 32, lh = lane / 32;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
     const float* q = qkv + tok0 * sh.row + h * kD;
     const float* k = q + sh.heads * kD;
     const float* v = k + sh.heads * kD;
     const float* go = dout + tok0 * sh.out_row + h * kD;
     const float* o = out + tok0 * sh.out_row + h * kD;
+    float* tile = tiles + wave * kTile;
     const int i0 = qb * kBlock;
     const int query = i0 + li;
 
@@ -196,13 +287,20 @@ __global__ __launch_bounds__(64) void attention_dq_kernel(float* __restrict__ dq
         dl = part + __shfl_xor(part, 32);
     }
     const float row_lse = query < sh.length ? lse[static_cast<int64_t>(bh) * sh.length + query] : 0.f;
-    if (query < sh.length && lh == 0) delta[static_cast<int64_t>(bh) * sh.length + query] = dl;
+    if (wave == 0 && query < sh.length && lh == 0) delta[static_cast<int64_t>(bh) * sh.length + query] = dl;
 
     v16f dq[2] = {zero16(), zero16()};
-    for (int kb = 0; kb <= qb; ++kb) {
+    const int rounds = (qb + kWaves) / kWaves;
+    for (int it = 0; it < rounds; ++it) {
+        const int kb = it * kWaves + wave;
+        const bool mine = kb <= qb;
+        __syncthreads();
+        if (mine) stage_tile(tile, k, kb * kBlock, sh.length, sh.row, lane);
+        __syncthreads();
+        if (!mine) continue;
         const int j0 = kb * kBlock;
         float kreg[32], vreg[32];
-        load_half_row(kreg, k, j0 + li, sh.length, sh.row, lh);
+        lds_half_row(kreg, tile, li, lh);
         load_half_row(vreg, v, j0 + li, sh.length, sh.row, lh);
         v16f s = zero16(), dp = zero16();
 #pragma unroll
@@ -215,42 +313,38 @@ __global__ __launch_bounds__(64) void attention_dq_kernel(float* __restrict__ dq
         for (int r = 0; r < 16; ++r) {
             const int key = j0 + block_row(r, lh);
             const bool live = key <= query && key < sh.length && query < sh.length;
-            const float p = live ? expf(s[r] / sh.scale - row_lse) : 0.f;
-            s[r] = p * (dp[r] - dl) / sh.scale;
+            const float p = live ? expf(s[r] * sh.inv_scale - row_lse) : 0.f;
+            s[r] = p * (dp[r] - dl) * sh.inv_scale;
         }
         // dQ[i][d] += sum_j dS[i][j] K[j][d]: A = dS (lane li: query li), B = K (feature 32 dt + li)
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int key = j0 + block_row(t, lh);
-                const float kk = key < sh.length ? k[key * sh.row + 32 * dt + li] : 0.f;
-                dq[dt] = mfma(s[t], kk, dq[dt]);
-            }
+        for (int t = 0; t < 16; ++t) {
+            const float* kr = tile + block_row(t, lh) * kLd + li;
+            dq[0] = mfma(s[t], kr[0], dq[0]);
+            dq[1] = mfma(s[t], kr[32], dq[1]);
         }
     }
-    // dq[dt][r] = dQ[i0 + block_row(r, lh)][32 dt + li]
-    float* dst = dqkv + tok0 * sh.row + h * kD;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = i0 + block_row(r, lh);
-        if (row < sh.length) {
-            dst[row * sh.row + li] = dq[0][r];
-            dst[row * sh.row + 32 + li] = dq[1][r];
-        }
-    }
+    // dq[dt][r] = dQ[i0 + block_row(r, lh)][32 dt + li]: the waves' partial sums, added in wave order
+    __syncthreads();
+    spill_pair(tile, dq, li, lh);
+    __syncthreads();
+    store_tile_sum(dqkv + tok0 * sh.row + h * kD, tiles, i0, sh.length, sh.row, wave, lane);
 }
 
 // ---- backward: dK and dV ------------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void attention_dkv_kernel(float* __restrict__ dqkv, const float* __restrict__ delta,
-                                                           const float* __restrict__ dout, const float* __restrict__ qkv,
-                                                           const float* __restrict__ lse, AttentionShape sh) {
+__global__ __launch_bounds__(kWaves * 64) void attention_dkv_kernel(float* __restrict__ dqkv,
+                                                                    const float* __restrict__ delta,
+                                                                    const float* __restrict__ dout,
+                                                                    const float* __restrict__ qkv,
+                                                                    const float* __restrict__ lse, AttentionShape sh) {
+    __shared__ float tiles[2 * kWaves * kTile];
+    __shared__ float lses[kWaves][kBlock], deltas[kWaves][kBlock];
     const int blocks = (sh.length + kBlock - 1) / kBlock;
     const int bh = blockIdx.x / blocks;
     const int kb = static_cast<int>(blockIdx.x % blocks);  // key block 0 has the most query blocks
     const int b = bh / sh.heads, h = bh % sh.heads;
-    const int lane = threadIdx.x, li = lane % 32, lh = lane / 32;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
     const float* q = qkv + tok0 * sh.row + h * kD;
     const float* k = q + sh.heads * kD;
@@ -258,6 +352,8 @@ __global__ __launch_bounds__(64) void attention_dkv_kernel(float* __restrict__ d
     const float* go = dout + tok0 * sh.out_row + h * kD;
     const float* row_lse = lse + static_cast<int64_t>(bh) * sh.length;
     const float* row_delta = delta + static_cast<int64_t>(bh) * sh.length;
+    float* qtile = tiles + wave * kTile;
+    float* gtile = tiles + (kWaves + wave) * kTile;
     const int j0 = kb * kBlock;
     const int key = j0 + li;
 
@@ -266,11 +362,25 @@ __global__ __launch_bounds__(64) void attention_dkv_kernel(float* __restrict__ d
     load_half_row(vreg, v, key, sh.length, sh.row, lh);
 
     v16f dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
-    for (int qb = kb; qb < blocks; ++qb) {
+    const int rounds = (blocks - kb + kWaves - 1) / kWaves;
+    for (int it = 0; it < rounds; ++it) {
+        const int qb = kb + it * kWaves + wave;
+        const bool mine = qb < blocks;
         const int i0 = qb * kBlock;
+        __syncthreads();
+        if (mine) {
+            stage_tile(qtile, q, i0, sh.length, sh.row, lane);
+            stage_tile(gtile, go, i0, sh.length, sh.out_row, lane);
+            if (lane < kBlock) {
+                lses[wave][lane] = i0 + lane < sh.length ? row_lse[i0 + lane] : 0.f;
+                deltas[wave][lane] = i0 + lane < sh.length ? row_delta[i0 + lane] : 0.f;
+            }
+        }
+        __syncthreads();
+        if (!mine) continue;
         float qreg[32], doreg[32];
-        load_half_row(qreg, q, i0 + li, sh.length, sh.row, lh);
-        load_half_row(doreg, go, i0 + li, sh.length, sh.out_row, lh);
+        lds_half_row(qreg, qtile, li, lh);
+        lds_half_row(doreg, gtile, li, lh);
         v16f s = zero16(), dp = zero16();
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -281,41 +391,31 @@ __global__ __launch_bounds__(64) void attention_dkv_kernel(float* __restrict__ d
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int query = i0 + block_row(r, lh);
+            const int local = block_row(r, lh);
+            const int query = i0 + local;
             const bool live = key <= query && query < sh.length && key < sh.length;
-            const float lq = query < sh.length ? row_lse[query] : 0.f;
-            const float dq = query < sh.length ? row_delta[query] : 0.f;
-            p[r] = live ? expf(s[r] / sh.scale - lq) : 0.f;
-            s[r] = p[r] * (dp[r] - dq) / sh.scale;
+            p[r] = live ? expf(s[r] * sh.inv_scale - lses[wave][local]) : 0.f;
+            s[r] = p[r] * (dp[r] - deltas[wave][local]) * sh.inv_scale;
         }
         // dV[j][d] += sum_i P[i][j] dO[i][d], dK[j][d] += sum_i dS[i][j] Q[i][d]:
         // A = P^T / dS^T (lane li: key li), B = dO / Q (feature 32 dt + li)
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int query = i0 + block_row(t, lh);
-                const bool in = query < sh.length;
-                const float gov = in ? go[query * sh.out_row + 32 * dt + li] : 0.f;
-                const float qv = in ? q[query * sh.row + 32 * dt + li] : 0.f;
-                dv[dt] = mfma(p[t], gov, dv[dt]);
-                dk[dt] = mfma(s[t], qv, dk[dt]);
-            }
+        for (int t = 0; t < 16; ++t) {
+            const int off = block_row(t, lh) * kLd + li;
+            dv[0] = mfma(p[t], gtile[off], dv[0]);
+            dv[1] = mfma(p[t], gtile[off + 32], dv[1]);
+            dk[0] = mfma(s[t], qtile[off], dk[0]);
+            dk[1] = mfma(s[t], qtile[off + 32], dk[1]);
         }
     }
-    // dk[dt][r] = dK[j0 + block_row(r, lh)][32 dt + li]
+    // dk / dv[dt][r] = dK / dV[j0 + block_row(r, lh)][32 dt + li]: partial sums added in wave order
+    __syncthreads();
+    spill_pair(qtile, dk, li, lh);
+    spill_pair(gtile, dv, li, lh);
+    __syncthreads();
     float* dstk = dqkv + tok0 * sh.row + sh.heads * kD + h * kD;
-    float* dstv = dstk + sh.heads * kD;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = j0 + block_row(r, lh);
-        if (row < sh.length) {
-            dstk[row * sh.row + li] = dk[0][r];
-            dstk[row * sh.row + 32 + li] = dk[1][r];
-            dstv[row * sh.row + li] = dv[0][r];
-            dstv[row * sh.row + 32 + li] = dv[1][r];
-        }
-    }
+    store_tile_sum(dstk, tiles, j0, sh.length, sh.row, wave, lane);
+    store_tile_sum(dstk + sh.heads * kD, tiles + kWaves * kTile, j0, sh.length, sh.row, wave, lane);
 }
 
 int check_shape(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t head_dim, AttentionShape& sh,
@@ -332,7 +432,7 @@ int check_shape(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t
     sh.heads = static_cast<int>(heads);
     sh.row = row;
     sh.out_row = heads * kD;
-    sh.scale = static_cast<float>(std::sqrt(static_cast<double>(head_dim)));
+    sh.inv_scale = 0.125f;  // D = 64: a power of two, so the product is the division's exact result
     return KD_OK;
 }
 
@@ -352,7 +452,7 @@ extern "C" int kd_causal_attention(int dtype, void* out, void* lse, const void* 
         return fail(KD_E_INVALID, "kd_causal_attention: out and qkv must be 16-byte aligned, lse given");
     if (int rc = ensure_device()) return rc;
     const int64_t blocks = (length + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(attention_forward_kernel, dim3(static_cast<uint32_t>(batch * heads * blocks)), dim3(64), 0,
+    hipLaunchKernelGGL(attention_forward_kernel, dim3(static_cast<uint32_t>(batch * heads * blocks)), dim3(kWaves * 64), 0,
                        stream(), static_cast<float*>(out), static_cast<float*>(lse), static_cast<const float*>(qkv), sh);
     KD_LAUNCH_CHECK();
     return KD_OK;
@@ -371,11 +471,11 @@ extern "C" int kd_causal_attention_backward(int dtype, void* dqkv, const void* d
     if (int rc = workspace(ws, static_cast<size_t>(batch * heads * length) * sizeof(float))) return rc;
     float* delta = static_cast<float*>(ws.ptr);
     const dim3 grid(static_cast<uint32_t>(batch * heads * blocks));
-    hipLaunchKernelGGL(attention_dq_kernel, grid, dim3(64), 0, stream(), static_cast<float*>(dqkv), delta,
+    hipLaunchKernelGGL(attention_dq_kernel, grid, dim3(kWaves * 64), 0, stream(), static_cast<float*>(dqkv), delta,
                        static_cast<const float*>(dout), static_cast<const float*>(qkv), static_cast<const float*>(out),
                        static_cast<const float*>(lse), sh);
     KD_LAUNCH_CHECK();
-    hipLaunchKernelGGL(attention_dkv_kernel, grid, dim3(64), 0, stream(), static_cast<float*>(dqkv),
+    hipLaunchKernelGGL(attention_dkv_kernel, grid, dim3(kWaves * 64), 0, stream(), static_cast<float*>(dqkv),
                        static_cast<const float*>(delta), static_cast<const float*>(dout), static_cast<const float*>(qkv),
                        static_cast<const float*>(lse), sh);
     KD_LAUNCH_CHECK();

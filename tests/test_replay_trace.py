@@ -24,10 +24,12 @@ def test_trace_is_well_formed(name):
     assert {"matmul_strided", "cross_entropy_rows", "cross_entropy_grad", "d2h"} <= ops
     assert ("sgd_step" if name == "c3" else "adam_step_many") in ops
     if name == "c4":
-        # the fused row kernels and their backward passes, the per-head attention products, the
-        # Linear products with their bias and the column sums are in the step
-        assert {"softmax_rows", "layer_norm_rows", "softmax_rows_backward", "layer_norm_rows_backward",
-                "matmul_strided_heads", "matmul_strided_bias", "reduce_columns", "gather", "scatter_add"} <= ops
+        # the fused LayerNorms and their backward passes, the fused attention and its backward, the
+        # Linear products with their bias, the column sums and the one-call index range checks are
+        # in the step; the attention's own products, mask and softmax are not
+        assert {"layer_norm_rows", "layer_norm_rows_backward", "causal_attention", "causal_attention_backward",
+                "matmul_strided_bias", "reduce_columns", "gather", "scatter_add", "index_bounds"} <= ops
+        assert not {"softmax_rows", "softmax_rows_backward", "matmul_strided_heads"} & ops
     # the step's products: C3 has 3 (forward 2, backward 3 minus the input gradient), C4 dozens
     assert replay.matmul_flops(steps[-1]) > (1e7 if name == "c3" else 1e10)
 
