@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_dq_kernel(float* __rest
 
 // ---- backward: dK and dV ------------------------------------------------------------------
 
-__global__ __launch_bounds__(kWaves * 64) void attention_dkv_kernel(float* __restrict__ dqkv,
+__global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __restrict__ dqkv,
                                                                     const float* __restrict__ delta,
                                                                     const float* __restrict__ dout,
                                                                     const float* __restrict__ qkv,
