@@ -21,7 +21,8 @@
 //     S, dP = dO_I . V_J^T, dS, dV += P^T . dO_I and dK += dS^T . Q_I;
 //   the four waves split the blocks they walk and add their partial sums in wave order.
 // Every MFMA sums over 64 features (or 32 keys / queries) with the operands' features split as
-// k-pairs (s, 32 + s), which is a reordering of the same sum.
+// k-pairs (s, 32 + s), which is a reordering of the same sum. The softmax exponentials use the
+// hardware exp2 (__expf: a few ulp), well inside the device tolerance kael's tests apply.
 #include <algorithm>
 #include <cmath>
 
@@ -192,11 +193,11 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
         }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
         const float mnew = fmaxf(m, bmax);
-        const float alpha = mnew == -INFINITY ? 1.f : expf(m - mnew);
+        const float alpha = mnew == -INFINITY ? 1.f : __expf(m - mnew);
         float bsum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float p = s[r] == -INFINITY ? 0.f : expf(s[r] - mnew);
+            const float p = s[r] == -INFINITY ? 0.f : __expf(s[r] - mnew);
             s[r] = p;
             bsum += p;
         }
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
         float total = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float f = ms[w][row] == -INFINITY ? 0.f : expf(ms[w][row] - mx);
+            const float f = ms[w][row] == -INFINITY ? 0.f : __expf(ms[w][row] - mx);
             total += f * ls[w][row];
 #pragma unroll
             for (int c = 0; c < 8; ++c) acc[c] += f * tiles[w * kTile + row * kLd + c0 + c];
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_dq_kernel(float* __rest
         for (int r = 0; r < 16; ++r) {
             const int key = j0 + block_row(r, lh);
             const bool live = key <= query && key < sh.length && query < sh.length;
-            const float p = live ? expf(s[r] * sh.inv_scale - row_lse) : 0.f;
+            const float p = live ? __expf(s[r] * sh.inv_scale - row_lse) : 0.f;
             s[r] = p * (dp[r] - dl) * sh.inv_scale;
         }
         // dQ[i][d] += sum_j dS[i][j] K[j][d]: A = dS (lane li: query li), B = K (feature 32 dt + li)
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
             const int local = block_row(r, lh);
             const int query = i0 + local;
             const bool live = key <= query && query < sh.length && key < sh.length;
-            p[r] = live ? expf(s[r] * sh.inv_scale - lses[wave][local]) : 0.f;
+            p[r] = live ? __expf(s[r] * sh.inv_scale - lses[wave][local]) : 0.f;
             s[r] = p[r] * (dp[r] - deltas[wave][local]) * sh.inv_scale;
         }
         // dV[j][d] += sum_i P[i][j] dO[i][d], dK[j][d] += sum_i dS[i][j] Q[i][d]:
