@@ -835,7 +835,8 @@ int ref_head_grads(int device, int64_t batch, int64_t m, int64_t k, int64_t n, u
 //   4  selects along two different dims;
 //   5  the split of case 0 on an intermediate that retains its gradient (also written to p_grad);
 //   6  case 0 with anomaly detection on;
-//   7  a select of a select, and a select along the last dim.
+//   7  a select of a select, and a select along the last dim;
+//   8  the split of case 0, backward twice with the graph retained (x.grad accumulates).
 // Writes x.grad (72 values) and, for case 5, the intermediate's gradient (else zeros).
 int ref_select_grads(int device, int which, uint64_t seed, float* x_grad, float* p_grad) {
     return guarded([&] {
@@ -854,7 +855,7 @@ int ref_select_grads(int device, int which, uint64_t seed, float* x_grad, float*
         };
         auto make_loss = [&]() -> kael::Tensor {
             switch (which) {
-            case 0: case 6: return split(x * 1.0);
+            case 0: case 6: case 8: return split(x * 1.0);
             case 1: return kael::sum(x.select(2, 0) * wk) + kael::sum(x.select(2, -1) * wv);
             case 2:
                 return kael::sum(x.select(-2, 1) * wk) + kael::sum(x.select(2, 1) * wv) +
@@ -874,6 +875,7 @@ int ref_select_grads(int device, int which, uint64_t seed, float* x_grad, float*
         const kael::Tensor loss = make_loss();
         if (which == 6) kael::set_anomaly_detection(true);
         try {
+            if (which == 8) loss.backward(true);
             loss.backward();
         } catch (...) {
             if (which == 6) kael::set_anomaly_detection(false);

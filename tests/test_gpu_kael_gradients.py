@@ -81,7 +81,7 @@ LR = 1e-3  # kael's Adam default (include/kael/optim/adam.h:11-17)
 
 
 SELECT_CASES = ["attention_split", "two_of_three", "same_index_twice", "mixed_with_whole", "two_dims",
-                "retained_intermediate", "anomaly_detection", "select_of_select"]
+                "retained_intermediate", "anomaly_detection", "select_of_select", "retained_graph_twice"]
 
 
 def select_grads(lib, device, which, seed=11):

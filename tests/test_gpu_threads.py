@@ -4,13 +4,16 @@ kael may call its device backend from more than one host thread (reference
 docs/08-cpu-performance.md:191: the Python/server thread beside the main thread), and the
 reference backend takes no lock (src/cuda/backend.cu). This backend shares one scratch buffer
 per device between the split reductions, the split cumsum and the split-K products, growing it
-on demand; these tests drive those paths from three threads at once, with workspace sizes that
+on demand; these tests drive those paths from four threads at once, with workspace sizes that
 grow while the threads run, and require every result to equal, bit for bit, the same call made
-alone afterwards (each of these kernels reduces in a fixed order).
+alone afterwards (each of these kernels reduces in a fixed order). The fourth thread also takes
+the index range checks' pinned host slots (one per call in flight) and the attention backward's
+workspace.
 
 The check runs in a child process so that the workspace starts empty and its growths happen
 during the concurrent phase, whatever earlier tests allocated.
 """
+import ctypes
 import os
 import subprocess
 import sys
@@ -80,13 +83,41 @@ def _skinny_jobs(backend, rng):
     return jobs
 
 
+def _bounds_and_attention_jobs(backend, rng):
+    """Index range checks (each holds a pinned host slot from its launch to its read; the larger
+    ones also a workspace for the workgroups' pairs) and the attention backward (its delta rows in
+    the workspace)."""
+    jobs = []
+    for count in (4096, 1 << 20, 3_000_001):
+        ids = backend.to_device(rng.integers(-(1 << 40), 1 << 40, count).astype(np.int64))
+
+        def bounds(ids=ids, count=count):
+            pair = np.zeros(2, np.int64)
+            backend.call("index_bounds", ids.ptr, count, 1, pair.ctypes.data_as(ctypes.c_void_p))
+            return pair
+        jobs.append((f"index_bounds {count}", bounds))
+    b, t, h = 4, 128, 4
+    qkv = backend.to_device(rng.uniform(-1, 1, (b, t, 3 * h * 64)).astype(np.float32))
+    dout = backend.to_device(rng.uniform(-1, 1, (b, t, h * 64)).astype(np.float32))
+
+    def attention():
+        out, lse = backend.empty((b, t, h * 64), np.float32), backend.empty((b, h, t), np.float32)
+        dq = backend.empty((b, t, 3 * h * 64), np.float32)
+        backend.call("causal_attention", kd.F32, out.ptr, lse.ptr, qkv.ptr, b, t, h, 64)
+        backend.call("causal_attention_backward", kd.F32, dq.ptr, dout.ptr, qkv.ptr, out.ptr, lse.ptr, b, t, h, 64)
+        return dq.numpy()
+    jobs.append(("causal_attention 4x128x4", attention))
+    return jobs
+
+
 def child() -> int:
     backend = kd.load()
     if not backend.lib.kd_available():
         print(f"no device: {backend.error()}", flush=True)
         return 2
     rng = np.random.default_rng(11)
-    groups = [_reduce_jobs(backend, rng), _matmul_jobs(backend, rng), _skinny_jobs(backend, rng)]
+    groups = [_reduce_jobs(backend, rng), _matmul_jobs(backend, rng), _skinny_jobs(backend, rng),
+              _bounds_and_attention_jobs(backend, rng)]
     results = [[] for _ in groups]
     errors = []
 

@@ -109,3 +109,11 @@ def test_select_gradients_skip_the_zero_fills(tmp_path, which, unmodified, fused
         recs = [json.loads(line) for line in trace.read_text().splitlines() if line.strip()]
         fills[name] = sum(1 for r in recs if r["op"] == "fill" and r["count"] == 72)
     assert fills == {"libkael_oracle.so": unmodified, "libkael_oracle_fused.so": fused}
+
+
+def test_select_gradients_with_the_graph_retained_accumulate(kael_oracle_fused):
+    """Backward twice over the same graph (retain_graph): each pass defers and writes its own select
+    gradients, so x.grad is exactly twice one pass's (g + g rounds to 2g)."""
+    once, _ = select_grads(kael_oracle_fused, 1, SELECT_CASES.index("attention_split"))
+    twice, _ = select_grads(kael_oracle_fused, 1, SELECT_CASES.index("retained_graph_twice"))
+    assert np.array_equal(twice, 2 * once)
