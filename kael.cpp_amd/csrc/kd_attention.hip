@@ -449,8 +449,8 @@ extern "C" int kd_causal_attention(int dtype, void* out, void* lse, const void* 
                                    int64_t heads, int64_t head_dim) {
     AttentionShape sh;
     if (int rc = check_shape(dtype, batch, length, heads, head_dim, sh, "kd_causal_attention")) return rc;
-    if (!aligned16(out) || !aligned16(qkv) || lse == nullptr)
-        return fail(KD_E_INVALID, "kd_causal_attention: out and qkv must be 16-byte aligned, lse given");
+    if (out == nullptr || qkv == nullptr || lse == nullptr || !aligned16(out) || !aligned16(qkv))
+        return fail(KD_E_INVALID, "kd_causal_attention: out, lse and qkv must be given, out and qkv 16-byte aligned");
     if (int rc = ensure_device()) return rc;
     const int64_t blocks = (length + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(attention_forward_kernel, dim3(static_cast<uint32_t>(batch * heads * blocks)), dim3(kWaves * 64), 0,
@@ -464,8 +464,9 @@ extern "C" int kd_causal_attention_backward(int dtype, void* dqkv, const void* d
                                             int64_t head_dim) {
     AttentionShape sh;
     if (int rc = check_shape(dtype, batch, length, heads, head_dim, sh, "kd_causal_attention_backward")) return rc;
-    if (!aligned16(dqkv) || !aligned16(dout) || !aligned16(qkv) || !aligned16(out) || lse == nullptr)
-        return fail(KD_E_INVALID, "kd_causal_attention_backward: operands must be 16-byte aligned, lse given");
+    if (dqkv == nullptr || dout == nullptr || qkv == nullptr || out == nullptr || lse == nullptr || !aligned16(dqkv) ||
+        !aligned16(dout) || !aligned16(qkv) || !aligned16(out))
+        return fail(KD_E_INVALID, "kd_causal_attention_backward: every operand must be given, 16-byte aligned");
     if (int rc = ensure_device()) return rc;
     const int64_t blocks = (length + kBlock - 1) / kBlock;
     Workspace ws;  // delta, held until the dkv kernel is enqueued

@@ -52,6 +52,13 @@ def test_attention_rejects_unsupported_shapes(kdb):
         kdb.call("causal_attention", kd.F32, x.ptr, x.ptr, x.ptr, 1, 1, 2, 32)
     with pytest.raises(kd.KdError):
         kdb.call("causal_attention_backward", kd.F32, x.ptr, x.ptr, x.ptr, x.ptr, x.ptr, 1, 0, 1, 64)
+    # missing or misaligned operands are rejected on the host, before any launch
+    with pytest.raises(kd.KdError):
+        kdb.call("causal_attention", kd.F32, None, x.ptr, x.ptr, 1, 1, 1, 64)
+    with pytest.raises(kd.KdError):
+        kdb.call("causal_attention", kd.F32, x.ptr, x.ptr, x.ptr + 4, 1, 1, 1, 64)
+    with pytest.raises(kd.KdError):
+        kdb.call("causal_attention_backward", kd.F32, x.ptr, None, x.ptr, x.ptr, x.ptr, 1, 1, 1, 64)
 
 
 @pytest.mark.parametrize("shape", [(32, 128, 256, 4), (2, 9, 128, 2), (1, 200, 768, 12)],
