@@ -70,3 +70,19 @@ def test_module_through_the_fused_branch_on_the_device(kael_hip_fused, shape):
     dev = module_grads(kael_hip_fused, 1, shape)
     for got, want, what in zip(dev, cpu, ("out", "x.grad", "parameter grads")):
         close(got, want.astype(np.float64), what)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_attention_random_shapes(kdb, oracle, seed):
+    """Seeded random shapes (1-3 batch rows, 1-300 positions, 1-6 heads): every ragged tail of the
+    32-row blocks, the forward and backward against the oracle at the device tolerance."""
+    rng = np.random.default_rng(1000 + seed)
+    b, t, h = int(rng.integers(1, 4)), int(rng.integers(1, 301)), int(rng.integers(1, 7))
+    qkv, dout = inputs(b, t, h, 64, seed)
+    want = oracle_attention(oracle, qkv, dout, b, t, h, 64)
+    got = device_attention(kdb, qkv, dout, b, t, h)
+    for g, w, what in zip(got, want, ("out", "lse", "qkv.grad")):
+        try:
+            close(g, w.astype(np.float64), what)
+        except AssertionError as e:
+            raise AssertionError(f"seed {seed}: {b}x{t}x{h}: {e}") from None
