@@ -522,6 +522,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gpt-eager", action="store_true", help="GPT-2 steps without graph replay (profiling)")
+    ap.add_argument("--gpt-tokens", type=int, default=256, help="GPT-2 new tokens per run (shorter profiling runs)")
+    ap.add_argument("--gpt-repeats", type=int, default=3, help="GPT-2 timed runs (the best is reported)")
     ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "f64", "copy", "c2", "rows", "attention",
                                                   "train", "c3", "c4", "gpt2"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
@@ -540,7 +542,8 @@ def main() -> int:
         print(json.dumps({"metric": "copy calibration", "extra": extra}))
         return 0
     if args.only == "gpt2":
-        extra["gpt2_decode"] = bench_gpt2(backend, eager=args.gpt_eager)
+        extra["gpt2_decode"] = bench_gpt2(backend, new_tokens=args.gpt_tokens, repeats=args.gpt_repeats,
+                                          eager=args.gpt_eager)
         print(json.dumps({"metric": "GPT-2-small decode tok/s", "extra": extra}))
         return 0
     if args.only == "f64":

@@ -443,14 +443,10 @@ typedef struct kd_gpt_config {
                               replaying the captured graph (for kernel-level profiling);
                               KD_GPT_STEPWISE_PREFILL: run the prompt one cached step per
                               position instead of the batched prefill (for comparison);
-                              KD_GPT_PERSISTENT: run each token as one persistent launch
-                              whose workgroups hand activations to each other, instead of one
-                              kernel per phase (63 for GPT-2 small); slower on MI355X for GPT-2
-                              small, kept for comparison */
+                              other bits are KD_E_INVALID */
 } kd_gpt_config;
 #define KD_GPT_EAGER 1
 #define KD_GPT_STEPWISE_PREFILL 2
-#define KD_GPT_PERSISTENT 4
 
 int kd_gpt_create(void** handle, const kd_gpt_config* config);
 /* KD_OK when kd_gpt_create would accept `config` on this device (sizes, head_dim a multiple of 4 up

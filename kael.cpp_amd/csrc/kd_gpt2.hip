@@ -732,766 +732,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
     }
 }
 
-// ---- persistent decode step (KD_GPT_PERSISTENT) -------------------------------------------------
-//
-// Opt-in: for GPT-2 small it decodes at about 2.47k tokens/s against the phased step's 2.66k. A
-// hand-over between workgroups on different XCDs (a write-through store, then polling loads that
-// miss every L2) takes about 3 us from the producer's store to the consumer holding the vector, so
-// the five or six hand-overs of a layer cost about as much as the phased step's kernel boundaries.
-//
-// One launch per token. Every workgroup (one per CU) runs the whole token, per layer:
-//   A  LN1 + qkv rows [g 3d / G, (g + 1) 3d / G)  (every workgroup; layer 0 embeds x itself)
-//   B  attention of head h in C chunks of key rows, one workgroup per chunk; the head's chunk-0
-//      workgroup combines the chunks' partials into the head's output
-//   C  proj rows (+ bias, + residual)    D  LN2 + fc1 rows (+ bias, GELU)    E  fc2 rows (+ bias, + residual)
-// then the head rows with the final LayerNorm and workgroup 0's greedy pick.
-// A phase's input vector is produced by other workgroups, on other XCDs (whose L2s are not
-// coherent with each other). It is handed over in 8-byte slots: the 32-bit value and the 32-bit
-// tag of the token step, written by one 64-bit agent-scope store (write-through to memory) and read
-// by one 64-bit agent-scope load, so a reader sees either an older tag (and polls again) or the value
-// with its tag. No grid barrier or counter is needed: a workgroup waits for exactly the slots it
-// reads. The tag (Ctl::epoch) is advanced once per launch by the pick; every slot buffer is written
-// once per launch, so a slot never holds the current tag before its producer has written it.
-// At the end of a phase each workgroup starts direct loads into LDS of the next Linear phase's
-// weight rows, LayerNorm gain and bias and Linear biases (and an attention workgroup those of its
-// chunk's cached key and value rows), so they stream from HBM while the hand-over latency runs and
-// hold no registers. Cross-lane sums use DPP within 16-lane rows. Every wait is bounded (wall clock, plus an abort flag that the
-// first workgroup to time out sets), so a launch always ends; the host reports a timeout.
-// Data written in earlier launches (the KV cache, the token sequence, Ctl) is read with ordinary
-// loads: the kernel boundary makes it visible on every XCD.
-
-constexpr int kWaves = kThreads / 64;
-
-struct Ctl {
-    uint32_t epoch;  // tag of the current launch's slots (advanced by the pick)
-    uint32_t abort;  // set by the first workgroup whose wait timed out
-    uint32_t error;  // 1 + the phase that timed out (0: none)
-    uint32_t pad;
-};
-
-struct LayerParams {
-    const float *ln1_w, *ln1_b, *qkv_w, *qkv_b, *proj_w, *proj_b, *ln2_w, *ln2_b, *fc1_w, *fc1_b, *fc2_w, *fc2_b;
-};
-
-struct StepArgs {
-    const LayerParams* layer;  // [layers], device memory
-    const float* wte;
-    const float* wpe;
-    const float* lnf_w;
-    const float* lnf_b;
-    int64_t layers, d, heads, hd, ff, vocab, max_positions;
-    float* kcache;
-    float* vcache;
-    // slots, [layers][n] each: x after proj (xa) and after fc2 (xb), qkv, attention output, fc1 output
-    uint64_t* xa;
-    uint64_t* xb;
-    uint64_t* qkv;
-    uint64_t* att;
-    uint64_t* f;
-    uint64_t* best;  // [2 G]: each workgroup's best head row (value, index)
-    uint64_t* part;  // [layers][heads][chunks][hd + 3]: partial attention of each key chunk
-    int64_t chunks;  // key chunks per head (workgroups per head in the attention phase)
-    float* logits;
-    Step* st;
-    int64_t* seq;
-    Ctl* ctl;
-    float divisor;
-    int tanh_gelu;
-};
-
-__device__ __forceinline__ void slot_put(uint64_t* s, float v, uint32_t tag) {
-    const uint64_t bits = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
-    __hip_atomic_store(s, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t slot_get(const uint64_t* s) {
-    return __hip_atomic_load(const_cast<uint64_t*>(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-constexpr uint64_t kWaitTicks = 2000000;  // 20 ms of s_memrealtime (100 MHz)
-constexpr int kMaxPickSlots = 1024;       // 2 per workgroup: grids of at most 512 workgroups
-
-// s_waitcnt vmcnt(0) (gfx9 encoding, expcnt and lgkmcnt left at their maxima): the wave's vector
-// memory operations, direct loads into LDS included, have completed.
-constexpr int kWaitVmcnt = 0x0F70;
-
-// Direct loads from global memory into LDS (global_load_lds): lane i of the wave writes its element
-// at wave_dst + i, wave_dst being the same for the whole wave. They hold no registers; a wave waits
-// for them only where it waits for its later vector loads (s_waitcnt vmcnt counts in issue order).
-__device__ __forceinline__ void lds_load16(const float4* src, float4* wave_dst) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                     (__attribute__((address_space(3))) void*)(wave_dst), 16, 0, 0);
-}
-
-__device__ __forceinline__ void lds_load4(const float* src, float* wave_dst) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                     (__attribute__((address_space(3))) void*)(wave_dst), 4, 0, 0);
-}
-
-// Waits until slots s[0, n) all hold `tag` and stores their values in dst[0, n) (LDS); n <= PER *
-// kThreads. Wave 0 first polls up to 64 slots spread over the range while the other waves wait at
-// the barrier: the workgroups waiting for a phase then put little traffic on the few memory channels
-// that hold its slots. Then every thread reads its own slots until they hold `tag`. On return every
-// wave's vector loads, direct LDS loads included, have completed and are visible to the whole
-// workgroup. Returns false for the whole workgroup when the launch is being aborted or this wait timed
-// out (then it sets the abort flag and records `phase`). Callers pass a barrier between two calls.
-template <int PER>
-__device__ __forceinline__ bool gather_slots(const uint64_t* s, int64_t n, uint32_t tag, float* dst, Ctl* ctl, int phase) {
-    __shared__ int failed;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    // every 16th round: is the launch being aborted, or has this wait run out of time?
-    const auto give_up = [&](uint32_t round) {
-        if ((round & 15) != 15) return false;
-        if (__hip_atomic_load(&ctl->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
-            __builtin_amdgcn_s_memrealtime() - t0 <= kWaitTicks)
-            return false;
-        if (__hip_atomic_exchange(&ctl->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
-            __hip_atomic_store(&ctl->error, static_cast<uint32_t>(1 + phase), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return true;
-    };
-    if (threadIdx.x < 64) {
-        if (threadIdx.x == 0) failed = 0;
-        const int64_t stride = (n + 63) / 64;
-        const int64_t i = static_cast<int64_t>(threadIdx.x) * stride;
-        bool ready = i >= n;
-        for (uint32_t round = 0;; ++round) {
-            if (!ready) ready = static_cast<uint32_t>(slot_get(s + i) >> 32) == tag;
-            if (__all(ready)) break;
-            if (give_up(round)) {
-                failed = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-    __syncthreads();
-    if (failed != 0) return false;
-    uint32_t pending = 0;
-#pragma unroll
-    for (int k = 0; k < PER; ++k)
-        if (threadIdx.x + k * kThreads < n) pending |= 1u << k;
-    for (uint32_t round = 0; pending != 0; ++round) {
-        uint64_t v[PER];
-#pragma unroll
-        for (int k = 0; k < PER; ++k)
-            if (pending & (1u << k)) v[k] = slot_get(s + threadIdx.x + k * kThreads);
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            if ((pending & (1u << k)) && static_cast<uint32_t>(v[k] >> 32) == tag) {
-                dst[threadIdx.x + k * kThreads] = __uint_as_float(static_cast<uint32_t>(v[k]));
-                pending &= ~(1u << k);
-            }
-        }
-        if (pending == 0) break;
-        if (give_up(round)) {
-            failed = 1;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt);
-    __syncthreads();
-    return failed == 0;
-}
-
-// This workgroup's share [r0, r1) of n rows.
-struct Rows {
-    int64_t r0, r1;
-};
-__device__ __forceinline__ Rows rows_of(int64_t n) {
-    return Rows{n * blockIdx.x / gridDim.x, n * (blockIdx.x + 1) / gridDim.x};
-}
-
-// A workgroup's weight block W[r0, r1) x K as items of 64 float4 (one per lane): item j covers row
-// r0 + j / S, float4 columns [64 (j % S), 64 (j % S) + 64) with S = ceil(K / 256) segments per row;
-// wave w holds items w, w + kWaves, w + 2 kWaves, ... The item -> (row, segment) map of each phase is
-// an LDS table built once per launch: reading it is a broadcast, and keeping it in LDS keeps the
-// compiler from holding every item's offsets of every phase in registers across the layer loop.
-constexpr uint32_t kNoItem = 0xffffffffu;
-
-struct Block {
-    const float* W;       // row r0 of the weight matrix
-    uint32_t K;           // row length (floats)
-    uint32_t rows;        // r1 - r0
-    const uint32_t* map;  // [kWaves * NI]: (row << 16 | segment) or kNoItem
-};
-
-// Fills map[0, count) for a block of `rows` rows of K floats.
-__device__ __forceinline__ void build_map(uint32_t* map, int count, int64_t rows, int64_t K) {
-    const uint32_t S = static_cast<uint32_t>((K / 4 + 63) / 64);
-    const uint32_t items = static_cast<uint32_t>(rows) * S;
-    for (int j = threadIdx.x; j < count; j += kThreads)
-        map[j] = static_cast<uint32_t>(j) < items ? (static_cast<uint32_t>(j) / S) << 16 | (static_cast<uint32_t>(j) % S) : kNoItem;
-}
-
-// The waves of a workgroup split the work of a phase's end: wave 0 goes straight on to poll for the
-// next phase's input, waves 1..kWaves-1 issue the direct LDS loads of the next phase's operands, and
-// the slot outputs are written by threads from 64 on (output r by thread writer_of(r)). A wave's
-// loads return in issue order, so a poll issued behind loads or stores would wait for them too.
-constexpr int kLoaders = kWaves - 1;
-__device__ __forceinline__ int writer_row() { return (static_cast<int>(threadIdx.x) + kThreads - 64) % kThreads; }
-
-// Starts the direct loads of the block into buf (LDS, kWaves * NI items of 64 float4): item j at
-// buf[64 j, 64 j + 64), issued by the loader waves. Lanes past the end of a row load nothing
-// (block_dot skips them).
-template <int NI> __device__ __forceinline__ void block_prefetch(const Block& b, float4* buf) {
-    constexpr int kPer = (kWaves * NI + kLoaders - 1) / kLoaders;  // items per loader wave
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    if (wave == 0) return;
-    const uint32_t q = b.K / 4;
-    const float4* W4 = reinterpret_cast<const float4*>(b.W);
-    uint32_t e[kPer];  // all map reads first: one LDS round trip, not one per load
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int j = wave - 1 + i * kLoaders;
-        e[i] = j < kWaves * NI ? b.map[j] : kNoItem;
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const uint32_t c = (e[i] & 0xffffu) * 64 + lane;
-        if (e[i] != kNoItem && c < q) lds_load16(W4 + (e[i] >> 16) * q + c, buf + 64 * (wave - 1 + i * kLoaders));
-    }
-}
-
-// Row dot products of the block in buf (LDS, loaded by block_prefetch) with the vector h (LDS, K
-// floats): returns the dot of row r0 + threadIdx.x for threadIdx.x < rows (segments added in order).
-template <int NI>
-__device__ __forceinline__ float block_dot(const Block& b, const float4* buf, const float4* h4, float* itemsum) {
-    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const uint32_t q = b.K / 4;
-    const uint32_t S = (q + 63) / 64;
-    // Branch-free: every lane reads its (in-bounds, clamped) operands of every item, so the LDS reads
-    // of all items are in flight together; lanes past a row's end and absent items select 0 (their
-    // buffer words are stale LDS, never multiplied).
-    uint32_t e[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) e[i] = b.map[wave + i * kWaves];
-    float p[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const uint32_t c = (e[i] & 0xffffu) * 64 + lane;
-        const float4 w = buf[64 * (wave + i * kWaves) + lane];
-        const float4 x = h4[c < q ? c : q - 1];
-        const float t = w.x * x.x + w.y * x.y + w.z * x.z + w.w * x.w;
-        p[i] = e[i] != kNoItem && c < q ? t : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        if (e[i] != kNoItem) {
-            const float t = wave_sum(p[i]);
-            if (lane == 0) itemsum[wave + i * kWaves] = t;
-        }
-    }
-    __syncthreads();
-    float sum = 0.f;  // row writer_row()'s dot, in that row's writer thread
-    if (static_cast<uint32_t>(writer_row()) < b.rows) {
-        const float* row = itemsum + writer_row() * S;
-        uint32_t s = 0;
-        for (; s + 4 <= S; s += 4) {  // four reads in flight, added in order
-            const float v0 = row[s], v1 = row[s + 1], v2 = row[s + 2], v3 = row[s + 3];
-            sum = (((sum + v0) + v1) + v2) + v3;
-        }
-        for (; s < S; ++s) sum += row[s];
-    }
-    __syncthreads();  // itemsum is reused by the next phase
-    return sum;
-}
-
-// Starts the direct loads of n floats from src into dst (LDS) in blocks of 64, on the loader waves.
-__device__ __forceinline__ void lds_copy(const float* src, int64_t n, float* dst) {
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    if (wave == 0) return;
-    for (int64_t blk = wave - 1; 64 * blk < n; blk += kLoaders)
-        if (64 * blk + lane < n) lds_load4(src + 64 * blk + lane, dst + 64 * blk);
-}
-
-// Starts the direct loads of a LayerNorm's gain and bias (d floats each) into lw / lb (LDS).
-__device__ __forceinline__ void ln_prefetch(const float* w, const float* b, int64_t d, float* lw, float* lb) {
-    lds_copy(w, d, lw);
-    lds_copy(b, d, lb);
-}
-
-// LayerNorm of xs[0, d) (LDS) into h (LDS) with gain lw and bias lb (LDS), as ln_load / ln_finish
-// compute it.
-__device__ __forceinline__ void ln_lds(const float* xs, int64_t d, const float* lw, const float* lb, float* h) {
-    LnIn r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // in bounds (kMaxLnDim elements each): read, then select
-        const int64_t i = threadIdx.x + j * kThreads;
-        const float x = xs[i], w = lw[i], b = lb[i];
-        r.x[j] = i < d ? x : 0.f;
-        r.w[j] = i < d ? w : 0.f;
-        r.b[j] = i < d ? b : 0.f;
-    }
-    r.c = xs[0];
-    ln_finish(r, d, h);
-    __syncthreads();
-}
-
-// Key (and value) rows per 16-lane group that an attention workgroup stages in LDS ahead of its
-// phase: K and V rows of 16 float4 for 16 groups fill at most one weight buffer of kWaves * NI items.
-template <int NI> constexpr int kv_staged() { return NI / 2 < 8 ? NI / 2 : 8; }
-
-// Attention runs in chunks of key rows: head h's chunk c of C covers rows [j0, j1), R = ceil((pos +
-// 1) / C) rows per chunk, each chunk on its own workgroup; chunks past the last row are empty.
-struct KeyRange {
-    int64_t j0, j1;
-};
-__device__ __forceinline__ KeyRange chunk_rows(int64_t pos, int64_t c, int64_t C) {
-    const int64_t R = (pos + C) / C;
-    const int64_t j0 = c * R < pos + 1 ? c * R : pos + 1;
-    return KeyRange{j0, j0 + R < pos + 1 ? j0 + R : pos + 1};
-}
-__device__ __forceinline__ int64_t active_chunks(int64_t pos, int64_t C) {
-    const int64_t R = (pos + C) / C;
-    return (pos + R) / R;
-}
-
-// Partial attention of head h over key rows [j0, j1) (j0 < j1 <= pos + 1), one workgroup: the scaled
-// scores q.k / sqrt(hd) (16-lane group gq takes rows j0 + gq, j0 + gq + 16, ...), their maximum m, the
-// exponentials exp(score - m) summed in double (s) and the exponential-weighted sum of the value rows
-// (acc). Rows below j0 + 16 U come from kv (LDS: row j0 + r's K at kv[16 r, 16 r + 16), its V U
-// kThreads float4 further; lanes past head_dim hold stale LDS and read zeros instead), other cached
-// rows from the cache, row pos from (kn, vn). Leaves part[0] = m, part[1] / part[2] = the high / low
-// words of s and part[3 + i] = acc[i] for i < hd (LDS), then a barrier.
-template <int U>
-__device__ __forceinline__ void attention_chunk(const StepArgs& a, int64_t l, int64_t h, int64_t pos, int64_t j0, int64_t j1,
-                                                const float* qh, const float* kn, const float* vn, const float4* kv,
-                                                float* scores, float* part) {
-    __shared__ float red_f[kWaves];
-    __shared__ double red_d[kWaves];
-    __shared__ float4 acc_part[kWaves][16];
-    const int64_t hd = a.hd;
-    const int64_t rows = j1 - j0;
-    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-    const int sub = tid % 16, group = tid / 16;
-    constexpr int kGroups = kThreads / 16;
-    const bool dims_ok = 4 * sub < hd;
-    const float* K = a.kcache + ((l * a.heads + h) * a.max_positions) * hd + 4 * sub;
-    const float* V = a.vcache + ((l * a.heads + h) * a.max_positions) * hd + 4 * sub;
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4 qv = dims_ok ? reinterpret_cast<const float4*>(qh)[sub] : zero;
-    const int64_t r_pos = pos - j0;  // row pos (from the slots) if it is in this chunk
-    // this lane's float4 of staged row r (K: base 0, V: base U kThreads)
-    const auto staged = [&](int64_t r, int base) { return dims_ok ? kv[base + 16 * r + sub] : zero; };
-    float local_max = -INFINITY;
-    const auto score = [&](int64_t r, float4 k) {  // a whole 16-lane group calls it for row r
-        float sc = qv.x * k.x + qv.y * k.y + qv.z * k.z + qv.w * k.w;
-        sc = __fdiv_rn(row16_sum(sc), a.divisor);
-        if (sub == 0) scores[r] = sc;
-        local_max = max_na(local_max, sc);
-    };
-    float4 kst[U];  // staged rows read before any is used (in bounds: r < 16 U)
-#pragma unroll
-    for (int u = 0; u < U; ++u) kst[u] = staged(group + u * kGroups, 0);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t r = group + u * kGroups;
-        if (r < rows && r != r_pos) score(r, kst[u]);
-    }
-    for (int64_t rb = group + U * kGroups; rb < rows; rb += kAttnRegs * kGroups) {
-        float4 kb[kAttnRegs];
-#pragma unroll
-        for (int u = 0; u < kAttnRegs; ++u) {
-            const int64_t r = rb + u * kGroups;
-            kb[u] = dims_ok && r < rows && r != r_pos ? gload4(reinterpret_cast<const float4*>(K + (j0 + r) * hd)) : zero;
-        }
-#pragma unroll
-        for (int u = 0; u < kAttnRegs; ++u) {
-            const int64_t r = rb + u * kGroups;
-            if (r < rows && r != r_pos) score(r, kb[u]);
-        }
-    }
-    if (r_pos < rows && group == r_pos % kGroups) score(r_pos, dims_ok ? reinterpret_cast<const float4*>(kn)[sub] : zero);
-    local_max = wave_max(local_max);
-    if (lane == 0) red_f[wave] = local_max;
-    __syncthreads();
-    float m = red_f[0];
-    for (int w = 1; w < kWaves; ++w) m = max_na(m, red_f[w]);
-    double total = 0.0;
-    for (int64_t r = tid; r < rows; r += kThreads) {
-        const float e = std::exp(__fsub_rn(scores[r], m));
-        scores[r] = e;
-        total += static_cast<double>(e);
-    }
-    total = wave_sum(total);
-    if (lane == 0) red_d[wave] = total;
-    __syncthreads();
-    float4 acc = zero;
-    const auto accumulate = [&](int64_t r, float4 v) {
-        const float w = scores[r];
-        acc.x += w * v.x;
-        acc.y += w * v.y;
-        acc.z += w * v.z;
-        acc.w += w * v.w;
-    };
-#pragma unroll
-    for (int u = 0; u < U; ++u) kst[u] = staged(group + u * kGroups, U * kThreads);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t r = group + u * kGroups;
-        if (r < rows && r != r_pos) accumulate(r, kst[u]);
-    }
-    for (int64_t rb = group + U * kGroups; rb < rows; rb += kAttnRegs * kGroups) {
-        float4 vb[kAttnRegs];
-#pragma unroll
-        for (int u = 0; u < kAttnRegs; ++u) {
-            const int64_t r = rb + u * kGroups;
-            vb[u] = dims_ok && r < rows && r != r_pos ? gload4(reinterpret_cast<const float4*>(V + (j0 + r) * hd)) : zero;
-        }
-#pragma unroll
-        for (int u = 0; u < kAttnRegs; ++u) {
-            const int64_t r = rb + u * kGroups;
-            if (r < rows && r != r_pos) accumulate(r, vb[u]);
-        }
-    }
-    if (r_pos < rows && group == r_pos % kGroups) accumulate(r_pos, dims_ok ? reinterpret_cast<const float4*>(vn)[sub] : zero);
-    // the four groups of each wave (lanes sub, sub + 16, sub + 32, sub + 48), then the waves
-#pragma unroll
-    for (int m = 16; m <= 32; m *= 2) {
-        acc.x += __shfl_xor(acc.x, m, 64);
-        acc.y += __shfl_xor(acc.y, m, 64);
-        acc.z += __shfl_xor(acc.z, m, 64);
-        acc.w += __shfl_xor(acc.w, m, 64);
-    }
-    if (lane < 16) acc_part[wave][sub] = acc;
-    __syncthreads();
-    if (tid < hd) {
-        const int s4 = tid / 4, e = tid % 4;
-        float4 pw[kWaves];
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) pw[w] = acc_part[w][s4];
-        float r = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) r += e == 0 ? pw[w].x : e == 1 ? pw[w].y : e == 2 ? pw[w].z : pw[w].w;
-        part[3 + tid] = r;
-    }
-    if (tid == 0) {
-        double sum = red_d[0];
-        for (int w = 1; w < kWaves; ++w) sum += red_d[w];
-        const uint64_t bits = __builtin_bit_cast(uint64_t, sum);
-        part[0] = m;
-        part[1] = __uint_as_float(static_cast<uint32_t>(bits >> 32));
-        part[2] = __uint_as_float(static_cast<uint32_t>(bits));
-    }
-    __syncthreads();
-}
-
-// Head h's attention output (element i < hd) from its chunks' partials p (LDS, `chunks` runs of hd +
-// 3 as attention_chunk leaves them): each chunk's exponentials rescaled by exp(m_c - M) to the
-// largest maximum M, the weighted value sums added in chunk order and divided by the float rounding
-// of the rescaled exponential sum (for one chunk: acc / s, the row softmax's own division).
-__device__ __forceinline__ float attention_combine(const float* p, int64_t chunks, int64_t hd, int64_t i) {
-    float M = p[0];
-    for (int64_t c = 1; c < chunks; ++c) M = max_na(M, p[c * (hd + 3)]);
-    double S = 0.0;
-    float o = 0.f;
-    for (int64_t c = 0; c < chunks; ++c) {
-        const float* q = p + c * (hd + 3);
-        const float f = std::exp(__fsub_rn(q[0], M));
-        const uint64_t bits = static_cast<uint64_t>(__float_as_uint(q[1])) << 32 | __float_as_uint(q[2]);
-        S += __builtin_bit_cast(double, bits) * static_cast<double>(f);
-        o += q[3 + i] * f;
-    }
-    return __fdiv_rn(o, static_cast<float>(S));
-}
-
-// The phases of a step, in order: five per layer, then the head and the pick. One loop runs them,
-// so the gather, LayerNorm and row-dot code exists once (the kernel's code stays small enough for
-// the instruction cache, which a fully unrolled sequence of phases overflowed).
-enum StepPhase { kPhQkv = 0, kPhAttention = 1, kPhProj = 2, kPhFc1 = 3, kPhFc2 = 4 };
-
-constexpr int64_t kMaxStepLayers = 48;  // layers of the persistent step's parameter table (LDS)
-
-// One decode step in one launch of G workgroups (one per CU, all resident): every Linear phase
-// splits its rows over the workgroups, which hand activations to each other through tagged slots.
-// The operands of the next Linear phase (its weight rows, LayerNorm gain and bias, Linear biases) and
-// the attention workgroups' first cached key / value rows are loaded straight into LDS at the end of
-// a phase, so that they arrive while the workgroup waits for the next phase's input.
-template <int NI>
-__global__ __launch_bounds__(kThreads) void decode_step_kernel(StepArgs a) {
-    extern __shared__ float scores[];  // [max_positions]
-    // weight blocks of the Linear phases: qkv and fc1 use buffer 0, proj and fc2 buffer 1; buffer 0
-    // also holds an attention workgroup's staged key / value rows and the head's first rows
-    __shared__ float4 wbuf[2][kWaves * NI * 64];
-    __shared__ float4 xs4[kMaxLnDim / 4];  // the layer's input x (raw), for LayerNorm and the residual
-    __shared__ float4 hs4[kMaxK / 4];      // the GEMV input (LayerNorm output, attention output or fc1 output)
-    __shared__ float4 qkv4[3 * 64 / 4];    // an attention workgroup's q, k, v rows of its head
-    __shared__ float part_s[64 + 3];       // its chunk's partial attention
-    __shared__ float lnw[kMaxLnDim], lnb[kMaxLnDim];  // LayerNorm gain and bias of the next LayerNorm
-    __shared__ float bias_s[kThreads];     // this workgroup's Linear biases of the next Linear phase
-    __shared__ float itemsum[kWaves * NI];
-    __shared__ uint32_t item_map[4][kWaves * NI];  // qkv, proj, fc1, fc2
-    float* xs = reinterpret_cast<float*>(xs4);
-    float* hs = reinterpret_cast<float*>(hs4);
-    float* qh = reinterpret_cast<float*>(qkv4);
-    // The previous launch wrote these; agent-scope loads read them from memory on every XCD.
-    const uint32_t tag = __hip_atomic_load(&a.ctl->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t pos = __hip_atomic_load(&a.st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t tok = __hip_atomic_load(a.seq + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t d = a.d, hd = a.hd, ff = a.ff;
-    const int g = blockIdx.x;
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    // the per-layer parameter table, copied into LDS once (scalar loads of it would miss: the weights
-    // streaming through the caches evict it, and a miss stalls the next phase's operand loads)
-    __shared__ LayerParams layer[kMaxStepLayers];
-    {
-        static_assert(sizeof(LayerParams) % sizeof(uint64_t) == 0, "LayerParams is an array of pointers");
-        constexpr int kWords = sizeof(LayerParams) / sizeof(uint64_t);
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.layer);
-        uint64_t* dst = reinterpret_cast<uint64_t*>(layer);
-        for (int64_t i = threadIdx.x; i < a.layers * kWords; i += kThreads) dst[i] = src[i];
-    }
-    // this workgroup's rows of the four Linear products (qkv, proj, fc1, fc2) and of the head
-    // (an LDS table: a private array indexed by the phase would live in scratch memory, whose loads
-    // wait behind the staged operand loads)
-    __shared__ int64_t row_lo[4], row_hi[4];
-    if (threadIdx.x < 4) {
-        const Rows r = rows_of(threadIdx.x == 0 ? 3 * d : threadIdx.x == 2 ? ff : d);
-        row_lo[threadIdx.x] = r.r0;
-        row_hi[threadIdx.x] = r.r1;
-    }
-    __syncthreads();
-    const auto rows_for = [&](int m) { return Rows{row_lo[m], row_hi[m]}; };
-    const auto k_for = [&](int m) { return m == 3 ? ff : d; };
-    const Rows rh = rows_of(a.vocab);
-    for (int m = 0; m < 4; ++m) build_map(item_map[m], kWaves * NI, rows_for(m).r1 - rows_for(m).r0, k_for(m));
-    __syncthreads();
-    const auto block = [&](int64_t l, int m) {
-        const float* W = m == 0 ? layer[l].qkv_w : m == 1 ? layer[l].proj_w : m == 2 ? layer[l].fc1_w : layer[l].fc2_w;
-        const Rows r = rows_for(m);
-        return Block{W + r.r0 * k_for(m), static_cast<uint32_t>(k_for(m)), static_cast<uint32_t>(r.r1 - r.r0), item_map[m]};
-    };
-    // the attention chunk this workgroup runs, if any: chunk k of the heads * C is workgroup
-    // floor(k G / (heads * C)), so the chunks spread over the grid (and its XCDs)
-    const int64_t C = a.chunks, n_chunks = a.heads * a.chunks, G = gridDim.x;
-    int64_t my_head = -1, my_chunk = -1;
-    {
-        const int64_t k = (g * n_chunks + G - 1) / G;
-        if (k < n_chunks && k * G / n_chunks == g) {
-            my_head = k / C;
-            my_chunk = k - my_head * C;
-        }
-    }
-    const int64_t active = active_chunks(pos, C);
-    if (my_chunk >= active) my_head = my_chunk = -1;  // an empty chunk
-    const KeyRange keys = chunk_rows(pos, my_chunk < 0 ? 0 : my_chunk, C);
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4* W4 = reinterpret_cast<const float4*>(a.wte);
-    const int64_t k4 = d / 4;
-    constexpr int U = kv_staged<NI>();
-    // The head's first row pair of each wave (rows r0 + wave and r0 + wave + kWaves) is staged in
-    // buffer 0 when it fits there.
-    constexpr bool kHeadStaged = 2 * kHeadVec <= NI;
-    float4* head_stage = wbuf[0] + 2 * kHeadVec * 64 * wave;  // this wave's staged head rows
-    const int64_t last = 5 * a.layers;  // phase `last` is the head
-    // Starts the loads of the operands of phase q (a Linear phase or the head) into LDS.
-    const auto prefetch = [&](int64_t q) {
-        const int64_t lq = q / 5;
-        const int kq = static_cast<int>(q - 5 * lq);
-        if (q == last) {
-            ln_prefetch(a.lnf_w, a.lnf_b, d, lnw, lnb);
-            if constexpr (kHeadStaged) {
-                // block (w, r, i): consumer wave w's row r0 + w + r kWaves, float4 [64 i, 64 i + 64)
-                for (int blk = wave - 1; wave > 0 && blk < kWaves * 2 * kHeadVec; blk += kLoaders) {
-                    const int w = blk / (2 * kHeadVec), r = blk / kHeadVec % 2, i = blk % kHeadVec;
-                    const int64_t n = rh.r0 + w + r * kWaves;
-                    if (n < rh.r1 && lane + 64 * i < k4)
-                        lds_load16(W4 + n * k4 + lane + 64 * i, wbuf[0] + 2 * kHeadVec * 64 * w + (r * kHeadVec + i) * 64);
-                }
-            }
-            return;
-        }
-        const int mq = kq == kPhQkv ? 0 : kq - 1;
-        block_prefetch<NI>(block(lq, mq), wbuf[mq & 1]);
-        if (kq == kPhQkv) ln_prefetch(layer[lq].ln1_w, layer[lq].ln1_b, d, lnw, lnb);
-        if (kq == kPhFc1) ln_prefetch(layer[lq].ln2_w, layer[lq].ln2_b, d, lnw, lnb);
-        const float* bvec = mq == 0 ? layer[lq].qkv_b : mq == 1 ? layer[lq].proj_b : mq == 2 ? layer[lq].fc1_b : layer[lq].fc2_b;
-        const Rows rq = rows_for(mq);
-        lds_copy(bvec + rq.r0, rq.r1 - rq.r0, bias_s);
-    };
-    prefetch(0);
-    for (int64_t p = 0; p <= last; ++p) {
-        const int64_t l = p / 5;
-        const int kind = static_cast<int>(p - 5 * l);
-        if (p < last && kind == kPhAttention) {
-            if (my_head >= 0) {
-                const int64_t h = my_head;
-                // head-major qkv slots: q, k, v of head h in one run
-                if (!gather_slots<kMaxK / kThreads>(a.qkv + l * 3 * d + h * 3 * hd, 3 * hd, tag, qh, a.ctl, 1)) return;
-                attention_chunk<U>(a, l, h, pos, keys.j0, keys.j1, qh, qh + hd, qh + 2 * hd, wbuf[0], scores, part_s);
-                uint64_t* parts = a.part + (l * a.heads + h) * C * (hd + 3);
-                const int wr = writer_row();
-                if (wr < hd + 3) slot_put(parts + my_chunk * (hd + 3) + wr, part_s[wr], tag);
-                if (my_chunk == 0) {  // the head's combining workgroup
-                    if (!gather_slots<kMaxK / kThreads>(parts, active * (hd + 3), tag, hs, a.ctl, 7)) return;
-                    if (wr < hd) slot_put(a.att + l * d + h * hd + wr, attention_combine(hs, active, hd, wr), tag);
-                }
-            }
-            continue;
-        }
-        const int m = p == last ? 0 : kind == kPhQkv ? 0 : kind - 1;  // Linear product of this phase
-        // this phase's input vector
-        const uint64_t* src = p == last           ? a.xb + (l - 1) * d
-                              : kind == kPhQkv    ? a.xb + (l - 1) * d
-                              : kind == kPhProj   ? a.att + l * d
-                              : kind == kPhFc1    ? a.xa + l * d
-                                                  : a.f + l * ff;
-        const int64_t n_in = kind == kPhFc2 && p < last ? ff : d;
-        const bool to_x = p == last || kind == kPhQkv || kind == kPhFc1;  // kept raw in xs, normalised into hs
-        if (kind == kPhQkv && l == 0 && p < last) {
-            for (int64_t i = threadIdx.x; i < d; i += kThreads) xs[i] = __fadd_rn(gload(a.wte + tok * d + i), gload(a.wpe + pos * d + i));
-            __builtin_amdgcn_s_waitcnt(kWaitVmcnt);  // the staged operands of this phase, for every wave
-            __syncthreads();
-        } else if (!gather_slots<kMaxK / kThreads>(src, n_in, tag, to_x ? xs : hs, a.ctl, p == last ? 5 : kind)) {
-            return;
-        }
-        if (to_x) ln_lds(xs, d, lnw, lnb, hs);
-        if (p == last) break;
-        const float dot = block_dot<NI>(block(l, m), wbuf[m & 1], hs4, itemsum);
-        const Rows rm = rows_for(m);
-        const int wr = writer_row();  // block_dot left row wr's dot in this thread
-        if (wr < rm.r1 - rm.r0) {
-            const int64_t n = rm.r0 + wr;
-            const float y = __fadd_rn(dot, bias_s[wr]);
-            if (kind == kPhQkv) {
-                const uint32_t nn = static_cast<uint32_t>(n), dd = static_cast<uint32_t>(d), hh = static_cast<uint32_t>(hd);
-                const uint32_t part = nn / dd;  // 0 query, 1 key, 2 value
-                const uint32_t within = nn - part * dd;
-                const uint32_t head = within / hh, dim = within - head * hh;
-                // head-major slots, so that an attention workgroup gathers one run: q, k, v of its head
-                slot_put(a.qkv + l * 3 * d + (head * 3 + part) * hh + dim, y, tag);
-                if (part > 0) {  // the key / value row of this position, kept for later tokens
-                    float* cache = part == 1 ? a.kcache : a.vcache;
-                    gstore(cache + ((l * a.heads + head) * a.max_positions + pos) * hd + dim, y);
-                }
-            } else if (kind == kPhProj) {
-                slot_put(a.xa + l * d + n, __fadd_rn(xs[n], y), tag);
-            } else if (kind == kPhFc1) {
-                slot_put(a.f + l * ff + n, a.tanh_gelu ? gelu_of<kGeluTanh>(y) : gelu_of<kGeluExact>(y), tag);
-            } else {
-                slot_put(a.xb + l * d + n, __fadd_rn(xs[n], y), tag);
-            }
-        }
-        __syncthreads();  // bias_s, lnw / lnb and this phase's weight buffer are free again
-        // the next Linear phase's operands (the phase after qkv is attention, then proj)
-        prefetch(kind == kPhQkv ? p + 2 : p + 1);
-        if (kind == kPhQkv && my_head >= 0 && wave > 0) {
-            // the chunk's first 16 U cached key / value rows of this layer, for the attention phase:
-            // row j0 + r's float4 `sub` at 16 r + sub, so block (u, w) of 64 lanes holds rows 16 u + 4 w
-            // .. 16 u + 4 w + 3; the loader waves issue the blocks
-            const int sub = lane % 16;
-            const float* K = a.kcache + ((l * a.heads + my_head) * a.max_positions) * hd;
-            const float* V = a.vcache + ((l * a.heads + my_head) * a.max_positions) * hd;
-            for (int blk = wave - 1; blk < U * kWaves; blk += kLoaders) {
-                const int u = blk / kWaves, w = blk % kWaves;
-                const int64_t j = keys.j0 + 16 * u + 4 * w + lane / 16;
-                if (4 * sub < hd && j < keys.j1 && j < pos) {
-                    lds_load16(reinterpret_cast<const float4*>(K + j * hd + 4 * sub), wbuf[0] + u * kThreads + 64 * w);
-                    lds_load16(reinterpret_cast<const float4*>(V + j * hd + 4 * sub), wbuf[0] + (U + u) * kThreads + 64 * w);
-                }
-            }
-        }
-    }
-    // ---- head: logits of rows rh and this workgroup's first maximum ----
-    float4 hv[kHeadVec];
-#pragma unroll
-    for (int i = 0; i < kHeadVec; ++i) {
-        const int64_t j = lane + 64 * i;
-        hv[i] = j < k4 ? hs4[j] : zero;
-    }
-    // head rows r0 + wave, r0 + wave + kWaves, ...
-    const auto load_row = [&](int64_t n, float4 (&r)[kHeadVec]) {
-#pragma unroll
-        for (int i = 0; i < kHeadVec; ++i) {
-            const int64_t j = lane + 64 * i;
-            r[i] = n < rh.r1 && j < k4 ? nt_load4(W4 + n * k4 + j) : zero;
-        }
-    };
-    float4 c0[kHeadVec], c1[kHeadVec];
-    if constexpr (kHeadStaged) {
-#pragma unroll
-        for (int i = 0; i < kHeadVec; ++i) {
-            // lanes past the row end hold stale LDS: select zeros, not products with them
-            const bool in_row = lane + 64 * i < k4;
-            c0[i] = in_row ? head_stage[i * 64 + lane] : zero;
-            c1[i] = in_row ? head_stage[(kHeadVec + i) * 64 + lane] : zero;
-        }
-    } else {
-        load_row(rh.r0 + wave, c0);
-        load_row(rh.r0 + wave + kWaves, c1);
-    }
-    Best best{-INFINITY, INT64_MAX};
-    for (int64_t n = rh.r0 + wave; n < rh.r1; n += 2 * kWaves) {
-        float4 n0[kHeadVec], n1[kHeadVec];
-        load_row(n + 2 * kWaves, n0);
-        load_row(n + 3 * kWaves, n1);
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int i = 0; i < kHeadVec; ++i) {
-            s0 += c0[i].x * hv[i].x + c0[i].y * hv[i].y + c0[i].z * hv[i].z + c0[i].w * hv[i].w;
-            s1 += c1[i].x * hv[i].x + c1[i].y * hv[i].y + c1[i].z * hv[i].z + c1[i].w * hv[i].w;
-        }
-        s0 = wave_sum(s0);
-        s1 = wave_sum(s1);
-        if (lane == 0) a.logits[n] = s0;
-        const Best o0{s0, n};
-        if (better(o0, best)) best = o0;
-        if (n + kWaves < rh.r1) {
-            if (lane == 0) a.logits[n + kWaves] = s1;
-            const Best o1{s1, n + kWaves};
-            if (better(o1, best)) best = o1;
-        }
-#pragma unroll
-        for (int i = 0; i < kHeadVec; ++i) {
-            c0[i] = n0[i];
-            c1[i] = n1[i];
-        }
-    }
-    __shared__ float bv[kWaves];
-    __shared__ int64_t bi[kWaves];
-    if (lane == 0) {
-        bv[wave] = best.v;
-        bi[wave] = best.i;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        Best r{bv[0], bi[0]};
-        for (int w = 1; w < kWaves; ++w) {
-            const Best o{bv[w], bi[w]};
-            if (better(o, r)) r = o;
-        }
-        // an empty share (vocab < G) reports index -1
-        slot_put(a.best + 2 * g, r.v, tag);
-        slot_put(a.best + 2 * g + 1, __int_as_float(r.i == INT64_MAX ? -1 : static_cast<int>(r.i)), tag);
-    }
-    // ---- the greedy pick: workgroup 0 ----
-    if (g != 0) return;
-    if (!gather_slots<kMaxPickSlots / kThreads>(a.best, 2 * static_cast<int64_t>(gridDim.x), tag, hs, a.ctl, 6)) return;
-    Best r{-INFINITY, INT64_MAX};
-    for (int w = threadIdx.x; w < static_cast<int>(gridDim.x); w += kThreads) {
-        const int idx = __float_as_int(hs[2 * w + 1]);
-        const Best o{hs[2 * w], idx};
-        if (idx >= 0 && better(o, r)) r = o;
-    }
-    r = wave_best(r);
-    if (lane == 0) {
-        bv[wave] = r.v;
-        bi[wave] = r.i;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        r = Best{bv[0], bi[0]};
-        for (int w = 1; w < kWaves; ++w) {
-            const Best o{bv[w], bi[w]};
-            if (better(o, r)) r = o;
-        }
-        if (pos + 1 >= a.st->forced) __hip_atomic_store(a.seq + pos + 1, r.i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&a.st->pos, pos + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&a.ctl->epoch, tag + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
 // ---- batched prefill ---------------------------------------------------------------------------
 //
 // The prompt's T positions pass each layer together: row LayerNorms, the four Linear products
@@ -1648,15 +888,6 @@ struct Engine {
     int64_t* seq = nullptr;
     Step* st = nullptr;
     hipGraphExec_t graph = nullptr;
-    // persistent step (decode_step_kernel): control word, per-layer parameter pointers, slots
-    Ctl* ctl = nullptr;
-    LayerParams* layer_params = nullptr;
-    uint64_t* slots = nullptr;  // xa, xb, qkv, att, f ([layers][n] each), then best [2 G]
-    int64_t slot_count = 0;
-    int grid = 0;               // workgroups of the persistent step (one per CU)
-    int items = 0;              // its weight items per wave (template argument)
-    int64_t chunks = 0;         // its key chunks per head
-    bool broken = false;        // a step timed out: the slots may hold the current tag
     int64_t host_pos = 0;     // mirror of st->pos: positions in the KV cache
     std::vector<int64_t> history;  // the whole sequence so far (prompt + generated), host copy
     int64_t host_forced = 0;
@@ -1705,58 +936,8 @@ struct Engine {
         else hipLaunchKernelGGL((gemv_kernel<Epi, 1, Pro>), rows_grid(a.N, false), dim3(kThreads), 0, s, a);
     }
 
-    // One kernel per phase: the default, and whenever the persistent step was not asked for or does
-    // not fit this configuration.
-    bool phased() const { return (cfg.flags & KD_GPT_PERSISTENT) == 0 || grid == 0; }
-
-    StepArgs step_args() const {
-        StepArgs a{};
-        a.layer = layer_params;
-        a.wte = p("token_embedding.weight");
-        a.wpe = p("position_embedding.weight");
-        a.lnf_w = p("ln_final.weight");
-        a.lnf_b = p("ln_final.bias");
-        a.layers = cfg.layers;
-        a.d = d;
-        a.heads = cfg.heads;
-        a.hd = hd;
-        a.ff = ff;
-        a.vocab = cfg.vocab_size;
-        a.max_positions = cfg.max_positions;
-        a.kcache = kcache;
-        a.vcache = vcache;
-        a.xa = slots;
-        a.xb = a.xa + cfg.layers * d;
-        a.qkv = a.xb + cfg.layers * d;
-        a.att = a.qkv + cfg.layers * 3 * d;
-        a.f = a.att + cfg.layers * d;
-        a.best = a.f + cfg.layers * ff;
-        a.part = a.best + 2 * static_cast<int64_t>(grid);
-        a.chunks = chunks;
-        a.logits = logits;
-        a.st = st;
-        a.seq = seq;
-        a.ctl = ctl;
-        a.divisor = static_cast<float>(std::sqrt(static_cast<double>(hd)));
-        a.tanh_gelu = cfg.tanh_gelu;
-        return a;
-    }
-
-    size_t step_lds() const { return static_cast<size_t>(cfg.max_positions) * sizeof(float); }
-
+    // One decode step: one kernel per phase, 63 launches per GPT-2-small token.
     int record_step(hipStream_t s) {
-        if (phased()) return record_phased(s);
-        const StepArgs a = step_args();
-        const dim3 grid_dim(static_cast<uint32_t>(grid)), block(kThreads);
-        switch (items) {
-        case 4: hipLaunchKernelGGL((decode_step_kernel<4>), grid_dim, block, step_lds(), s, a); break;
-        default: hipLaunchKernelGGL((decode_step_kernel<9>), grid_dim, block, step_lds(), s, a); break;
-        }
-        return KD_OK;
-    }
-
-    // The previous design: one kernel per phase (63 launches per GPT-2-small token).
-    int record_phased(hipStream_t s) {
         const int64_t L = cfg.layers;
         hipLaunchKernelGGL(embed_kernel, dim3(static_cast<uint32_t>((d + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, st,
                            seq, p("token_embedding.weight"), p("position_embedding.weight"), x, d);
@@ -1853,25 +1034,7 @@ struct Engine {
 
     bool eager() const { return (cfg.flags & KD_GPT_EAGER) != 0; }
 
-    // After the engine stream has been synchronised: a persistent step that timed out reports here.
-    int check_steps() {
-        if (phased()) return KD_OK;
-        Ctl c{};
-        KD_HIP(hipMemcpy(&c, ctl, sizeof c, hipMemcpyDeviceToHost));
-        if (c.error != 0 || c.abort != 0) {
-            broken = true;
-            static const char* const kPhase[] = {"the layer input", "the query, key and value rows", "the attention output",
-                                                 "the proj output", "the fc1 output", "the final hidden state",
-                                                 "the head partials", "the attention chunk partials"};
-            const uint32_t ph = c.error >= 1 && c.error <= 8 ? c.error - 1 : 0;
-            return fail(KD_E_RUNTIME, std::string("kd_gpt: a decode step timed out waiting for ") + kPhase[ph] +
-                                          " (a workgroup of the persistent step did not run; the engine must be recreated)");
-        }
-        return KD_OK;
-    }
-
     int steps(int64_t count) {
-        if (broken) return fail(KD_E_RUNTIME, "kd_gpt: an earlier decode step timed out; recreate the engine");
         if (host_pos + count > cfg.max_positions)
             return fail(KD_E_INVALID, "kd_gpt: cached steps past max_positions");
         for (int64_t i = 0; i < count; ++i) {
@@ -2025,7 +1188,6 @@ struct Engine {
         int64_t next = 0;
         KD_HIP(hipMemcpyAsync(&next, seq + window, sizeof next, hipMemcpyDeviceToHost, stream));
         KD_HIP(hipStreamSynchronize(stream));
-        if (int rc = check_steps()) return rc;
         history.push_back(next);
         return KD_OK;
     }
@@ -2044,7 +1206,6 @@ struct Engine {
                 KD_HIP(hipMemcpyAsync(history.data() + old, seq + first, static_cast<size_t>(n) * sizeof(int64_t),
                                       hipMemcpyDeviceToHost, stream));
                 KD_HIP(hipStreamSynchronize(stream));
-                if (int rc = check_steps()) return rc;
                 produced += n;
             } else {
                 if (int rc = run_window()) return rc;
@@ -2059,8 +1220,6 @@ struct Engine {
         for (void* ptr : {static_cast<void*>(pf_x), static_cast<void*>(pf_h), static_cast<void*>(pf_q),
                           static_cast<void*>(pf_a), static_cast<void*>(pf_f), static_cast<void*>(pf_p),
                           static_cast<void*>(wt)})
-            if (ptr) (void)hipFree(ptr);
-        for (void* ptr : {static_cast<void*>(ctl), static_cast<void*>(layer_params), static_cast<void*>(slots)})
             if (ptr) (void)hipFree(ptr);
         for (void* ptr : {static_cast<void*>(params), static_cast<void*>(kcache), static_cast<void*>(vcache),
                           static_cast<void*>(x), static_cast<void*>(q), static_cast<void*>(partials.m),
@@ -2079,52 +1238,6 @@ template <typename T> int alloc(T** out, int64_t count) {
     return KD_OK;
 }
 
-// Weight items per wave (64 float4 each, staged in LDS) that the persistent step needs: a
-// workgroup's share of a phase is at most ceil(n / G) rows of ceil(K / 256) items, spread over kWaves
-// waves. 0: more than 9 (two buffers of them no longer fit in LDS).
-int persistent_items(const kd_gpt_config& c, int grid) {
-    const int64_t d = c.dimension, ff = 4 * c.dimension;
-    const auto need = [&](int64_t n, int64_t k) { return ((n + grid - 1) / grid * ((k / 4 + 63) / 64) + kWaves - 1) / kWaves; };
-    const int64_t most = std::max({need(3 * d, d), need(d, d), need(ff, d), need(d, ff)});
-    return most <= 4 ? 4 : most <= 9 ? 9 : 0;
-}
-
-int create_persistent(Engine& e) {
-    const kd_gpt_config& c = e.cfg;
-    // Configurations it does not fit keep grid 0 and run the phased step.
-    const int grid = compute_units();
-    e.items = persistent_items(c, grid);
-    if (e.items == 0 || grid > kMaxPickSlots / 2 || c.heads > grid || c.layers > kMaxStepLayers) return KD_OK;
-    // Every workgroup of the step must be resident at once (they wait for each other's slots).
-    int per_cu = 0;
-    const void* fn = e.items == 4 ? reinterpret_cast<const void*>(decode_step_kernel<4>)
-                                  : reinterpret_cast<const void*>(decode_step_kernel<9>);
-    KD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, e.step_lds()));
-    if (per_cu < 1) return KD_OK;
-    e.grid = grid;
-    if (int rc = alloc(&e.ctl, 1)) return rc;
-    const Ctl init{1, 0, 0, 0};
-    KD_HIP(hipMemcpy(e.ctl, &init, sizeof init, hipMemcpyHostToDevice));
-    // key chunks per head: up to 16 (a chunk stages 64 rows of a 1024-position cache)
-    e.chunks = std::max<int64_t>(1, std::min<int64_t>(16, grid / c.heads));
-    e.slot_count = c.layers * (e.d + e.d + 3 * e.d + e.d + e.ff) + 2 * static_cast<int64_t>(e.grid) +
-                   c.layers * c.heads * e.chunks * (e.hd + 3);
-    if (int rc = alloc(&e.slots, e.slot_count)) return rc;
-    KD_HIP(hipMemset(e.slots, 0, static_cast<size_t>(e.slot_count) * sizeof(uint64_t)));  // tag 0: never current
-    std::vector<LayerParams> lp(static_cast<size_t>(c.layers));
-    for (int64_t l = 0; l < c.layers; ++l) {
-        const std::string b = "blocks." + std::to_string(l) + ".";
-        lp[static_cast<size_t>(l)] = LayerParams{e.p(b + "ln1.weight"),     e.p(b + "ln1.bias"),     e.p(b + "attn.qkv.weight"),
-                                                 e.p(b + "attn.qkv.bias"),  e.p(b + "attn.proj.weight"),
-                                                 e.p(b + "attn.proj.bias"), e.p(b + "ln2.weight"),    e.p(b + "ln2.bias"),
-                                                 e.p(b + "mlp.fc1.weight"), e.p(b + "mlp.fc1.bias"),  e.p(b + "mlp.fc2.weight"),
-                                                 e.p(b + "mlp.fc2.bias")};
-    }
-    if (int rc = alloc(&e.layer_params, c.layers)) return rc;
-    KD_HIP(hipMemcpy(e.layer_params, lp.data(), lp.size() * sizeof(LayerParams), hipMemcpyHostToDevice));
-    return KD_OK;
-}
-
 // The shapes this engine's kernels handle (KD_OK) or the reason they do not.
 int check_config(const kd_gpt_config& c) {
     if (c.vocab_size <= 0 || c.max_positions <= 0 || c.layers <= 0 || c.heads <= 0 || c.dimension <= 0)
@@ -2138,6 +1251,7 @@ int check_config(const kd_gpt_config& c) {
     static_assert(kMaxK / 4 <= kMaxLnDim, "ln_load holds a row of at most kMaxLnDim elements");
     if (c.heads > kMaxHeads) return fail(KD_E_UNSUPPORTED, "kd_gpt: more than 64 heads is not supported");
     if (c.max_positions > 8192) return fail(KD_E_UNSUPPORTED, "kd_gpt: max_positions above 8192");
+    if ((c.flags & ~(KD_GPT_EAGER | KD_GPT_STEPWISE_PREFILL)) != 0) return fail(KD_E_INVALID, "kd_gpt: unknown flags");
     return KD_OK;
 }
 
@@ -2195,7 +1309,7 @@ int create(Engine& e, const kd_gpt_config& c) {
 
     if (int rc = alloc(&e.seq, c.max_positions + 1)) return rc;
     if (int rc = alloc(&e.st, 1)) return rc;
-    return (c.flags & KD_GPT_PERSISTENT) != 0 ? create_persistent(e) : KD_OK;
+    return KD_OK;
 }
 
 // Copies one parameter into the engine from host or device memory.
@@ -2358,7 +1472,7 @@ int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, fl
     e->history.push_back(0);
     KD_HIP(hipMemcpyAsync(&e->history.back(), e->seq + count, sizeof(int64_t), hipMemcpyDeviceToHost, e->stream));
     KD_HIP(hipStreamSynchronize(e->stream));
-    return e->check_steps();
+    return KD_OK;
 }
 
 int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* length) {

@@ -276,13 +276,11 @@ class Gpt:
 
     EAGER = 1
     STEPWISE_PREFILL = 2
-    PERSISTENT = 4
 
     def __init__(self, backend: Backend, vocab_size=50257, max_positions=1024, layers=12, heads=12, dimension=768,
-                 tanh_gelu=True, eager=False, stepwise_prefill=False, persistent=False):
+                 tanh_gelu=True, eager=False, stepwise_prefill=False):
         self.b = backend
-        flags = ((self.EAGER if eager else 0) | (self.STEPWISE_PREFILL if stepwise_prefill else 0)
-                 | (self.PERSISTENT if persistent else 0))
+        flags = (self.EAGER if eager else 0) | (self.STEPWISE_PREFILL if stepwise_prefill else 0)
         self.config = GptConfig(vocab_size, max_positions, layers, heads, dimension, int(bool(tanh_gelu)), flags)
         h = c_void_p()
         backend.check(backend.lib.kd_gpt_create(ctypes.byref(h), ctypes.byref(self.config)), "kd_gpt_create")

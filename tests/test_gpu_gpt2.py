@@ -259,53 +259,8 @@ def test_generation_past_the_context(kdb, refdev, prompt_len):
         ref.ref_gpt_destroy(h)
 
 
-def test_persistent_step_against_phased_step(kdb, refdev):
-    """The persistent step (KD_GPT_PERSISTENT: one launch per token, workgroups handing activations
-    to each other, attention in key chunks) against the default one-kernel-per-phase step on GPT-2
-    small: the same greedy tokens over 40 steps after a 64-token prompt, and every step's logits
-    within 1e-5 of the largest |logit| (only summation orders differ), both within 1e-4 of kael's
-    cached forward."""
-    ref = refdev
-    ref.ref_set_threads(min(16, max(1, __import__("os").cpu_count() or 1)))
-    h = ref.ref_gpt_create(50257, 1024, 12, 12, 768, 4, 1)
-    assert h, support.ref_error(ref)
-    try:
-        params = export_params(ref, h)
-        prompt = np.random.default_rng(6).integers(0, 50257, 64)
-        runs = []
-        for persistent in (True, False):
-            g = kd.Gpt(kdb, persistent=persistent)
-            for name, data in params:
-                g.load(name, data)
-            g.prefill(prompt)
-            got = [g.logits()]
-            for _ in range(40):
-                g.decode(1)
-                got.append(g.logits())
-            runs.append((g.sequence(), np.stack(got)))
-        np.testing.assert_array_equal(runs[0][0], runs[1][0])
-        scale = np.abs(runs[1][1]).max()
-        assert np.abs(runs[0][1] - runs[1][1]).max() <= 1e-5 * scale
-        want = cpu_cached_logits(ref, h, runs[0][0][:-1], 64, 50257)
-        assert np.abs(runs[0][1] - want).max() <= 1e-4 * np.abs(want).max()
-    finally:
-        ref.ref_gpt_destroy(h)
-
-
-@pytest.mark.parametrize("prompt_len", [1, 5, 16])
-def test_small_model_persistent_step(kdb, refdev, prompt_len):
-    """The persistent step on the small model (head_dim 4: lanes past head_dim in the staged key
-    rows, two heads over the whole grid, chunks of one key row at the first positions): kael's
-    logits and greedy tokens."""
-    ref = refdev
-    h = ref.ref_gpt_create(11, 24, 2, 2, 8, 31, 1)
-    assert h, support.ref_error(ref)
-    try:
-        params = export_params(ref, h)
-        g = kd.Gpt(kdb, 11, 24, 2, 2, 8, True, persistent=True)
-        for name, data in params:
-            g.load(name, data)
-        prompt = np.random.default_rng(prompt_len).integers(0, 11, prompt_len)
-        check_prefill_and_steps(g, ref, h, prompt, min(6, 24 - prompt_len - 1), 11, 1e-5)
-    finally:
-        ref.ref_gpt_destroy(h)
+def test_unknown_flags_are_rejected(kdb):
+    cfg = kd.GptConfig(11, 16, 1, 2, 8, 1, 4)  # bit 2: no such mode
+    h = ctypes.c_void_p()
+    assert kdb.lib.kd_gpt_supported(ctypes.byref(cfg)) == -1  # KD_E_INVALID
+    assert kdb.lib.kd_gpt_create(ctypes.byref(h), ctypes.byref(cfg)) == -1
