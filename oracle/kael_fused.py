@@ -31,11 +31,9 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      over the leading dims of a contiguous tensor (:316-319)
                                      read in place, without plan_reduction's transposed copy
   src/ops/sequence.cpp               cumsum (:95-117) of a device tensor on the device
-  src/autograd/functions_view.cpp    SelectBackward (:77-88) of a device tensor inside a backward pass:
-                                     the full gradient deferred (no zero fill, no copy yet)
-  src/autograd/engine.cpp            backward (:107-153): deferred select gradients of one tensor
-                                     merged in add_to_buffer (:83-88) and written once, slices as
-                                     copies and the rest as zeros, before the receiving node runs
+  src/autograd/node.cpp              AccumulateGrad::apply (:18-36): a device gradient that nothing
+                                     else references becomes the leaf's first gradient without the
+                                     clone's device copy
   src/ops/indexing.cpp, inplace.cpp  gather (:143-156) and scatter_add_ (:160-178) with broadcast 1-D
                                      indices (index_select, index_add_): one range check of the
                                      line (kd_index_bounds) and the indices read in place, instead
@@ -618,148 +616,6 @@ std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const Ge
 
 """
 
-DEFERRED_SELECT_HELPERS = """// MI355X: the gradient of a select during a backward pass (kael's attention takes q, k and v as
-// selects of one fused projection, so three such gradients reach the projection's node) is kept as
-// (dim, [(index, slice gradient)]) beside an allocated but unwritten full tensor, instead of a zero
-// fill of the full shape and a copy into the slice. Two deferred gradients of the same tensor merge
-// into one list (slice gradients of the same index are added), and the engine writes the full
-// tensor once, right before the node that receives it runs: the slices as copies, the rest as
-// zeros, which is the sum kael's buffer would have built from three zero-filled tensors (a -0 in a
-// slice gradient stays -0, where kael's sum of zeros gives +0; the two compare equal). Only the
-// engine sees a deferred tensor: Node::apply is called from the loop below alone, each gradient a
-// node returns goes to add_to_buffer, and each buffered gradient is written before it leaves the
-// buffer. Anomaly detection reads the gradients a node returns, so it turns deferral off.
-struct DeferredSelect {
-    Tensor full;
-    std::int64_t dim = 0;
-    std::vector<std::pair<std::int64_t, Tensor>> parts;
-};
-
-struct DeferredSelects {
-    std::vector<DeferredSelect> entries;
-
-    DeferredSelect* find(const Tensor& t) {
-        for (DeferredSelect& entry : entries) {
-            if (entry.full.impl().get() == t.impl().get()) {
-                return &entry;
-            }
-        }
-        return nullptr;
-    }
-    void erase(const DeferredSelect* entry) {
-        entries.erase(entries.begin() + (entry - entries.data()));
-    }
-};
-
-thread_local DeferredSelects* active_deferred_selects = nullptr;
-
-class DeferredSelectScope {
-public:
-    DeferredSelectScope() : previous_(active_deferred_selects) {
-        active_deferred_selects = detail::anomaly_detection().load() ? nullptr : &selects_;
-    }
-    ~DeferredSelectScope() { active_deferred_selects = previous_; }
-    DeferredSelectScope(const DeferredSelectScope&) = delete;
-    DeferredSelectScope& operator=(const DeferredSelectScope&) = delete;
-
-private:
-    DeferredSelects selects_;
-    DeferredSelects* previous_;
-};
-
-void write_deferred(DeferredSelects& selects, DeferredSelect* entry) {
-    const DeferredSelect taken = std::move(*entry);
-    selects.erase(entry);
-    Tensor full = taken.full;
-    if (static_cast<std::int64_t>(taken.parts.size()) < full.size(taken.dim)) {
-        // one fill kernel over the whole (contiguous, freshly allocated) tensor, as zeros() does;
-        // all-zero bytes are zero in every dtype
-        const std::int64_t zero_bytes = 0;
-        device::fill(full.dtype(), full.device_data(), full.numel(), &zero_bytes);
-    }
-    for (const auto& [index, gradient] : taken.parts) {
-        full.select(taken.dim, index).copy_(gradient);
-    }
-}
-
-void write_if_deferred(const Tensor& t) {
-    if (DeferredSelects* selects = active_deferred_selects) {
-        if (DeferredSelect* entry = selects->find(t)) {
-            write_deferred(*selects, entry);
-        }
-    }
-}
-
-// Merges the deferred gradient `incoming` into the deferred gradient `held` when both are selects
-// of the same tensor along the same dim (true: `held` now stands for their sum); otherwise writes
-// whichever of them is deferred, for the ordinary sum (false).
-bool merge_deferred(const Tensor& held, const Tensor& incoming) {
-    DeferredSelects* selects = active_deferred_selects;
-    if (selects == nullptr) {
-        return false;
-    }
-    DeferredSelect* into = selects->find(held);
-    DeferredSelect* from = selects->find(incoming);
-    if (into != nullptr && from != nullptr && into != from && into->dim == from->dim &&
-        held.shape() == incoming.shape() && held.dtype() == incoming.dtype()) {
-        for (auto& [index, gradient] : from->parts) {
-            auto same = std::find_if(into->parts.begin(), into->parts.end(),
-                                     [index = index](const auto& part) { return part.first == index; });
-            if (same != into->parts.end()) {
-                same->second = same->second + gradient;
-            } else {
-                into->parts.emplace_back(index, gradient);
-            }
-        }
-        selects->erase(from);
-        return true;
-    }
-    write_if_deferred(held);
-    write_if_deferred(incoming);
-    return false;
-}
-
-"""
-
-DEFER_SELECT_FUNCTION = """namespace detail {
-
-std::optional<Tensor> defer_select_gradient(const Shape& shape, DType dtype, Device device,
-                                            std::int64_t dim, std::int64_t index, const Tensor& g) {
-    DeferredSelects* selects = active_deferred_selects;
-    if (selects == nullptr || device == Device::CPU) {
-        return std::nullopt;
-    }
-    const auto rank = static_cast<std::int64_t>(shape.size());
-    const std::int64_t wrapped_dim = dim < 0 ? dim + rank : dim;
-    const std::int64_t wrapped_index = index < 0 ? index + shape[wrapped_dim] : index;
-    DeferredSelect entry{empty(shape, dtype, device), wrapped_dim, {}};
-    entry.parts.emplace_back(wrapped_index, g);
-    selects->entries.push_back(std::move(entry));
-    return selects->entries.back().full;
-}
-
-} // namespace detail
-
-"""
-
-DEFER_SELECT_DECLARATION = """namespace detail {
-
-// The full gradient of x.select(dim, index) for the slice gradient g, deferred by the backward
-// pass that is running on this thread (written right before the node that receives it runs);
-// nullopt outside a backward pass or on the CPU.
-std::optional<Tensor> defer_select_gradient(const Shape& shape, DType dtype, Device device,
-                                            std::int64_t dim, std::int64_t index, const Tensor& g);
-
-} // namespace detail
-
-"""
-
-DEFER_SELECT_BRANCH = """                        if (std::optional<Tensor> deferred =
-                                detail::defer_select_gradient(shape, dtype, device, dim, index, g)) {
-                            return *deferred;
-                        }
-"""
-
 INDEX_LINE_HELPER = """// MI355X: indices that are one line broadcast over the other dims (every stride 0 but the
 // indexed dim's: index_select's and index_add_'s expanded 1-D indices) are range-checked on the
 // line itself, min and max in one device call and one sync, and handed to the kernel in place
@@ -960,19 +816,6 @@ EDITS = [
      GENERATE_BRANCH),
     ("src/ops/sequence.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/ops/sequence.cpp", "        return t.to(dtype).clone();\n    }\n", "after", CUMSUM_BRANCH),
-    ("src/autograd/engine.cpp", "#include <cstdlib>\n", "before", "#include <algorithm>\n"),
-    ("src/autograd/engine.cpp", "#include <iostream>\n", "after", "#include <optional>\n"),
-    ("src/autograd/engine.cpp", '#include "kael/autograd/node.h"\n', "after", '#include "kael/device_kernels.h"\n'),
-    ("src/autograd/engine.cpp", "Tensor seed_gradient(const Tensor& root, const std::optional<Tensor>& gradient) {\n",
-     "before", DEFERRED_SELECT_HELPERS),
-    ("src/autograd/engine.cpp", "    if (!inserted) {\n        slot->second = slot->second + gradient;\n", "replace",
-     "    if (!inserted) {\n        if (merge_deferred(slot->second, gradient)) {\n            return;\n        }\n"
-     "        slot->second = slot->second + gradient;\n"),
-    ("src/autograd/engine.cpp", "namespace detail {\n\nstd::atomic<std::ostream*>& trace_output() {\n", "before",
-     DEFER_SELECT_FUNCTION),
-    ("src/autograd/engine.cpp", "    const NoGradGuard guard;\n", "after", "    const DeferredSelectScope deferred_selects;\n"),
-    ("src/autograd/engine.cpp", "            buffers.erase(buffered);\n", "after", "            write_if_deferred(incoming);\n"),
-    ("src/autograd/functions_view.cpp", '#include "kael/ops.h"\n', "after", "\n#include <optional>\n"),
     ("src/ops/indexing.cpp", '#include "kael/kernels.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/ops/indexing.cpp", "namespace kael {\n\nnamespace {\n", "after", INDEX_LINE_HELPER),
     ("src/ops/indexing.cpp",
@@ -988,10 +831,6 @@ EDITS = [
     ("src/nn/loss.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/nn/loss.cpp", "    const auto largest = kael::max(targets).item<std::int64_t>();\n"
      "    const auto smallest = kael::min(targets).item<std::int64_t>();\n", "replace", TARGET_BOUNDS % {"ns": "kael::"}),
-    ("src/autograd/functions_view.cpp", "namespace kael::autograd {\n\n", "after", DEFER_SELECT_DECLARATION),
-    ("src/autograd/functions_view.cpp",
-     "                        Tensor full_gradient = zeros(shape, dtype, device);\n"
-     "                        full_gradient.select(dim, index).copy_(g);\n", "before", DEFER_SELECT_BRANCH),
 ]
 
 

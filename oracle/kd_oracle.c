@@ -18,6 +18,11 @@
  *                            src/ops/sequence.cpp:95-117 cumsum (sequential, in the output dtype)
  *   - optimizer steps        src/optim/optimizer.cpp:60-80 SGD, :93-120 Adam / AdamW (the chain of
  *                            whole-tensor ops, each rounded to the element type)
+ *   - random draws           src/random.cpp:66-84 rand (std::uniform_real_distribution<double> over
+ *                            std::mt19937_64), :106-110 bernoulli; src/nn/functional.cpp:32-39
+ *                            dropout. The engine is the C++ standard's mt19937_64 ([rand.predef])
+ *                            in its sequential textbook form (Matsumoto & Nishimura); the draw is
+ *                            libstdc++'s generate_canonical<double, 53> over a 64-bit engine.
  *
  * Deliberate choices where the reference is undefined: integer division by zero yields 0 and
  * INT64_MIN / -1 yields INT64_MIN (the reference host would trap). Floating ops on integer
@@ -1561,5 +1566,90 @@ int oracle_layout_build(kd_element_layout* out, int operands, const int* ranks,
         for (int op = 0; op < operands; ++op) out->strides[op][d] = mst[op][d];
     }
     for (int op = 0; op < operands; ++op) out->base[op] = bases ? bases[op] : NULL;
+    return KD_OK;
+}
+
+
+/* ---- random draws ----------------------------------------------------------------------------
+ * std::mt19937_64, sequentially: state words x[0..311] and the position of the next word; at
+ * position 312 the whole state is regenerated in place (k = 0..311, each new word from x[k],
+ * x[k+1 mod 312] and x[k+156 mod 312], the later ones already new), then tempered word by word. */
+
+#define MT_N 312
+#define MT_M 156
+
+void oracle_mt19937_64_seed(uint64_t* state, uint64_t seed) {
+    state[0] = seed;
+    for (int i = 1; i < MT_N; ++i)
+        state[i] = 6364136223846793005ULL * (state[i - 1] ^ (state[i - 1] >> 62)) + (uint64_t)i;
+    state[MT_N] = MT_N;
+}
+
+static uint64_t mt_next(uint64_t* state) {
+    if (state[MT_N] >= MT_N) {
+        for (int k = 0; k < MT_N; ++k) {
+            const uint64_t y = (state[k] & 0xFFFFFFFF80000000ULL) | (state[(k + 1) % MT_N] & 0x7FFFFFFFULL);
+            state[k] = state[(k + MT_M) % MT_N] ^ (y >> 1) ^ ((y & 1) ? 0xB5026F5AA96619E9ULL : 0);
+        }
+        state[MT_N] = 0;
+    }
+    uint64_t x = state[state[MT_N]++];
+    x ^= (x >> 29) & 0x5555555555555555ULL;
+    x ^= (x << 17) & 0x71D67FFFEDA60000ULL;
+    x ^= (x << 37) & 0xFFF7EEE000000000ULL;
+    x ^= x >> 43;
+    return x;
+}
+
+int oracle_mt19937_64_draws(uint64_t* state, int64_t count, uint64_t* out) {
+    if (count < 0 || state[MT_N] > MT_N) return fail("oracle_mt19937_64_draws: bad count or state");
+    for (int64_t i = 0; i < count; ++i) out[i] = mt_next(state);
+    return KD_OK;
+}
+
+/* std::uniform_real_distribution<double>(0, 1): generate_canonical<double, 53> takes one 64-bit
+ * word, converts it to double (rounded to nearest) and divides by 2^64; a result of 1 becomes the
+ * largest double below 1. */
+static double uniform01(uint64_t* state) {
+    const double u = (double)mt_next(state) / 18446744073709551616.0;
+    return u >= 1.0 ? nextafter(1.0, 0.0) : u;
+}
+
+int oracle_bernoulli(int dtype, void* out, int64_t count, double probability, uint64_t* state) {
+    if (count < 0 || !(probability >= 0.0 && probability <= 1.0) || state[MT_N] > MT_N)
+        return fail("oracle_bernoulli: bad arguments");
+    for (int64_t i = 0; i < count; ++i) {
+        const int hit = uniform01(state) < probability;
+        switch (dtype) {
+        case KD_F32: ((float*)out)[i] = hit ? 1.0f : 0.0f; break;
+        case KD_F64: ((double*)out)[i] = hit ? 1.0 : 0.0; break;
+        case KD_I64: ((int64_t*)out)[i] = hit; break;
+        case KD_BOOL: ((uint8_t*)out)[i] = (uint8_t)hit; break;
+        default: return fail("oracle_bernoulli: unknown dtype");
+        }
+    }
+    return KD_OK;
+}
+
+/* dropout: input * bernoulli(keep) / keep, the multiply and the divide each rounded to the element
+ * type, keep converted to it (kael's scalar operand). */
+int oracle_dropout(int dtype, void* out, const void* in, int64_t count, double keep, uint64_t* state) {
+    if (count < 0 || !(keep > 0.0 && keep <= 1.0) || state[MT_N] > MT_N) return fail("oracle_dropout: bad arguments");
+    if (dtype == KD_F32) {
+        const float k = (float)keep;
+        for (int64_t i = 0; i < count; ++i) {
+            const float m = uniform01(state) < keep ? 1.0f : 0.0f;
+            const float product = ((const float*)in)[i] * m;
+            ((float*)out)[i] = product / k;
+        }
+    } else if (dtype == KD_F64) {
+        for (int64_t i = 0; i < count; ++i) {
+            const double m = uniform01(state) < keep ? 1.0 : 0.0;
+            const double product = ((const double*)in)[i] * m;
+            ((double*)out)[i] = product / keep;
+        }
+    } else {
+        return fail("oracle_dropout: dtype must be f32 or f64");
+    }
     return KD_OK;
 }

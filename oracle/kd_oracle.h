@@ -34,6 +34,10 @@ int oracle_causal_attention_backward(int dtype, void* dqkv, const void* dout, co
 int oracle_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
                       int64_t output_count);
 int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);
+void oracle_mt19937_64_seed(uint64_t* state, uint64_t seed);
+int oracle_mt19937_64_draws(uint64_t* state, int64_t count, uint64_t* out);
+int oracle_bernoulli(int dtype, void* out, int64_t count, double probability, uint64_t* state);
+int oracle_dropout(int dtype, void* out, const void* in, int64_t count, double keep, uint64_t* state);
 /* exact == 0: the reference device order (MatmulTiles, sequential k in T);
  * exact != 0: f32 inputs accumulated in double (error-analysis reference). */
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,

@@ -767,6 +767,44 @@ int ref_train_gpt_params(int device, int64_t steps, int64_t vocab, int64_t conte
     });
 }
 
+// One forward and backward of the char-GPT that ref_train_gpt_params builds (same seed, ids and
+// targets), no optimizer step: writes the loss and every parameter's gradient, flattened in
+// GPT::parameters() order (ref_gpt_param_total floats), and, when params_out is non-NULL, the
+// initial parameters in the same order.
+int ref_gpt_grads(int device, int64_t vocab, int64_t context, int64_t layers, int64_t heads, int64_t dimension,
+                  int64_t batch, float* loss_out, float* grads_out, float* params_out) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(3);
+        kael::nn::GptConfig config;
+        config.vocab_size = vocab;
+        config.max_positions = context;
+        config.layers = layers;
+        config.heads = heads;
+        config.dimension = dimension;
+        kael::nn::GPT model(config);
+        const kael::Tensor ids = kael::randint(0, vocab, {batch, context}).to(dev);
+        const kael::Tensor targets = kael::randint(0, vocab, {batch * context}).to(dev);
+        model.to(dev);
+        if (params_out != nullptr) {
+            const std::vector<float> flat = flat_parameters(model.parameters());
+            std::memcpy(params_out, flat.data(), flat.size() * sizeof(float));
+        }
+        const kael::Tensor logits = model(ids).reshape({batch * context, vocab});
+        const kael::Tensor loss = kael::nn::cross_entropy(logits, targets);
+        loss.backward();
+        *loss_out = loss.item<float>();
+        std::vector<kael::Tensor> grads;
+        for (const kael::Tensor& p : model.parameters()) {
+            const std::optional<kael::Tensor> g = p.grad();
+            if (!g) throw kael::Error("ref_gpt_grads: a parameter received no gradient");
+            grads.push_back(*g);
+        }
+        const std::vector<float> flat = flat_parameters(grads);
+        std::memcpy(grads_out, flat.data(), flat.size() * sizeof(float));
+    });
+}
+
 // Number of parameters of the GPT that ref_train_gpt_params builds (the size of params_out).
 int64_t ref_gpt_param_total(int64_t vocab, int64_t context, int64_t layers, int64_t heads, int64_t dimension) {
     int64_t total = -1;

@@ -97,6 +97,7 @@ REF_SIGS = {
     "train_gpt_params": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                  c_void_p, POINTER(c_double)]),
     "gpt_param_total": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "gpt_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "row_grad": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "linear_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
     "head_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),

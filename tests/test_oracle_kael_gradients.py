@@ -64,9 +64,9 @@ def test_head_empty_dims_keep_kaels_path(kael_oracle_fused, shape):
 
 @pytest.mark.parametrize("which", range(len(SELECT_CASES)), ids=SELECT_CASES)
 def test_select_gradients_through_the_fused_branches(kael_oracle_fused, which):
-    """Deferred select gradients on the oracle device equal kael's CPU path value for value,
-    including the slices no select reached (zeros), repeated indices (summed), gradients of the
-    whole tensor mixed in, a retained intermediate and anomaly detection (deferral off)."""
+    """Select gradients on the oracle device equal kael's CPU path value for value, including the
+    slices no select reached (zeros), repeated indices (summed), gradients of the whole tensor
+    mixed in, a retained intermediate and anomaly detection."""
     cpu_x, cpu_p = select_grads(kael_oracle_fused, 0, which)
     dev_x, dev_p = select_grads(kael_oracle_fused, 1, which)
     assert np.array_equal(dev_x, cpu_x) and np.array_equal(dev_p, cpu_p)
@@ -80,40 +80,31 @@ def test_select_gradients_reject_unknown_case(kael_oracle_fused):
     assert kael_oracle_fused.ref_select_grads(1, 99, 1, support.ptr(xg), support.ptr(pg)) != 0
 
 
-_TRACE_SELECT = """
-import ctypes, sys
-import numpy as np
-lib = ctypes.CDLL(sys.argv[1])
-xg, pg = np.empty(72, np.float32), np.empty(72, np.float32)
-sys.exit(lib.ref_select_grads(1, int(sys.argv[2]), ctypes.c_uint64(11), xg.ctypes.data_as(ctypes.c_void_p),
-                              pg.ctypes.data_as(ctypes.c_void_p)))
-"""
-
-
-@pytest.mark.parametrize("which, unmodified, fused", [(0, 3, 0), (1, 2, 1), (2, 3, 1)],
-                         ids=["attention_split", "two_of_three", "same_index_twice"])
-def test_select_gradients_skip_the_zero_fills(tmp_path, which, unmodified, fused):
-    """The device calls of one backward pass (the oracle backend's call trace): kael fills a
-    zero tensor of the full shape [2, 3, 3, 4] per select; with the select gradients deferred,
-    only a full tensor that some slice of the selected dim never reaches is filled (once)."""
-    import json
-    import subprocess
-    import sys
-
-    fills = {}
-    for name in ("libkael_oracle.so", "libkael_oracle_fused.so"):
-        trace = tmp_path / f"{name}.jsonl"
-        env = dict(os.environ, KD_ORACLE_TRACE=str(trace))
-        subprocess.run([sys.executable, "-c", _TRACE_SELECT, str(support.REF_DIR / name), str(which)],
-                       env=env, check=True, timeout=120)
-        recs = [json.loads(line) for line in trace.read_text().splitlines() if line.strip()]
-        fills[name] = sum(1 for r in recs if r["op"] == "fill" and r["count"] == 72)
-    assert fills == {"libkael_oracle.so": unmodified, "libkael_oracle_fused.so": fused}
-
-
 def test_select_gradients_with_the_graph_retained_accumulate(kael_oracle_fused):
-    """Backward twice over the same graph (retain_graph): each pass defers and writes its own select
-    gradients, so x.grad is exactly twice one pass's (g + g rounds to 2g)."""
+    """Backward twice over the same graph (retain_graph): each pass writes its own select gradients,
+    so x.grad is exactly twice one pass's (g + g rounds to 2g)."""
     once, _ = select_grads(kael_oracle_fused, 1, SELECT_CASES.index("attention_split"))
     twice, _ = select_grads(kael_oracle_fused, 1, SELECT_CASES.index("retained_graph_twice"))
     assert np.array_equal(twice, 2 * once)
+
+
+SMALL_GPT = (11, 16, 2, 2, 8, 3)  # vocab, context, layers, heads, dimension, batch
+
+
+@pytest.mark.parametrize("variant", ["oracle", "oracle_fused"])
+def test_gpt_gradients_on_the_oracle_device(request, variant):
+    """ref_gpt_grads (the one-backward C4 check's harness) on a small char-GPT with the C oracle as
+    the device, unmodified kael and with its device branches: every parameter gradient against
+    kael's CPU path at the reference's f32 device tolerance, the initial parameters bit for bit."""
+    lib = request.getfixturevalue("kael_" + variant)
+    total = lib.ref_gpt_param_total(*SMALL_GPT[:5])
+    out = {}
+    for device in (0, 1):
+        loss, grads, params = ctypes.c_float(), np.zeros(total, np.float32), np.zeros(total, np.float32)
+        assert lib.ref_gpt_grads(device, *SMALL_GPT, ctypes.byref(loss), support.ptr(grads), support.ptr(params)) == 0, \
+            support.ref_error(lib)
+        out[device] = (loss.value, grads, params)
+    np.testing.assert_array_equal(out[1][2], out[0][2])
+    assert np.count_nonzero(out[0][1]) > total // 2
+    assert_reference_close(out[1][1], out[0][1], "gradients")
+    assert abs(out[1][0] - out[0][0]) <= 1e-5 * abs(out[0][0])
