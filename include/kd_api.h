@@ -230,6 +230,28 @@ int kd_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data,
  * reference: equal within rounding); i64/bool store wrapping int64 (bit-exact). */
 int kd_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);
 
+/* kael's random draws on the device. `state` (host memory, 313 words) is a std::mt19937_64 in the
+ * layout libstdc++ streams it with operator<<: the 312 state words, then the index (0..312) of the
+ * next word to temper. Each call draws exactly `count` values, one per element in order, as
+ * std::uniform_real_distribution<double>(0, 1) draws them from that engine (libstdc++'s
+ * generate_canonical: one 64-bit word per value), writes the result, and returns with `state`
+ * advanced past those draws; the call blocks until both are done. */
+
+/* Writes the state of std::mt19937_64(seed) (kael::manual_seed, reference src/random.cpp:62-65);
+ * host only. */
+void kd_mt19937_64_seed(uint64_t* state, uint64_t seed);
+
+/* reference src/random.cpp:106-110 `bernoulli(shape, probability, dtype)` =
+ * (rand(shape, F64) < probability).to(dtype), without the host tensor and its copy: out[i] = 1
+ * where draw i < probability, else 0, in dtype (f32, f64, i64 or bool). */
+int kd_bernoulli(int dtype, void* out, int64_t count, double probability, uint64_t* state);
+
+/* reference src/nn/functional.cpp:32-39 `dropout(input, p, training)` with keep = 1 - p: out[i] =
+ * (in[i] * m[i]) / T(keep), m as kd_bernoulli(dtype, ..., keep) draws it and each op rounded to
+ * the element type, in one launch; `mask` (may be NULL) receives m, which the backward pass
+ * needs. f32 or f64, contiguous `count` elements; keep in (0, 1]; out may equal in. */
+int kd_dropout(int dtype, void* out, void* mask, const void* in, int64_t count, double keep, uint64_t* state);
+
 /* reference device_kernels.h:111-112 `matmul(DType, const std::byte* a, const std::byte* b,
  * std::byte* out, const MatmulSizes&)`: out[b] = a[b] . b[b] for contiguous row-major
  * batches, overwriting out. f32 on the FP32 matrix cores; f64 and i64 (wrapping) on the

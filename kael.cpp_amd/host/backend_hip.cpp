@@ -245,6 +245,11 @@ void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t s
     check(kd_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
 }
 
+void dropout(DType dtype, std::byte* out, std::byte* mask, const std::byte* in, std::int64_t count, double keep,
+             std::uint64_t* state) {
+    check(kd_dropout(static_cast<int>(dtype), out, mask, in, count, keep, state), "dropout");
+}
+
 void reduce_columns(ReduceOp op, DType out, DType in, std::byte* results, const std::byte* data, std::int64_t outer,
                     std::int64_t inner) {
     check(kd_reduce_columns(static_cast<int>(op), static_cast<int>(out), static_cast<int>(in), results, data, outer,

@@ -2,8 +2,8 @@
 // interface (reference include/kael/device_kernels.h:96-116) for the fused paths: row softmax /
 // log-softmax, row standardization, cross-entropy losses and gradient, GELU backward as one
 // element op, matmul over strided (transposed or batch-broadcast) operands, the Adam / SGD
-// parameter updates as one kernel per tensor (Adam also over a list of tensors), and the reductions kael otherwise computes on the
-// host (prod, all, any, argmax / argmin, cumsum).
+// parameter updates as one kernel per tensor (Adam also over a list of tensors), the reductions kael otherwise computes on the
+// host (prod, all, any, argmax / argmin, cumsum), and dropout with its mask drawn on the device.
 //
 // Defined in backend_hip.cpp. Unmodified kael never calls them; the device branches that do are
 // optional kael patches (a one-line include of this header at the end of kael/device_kernels.h,
@@ -154,6 +154,13 @@ void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* do
 // Running sums along `rows` contiguous rows of `size` elements (reference src/ops/sequence.cpp:95-117):
 // f32 / f64 store In, i64 / bool wrapping int64.
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows);
+
+// Dropout of `count` contiguous f32 / f64 elements with the mask drawn on the device (reference
+// src/nn/functional.cpp:32-39, bernoulli src/random.cpp:106-110): out = in * m / T(keep) and mask = m,
+// m[i] = 1 where the i-th uniform draw of the std::mt19937_64 whose libstdc++ stream form is
+// `state` (312 words, then the position) is below keep; `state` comes back advanced by `count` draws.
+void dropout(DType dtype, std::byte* out, std::byte* mask, const std::byte* in, std::int64_t count, double keep,
+             std::uint64_t* state);
 
 // The GPT decode engine (kd_gpt_*), for the optional branch of nn::generate (reference
 // src/nn/transformer.cpp:256-295) that runs greedy generation with a KV cache on the device.

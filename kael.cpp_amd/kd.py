@@ -116,6 +116,9 @@ SIGNATURES = {
     "reduce_columns": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "arg_reduce": (c_int, [c_int, c_int, c_void_p, c_void_p, c_int64, c_int64]),
     "cumsum": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64]),
+    "mt19937_64_seed": (None, [c_void_p, ctypes.c_uint64]),
+    "bernoulli": (c_int, [c_int, c_void_p, c_int64, c_double, c_void_p]),
+    "dropout": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_double, c_void_p]),
     "gather": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
     "scatter_add": (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(IndexLayout)]),
     "index_bounds": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),

@@ -40,6 +40,11 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      of a contiguous copy checked by two reductions and two reads
   src/ops/nn.cpp, src/nn/loss.cpp    the cross-entropy targets' range check (:97-98, :27-28) in one
                                      call
+  src/random.cpp, src/nn/functional.cpp
+                                     dropout (functional.cpp:32-39) of a contiguous f32 / f64 device
+                                     tensor: the bernoulli mask drawn on the device from kael's
+                                     generator (random.cpp:106-110), output and mask in one launch,
+                                     the generator advanced as the host draws advance it
   src/nn/transformer.cpp             CausalSelfAttention::forward (:103-138) without a cache or
                                      dropout, f32 heads of 64: one device call forward and one node
                                      (two launches) backward (kd_causal_attention);
@@ -725,6 +730,57 @@ GENERATE_BRANCH = """    if (auto out = device_generate(model, prompt, options))
 """
 
 # (relative path, anchor line(s), where, text). where: "before", "after", "replace", "append".
+DROPOUT_HELPER = """// MI355X: dropout of a contiguous f32 / f64 device tensor with its bernoulli mask drawn on the
+// device from this generator: one launch writes the output and the mask, and the generator comes
+// back advanced by exactly numel() draws, as bernoulli's host draws advance it. The backward pass
+// is kael's for input * mask / keep: (g / keep) * mask. nullopt for any other tensor, which keeps
+// kael's ops.
+std::optional<Tensor> device_dropout(const Tensor& input, double keep) {
+    if (input.device() == Device::CPU || !input.is_contiguous() ||
+        (input.dtype() != DType::F32 && input.dtype() != DType::F64)) {
+        return std::nullopt;
+    }
+    Tensor out = empty(input.shape(), input.dtype(), input.device());
+    Tensor mask = empty(input.shape(), input.dtype(), input.device());
+    if (input.numel() > 0) {
+        std::array<std::uint64_t, 313> state{};  // libstdc++'s stream form: 312 words, then the position
+        const auto lock = lock_generator();
+        std::stringstream words;
+        words << global_generator();
+        for (std::uint64_t& word : state) {
+            words >> word;
+        }
+        device::dropout(input.dtype(), out.device_data(), mask.device_data(), input.device_data(), input.numel(),
+                        keep, state.data());
+        std::stringstream advanced;
+        for (const std::uint64_t word : state) {
+            advanced << word << ' ';
+        }
+        advanced >> global_generator();
+    }
+    if (autograd::should_record(out, {&input})) {
+        autograd::set_history(out, "DropoutBackward", {input},
+                              {[mask, keep](const Tensor& g) { return (g / keep) * mask; }});
+    }
+    return out;
+}
+
+"""
+
+DROPOUT_DECLARATION = """
+#include <optional>
+
+namespace kael {
+// MI355X: defined beside the generator in src/random.cpp.
+std::optional<Tensor> device_dropout(const Tensor& input, double keep);
+} // namespace kael
+"""
+
+DROPOUT_BRANCH = """    if (std::optional<Tensor> out = device_dropout(input, keep)) {
+        return *out;
+    }
+"""
+
 EDITS = [
     ("include/kael/device_kernels.h", None, "append", '\n#include "kd_kael_extensions.h"\n'),
     ("src/ops/nn.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
@@ -831,6 +887,13 @@ EDITS = [
     ("src/nn/loss.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/nn/loss.cpp", "    const auto largest = kael::max(targets).item<std::int64_t>();\n"
      "    const auto smallest = kael::min(targets).item<std::int64_t>();\n", "replace", TARGET_BOUNDS % {"ns": "kael::"}),
+    ("src/random.cpp", '#include "kael/ops.h"\n', "after",
+     '#include "kael/device_kernels.h"\n\n#include <array>\n#include <optional>\n#include <sstream>\n\n'
+     '#include "recording.h"\n'),
+    ("src/random.cpp", "Tensor multinomial(const Tensor& weights, std::int64_t samples, bool replacement) {\n", "before",
+     DROPOUT_HELPER),
+    ("src/nn/functional.cpp", '#include "kael/random.h"\n', "after", DROPOUT_DECLARATION),
+    ("src/nn/functional.cpp", "    const double keep = 1.0 - p;\n", "after", DROPOUT_BRANCH),
 ]
 
 

@@ -1633,7 +1633,7 @@ int oracle_bernoulli(int dtype, void* out, int64_t count, double probability, ui
 
 /* dropout: input * bernoulli(keep) / keep, the multiply and the divide each rounded to the element
  * type, keep converted to it (kael's scalar operand). */
-int oracle_dropout(int dtype, void* out, const void* in, int64_t count, double keep, uint64_t* state) {
+int oracle_dropout(int dtype, void* out, void* mask, const void* in, int64_t count, double keep, uint64_t* state) {
     if (count < 0 || !(keep > 0.0 && keep <= 1.0) || state[MT_N] > MT_N) return fail("oracle_dropout: bad arguments");
     if (dtype == KD_F32) {
         const float k = (float)keep;
@@ -1641,12 +1641,14 @@ int oracle_dropout(int dtype, void* out, const void* in, int64_t count, double k
             const float m = uniform01(state) < keep ? 1.0f : 0.0f;
             const float product = ((const float*)in)[i] * m;
             ((float*)out)[i] = product / k;
+            if (mask) ((float*)mask)[i] = m;
         }
     } else if (dtype == KD_F64) {
         for (int64_t i = 0; i < count; ++i) {
             const double m = uniform01(state) < keep ? 1.0 : 0.0;
             const double product = ((const double*)in)[i] * m;
             ((double*)out)[i] = product / keep;
+            if (mask) ((double*)mask)[i] = m;
         }
     } else {
         return fail("oracle_dropout: dtype must be f32 or f64");

@@ -37,7 +37,7 @@ int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t
 void oracle_mt19937_64_seed(uint64_t* state, uint64_t seed);
 int oracle_mt19937_64_draws(uint64_t* state, int64_t count, uint64_t* out);
 int oracle_bernoulli(int dtype, void* out, int64_t count, double probability, uint64_t* state);
-int oracle_dropout(int dtype, void* out, const void* in, int64_t count, double keep, uint64_t* state);
+int oracle_dropout(int dtype, void* out, void* mask, const void* in, int64_t count, double keep, uint64_t* state);
 /* exact == 0: the reference device order (MatmulTiles, sequential k in T);
  * exact != 0: f32 inputs accumulated in double (error-analysis reference). */
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* sizes,

@@ -245,8 +245,8 @@ namespace {
 // 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
 // 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads, 16 layer_norm_rows,
 // 17 layer_norm_rows_backward, 18 matmul_strided_bias, 19 index_bounds, 20 causal_attention,
-// 21 causal_attention_backward.
-constexpr int kExtensions = 22;
+// 21 causal_attention_backward, 22 dropout.
+constexpr int kExtensions = 23;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -498,6 +498,14 @@ void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t s
     KD_TRACE("cumsum", kv("in", static_cast<int>(in)) + "," + kv("out", tp(out)) + "," + kv("data", tp(data)) + "," +
                            kv("size", size) + "," + kv("rows", rows));
     check(oracle_cumsum(static_cast<int>(in), out, data, size, rows), "cumsum_rows");
+}
+
+void dropout(DType dtype, std::byte* out, std::byte* mask, const std::byte* in, std::int64_t count, double keep,
+             std::uint64_t* state) {
+    ++g_extension_calls[22];
+    KD_TRACE("dropout", kv("dtype", static_cast<int>(dtype)) + "," + kv("out", tp(out)) + "," + kv("mask", tp(mask)) +
+                            "," + kv("in", tp(in)) + "," + kv("count", count) + "," + kv("keep", real(keep)));
+    check(oracle_dropout(static_cast<int>(dtype), out, mask, in, count, keep, state), "dropout");
 }
 
 // The C oracle has no GPT decode engine: nn::generate's optional branch sees an unsupported

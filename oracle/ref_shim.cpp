@@ -19,6 +19,8 @@
 #include <limits>
 #include <memory>
 #include <optional>
+#include <random>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -30,6 +32,7 @@
 #include "kael/nn/linear.h"
 #include "kael/nn/loss.h"
 #include "kael/nn/activation.h"
+#include "kael/nn/functional.h"
 #include "kael/nn/sequential.h"
 #include "kael/nn/transformer.h"
 #include "kael/optim/adam.h"
@@ -763,6 +766,55 @@ int ref_train_gpt_params(int device, int64_t steps, int64_t vocab, int64_t conte
         if (params_out != nullptr) {
             const std::vector<float> flat = flat_parameters(model.parameters());
             std::memcpy(params_out, flat.data(), flat.size() * sizeof(float));
+        }
+    });
+}
+
+// std::mt19937_64(seed) after `skip` draws: the next `count` raw draws into `out`, then the
+// engine's libstdc++ stream form (operator<<: 312 state words, then the position) into
+// state_out[313].
+int ref_mt_draws(uint64_t seed, int64_t skip, int64_t count, uint64_t* out, uint64_t* state_out) {
+    return guarded([&] {
+        std::mt19937_64 engine(seed);
+        engine.discard(static_cast<unsigned long long>(skip));
+        for (int64_t i = 0; i < count; ++i) out[i] = engine();
+        std::stringstream words;
+        words << engine;
+        for (int i = 0; i < 313; ++i) words >> state_out[i];
+        if (!words) throw kael::Error("ref_mt_draws: the engine's stream form is not 313 words");
+    });
+}
+
+// kael::bernoulli({count}, p, dtype) on the CPU after manual_seed(seed) and `skip` draws of
+// kael::rand; writes the mask and the next kael::rand F64 value (the generator's continuation).
+int ref_bernoulli(uint64_t seed, int64_t skip, int dtype, int64_t count, double p, void* out, double* next) {
+    return guarded([&] {
+        kael::manual_seed(seed);
+        if (skip > 0) (void)kael::rand({skip}, kael::DType::F64);
+        copy_out(kael::bernoulli({count}, p, to_dtype(dtype)), out);
+        *next = kael::rand({1}, kael::DType::F64).item<double>();
+    });
+}
+
+// kael::nn::functional::dropout(x, p, true) over `count` elements of `in` (dtype code f32 / f64) on
+// `device` (0 CPU, 1 the linked backend) after manual_seed(seed) and `skip` draws of kael::rand;
+// writes the output and the next kael::rand F64 value. With `g` and `grad_out` non-NULL, also the
+// gradient of sum(dropout(x) * g) with respect to x.
+int ref_dropout(int device, uint64_t seed, int64_t skip, int dtype, const void* in, int64_t count, double p,
+                void* out, double* next, const void* g, void* grad_out) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        const kael::DType dt = to_dtype(dtype);
+        kael::manual_seed(seed);
+        if (skip > 0) (void)kael::rand({skip}, kael::DType::F64);
+        kael::Tensor x = host_tensor(in, {count}, dt).to(dev);
+        if (grad_out != nullptr) x.requires_grad_(true);
+        const kael::Tensor y = kael::nn::functional::dropout(x, p, true);
+        copy_out(y.detach().cpu(), out);
+        *next = kael::rand({1}, kael::DType::F64).item<double>();
+        if (grad_out != nullptr) {
+            kael::sum(y * host_tensor(g, {count}, dt).to(dev)).backward();
+            copy_out(x.grad()->cpu(), grad_out);
         }
     });
 }

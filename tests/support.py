@@ -43,6 +43,7 @@ def ref_path(variant: str) -> Path:
 ORACLE_SIGS = dict(kd.SIGNATURES)
 ORACLE_SIGS["matmul"] = (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.MatmulSizes), c_int])
 ORACLE_SIGS["last_error"] = (c_char_p, [])
+ORACLE_SIGS["mt19937_64_draws"] = (c_int, [c_void_p, c_int64, c_void_p])
 
 
 def load_oracle() -> ctypes.CDLL:
@@ -97,6 +98,10 @@ REF_SIGS = {
     "train_gpt_params": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                  c_void_p, POINTER(c_double)]),
     "gpt_param_total": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "mt_draws": (c_int, [ctypes.c_uint64, c_int64, c_int64, c_void_p, c_void_p]),
+    "bernoulli": (c_int, [ctypes.c_uint64, c_int64, c_int, c_int64, c_double, c_void_p, c_void_p]),
+    "dropout": (c_int, [c_int, ctypes.c_uint64, c_int64, c_int, c_void_p, c_int64, c_double, c_void_p, c_void_p,
+                        c_void_p, c_void_p]),
     "gpt_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "row_grad": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "linear_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
