@@ -273,21 +273,10 @@ def bench_copy(backend, steps, warmup, mib=256):
 
 
 def gpt2_weights(seed=4):
-    """Random-init GPT-2 small in kael's layout: N(0, 0.02) weights, residual projections
-    N(0, 0.02/sqrt(2*layers)), LayerNorm gain 1 / bias 0, Linear biases 0
-    (reference src/nn/transformer.cpp:187-207)."""
-    rng = np.random.default_rng(seed)
-    out = []
-    for name, shape in kd.gpt2_parameter_shapes():
-        if name.endswith("ln1.weight") or name.endswith("ln2.weight") or name == "ln_final.weight":
-            a = np.ones(shape, np.float32)
-        elif name.endswith(".bias"):
-            a = np.zeros(shape, np.float32)
-        else:
-            std = 0.02 / np.sqrt(24.0) if (name.endswith("attn.proj.weight") or name.endswith("mlp.fc2.weight")) else 0.02
-            a = rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
-        out.append((name, a))
-    return out
+    """Config C5's model: kael's GPT-2 small after manual_seed(4) (N(0, 0.02) weights, residual
+    projections N(0, 0.02/sqrt(2*layers)), LayerNorm gain 1 / bias 0, Linear biases 0; reference
+    src/nn/transformer.cpp:167-207), drawn on the host by kd_gpt_kael_init as kael draws it."""
+    return kd.kael_gpt_parameters(kd.load(), seed)
 
 
 def bench_gpt2(backend, prompt_len=64, new_tokens=256, repeats=3, eager=False):
@@ -335,8 +324,9 @@ def bench_replay(backend, name, steps):
     replays the step's recorded device calls (tests/golden/<name>_step_calls.jsonl.gz, written by
     tests/golden/make_step_traces.py from kael's own training loop with the optional device
     branches) against the C ABI: the same calls, shapes, strides and order as kael issues them,
-    including the blocking loss read. Parameters upload as zeros in C4 (only token ids and targets
-    are recorded); C3 records every upload, so its replay reproduces kael's losses.
+    including the blocking loss read. C3 records every upload; C4 records its token ids and targets,
+    and its parameters are drawn as kael draws them (kd_gpt_kael_init, seed 3). Both replays
+    reproduce kael's losses.
 
     step_ms: HIP-event time per replayed step (K repetitions of the last traced step, Python issuing
     the calls); kernel_ms: the sum of per-call event times, one pass with events around every call;
@@ -345,12 +335,23 @@ def bench_replay(backend, name, steps):
 
     recs = replay.load(ROOT / "tests" / "golden" / f"{name}_step_calls.jsonl.gz")
     setup, step_recs = replay.split_steps(recs)
-    rp = replay.Replay(backend, recs)
+    uploads = {}
+    if name == "c4":
+        # The trace keeps the token ids and targets (uploads 0 and 1); the 52 parameter uploads that
+        # follow get config C4's model, kael's GPT after manual_seed(3) (kd_gpt_kael_init).
+        params = kd.kael_gpt_parameters(backend, 3, 96, 128, 4, 4, 256)
+        uploads = {2 + i: a for i, (_, a) in enumerate(params)}
+    rp = replay.Replay(backend, recs, uploads)
     rp.run(setup)
     for s in step_recs:
         rp.run(s)  # the traced steps, with their index operands checked
     backend.synchronize()
-    losses = list(rp.losses)
+    # kael's loss of each traced step is the last f32 scalar the step reads back
+    per_step = len(rp.losses) // len(step_recs)
+    losses = [rp.losses[(i + 1) * per_step - 1] for i in range(len(step_recs))]
+    kael_losses = replay.traced_losses(recs)
+    if kael_losses and not np.allclose(losses, kael_losses, rtol=1e-4):
+        raise RuntimeError(f"{name} replay losses {losses} differ from kael's {kael_losses}")
     last = step_recs[-1]
     for _ in range(3):
         rp.run(last, checked=False)
@@ -404,9 +405,9 @@ def bench_replay(backend, name, steps):
                        "frac_peak": flops / (mm_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if mm_ms else None},
             "row_kernels": {"count": len(rows), "ms": row_ms, "gbytes": row_bytes / 1e9,
                             "tb_s": row_bytes / (row_ms * 1e-3) / 1e12 if row_ms else None},
-            "replay_losses": losses, "kael_losses": replay.traced_losses(recs),
+            "replay_losses": losses, "kael_losses": kael_losses,
             "data": "C3: kael's recorded inputs and initial parameters; C4: recorded token ids and targets, "
-                    "parameters zero"}
+                    "kael's seed-3 parameters (kd_gpt_kael_init)"}
 
 
 def cpu_train_baseline(name):

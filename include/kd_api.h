@@ -475,6 +475,13 @@ int kd_gpt_create(void** handle, const kd_gpt_config* config);
  * to 64, 4 * dimension <= 4096, at most 64 heads and 8192 positions); otherwise the status and
  * message kd_gpt_create would give. Allocates nothing. */
 int kd_gpt_supported(const kd_gpt_config* config);
+/* The parameters of kael's GPT as `manual_seed(seed); GPT model(config)` initialises them (reference
+ * src/nn/transformer.cpp:167-207 with src/nn/layers.cpp:17-73 and src/random.cpp:62-88), on the
+ * host, concatenated in GPT::named_parameters() order (the names kd_gpt_load_parameter takes):
+ * *count receives the total; with params non-NULL, `capacity` floats must hold it. Draws through
+ * the standard library's std::mt19937_64 and distributions as kael does, so the values are kael's
+ * on the same standard library. Needs no device. */
+int kd_gpt_kael_init(const kd_gpt_config* config, uint64_t seed, float* params, int64_t capacity, int64_t* count);
 void kd_gpt_destroy(void* handle);
 /* Uploads one parameter by its kael name (GPT::named_parameters(), e.g. "blocks.3.attn.qkv.weight")
  * from host f32 data holding all `count` elements in kael's row-major layout. */

@@ -174,6 +174,7 @@ BACKEND_ONLY = {
     "safetensors_tensor": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int64, POINTER(c_int64),
                                    POINTER(c_int32)]),
     "gpt_supported": (c_int, [POINTER(GptConfig)]),
+    "gpt_kael_init": (c_int, [POINTER(GptConfig), ctypes.c_uint64, c_void_p, c_int64, POINTER(c_int64)]),
     "gpt_prefill": (c_int, [c_void_p, c_void_p, c_int64]),
     "gpt_decode": (c_int, [c_void_p, c_int64, c_void_p]),
     "gpt_forward_logits": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
@@ -354,6 +355,26 @@ def gpt2_parameter_shapes(vocab_size=50257, max_positions=1024, layers=12, dimen
                    (b + "mlp.fc1.bias", (4 * d,)), (b + "mlp.fc2.weight", (d, 4 * d)), (b + "mlp.fc2.bias", (d,))]
     shapes += [("ln_final.weight", (d,)), ("ln_final.bias", (d,))]
     return shapes
+
+
+def kael_gpt_parameters(backend: "Backend", seed: int, vocab_size=50257, max_positions=1024, layers=12, heads=12,
+                        dimension=768) -> list:
+    """kael's GPT parameters after manual_seed(seed) (kd_gpt_kael_init, host only) as (name, f32 array)
+    pairs in GPT::named_parameters() order; the arrays are views of one buffer."""
+    cfg = GptConfig(vocab_size, max_positions, layers, heads, dimension, 1, 0)
+    total = c_int64()
+    backend.check(backend.lib.kd_gpt_kael_init(ctypes.byref(cfg), seed, None, 0, ctypes.byref(total)),
+                  "kd_gpt_kael_init")
+    flat = np.empty(total.value, np.float32)
+    backend.check(backend.lib.kd_gpt_kael_init(ctypes.byref(cfg), seed, flat.ctypes.data_as(c_void_p), flat.size,
+                                               ctypes.byref(total)), "kd_gpt_kael_init")
+    out, at = [], 0
+    for name, shape in gpt2_parameter_shapes(vocab_size, max_positions, layers, dimension):
+        n = int(np.prod(shape))
+        out.append((name, flat[at:at + n].reshape(shape)))
+        at += n
+    assert at == flat.size
+    return out
 
 
 _BACKEND: Backend | None = None

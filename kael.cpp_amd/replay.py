@@ -159,9 +159,14 @@ def index_span(layout: dict, skip_axis: bool) -> int:
 class Replay:
     """The calls of one trace bound to device buffers of their allocations."""
 
-    def __init__(self, backend: kd.Backend, records: list[dict]):
+    def __init__(self, backend: kd.Backend, records: list[dict], uploads: dict | None = None):
+        """`uploads` maps the ordinal of a host-to-device copy among the trace's copies to the bytes it
+        uploads instead of the recorded ones (or zeros): it must have the copy's size and, where the
+        trace recorded the bytes, equal them."""
         self.b = backend
         self.records = records
+        self.uploads = dict(uploads or {})
+        self._h2d = 0
         sizes = {r["id"]: r["bytes"] for r in records if r["op"] == "alloc"}
         self.buffers = {i: backend.empty((max(n, 1),), np.uint8) for i, n in sizes.items()}
         zero = np.zeros(1, np.uint8)
@@ -170,6 +175,8 @@ class Replay:
                           "kd_fill")
         backend.synchronize()
         self.bound = [self._bind(r) for r in records]
+        if self.uploads:
+            raise ReplayError(f"uploads {sorted(self.uploads)} name no host-to-device copy of the trace")
         self.losses: list[float] = []  # f32 scalars the replay read back (kael's loss.item())
 
     # -- pointers --
@@ -207,6 +214,15 @@ class Replay:
             return None, None
         if op == "h2d":
             data = np.frombuffer(bytes.fromhex(r["data"]), np.uint8).copy() if "data" in r else np.zeros(r["bytes"], np.uint8)
+            given = self.uploads.pop(self._h2d, None)
+            self._h2d += 1
+            if given is not None:
+                given = np.ascontiguousarray(given).view(np.uint8).ravel()
+                if given.size != r["bytes"]:
+                    raise ReplayError(f"upload {self._h2d - 1}: {given.size} bytes given for a copy of {r['bytes']}")
+                if "data" in r and not np.array_equal(given, data):
+                    raise ReplayError(f"upload {self._h2d - 1}: the given bytes differ from the recorded ones")
+                data = given.copy()
             t, n = c_void_p(P(r["t"])), r["bytes"]
             return (lambda: chk(lib.kd_copy_h2d(t, data.ctypes.data_as(c_void_p), n), "kd_copy_h2d")), None
         if op == "d2h":

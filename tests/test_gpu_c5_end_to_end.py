@@ -2,9 +2,10 @@
 length, against kael's own CPU path (reference examples/gpt2_generate.cpp:62-95 ->
 nn::generate, src/nn/transformer.cpp:256-295):
 
-  - the benchmark's exact run (bench.py's seed-4 random weights, its seed-4 64-token prompt,
-    256 new tokens): the decode engine's tokens equal kael's CPU generate token for token, and the
-    teacher-forced logits of all 320 positions are within 1e-4 of each row's largest |logit|;
+  - the benchmark's exact run (kael's seed-4 GPT-2 small, which bench.py draws with
+    kd_gpt_kael_init, its seed-4 64-token prompt, 256 new tokens): the decode engine's tokens equal
+    kael's CPU generate token for token, and the teacher-forced logits of all 320 positions are
+    within 1e-4 of each row's largest |logit|;
   - kael's seed-4 GPT-2 small over a 1024-token sequence (every position of the context, the
     cache filled to max_positions): the engine's cached logits against kael's full forward;
   - kael's unmodified nn::generate running on the MI355X through this backend

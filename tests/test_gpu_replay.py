@@ -5,12 +5,13 @@ checked before its kernel runs.
 C3's trace holds every upload (inputs and Kaiming-uniform parameters from manual_seed(2)), so the
 replay recomputes kael's run: both steps' losses within 1e-5 of the losses kael reported when the
 trace was recorded (rtol 1e-5: the products run on the MFMA path here, in kael's order on the C
-oracle). C4's trace holds the token ids and targets only, so its parameters are zero and the first
-step's logits are all 0: its loss must be ln(96); the second (after one Adam step) finite.
-Repeating the last step must keep the losses finite and the buffers in bounds (no index
-re-check)."""
+oracle). C4's trace holds the token ids and targets; its parameters are kael's seed-3 model as
+bench.py draws it (kd_gpt_kael_init), so the replay also recomputes kael's run. Repeating the last
+step must keep the losses finite and the buffers in bounds (no index re-check)."""
 import math
 from pathlib import Path
+
+import kd
 
 import numpy as np
 import pytest
@@ -21,10 +22,15 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
+def c4_uploads(backend):
+    """The 52 parameter uploads of C4's trace (after its ids and targets): kael's seed-3 char-GPT."""
+    return {2 + i: a for i, (_, a) in enumerate(kd.kael_gpt_parameters(backend, 3, 96, 128, 4, 4, 256))}
+
+
 def run_trace(kdb, name, repeats):
     recs = replay.load(GOLDEN / f"{name}_step_calls.jsonl.gz")
     setup, steps = replay.split_steps(recs)
-    rp = replay.Replay(kdb, recs)
+    rp = replay.Replay(kdb, recs, c4_uploads(kdb) if name == "c4" else None)
     rp.run(setup)
     for s in steps:
         rp.run(s)
@@ -41,10 +47,11 @@ def test_c3_replay_reproduces_kael_losses(kdb):
     np.testing.assert_allclose(got, kael, rtol=1e-5)
 
 
-def test_c4_replay_with_zero_parameters(kdb):
+def test_c4_replay_reproduces_kael_losses(kdb):
     rp, kael = run_trace(kdb, "c4", 2)
     assert len(kael) == 2
     per_step = len(rp.losses) // 4
-    first = rp.losses[per_step - 1]
-    assert abs(first - math.log(96)) <= 1e-5 * math.log(96), first
+    got = [rp.losses[per_step - 1], rp.losses[2 * per_step - 1]]
+    np.testing.assert_allclose(got, kael, rtol=1e-5)
+    assert abs(got[0] - math.log(96)) > 0.01  # a real model, not uniform logits
     assert all(math.isfinite(x) for x in rp.losses)

@@ -85,3 +85,23 @@ def test_every_record_binds(name):
     assert "alloc" not in kinds and "mark" not in kinds
     assert len([1 for call, _ in rp.bound if call is not None]) == \
         len([r for r in recs if r["op"] not in ("alloc", "free", "mark", "result")])
+
+
+def test_uploads_replace_the_parameter_copies():
+    """C4's parameter uploads given as kael's seed-3 model bind (their sizes match, and where the
+    trace recorded the bytes, the LayerNorm ones and zero biases, they equal them); a wrong size, a
+    byte that differs from a recorded copy, or an ordinal past the trace's copies is an error."""
+    import kd
+    import numpy as np
+
+    recs = replay.load(GOLDEN / "c4_step_calls.jsonl.gz")
+    params = kd.kael_gpt_parameters(kd.Backend(), 3, 96, 128, 4, 4, 256)
+    uploads = {2 + i: a for i, (_, a) in enumerate(params)}
+    replay.Replay(_StandIn(), recs, uploads)
+    with pytest.raises(replay.ReplayError):
+        replay.Replay(_StandIn(), recs, {2: params[0][1][:-1]})
+    ln = dict(params)["blocks.0.ln1.weight"]
+    with pytest.raises(replay.ReplayError):
+        replay.Replay(_StandIn(), recs, {4: ln * 2})  # recorded as ones
+    with pytest.raises(replay.ReplayError):
+        replay.Replay(_StandIn(), recs, {10**6: np.zeros(4, np.uint8)})
