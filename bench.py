@@ -17,7 +17,7 @@ The CPU baseline is kael's own CPU matmul (oracle/_ref, built from the reference
 threaded over the host cores) on a bounded sample, reported beside the GPU figure.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only matmul|c1|f64|c2|rows|attention|train|c3|c4|gpt2|copy]
+                       [--only matmul|c1|f64|c2|rows|attention|train|c3|c4|gpt2|refdev|copy]
 """
 from __future__ import annotations
 
@@ -270,6 +270,100 @@ def bench_copy(backend, steps, warmup, mib=256):
     fn = backend.lib.kd_convert
     ms, _ = time_steps(backend, lambda i: fn(kd.F32, kd.F32, ctypes.byref(lay)), steps, warmup, MIN_WARMUP_S)
     return {"us": ms * 1e3, "bytes_per_launch": 2 * n * 4, "gbps": 2 * n * 4 / (ms * 1e-3) / 1e9}
+
+
+def synced_call_s(backend, fn, iters):
+    """Median wall seconds of one call followed by kd_synchronize, the way the reference's device
+    benchmarks time an iteration (benchmarks/bench_cuda.cpp:11-21); 3 untimed calls first."""
+    for _ in range(3):
+        fn()
+        backend.synchronize()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        backend.synchronize()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def bench_reference_device(backend, steps, warmup):
+    """The reference's own device benchmarks (benchmarks/bench_cuda.cpp:23-52) at their shapes,
+    f32 uniform [0, 1) inputs, through the C ABI: BM_DeviceAdd (a + b, contiguous) and BM_DeviceSum
+    (the global sum) at 2^20 and 2^24 elements, BM_DeviceMatmul at 512, 1024 and 2048. Each is timed
+    two ways: `kernel_*` from HIP events over K back-to-back calls, and `synced_*` as bench_cuda.cpp
+    times an iteration, one call then kd_synchronize, the median of K wall times (outputs
+    preallocated, as kael's caching allocator hands them out in a steady loop). Units are the
+    reference's: elements/s for add and sum, FLOP/s for matmul. Also kael's dropout of C4's
+    activation size (32 x 128 x 256, p 0.1) with the mask drawn on the device (kd_dropout, which
+    returns the advanced generator state, so every call is synchronous)."""
+    rng = np.random.default_rng(0)
+    iters = max(steps, 20)
+    out = {}
+    for n in (1 << 20, 1 << 24):
+        a = backend.to_device(rng.random(n, dtype=np.float32))
+        b = backend.to_device(rng.random(n, dtype=np.float32))
+        o = backend.empty((n,), np.float32)
+        lay = kd.element_layout((n,), [(4,), (4,), (4,)], [o.ptr, a.ptr, b.ptr])
+        p = kd.params()
+        add = lambda i=0: backend.lib.kd_elementwise(kd.OP["PLUS"], kd.F32, kd.F32, ctypes.byref(lay), p)
+        ms, _ = time_steps(backend, add, iters, warmup, MIN_WARMUP_S)
+        sync_s = synced_call_s(backend, add, iters)
+        out[f"BM_DeviceAdd/{n}"] = {"kernel_us": ms * 1e3, "kernel_items_per_s": n / (ms * 1e-3),
+                                    "kernel_gbps": 12 * n / (ms * 1e-3) / 1e9, "synced_us": sync_s * 1e6,
+                                    "synced_items_per_s": n / sync_s}
+        r = backend.empty((1,), np.float32)
+        total = lambda i=0: backend.lib.kd_reduce(kd.REDUCE_SUM, kd.F32, kd.F32, r.ptr, a.ptr, n, 1)
+        ms, _ = time_steps(backend, total, iters, warmup, MIN_WARMUP_S)
+        sync_s = synced_call_s(backend, total, iters)
+        out[f"BM_DeviceSum/{n}"] = {"kernel_us": ms * 1e3, "kernel_items_per_s": n / (ms * 1e-3),
+                                    "kernel_gbps": 4 * n / (ms * 1e-3) / 1e9, "synced_us": sync_s * 1e6,
+                                    "synced_items_per_s": n / sync_s}
+    for n in (512, 1024, 2048):
+        a = backend.to_device(rng.random((n, n), dtype=np.float32))
+        b = backend.to_device(rng.random((n, n), dtype=np.float32))
+        c = backend.empty((n, n), np.float32)
+        sizes = kd.MatmulSizes(1, n, n, n)
+        mm = lambda i=0: backend.lib.kd_matmul(kd.F32, a.ptr, b.ptr, c.ptr, ctypes.byref(sizes))
+        ms, _ = time_steps(backend, mm, iters, warmup, MIN_WARMUP_S)
+        sync_s = synced_call_s(backend, mm, iters)
+        flop = 2.0 * n ** 3
+        out[f"BM_DeviceMatmul/{n}"] = {"kernel_us": ms * 1e3, "kernel_gflops": flop / (ms * 1e-3) / 1e9,
+                                       "synced_us": sync_s * 1e6, "synced_gflops": flop / sync_s / 1e9}
+    n = 32 * 128 * 256
+    x = backend.to_device(rng.normal(0, 1, n).astype(np.float32))
+    y, m = backend.empty((n,), np.float32), backend.empty((n,), np.float32)
+    state = np.zeros(313, np.uint64)
+    backend.lib.kd_mt19937_64_seed(state.ctypes.data_as(ctypes.c_void_p), 0)
+    drop = lambda i=0: backend.check(backend.lib.kd_dropout(kd.F32, y.ptr, m.ptr, x.ptr, n, 0.9,
+                                                            state.ctypes.data_as(ctypes.c_void_p)), "kd_dropout")
+    sync_s = synced_call_s(backend, drop, iters)
+    out["dropout_c4"] = {"elements": n, "synced_us": sync_s * 1e6, "synced_items_per_s": n / sync_s,
+                         "note": "one launch: mt19937_64 draws, compare, x * mask / keep, mask stored; "
+                                 "the generator state copied in and back"}
+    return out
+
+
+def cpu_reference_device_baseline(iters=5):
+    """The same benchmark bodies on kael's CPU path (reference build, threaded), median of `iters`."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import support
+
+    lib = support.load_ref("ref")
+    threads = int(os.environ.get("KAEL_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    lib.ref_set_threads(threads)
+    out = {}
+    for which, name, sizes in ((0, "BM_DeviceAdd", (1 << 20, 1 << 24)), (1, "BM_DeviceSum", (1 << 20, 1 << 24)),
+                               (2, "BM_DeviceMatmul", (512, 1024, 2048)), (3, "dropout_c4", (32 * 128 * 256,))):
+        for n in sizes:
+            t = ctypes.c_double()
+            if lib.ref_time_device_bench(which, n, iters, ctypes.byref(t)) != 0:
+                raise RuntimeError(support.ref_error(lib))
+            key = name if which == 3 else f"{name}/{n}"
+            out[key] = ({"us": t.value * 1e6, "gflops": 2.0 * n ** 3 / t.value / 1e9} if which == 2
+                        else {"us": t.value * 1e6, "items_per_s": n / t.value})
+    return {"ops": out, "cores": threads, "kind": "reference",
+            "sample": f"kael CPU path, the same benchmark bodies (kael::rand inputs), median of {iters} calls each"}
 
 
 def gpt2_weights(seed=4):
@@ -526,7 +620,7 @@ def main() -> int:
     ap.add_argument("--gpt-tokens", type=int, default=256, help="GPT-2 new tokens per run (shorter profiling runs)")
     ap.add_argument("--gpt-repeats", type=int, default=3, help="GPT-2 timed runs (the best is reported)")
     ap.add_argument("--only", default="", choices=["", "all", "matmul", "c1", "f64", "copy", "c2", "rows", "attention",
-                                                  "train", "c3", "c4", "gpt2"],
+                                                  "train", "c3", "c4", "gpt2", "refdev"],
                     help="run one group only (profiling runs); the JSON line is printed either way")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -565,6 +659,12 @@ def main() -> int:
             extra[args.only]["cpu_baseline"] = guarded_cpu(cpu_train_baseline, args.only)
         print(json.dumps({"metric": f"{args.only} training step (replayed kael device calls)", "extra": extra}))
         return 0
+    if args.only == "refdev":
+        extra["reference_device"] = bench_reference_device(backend, args.steps, args.warmup)
+        if not args.no_cpu:
+            extra["reference_device"]["cpu_baseline"] = guarded_cpu(cpu_reference_device_baseline)
+        print(json.dumps({"metric": "reference device benchmarks", "extra": extra}))
+        return 0
     if args.only == "attention":
         extra["attention"] = bench_attention(backend, max(args.steps, 20), args.warmup)
     if args.only in ("c2", "rows", "train"):
@@ -590,6 +690,7 @@ def main() -> int:
         extra["c3"] = bench_replay(backend, "c3", max(args.steps, 20))
         extra["c4"] = bench_replay(backend, "c4", max(args.steps, 10))
         extra["gpt2_decode"] = bench_gpt2(backend)
+        extra["reference_device"] = bench_reference_device(backend, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu:
         try:
@@ -603,6 +704,8 @@ def main() -> int:
         for name in ("c3", "c4"):
             if name in extra:
                 extra[name]["cpu_baseline"] = guarded_cpu(cpu_train_baseline, name)
+        if "reference_device" in extra:
+            extra["reference_device"]["cpu_baseline"] = guarded_cpu(cpu_reference_device_baseline)
         if "gpt2_decode" in extra:
             try:
                 gcpu = cpu_gpt2_baseline()

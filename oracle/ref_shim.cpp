@@ -306,6 +306,35 @@ int ref_time_matmul(int64_t m, int64_t k, int64_t n, int iters, double* median_s
 
 // Times one of the elementwise/reduction ops of the C2 config on CPU tensors; `which`:
 // 0 a+b, 1 a*b, 2 a.T()+b, 3 sum(a,{1}), 4 max(a). Median seconds per call.
+// The reference's own device benchmark bodies (benchmarks/bench_cuda.cpp:23-52) on kael's CPU path:
+// which 0 = rand({n}) + rand({n}), 1 = sum(rand({n})), 2 = matmul(rand({n,n}), rand({n,n})),
+// 3 = nn::functional::dropout(rand({n}), 0.1, true) (a fresh mask every call); median seconds.
+int ref_time_device_bench(int which, int64_t n, int iters, double* median_seconds) {
+    return guarded([&] {
+        kael::manual_seed(0);
+        const kael::Tensor a = which == 2 ? kael::rand({n, n}) : kael::rand({n});
+        const kael::Tensor b = which == 2 ? kael::rand({n, n}) : kael::rand({n});
+        const auto run = [&] {
+            switch (which) {
+            case 0: return a + b;
+            case 1: return kael::sum(a);
+            case 2: return kael::matmul(a, b);
+            default: return kael::nn::functional::dropout(a, 0.1, true);
+            }
+        };
+        (void)run();
+        std::vector<double> times;
+        for (int i = 0; i < iters; ++i) {
+            const auto t0 = std::chrono::steady_clock::now();
+            const kael::Tensor c = run();
+            const auto t1 = std::chrono::steady_clock::now();
+            times.push_back(std::chrono::duration<double>(t1 - t0).count());
+        }
+        std::sort(times.begin(), times.end());
+        *median_seconds = times[times.size() / 2];
+    });
+}
+
 int ref_time_c2(int which, int64_t rows, int64_t cols, int iters, double* median_seconds) {
     return guarded([&] {
         kael::manual_seed(1);

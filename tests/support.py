@@ -102,6 +102,7 @@ REF_SIGS = {
     "bernoulli": (c_int, [ctypes.c_uint64, c_int64, c_int, c_int64, c_double, c_void_p, c_void_p]),
     "dropout": (c_int, [c_int, ctypes.c_uint64, c_int64, c_int, c_void_p, c_int64, c_double, c_void_p, c_void_p,
                         c_void_p, c_void_p]),
+    "time_device_bench": (c_int, [c_int, c_int64, c_int, POINTER(c_double)]),
     "gpt_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "row_grad": (c_int, [c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "linear_grads": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p]),
