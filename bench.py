@@ -40,10 +40,10 @@ FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense FP32 matrix (AMD spec)
 FP64_MFMA_PEAK_TFLOPS = 78.6    # MI355X dense FP64 matrix (AMD spec)
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
 # HBM bytes one 4096^3 launch of the headline kernel (mfma_f32_trans_kernel<false,false>) moves,
-# from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (199 435 KiB and 65 536 KiB per dispatch), scaled
+# from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (198 999 KiB and 65 536 KiB per dispatch), scaled
 # by the factors a plain 256 MiB copy gives the same counters (x2.0 fetch, x1.0 write). The PMC
 # runs and commands are kept in profiles/.
-MATMUL_4096_TRAFFIC_BYTES = (2 * 199435 + 65536) * 1024
+MATMUL_4096_TRAFFIC_BYTES = (2 * 198999 + 65536) * 1024
 
 
 class Timer:
