@@ -85,28 +85,50 @@ struct AttentionShape {
 // A workgroup is 4 waves on one block of 32 rows: the forward and dq kernels on a query block,
 // wave w taking key blocks w, w + 4, ... up to the diagonal; the dkv kernel on a key block, wave w
 // taking query blocks kb + w, kb + w + 4, ... Each wave stages the blocks whose elements it reads
-// one per lane along a row (the operand of a product over rows) in an LDS tile of its own, with
-// coalesced 16-byte loads (zeros past the last row) and rows padded to 68 floats. At the end the
-// waves' partial results meet in LDS and are combined in wave order: the forward's (max, sum,
-// output) triples as an online-softmax merge, the gradients as sums.
+// one per lane along a row (the operand of a product over rows) in an LDS tile of its own (rows
+// padded to 68 floats), so the waves never wait for each other inside the loop: a wave issues every
+// global load of its first block at once, keeps the next block's loads in flight in registers
+// while it computes the current one, and orders its own LDS writes and reads with wave-level
+// fences only. At the end the waves' partial results meet in LDS behind one workgroup barrier and
+// are combined in wave order: the forward's (max, sum, output) triples as an online-softmax merge,
+// the gradients as sums.
 
 constexpr int kWaves = 4;
 constexpr int kLd = kD + 4;           // padded LDS row
 constexpr int kTile = kBlock * kLd;   // one 32-row tile
+constexpr int kTileVec = kBlock * kD / 4 / 64;  // 16-byte pieces of a tile per lane
 
-// A wave stages rows t0 .. t0 + 31 of a [T, D] head matrix (row stride ld) into `tile`.
-__device__ __forceinline__ void stage_tile(float* __restrict__ tile, const float* __restrict__ base, int t0, int length,
-                                           int64_t ld, int lane) {
+// Orders a wave's LDS accesses across its lanes: a wave's LDS operations execute in issue order,
+// so it only has to keep the compiler from moving them across this point.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Rows t0 .. t0 + 31 of a [T, D] head matrix (row stride ld) into registers, 16 bytes per load,
+// zeros past the last row; tile_store writes them to a wave's LDS tile.
+__device__ __forceinline__ void tile_load(v4f (&reg)[kTileVec], const float* __restrict__ base, int t0, int length,
+                                          int64_t ld, int lane) {
 #pragma unroll
-    for (int q = 0; q < kBlock * kD / 4 / 64; ++q) {
+    for (int q = 0; q < kTileVec; ++q) {
         const int idx = lane + 64 * q;
         const int row = idx / (kD / 4), c4 = idx % (kD / 4);
-        v4f v = {0.f, 0.f, 0.f, 0.f};
-        if (t0 + row < length) v = *reinterpret_cast<const v4f*>(base + static_cast<int64_t>(t0 + row) * ld + 4 * c4);
-        *reinterpret_cast<v4f*>(tile + row * kLd + 4 * c4) = v;
+        reg[q] = v4f{0.f, 0.f, 0.f, 0.f};
+        if (t0 + row < length) reg[q] = *reinterpret_cast<const v4f*>(base + static_cast<int64_t>(t0 + row) * ld + 4 * c4);
     }
 }
 
+__device__ __forceinline__ void tile_store(float* __restrict__ tile, const v4f (&reg)[kTileVec], int lane) {
+#pragma unroll
+    for (int q = 0; q < kTileVec; ++q) {
+        const int idx = lane + 64 * q;
+        const int row = idx / (kD / 4), c4 = idx % (kD / 4);
+        *reinterpret_cast<v4f*>(tile + row * kLd + 4 * c4) = reg[q];
+    }
+}
+
+// Row `row` (features 32 * lh .. 32 * lh + 31) of a wave's LDS tile.
 __device__ __forceinline__ void lds_half_row(float (&reg)[32], const float* __restrict__ tile, int row, int lh) {
     const v4f* src = reinterpret_cast<const v4f*>(tile + row * kLd + 32 * lh);
 #pragma unroll
@@ -146,6 +168,18 @@ __device__ __forceinline__ void store_tile_sum(float* __restrict__ dst, const fl
     *reinterpret_cast<v4f*>(out + 4) = v4f{acc[4], acc[5], acc[6], acc[7]};
 }
 
+// X^T . Y^T over 64 features in two independent MFMA chains (even and odd k-pairs), added at the
+// end: a[t] / b[t] hold features t and 32 + t of the lane's row (half lh).
+__device__ __forceinline__ v16f dot_rows(const float (&a)[32], const float (&b)[32]) {
+    v16f s0 = zero16(), s1 = zero16();
+#pragma unroll
+    for (int t = 0; t < 32; t += 2) {
+        s0 = mfma(a[t], b[t], s0);
+        s1 = mfma(a[t + 1], b[t + 1], s1);
+    }
+    return s0 + s1;
+}
+
 // ---- forward -----------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* __restrict__ out, float* __restrict__ lse,
@@ -163,25 +197,27 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
     float* tile = tiles + wave * kTile;
     const int query = qb * kBlock + li;
 
-    float qreg[32];
+    // every load of the first key block in flight together: the query row, the key row, the V tile
+    float qreg[32], kreg[32];
+    v4f vnext[kTileVec];
     load_half_row(qreg, q, query, sh.length, sh.row, lh);
-
+    if (wave <= qb) {
+        load_half_row(kreg, k, wave * kBlock + li, sh.length, sh.row, lh);
+        tile_load(vnext, v, wave * kBlock, sh.length, sh.row, lane);
+    }
     v16f o[2] = {zero16(), zero16()};
     float m = -INFINITY, l = 0.f;
-    const int rounds = (qb + kWaves) / kWaves;  // ceil((qb + 1) / 4), the same for every wave
-    for (int it = 0; it < rounds; ++it) {
-        const int kb = it * kWaves + wave;
-        const bool mine = kb <= qb;
-        __syncthreads();  // the tile's previous block is consumed
-        if (mine) stage_tile(tile, v, kb * kBlock, sh.length, sh.row, lane);
-        __syncthreads();
-        if (!mine) continue;
+    for (int kb = wave; kb <= qb; kb += kWaves) {
         const int j0 = kb * kBlock;
-        float kreg[32];
-        load_half_row(kreg, k, j0 + li, sh.length, sh.row, lh);
-        v16f s = zero16();
-#pragma unroll
-        for (int t = 0; t < 32; ++t) s = mfma(kreg[t], qreg[t], s);
+        tile_store(tile, vnext, lane);  // V of this block (the previous block's reads are done)
+        wave_sync();
+        const bool more = kb + kWaves <= qb;
+        float knext[32];
+        if (more) {  // the next block's loads run while this block computes
+            load_half_row(knext, k, j0 + kWaves * kBlock + li, sh.length, sh.row, lh);
+            tile_load(vnext, v, j0 + kWaves * kBlock, sh.length, sh.row, lane);
+        }
+        v16f s = dot_rows(kreg, qreg);
         // scale, mask, block max of this query's scores (16 here, 16 in lane li + 32)
         float bmax = -INFINITY;
 #pragma unroll
@@ -216,9 +252,13 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
             o[0] = mfma(vr[0], s[t], o[0]);
             o[1] = mfma(vr[32], s[t], o[1]);
         }
+        wave_sync();
+        if (more) {
+#pragma unroll
+            for (int t = 0; t < 32; ++t) kreg[t] = knext[t];
+        }
     }
     // merge: o[dt][r] = O^T[32 dt + block_row(r, lh)][query li] of this wave's key blocks
-    __syncthreads();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         tile[li * kLd + 32 * 0 + block_row(r, lh)] = o[0][r];
@@ -254,7 +294,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
 
 // ---- backward: delta and dQ ---------------------------------------------------------------
 
-__global__ __launch_bounds__(kWaves * 64) void attention_dq_kernel(float* __restrict__ dqkv, float* __restrict__ delta,
+__global__ __launch_bounds__(kWaves * 64, 2) void attention_dq_kernel(float* __restrict__ dqkv, float* __restrict__ delta,
                                                                    const float* __restrict__ dout,
                                                                    const float* __restrict__ qkv,
                                                                    const float* __restrict__ out,
@@ -275,34 +315,36 @@ __global__ __launch_bounds__(kWaves * 64) void attention_dq_kernel(float* __rest
     const int i0 = qb * kBlock;
     const int query = i0 + li;
 
-    float qreg[32], doreg[32];
+    float qreg[32], doreg[32], oreg[32], vreg[32];
+    v4f kload[kTileVec];
     load_half_row(qreg, q, query, sh.length, sh.row, lh);
     load_half_row(doreg, go, query, sh.length, sh.out_row, lh);
+    load_half_row(oreg, o, query, sh.length, sh.out_row, lh);
+    const float row_lse = query < sh.length ? lse[static_cast<int64_t>(bh) * sh.length + query] : 0.f;
+    if (wave <= qb) {  // the first key block's loads in flight with the query block's
+        tile_load(kload, k, wave * kBlock, sh.length, sh.row, lane);
+        load_half_row(vreg, v, wave * kBlock + li, sh.length, sh.row, lh);
+    }
     float dl;
     {
-        float oreg[32];
-        load_half_row(oreg, o, query, sh.length, sh.out_row, lh);
         float part = 0.f;
 #pragma unroll
         for (int t = 0; t < 32; ++t) part += doreg[t] * oreg[t];
         dl = part + __shfl_xor(part, 32);
     }
-    const float row_lse = query < sh.length ? lse[static_cast<int64_t>(bh) * sh.length + query] : 0.f;
     if (wave == 0 && query < sh.length && lh == 0) delta[static_cast<int64_t>(bh) * sh.length + query] = dl;
 
     v16f dq[2] = {zero16(), zero16()};
-    const int rounds = (qb + kWaves) / kWaves;
-    for (int it = 0; it < rounds; ++it) {
-        const int kb = it * kWaves + wave;
-        const bool mine = kb <= qb;
-        __syncthreads();
-        if (mine) stage_tile(tile, k, kb * kBlock, sh.length, sh.row, lane);
-        __syncthreads();
-        if (!mine) continue;
+    for (int kb = wave; kb <= qb; kb += kWaves) {
         const int j0 = kb * kBlock;
-        float kreg[32], vreg[32];
+        if (kb > wave) {
+            tile_load(kload, k, j0, sh.length, sh.row, lane);
+            load_half_row(vreg, v, j0 + li, sh.length, sh.row, lh);
+        }
+        tile_store(tile, kload, lane);  // K of this block (the previous block's reads are done)
+        wave_sync();
+        float kreg[32];
         lds_half_row(kreg, tile, li, lh);
-        load_half_row(vreg, v, j0 + li, sh.length, sh.row, lh);
         v16f s = zero16(), dp = zero16();
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -324,9 +366,9 @@ __global__ __launch_bounds__(kWaves * 64) void attention_dq_kernel(float* __rest
             dq[0] = mfma(s[t], kr[0], dq[0]);
             dq[1] = mfma(s[t], kr[32], dq[1]);
         }
+        wave_sync();
     }
     // dq[dt][r] = dQ[i0 + block_row(r, lh)][32 dt + li]: the waves' partial sums, added in wave order
-    __syncthreads();
     spill_pair(tile, dq, li, lh);
     __syncthreads();
     store_tile_sum(dqkv + tok0 * sh.row + h * kD, tiles, i0, sh.length, sh.row, wave, lane);
@@ -359,26 +401,28 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
     const int key = j0 + li;
 
     float kreg[32], vreg[32];
+    v4f qload[kTileVec], gload[kTileVec];
+    float lload = 0.f, dload = 0.f;
+    // the key block's rows and every load of the first query block, in flight together
     load_half_row(kreg, k, key, sh.length, sh.row, lh);
     load_half_row(vreg, v, key, sh.length, sh.row, lh);
 
     v16f dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
-    const int rounds = (blocks - kb + kWaves - 1) / kWaves;
-    for (int it = 0; it < rounds; ++it) {
-        const int qb = kb + it * kWaves + wave;
-        const bool mine = qb < blocks;
+    for (int qb = kb + wave; qb < blocks; qb += kWaves) {
         const int i0 = qb * kBlock;
-        __syncthreads();
-        if (mine) {
-            stage_tile(qtile, q, i0, sh.length, sh.row, lane);
-            stage_tile(gtile, go, i0, sh.length, sh.out_row, lane);
-            if (lane < kBlock) {
-                lses[wave][lane] = i0 + lane < sh.length ? row_lse[i0 + lane] : 0.f;
-                deltas[wave][lane] = i0 + lane < sh.length ? row_delta[i0 + lane] : 0.f;
-            }
+        tile_load(qload, q, i0, sh.length, sh.row, lane);
+        tile_load(gload, go, i0, sh.length, sh.out_row, lane);
+        if (lane < kBlock) {
+            lload = i0 + lane < sh.length ? row_lse[i0 + lane] : 0.f;
+            dload = i0 + lane < sh.length ? row_delta[i0 + lane] : 0.f;
         }
-        __syncthreads();
-        if (!mine) continue;
+        tile_store(qtile, qload, lane);  // the previous block's reads are done
+        tile_store(gtile, gload, lane);
+        if (lane < kBlock) {
+            lses[wave][lane] = lload;
+            deltas[wave][lane] = dload;
+        }
+        wave_sync();
         float qreg[32], doreg[32];
         lds_half_row(qreg, qtile, li, lh);
         lds_half_row(doreg, gtile, li, lh);
@@ -408,9 +452,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
             dk[0] = mfma(s[t], qtile[off], dk[0]);
             dk[1] = mfma(s[t], qtile[off + 32], dk[1]);
         }
+        wave_sync();
     }
     // dk / dv[dt][r] = dK / dV[j0 + block_row(r, lh)][32 dt + li]: partial sums added in wave order
-    __syncthreads();
     spill_pair(qtile, dk, li, lh);
     spill_pair(gtile, dv, li, lh);
     __syncthreads();
