@@ -211,8 +211,10 @@ int kd_reduce_columns(int op, int out_dtype, int in_dtype, void* results, const 
  * partials of its split path (few long rows) go to a static 64 KiB device buffer that each GPU
  * holds until the process ends, instead of the backend's growable workspace. A call whose
  * partials would not fit fails with KD_E_INVALID (on 256 CUs they take at most 12 KiB). Every
- * call on one GPU shares that buffer: calls that overlap on one GPU (different streams or host
- * threads at once) race; calls in one stream's order do not. */
+ * call on one GPU shares that buffer. Calls from several host threads are serialised around it
+ * (each call's two launches are enqueued together under a lock), and a call on another stream
+ * than the previous call's first drains that stream, so calls never overlap on the buffer; work
+ * that another library or a graph replay puts on the buffer's stream meanwhile is not covered. */
 int kd_reduce_noalloc(int op, int out_dtype, int in_dtype, void* results, const void* data,
                       int64_t chunk_size, int64_t output_count);
 

@@ -818,6 +818,17 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
+// Who used a device's scratch last. A call holds its device's lock from before its split kernel
+// until its combine kernel is enqueued, so calls from several host threads on one stream enqueue
+// their launch pairs whole, one pair after another; when the stream differs from the previous
+// call's, that stream is drained first, so calls on different streams never overlap either.
+struct ScratchUse {
+    std::mutex mutex;
+    hipStream_t last = nullptr;
+    bool used = false;
+};
+ScratchUse g_scratch_use[kMaxDevices];
+
 // The device address of `scratch` on the current device, looked up once per device (with that
 // device current) and kept.
 int static_scratch(void** out) {
@@ -859,8 +870,19 @@ extern "C" int kd_reduce_noalloc(int op, int out_dtype, int in_dtype, void* resu
     if (output_count > 0 && chunk_size >= 0) {
         if (int rc = ensure_device()) return rc;
         if (int rc = static_scratch(&ptr)) return rc;
+        int dev = 0;
+        KD_HIP(hipGetDevice(&dev));  // static_scratch checked the ordinal
+        ScratchUse& use = g_scratch_use[dev];
+        std::lock_guard<std::mutex> lock(use.mutex);
+        hipStream_t current = stream();
+        if (use.used && use.last != current) KD_HIP(hipStreamSynchronize(use.last));
+        const int rc = reduce_entry("kd_reduce_noalloc", op, in_dtype, results, data, chunk_size, output_count, ptr,
+                                    kStaticScratchBytes);
+        use.last = current;
+        use.used = true;
+        return rc;
     }
-    return reduce_entry("kd_reduce_noalloc", op, in_dtype, results, data, chunk_size, output_count, ptr,
+    return reduce_entry("kd_reduce_noalloc", op, in_dtype, results, data, chunk_size, output_count, nullptr,
                         kStaticScratchBytes);
 }
 

@@ -7,8 +7,11 @@ kept them, and "mark" records at the start of each training step. Replaying it i
 backend calls that kael's host code made, in the same order, without kael itself: bench.py times a
 C3 / C4 training step this way.
 
-Every allocation of the trace gets its own device buffer, zero-filled first; copies whose bytes
-were not recorded upload zeros. The first run of the records checks every call that reads indices
+Before any device work the whole trace is validated on the host: every operand's byte extent, from
+the record's sizes, strides and dtypes, must lie inside its live allocation. Every allocation of
+the trace gets its own device buffer, zero-filled first; copies whose bytes were not recorded
+upload zeros (or bytes the caller supplies). The first run of the records checks every call that
+reads indices
 (gather, scatter_add, cross-entropy targets) against the bytes of what it indexes, reading the
 indices back, so that no replayed kernel can address memory outside its buffers; `run(checked=False)`
 then replays the same records without those reads.
@@ -82,21 +85,142 @@ POINTERS = {
 }
 
 
+ELEMENT_SIZE = {kd.F32: 4, kd.F64: 8, kd.I64: 8, kd.BOOL: 1}
+COMPARE_OPS = {kd.OP[n] for n in ("EQUAL", "NOT_EQUAL", "LESS", "LESS_EQUAL", "GREATER", "GREATER_EQUAL",
+                                  "LOGICAL_AND", "LOGICAL_OR", "LOGICAL_XOR", "IS_ZERO")}
+
+
+def strided_span(shape, strides) -> tuple[int, int]:
+    """(lowest, highest + 1) offset, in the strides' own unit, of the elements a strided view of
+    `shape` addresses from its base; (0, 0) when it has none."""
+    if any(n <= 0 for n in shape):
+        return 0, 0
+    lo = sum(min(0, (n - 1) * st) for n, st in zip(shape, strides))
+    hi = sum(max(0, (n - 1) * st) for n, st in zip(shape, strides))
+    return lo, hi + 1
+
+
+def operand_extents(r: dict) -> dict:
+    """For a kernel record: pointer field -> (lowest, one past the highest) byte offset the call
+    touches from it, derived from the record's sizes, strides and dtypes. Index-addressed data
+    (gather's data, scatter_add's target) is absent: its reach depends on the index values, which
+    the replay reads back and checks before the launch."""
+    op = r["op"]
+    e = ELEMENT_SIZE.get(r.get("dtype", kd.F32), 4)
+
+    def dense(n, es=None):
+        es = e if es is None else es
+        return (0, n * es) if n > 0 else (0, 0)
+
+    def strided(shape, strides, es=None):
+        es = e if es is None else es
+        lo, hi = strided_span(shape, strides)
+        return (lo * es, (hi - 1) * es + es) if hi > 0 else (0, 0)
+
+    if op == "fill":
+        return {"t": dense(r["count"])}
+    if op in ("convert", "elementwise"):
+        lay = r["layout"]
+        out_es = 1 if op == "elementwise" and r["eop"] in COMPARE_OPS else ELEMENT_SIZE[r["out"]]
+        ext = {}
+        for o in range(lay["operands"]):
+            es = out_es if o == 0 else ELEMENT_SIZE[r["in"]]
+            lo, hi = strided_span(lay["shape"][:lay["dims"]], lay["strides"][o][:lay["dims"]])
+            ext[f"base{o}"] = (lo, hi - 1 + es) if hi > 0 and lay["count"] > 0 else (0, 0)
+        return ext
+    if op == "reduce":
+        out_es = 8 if r["in"] in (kd.I64, kd.BOOL) and r["rop"] == kd.REDUCE_SUM else ELEMENT_SIZE[r["in"]]
+        return {"data": dense(r["chunk"] * r["rows"], ELEMENT_SIZE[r["in"]]), "results": dense(r["rows"], out_es)}
+    if op == "reduce_columns":
+        out_es = 8 if r["in"] in (kd.I64, kd.BOOL) and r["rop"] == kd.REDUCE_SUM else ELEMENT_SIZE[r["in"]]
+        return {"data": dense(r["outer"] * r["inner"], ELEMENT_SIZE[r["in"]]), "results": dense(r["inner"], out_es)}
+    if op == "arg_reduce":
+        return {"data": dense(r["chunk"] * r["rows"], ELEMENT_SIZE[r["in"]]), "results": dense(r["rows"], 8)}
+    if op == "cumsum":
+        n = r["size"] * r["rows"]
+        return {"data": dense(n, ELEMENT_SIZE[r["in"]]), "out": dense(n, 8 if r["in"] in (kd.I64, kd.BOOL) else
+                                                                      ELEMENT_SIZE[r["in"]])}
+    if op == "matmul":
+        bt, m, k, n = r["sizes"]
+        return {"a": dense(bt * m * k), "b": dense(bt * k * n), "c": dense(bt * m * n)}
+    if op in ("matmul_strided", "matmul_strided_bias", "matmul_strided_heads"):
+        bt, m, k, n = r["sizes"]
+        if op == "matmul_strided_heads":
+            heads, ha, hb, hc = r["heads"]
+            outer = bt // heads if heads > 0 else 0
+            a = strided([outer, heads, m, k], [r["sa"][0], ha, r["sa"][1], r["sa"][2]])
+            b = strided([outer, heads, k, n], [r["sb"][0], hb, r["sb"][1], r["sb"][2]])
+            c = strided([outer, heads, m, n], [r["sc"][0], hc, r["sc"][1], r["sc"][2]])
+        else:
+            a = strided([bt, m, k], r["sa"])
+            b = strided([bt, k, n], r["sb"])
+            c = strided([bt, m, n], r["sc"])
+        ext = {"a": a, "b": b, "c": c}
+        if op == "matmul_strided_bias" and r.get("bias") is not None:
+            ext["bias"] = dense(n)
+        return ext
+    if op == "gather":
+        lay = r["layout"]
+        return {"out": dense(lay["count"]),
+                "indices": strided(lay["shape"][:lay["dims"]], lay["index_strides"][:lay["dims"]], 8)}
+    if op == "scatter_add":
+        lay = r["layout"]
+        return {"source": strided(lay["shape"][:lay["dims"]], lay["source_strides"][:lay["dims"]]),
+                "indices": strided(lay["shape"][:lay["dims"]], lay["index_strides"][:lay["dims"]], 8)}
+    if op == "index_bounds":
+        return {"indices": strided([r["count"]], [r["stride"]], 8)}
+    if op in ("causal_attention", "causal_attention_backward"):
+        bt, t, h, d = r["batch"], r["length"], r["heads"], r["head_dim"]
+        qkv, rows, lse = dense(bt * t * 3 * h * d), dense(bt * t * h * d), dense(bt * h * t)
+        if op == "causal_attention":
+            return {"out": rows, "lse": lse, "qkv": qkv}
+        return {"dqkv": qkv, "dout": rows, "qkv": qkv, "out": rows, "lse": lse}
+    rc = r.get("rows", 0) * r.get("cols", 0)
+    if op in ("softmax_rows", "standardize_rows"):
+        return {"out": dense(rc), "x": dense(rc)}
+    if op == "cross_entropy_rows":
+        return {"losses": dense(r["rows"]), "logits": dense(rc), "targets": dense(r["rows"], 8)}
+    if op == "cross_entropy_grad":
+        ext = {"out": dense(rc), "logits": dense(rc), "targets": dense(r["rows"], 8)}
+        if r.get("weights") is not None:
+            ext["weights"] = dense(r["rows"])
+        return ext
+    if op == "softmax_rows_backward":
+        return {"out": dense(rc), "y": dense(rc), "grad": dense(rc)}
+    if op == "standardize_rows_backward":
+        return {"out": dense(rc), "x": dense(rc), "y": dense(rc), "grad": dense(rc)}
+    if op == "layer_norm_rows":
+        return {"out": dense(rc), "y": dense(rc), "x": dense(rc), "w": dense(r["cols"]), "b": dense(r["cols"])}
+    if op == "layer_norm_rows_backward":
+        ext = {"gx": dense(rc), "x": dense(rc), "y": dense(rc), "grad": dense(rc), "w": dense(r["cols"])}
+        for key in ("gw", "gb"):
+            if r.get(key) is not None:
+                ext[key] = dense(r["cols"])
+        return ext
+    if op == "adam_step":
+        return {key: dense(r["count"]) for key in ("p", "g", "m", "v")}
+    if op == "sgd_step":
+        return {key: dense(r["count"]) for key in ("p", "g")}
+    return {}
+
+
 def validate(records: list[dict]) -> None:
     """Checks a trace without a device: known record kinds, every device pointer inside an
-    allocation that is live at that record (allocated before, not yet freed), copies inside their
-    allocations."""
+    allocation that is live at that record (allocated before, not yet freed), and every byte each
+    call reads or writes through it (its extent from the record's sizes, strides and dtypes; copies
+    by their byte counts) inside that allocation. Index-addressed data is checked by the replay
+    against the index values before its launch."""
     size: dict[int, int] = {}
     live: set[int] = set()
 
-    def check(p, what, need=0):
+    def check(p, what, need=0, low=0):
         if p is None:
             return
         i, off = p
         if i not in live:
             raise ReplayError(f"{what}: allocation {i} is not live")
-        if off < 0 or off + need > size[i]:
-            raise ReplayError(f"{what}: [{off}, {off + need}) outside allocation {i} ({size[i]} bytes)")
+        if off + low < 0 or off + need > size[i]:
+            raise ReplayError(f"{what}: [{off + low}, {off + need}) outside allocation {i} ({size[i]} bytes)")
 
     for n, r in enumerate(records):
         op = r["op"]
@@ -110,14 +234,16 @@ def validate(records: list[dict]) -> None:
         elif op not in POINTERS:
             raise ReplayError(f"record {n}: unknown kind {op!r}")
         else:
+            ext = operand_extents(r)
             for key in POINTERS[op]:
-                need = r["bytes"] if op in ("h2d", "d2h", "d2d") else 0
-                if key == "weights" and r.get(key) is None:
+                if r.get(key) is None and key in ("weights", "bias", "gw", "gb"):
                     continue
-                check(r[key], f"record {n} {op}.{key}", need)
+                low, need = (0, r["bytes"]) if op in ("h2d", "d2h", "d2d") else ext.get(key, (0, 0))
+                check(r[key], f"record {n} {op}.{key}", need, low)
             if op in ("convert", "elementwise"):
                 for o, p in enumerate(r["layout"]["base"]):
-                    check(p, f"record {n} {op}.base[{o}]")
+                    low, need = ext.get(f"base{o}", (0, 0))
+                    check(p, f"record {n} {op}.base[{o}]", need, low)
             if op == "adam_step_many":
                 esize = 4 if r["dtype"] == kd.F32 else 8
                 for t, x in enumerate(r["tensors"]):
@@ -163,6 +289,7 @@ class Replay:
         """`uploads` maps the ordinal of a host-to-device copy among the trace's copies to the bytes it
         uploads instead of the recorded ones (or zeros): it must have the copy's size and, where the
         trace recorded the bytes, equal them."""
+        validate(records)  # every operand's extent inside its allocation, before any launch
         self.b = backend
         self.records = records
         self.uploads = dict(uploads or {})

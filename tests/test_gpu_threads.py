@@ -8,7 +8,8 @@ on demand; these tests drive those paths from four threads at once, with workspa
 grow while the threads run, and require every result to equal, bit for bit, the same call made
 alone afterwards (each of these kernels reduces in a fixed order). The fourth thread also takes
 the index range checks' pinned host slots (one per call in flight) and the attention backward's
-workspace.
+workspace; two more threads run kd_reduce_noalloc at once, whose split path shares one static
+buffer per device.
 
 The check runs in a child process so that the workspace starts empty and its growths happen
 during the concurrent phase, whatever earlier tests allocated.
@@ -110,6 +111,21 @@ def _bounds_and_attention_jobs(backend, rng):
     return jobs
 
 
+def _noalloc_jobs(backend, rng, shapes):
+    """kd_reduce_noalloc on its split path (few long rows): the segment partials in the one static
+    buffer per device that every call shares; two threads run these at once."""
+    jobs = []
+    for rows, chunk in shapes:
+        x = backend.to_device(rng.uniform(-1, 1, (rows, chunk)).astype(np.float32))
+
+        def run(x=x, rows=rows, chunk=chunk):
+            out = backend.empty((rows,), np.float32)
+            backend.call("reduce_noalloc", kd.REDUCE_SUM, kd.F32, kd.F32, out.ptr, x.ptr, chunk, rows)
+            return out.numpy()
+        jobs.append((f"reduce_noalloc {rows}x{chunk}", run))
+    return jobs
+
+
 def child() -> int:
     backend = kd.load()
     if not backend.lib.kd_available():
@@ -117,7 +133,8 @@ def child() -> int:
         return 2
     rng = np.random.default_rng(11)
     groups = [_reduce_jobs(backend, rng), _matmul_jobs(backend, rng), _skinny_jobs(backend, rng),
-              _bounds_and_attention_jobs(backend, rng)]
+              _bounds_and_attention_jobs(backend, rng), _noalloc_jobs(backend, rng, ((3, 1 << 20), (1, 1 << 22))),
+              _noalloc_jobs(backend, rng, ((2, 3 << 19), (4, 1 << 19)))]
     results = [[] for _ in groups]
     errors = []
 

@@ -47,6 +47,41 @@ def test_validate_rejects_pointer_outside_allocation():
         replay.validate(recs)
 
 
+@pytest.mark.parametrize("kind", ["matmul_strided", "layer_norm_rows", "elementwise", "causal_attention",
+                                  "adam_step_many", "scatter_add"])
+def test_validate_rejects_overrunning_extents(kind):
+    """A record whose sizes or strides reach past an allocation is refused on the CPU before any
+    launch, for each kind of extent: strided products, row kernels, element layouts, attention,
+    the Adam table, index operands. The unmodified C4 record of that kind passes."""
+    import copy
+    import gzip
+    import json
+
+    recs = [json.loads(line) for line in gzip.open(GOLDEN / "c4_step_calls.jsonl.gz", "rt")]
+    at = next(i for i, r in enumerate(recs) if r["op"] == kind)
+    replay.validate(recs[:at + 1])
+    bad = copy.deepcopy(recs[:at + 1])
+    r = bad[at]
+    # twice the size along one dim: past the allocation (the caching allocator's blocks round up to
+    # powers of two, so one more row may still fit)
+    if kind == "matmul_strided":
+        r["sizes"][1] *= 2  # output rows
+    elif kind == "layer_norm_rows":
+        r["rows"] *= 2
+    elif kind == "elementwise":
+        r["layout"]["count"] *= 2
+        r["layout"]["shape"][0] *= 2
+    elif kind == "causal_attention":
+        r["length"] *= 2
+    elif kind == "adam_step_many":
+        r["tensors"][0]["count"] *= 2
+    else:
+        r["layout"]["count"] *= 2
+        r["layout"]["shape"][0] *= 2
+    with pytest.raises(replay.ReplayError):
+        replay.validate(bad)
+
+
 class _HostBuffer:
     def __init__(self, n):
         self.data = bytearray(n)
