@@ -208,3 +208,46 @@ def test_gpt2_names_follow_the_reference_translation(tmp_path):
     out = subprocess.run([str(exe), *cases], check=True, capture_output=True, text=True).stdout.split("\n")
     for (stored, (name, transposed)), line in zip(cases.items(), out):
         assert line == f"{name} {transposed}", stored
+
+
+def test_reader_survives_mutated_files(tmp_path, lib):
+    """Seeded mutations of a valid file (bytes of the header and its length field overwritten,
+    bytes inserted or removed, the file truncated): every call returns a status (OK only when the
+    tensor then reads back at its full size). Run against a library whose host code is built with
+    AddressSanitizer and UndefinedBehaviorSanitizer, a stray access here fails the run."""
+    from safetensors.numpy import save_file
+
+    good = tmp_path / "good.safetensors"
+    save_file({"x": np.arange(24, dtype=np.float32).reshape(4, 6), "y": np.ones(3, np.float64)}, str(good))
+    base = bytearray(good.read_bytes())
+    header_end = 8 + struct.unpack("<Q", bytes(base[:8]))[0]
+    rng = np.random.default_rng(12)
+    path = tmp_path / "m.safetensors"
+    for trial in range(300):
+        data = bytearray(base)
+        kind = trial % 4
+        if kind == 0:  # overwrite header bytes
+            for _ in range(int(rng.integers(1, 6))):
+                data[int(rng.integers(0, header_end))] = int(rng.integers(0, 256))
+        elif kind == 1:  # insert bytes into the header
+            at = int(rng.integers(8, header_end))
+            data[at:at] = bytes(rng.integers(0, 256, int(rng.integers(1, 5))).astype(np.uint8))
+        elif kind == 2:  # remove bytes
+            at = int(rng.integers(0, len(data) - 1))
+            del data[at:at + int(rng.integers(1, 9))]
+        else:  # truncate
+            data = data[:int(rng.integers(0, len(data)))]
+        path.write_bytes(bytes(data))
+        for name in ("x", "y"):
+            rc = status(lib, path, name)
+            assert rc in (0, -1, -4), (trial, name, rc)
+            if rc == 0:
+                shape = (kd.c_int64 * 8)()
+                dims = kd.c_int32()
+                assert lib.lib.kd_safetensors_tensor(str(path).encode(), name.encode(), None, 0, shape,
+                                                     kd.ctypes.byref(dims)) == 0
+                count = int(np.prod([shape[i] for i in range(dims.value)])) if dims.value else 1
+                out = np.empty(max(count, 1), np.float32)
+                assert lib.lib.kd_safetensors_tensor(str(path).encode(), name.encode(),
+                                                     out.ctypes.data_as(kd.c_void_p), out.size, None,
+                                                     kd.ctypes.byref(dims)) == 0

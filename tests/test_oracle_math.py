@@ -179,7 +179,8 @@ def test_matmul_two_level_batches_against_numpy_views(oracle):
     st.b[:] = [T * 3 * C, 1, 3 * C]
     st.out[:] = [H * T * T, T, 1]
     heads = kd.MatmulHeads(H, D, D, T * T)
-    flat = qkv.ravel()
+    # zero padding after the store keeps the mistaken-stride call below inside its buffer
+    flat = np.concatenate([qkv.ravel(), np.zeros(2 * T * 3 * C, np.int64)])
     out = np.zeros(B * H * T * T, np.int64)
     assert oracle.oracle_matmul_strided_heads(kd.I64, P(flat), P(flat[C:].copy()), P(out), kd.MatmulSizes(B * H, T, D, T),
                                               st, heads) == 0
