@@ -49,26 +49,6 @@ __device__ __forceinline__ v16f zero16() {
     return z;
 }
 
-// Row `t` (features 32 * lh .. 32 * lh + 31) of a [T, D] head matrix with row stride `ld`, or
-// zeros past the last row: the lane-per-row operand of a product that sums over features.
-__device__ __forceinline__ void load_half_row(float (&reg)[32], const float* __restrict__ base, int t, int length,
-                                              int64_t ld, int lh) {
-    if (t < length) {
-        const v4f* src = reinterpret_cast<const v4f*>(base + t * ld + 32 * lh);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const v4f v = src[q];
-            reg[4 * q] = v[0];
-            reg[4 * q + 1] = v[1];
-            reg[4 * q + 2] = v[2];
-            reg[4 * q + 3] = v[3];
-        }
-    } else {
-#pragma unroll
-        for (int s = 0; s < 32; ++s) reg[s] = 0.f;
-    }
-}
-
 // Row of block position 8 (s / 4) + 4 lh + s % 4: the k index of MFMA step s in the products
 // whose k runs over a block of 32 (the score registers' layout).
 __device__ __forceinline__ int block_row(int s, int lh) { return 8 * (s / 4) + 4 * lh + (s % 4); }
@@ -84,14 +64,20 @@ struct AttentionShape {
 //
 // A workgroup is 4 waves on one block of 32 rows: the forward and dq kernels on a query block,
 // wave w taking key blocks w, w + 4, ... up to the diagonal; the dkv kernel on a key block, wave w
-// taking query blocks kb + w, kb + w + 4, ... Each wave stages the blocks whose elements it reads
-// one per lane along a row (the operand of a product over rows) in an LDS tile of its own (rows
-// padded to 68 floats), so the waves never wait for each other inside the loop: a wave issues every
-// global load of its first block at once, keeps the next block's loads in flight in registers
-// while it computes the current one, and orders its own LDS writes and reads with wave-level
-// fences only. At the end the waves' partial results meet in LDS behind one workgroup barrier and
-// are combined in wave order: the forward's (max, sum, output) triples as an online-softmax merge,
-// the gradients as sums.
+// taking query blocks kb + w, kb + w + 4, ... Workgroups run longest first (the last query blocks,
+// the first key blocks), with all (batch, head) pairs interleaved so that every XCD gets its share of
+// each length.
+//
+// Every global load reads whole rows, 16 bytes per lane and four 256-byte rows per instruction:
+// a lane-per-row operand loaded directly would touch 64 cache lines per instruction, and those
+// loads made up the largest part of a wave's time. The block all four waves share (the query rows,
+// or the dkv kernel's key rows) is loaded a quarter per wave into a shared LDS tile behind one
+// workgroup barrier; the blocks a wave walks pass through an LDS tile of its own (rows padded to 68
+// floats), so the waves never wait for each other inside the loop: a wave issues every global load
+// of its first block at once, keeps the next block's loads in flight in registers while it computes
+// the current one, and orders its own LDS writes and reads with wave-level fences only. At the end
+// the waves' partial results meet in LDS behind one workgroup barrier and are combined in wave
+// order: the forward's (max, sum, output) triples as an online-softmax merge, the gradients as sums.
 
 constexpr int kWaves = 4;
 constexpr int kLd = kD + 4;           // padded LDS row
@@ -106,6 +92,13 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Floats 4 c4 .. 4 c4 + 3 of row `row` of a [T, D] head matrix (row stride ld), zeros for a row past
+// the last: the load reads the last row instead, so no load needs a branch.
+__device__ __forceinline__ v4f row_piece(const float* __restrict__ base, int row, int length, int64_t ld, int c4) {
+    const v4f x = *reinterpret_cast<const v4f*>(base + static_cast<int64_t>(min(row, length - 1)) * ld + 4 * c4);
+    return row < length ? x : v4f{0.f, 0.f, 0.f, 0.f};
+}
+
 // Rows t0 .. t0 + 31 of a [T, D] head matrix (row stride ld) into registers, 16 bytes per load,
 // zeros past the last row; tile_store writes them to a wave's LDS tile.
 __device__ __forceinline__ void tile_load(v4f (&reg)[kTileVec], const float* __restrict__ base, int t0, int length,
@@ -114,8 +107,7 @@ __device__ __forceinline__ void tile_load(v4f (&reg)[kTileVec], const float* __r
     for (int q = 0; q < kTileVec; ++q) {
         const int idx = lane + 64 * q;
         const int row = idx / (kD / 4), c4 = idx % (kD / 4);
-        reg[q] = v4f{0.f, 0.f, 0.f, 0.f};
-        if (t0 + row < length) reg[q] = *reinterpret_cast<const v4f*>(base + static_cast<int64_t>(t0 + row) * ld + 4 * c4);
+        reg[q] = row_piece(base, t0 + row, length, ld, c4);
     }
 }
 
@@ -168,6 +160,49 @@ __device__ __forceinline__ void store_tile_sum(float* __restrict__ dst, const fl
     *reinterpret_cast<v4f*>(out + 4) = v4f{acc[4], acc[5], acc[6], acc[7]};
 }
 
+// A wave's quarter (rows 8 wave .. 8 wave + 7) of rows t0 .. t0 + 31 of a [T, D] head matrix, 16
+// bytes per load and 4 whole rows per instruction, zeros past the last row: the four waves load a
+// block that all of them read together, and part_store puts it in a workgroup-shared tile.
+constexpr int kPartVec = kTileVec / kWaves;
+
+__device__ __forceinline__ void part_load(v4f (&reg)[kPartVec], const float* __restrict__ base, int t0, int length,
+                                          int64_t ld, int wave, int lane) {
+#pragma unroll
+    for (int q = 0; q < kPartVec; ++q) {
+        const int row = 8 * wave + 4 * q + lane / (kD / 4), c4 = lane % (kD / 4);
+        reg[q] = row_piece(base, t0 + row, length, ld, c4);
+    }
+}
+
+__device__ __forceinline__ void part_store(float* __restrict__ tile, const v4f (&reg)[kPartVec], int wave, int lane) {
+#pragma unroll
+    for (int q = 0; q < kPartVec; ++q) {
+        const int row = 8 * wave + 4 * q + lane / (kD / 4), c4 = lane % (kD / 4);
+        *reinterpret_cast<v4f*>(tile + row * kLd + 4 * c4) = reg[q];
+    }
+}
+
+// x of this lane and of lane ^ 32, in some order: v_permlane32_swap exchanges lanes 0-31 of one copy
+// with lanes 32-63 of the other, so every lane holds its own value in one result and its partner's in
+// the other. Their max or sum is the same in both halves (either order gives the same float).
+__device__ __forceinline__ void both_halves(float x, float& a, float& b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+
+__device__ __forceinline__ float halves_max(float x) {
+    float a, b;
+    both_halves(x, a, b);
+    return fmaxf(a, b);
+}
+
+__device__ __forceinline__ float halves_sum(float x) {
+    float a, b;
+    both_halves(x, a, b);
+    return a + b;
+}
+
 // X^T . Y^T over 64 features in two independent MFMA chains (even and odd k-pairs), added at the
 // end: a[t] / b[t] hold features t and 32 + t of the lane's row (half lh).
 __device__ __forceinline__ v16f dot_rows(const float (&a)[32], const float (&b)[32]) {
@@ -182,13 +217,16 @@ __device__ __forceinline__ v16f dot_rows(const float (&a)[32], const float (&b)[
 
 // ---- forward -----------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* __restrict__ out, float* __restrict__ lse,
-                                                                        const float* __restrict__ qkv, AttentionShape sh) {
-    __shared__ float tiles[kWaves * kTile];
+__global__ __launch_bounds__(kWaves * 64, 2) void attention_forward_kernel(float* __restrict__ out, float* __restrict__ lse,
+                                                                           const float* __restrict__ qkv,
+                                                                           AttentionShape sh) {
+    __shared__ float tiles[kWaves * kTile];  // each wave's K, then V, tile of its current key block
+    __shared__ float qtile[kTile];           // the query block
     __shared__ float ms[kWaves][kBlock], ls[kWaves][kBlock];
     const int blocks = (sh.length + kBlock - 1) / kBlock;
-    const int bh = blockIdx.x / blocks;
-    const int qb = blocks - 1 - static_cast<int>(blockIdx.x % blocks);  // longest rows first
+    const int units = sh.batch * sh.heads;
+    const int bh = static_cast<int>(blockIdx.x % units);
+    const int qb = blocks - 1 - static_cast<int>(blockIdx.x / units);  // longest rows first, all heads interleaved
     const int b = bh / sh.heads, h = bh % sh.heads;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const float* q = qkv + static_cast<int64_t>(b) * sh.length * sh.row + h * kD;
@@ -197,25 +235,32 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
     float* tile = tiles + wave * kTile;
     const int query = qb * kBlock + li;
 
-    // every load of the first key block in flight together: the query row, the key row, the V tile
-    float qreg[32], kreg[32];
-    v4f vnext[kTileVec];
-    load_half_row(qreg, q, query, sh.length, sh.row, lh);
+    // every load in flight together: the wave's quarter of the query block, its first K and V tiles
+    v4f qpart[kPartVec], kload[kTileVec], vload[kTileVec];
+    part_load(qpart, q, qb * kBlock, sh.length, sh.row, wave, lane);
     if (wave <= qb) {
-        load_half_row(kreg, k, wave * kBlock + li, sh.length, sh.row, lh);
-        tile_load(vnext, v, wave * kBlock, sh.length, sh.row, lane);
+        tile_load(kload, k, wave * kBlock, sh.length, sh.row, lane);
+        tile_load(vload, v, wave * kBlock, sh.length, sh.row, lane);
     }
+    part_store(qtile, qpart, wave, lane);
+    __syncthreads();
+    float qreg[32];
+    lds_half_row(qreg, qtile, li, lh);
     v16f o[2] = {zero16(), zero16()};
     float m = -INFINITY, l = 0.f;
     for (int kb = wave; kb <= qb; kb += kWaves) {
         const int j0 = kb * kBlock;
-        tile_store(tile, vnext, lane);  // V of this block (the previous block's reads are done)
+        float kreg[32];
+        tile_store(tile, kload, lane);  // K of this block (the previous block's reads are done)
+        wave_sync();
+        lds_half_row(kreg, tile, li, lh);
+        wave_sync();
+        tile_store(tile, vload, lane);  // then V in its place: a wave's LDS operations run in issue order
         wave_sync();
         const bool more = kb + kWaves <= qb;
-        float knext[32];
         if (more) {  // the next block's loads run while this block computes
-            load_half_row(knext, k, j0 + kWaves * kBlock + li, sh.length, sh.row, lh);
-            tile_load(vnext, v, j0 + kWaves * kBlock, sh.length, sh.row, lane);
+            tile_load(kload, k, j0 + kWaves * kBlock, sh.length, sh.row, lane);
+            tile_load(vload, v, j0 + kWaves * kBlock, sh.length, sh.row, lane);
         }
         v16f s = dot_rows(kreg, qreg);
         // scale, mask, block max of this query's scores (16 here, 16 in lane li + 32)
@@ -227,7 +272,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
             s[r] = x;
             bmax = fmaxf(bmax, x);
         }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = halves_max(bmax);
         const float mnew = fmaxf(m, bmax);
         const float alpha = mnew == -INFINITY ? 1.f : __expf(m - mnew);
         float bsum = 0.f;
@@ -237,7 +282,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
             s[r] = p;
             bsum += p;
         }
-        bsum += __shfl_xor(bsum, 32);
+        bsum = halves_sum(bsum);
         l = l * alpha + bsum;
         m = mnew;
 #pragma unroll
@@ -253,10 +298,6 @@ __global__ __launch_bounds__(kWaves * 64) void attention_forward_kernel(float* _
             o[1] = mfma(vr[32], s[t], o[1]);
         }
         wave_sync();
-        if (more) {
-#pragma unroll
-            for (int t = 0; t < 32; ++t) kreg[t] = knext[t];
-        }
     }
     // merge: o[dt][r] = O^T[32 dt + block_row(r, lh)][query li] of this wave's key blocks
 #pragma unroll
@@ -299,10 +340,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dq_kernel(float* __r
                                                                    const float* __restrict__ qkv,
                                                                    const float* __restrict__ out,
                                                                    const float* __restrict__ lse, AttentionShape sh) {
-    __shared__ float tiles[kWaves * kTile];
+    __shared__ float tiles[kWaves * kTile];  // each wave's V, then K, tile of its current key block
+    __shared__ float rows[3][kTile];         // the query block's Q, dO and O
     const int blocks = (sh.length + kBlock - 1) / kBlock;
-    const int bh = blockIdx.x / blocks;
-    const int qb = blocks - 1 - static_cast<int>(blockIdx.x % blocks);
+    const int units = sh.batch * sh.heads;
+    const int bh = static_cast<int>(blockIdx.x % units);
+    const int qb = blocks - 1 - static_cast<int>(blockIdx.x / units);
     const int b = bh / sh.heads, h = bh % sh.heads;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
@@ -315,41 +358,57 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dq_kernel(float* __r
     const int i0 = qb * kBlock;
     const int query = i0 + li;
 
-    float qreg[32], doreg[32], oreg[32], vreg[32];
-    v4f kload[kTileVec];
-    load_half_row(qreg, q, query, sh.length, sh.row, lh);
-    load_half_row(doreg, go, query, sh.length, sh.out_row, lh);
-    load_half_row(oreg, o, query, sh.length, sh.out_row, lh);
+    // every load in flight together: the wave's quarter of the query block's Q, dO and O, its first
+    // K and V tiles
+    v4f qpart[kPartVec], gpart[kPartVec], opart[kPartVec], kload[kTileVec], vload[kTileVec];
+    part_load(qpart, q, i0, sh.length, sh.row, wave, lane);
+    part_load(gpart, go, i0, sh.length, sh.out_row, wave, lane);
+    part_load(opart, o, i0, sh.length, sh.out_row, wave, lane);
     const float row_lse = query < sh.length ? lse[static_cast<int64_t>(bh) * sh.length + query] : 0.f;
-    if (wave <= qb) {  // the first key block's loads in flight with the query block's
+    if (wave <= qb) {
         tile_load(kload, k, wave * kBlock, sh.length, sh.row, lane);
-        load_half_row(vreg, v, wave * kBlock + li, sh.length, sh.row, lh);
+        tile_load(vload, v, wave * kBlock, sh.length, sh.row, lane);
     }
+    part_store(rows[0], qpart, wave, lane);
+    part_store(rows[1], gpart, wave, lane);
+    part_store(rows[2], opart, wave, lane);
+    __syncthreads();
+    float qreg[32], doreg[32];
+    lds_half_row(qreg, rows[0], li, lh);
+    lds_half_row(doreg, rows[1], li, lh);
     float dl;
     {
+        float oreg[32];
+        lds_half_row(oreg, rows[2], li, lh);
         float part = 0.f;
 #pragma unroll
         for (int t = 0; t < 32; ++t) part += doreg[t] * oreg[t];
-        dl = part + __shfl_xor(part, 32);
+        dl = halves_sum(part);
     }
     if (wave == 0 && query < sh.length && lh == 0) delta[static_cast<int64_t>(bh) * sh.length + query] = dl;
 
     v16f dq[2] = {zero16(), zero16()};
     for (int kb = wave; kb <= qb; kb += kWaves) {
         const int j0 = kb * kBlock;
-        if (kb > wave) {
-            tile_load(kload, k, j0, sh.length, sh.row, lane);
-            load_half_row(vreg, v, j0 + li, sh.length, sh.row, lh);
+        v16f dp, s;
+        {
+            float vreg[32];
+            tile_store(tile, vload, lane);  // V of this block (the previous block's reads are done)
+            wave_sync();
+            lds_half_row(vreg, tile, li, lh);
+            wave_sync();
+            tile_store(tile, kload, lane);  // then K in its place: a wave's LDS operations run in issue order
+            wave_sync();
+            dp = dot_rows(vreg, doreg);
         }
-        tile_store(tile, kload, lane);  // K of this block (the previous block's reads are done)
-        wave_sync();
-        float kreg[32];
-        lds_half_row(kreg, tile, li, lh);
-        v16f s = zero16(), dp = zero16();
-#pragma unroll
-        for (int t = 0; t < 32; ++t) {
-            s = mfma(kreg[t], qreg[t], s);
-            dp = mfma(vreg[t], doreg[t], dp);
+        {
+            float kreg[32];
+            lds_half_row(kreg, tile, li, lh);
+            s = dot_rows(kreg, qreg);  // the forward's product, term for term
+        }
+        if (kb + kWaves <= qb) {  // the next block's loads run while this block finishes
+            tile_load(kload, k, j0 + kWaves * kBlock, sh.length, sh.row, lane);
+            tile_load(vload, v, j0 + kWaves * kBlock, sh.length, sh.row, lane);
         }
         // s[r] = S[query][key], dp[r] = dP[query][key] for key j0 + block_row(r, lh)
 #pragma unroll
@@ -381,11 +440,13 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
                                                                     const float* __restrict__ dout,
                                                                     const float* __restrict__ qkv,
                                                                     const float* __restrict__ lse, AttentionShape sh) {
-    __shared__ float tiles[2 * kWaves * kTile];
+    __shared__ float tiles[2 * kWaves * kTile];  // each wave's Q and dO tiles (the first holds K at the start)
+    __shared__ float vtile[kTile];               // the key block's V
     __shared__ float lses[kWaves][kBlock], deltas[kWaves][kBlock];
     const int blocks = (sh.length + kBlock - 1) / kBlock;
-    const int bh = blockIdx.x / blocks;
-    const int kb = static_cast<int>(blockIdx.x % blocks);  // key block 0 has the most query blocks
+    const int units = sh.batch * sh.heads;
+    const int bh = static_cast<int>(blockIdx.x % units);
+    const int kb = static_cast<int>(blockIdx.x / units);  // key block 0 has the most query blocks: first
     const int b = bh / sh.heads, h = bh % sh.heads;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
@@ -400,22 +461,32 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
     const int j0 = kb * kBlock;
     const int key = j0 + li;
 
-    float kreg[32], vreg[32];
-    v4f qload[kTileVec], gload[kTileVec];
+    v4f kpart[kPartVec], vpart[kPartVec], qload[kTileVec], gload[kTileVec];
     float lload = 0.f, dload = 0.f;
-    // the key block's rows and every load of the first query block, in flight together
-    load_half_row(kreg, k, key, sh.length, sh.row, lh);
-    load_half_row(vreg, v, key, sh.length, sh.row, lh);
-
-    v16f dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
-    for (int qb = kb + wave; qb < blocks; qb += kWaves) {
-        const int i0 = qb * kBlock;
+    // every load in flight together: the wave's quarter of the key block's K and V, and the wave's
+    // first query block (Q, dO, log-sum-exp and delta rows)
+    part_load(kpart, k, j0, sh.length, sh.row, wave, lane);
+    part_load(vpart, v, j0, sh.length, sh.row, wave, lane);
+    const auto load_query_block = [&](int i0) {
         tile_load(qload, q, i0, sh.length, sh.row, lane);
         tile_load(gload, go, i0, sh.length, sh.out_row, lane);
         if (lane < kBlock) {
             lload = i0 + lane < sh.length ? row_lse[i0 + lane] : 0.f;
             dload = i0 + lane < sh.length ? row_delta[i0 + lane] : 0.f;
         }
+    };
+    if (kb + wave < blocks) load_query_block((kb + wave) * kBlock);
+    // K passes through the first tile, which wave 0 reuses only after the second barrier; V stays in
+    // LDS (read again for every query block, which leaves the registers to the products)
+    part_store(tiles, kpart, wave, lane);
+    part_store(vtile, vpart, wave, lane);
+    __syncthreads();
+    float kreg[32];
+    lds_half_row(kreg, tiles, li, lh);
+    __syncthreads();
+
+    v16f dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
+    const auto block_products = [&](int i0) {
         tile_store(qtile, qload, lane);  // the previous block's reads are done
         tile_store(gtile, gload, lane);
         if (lane < kBlock) {
@@ -423,14 +494,17 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
             deltas[wave][lane] = dload;
         }
         wave_sync();
-        float qreg[32], doreg[32];
-        lds_half_row(qreg, qtile, li, lh);
-        lds_half_row(doreg, gtile, li, lh);
-        v16f s = zero16(), dp = zero16();
-#pragma unroll
-        for (int t = 0; t < 32; ++t) {
-            s = mfma(qreg[t], kreg[t], s);
-            dp = mfma(doreg[t], vreg[t], dp);
+        v16f s, dp;
+        {
+            float qreg[32];
+            lds_half_row(qreg, qtile, li, lh);
+            s = dot_rows(qreg, kreg);
+        }
+        {
+            float doreg[32], vreg[32];
+            lds_half_row(doreg, gtile, li, lh);
+            lds_half_row(vreg, vtile, li, lh);
+            dp = dot_rows(doreg, vreg);
         }
         // s[r] = S[query][key], dp[r] = dP[query][key] for query i0 + block_row(r, lh), key li
         float p[16];
@@ -453,6 +527,15 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
             dk[1] = mfma(s[t], qtile[off + 32], dk[1]);
         }
         wave_sync();
+    };
+    // the first query block's loads were issued before the barriers; each later one's just before use
+    // (loads kept in flight across a block would need registers the products use)
+    if (kb + wave < blocks) {
+        block_products((kb + wave) * kBlock);
+        for (int qb = kb + wave + kWaves; qb < blocks; qb += kWaves) {
+            load_query_block(qb * kBlock);
+            block_products(qb * kBlock);
+        }
     }
     // dk / dv[dt][r] = dK / dV[j0 + block_row(r, lh)][32 dt + li]: partial sums added in wave order
     spill_pair(qtile, dk, li, lh);
