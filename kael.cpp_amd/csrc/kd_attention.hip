@@ -1,7 +1,7 @@
 // kd_attention.hip - kael's causal self-attention (reference src/nn/transformer.cpp:103-138: the
 // fused projection's output viewed [B, T, 3, H, D], q / k / v selected and transposed per head,
 // softmax(mask(q . k^T / sqrt(D))) . v, the heads merged back to [B, T, H * D]) as one kernel
-// forward and two backward, for f32 and D = 64, without a KV cache or dropout.
+// forward and one backward, for f32 and D = 64, without a KV cache or dropout.
 //
 // Forward: one workgroup of four waves per (batch, head, block of 32 queries); wave w walks key
 // blocks w, w + 4, ... up to the diagonal: S^T = K_J . Q_I^T on v_mfma_f32_32x32x2f32 (each lane then holds 16 scores
@@ -14,10 +14,11 @@
 //
 // Backward (the gradient of every op of kael's chain: the products, the scale, the mask and
 // softmax backward y (g - sum(g y))): with delta_i = sum_d dO[i][d] O[i][d] (= sum_j P dP over
-// the row) and P recomputed from the log-sum-exp, dS = P (dP - delta) / sqrt(D);
-//   dq kernel, a workgroup per (batch, head, query block): delta (kept for the next launch),
-//     then for each key block S^T, dP^T = V_J . dO_I^T, dS^T, and dQ += dS . K_J;
-//   dkv kernel, a workgroup per (batch, head, key block): for each query block at or after it
+// the row) and P recomputed from the log-sum-exp, dS = P (dP - delta) / sqrt(D), one launch of two
+// kinds of workgroup:
+//   dQ groups, one per (batch, head, query block): delta, then for each key block S^T,
+//     dP^T = V_J . dO_I^T, dS^T, and dQ += dS . K_J;
+//   dK / dV groups, one per (batch, head, key block): for each query block at or after it delta,
 //     S, dP = dO_I . V_J^T, dS, dV += P^T . dO_I and dK += dS^T . Q_I;
 //   the four waves split the blocks they walk and add their partial sums in wave order.
 // Every MFMA sums over 64 features (or 32 keys / queries) with the operands' features split as
@@ -62,8 +63,8 @@ struct AttentionShape {
 
 // ---- work split and LDS tiles --------------------------------------------------------------
 //
-// A workgroup is 4 waves on one block of 32 rows: the forward and dq kernels on a query block,
-// wave w taking key blocks w, w + 4, ... up to the diagonal; the dkv kernel on a key block, wave w
+// A workgroup is 4 waves on one block of 32 rows: the forward and dQ groups on a query block,
+// wave w taking key blocks w, w + 4, ... up to the diagonal; a dK / dV group on a key block, wave w
 // taking query blocks kb + w, kb + w + 4, ... Workgroups run longest first (the last query blocks,
 // the first key blocks), with all (batch, head) pairs interleaved so that every XCD gets its share of
 // each length.
@@ -71,7 +72,7 @@ struct AttentionShape {
 // Every global load reads whole rows, 16 bytes per lane and four 256-byte rows per instruction:
 // a lane-per-row operand loaded directly would touch 64 cache lines per instruction, and those
 // loads made up the largest part of a wave's time. The block all four waves share (the query rows,
-// or the dkv kernel's key rows) is loaded a quarter per wave into a shared LDS tile behind one
+// or a dK / dV group's key rows) is loaded a quarter per wave into a shared LDS tile behind one
 // workgroup barrier; the blocks a wave walks pass through an LDS tile of its own (rows padded to 68
 // floats), so the waves never wait for each other inside the loop: a wave issues every global load
 // of its first block at once, keeps the next block's loads in flight in registers while it computes
@@ -333,19 +334,31 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_forward_kernel(float
     }
 }
 
-// ---- backward: delta and dQ ---------------------------------------------------------------
+// ---- backward ----------------------------------------------------------------------------
+//
+// One launch holds both kinds of workgroup: first the dK / dV groups (a key block each, the longer
+// ones), then the dQ groups (a query block each). Each computes the delta of the query rows it
+// needs, with the same expression, so neither waits for the other.
 
-__global__ __launch_bounds__(kWaves * 64, 2) void attention_dq_kernel(float* __restrict__ dqkv, float* __restrict__ delta,
-                                                                   const float* __restrict__ dout,
-                                                                   const float* __restrict__ qkv,
-                                                                   const float* __restrict__ out,
-                                                                   const float* __restrict__ lse, AttentionShape sh) {
-    __shared__ float tiles[kWaves * kTile];  // each wave's V, then K, tile of its current key block
-    __shared__ float rows[3][kTile];         // the query block's Q, dO and O
+// delta of one query row, sum_d dO[d] O[d]: each half's 32 products summed in order, then the halves.
+__device__ __forceinline__ float row_delta(const float (&g)[32], const float (&o)[32]) {
+    float part = 0.f;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) part += g[t] * o[t];
+    return halves_sum(part);
+}
+
+// The dQ group `group`: lds holds 7 tiles.
+__device__ __forceinline__ void dq_group(int group, float* __restrict__ lds, float* __restrict__ dqkv,
+                                         const float* __restrict__ dout, const float* __restrict__ qkv,
+                                         const float* __restrict__ out, const float* __restrict__ lse,
+                                         const AttentionShape& sh) {
+    float* tiles = lds;                   // each wave's V, then K, tile of its current key block
+    float* rows[3] = {lds + kWaves * kTile, lds + (kWaves + 1) * kTile, lds + (kWaves + 2) * kTile};  // Q, dO, O
     const int blocks = (sh.length + kBlock - 1) / kBlock;
     const int units = sh.batch * sh.heads;
-    const int bh = static_cast<int>(blockIdx.x % units);
-    const int qb = blocks - 1 - static_cast<int>(blockIdx.x / units);
+    const int bh = group % units;
+    const int qb = blocks - 1 - group / units;
     const int b = bh / sh.heads, h = bh % sh.heads;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
@@ -380,12 +393,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dq_kernel(float* __r
     {
         float oreg[32];
         lds_half_row(oreg, rows[2], li, lh);
-        float part = 0.f;
-#pragma unroll
-        for (int t = 0; t < 32; ++t) part += doreg[t] * oreg[t];
-        dl = halves_sum(part);
+        dl = row_delta(doreg, oreg);
     }
-    if (wave == 0 && query < sh.length && lh == 0) delta[static_cast<int64_t>(bh) * sh.length + query] = dl;
 
     v16f dq[2] = {zero16(), zero16()};
     for (int kb = wave; kb <= qb; kb += kWaves) {
@@ -433,20 +442,19 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dq_kernel(float* __r
     store_tile_sum(dqkv + tok0 * sh.row + h * kD, tiles, i0, sh.length, sh.row, wave, lane);
 }
 
-// ---- backward: dK and dV ------------------------------------------------------------------
-
-__global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __restrict__ dqkv,
-                                                                    const float* __restrict__ delta,
-                                                                    const float* __restrict__ dout,
-                                                                    const float* __restrict__ qkv,
-                                                                    const float* __restrict__ lse, AttentionShape sh) {
-    __shared__ float tiles[2 * kWaves * kTile];  // each wave's Q and dO tiles (the first holds K at the start)
-    __shared__ float vtile[kTile];               // the key block's V
-    __shared__ float lses[kWaves][kBlock], deltas[kWaves][kBlock];
+// The dK / dV group `group`: lds holds 9 tiles and 2 x 4 rows of 32.
+__device__ __forceinline__ void dkv_group(int group, float* __restrict__ lds, float* __restrict__ dqkv,
+                                          const float* __restrict__ dout, const float* __restrict__ qkv,
+                                          const float* __restrict__ out, const float* __restrict__ lse,
+                                          const AttentionShape& sh) {
+    float* tiles = lds;                        // each wave's Q (O first) and dO tiles; the first holds K at the start
+    float* vtile = lds + 2 * kWaves * kTile;   // the key block's V
+    float (*lses)[kBlock] = reinterpret_cast<float (*)[kBlock]>(vtile + kTile);
+    float (*deltas)[kBlock] = lses + kWaves;
     const int blocks = (sh.length + kBlock - 1) / kBlock;
     const int units = sh.batch * sh.heads;
-    const int bh = static_cast<int>(blockIdx.x % units);
-    const int kb = static_cast<int>(blockIdx.x / units);  // key block 0 has the most query blocks: first
+    const int bh = group % units;
+    const int kb = group / units;  // key block 0 has the most query blocks: first
     const int b = bh / sh.heads, h = bh % sh.heads;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 32, lh = lane / 32;
     const int64_t tok0 = static_cast<int64_t>(b) * sh.length;
@@ -454,26 +462,24 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
     const float* k = q + sh.heads * kD;
     const float* v = k + sh.heads * kD;
     const float* go = dout + tok0 * sh.out_row + h * kD;
+    const float* o = out + tok0 * sh.out_row + h * kD;
     const float* row_lse = lse + static_cast<int64_t>(bh) * sh.length;
-    const float* row_delta = delta + static_cast<int64_t>(bh) * sh.length;
     float* qtile = tiles + wave * kTile;
     float* gtile = tiles + (kWaves + wave) * kTile;
     const int j0 = kb * kBlock;
     const int key = j0 + li;
 
-    v4f kpart[kPartVec], vpart[kPartVec], qload[kTileVec], gload[kTileVec];
-    float lload = 0.f, dload = 0.f;
+    v4f kpart[kPartVec], vpart[kPartVec], qload[kTileVec], gload[kTileVec], oload[kTileVec];
+    float lload = 0.f;
     // every load in flight together: the wave's quarter of the key block's K and V, and the wave's
-    // first query block (Q, dO, log-sum-exp and delta rows)
+    // first query block (Q, dO, O and log-sum-exp rows)
     part_load(kpart, k, j0, sh.length, sh.row, wave, lane);
     part_load(vpart, v, j0, sh.length, sh.row, wave, lane);
     const auto load_query_block = [&](int i0) {
         tile_load(qload, q, i0, sh.length, sh.row, lane);
         tile_load(gload, go, i0, sh.length, sh.out_row, lane);
-        if (lane < kBlock) {
-            lload = i0 + lane < sh.length ? row_lse[i0 + lane] : 0.f;
-            dload = i0 + lane < sh.length ? row_delta[i0 + lane] : 0.f;
-        }
+        tile_load(oload, o, i0, sh.length, sh.out_row, lane);
+        if (lane < kBlock) lload = i0 + lane < sh.length ? row_lse[i0 + lane] : 0.f;
     };
     if (kb + wave < blocks) load_query_block((kb + wave) * kBlock);
     // K passes through the first tile, which wave 0 reuses only after the second barrier; V stays in
@@ -487,12 +493,19 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
 
     v16f dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
     const auto block_products = [&](int i0) {
-        tile_store(qtile, qload, lane);  // the previous block's reads are done
+        tile_store(qtile, oload, lane);  // O first, for the rows' delta (the previous block's reads are done)
         tile_store(gtile, gload, lane);
-        if (lane < kBlock) {
-            lses[wave][lane] = lload;
-            deltas[wave][lane] = dload;
+        if (lane < kBlock) lses[wave][lane] = lload;
+        wave_sync();
+        {
+            float greg[32], oreg[32];
+            lds_half_row(greg, gtile, li, lh);
+            lds_half_row(oreg, qtile, li, lh);
+            const float dl = row_delta(greg, oreg);
+            if (lh == 0) deltas[wave][li] = dl;
         }
+        wave_sync();
+        tile_store(qtile, qload, lane);  // then Q in its place: a wave's LDS operations run in issue order
         wave_sync();
         v16f s, dp;
         {
@@ -546,6 +559,23 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_dkv_kernel(float* __
     store_tile_sum(dstk + sh.heads * kD, tiles + kWaves * kTile, j0, sh.length, sh.row, wave, lane);
 }
 
+constexpr int kBackwardLds = (2 * kWaves + 1) * kTile + 2 * kWaves * kBlock;  // the dK / dV group's, the larger
+
+__global__ __launch_bounds__(kWaves * 64, 2) void attention_backward_kernel(float* __restrict__ dqkv,
+                                                                            const float* __restrict__ dout,
+                                                                            const float* __restrict__ qkv,
+                                                                            const float* __restrict__ out,
+                                                                            const float* __restrict__ lse,
+                                                                            AttentionShape sh) {
+    __shared__ float lds[kBackwardLds];
+    const int groups = sh.batch * sh.heads * ((sh.length + kBlock - 1) / kBlock);
+    const int i = static_cast<int>(blockIdx.x);
+    if (i < groups)
+        dkv_group(i, lds, dqkv, dout, qkv, out, lse, sh);
+    else
+        dq_group(i - groups, lds, dqkv, dout, qkv, out, lse, sh);
+}
+
 int check_shape(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t head_dim, AttentionShape& sh,
                 const char* what) {
     if (dtype != KD_F32) return fail(KD_E_UNSUPPORTED, std::string(what) + ": dtype must be f32");
@@ -553,7 +583,7 @@ int check_shape(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t
     if (batch < 1 || length < 1 || heads < 1) return fail(KD_E_INVALID, std::string(what) + ": empty shape");
     const int64_t blocks = (length + kBlock - 1) / kBlock;
     const int64_t row = 3 * heads * kD;
-    if (batch * heads * blocks >= (int64_t{1} << 31) || length * row >= (int64_t{1} << 31) || batch > INT32_MAX)
+    if (2 * batch * heads * blocks >= (int64_t{1} << 31) || length * row >= (int64_t{1} << 31) || batch > INT32_MAX)
         return fail(KD_E_INVALID, std::string(what) + ": shape too large");
     sh.batch = static_cast<int>(batch);
     sh.length = static_cast<int>(length);
@@ -596,17 +626,10 @@ extern "C" int kd_causal_attention_backward(int dtype, void* dqkv, const void* d
         return fail(KD_E_INVALID, "kd_causal_attention_backward: every operand must be given, 16-byte aligned");
     if (int rc = ensure_device()) return rc;
     const int64_t blocks = (length + kBlock - 1) / kBlock;
-    Workspace ws;  // delta, held until the dkv kernel is enqueued
-    if (int rc = workspace(ws, static_cast<size_t>(batch * heads * length) * sizeof(float))) return rc;
-    float* delta = static_cast<float*>(ws.ptr);
-    const dim3 grid(static_cast<uint32_t>(batch * heads * blocks));
-    hipLaunchKernelGGL(attention_dq_kernel, grid, dim3(kWaves * 64), 0, stream(), static_cast<float*>(dqkv), delta,
-                       static_cast<const float*>(dout), static_cast<const float*>(qkv), static_cast<const float*>(out),
-                       static_cast<const float*>(lse), sh);
-    KD_LAUNCH_CHECK();
-    hipLaunchKernelGGL(attention_dkv_kernel, grid, dim3(kWaves * 64), 0, stream(), static_cast<float*>(dqkv),
-                       static_cast<const float*>(delta), static_cast<const float*>(dout), static_cast<const float*>(qkv),
-                       static_cast<const float*>(lse), sh);
+    hipLaunchKernelGGL(attention_backward_kernel, dim3(static_cast<uint32_t>(2 * batch * heads * blocks)),
+                       dim3(kWaves * 64), 0, stream(), static_cast<float*>(dqkv), static_cast<const float*>(dout),
+                       static_cast<const float*>(qkv), static_cast<const float*>(out), static_cast<const float*>(lse),
+                       sh);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }
