@@ -328,9 +328,23 @@ int kd_causal_attention(int dtype, void* out, void* lse, const void* qkv, int64_
 /* Its backward (kael's autograd for the same chain: the two products' MatmulBackward,
  * SoftmaxBackward, MaskedFillBackward, the division's backward and the select / transpose
  * backward into one tensor): dqkv [B, T, 3, H, D], every element written, from dout
- * [B, T, H * D] and the forward's qkv, out and lse, in two launches. */
+ * [B, T, H * D] and the forward's qkv, out and lse, in one launch. */
 int kd_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
                                  const void* lse, int64_t batch, int64_t length, int64_t heads, int64_t head_dim);
+
+/* kael's causal self-attention with a KV cache (reference src/nn/transformer.cpp:103-138: the
+ * cached keys and values concatenated with the new ones at :119-126, the future mask's rows
+ * past .. past + T at :131, then the chain above), forward only, as one launch: `length` new
+ * queries at positions keys - length .. keys - 1 against the keys and values of positions
+ * 0 .. keys - 1, query t seeing keys 0 .. keys - length + t. q is [batch, heads, length, 64] and
+ * k, v are [batch, heads, keys, 64], each read in place through the strides (elements) of its
+ * batch, head and position dims in q_strides / k_strides / v_strides (features contiguous):
+ * kael's per-head views of the fused projection and its cache tensors. out [batch, length,
+ * heads * 64] receives the heads merged (transpose(1, 2).contiguous()). f32 and D = 64 only
+ * (KD_E_UNSUPPORTED otherwise). */
+int kd_cached_attention(int dtype, void* out, const void* q, const int64_t* q_strides, const void* k,
+                        const int64_t* k_strides, const void* v, const int64_t* v_strides, int64_t batch,
+                        int64_t heads, int64_t length, int64_t keys, int64_t head_dim);
 
 /* ---- fused row kernels (extensions replacing composed device paths) ---- */
 

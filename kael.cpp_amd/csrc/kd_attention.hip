@@ -576,6 +576,113 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attention_backward_kernel(floa
         dq_group(i - groups, lds, dqkv, dout, qkv, out, lse, sh);
 }
 
+// ---- attention of new queries against a KV cache -------------------------------------------------
+//
+// kael's CausalSelfAttention::forward with a cache (generation): `length` new queries at positions
+// past .. past + length - 1 against the keys and values of positions 0 .. keys - 1 (past = keys -
+// length), query t seeing keys 0 .. past + t. The operands are read in place through their strides
+// (kael's per-head views of the fused projection and its concatenated cache tensors), features
+// contiguous. A workgroup per (batch, head, query); wave w walks key groups w, w + waves, ... of 32
+// keys. A lane holds one feature: every key row is one coalesced 256-byte load, and the 32 lanes'
+// products of a group reduce in a butterfly (5 halving exchanges, then one add) that leaves key
+// (lane / 2)'s score in lanes 2j and 2j + 1. The online softmax runs per group (running max and
+// sum, the output rescaled when the max grows), each lane accumulating its feature of the output
+// over the group's keys in key order; the waves' (max, sum, output) merge in LDS in wave order.
+// Decode has few (batch, head) rows, so a workgroup then takes 16 waves.
+
+struct CachedShape {
+    int batch, heads, length, keys;
+    int64_t qs[3], ks[3], vs[3];  // strides (batch, head, position) in elements
+};
+
+constexpr int kCachedGroup = 32;
+constexpr int kCachedMaxWaves = 16;
+
+// The 2N values x of every lane summed pairwise with lane ^ D's: a lane whose bit D is set keeps
+// the upper N sums, the other the lower N.
+template <int N, int D>
+__device__ __forceinline__ void butterfly_step(const float (&x)[2 * N], float (&y)[N], int lane) {
+    const bool upper = (lane & D) != 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float send = upper ? x[i] : x[N + i];
+        const float keep = upper ? x[N + i] : x[i];
+        y[i] = keep + __shfl_xor(send, D);
+    }
+}
+
+__global__ __launch_bounds__(kCachedMaxWaves * 64) void cached_attention_kernel(float* __restrict__ out,
+                                                                                const float* __restrict__ q,
+                                                                                const float* __restrict__ k,
+                                                                                const float* __restrict__ v,
+                                                                                CachedShape sh) {
+    __shared__ float ms[kCachedMaxWaves], ls[kCachedMaxWaves];
+    __shared__ float os[kCachedMaxWaves][kD];
+    const int waves = static_cast<int>(blockDim.x) / 64;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int row = static_cast<int>(blockIdx.x);
+    const int t = row % sh.length, h = (row / sh.length) % sh.heads, b = row / (sh.length * sh.heads);
+    const int limit = sh.keys - sh.length + t + 1;  // keys 0 .. limit - 1 are visible
+    const float qd = q[b * sh.qs[0] + h * sh.qs[1] + t * sh.qs[2] + lane];
+    const float* kb = k + b * sh.ks[0] + h * sh.ks[1] + lane;
+    const float* vb = v + b * sh.vs[0] + h * sh.vs[1] + lane;
+    const int groups = (limit + kCachedGroup - 1) / kCachedGroup;
+    float m = -INFINITY, l = 0.f, o = 0.f;
+    for (int g = wave; g < groups; g += waves) {
+        const int j0 = g * kCachedGroup;
+        float x[32], vr[32];
+#pragma unroll
+        for (int jj = 0; jj < 32; ++jj) {
+            const int64_t j = min(j0 + jj, limit - 1);  // a key past the limit reads the last visible row, masked below
+            x[jj] = kb[j * sh.ks[2]];
+            vr[jj] = vb[j * sh.vs[2]];
+        }
+#pragma unroll
+        for (int jj = 0; jj < 32; ++jj) x[jj] *= qd;
+        float y16[16], y8[8], y4[4], y2[2], y1[1];
+        butterfly_step<16, 32>(x, y16, lane);
+        butterfly_step<8, 16>(y16, y8, lane);
+        butterfly_step<4, 8>(y8, y4, lane);
+        butterfly_step<2, 4>(y4, y2, lane);
+        butterfly_step<1, 2>(y2, y1, lane);
+        // lanes 2j and 2j + 1 hold the two halves of key j0 + j's sum: every lane now has the score
+        float s = y1[0] + __shfl_xor(y1[0], 1);
+        s = j0 + lane / 2 < limit ? s * 0.125f : -INFINITY;  // 1 / sqrt(64), exact
+        float gmax = s;
+#pragma unroll
+        for (int d = 2; d < 64; d *= 2) gmax = fmaxf(gmax, __shfl_xor(gmax, d));
+        const float mnew = fmaxf(m, gmax);
+        const float alpha = mnew == -INFINITY ? 1.f : __expf(m - mnew);
+        const float p = s == -INFINITY ? 0.f : __expf(s - mnew);
+        float gsum = p;  // each key once: the lanes that differ in bits 1-5
+#pragma unroll
+        for (int d = 2; d < 64; d *= 2) gsum += __shfl_xor(gsum, d);
+        l = l * alpha + gsum;
+        o *= alpha;
+#pragma unroll
+        for (int jj = 0; jj < 32; ++jj)
+            o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 2 * jj)) * vr[jj];
+        m = mnew;
+    }
+    if (lane == 0) {
+        ms[wave] = m;
+        ls[wave] = l;
+    }
+    os[wave][lane] = o;
+    __syncthreads();
+    if (wave == 0) {
+        float mx = -INFINITY;
+        for (int w = 0; w < waves; ++w) mx = fmaxf(mx, ms[w]);
+        float total = 0.f, acc = 0.f;
+        for (int w = 0; w < waves; ++w) {
+            const float f = ms[w] == -INFINITY ? 0.f : __expf(ms[w] - mx);
+            total += f * ls[w];
+            acc += f * os[w][lane];
+        }
+        out[((static_cast<int64_t>(b) * sh.length + t) * sh.heads + h) * kD + lane] = acc / total;
+    }
+}
+
 int check_shape(int dtype, int64_t batch, int64_t length, int64_t heads, int64_t head_dim, AttentionShape& sh,
                 const char* what) {
     if (dtype != KD_F32) return fail(KD_E_UNSUPPORTED, std::string(what) + ": dtype must be f32");
@@ -630,6 +737,48 @@ extern "C" int kd_causal_attention_backward(int dtype, void* dqkv, const void* d
                        dim3(kWaves * 64), 0, stream(), static_cast<float*>(dqkv), static_cast<const float*>(dout),
                        static_cast<const float*>(qkv), static_cast<const float*>(out), static_cast<const float*>(lse),
                        sh);
+    KD_LAUNCH_CHECK();
+    return KD_OK;
+}
+
+extern "C" int kd_cached_attention(int dtype, void* out, const void* q, const int64_t* q_strides, const void* k,
+                                   const int64_t* k_strides, const void* v, const int64_t* v_strides, int64_t batch,
+                                   int64_t heads, int64_t length, int64_t keys, int64_t head_dim) {
+    const char* what = "kd_cached_attention";
+    if (dtype != KD_F32) return fail(KD_E_UNSUPPORTED, std::string(what) + ": dtype must be f32");
+    if (head_dim != kD) return fail(KD_E_UNSUPPORTED, std::string(what) + ": head dim must be 64");
+    if (batch < 1 || heads < 1 || length < 1 || keys < length)
+        return fail(KD_E_INVALID, std::string(what) + ": needs batch, heads, length >= 1 and keys >= length");
+    if (out == nullptr || q == nullptr || k == nullptr || v == nullptr || q_strides == nullptr ||
+        k_strides == nullptr || v_strides == nullptr)
+        return fail(KD_E_INVALID, std::string(what) + ": every operand and stride array must be given");
+    CachedShape sh;
+    // every element the kernel reads lies at or below the last row's last feature of each operand
+    const int64_t dims[3][3] = {{batch, heads, length}, {batch, heads, keys}, {batch, heads, keys}};
+    const int64_t* strides[3] = {q_strides, k_strides, v_strides};
+    int64_t* dst[3] = {sh.qs, sh.ks, sh.vs};
+    for (int o = 0; o < 3; ++o) {
+        int64_t last = kD - 1;
+        for (int d = 0; d < 3; ++d) {
+            if (strides[o][d] < 0) return fail(KD_E_INVALID, std::string(what) + ": negative stride");
+            last += (dims[o][d] - 1) * strides[o][d];
+            dst[o][d] = strides[o][d];
+        }
+        if (last >= (int64_t{1} << 40)) return fail(KD_E_INVALID, std::string(what) + ": operand too large");
+    }
+    const int64_t rows = batch * heads * length;
+    if (rows >= (int64_t{1} << 31) || keys >= (int64_t{1} << 31))
+        return fail(KD_E_INVALID, std::string(what) + ": shape too large");
+    sh.batch = static_cast<int>(batch);
+    sh.heads = static_cast<int>(heads);
+    sh.length = static_cast<int>(length);
+    sh.keys = static_cast<int>(keys);
+    if (int rc = ensure_device()) return rc;
+    // few rows (decode): 16 waves share each row's keys; otherwise 4 waves and more workgroups
+    const int waves = rows < 2 * compute_units() ? kCachedMaxWaves : 4;
+    hipLaunchKernelGGL(cached_attention_kernel, dim3(static_cast<uint32_t>(rows)), dim3(waves * 64), 0, stream(),
+                       static_cast<float*>(out), static_cast<const float*>(q), static_cast<const float*>(k),
+                       static_cast<const float*>(v), sh);
     KD_LAUNCH_CHECK();
     return KD_OK;
 }

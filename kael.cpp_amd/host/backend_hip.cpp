@@ -271,6 +271,15 @@ void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* do
           "causal_attention_backward");
 }
 
+void cached_attention(DType dtype, std::byte* out, const std::byte* q, const std::int64_t* q_strides,
+                      const std::byte* k, const std::int64_t* k_strides, const std::byte* v,
+                      const std::int64_t* v_strides, std::int64_t batch, std::int64_t heads, std::int64_t length,
+                      std::int64_t keys, std::int64_t head_dim) {
+    check(kd_cached_attention(static_cast<int>(dtype), out, q, q_strides, k, k_strides, v, v_strides, batch, heads,
+                              length, keys, head_dim),
+          "cached_attention");
+}
+
 void index_bounds(const std::int64_t* indices, std::int64_t count, std::int64_t stride, std::int64_t bounds[2]) {
     check(kd_index_bounds(indices, count, stride, bounds), "index_bounds");
 }

@@ -151,6 +151,15 @@ void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* do
                                const std::byte* out, const std::byte* lse, std::int64_t batch, std::int64_t length,
                                std::int64_t heads, std::int64_t head_dim);
 
+// The attention of `length` new queries against a KV cache of `keys` positions (reference
+// src/nn/transformer.cpp:103-138 with a cache), forward only: q [B, H, length, D], k and v
+// [B, H, keys, D] read through the element strides of their batch, head and position dims
+// (features contiguous); out [B, length, H * D] with the heads merged. f32, D = 64.
+void cached_attention(DType dtype, std::byte* out, const std::byte* q, const std::int64_t* q_strides,
+                      const std::byte* k, const std::int64_t* k_strides, const std::byte* v,
+                      const std::int64_t* v_strides, std::int64_t batch, std::int64_t heads, std::int64_t length,
+                      std::int64_t keys, std::int64_t head_dim);
+
 // Running sums along `rows` contiguous rows of `size` elements (reference src/ops/sequence.cpp:95-117):
 // f32 / f64 store In, i64 / bool wrapping int64.
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows);

@@ -125,6 +125,8 @@ SIGNATURES = {
     "causal_attention": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64]),
     "causal_attention_backward": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                           c_int64, c_int64]),
+    "cached_attention": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                 c_int64, c_int64, c_int64, c_int64]),
     "softmax_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int]),
     "standardize_rows": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p]),
     "cross_entropy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64]),

@@ -47,7 +47,10 @@ training configs with kael's own host code calling the backend's fused entry poi
                                      the generator advanced as the host draws advance it
   src/nn/transformer.cpp             CausalSelfAttention::forward (:103-138) without a cache or
                                      dropout, f32 heads of 64: one device call forward and one node
-                                     (two launches) backward (kd_causal_attention);
+                                     (one launch) backward (kd_causal_attention); with a cache and
+                                     no gradient recorded, the new queries against the cached keys
+                                     and values read in place, one device call
+                                     (kd_cached_attention);
                                      nn::generate (:256-295) with temperature 0, the KV cache and a
                                      batch-1 prompt on the device runs on the decode engine
                                      (kd_gpt_*), token for token the greedy sequence of the loop
@@ -681,8 +684,8 @@ ATTENTION_HELPER = """
 // MI355X: the attention of CausalSelfAttention::forward without a KV cache or dropout, for f32
 // heads of 64, as one device call over the fused projection's output parts [B, T, 3, H, D]
 // (contiguous): the output comes back with the heads merged ([B, T, H * D], what
-// transpose(1, 2).contiguous() gives), and one node takes the whole chain's backward (two
-// launches writing the q, k and v gradients into one [B, T, 3, H, D] tensor) instead of the
+// transpose(1, 2).contiguous() gives), and one node takes the whole chain's backward (one
+// launch writing the q, k and v gradients into one [B, T, 3, H, D] tensor) instead of the
 // products, scale, mask, softmax, merge copy and three select gradients. nullopt for any other
 // case, which keeps kael's ops.
 std::optional<Tensor> device_causal_attention(const Tensor& parts, std::int64_t heads, std::int64_t head_dim) {
@@ -714,6 +717,47 @@ std::optional<Tensor> device_causal_attention(const Tensor& parts, std::int64_t 
     }
     return out;
 }
+"""
+
+CACHED_ATTENTION_HELPER = """
+// MI355X: the attention of CausalSelfAttention::forward with a KV cache when no gradient is
+// recorded (generation), for f32 heads of 64: one device call reads the new queries (a view of the
+// fused projection) and the keys and values (the cache's concatenated tensors, or at the first
+// step the views themselves) in place and returns the heads merged ([B, T, H * D]), instead of
+// the two products, scale, mask, softmax and merge copy. nullopt for any other case, which keeps
+// kael's ops.
+std::optional<Tensor> device_cached_attention(const Tensor& queries, const Tensor& keys, const Tensor& values,
+                                              std::int64_t head_dim) {
+    for (const Tensor* t : {&queries, &keys, &values}) {
+        if (t->device() == Device::CPU || t->dtype() != DType::F32 || t->dim() != 4 || t->size(3) != head_dim ||
+            t->strides()[3] != 1 || t->numel() == 0 || (autograd::GradMode::is_enabled() && t->requires_grad())) {
+            return std::nullopt;
+        }
+    }
+    const std::int64_t batch = queries.size(0);
+    const std::int64_t heads = queries.size(1);
+    const std::int64_t length = queries.size(2);
+    const std::int64_t total = keys.size(2);
+    if (head_dim != 64 || values.size(2) != total || total < length || keys.size(0) != batch ||
+        values.size(0) != batch || keys.size(1) != heads || values.size(1) != heads) {
+        return std::nullopt;
+    }
+    const std::int64_t qs[3] = {queries.strides()[0], queries.strides()[1], queries.strides()[2]};
+    const std::int64_t ks[3] = {keys.strides()[0], keys.strides()[1], keys.strides()[2]};
+    const std::int64_t vs[3] = {values.strides()[0], values.strides()[1], values.strides()[2]};
+    Tensor out = empty({batch, length, heads * head_dim}, DType::F32, queries.device());
+    device::cached_attention(DType::F32, out.device_data(), queries.device_data(), qs, keys.device_data(), ks,
+                             values.device_data(), vs, batch, heads, length, total, head_dim);
+    return out;
+}
+"""
+
+CACHED_ATTENTION_BRANCH = """    if (cache != nullptr && (dropout_ == 0.0 || !is_training())) {
+        if (std::optional<Tensor> mixed = device_cached_attention(queries, keys, values, head_dimension_)) {
+            const Tensor output = projection_->forward(mixed->view({batch, length, dimension_}));
+            return functional::dropout(output, dropout_, is_training());
+        }
+    }
 """
 
 ATTENTION_BRANCH = """    if (cache == nullptr && (dropout_ == 0.0 || !is_training())) {
@@ -864,12 +908,14 @@ EDITS = [
     ("src/nn/transformer.cpp", '#include "kael/autograd/grad_mode.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/nn/transformer.cpp", "class TrainingModeRestorer {\n", "before", GENERATE_HELPER),
     ("src/nn/transformer.cpp", '#include "kael/random.h"\n', "after", '\n#include "recording.h"\n'),
-    ("src/nn/transformer.cpp", "constexpr double kInitialStd = 0.02;\n", "after", ATTENTION_HELPER),
+    ("src/nn/transformer.cpp", "constexpr double kInitialStd = 0.02;\n", "after", ATTENTION_HELPER + CACHED_ATTENTION_HELPER),
     ("src/nn/transformer.cpp",
      "        query_key_value_->forward(input).view({batch, length, 3, heads_, head_dimension_});\n", "after",
      ATTENTION_BRANCH),
     ("src/nn/transformer.cpp", "    const std::int64_t context = model.config().max_positions;\n", "after",
      GENERATE_BRANCH),
+    ("src/nn/transformer.cpp", "    if (future_mask_.device() != input.device()) {\n", "before",
+     CACHED_ATTENTION_BRANCH),
     ("src/ops/sequence.cpp", '#include "kael/ops.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/ops/sequence.cpp", "        return t.to(dtype).clone();\n    }\n", "after", CUMSUM_BRANCH),
     ("src/ops/indexing.cpp", '#include "kael/kernels.h"\n', "after", '#include "kael/device_kernels.h"\n'),

@@ -959,6 +959,62 @@ int oracle_causal_attention_backward(int dtype, void* dqkv, const void* dout, co
     return rc;
 }
 
+/* ---- causal self-attention with a KV cache ----------------------------------------------------
+ *
+ * kael's CausalSelfAttention::forward with a cache (reference src/nn/transformer.cpp:103-138): the
+ * new queries Q [T, D] of positions past .. past + T - 1 (past = keys - T), the keys and values
+ * K, V [keys, D] of positions 0 .. keys - 1 (the cache's cat with the new rows, :119-126), each
+ * per (batch, head) a strided view read element by element; S = Q . K^T (oracle_matmul); S / sqrt(D)
+ * rounded to f32; masked_fill with -inf where key > past + query (the future mask's rows past ..
+ * past + T, :131); softmax rows; O = P . V; out[b, t, h, :] = O[t]. With past = 0 this is the
+ * uncached chain above, op for op. */
+int oracle_cached_attention(int dtype, void* out, const void* q, const int64_t* q_strides, const void* k,
+                            const int64_t* k_strides, const void* v, const int64_t* v_strides, int64_t batch,
+                            int64_t heads, int64_t length, int64_t keys, int64_t head_dim) {
+    if (dtype != KD_F32) return fail("cached_attention: f32 only");
+    if (batch < 1 || heads < 1 || length < 1 || head_dim < 1 || keys < length)
+        return fail("cached_attention: needs batch, heads, length, head_dim >= 1 and keys >= length");
+    const float* qf = (const float*)q;
+    const float* kf = (const float*)k;
+    const float* vf = (const float*)v;
+    const int64_t past = keys - length;
+    float* qm = (float*)malloc((size_t)(length * head_dim) * 4);
+    float* kt = (float*)malloc((size_t)(head_dim * keys) * 4);
+    float* vm = (float*)malloc((size_t)(keys * head_dim) * 4);
+    float* scores = (float*)malloc((size_t)(length * keys) * 4);
+    float* p = (float*)malloc((size_t)(length * keys) * 4);
+    float* o = (float*)malloc((size_t)(length * head_dim) * 4);
+    const float scale = (float)sqrt((double)head_dim);
+    int rc = KD_OK;
+    for (int64_t b = 0; b < batch && rc == KD_OK; ++b)
+        for (int64_t h = 0; h < heads && rc == KD_OK; ++h) {
+            for (int64_t t = 0; t < length; ++t)
+                for (int64_t d = 0; d < head_dim; ++d)
+                    qm[t * head_dim + d] = qf[b * q_strides[0] + h * q_strides[1] + t * q_strides[2] + d];
+            for (int64_t j = 0; j < keys; ++j)
+                for (int64_t d = 0; d < head_dim; ++d) {
+                    kt[d * keys + j] = kf[b * k_strides[0] + h * k_strides[1] + j * k_strides[2] + d];
+                    vm[j * head_dim + d] = vf[b * v_strides[0] + h * v_strides[1] + j * v_strides[2] + d];
+                }
+            kd_matmul_sizes s_qk = {1, length, head_dim, keys};
+            rc = oracle_matmul(KD_F32, qm, kt, scores, &s_qk, 0);
+            if (rc != KD_OK) break;
+            for (int64_t i = 0; i < length; ++i)
+                for (int64_t j = 0; j < keys; ++j) {
+                    const float x = scores[i * keys + j] / scale;
+                    scores[i * keys + j] = j > past + i ? -INFINITY : x;
+                }
+            rc = oracle_softmax_rows(KD_F32, p, scores, length, keys, 0);
+            kd_matmul_sizes s_pv = {1, length, keys, head_dim};
+            if (rc == KD_OK) rc = oracle_matmul(KD_F32, p, vm, o, &s_pv, 0);
+            for (int64_t t = 0; t < length && rc == KD_OK; ++t)
+                for (int64_t d = 0; d < head_dim; ++d)
+                    ((float*)out)[((b * length + t) * heads + h) * head_dim + d] = o[t * head_dim + d];
+        }
+    free(qm); free(kt); free(vm); free(scores); free(p); free(o);
+    return rc;
+}
+
 /* ---- matmul: kernels.inl:136-177 -------------------------------------------------------------- */
 
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,

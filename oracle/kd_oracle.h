@@ -31,6 +31,9 @@ int oracle_causal_attention(int dtype, void* out, void* lse, const void* qkv, in
                             int64_t heads, int64_t head_dim);
 int oracle_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
                                      const void* lse, int64_t batch, int64_t length, int64_t heads, int64_t head_dim);
+int oracle_cached_attention(int dtype, void* out, const void* q, const int64_t* q_strides, const void* k,
+                            const int64_t* k_strides, const void* v, const int64_t* v_strides, int64_t batch,
+                            int64_t heads, int64_t length, int64_t keys, int64_t head_dim);
 int oracle_arg_reduce(int largest, int in_dtype, int64_t* results, const void* data, int64_t chunk_size,
                       int64_t output_count);
 int oracle_cumsum(int in_dtype, void* out, const void* in, int64_t size, int64_t rows);

@@ -245,8 +245,8 @@ namespace {
 // 9 arg_reduce, 10 cumsum_rows, 11 softmax_rows_backward, 12 standardize_rows_backward,
 // 13 reduce_columns, 14 adam_step_many, 15 matmul_strided_heads, 16 layer_norm_rows,
 // 17 layer_norm_rows_backward, 18 matmul_strided_bias, 19 index_bounds, 20 causal_attention,
-// 21 causal_attention_backward, 22 dropout.
-constexpr int kExtensions = 23;
+// 21 causal_attention_backward, 22 dropout, 23 cached_attention.
+constexpr int kExtensions = 24;
 std::atomic<long long> g_extension_calls[kExtensions];
 } // namespace
 
@@ -491,6 +491,16 @@ void causal_attention_backward(DType dtype, std::byte* dqkv, const std::byte* do
     check(oracle_causal_attention_backward(static_cast<int>(dtype), dqkv, dout, qkv, out, lse, batch, length, heads,
                                            head_dim),
           "causal_attention_backward");
+}
+
+void cached_attention(DType dtype, std::byte* out, const std::byte* q, const std::int64_t* q_strides,
+                      const std::byte* k, const std::int64_t* k_strides, const std::byte* v,
+                      const std::int64_t* v_strides, std::int64_t batch, std::int64_t heads, std::int64_t length,
+                      std::int64_t keys, std::int64_t head_dim) {
+    ++g_extension_calls[23];
+    check(oracle_cached_attention(static_cast<int>(dtype), out, q, q_strides, k, k_strides, v, v_strides, batch,
+                                  heads, length, keys, head_dim),
+          "cached_attention");
 }
 
 void cumsum_rows(DType in, std::byte* out, const std::byte* data, std::int64_t size, std::int64_t rows) {

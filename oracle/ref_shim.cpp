@@ -1066,6 +1066,30 @@ int ref_attention_module(int device, int64_t batch, int64_t length, int64_t dim,
     });
 }
 
+// kael's CausalSelfAttention module with a KV cache (reference src/nn/transformer.cpp:103-138)
+// on `device` (0 CPU, 1 the linked device backend), as generation runs it (no gradient):
+// manual_seed(seed), the module for `total` positions, x [B, total, C] uniform in [-1, 1), then
+// forward(x[:, :prompt], &cache) and forward(x[:, t:t+step], &cache) for t = prompt, prompt + step,
+// ... (the last chunk may be shorter). Writes the outputs, concatenated along the positions, to
+// out_cached (B total C) and the cacheless forward of the whole x to out_full.
+int ref_cached_attention_module(int device, int64_t batch, int64_t prompt, int64_t total, int64_t step, int64_t dim,
+                                int64_t heads, uint64_t seed, float* out_cached, float* out_full) {
+    return guarded([&] {
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        kael::manual_seed(seed);
+        kael::nn::CausalSelfAttention attention(dim, heads, total);
+        const kael::Tensor x = (kael::rand({batch, total, dim}) * 2 - 1).to(dev);
+        attention.to(dev);
+        const kael::autograd::NoGradGuard guard;
+        kael::nn::LayerCache cache;
+        std::vector<kael::Tensor> parts{attention.forward(x.slice(1, 0, prompt), &cache)};
+        for (int64_t t = prompt; t < total; t += step)
+            parts.push_back(attention.forward(x.slice(1, t, std::min(total, t + step)), &cache));
+        copy_out(kael::cat(parts, 1).cpu(), out_cached);
+        copy_out(attention.forward(x).cpu(), out_full);
+    });
+}
+
 // kael's LayerNorm module (reference src/nn/layers.cpp:55-68) through its autograd on `device` (0
 // CPU, 1 the linked device backend): weight and bias set from w / b, x [rows, cols] (dtype 0 f32,
 // 1 f64) requires grad, sum(LayerNorm(x) * g).backward(). Writes the output, kael's standardize(x)
@@ -1157,6 +1181,28 @@ int ref_gpt_generate_on(void* handle, int device, const int64_t* prompt, int64_t
         const kael::Tensor ids = host_tensor(prompt, {1, length}, kael::DType::I64).to(dev);
         const auto t0 = std::chrono::steady_clock::now();
         const kael::Tensor seq = kael::nn::generate(model, ids, {.max_new_tokens = new_tokens, .temperature = 0.0});
+        const auto t1 = std::chrono::steady_clock::now();
+        *seconds = std::chrono::duration<double>(t1 - t0).count();
+        copy_out(seq.cpu(), out_tokens);
+        model.to(kael::Device::CPU);
+    });
+}
+
+// kael's nn::generate with sampling (temperature > 0, optional top-k; reference
+// src/nn/transformer.cpp:39-50, 256-295) of a batch-1 prompt on `device`, after
+// kael::manual_seed(seed): the loop of generate with its KV cache, sample_next on the host.
+// Writes the sequence (length + new_tokens ids) and the wall time.
+int ref_gpt_generate_sampled(void* handle, int device, const int64_t* prompt, int64_t length, int64_t new_tokens,
+                             double temperature, int64_t top_k, uint64_t seed, int64_t* out_tokens, double* seconds) {
+    return guarded([&] {
+        auto& model = *static_cast<RefGpt*>(handle)->model;
+        const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
+        model.to(dev);
+        const kael::Tensor ids = host_tensor(prompt, {1, length}, kael::DType::I64).to(dev);
+        kael::manual_seed(seed);
+        const auto t0 = std::chrono::steady_clock::now();
+        const kael::Tensor seq = kael::nn::generate(
+            model, ids, {.max_new_tokens = new_tokens, .temperature = temperature, .top_k = top_k});
         const auto t1 = std::chrono::steady_clock::now();
         *seconds = std::chrono::duration<double>(t1 - t0).count();
         copy_out(seq.cpu(), out_tokens);

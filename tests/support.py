@@ -95,6 +95,8 @@ REF_SIGS = {
     "train_gpt": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                           POINTER(c_double)]),
     "gpt_generate_on": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
+    "gpt_generate_sampled": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_double, c_int64,
+                                     ctypes.c_uint64, c_void_p, POINTER(c_double)]),
     "train_gpt_params": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                  c_void_p, POINTER(c_double)]),
     "gpt_param_total": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
@@ -111,6 +113,8 @@ REF_SIGS = {
     "attention_chain": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "attention_module": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p,
                                  c_void_p]),
+    "cached_attention_module": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64,
+                                        c_void_p, c_void_p]),
     "layer_norm_grads": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_double,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "suite_size": (c_int, []),

@@ -220,3 +220,31 @@ def test_generate_with_on_token_on_the_engine(kael_hip_fused):
         np.testing.assert_array_equal(dev_seq, cpu_seq)
         np.testing.assert_array_equal(dev_seen, cpu_seen)
         assert len(cpu_seen) == stop_after and len(cpu_seq) == 12 + stop_after
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("variant", ["hip", "hip_fused"])
+def test_kael_sampled_generate_with_its_cache_on_the_device(request, variant):
+    """kael's nn::generate with sampling (temperature 0.8, top-k 1, seed 9): its own loop with the KV
+    cache runs on the device (no engine), sample_next on the host. top-k 1 leaves one token with
+    probability 1, so the draw is fixed and the device sequence must equal kael's CPU one. Through
+    the fused build the attention of every cached step is one kd_cached_attention call."""
+    lib = request.getfixturevalue("kael_hip" if variant == "hip" else "kael_hip_fused")
+    lib.ref_set_threads(threads())
+    prompt = np.ascontiguousarray(np.random.default_rng(9).integers(0, VOCAB, 16), np.int64)
+    new = 24
+    seqs, secs = [], []
+    for device in (0, 1):
+        h = kael_model(lib)
+        out, t = np.zeros(len(prompt) + new, np.int64), ctypes.c_double()
+        try:
+            assert lib.ref_gpt_generate_sampled(h, device, prompt.ctypes.data_as(ctypes.c_void_p), len(prompt), new,
+                                                0.8, 1, 9, out.ctypes.data_as(ctypes.c_void_p),
+                                                ctypes.byref(t)) == 0, support.ref_error(lib)
+        finally:
+            lib.ref_gpt_destroy(h)
+        seqs.append(out)
+        secs.append(t.value)
+    np.testing.assert_array_equal(seqs[1], seqs[0])
+    print(f"\nkael nn::generate sampled with its KV cache on the MI355X ({variant}): {new} tokens in "
+          f"{secs[1]:.2f} s = {new / secs[1]:.1f} tokens/s; kael CPU {new / secs[0]:.2f} tokens/s")

@@ -12,6 +12,13 @@ oracle_causal_attention / _backward, reference src/nn/transformer.cpp:114-136) p
 Then kael's CausalSelfAttention module and a small GPT through the fused branch with the oracle as
 the device (oracle/kael_fused.py: the attention as one device call and one backward node for f32
 heads of 64), against kael's CPU path, and the branch's call counters.
+
+The cached restatement (oracle_cached_attention: new queries against the cache's keys and values,
+reference src/nn/transformer.cpp:103-138 with a cache) is pinned to the uncached one, which the
+checks above pin: with no past it is the uncached chain bit for bit; the attention of the last T
+queries against all L keys is bit for bit the last T rows of the full attention over L positions;
+strided views and contiguous copies give the same bits. kael's module with a KV cache (a prompt,
+then single tokens and chunks) through the branch on the oracle device matches kael's CPU path.
 """
 import ctypes
 
@@ -143,3 +150,91 @@ def test_gpt_with_heads_of_64_through_the_fused_branch(kael_oracle_fused):
     np.testing.assert_allclose(dev_l, cpu_l, rtol=1e-4)
     assert after["causal_attention"] - before["causal_attention"] >= steps
     assert after["causal_attention_backward"] - before["causal_attention_backward"] == steps
+
+
+# ---- attention against a KV cache ---------------------------------------------------------------
+
+def qkv_views(qkv, b, t, h, d, start=0):
+    """Pointers and (batch, head, position) strides of the q / k / v per-head views of qkv
+    [b, t, 3, h, d] from position `start` (what selects and transposes give kael)."""
+    base = qkv.ctypes.data + start * 3 * h * d * 4
+    strides = np.array([t * 3 * h * d, d, 3 * h * d], np.int64)
+    return [(base + part * h * d * 4, strides) for part in range(3)]
+
+
+def oracle_cached(oracle, q, k, v, b, h, t, keys, d=64):
+    out = np.zeros((b, t, h * d), np.float32)
+    (qp, qs), (kp, ks), (vp, vs) = q, k, v
+    rc = oracle.oracle_cached_attention(0, P(out), qp, P(qs), kp, P(ks), vp, P(vs), b, h, t, keys, d)
+    assert rc == 0, oracle.oracle_last_error()
+    return out
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (2, 9, 2), (1, 40, 3)], ids=["1x1x1", "2x9x2", "1x40x3"])
+def test_cached_oracle_without_past_is_the_uncached_chain(oracle, shape):
+    b, t, h = shape
+    qkv, dout = inputs(b, t, h, 64)
+    want, _, _ = oracle_attention(oracle, qkv, dout, b, t, h, 64)
+    q, k, v = qkv_views(qkv, b, t, h, 64)
+    np.testing.assert_array_equal(oracle_cached(oracle, q, k, v, b, h, t, t), want)
+
+
+@pytest.mark.parametrize("shape", [(1, 10, 1, 1), (2, 33, 2, 5), (1, 70, 3, 70)], ids=["L10_T1", "L33_T5", "L70_T70"])
+def test_cached_oracle_rows_are_the_full_attentions_last_rows(oracle, shape):
+    b, length, h, t = shape
+    qkv, dout = inputs(b, length, h, 64, seed=11)
+    full, _, _ = oracle_attention(oracle, qkv, dout, b, length, h, 64)
+    q, _, _ = qkv_views(qkv, b, length, h, 64, start=length - t)
+    _, k, v = qkv_views(qkv, b, length, h, 64)
+    got = oracle_cached(oracle, q, k, v, b, h, t, length)
+    np.testing.assert_array_equal(got, full[:, length - t:])
+
+
+def test_cached_oracle_reads_strided_and_contiguous_operands_alike(oracle):
+    b, length, h, t = 2, 21, 3, 4
+    qkv, _ = inputs(b, length, h, 64, seed=17)
+    q, k, v = qkv_views(qkv, b, length, h, 64, start=length - t)
+    _, k, v = qkv_views(qkv, b, length, h, 64)
+    strided = oracle_cached(oracle, q, k, v, b, h, t, length)
+    x = qkv.reshape(b, length, 3, h, 64)
+    kc = np.ascontiguousarray(x[:, :, 1].transpose(0, 2, 1, 3))
+    vc = np.ascontiguousarray(x[:, :, 2].transpose(0, 2, 1, 3))
+    cs = np.array([h * length * 64, length * 64, 64], np.int64)
+    contiguous = oracle_cached(oracle, q, (kc.ctypes.data, cs), (vc.ctypes.data, cs), b, h, t, length)
+    np.testing.assert_array_equal(strided, contiguous)
+
+
+def test_cached_oracle_rejects_bad_shapes(oracle):
+    x = np.zeros(64 * 3 * 4, np.float32)
+    s = np.array([0, 0, 64], np.int64)
+    out = np.zeros(64 * 4, np.float32)
+    assert oracle.oracle_cached_attention(1, P(out), P(x), P(s), P(x), P(s), P(x), P(s), 1, 1, 1, 1, 64) != 0
+    assert oracle.oracle_cached_attention(0, P(out), P(x), P(s), P(x), P(s), P(x), P(s), 1, 1, 2, 1, 64) != 0
+
+
+def cached_module(lib, device, shape, seed=6):
+    b, prompt, total, step, c, h = shape
+    cached, full = np.empty((b, total, c), np.float32), np.empty((b, total, c), np.float32)
+    assert lib.ref_cached_attention_module(device, b, prompt, total, step, c, h, seed, P(cached), P(full)) == 0, \
+        support.ref_error(lib)
+    return cached, full
+
+
+@pytest.mark.parametrize("shape, fused", [((1, 5, 12, 1, 128, 2), True), ((2, 3, 20, 4, 64, 1), True),
+                                          ((1, 4, 9, 1, 32, 2), False)],
+                         ids=["prompt5_tokens", "batch2_chunks4", "heads_of_16"])
+def test_cached_module_through_the_branch(kael_oracle_fused, shape, fused):
+    """kael's CausalSelfAttention with a KV cache (a prompt, then single tokens or chunks; no
+    gradient) on the oracle device through the cached branch, against kael's CPU path with the
+    cache; kael's own cached outputs against its cacheless forward on the CPU; the branch runs once
+    per forward call (heads of 16 keep kael's ops)."""
+    lib = kael_oracle_fused
+    b, prompt, total, step = shape[:4]
+    cpu_cached, cpu_full = cached_module(lib, 0, shape)
+    close(cpu_cached, cpu_full.astype(np.float64), "kael cached vs cacheless")
+    before = calls(lib)
+    dev_cached, _ = cached_module(lib, 1, shape)
+    after = calls(lib)
+    close(dev_cached, cpu_cached.astype(np.float64), "cached")
+    forwards = 1 + -(-(total - prompt) // step)
+    assert after["cached_attention"] - before["cached_attention"] == (forwards if fused else 0)

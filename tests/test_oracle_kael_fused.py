@@ -23,7 +23,7 @@ EXTENSIONS = ["softmax_rows", "standardize_rows", "cross_entropy_rows", "cross_e
               "matmul_strided", "adam_step", "sgd_step", "reduce_extra", "arg_reduce", "cumsum_rows",
               "softmax_rows_backward", "standardize_rows_backward", "reduce_columns", "adam_step_many",
               "matmul_strided_heads", "layer_norm_rows", "layer_norm_rows_backward", "matmul_strided_bias",
-              "index_bounds", "causal_attention", "causal_attention_backward"]
+              "index_bounds", "causal_attention", "causal_attention_backward", "dropout", "cached_attention"]
 # The entry points a char-GPT training step reaches (forward, backward, Adam over the parameter list;
 # layer_norm_rows(_backward): every LayerNorm; reduce_columns: the bias gradients summed over every
 # token; matmul_strided_heads: the attention products over per-head views; matmul_strided_bias: every
