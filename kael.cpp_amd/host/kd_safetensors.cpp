@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cstring>
 #include <limits>
+#include <string_view>
 #include <utility>
 
 namespace kd::safetensors {
@@ -555,36 +556,42 @@ void File::to_f32(const Entry& e, float* out, bool transpose) const {
         }
 }
 
+// The Hugging Face GPT-2 checkpoint's names against kael's module names (the mapping of reference
+// src/nn/transformer.cpp:54-91, a format): an optional "transformer." prefix is dropped, a name
+// starting with a top-level entry's `from` has it replaced, and a block's name ("h.<i>." ->
+// "blocks.<i>.") then has each sub-module's first occurrence renamed.
+struct Rename {
+    std::string_view from, to;
+};
+constexpr Rename kTopLevel[] = {
+    {"wte.", "token_embedding."}, {"wpe.", "position_embedding."}, {"ln_f.", "ln_final."}, {"h.", "blocks."}};
+constexpr Rename kInBlock[] = {{".ln_1.", ".ln1."},           {".ln_2.", ".ln2."},
+                               {".attn.c_attn.", ".attn.qkv."}, {".attn.c_proj.", ".attn.proj."},
+                               {".mlp.c_fc.", ".mlp.fc1."},     {".mlp.c_proj.", ".mlp.fc2."}};
+// The four Conv1D modules (kael's names), whose weights the checkpoint stores [in, out].
+constexpr std::string_view kConv1d[] = {".attn.qkv.", ".attn.proj.", ".mlp.fc1.", ".mlp.fc2."};
+
 std::string translated_gpt2_name(std::string name) {
-    const std::string prefix = "transformer.";
-    if (name.rfind(prefix, 0) == 0) name.erase(0, prefix.size());
-    const auto replace = [&](const std::string& from, const std::string& to) {
-        const auto at = name.find(from);
-        if (at != std::string::npos) name.replace(at, from.size(), to);
-    };
-    if (name.rfind("wte.", 0) == 0) {
-        replace("wte.", "token_embedding.");
-    } else if (name.rfind("wpe.", 0) == 0) {
-        replace("wpe.", "position_embedding.");
-    } else if (name.rfind("ln_f.", 0) == 0) {
-        replace("ln_f.", "ln_final.");
-    } else if (name.rfind("h.", 0) == 0) {
-        name.replace(0, 2, "blocks.");
-        replace(".ln_1.", ".ln1.");
-        replace(".ln_2.", ".ln2.");
-        replace(".attn.c_attn.", ".attn.qkv.");
-        replace(".attn.c_proj.", ".attn.proj.");
-        replace(".mlp.c_fc.", ".mlp.fc1.");
-        replace(".mlp.c_proj.", ".mlp.fc2.");
+    constexpr std::string_view prefix = "transformer.";
+    if (name.starts_with(prefix)) name.erase(0, prefix.size());
+    for (const Rename& top : kTopLevel) {
+        if (!name.starts_with(top.from)) continue;
+        name.replace(0, top.from.size(), top.to);
+        if (top.from == "h.") {
+            for (const Rename& sub : kInBlock) {
+                const auto at = name.find(sub.from);
+                if (at != std::string::npos) name.replace(at, sub.from.size(), sub.to);
+            }
+        }
+        break;
     }
     return name;
 }
 
 bool stored_transposed(const std::string& name) {
-    const bool conv1d = name.find(".attn.qkv.") != std::string::npos || name.find(".attn.proj.") != std::string::npos ||
-                        name.find(".mlp.fc1.") != std::string::npos || name.find(".mlp.fc2.") != std::string::npos;
-    const std::string suffix = ".weight";
-    return conv1d && name.size() >= suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0;
+    bool conv1d = false;
+    for (const std::string_view module : kConv1d) conv1d = conv1d || name.find(module) != std::string::npos;
+    return conv1d && name.ends_with(".weight");
 }
 
 }  // namespace kd::safetensors
