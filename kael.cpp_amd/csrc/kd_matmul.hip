@@ -557,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_rowmajor_kernel(const float
 // order and results are those of mfma_f32_rowmajor_kernel (bit for bit). `lda` / `ldb` / `ldo`
 // are the strides between consecutive rows of the stored operands: of A's k (AT) or m rows, of
 // B's n (BT) or k rows, of the output's m rows.
-template <bool AT, bool BT, bool Bias = false>
+template <bool AT, bool BT, bool Bias = false, bool Deep = false>
 __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* __restrict__ a,
                                                                   const float* __restrict__ b,
                                                                   float* __restrict__ out, int M, int N, int K,
@@ -620,12 +620,11 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* _
     }
     const int g_step = loads_a ? (AT ? kBK * lda : kBK) : (BT ? kBK : kBK * ldb);
     const float* src = loads_a ? a : b;
-    f4 r[4];
-    const auto fetch = [&](int ks) {
+    const auto fetch = [&](f4 (&r)[4], int ks) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const f4*>(src + g_off + ks * g_step + j * g_row);
     };
-    const auto stash = [&](int buf) {
+    const auto stash = [&](const f4 (&r)[4], int buf) {
         if (loads_a) {
             if (AT) {
                 // r[j][e] = A[m0 + 4*(u%32) + e][4*(u/32) + j]
@@ -660,15 +659,7 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* _
             const int row = wm * 64 + i * 32 + li;
             a_rd[i][h] = row * kAld + aswz(row, 8 * h + 4 * lh);
         }
-    fetch(0);
-    stash(0);
-    __syncthreads();
-
-    const int ksteps = K / kBK;
-    for (int ks = 0; ks < ksteps; ++ks) {
-        const int cur = ks & 1;
-        const bool more = ks + 1 < ksteps;
-        if (more) fetch(ks + 1);
+    const auto step = [&](int cur) {
         const float* as = As[cur];
         const float* bs = Bs[cur];
         __builtin_amdgcn_s_setprio(1);
@@ -691,8 +682,43 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_trans_kernel(const float* _
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s4], bf[j][s4], acc[i][j], 0, 0, 0);
         }
         __builtin_amdgcn_s_setprio(0);
-        if (more) stash(cur ^ 1);
+    };
+    const int ksteps = K / kBK;
+    if constexpr (Deep) {
+        // Grids of at most one workgroup per CU: a wave per SIMD cannot hide one step's load
+        // latency behind other waves, so the global loads run two K steps ahead (step s fetched
+        // into register set s % 2 at the start of step s - 2, written to LDS buffer s % 2 at the
+        // end of step s - 1). Same MFMA order, same results.
+        f4 r0[4], r1[4];
+        fetch(r0, 0);
+        if (ksteps > 1) fetch(r1, 1);
+        stash(r0, 0);
         __syncthreads();
+        int ks = 0;
+        for (; ks + 1 < ksteps; ks += 2) {
+            if (ks + 2 < ksteps) fetch(r0, ks + 2);
+            step(0);
+            stash(r1, 1);
+            __syncthreads();
+            if (ks + 3 < ksteps) fetch(r1, ks + 3);
+            step(1);
+            if (ks + 2 < ksteps) stash(r0, 0);
+            __syncthreads();
+        }
+        if (ks < ksteps) step(0);  // an odd step count's last step
+    } else {
+        f4 r[4];
+        fetch(r, 0);
+        stash(r, 0);
+        __syncthreads();
+        for (int ks = 0; ks < ksteps; ++ks) {
+            const int cur = ks & 1;
+            const bool more = ks + 1 < ksteps;
+            if (more) fetch(r, ks + 1);
+            step(cur);
+            if (more) stash(r, cur ^ 1);
+            __syncthreads();
+        }
     }
 
 #pragma unroll
@@ -787,12 +813,11 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
     }
     const int g_step = loads_a ? (AT ? kT64K * lda : kT64K) : (BT ? kT64K : kT64K * ldb);
     const float* src = loads_a ? a : b;
-    f4 r[4];
-    const auto fetch = [&](int ks) {
+    const auto fetch = [&](f4 (&r)[4], int ks) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const f4*>(src + g_off + ks * g_step + j * g_row);
     };
-    const auto stash = [&](int buf) {
+    const auto stash = [&](const f4 (&r)[4], int buf) {
         if (loads_a) {
             if (AT) {
                 // r[j][e] = A[m0 + 4*(u%16) + e][4*(u/16) + j]
@@ -823,15 +848,7 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
     int a_rd[kT64K / 8];
 #pragma unroll
     for (int h = 0; h < kT64K / 8; ++h) a_rd[h] = arow * kT64Ald + aswz(arow, 8 * h + 4 * lh);
-    fetch(0);
-    stash(0);
-    __syncthreads();
-
-    const int ksteps = K / kT64K;
-    for (int ks = 0; ks < ksteps; ++ks) {
-        const int cur = ks & 1;
-        const bool more = ks + 1 < ksteps;
-        if (more) fetch(ks + 1);
+    const auto step = [&](int cur) {
         const float* as = As[cur];
         const float* bs = Bs[cur];
 #pragma unroll
@@ -843,9 +860,29 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s4], bf[s4], acc, 0, 0, 0);
         }
-        if (more) stash(cur ^ 1);
+    };
+    // Global loads run two K steps ahead of the MFMAs: a grid of at most a few workgroups per CU
+    // has too few waves to cover one step's load latency with the others' work. Step s is
+    // fetched into register set s % 2 at the start of step s - 2 and written to LDS buffer s % 2
+    // at the end of step s - 1.
+    const int ksteps = K / kT64K;
+    f4 r0[4], r1[4];
+    fetch(r0, 0);
+    if (ksteps > 1) fetch(r1, 1);
+    stash(r0, 0);
+    __syncthreads();
+    int ks = 0;
+    for (; ks + 1 < ksteps; ks += 2) {
+        if (ks + 2 < ksteps) fetch(r0, ks + 2);
+        step(0);
+        stash(r1, 1);
+        __syncthreads();
+        if (ks + 3 < ksteps) fetch(r1, ks + 3);
+        step(1);
+        if (ks + 2 < ksteps) stash(r0, 0);
         __syncthreads();
     }
+    if (ks < ksteps) step(0);  // an odd step count's last step
 
     const int col = n0 + wn * 32 + li;
     if (bs.bias == nullptr) {
@@ -1237,6 +1274,23 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
     return true;
 }
 
+// mfma_f32_trans_kernel on `grid`: the instantiation that keeps two K steps of loads in flight
+// where the grid leaves at most two workgroups per CU (C4's products: 192-256 workgroups, one wave
+// per SIMD), the one-step pipeline (fewer registers, four waves per SIMD) otherwise.
+template <bool AT, bool BT, bool Bias = false>
+void launch_trans(dim3 grid, const float* a, const float* b, float* out, int64_t M, int64_t N, int64_t K, int64_t lda,
+                  int64_t ldb, int64_t ldo, const BatchStrides& bs) {
+    const int64_t groups = int64_t{grid.x} * grid.y * grid.z;
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    const int la = static_cast<int>(lda), lb = static_cast<int>(ldb), lo = static_cast<int>(ldo);
+    if (groups <= 2 * int64_t{compute_units()})
+        hipLaunchKernelGGL((mfma_f32_trans_kernel<AT, BT, Bias, true>), grid, dim3(kThreads), 0, stream(), a, b, out, m,
+                           n, k, la, lb, lo, bs);
+    else
+        hipLaunchKernelGGL((mfma_f32_trans_kernel<AT, BT, Bias, false>), grid, dim3(kThreads), 0, stream(), a, b, out, m,
+                           n, k, la, lb, lo, bs);
+}
+
 template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, float* out, const MatmulArgs& p) {
     const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN);
     if (p.batches > 65535) return fail(KD_E_INVALID, "kd_matmul: too many batches");
@@ -1283,15 +1337,9 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
             // each), which measured ~1 % faster than mfma_f32_rowmajor_kernel at 4096^3 with
             // bit-identical results. The bounds checked above cover its 32-bit offsets.
             if (p.bias != nullptr)
-                hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false, true>), grid, dim3(kThreads), 0, stream(), a, b,
-                                   out, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                                   static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r),
-                                   batch_strides(p));
+                launch_trans<false, false, true>(grid, a, b, out, p.M, p.N, p.K, p.sa.r, p.sb.r, p.so.r, batch_strides(p));
             else
-                hipLaunchKernelGGL((mfma_f32_trans_kernel<false, false>), grid, dim3(kThreads), 0, stream(), a, b, out,
-                                   static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                                   static_cast<int>(p.sa.r), static_cast<int>(p.sb.r), static_cast<int>(p.so.r),
-                                   batch_strides(p));
+                launch_trans<false, false>(grid, a, b, out, p.M, p.N, p.K, p.sa.r, p.sb.r, p.so.r, batch_strides(p));
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
@@ -1327,12 +1375,9 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                         Workspace ws;  // held until split_sum_kernel is enqueued
                         if (int rc = workspace(ws, static_cast<size_t>(splits * per) * sizeof(float))) return rc;
                         const int64_t kc = p.K / splits;
-                        hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>),
-                                           dim3(static_cast<uint32_t>(flat_tiles), static_cast<uint32_t>(splits)),
-                                           dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr),
-                                           static_cast<int>(rows), static_cast<int>(p.N), static_cast<int>(kc),
-                                           static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.N),
-                                           batch_strides(at ? kc * lda : kc, bt ? kc : kc * ldb, per));
+                        launch_trans<at, bt>(dim3(static_cast<uint32_t>(flat_tiles), static_cast<uint32_t>(splits)), a, b,
+                                             static_cast<float*>(ws.ptr), rows, p.N, kc, lda, ldb, p.N,
+                                             batch_strides(at ? kc * lda : kc, bt ? kc : kc * ldb, per));
                         KD_LAUNCH_CHECK();
                         MatmulArgs flat = p;
                         flat.batches = 1;
@@ -1346,15 +1391,9 @@ template <int AMode, int BMode> int launch_mfma(const float* a, const float* b, 
                 }
             }
             if (p.bias != nullptr)
-                hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt, true>), grid, dim3(kThreads), 0, stream(), a, b, out,
-                                   static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                                   static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
-                                   batch_strides(p));
+                launch_trans<at, bt, true>(grid, a, b, out, p.M, p.N, p.K, lda, ldb, p.so.r, batch_strides(p));
             else
-                hipLaunchKernelGGL((mfma_f32_trans_kernel<at, bt>), grid, dim3(kThreads), 0, stream(), a, b, out,
-                                   static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),
-                                   static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
-                                   batch_strides(p));
+                launch_trans<at, bt>(grid, a, b, out, p.M, p.N, p.K, lda, ldb, p.so.r, batch_strides(p));
             KD_LAUNCH_CHECK();
             return KD_OK;
         }
