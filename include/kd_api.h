@@ -524,13 +524,13 @@ int kd_gpt_load_safetensors(void* handle, const char* path);
 int kd_safetensors_tensor(const char* path, const char* name, float* out, int64_t capacity, int64_t* shape,
                           int32_t* dims);
 /* Runs the prompt through the model from position 0 with an empty KV cache; the last position's
- * greedy token becomes the first generated token. Clears any previous sequence. A prompt longer
+ * picked token (greedy or sampled, kd_gpt_set_sampling) becomes the first generated token. Clears any previous sequence. A prompt longer
  * than max_positions runs its last max_positions tokens, as nn::generate does (reference
  * src/nn/transformer.cpp:270-284). By default all positions pass each layer together (GEMMs on
  * the matrix cores, causal attention); KD_GPT_STEPWISE_PREFILL runs them as cached single-token
  * steps. */
 int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length);
-/* Generates `count` more tokens greedily (reference nn::generate with use_cache, temperature 0):
+/* Generates `count` more tokens, greedily or sampled (reference nn::generate with use_cache):
  * one cached step each while the KV cache has room; once it holds max_positions positions, each
  * token clears it and reruns the sequence's last max_positions tokens from position 0, as
  * nn::generate does. `tokens` (host, may be NULL) receives the `count` new ids. */
@@ -545,6 +545,20 @@ int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* lengt
  * after kd_gpt_prefill, the last step's after kd_gpt_decode. No reference counterpart (kael's
  * generate returns tokens only); for parity checks of the prefill paths. */
 int kd_gpt_logits(void* handle, float* logits);
+/* The pick of every following prefill and decode step: temperature 0 is the greedy pick (the
+ * default); temperature > 0 with 0 < top_k < vocab_size is kael's sample_next (reference
+ * src/nn/transformer.cpp:39-50: logits / temperature, the top_k largest kept, softmax,
+ * multinomial of one sample, src/random.cpp:106-160) on the device, drawing the next uniform
+ * given by kd_gpt_set_uniforms for each sampled token. Without a top-k, kael's multinomial sums
+ * every probability of the vocabulary in sequence: KD_E_UNSUPPORTED (kael's own loop samples). */
+int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k);
+/* The uniform draws in [0, 1) for the next `count` sampled picks, in order (at most
+ * max_positions + 1): what uniform_real_distribution<double>(0, 1) on kael's generator returns
+ * for each multinomial sample (one draw per sampled token). A sampled pick with no draw left
+ * fails the call that ran it. No reference counterpart: kael draws inside multinomial. */
+int kd_gpt_set_uniforms(void* handle, const double* uniforms, int64_t count);
+/* How many of the uniforms given by kd_gpt_set_uniforms the sampled picks have used. */
+int kd_gpt_draws_used(void* handle, int64_t* used);
 
 /* ---- measurement helpers (no reference counterpart; used by the bench) -- */
 

@@ -50,6 +50,17 @@ struct Step {
     int64_t forced;  // positions < forced take their token from `seq` (teacher forcing)
 };
 
+// The pick's mode: greedy (top_k 0) or kael's sample_next with a temperature and a top-k
+// (reference src/nn/transformer.cpp:39-50), one uniform draw per sampled token taken from
+// `uniforms` in order. `error` is set when a pick finds a non-finite logit or no draw left.
+struct Sampler {
+    float temperature;  // kael's scalar in the logits' dtype
+    int32_t error;
+    int64_t top_k;
+    int64_t draw;       // next draw
+    int64_t draws;      // draws uploaded
+};
+
 // ---- kernels -------------------------------------------------------------------------------
 
 // Whole-workgroup LayerNorm of x[0, d) into h, d <= 4 * kThreads: one read of x into registers,
@@ -325,7 +336,7 @@ struct GemvArgs {
     float* kcache;
     float* vcache;
     int64_t d, head_dim, max_positions;
-    // head_kernel: per-workgroup argmax partials (argmax_final_kernel picks the winner)
+    // head_kernel: per-workgroup argmax partials (pick_kernel picks the winner)
     float* best_v;
     int64_t* best_i;
     Step* st;
@@ -478,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 }
 
 // Logits of the tied head, logits[n] = wte[n, :] . LayerNorm_f(x), and each workgroup's best
-// row (first maximum, first NaN; reference src/ops/reduce.cpp:236-254) for argmax_final_kernel.
+// row (first maximum, first NaN; reference src/ops/reduce.cpp:236-254) for pick_kernel.
 // A fixed grid of 4 workgroups per CU (its occupancy at 108 VGPRs) streams the [vocab, d] table:
 // each wave takes row pairs p, p + stride, ... and issues the next pair's loads before the
 // current pair's dot products, so every wave keeps two pairs in flight. The final LayerNorm is
@@ -590,18 +601,187 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
     }
 }
 
-// Picks the greedy token among the head's workgroup partials, appends it to the sequence unless
-// the next position is teacher-forced, and advances the position. One workgroup of 1024 lanes:
-// GPT-2's 6283 partials take 7 loads per lane (4.7 us less per token than with 256 lanes).
+// Picks the next token, appends it to the sequence unless the next position is teacher-forced,
+// and advances the position. One workgroup of 1024 lanes.
+//   Greedy (sampler top_k 0): the first maximum among the head's workgroup partials (GPT-2's
+//   6283 partials take 7 loads per lane).
+//   Sampled: kael's sample_next (reference src/nn/transformer.cpp:39-50) and multinomial
+//   (src/random.cpp:106-160) for 0 < top_k < vocab: x = logits / temperature (f32 division);
+//   the k-th largest x by a radix select over order-preserving 32-bit keys (four 8-bit digits,
+//   per-wave histograms); the kept entries (x >= the k-th largest: masked_fill's complement)
+//   listed in index order; then, in one lane and in kael's order, softmax's e = exp(x - max) with
+//   the sum in double rounded to f32, p = e / sum, the cumulative double sum of p, point = u * sum,
+//   the first kept entry whose cumulative sum exceeds the point (upper_bound; the masked entries add
+//   zeros, which leave every partial sum unchanged), or else the last kept entry with p > 0.
 constexpr int kPickThreads = 1024;
+constexpr int kPickWaves = kPickThreads / 64;
 
-__global__ __launch_bounds__(kPickThreads) void argmax_final_kernel(Step* st, int64_t* seq, const float* pv,
-                                                                    const int64_t* pi, int64_t parts) {
-    __shared__ float bv[kPickThreads / 64];
-    __shared__ int64_t bi[kPickThreads / 64];
+__device__ __forceinline__ uint32_t order_key(float x) {
+    const uint32_t b = __float_as_uint(x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+struct PickArgs {
+    Step* st;
+    int64_t* seq;
+    const float* pv;
+    const int64_t* pi;
+    int64_t parts;
+    const float* logits;
+    int64_t vocab;
+    Sampler* sp;
+    const double* uniforms;
+    int32_t* kept;   // [vocab] scratch: kept indices in index order
+    float* kept_e;   // [vocab] scratch: their exponentials
+};
+
+// Inclusive prefix sum of v over the workgroup's first `n` lanes (n a multiple of 64, at most
+// kPickThreads); every thread of the workgroup must call it.
+__device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int n, int64_t* wave_totals) {
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t o = __shfl_up(v, off);
+        if (lane >= off) v += o;
+    }
+    if (lane == 63 && tid < n) wave_totals[wave] = v;
+    __syncthreads();
+    int64_t before = 0;
+    for (int w = 0; w < wave && w < n / 64; ++w) before += wave_totals[w];
+    __syncthreads();
+    return v + before;
+}
+
+__device__ void sample_pick(const PickArgs& a, int64_t& token) {
+    __shared__ uint32_t hist[kPickWaves][256];
+    __shared__ int64_t wave_totals[kPickWaves];
+    __shared__ uint32_t wmax[kPickWaves];
+    __shared__ int32_t bad[kPickWaves];
+    __shared__ uint32_t chosen;
+    __shared__ int64_t remaining;
+    __shared__ int64_t total_kept;
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int64_t V = a.vocab;
+    const float temp = a.sp->temperature;
+    const auto x_of = [&](int64_t i) { return __fdiv_rn(a.logits[i], temp); };
+    if (tid == 0) remaining = a.sp->top_k;
+    uint32_t prefix = 0, mask = 0, kmax = 0;
+    int32_t nonfinite = 0;
+    // radix select of the k-th largest key, one 8-bit digit per pass from the top
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = lane; b < 256; b += 64) hist[wave][b] = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < V; i += kPickThreads) {
+            const float x = x_of(i);
+            const uint32_t key = order_key(x);
+            if (shift == 24) {
+                kmax = max(kmax, key);
+                nonfinite |= !isfinite(x);
+            }
+            if ((key & mask) == prefix) atomicAdd(&hist[wave][(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        // the digit: the bin b whose count from the top reaches the remaining rank
+        const int b = 255 - tid;  // lanes 0..255 take the bins from the top
+        int64_t n = 0;
+        if (tid < 256)
+            for (int w = 0; w < kPickWaves; ++w) n += hist[w][b];
+        const int64_t need = remaining;  // read before the scan's barriers; written after them
+        const int64_t from_top = block_inclusive_scan(tid < 256 ? n : 0, 256, wave_totals);
+        if (tid < 256 && from_top >= need && from_top - n < need) {
+            chosen = static_cast<uint32_t>(b);
+            remaining = need - (from_top - n);
+        }
+        __syncthreads();
+        prefix |= chosen << shift;
+        mask |= 0xffu << shift;
+    }
+    // the largest key and whether any x is not finite
+    for (int off = 32; off > 0; off >>= 1) {
+        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), off)));
+        nonfinite |= __shfl_xor(nonfinite, off);
+    }
+    if (lane == 0) {
+        wmax[wave] = kmax;
+        bad[wave] = nonfinite;
+    }
+    __syncthreads();
+    kmax = wmax[0];
+    nonfinite = bad[0];
+    for (int w = 1; w < kPickWaves; ++w) {
+        kmax = max(kmax, wmax[w]);
+        nonfinite |= bad[w];
+    }
+    const uint32_t kth = prefix;
+    // kept entries (x >= the k-th largest) in index order: thread t lists its contiguous chunk's
+    const int64_t chunk = (V + kPickThreads - 1) / kPickThreads;
+    const int64_t lo = min(V, tid * chunk), hi = min(V, lo + chunk);
+    int64_t mine = 0;
+    for (int64_t i = lo; i < hi; ++i) mine += order_key(x_of(i)) >= kth;
+    const int64_t through = block_inclusive_scan(mine, kPickThreads, wave_totals);
+    if (tid == kPickThreads - 1) total_kept = through;
+    int64_t at = through - mine;
+    for (int64_t i = lo; i < hi; ++i)
+        if (order_key(x_of(i)) >= kth) a.kept[at++] = static_cast<int32_t>(i);
+    __syncthreads();
+    if (tid != 0) return;
+    Sampler& sp = *a.sp;
+    if (nonfinite || sp.draw >= sp.draws) {
+        sp.error = nonfinite ? 1 : 2;
+        token = 0;
+        return;
+    }
+    const double u = a.uniforms[sp.draw++];
+    const float mx = key_value(kmax);
+    const int64_t m = total_kept;
+    // softmax over the kept entries as kael's row softmax (src/ops/nn.cpp:60-71): f32
+    // exponentials, their sum in double in index order, rounded to f32, each divided by it
+    double sum = 0.0;
+    for (int64_t r = 0; r < m; ++r) {
+        const float e = expf(x_of(a.kept[r]) - mx);
+        a.kept_e[r] = e;
+        sum += static_cast<double>(e);
+    }
+    const float denominator = static_cast<float>(sum);
+    // multinomial (src/random.cpp:143-151): the cumulative sum in double, point = u * total,
+    // upper_bound, and the step back to a positive weight when the point is past every sum
+    double cumulative = 0.0;
+    for (int64_t r = 0; r < m; ++r) cumulative += static_cast<double>(__fdiv_rn(a.kept_e[r], denominator));
+    const double point = u * cumulative;
+    double run = 0.0;
+    int64_t pick = -1, last_positive = a.kept[0];
+    for (int64_t r = 0; r < m; ++r) {
+        const float p = __fdiv_rn(a.kept_e[r], denominator);
+        run += static_cast<double>(p);
+        if (p > 0.f) last_positive = a.kept[r];
+        if (run > point) {
+            pick = a.kept[r];
+            break;
+        }
+    }
+    token = pick >= 0 ? pick : last_positive;
+}
+
+__global__ __launch_bounds__(kPickThreads) void pick_kernel(PickArgs a) {
+    __shared__ float bv[kPickWaves];
+    __shared__ int64_t bi[kPickWaves];
+    if (a.sp->top_k > 0) {
+        int64_t token = 0;
+        sample_pick(a, token);
+        if (threadIdx.x == 0) {
+            const int64_t pos = a.st->pos;
+            if (pos + 1 >= a.st->forced) a.seq[pos + 1] = token;
+            a.st->pos = pos + 1;
+        }
+        return;
+    }
     Best r{-INFINITY, INT64_MAX};
-    for (int64_t i = threadIdx.x; i < parts; i += kPickThreads) {
-        Best o{pv[i], pi[i]};
+    for (int64_t i = threadIdx.x; i < a.parts; i += kPickThreads) {
+        Best o{a.pv[i], a.pi[i]};
         if (better(o, r)) r = o;
     }
     r = wave_best(r);
@@ -612,13 +792,13 @@ __global__ __launch_bounds__(kPickThreads) void argmax_final_kernel(Step* st, in
     __syncthreads();
     if (threadIdx.x == 0) {
         Best w{bv[0], bi[0]};
-        for (int k = 1; k < kPickThreads / 64; ++k) {
+        for (int k = 1; k < kPickWaves; ++k) {
             Best o{bv[k], bi[k]};
             if (better(o, w)) w = o;
         }
-        const int64_t pos = st->pos;
-        if (pos + 1 >= st->forced) seq[pos + 1] = w.i;
-        st->pos = pos + 1;
+        const int64_t pos = a.st->pos;
+        if (pos + 1 >= a.st->forced) a.seq[pos + 1] = w.i;
+        a.st->pos = pos + 1;
     }
 }
 
@@ -887,6 +1067,11 @@ struct Engine {
     int64_t* pi = nullptr;
     int64_t* seq = nullptr;
     Step* st = nullptr;
+    Sampler* sp = nullptr;       // the pick's mode and draws (device)
+    double* uniforms = nullptr;  // [max_positions + 1] draws for sampled picks
+    int32_t* kept = nullptr;     // [vocab] sampling scratch
+    float* kept_e = nullptr;     // [vocab]
+    Sampler host_sp{0.f, 0, 0, 0, 0};
     hipGraphExec_t graph = nullptr;
     int64_t host_pos = 0;     // mirror of st->pos: positions in the KV cache
     std::vector<int64_t> history;  // the whole sequence so far (prompt + generated), host copy
@@ -912,6 +1097,10 @@ struct Engine {
         a.max_positions = cfg.max_positions;
         a.st = st;
         return a;
+    }
+
+    PickArgs pick_args() const {
+        return PickArgs{st, seq, pv, pi, head_groups(), logits, cfg.vocab_size, sp, uniforms, kept, kept_e};
     }
 
     // Workgroups of head_kernel: 4 per CU, fewer when the vocabulary has fewer row pairs than
@@ -1002,7 +1191,7 @@ struct Engine {
         head.best_i = pi;
         const int64_t parts = head_groups();
         hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
-        hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kPickThreads), 0, s, st, seq, pv, pi, parts);
+        hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kPickThreads), 0, s, pick_args());
         return KD_OK;
     }
 
@@ -1161,7 +1350,7 @@ struct Engine {
         head.best_i = pi;
         const int64_t parts = head_groups();
         hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
-        hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kPickThreads), 0, s, st, seq, pv, pi, parts);
+        hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kPickThreads), 0, s, pick_args());
         KD_LAUNCH_CHECK();
         KD_HIP(hipStreamSynchronize(s));
         host_pos = T;
@@ -1192,8 +1381,19 @@ struct Engine {
         return KD_OK;
     }
 
-    // `count` greedy tokens: cached single-token steps while the cache has room, then one
-    // window rerun per token.
+    // After picks in sampling mode: the error a pick recorded, if any.
+    int check_sampler() {
+        if (host_sp.top_k == 0) return KD_OK;
+        Sampler now{};
+        KD_HIP(hipMemcpy(&now, sp, sizeof now, hipMemcpyDeviceToHost));
+        if (now.error == 1) return fail(KD_E_INVALID, "kd_gpt: a sampled pick met a non-finite logit");
+        if (now.error == 2)
+            return fail(KD_E_INVALID, "kd_gpt: a sampled pick found no uniform draw left (kd_gpt_set_uniforms)");
+        return KD_OK;
+    }
+
+    // `count` tokens (greedy, or sampled as set by kd_gpt_set_sampling): cached single-token
+    // steps while the cache has room, then one window rerun per token.
     int generate(int64_t count) {
         int64_t produced = 0;
         while (produced < count) {
@@ -1225,7 +1425,9 @@ struct Engine {
                           static_cast<void*>(x), static_cast<void*>(q), static_cast<void*>(partials.m),
                           static_cast<void*>(partials.l), static_cast<void*>(partials.acc),
                           static_cast<void*>(f), static_cast<void*>(logits), static_cast<void*>(pv),
-                          static_cast<void*>(pi), static_cast<void*>(seq), static_cast<void*>(st)})
+                          static_cast<void*>(pi), static_cast<void*>(seq), static_cast<void*>(st),
+                          static_cast<void*>(sp), static_cast<void*>(uniforms), static_cast<void*>(kept),
+                          static_cast<void*>(kept_e)})
             if (ptr) (void)hipFree(ptr);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -1309,6 +1511,11 @@ int create(Engine& e, const kd_gpt_config& c) {
 
     if (int rc = alloc(&e.seq, c.max_positions + 1)) return rc;
     if (int rc = alloc(&e.st, 1)) return rc;
+    if (int rc = alloc(&e.sp, 1)) return rc;
+    if (int rc = alloc(&e.uniforms, c.max_positions + 1)) return rc;
+    if (int rc = alloc(&e.kept, c.vocab_size)) return rc;
+    if (int rc = alloc(&e.kept_e, c.vocab_size)) return rc;
+    KD_HIP(hipMemcpy(e.sp, &e.host_sp, sizeof(Sampler), hipMemcpyHostToDevice));  // greedy
     return KD_OK;
 }
 
@@ -1439,7 +1646,8 @@ int kd_gpt_prefill(void* handle, const int64_t* prompt, int64_t length) {
         if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab_size) return fail(KD_E_INVALID, "kd_gpt_prefill: token id out of range");
     if (int rc = e->ready()) return rc;
     e->history.assign(prompt, prompt + length);
-    return e->run_window();
+    if (int rc = e->run_window()) return rc;
+    return e->check_sampler();
 }
 
 int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens) {
@@ -1447,6 +1655,7 @@ int kd_gpt_decode(void* handle, int64_t count, int64_t* tokens) {
     if (e == nullptr || count < 0) return fail(KD_E_INVALID, "kd_gpt_decode: bad arguments");
     if (e->history.empty()) return fail(KD_E_INVALID, "kd_gpt_decode: call kd_gpt_prefill first");
     if (int rc = e->generate(count)) return rc;
+    if (int rc = e->check_sampler()) return rc;
     if (tokens != nullptr && count > 0)
         std::memcpy(tokens, e->history.data() + e->history.size() - count, static_cast<size_t>(count) * sizeof(int64_t));
     return KD_OK;
@@ -1457,6 +1666,7 @@ int kd_gpt_forward_logits(void* handle, const int64_t* tokens, int64_t count, fl
     if (e == nullptr || tokens == nullptr || logits == nullptr || count <= 0)
         return fail(KD_E_INVALID, "kd_gpt_forward_logits: bad arguments");
     if (count > e->cfg.max_positions) return fail(KD_E_INVALID, "kd_gpt_forward_logits: more tokens than max_positions");
+    if (e->host_sp.top_k > 0) return fail(KD_E_INVALID, "kd_gpt_forward_logits: needs the greedy pick (temperature 0)");
     for (int64_t i = 0; i < count; ++i)
         if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size) return fail(KD_E_INVALID, "kd_gpt_forward_logits: token id out of range");
     if (int rc = e->ready()) return rc;
@@ -1482,6 +1692,55 @@ int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* lengt
     *length = n;
     if (ids != nullptr && capacity > 0 && n > 0)
         std::memcpy(ids, e->history.data(), static_cast<size_t>(std::min(n, capacity)) * sizeof(int64_t));
+    return KD_OK;
+}
+
+int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || !(temperature >= 0.0) || top_k < 0)
+        return fail(KD_E_INVALID, "kd_gpt_set_sampling: needs a temperature >= 0 and top_k >= 0");
+    if (temperature > 0.0 && (top_k == 0 || top_k >= e->cfg.vocab_size))
+        return fail(KD_E_UNSUPPORTED,
+                    "kd_gpt_set_sampling: sampling on the device needs 0 < top_k < vocab_size (without a top-k, kael "
+                    "sums every probability of the vocabulary in sequence)");
+    const float t = static_cast<float>(temperature);
+    if (temperature > 0.0 && !(t > 0.f && std::isfinite(t)))
+        return fail(KD_E_INVALID, "kd_gpt_set_sampling: the temperature does not round to a positive finite float");
+    KD_HIP(hipStreamSynchronize(e->stream));
+    KD_HIP(hipStreamSynchronize(kd::stream()));
+    e->host_sp = Sampler{t, 0, temperature > 0.0 ? top_k : 0, 0, 0};
+    KD_HIP(hipMemcpy(e->sp, &e->host_sp, sizeof(Sampler), hipMemcpyHostToDevice));
+    return KD_OK;
+}
+
+int kd_gpt_set_uniforms(void* handle, const double* uniforms, int64_t count) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || count < 0 || (count > 0 && uniforms == nullptr))
+        return fail(KD_E_INVALID, "kd_gpt_set_uniforms: bad arguments");
+    if (count > e->cfg.max_positions + 1)
+        return fail(KD_E_INVALID, "kd_gpt_set_uniforms: more draws than max_positions + 1 at once");
+    for (int64_t i = 0; i < count; ++i)
+        if (!(uniforms[i] >= 0.0 && uniforms[i] < 1.0))
+            return fail(KD_E_INVALID, "kd_gpt_set_uniforms: every draw must lie in [0, 1)");
+    KD_HIP(hipStreamSynchronize(e->stream));
+    KD_HIP(hipStreamSynchronize(kd::stream()));
+    if (count > 0)
+        KD_HIP(hipMemcpy(e->uniforms, uniforms, static_cast<size_t>(count) * sizeof(double), hipMemcpyHostToDevice));
+    e->host_sp.draw = 0;
+    e->host_sp.draws = count;
+    e->host_sp.error = 0;
+    KD_HIP(hipMemcpy(e->sp, &e->host_sp, sizeof(Sampler), hipMemcpyHostToDevice));
+    return KD_OK;
+}
+
+int kd_gpt_draws_used(void* handle, int64_t* used) {
+    auto* e = static_cast<Engine*>(handle);
+    if (e == nullptr || used == nullptr) return fail(KD_E_INVALID, "kd_gpt_draws_used: bad arguments");
+    KD_HIP(hipStreamSynchronize(e->stream));
+    KD_HIP(hipStreamSynchronize(kd::stream()));
+    Sampler now{};
+    KD_HIP(hipMemcpy(&now, e->sp, sizeof now, hipMemcpyDeviceToHost));
+    *used = now.draw;
     return KD_OK;
 }
 

@@ -332,4 +332,12 @@ void gpt_engine_decode(void* engine, std::int64_t count, std::int64_t* tokens) {
     check(kd_gpt_decode(engine, count, tokens), "gpt_engine_decode");
 }
 
+void gpt_engine_set_sampling(void* engine, double temperature, std::int64_t top_k) {
+    check(kd_gpt_set_sampling(engine, temperature, top_k), "gpt_engine_set_sampling");
+}
+
+void gpt_engine_set_uniforms(void* engine, const double* uniforms, std::int64_t count) {
+    check(kd_gpt_set_uniforms(engine, uniforms, count), "gpt_engine_set_uniforms");
+}
+
 } // namespace kael::device

@@ -190,7 +190,12 @@ void gpt_engine_destroy(void* engine) noexcept;
 void gpt_engine_load(void* engine, const char* name, const std::byte* device_data, std::int64_t count);
 // Runs the prompt (host ids; its last max_positions when longer) and returns the first greedy token.
 std::int64_t gpt_engine_prefill(void* engine, const std::int64_t* prompt, std::int64_t length);
-// The next `count` greedy tokens into `tokens` (host).
+// The next `count` tokens into `tokens` (host), greedy or sampled.
 void gpt_engine_decode(void* engine, std::int64_t count, std::int64_t* tokens);
+// The pick of the following steps: temperature 0 greedy; temperature > 0 with 0 < top_k < vocab
+// kael's sample_next (src/nn/transformer.cpp:39-50) on the device.
+void gpt_engine_set_sampling(void* engine, double temperature, std::int64_t top_k);
+// The uniform draws of the next `count` sampled picks, in order (at most max_positions + 1).
+void gpt_engine_set_uniforms(void* engine, const double* uniforms, std::int64_t count);
 
 } // namespace kael::device

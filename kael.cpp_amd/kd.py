@@ -182,6 +182,9 @@ BACKEND_ONLY = {
     "gpt_forward_logits": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "gpt_sequence": (c_int, [c_void_p, c_void_p, c_int64, POINTER(c_int64)]),
     "gpt_logits": (c_int, [c_void_p, c_void_p]),
+    "gpt_set_sampling": (c_int, [c_void_p, c_double, c_int64]),
+    "gpt_set_uniforms": (c_int, [c_void_p, c_void_p, c_int64]),
+    "gpt_draws_used": (c_int, [c_void_p, POINTER(c_int64)]),
 }
 
 # Every symbol include/kd_api.h declares.
@@ -321,6 +324,19 @@ class Gpt:
         self.b.check(self.b.lib.kd_gpt_forward_logits(self.handle, t.ctypes.data_as(c_void_p), t.size,
                                                       out.ctypes.data_as(c_void_p)), "kd_gpt_forward_logits")
         return out
+
+    def set_sampling(self, temperature: float, top_k: int = 0) -> None:
+        self.b.check(self.b.lib.kd_gpt_set_sampling(self.handle, float(temperature), int(top_k)), "kd_gpt_set_sampling")
+
+    def set_uniforms(self, uniforms) -> None:
+        u = np.ascontiguousarray(uniforms, dtype=np.float64)
+        self.b.check(self.b.lib.kd_gpt_set_uniforms(self.handle, u.ctypes.data_as(c_void_p), u.size),
+                     "kd_gpt_set_uniforms")
+
+    def draws_used(self) -> int:
+        n = c_int64()
+        self.b.check(self.b.lib.kd_gpt_draws_used(self.handle, ctypes.byref(n)), "kd_gpt_draws_used")
+        return n.value
 
     def logits(self) -> np.ndarray:
         """Logits of the most recent position (the prompt's last after prefill)."""

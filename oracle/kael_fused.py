@@ -574,8 +574,10 @@ GENERATE_HELPER = """// MI355X: greedy generation with a KV cache of a batch-1 p
 // takes the model's shape; no value otherwise, and the loop of generate() runs.
 std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const GenerateOptions& options) {
     const GptConfig& config = model.config();
-    if (prompt.device() == Device::CPU || options.temperature != 0.0 || !options.use_cache || prompt.size(0) != 1 ||
-        options.max_new_tokens == 0 || config.dtype != DType::F32 || prompt.dtype() != DType::I64) {
+    const bool sampled = options.temperature != 0.0;
+    if (prompt.device() == Device::CPU || !options.use_cache || prompt.size(0) != 1 || options.max_new_tokens == 0 ||
+        config.dtype != DType::F32 || prompt.dtype() != DType::I64 ||
+        (sampled && (options.top_k <= 0 || options.top_k >= config.vocab_size))) {
         return std::nullopt;
     }
     const device::GptEngineShape shape{config.vocab_size, config.max_positions, config.layers,
@@ -600,22 +602,53 @@ std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const Ge
     const Tensor host_prompt = prompt.cpu().contiguous();
     const std::int64_t length = host_prompt.size(1);
     const std::int64_t* ids = host_prompt.data_ptr<std::int64_t>();
+    // Sampled picks take kael's generator's next draws in order (one per token, as multinomial
+    // takes them), handed to the engine in runs of at most one context; the generator is then
+    // advanced by exactly the draws used.
+    device::gpt_engine_set_sampling(engine.handle, options.temperature, sampled ? options.top_k : 0);
+    const std::int64_t run = config.max_positions + 1;
+    const auto hand_over = [&](std::int64_t picks) {
+        if (sampled) {
+            const std::vector<double> draws = device_peek_uniforms(picks);
+            device::gpt_engine_set_uniforms(engine.handle, draws.data(), picks);
+        }
+    };
+    const auto used = [&](std::int64_t picks) {
+        if (sampled) device_take_uniforms(picks);
+    };
+    const std::int64_t first_run = options.on_token ? 1 : std::min(options.max_new_tokens, run);
+    hand_over(first_run);
     std::vector<std::int64_t> generated{device::gpt_engine_prefill(engine.handle, ids, length)};
     // on_token sees each token as sample_next returns it: a [1, 1] int64 tensor on the device.
     const auto emit = [&](std::int64_t token) {
         return !options.on_token || options.on_token(from_vector<std::int64_t>({token}, {1, 1}).to(prompt.device()));
     };
     if (options.on_token) {
+        used(1);
         bool more = emit(generated.back());
         while (more && static_cast<std::int64_t>(generated.size()) < options.max_new_tokens) {
             std::int64_t token = 0;
+            hand_over(1);
             device::gpt_engine_decode(engine.handle, 1, &token);
+            used(1);
             generated.push_back(token);
             more = emit(token);
         }
     } else {
         generated.resize(static_cast<std::size_t>(options.max_new_tokens));
-        device::gpt_engine_decode(engine.handle, options.max_new_tokens - 1, generated.data() + 1);
+        std::int64_t done = 1, budget = first_run - 1;  // picks left in the current run of draws
+        while (done < options.max_new_tokens) {
+            if (budget == 0) {
+                used(run);
+                budget = std::min(options.max_new_tokens - done, run);
+                hand_over(budget);
+            }
+            const std::int64_t n = std::min(budget, options.max_new_tokens - done);
+            device::gpt_engine_decode(engine.handle, n, generated.data() + done);
+            done += n;
+            budget -= n;
+        }
+        used(options.max_new_tokens - (options.max_new_tokens - 1) / run * run);
     }
     const Tensor tail =
         from_vector<std::int64_t>(generated, {1, static_cast<std::int64_t>(generated.size())}).to(prompt.device());
@@ -811,6 +844,39 @@ std::optional<Tensor> device_dropout(const Tensor& input, double keep) {
 
 """
 
+UNIFORMS_HELPER = """// MI355X: the uniform draws multinomial would take from this generator (one
+// uniform_real_distribution<double>(0, 1) value per sample), for the decode engine's device
+// sampler: device_peek_uniforms returns the next `count` without advancing the generator, and
+// device_take_uniforms(used) then advances it by the draws the sampled picks used.
+std::vector<double> device_peek_uniforms(std::int64_t count) {
+    const auto lock = lock_generator();
+    std::mt19937_64 copy = global_generator();
+    std::uniform_real_distribution<double> uniform(0.0, 1.0);
+    std::vector<double> values(static_cast<std::size_t>(count));
+    for (double& value : values) {
+        value = uniform(copy);
+    }
+    return values;
+}
+
+void device_take_uniforms(std::int64_t used) {
+    const auto lock = lock_generator();
+    std::uniform_real_distribution<double> uniform(0.0, 1.0);
+    for (std::int64_t i = 0; i < used; ++i) {
+        (void)uniform(global_generator());
+    }
+}
+
+"""
+
+UNIFORMS_DECLARATION = """
+namespace kael {
+// MI355X: defined beside the generator in src/random.cpp.
+std::vector<double> device_peek_uniforms(std::int64_t count);
+void device_take_uniforms(std::int64_t used);
+} // namespace kael
+"""
+
 DROPOUT_DECLARATION = """
 #include <optional>
 
@@ -907,7 +973,7 @@ EDITS = [
     ("src/nn/transformer.cpp", "#include <map>\n", "after", "#include <optional>\n#include <vector>\n"),
     ("src/nn/transformer.cpp", '#include "kael/autograd/grad_mode.h"\n', "after", '#include "kael/device_kernels.h"\n'),
     ("src/nn/transformer.cpp", "class TrainingModeRestorer {\n", "before", GENERATE_HELPER),
-    ("src/nn/transformer.cpp", '#include "kael/random.h"\n', "after", '\n#include "recording.h"\n'),
+    ("src/nn/transformer.cpp", '#include "kael/random.h"\n', "after", '\n#include "recording.h"\n' + UNIFORMS_DECLARATION),
     ("src/nn/transformer.cpp", "constexpr double kInitialStd = 0.02;\n", "after", ATTENTION_HELPER + CACHED_ATTENTION_HELPER),
     ("src/nn/transformer.cpp",
      "        query_key_value_->forward(input).view({batch, length, 3, heads_, head_dimension_});\n", "after",
@@ -937,7 +1003,7 @@ EDITS = [
      '#include "kael/device_kernels.h"\n\n#include <array>\n#include <optional>\n#include <sstream>\n\n'
      '#include "recording.h"\n'),
     ("src/random.cpp", "Tensor multinomial(const Tensor& weights, std::int64_t samples, bool replacement) {\n", "before",
-     DROPOUT_HELPER),
+     DROPOUT_HELPER + UNIFORMS_HELPER),
     ("src/nn/functional.cpp", '#include "kael/random.h"\n', "after", DROPOUT_DECLARATION),
     ("src/nn/functional.cpp", "    const double keep = 1.0 - p;\n", "after", DROPOUT_BRANCH),
 ]

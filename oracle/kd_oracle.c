@@ -1015,6 +1015,70 @@ int oracle_cached_attention(int dtype, void* out, const void* q, const int64_t* 
     return rc;
 }
 
+/* ---- sampled next token: kael's sample_next with a top-k -------------------------------------
+ *
+ * Reference src/nn/transformer.cpp:39-50 for one row of `vocab` logits with temperature > 0 and
+ * 0 < top_k < vocab: x = logits / temperature (kael's scalar converted to f32, one f32
+ * division); topk(x, k) (src/ops/sequence.cpp:124-128) gives the k-th largest value t; x < t is
+ * masked_fill'ed with -inf; softmax's CPU row kernel (src/ops/nn.cpp:60-71: largest, f32
+ * exponentials of x - largest, their sum in double in index order rounded to f32, each divided
+ * by it); multinomial of one sample with the draw u (src/random.cpp:117-155: the weights as
+ * double, partial_sum, point = u * total, upper_bound, the end mapped to the last entry, then
+ * back to a positive weight). Finite logits only. */
+static int descending_float(const void* a, const void* b) {
+    const float x = *(const float*)a, y = *(const float*)b;
+    return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+int oracle_sample_topk(const float* logits, int64_t vocab, double temperature, int64_t top_k, double uniform,
+                       int64_t* token) {
+    if (logits == NULL || token == NULL || vocab < 2 || top_k <= 0 || top_k >= vocab || !(temperature > 0.0))
+        return fail("sample_topk: needs vocab >= 2, 0 < top_k < vocab and temperature > 0");
+    if (!(uniform >= 0.0 && uniform < 1.0)) return fail("sample_topk: the draw must lie in [0, 1)");
+    const float t = (float)temperature;
+    float* x = (float*)malloc((size_t)vocab * sizeof(float));
+    float* sorted = (float*)malloc((size_t)vocab * sizeof(float));
+    double* cumulative = (double*)malloc((size_t)vocab * sizeof(double));
+    int rc = KD_OK;
+    for (int64_t i = 0; i < vocab && rc == KD_OK; ++i) {
+        x[i] = logits[i] / t;
+        if (!isfinite(x[i])) rc = fail("sample_topk: non-finite logit");
+        sorted[i] = x[i];
+    }
+    if (rc == KD_OK) {
+        qsort(sorted, (size_t)vocab, sizeof(float), descending_float);
+        const float kth = sorted[top_k - 1];
+        float largest = -INFINITY;
+        for (int64_t i = 0; i < vocab; ++i) {
+            if (x[i] < kth) x[i] = -INFINITY;
+            if (x[i] > largest) largest = x[i];
+        }
+        double total = 0.0;
+        for (int64_t i = 0; i < vocab; ++i) {
+            x[i] = expf(x[i] - largest);
+            total += (double)x[i];
+        }
+        const float denominator = (float)total;
+        double run = 0.0;
+        for (int64_t i = 0; i < vocab; ++i) {
+            x[i] /= denominator;
+            run += (double)x[i];
+            cumulative[i] = run;
+        }
+        const double point = uniform * cumulative[vocab - 1];
+        int64_t picked = vocab - 1;
+        for (int64_t i = 0; i < vocab; ++i)
+            if (cumulative[i] > point) {
+                picked = i;
+                break;
+            }
+        while (x[picked] <= 0.0f && picked > 0) --picked;
+        *token = picked;
+    }
+    free(x); free(sorted); free(cumulative);
+    return rc;
+}
+
 /* ---- matmul: kernels.inl:136-177 -------------------------------------------------------------- */
 
 int oracle_matmul(int dtype, const void* a, const void* b, void* out, const kd_matmul_sizes* s,

@@ -31,6 +31,8 @@ int oracle_causal_attention(int dtype, void* out, void* lse, const void* qkv, in
                             int64_t heads, int64_t head_dim);
 int oracle_causal_attention_backward(int dtype, void* dqkv, const void* dout, const void* qkv, const void* out,
                                      const void* lse, int64_t batch, int64_t length, int64_t heads, int64_t head_dim);
+int oracle_sample_topk(const float* logits, int64_t vocab, double temperature, int64_t top_k, double uniform,
+                       int64_t* token);
 int oracle_cached_attention(int dtype, void* out, const void* q, const int64_t* q_strides, const void* k,
                             const int64_t* k_strides, const void* v, const int64_t* v_strides, int64_t batch,
                             int64_t heads, int64_t length, int64_t keys, int64_t head_dim);

@@ -530,6 +530,10 @@ std::int64_t gpt_engine_prefill(void*, const std::int64_t*, std::int64_t) {
     throw Error("oracle backend: no GPT decode engine");
 }
 void gpt_engine_decode(void*, std::int64_t, std::int64_t*) { throw Error("oracle backend: no GPT decode engine"); }
+void gpt_engine_set_sampling(void*, double, std::int64_t) { throw Error("oracle backend: no GPT decode engine"); }
+void gpt_engine_set_uniforms(void*, const double*, std::int64_t) {
+    throw Error("oracle backend: no GPT decode engine");
+}
 
 } // namespace kael::device
 

@@ -1066,6 +1066,26 @@ int ref_attention_module(int device, int64_t batch, int64_t length, int64_t dim,
     });
 }
 
+// kael's sample_next for one row of logits (reference src/nn/transformer.cpp:39-50, the
+// function is internal to that file, so its four ops are called here as it calls them) with
+// temperature > 0 and top_k, on the CPU path: manual_seed(seed), `skip` uniform draws
+// (kael::rand of that many f64 values), then logits / temperature, topk, masked_fill, softmax
+// and multinomial of one sample. Writes the picked id.
+int ref_sample_next(uint64_t seed, int64_t skip, const float* logits, int64_t vocab, double temperature, int64_t top_k,
+                    int64_t* token) {
+    return guarded([&] {
+        kael::manual_seed(seed);
+        if (skip > 0) (void)kael::rand({skip}, kael::DType::F64);
+        const kael::Tensor last = host_tensor(logits, {1, vocab}, kael::DType::F32);
+        kael::Tensor scaled = last / temperature;
+        const kael::Tensor smallest_kept = kael::topk(scaled, top_k).values.select(-1, top_k - 1);
+        scaled = kael::masked_fill(scaled, scaled < smallest_kept.unsqueeze(-1),
+                                   -std::numeric_limits<double>::infinity());
+        const kael::Tensor next = kael::multinomial(kael::softmax(scaled, -1), 1, true);
+        *token = next.item<std::int64_t>();
+    });
+}
+
 // kael's CausalSelfAttention module with a KV cache (reference src/nn/transformer.cpp:103-138)
 // on `device` (0 CPU, 1 the linked device backend), as generation runs it (no gradient):
 // manual_seed(seed), the module for `total` positions, x [B, total, C] uniform in [-1, 1), then
@@ -1189,16 +1209,21 @@ int ref_gpt_generate_on(void* handle, int device, const int64_t* prompt, int64_t
 }
 
 // kael's nn::generate with sampling (temperature > 0, optional top-k; reference
-// src/nn/transformer.cpp:39-50, 256-295) of a batch-1 prompt on `device`, after
-// kael::manual_seed(seed): the loop of generate with its KV cache, sample_next on the host.
-// Writes the sequence (length + new_tokens ids) and the wall time.
-int ref_gpt_generate_sampled(void* handle, int device, const int64_t* prompt, int64_t length, int64_t new_tokens,
-                             double temperature, int64_t top_k, uint64_t seed, int64_t* out_tokens, double* seconds) {
+// src/nn/transformer.cpp:39-50, 256-295) on `device`, after kael::manual_seed(seed), of the
+// prompt repeated over `batch` rows: the loop of generate with its KV cache and sample_next
+// (through kael's optional branches, a batch-1 prompt with 0 < top_k < vocab runs on the decode
+// engine instead). Writes the sequence (batch x (length + new_tokens) ids), the wall time and
+// the generator's next uniform draw after the call (kael::rand of one f64).
+int ref_gpt_generate_sampled(void* handle, int device, const int64_t* prompt, int64_t length, int64_t batch,
+                             int64_t new_tokens, double temperature, int64_t top_k, uint64_t seed, int64_t* out_tokens,
+                             double* seconds, double* next_draw) {
     return guarded([&] {
         auto& model = *static_cast<RefGpt*>(handle)->model;
         const kael::Device dev = device == 0 ? kael::Device::CPU : kael::Device::CUDA;
         model.to(dev);
-        const kael::Tensor ids = host_tensor(prompt, {1, length}, kael::DType::I64).to(dev);
+        std::vector<int64_t> rows;
+        for (int64_t b = 0; b < batch; ++b) rows.insert(rows.end(), prompt, prompt + length);
+        const kael::Tensor ids = host_tensor(rows.data(), {batch, length}, kael::DType::I64).to(dev);
         kael::manual_seed(seed);
         const auto t0 = std::chrono::steady_clock::now();
         const kael::Tensor seq = kael::nn::generate(
@@ -1206,6 +1231,7 @@ int ref_gpt_generate_sampled(void* handle, int device, const int64_t* prompt, in
         const auto t1 = std::chrono::steady_clock::now();
         *seconds = std::chrono::duration<double>(t1 - t0).count();
         copy_out(seq.cpu(), out_tokens);
+        *next_draw = kael::rand({1}, kael::DType::F64).item<double>();
         model.to(kael::Device::CPU);
     });
 }

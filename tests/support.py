@@ -44,6 +44,7 @@ ORACLE_SIGS = dict(kd.SIGNATURES)
 ORACLE_SIGS["matmul"] = (c_int, [c_int, c_void_p, c_void_p, c_void_p, POINTER(kd.MatmulSizes), c_int])
 ORACLE_SIGS["last_error"] = (c_char_p, [])
 ORACLE_SIGS["mt19937_64_draws"] = (c_int, [c_void_p, c_int64, c_void_p])
+ORACLE_SIGS["sample_topk"] = (c_int, [c_void_p, c_int64, c_double, c_int64, c_double, POINTER(c_int64)])
 
 
 def load_oracle() -> ctypes.CDLL:
@@ -95,8 +96,8 @@ REF_SIGS = {
     "train_gpt": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                           POINTER(c_double)]),
     "gpt_generate_on": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, POINTER(c_double)]),
-    "gpt_generate_sampled": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_double, c_int64,
-                                     ctypes.c_uint64, c_void_p, POINTER(c_double)]),
+    "gpt_generate_sampled": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_int64, c_double, c_int64,
+                                     ctypes.c_uint64, c_void_p, POINTER(c_double), POINTER(c_double)]),
     "train_gpt_params": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                  c_void_p, POINTER(c_double)]),
     "gpt_param_total": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
@@ -113,6 +114,7 @@ REF_SIGS = {
     "attention_chain": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "attention_module": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64, c_void_p, c_void_p,
                                  c_void_p]),
+    "sample_next": (c_int, [ctypes.c_uint64, c_int64, c_void_p, c_int64, c_double, c_int64, POINTER(c_int64)]),
     "cached_attention_module": (c_int, [c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, ctypes.c_uint64,
                                         c_void_p, c_void_p]),
     "layer_norm_grads": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_double,

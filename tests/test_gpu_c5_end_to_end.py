@@ -222,29 +222,54 @@ def test_generate_with_on_token_on_the_engine(kael_hip_fused):
         assert len(cpu_seen) == stop_after and len(cpu_seq) == 12 + stop_after
 
 
+def sampled(lib, device, prompt, batch, new, temperature, top_k, seed):
+    h = kael_model(lib)
+    out, t, after = np.zeros(batch * (len(prompt) + new), np.int64), ctypes.c_double(), ctypes.c_double()
+    p = np.ascontiguousarray(prompt, np.int64)
+    try:
+        assert lib.ref_gpt_generate_sampled(h, device, p.ctypes.data_as(ctypes.c_void_p), len(p), batch, new,
+                                            temperature, top_k, seed, out.ctypes.data_as(ctypes.c_void_p),
+                                            ctypes.byref(t), ctypes.byref(after)) == 0, support.ref_error(lib)
+    finally:
+        lib.ref_gpt_destroy(h)
+    return out.reshape(batch, -1), t.value, after.value
+
+
 @pytest.mark.timeout(300)
 @pytest.mark.parametrize("variant", ["hip", "hip_fused"])
 def test_kael_sampled_generate_with_its_cache_on_the_device(request, variant):
-    """kael's nn::generate with sampling (temperature 0.8, top-k 1, seed 9): its own loop with the KV
-    cache runs on the device (no engine), sample_next on the host. top-k 1 leaves one token with
-    probability 1, so the draw is fixed and the device sequence must equal kael's CPU one. Through
-    the fused build the attention of every cached step is one kd_cached_attention call."""
+    """kael's nn::generate with sampling (temperature 0.8, top-k 1, seed 9) of a prompt repeated
+    over two rows: its own loop with the KV cache runs on the device (the decode engine takes batch 1
+    only), sample_next on the host. top-k 1 leaves one token with probability 1, so the draws are
+    fixed and the device sequences must equal kael's CPU ones. Through the fused build the attention
+    of every cached step is one kd_cached_attention call."""
     lib = request.getfixturevalue("kael_hip" if variant == "hip" else "kael_hip_fused")
     lib.ref_set_threads(threads())
-    prompt = np.ascontiguousarray(np.random.default_rng(9).integers(0, VOCAB, 16), np.int64)
+    prompt = np.random.default_rng(9).integers(0, VOCAB, 16)
     new = 24
-    seqs, secs = [], []
-    for device in (0, 1):
-        h = kael_model(lib)
-        out, t = np.zeros(len(prompt) + new, np.int64), ctypes.c_double()
-        try:
-            assert lib.ref_gpt_generate_sampled(h, device, prompt.ctypes.data_as(ctypes.c_void_p), len(prompt), new,
-                                                0.8, 1, 9, out.ctypes.data_as(ctypes.c_void_p),
-                                                ctypes.byref(t)) == 0, support.ref_error(lib)
-        finally:
-            lib.ref_gpt_destroy(h)
-        seqs.append(out)
-        secs.append(t.value)
-    np.testing.assert_array_equal(seqs[1], seqs[0])
-    print(f"\nkael nn::generate sampled with its KV cache on the MI355X ({variant}): {new} tokens in "
-          f"{secs[1]:.2f} s = {new / secs[1]:.1f} tokens/s; kael CPU {new / secs[0]:.2f} tokens/s")
+    cpu, cpu_s, cpu_next = sampled(lib, 0, prompt, 2, new, 0.8, 1, 9)
+    dev, dev_s, dev_next = sampled(lib, 1, prompt, 2, new, 0.8, 1, 9)
+    np.testing.assert_array_equal(dev, cpu)
+    assert dev_next == cpu_next
+    print(f"\nkael nn::generate sampled with its KV cache, 2 rows, on the MI355X ({variant}): {new} tokens in "
+          f"{dev_s:.2f} s = {2 * new / dev_s:.1f} tokens/s; kael CPU {2 * new / cpu_s:.2f} tokens/s")
+
+
+@pytest.mark.timeout(300)
+def test_kael_sampled_generate_on_the_engine(kael_hip_fused):
+    """The reference example's sampling (examples/gpt2_generate.cpp: temperature 0.8, top-k 40) through
+    kael's nn::generate: the fused build runs it on the decode engine with the device sampler, the
+    draws taken from kael's generator; the tokens must equal kael's CPU generate with the same seed
+    (its sample_next on the host), for 64 tokens after a 16-token prompt, and the generator's next draw
+    afterwards must be the same (the engine used exactly one draw per token)."""
+    lib = kael_hip_fused
+    lib.ref_set_threads(threads())
+    prompt = np.random.default_rng(11).integers(0, VOCAB, 16)
+    new = 64
+    cpu, cpu_s, cpu_next = sampled(lib, 0, prompt, 1, new, 0.8, 40, 5)
+    dev, dev_s, dev_next = sampled(lib, 1, prompt, 1, new, 0.8, 40, 5)
+    np.testing.assert_array_equal(dev, cpu)
+    assert dev_next == cpu_next
+    assert len(set(cpu[0, 16:].tolist())) > 8  # sampled, not one repeated token
+    print(f"\nkael nn::generate, temperature 0.8, top-k 40, on the MI355X decode engine: {new} tokens in {dev_s:.2f} s "
+          f"= {new / dev_s:.1f} tokens/s (engine set-up and prefill included); kael CPU {new / cpu_s:.2f} tokens/s")

@@ -264,3 +264,68 @@ def test_unknown_flags_are_rejected(kdb):
     h = ctypes.c_void_p()
     assert kdb.lib.kd_gpt_supported(ctypes.byref(cfg)) == -1  # KD_E_INVALID
     assert kdb.lib.kd_gpt_create(ctypes.byref(h), ctypes.byref(cfg)) == -1
+
+
+def oracle_pick(oracle, logits, temperature, top_k, u):
+    tok = ctypes.c_int64()
+    assert oracle.oracle_sample_topk(logits.ctypes.data_as(ctypes.c_void_p), logits.size, temperature, top_k, u,
+                                     ctypes.byref(tok)) == 0, oracle.oracle_last_error()
+    return tok.value
+
+
+@pytest.mark.parametrize("vocab, temperature, top_k", [(11, 0.8, 3), (97, 1.3, 40), (97, 0.5, 96), (97, 2.0, 1)],
+                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1"])
+def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature, top_k):
+    """kael's sample_next on the device (kd_gpt_set_sampling, kd_gpt_set_uniforms): after the prefill and
+    after every decode step the engine's pick equals the oracle's restatement of sample_next on the
+    same logits with the same draw, and the draws are used one per token."""
+    ref = refdev
+    h, g = build(kdb, ref, vocab, 32, 2, 2, 8, 13)
+    try:
+        rng = np.random.default_rng(vocab + top_k)
+        prompt = rng.integers(0, vocab, 6)
+        steps = 20
+        u = rng.uniform(0, 1, steps + 1)
+        g.set_sampling(temperature, top_k)
+        g.set_uniforms(u)
+        g.prefill(prompt)
+        picks = [g.sequence()[-1]]
+        assert picks[0] == oracle_pick(oracle, g.logits(), temperature, top_k, u[0])
+        for s in range(1, steps + 1):
+            picks.extend(g.decode(1))
+            assert picks[-1] == oracle_pick(oracle, g.logits(), temperature, top_k, u[s]), s
+        assert g.draws_used() == steps + 1
+        if top_k > 1:
+            assert len(set(picks)) > 1
+        # the same draws in one decode call give the same tokens
+        g.set_uniforms(u)
+        g.prefill(prompt)
+        np.testing.assert_array_equal(g.decode(steps), picks[1:])
+        # greedy again after sampling: kael's greedy tokens
+        g.set_sampling(0.0)
+        seq, _ = cpu_generate(ref, h, prompt, 8)
+        g.prefill(prompt)
+        np.testing.assert_array_equal(g.decode(7), seq[len(prompt) + 1:])
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
+def test_sampling_arguments_and_missing_draws_fail(kdb, refdev):
+    ref = refdev
+    h, g = build(kdb, ref, 11, 16, 1, 2, 8, 3)
+    try:
+        for t, k in [(0.8, 0), (0.8, 11), (-1.0, 3)]:
+            with pytest.raises(kd.KdError):
+                g.set_sampling(t, k)
+        with pytest.raises(kd.KdError):
+            g.set_uniforms(np.array([0.5, 1.0]))
+        g.set_sampling(0.9, 4)
+        g.set_uniforms(np.array([0.25, 0.75]))
+        g.prefill(np.array([1, 2, 3]))
+        g.decode(1)
+        with pytest.raises(kd.KdError, match="no uniform draw left"):
+            g.decode(1)
+        with pytest.raises(kd.KdError):
+            g.forward_logits(np.array([1, 2]))
+    finally:
+        ref.ref_gpt_destroy(h)
