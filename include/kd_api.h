@@ -550,7 +550,10 @@ int kd_gpt_logits(void* handle, float* logits);
  * src/nn/transformer.cpp:39-50: logits / temperature, the top_k largest kept, softmax,
  * multinomial of one sample, src/random.cpp:106-160) on the device, drawing the next uniform
  * given by kd_gpt_set_uniforms for each sampled token. Without a top-k, kael's multinomial sums
- * every probability of the vocabulary in sequence: KD_E_UNSUPPORTED (kael's own loop samples). */
+ * every probability of the vocabulary in sequence: KD_E_UNSUPPORTED (kael's own loop samples); so
+ * is a vocabulary above KD_GPT_SAMPLE_MAX_VOCAB, whose keys no longer fit the picking workgroup's
+ * registers. */
+#define KD_GPT_SAMPLE_MAX_VOCAB 65536
 int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k);
 /* The uniform draws in [0, 1) for the next `count` sampled picks, in order (at most
  * max_positions + 1): what uniform_real_distribution<double>(0, 1) on kael's generator returns

@@ -340,6 +340,9 @@ struct GemvArgs {
     float* best_v;
     int64_t* best_i;
     Step* st;
+    // head_kernel when the sampler samples (top_k > 0): every row's order key of logit / temperature
+    const Sampler* sp;
+    uint32_t* keys;
 };
 
 constexpr int kMaxK = 4096;
@@ -509,6 +512,21 @@ typedef __attribute__((address_space(1))) const f32x4 global_f32x4;
 typedef __attribute__((address_space(1))) const float global_f32;
 typedef __attribute__((address_space(1))) float global_f32_out;
 
+// Order-preserving keys of floats for the sampled pick: unsigned order of the keys is the order of
+// the floats (-0 and +0 share +0's key, as they compare equal); the finite floats' keys lie in
+// [kFiniteKeyLow, kFiniteKeyHigh], the infinities' and NaNs' outside.
+__device__ __forceinline__ uint32_t order_key(float x) {
+    const uint32_t b = x == 0.f ? 0u : __float_as_uint(x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+constexpr uint32_t kFiniteKeyLow = 0x00800000u;   // key of -FLT_MAX
+constexpr uint32_t kFiniteKeyHigh = 0xff7fffffu;  // key of FLT_MAX
+
 __device__ __forceinline__ float4 nt_load4(const float4* p) {
     const f32x4 v = __builtin_nontemporal_load((global_f32x4*)(p));
     return make_float4(v.x, v.y, v.z, v.w);
@@ -547,6 +565,8 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
         }
     };
     int64_t p = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave;
+    const bool keyed = a.sp != nullptr && a.sp->top_k > 0;
+    const float temperature = keyed ? a.sp->temperature : 1.f;
     const LnIn ln = ln_load(a.x, a.K, a.ln_w, a.ln_b);
     float4 c0[kHeadVec], c1[kHeadVec];
     if (p < pairs) load(p, c0, c1);
@@ -573,6 +593,10 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
         const int64_t n = 2 * p;
         if (lane == 0) a.out[n] = a0;
         if (lane == 1 && n + 1 < N) a.out[n + 1] = a1;
+        if (keyed) {  // x = logits / temperature as kael's sample_next divides (f32)
+            if (lane == 0) a.keys[n] = order_key(__fdiv_rn(a0, temperature));
+            if (lane == 1 && n + 1 < N) a.keys[n + 1] = order_key(__fdiv_rn(a1, temperature));
+        }
         const Best o0{a0, n};
         if (better(o0, best)) best = o0;
         if (n + 1 < N) {
@@ -606,24 +630,25 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
 //   Greedy (sampler top_k 0): the first maximum among the head's workgroup partials (GPT-2's
 //   6283 partials take 7 loads per lane).
 //   Sampled: kael's sample_next (reference src/nn/transformer.cpp:39-50) and multinomial
-//   (src/random.cpp:106-160) for 0 < top_k < vocab: x = logits / temperature (f32 division);
-//   the k-th largest x by a radix select over order-preserving 32-bit keys (four 8-bit digits,
-//   per-wave histograms); the kept entries (x >= the k-th largest: masked_fill's complement)
-//   listed in index order; then, in one lane and in kael's order, softmax's e = exp(x - max) with
-//   the sum in double rounded to f32, p = e / sum, the cumulative double sum of p, point = u * sum,
-//   the first kept entry whose cumulative sum exceeds the point (upper_bound; the masked entries add
-//   zeros, which leave every partial sum unchanged), or else the last kept entry with p > 0.
+//   (src/random.cpp:106-160) for 0 < top_k < vocab: x = logits / temperature (f32 division, in
+//   head_kernel, which writes x's order-preserving 32-bit keys); the k-th largest x by radix
+//   selects (four 8-bit digits, per-wave histograms) over the keys, lane t holding those of
+//   indices t, t + 1024, ... in registers. For k <= 1024 the k-th largest of the lanes' maxima
+//   bounds the k-th largest key from below (k lanes hold a key at least that large), so only the
+//   keys at or above it (about k of them) are listed and selected from; otherwise, or when more
+//   than kPickLdsKept are, every key is. The kept entries (x >= the k-th largest: masked_fill's
+//   complement) are listed in index order with their e = exp(x - max); then, in kael's order, the
+//   sum of e in double rounded to f32, p = e / sum, the cumulative double sum of p, point = u *
+//   sum, the first kept entry whose cumulative sum exceeds the point (upper_bound; the masked
+//   entries add zeros, which leave every partial sum unchanged), or else the last kept entry with
+//   p > 0.
 constexpr int kPickThreads = 1024;
 constexpr int kPickWaves = kPickThreads / 64;
-
-__device__ __forceinline__ uint32_t order_key(float x) {
-    const uint32_t b = __float_as_uint(x);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ float key_value(uint32_t k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
+constexpr int kPickSlots = 64;         // keys per lane: sampled vocabularies up to 65536
+constexpr int kPickLdsKept = 4096;     // listed entries staged in LDS; more kept go to the global scratch
+static_assert(int64_t{kPickThreads} * kPickSlots == KD_GPT_SAMPLE_MAX_VOCAB);
+static_assert(kPickLdsKept % kPickThreads == 0 && kPickLdsKept / kPickThreads <= kPickSlots);
+constexpr int32_t kRawBufferWord3 = 0x00020000;  // buffer descriptor word 3: 32-bit data format
 
 struct PickArgs {
     Step* st;
@@ -635,8 +660,24 @@ struct PickArgs {
     int64_t vocab;
     Sampler* sp;
     const double* uniforms;
-    int32_t* kept;   // [vocab] scratch: kept indices in index order
+    int32_t* kept;   // [vocab] scratch: kept indices in index order, when more than kPickLdsKept
     float* kept_e;   // [vocab] scratch: their exponentials
+    const uint32_t* keys;  // [vocab] head_kernel's order keys of x = logits / temperature
+};
+
+struct PickShared {
+    uint32_t hist[kPickWaves][256];
+    uint32_t counts[kPickSlots * kPickWaves];  // per (item group, wave), then their offsets
+    int64_t wave_totals[kPickWaves];
+    uint32_t wmax[kPickWaves];
+    uint32_t wmin[kPickWaves];
+    uint32_t chosen;
+    int64_t remaining;
+    int64_t total;
+    uint32_t cand_key[kPickLdsKept];  // listed keys >= the lower bound, in index order
+    int32_t cand_idx[kPickLdsKept];
+    float kept_e[kPickLdsKept];       // kept entries, when at most kPickLdsKept
+    int32_t kept_i[kPickLdsKept];
 };
 
 // Inclusive prefix sum of v over the workgroup's first `n` lanes (n a multiple of 64, at most
@@ -656,111 +697,259 @@ __device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int n, int64_
     return v + before;
 }
 
-__device__ void sample_pick(const PickArgs& a, int64_t& token) {
-    __shared__ uint32_t hist[kPickWaves][256];
-    __shared__ int64_t wave_totals[kPickWaves];
-    __shared__ uint32_t wmax[kPickWaves];
-    __shared__ int32_t bad[kPickWaves];
-    __shared__ uint32_t chosen;
-    __shared__ int64_t remaining;
-    __shared__ int64_t total_kept;
+// Adds 1 to hist[bin] for every active lane. Most logits share their top key bits, and lane-by-lane
+// LDS atomics on one address serialise, so the first few distinct bins among the wave's lanes take
+// one atomic each (the bin read from the leading lane with readlane); the lanes left, whose bins
+// are then spread, add their own.
+__device__ __forceinline__ void wave_histogram_add(uint32_t* hist, uint32_t bin, bool active) {
+    uint64_t pending = __ballot(active);
+    const int lane = threadIdx.x % 64;
+    for (int round = 0; round < 4 && pending != 0; ++round) {
+        const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+        const uint32_t leader_bin = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bin), leader));
+        const uint64_t same = __ballot(active && bin == leader_bin) & pending;
+        if (lane == leader) atomicAdd(&hist[leader_bin], static_cast<uint32_t>(__popcll(same)));
+        pending &= ~same;
+    }
+    if ((pending >> lane) & 1) atomicAdd(&hist[bin], 1u);
+}
+
+// The rank-th largest (1-based) of the keys the lanes offer: visit(f) calls f(key, counted) for
+// each of the lane's keys, equally often in every lane of a wave. Four 8-bit digits from the top
+// with per-wave histograms; every thread of the workgroup calls it. rank must not exceed the
+// number of counted keys.
+template <class Visit>
+__device__ __forceinline__ uint32_t radix_select(const Visit& visit, int64_t rank, PickShared& sh) {
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const int64_t V = a.vocab;
-    const float temp = a.sp->temperature;
-    const auto x_of = [&](int64_t i) { return __fdiv_rn(a.logits[i], temp); };
-    if (tid == 0) remaining = a.sp->top_k;
-    uint32_t prefix = 0, mask = 0, kmax = 0;
-    int32_t nonfinite = 0;
-    // radix select of the k-th largest key, one 8-bit digit per pass from the top
+    if (tid == 0) sh.remaining = rank;
+    uint32_t prefix = 0, mask = 0;
+#pragma unroll 1
     for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = lane; b < 256; b += 64) hist[wave][b] = 0;
+        for (int b = lane; b < 256; b += 64) sh.hist[wave][b] = 0;
         __syncthreads();
-        for (int64_t i = tid; i < V; i += kPickThreads) {
-            const float x = x_of(i);
-            const uint32_t key = order_key(x);
-            if (shift == 24) {
-                kmax = max(kmax, key);
-                nonfinite |= !isfinite(x);
-            }
-            if ((key & mask) == prefix) atomicAdd(&hist[wave][(key >> shift) & 255u], 1u);
-        }
+        visit([&](uint32_t key, bool counted) {
+            wave_histogram_add(sh.hist[wave], (key >> shift) & 255u, counted && (key & mask) == prefix);
+        });
         __syncthreads();
         // the digit: the bin b whose count from the top reaches the remaining rank
         const int b = 255 - tid;  // lanes 0..255 take the bins from the top
         int64_t n = 0;
         if (tid < 256)
-            for (int w = 0; w < kPickWaves; ++w) n += hist[w][b];
-        const int64_t need = remaining;  // read before the scan's barriers; written after them
-        const int64_t from_top = block_inclusive_scan(tid < 256 ? n : 0, 256, wave_totals);
+            for (int w = 0; w < kPickWaves; ++w) n += sh.hist[w][b];
+        const int64_t need = sh.remaining;  // read before the scan's barriers; written after them
+        const int64_t from_top = block_inclusive_scan(tid < 256 ? n : 0, 256, sh.wave_totals);
         if (tid < 256 && from_top >= need && from_top - n < need) {
-            chosen = static_cast<uint32_t>(b);
-            remaining = need - (from_top - n);
+            sh.chosen = static_cast<uint32_t>(b);
+            sh.remaining = need - (from_top - n);
         }
         __syncthreads();
-        prefix |= chosen << shift;
+        prefix |= sh.chosen << shift;
         mask |= 0xffu << shift;
     }
-    // the largest key and whether any x is not finite
+    return prefix;
+}
+
+// Lists the lane's items j < groups (item j of lane t stands for j * kPickThreads + t) for which
+// keep(j) holds, in item order, which is (j, wave, lane) order: a count per (j, wave), an
+// exclusive scan of the counts, then each wave's items in lane order, emit(j, position, total)
+// writing one. Returns the total; every thread of the workgroup calls it.
+template <class Keep, class Emit>
+__device__ __forceinline__ int64_t ordered_compact(int groups, const Keep& keep, const Emit& emit, PickShared& sh) {
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    uint64_t mine = 0;  // bit j: item j kept
+#pragma unroll
+    for (int j = 0; j < kPickSlots; ++j) {
+        if (j < groups) {
+            const bool k = keep(j);
+            mine |= uint64_t{k} << j;
+            const uint64_t lanes = __ballot(k);
+            if (lane == 0) sh.counts[j * kPickWaves + wave] = static_cast<uint32_t>(__popcll(lanes));
+        }
+    }
+    __syncthreads();
+    const int64_t c = tid / kPickWaves < groups ? sh.counts[tid] : 0;
+    const int64_t through = block_inclusive_scan(c, kPickThreads, sh.wave_totals);
+    sh.counts[tid] = static_cast<uint32_t>(through - c);
+    if (tid == kPickThreads - 1) sh.total = through;
+    __syncthreads();
+    const int64_t total = sh.total;
+    uint64_t wave_items = mine;
     for (int off = 32; off > 0; off >>= 1) {
-        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), off)));
-        nonfinite |= __shfl_xor(nonfinite, off);
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(wave_items), off);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(wave_items >> 32), off);
+        wave_items |= (uint64_t{hi} << 32) | lo;
+    }
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    while (wave_items != 0) {
+        const int j = __ffsll(static_cast<unsigned long long>(wave_items)) - 1;
+        wave_items &= wave_items - 1;
+        const bool k = (mine >> j) & 1;
+        const uint64_t lanes = __ballot(k);
+        if (k) emit(j, sh.counts[j * kPickWaves + wave] + __popcll(lanes & below), total);
+    }
+    __syncthreads();
+    return total;
+}
+
+__device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
+    __shared__ PickShared sh;
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int64_t V = a.vocab;
+    const int slots = static_cast<int>((V + kPickThreads - 1) / kPickThreads);
+    const int64_t top_k = a.sp->top_k;
+    // the keys, slot s of lane t holding index s * 1024 + t (0 past the vocabulary, below every
+    // finite x's key; each phase reads them again from L2 rather than holding 64 registers over the
+    // barriers); the lane's largest, and the smallest over the vocabulary
+    // (buffer loads: one lane offset and a scalar offset per slot, where 64 global addresses would
+    // hold 128 registers over the passes)
+    const __amdgpu_buffer_rsrc_t keys_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(a.keys), 0, static_cast<int32_t>(V * sizeof(uint32_t)), kRawBufferWord3);
+    const auto key_at = [&](int s) -> uint32_t {
+        return int64_t{s} * kPickThreads + tid < V
+                   ? __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, tid * 4, s * kPickThreads * 4, 0)
+                   : 0u;
+    };
+    uint32_t tmax = 0, tmin = ~0u;
+#pragma unroll
+    for (int s = 0; s < kPickSlots; ++s) {
+        if (s < slots) {
+            const uint32_t k = key_at(s);
+            tmax = max(tmax, k);
+            if (int64_t{s} * kPickThreads + tid < V) tmin = min(tmin, k);
+        }
+    }
+    uint32_t wm = tmax, wn = tmin;
+    for (int off = 32; off > 0; off >>= 1) {
+        wm = max(wm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wm), off)));
+        wn = min(wn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wn), off)));
     }
     if (lane == 0) {
-        wmax[wave] = kmax;
-        bad[wave] = nonfinite;
+        sh.wmax[wave] = wm;
+        sh.wmin[wave] = wn;
     }
     __syncthreads();
-    kmax = wmax[0];
-    nonfinite = bad[0];
+    uint32_t kmax = sh.wmax[0], kmin = sh.wmin[0];
     for (int w = 1; w < kPickWaves; ++w) {
-        kmax = max(kmax, wmax[w]);
-        nonfinite |= bad[w];
+        kmax = max(kmax, sh.wmax[w]);
+        kmin = min(kmin, sh.wmin[w]);
     }
-    const uint32_t kth = prefix;
-    // kept entries (x >= the k-th largest) in index order: thread t lists its contiguous chunk's
-    const int64_t chunk = (V + kPickThreads - 1) / kPickThreads;
-    const int64_t lo = min(V, tid * chunk), hi = min(V, lo + chunk);
-    int64_t mine = 0;
-    for (int64_t i = lo; i < hi; ++i) mine += order_key(x_of(i)) >= kth;
-    const int64_t through = block_inclusive_scan(mine, kPickThreads, wave_totals);
-    if (tid == kPickThreads - 1) total_kept = through;
-    int64_t at = through - mine;
-    for (int64_t i = lo; i < hi; ++i)
-        if (order_key(x_of(i)) >= kth) a.kept[at++] = static_cast<int32_t>(i);
+    // a lower bound of the k-th largest key (a key of 0, past the vocabulary or a NaN, is never
+    // kept): for k <= 1024 the k-th largest lane maximum; the keys at or above it listed in index
+    // order with their indices when they fit the LDS
+    uint32_t low = 1;
+    bool listed = false;
+    int64_t listed_n = 0;
+    if (top_k <= kPickThreads) {
+        low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh));
+        listed_n = ordered_compact(
+            slots, [&](int s) { return key_at(s) >= low; },
+            [&](int s, int64_t at, int64_t total) {
+                if (total <= kPickLdsKept) {
+                    const int32_t i = s * kPickThreads + tid;
+                    sh.cand_idx[at] = i;
+                    sh.cand_key[at] = a.keys[i];
+                }
+            },
+            sh);
+        listed = listed_n <= kPickLdsKept;
+    }
+    // the k-th largest key and the kept entries (keys at or above it) in index order
+    int64_t m;
+    int32_t* kept;
+    float* kept_e;
+    if (listed) {
+        const int groups = static_cast<int>((listed_n + kPickThreads - 1) / kPickThreads);
+        const auto listed_key = [&](int j) {
+            const int64_t r = int64_t{j} * kPickThreads + tid;
+            return r < listed_n ? sh.cand_key[r] : 0u;
+        };
+        const uint32_t kth = radix_select(
+            [&](const auto& f) {
+                for (int j = 0; j < groups; ++j) f(listed_key(j), int64_t{j} * kPickThreads + tid < listed_n);
+            },
+            top_k, sh);
+        m = ordered_compact(
+            groups, [&](int j) { return int64_t{j} * kPickThreads + tid < listed_n && listed_key(j) >= kth; },
+            [&](int j, int64_t at, int64_t) { sh.kept_i[at] = sh.cand_idx[j * kPickThreads + tid]; }, sh);
+        kept = sh.kept_i;
+        kept_e = sh.kept_e;
+    } else {
+        const uint32_t kth = max(low, radix_select(
+                                          [&](const auto& f) {
+#pragma unroll
+                                              for (int s = 0; s < kPickSlots; ++s) {
+                                                  if (s < slots) {
+                                                      const uint32_t k = key_at(s);
+                                                      f(k, k >= low);
+                                                  }
+                                              }
+                                          },
+                                          top_k, sh));
+        m = ordered_compact(
+            slots, [&](int s) { return key_at(s) >= kth; },
+            [&](int s, int64_t at, int64_t total) {
+                (total <= kPickLdsKept ? sh.kept_i : a.kept)[at] = s * kPickThreads + tid;
+            },
+            sh);
+        kept = m <= kPickLdsKept ? sh.kept_i : a.kept;
+        kept_e = m <= kPickLdsKept ? sh.kept_e : a.kept_e;
+    }
+    // softmax's f32 exponentials exp(x - max) of the kept entries (src/ops/nn.cpp:60-71), x divided
+    // again as head_kernel divides it; key_value recovers the largest x exactly
+    const float temp = a.sp->temperature;
+    const float mx = key_value(kmax);
+    for (int64_t r = tid; r < m; r += kPickThreads) kept_e[r] = expf(__fdiv_rn(a.logits[kept[r]], temp) - mx);
     __syncthreads();
-    if (tid != 0) return;
+    int32_t nonfinite = kmax > kFiniteKeyHigh || kmin < kFiniteKeyLow;
+    if (wave != 0) return;
+    // The sums below run in index order in double, as kael's CPU loops do: wave 0 loads 64 entries
+    // at a time, one per lane, and folds them in lane order through readlane, so only one load per
+    // 64 entries stands in the dependent chain.
+    const auto lane_value = [](float v, int j) {
+        return static_cast<double>(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j)));
+    };
     Sampler& sp = *a.sp;
-    if (nonfinite || sp.draw >= sp.draws) {
-        sp.error = nonfinite ? 1 : 2;
+    const int64_t draw = sp.draw;
+    if (nonfinite || draw >= sp.draws) {
+        if (lane == 0) sp.error = nonfinite ? 1 : 2;
         token = 0;
         return;
     }
-    const double u = a.uniforms[sp.draw++];
-    const float mx = key_value(kmax);
-    const int64_t m = total_kept;
-    // softmax over the kept entries as kael's row softmax (src/ops/nn.cpp:60-71): f32
-    // exponentials, their sum in double in index order, rounded to f32, each divided by it
+    const double u = a.uniforms[draw];
+    if (lane == 0) sp.draw = draw + 1;
+    // the sum of e in double in index order, rounded to f32
     double sum = 0.0;
-    for (int64_t r = 0; r < m; ++r) {
-        const float e = expf(x_of(a.kept[r]) - mx);
-        a.kept_e[r] = e;
-        sum += static_cast<double>(e);
+    for (int64_t base = 0; base < m; base += 64) {
+        const float e = base + lane < m ? kept_e[base + lane] : 0.f;
+        const int n = static_cast<int>(min<int64_t>(64, m - base));
+        for (int j = 0; j < n; ++j) sum += lane_value(e, j);
     }
     const float denominator = static_cast<float>(sum);
     // multinomial (src/random.cpp:143-151): the cumulative sum in double, point = u * total,
     // upper_bound, and the step back to a positive weight when the point is past every sum
     double cumulative = 0.0;
-    for (int64_t r = 0; r < m; ++r) cumulative += static_cast<double>(__fdiv_rn(a.kept_e[r], denominator));
+    for (int64_t base = 0; base < m; base += 64) {
+        const float p = base + lane < m ? __fdiv_rn(kept_e[base + lane], denominator) : 0.f;
+        const int n = static_cast<int>(min<int64_t>(64, m - base));
+        for (int j = 0; j < n; ++j) cumulative += lane_value(p, j);
+    }
     const double point = u * cumulative;
     double run = 0.0;
-    int64_t pick = -1, last_positive = a.kept[0];
-    for (int64_t r = 0; r < m; ++r) {
-        const float p = __fdiv_rn(a.kept_e[r], denominator);
-        run += static_cast<double>(p);
-        if (p > 0.f) last_positive = a.kept[r];
-        if (run > point) {
-            pick = a.kept[r];
-            break;
+    int64_t pick = -1, last_positive = kept[0];
+    for (int64_t base = 0; base < m && pick < 0; base += 64) {
+        const bool in = base + lane < m;
+        const float p = in ? __fdiv_rn(kept_e[base + lane], denominator) : 0.f;
+        const int32_t index = in ? kept[base + lane] : 0;
+        const int n = static_cast<int>(min<int64_t>(64, m - base));
+        for (int j = 0; j < n; ++j) {
+            const double pj = lane_value(p, j);
+            const int32_t ij = __builtin_amdgcn_readlane(index, j);
+            run += pj;
+            if (pj > 0.0) last_positive = ij;
+            if (run > point) {
+                pick = ij;
+                break;
+            }
         }
     }
     token = pick >= 0 ? pick : last_positive;
@@ -1071,6 +1260,7 @@ struct Engine {
     double* uniforms = nullptr;  // [max_positions + 1] draws for sampled picks
     int32_t* kept = nullptr;     // [vocab] sampling scratch
     float* kept_e = nullptr;     // [vocab]
+    uint32_t* keys = nullptr;    // [vocab] order keys of the sampled pick's x
     Sampler host_sp{0.f, 0, 0, 0, 0};
     hipGraphExec_t graph = nullptr;
     int64_t host_pos = 0;     // mirror of st->pos: positions in the KV cache
@@ -1100,7 +1290,7 @@ struct Engine {
     }
 
     PickArgs pick_args() const {
-        return PickArgs{st, seq, pv, pi, head_groups(), logits, cfg.vocab_size, sp, uniforms, kept, kept_e};
+        return PickArgs{st, seq, pv, pi, head_groups(), logits, cfg.vocab_size, sp, uniforms, kept, kept_e, keys};
     }
 
     // Workgroups of head_kernel: 4 per CU, fewer when the vocabulary has fewer row pairs than
@@ -1189,6 +1379,8 @@ struct Engine {
         head.out = logits;
         head.best_v = pv;
         head.best_i = pi;
+        head.sp = sp;
+        head.keys = keys;
         const int64_t parts = head_groups();
         hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
         hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kPickThreads), 0, s, pick_args());
@@ -1348,6 +1540,8 @@ struct Engine {
         head.out = logits;
         head.best_v = pv;
         head.best_i = pi;
+        head.sp = sp;
+        head.keys = keys;
         const int64_t parts = head_groups();
         hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
         hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kPickThreads), 0, s, pick_args());
@@ -1427,7 +1621,7 @@ struct Engine {
                           static_cast<void*>(f), static_cast<void*>(logits), static_cast<void*>(pv),
                           static_cast<void*>(pi), static_cast<void*>(seq), static_cast<void*>(st),
                           static_cast<void*>(sp), static_cast<void*>(uniforms), static_cast<void*>(kept),
-                          static_cast<void*>(kept_e)})
+                          static_cast<void*>(kept_e), static_cast<void*>(keys)})
             if (ptr) (void)hipFree(ptr);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -1515,6 +1709,7 @@ int create(Engine& e, const kd_gpt_config& c) {
     if (int rc = alloc(&e.uniforms, c.max_positions + 1)) return rc;
     if (int rc = alloc(&e.kept, c.vocab_size)) return rc;
     if (int rc = alloc(&e.kept_e, c.vocab_size)) return rc;
+    if (int rc = alloc(&e.keys, c.vocab_size)) return rc;
     KD_HIP(hipMemcpy(e.sp, &e.host_sp, sizeof(Sampler), hipMemcpyHostToDevice));  // greedy
     return KD_OK;
 }
@@ -1703,6 +1898,9 @@ int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k) {
         return fail(KD_E_UNSUPPORTED,
                     "kd_gpt_set_sampling: sampling on the device needs 0 < top_k < vocab_size (without a top-k, kael "
                     "sums every probability of the vocabulary in sequence)");
+    if (temperature > 0.0 && e->cfg.vocab_size > KD_GPT_SAMPLE_MAX_VOCAB)
+        return fail(KD_E_UNSUPPORTED, "kd_gpt_set_sampling: sampling on the device takes vocabularies of at most "
+                                      "KD_GPT_SAMPLE_MAX_VOCAB (65536) entries");
     const float t = static_cast<float>(temperature);
     if (temperature > 0.0 && !(t > 0.f && std::isfinite(t)))
         return fail(KD_E_INVALID, "kd_gpt_set_sampling: the temperature does not round to a positive finite float");

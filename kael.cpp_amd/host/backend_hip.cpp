@@ -332,6 +332,8 @@ void gpt_engine_decode(void* engine, std::int64_t count, std::int64_t* tokens) {
     check(kd_gpt_decode(engine, count, tokens), "gpt_engine_decode");
 }
 
+static_assert(kGptSampleMaxVocab == KD_GPT_SAMPLE_MAX_VOCAB);
+
 void gpt_engine_set_sampling(void* engine, double temperature, std::int64_t top_k) {
     check(kd_gpt_set_sampling(engine, temperature, top_k), "gpt_engine_set_sampling");
 }

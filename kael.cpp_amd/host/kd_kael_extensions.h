@@ -193,7 +193,9 @@ std::int64_t gpt_engine_prefill(void* engine, const std::int64_t* prompt, std::i
 // The next `count` tokens into `tokens` (host), greedy or sampled.
 void gpt_engine_decode(void* engine, std::int64_t count, std::int64_t* tokens);
 // The pick of the following steps: temperature 0 greedy; temperature > 0 with 0 < top_k < vocab
-// kael's sample_next (src/nn/transformer.cpp:39-50) on the device.
+// kael's sample_next (src/nn/transformer.cpp:39-50) on the device, for vocabularies of at most
+// kGptSampleMaxVocab entries.
+inline constexpr std::int64_t kGptSampleMaxVocab = 65536;
 void gpt_engine_set_sampling(void* engine, double temperature, std::int64_t top_k);
 // The uniform draws of the next `count` sampled picks, in order (at most max_positions + 1).
 void gpt_engine_set_uniforms(void* engine, const double* uniforms, std::int64_t count);

@@ -577,7 +577,8 @@ std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const Ge
     const bool sampled = options.temperature != 0.0;
     if (prompt.device() == Device::CPU || !options.use_cache || prompt.size(0) != 1 || options.max_new_tokens == 0 ||
         config.dtype != DType::F32 || prompt.dtype() != DType::I64 ||
-        (sampled && (options.top_k <= 0 || options.top_k >= config.vocab_size))) {
+        (sampled && (options.top_k <= 0 || options.top_k >= config.vocab_size ||
+                     config.vocab_size > device::kGptSampleMaxVocab))) {
         return std::nullopt;
     }
     const device::GptEngineShape shape{config.vocab_size, config.max_positions, config.layers,

@@ -310,8 +310,67 @@ def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature,
         ref.ref_gpt_destroy(h)
 
 
+@pytest.mark.parametrize("vocab, spread", [(3000, "top"), (6000, "top"), (6000, "all")])
+def test_sampled_picks_with_tied_logits(kdb, refdev, oracle, vocab, spread):
+    """The device's top-k over vocabularies spanning several key slots of the picking workgroup (the
+    last one partial) with exactly tied logits (duplicated rows of the tied embedding): 40 copies of
+    the row with about the third largest logit spread over slots and waves, the cut at the tied
+    value (kael keeps every entry equal to the k-th largest, so more than k are kept), small k
+    (the listed candidates above the lanes' maxima bound) and k > 1024 (every key); or every row
+    alike, so that the bound lists more keys than the workgroup stages and the kept list (all of
+    the vocabulary) goes to the global scratch."""
+    ref = refdev
+    h = ref.ref_gpt_create(vocab, 32, 1, 2, 8, 21, 1)
+    assert h, support.ref_error(ref)
+    try:
+        params = export_params(ref, h)
+        wte = dict(params)["token_embedding.weight"]
+        g = kd.Gpt(kdb, vocab, 32, 1, 2, 8, True)
+        for name, data in params:
+            g.load(name, data)
+        rng = np.random.default_rng(vocab)
+        prompt = rng.integers(0, vocab, 5)
+        g.prefill(prompt)  # greedy, for the prompt's logits
+        lg = g.logits()
+        if spread == "top":
+            # copies off the prompt's tokens leave the prompt's hidden state as it is
+            source = next(int(i) for i in np.argsort(-lg, kind="stable")[2:] if i not in prompt)
+            copies = rng.choice(np.setdiff1d(np.arange(vocab), np.append(prompt, source)), 40, replace=False)
+        else:
+            source, copies = 0, np.arange(vocab)
+        wte[copies] = wte[source]
+        g.load("token_embedding.weight", wte)
+        g.prefill(prompt)
+        lg = g.logits()
+        assert np.count_nonzero(lg == lg[source]) >= min(41, vocab)  # identical rows, identical logits
+        rank = int(np.count_nonzero(lg > lg[source]))
+        if spread == "top":
+            cases = [(0.9, rank + 1), (0.9, rank + 20), (1.1, vocab - 50)]
+        else:
+            cases = [(0.9, 40), (1.1, 1500)]
+        for temperature, top_k in cases:
+            steps = 6
+            u = rng.uniform(0, 1, steps + 1)
+            g.set_sampling(temperature, top_k)
+            g.set_uniforms(u)
+            g.prefill(prompt)
+            got = g.sequence()[-1]
+            assert got == oracle_pick(oracle, g.logits(), temperature, top_k, u[0]), (temperature, top_k)
+            for s in range(1, steps + 1):
+                got = g.decode(1)[0]
+                assert got == oracle_pick(oracle, g.logits(), temperature, top_k, u[s]), (temperature, top_k, s)
+            assert g.draws_used() == steps + 1
+        g.set_sampling(0.0)
+    finally:
+        ref.ref_gpt_destroy(h)
+
+
 def test_sampling_arguments_and_missing_draws_fail(kdb, refdev):
     ref = refdev
+    big = kd.Gpt(kdb, 65537, 16, 1, 2, 8, True)
+    with pytest.raises(kd.KdError, match="65536"):
+        big.set_sampling(0.8, 40)
+    del big
     h, g = build(kdb, ref, 11, 16, 1, 2, 8, 3)
     try:
         for t, k in [(0.8, 0), (0.8, 11), (-1.0, 3)]:
