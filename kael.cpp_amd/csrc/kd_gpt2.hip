@@ -662,10 +662,11 @@ struct PickArgs {
     const double* uniforms;
     int32_t* kept;   // [vocab] scratch: kept indices in index order, when more than kPickLdsKept
     float* kept_e;   // [vocab] scratch: their exponentials
-    const uint32_t* keys;  // [vocab] head_kernel's order keys of x = logits / temperature
+    const uint32_t* keys;  // [kPickSlots * kPickThreads] head_kernel's order keys of x = logits /
+                           // temperature, zero past the vocabulary
 };
 
-struct PickShared {
+struct alignas(16) PickShared {  // hist rows are read 16 bytes at a time
     uint32_t hist[kPickWaves][256];
     uint32_t counts[kPickSlots * kPickWaves];  // per (item group, wave), then their offsets
     int64_t wave_totals[kPickWaves];
@@ -716,8 +717,9 @@ __device__ __forceinline__ void wave_histogram_add(uint32_t* hist, uint32_t bin,
 
 // The rank-th largest (1-based) of the keys the lanes offer: visit(f) calls f(key, counted) for
 // each of the lane's keys, equally often in every lane of a wave. Four 8-bit digits from the top
-// with per-wave histograms; every thread of the workgroup calls it. rank must not exceed the
-// number of counted keys.
+// with per-wave histograms; wave 0 finds each digit (lane l sums bins 255 - 4l .. 252 - 4l over the
+// waves, a scan over the lanes finds the bin where the count from the top reaches the remaining
+// rank). Every thread of the workgroup calls it; rank must not exceed the number of counted keys.
 template <class Visit>
 __device__ __forceinline__ uint32_t radix_select(const Visit& visit, int64_t rank, PickShared& sh) {
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
@@ -731,16 +733,32 @@ __device__ __forceinline__ uint32_t radix_select(const Visit& visit, int64_t ran
             wave_histogram_add(sh.hist[wave], (key >> shift) & 255u, counted && (key & mask) == prefix);
         });
         __syncthreads();
-        // the digit: the bin b whose count from the top reaches the remaining rank
-        const int b = 255 - tid;  // lanes 0..255 take the bins from the top
-        int64_t n = 0;
-        if (tid < 256)
-            for (int w = 0; w < kPickWaves; ++w) n += sh.hist[w][b];
-        const int64_t need = sh.remaining;  // read before the scan's barriers; written after them
-        const int64_t from_top = block_inclusive_scan(tid < 256 ? n : 0, 256, sh.wave_totals);
-        if (tid < 256 && from_top >= need && from_top - n < need) {
-            sh.chosen = static_cast<uint32_t>(b);
-            sh.remaining = need - (from_top - n);
+        if (wave == 0) {
+            uint4 c = make_uint4(0, 0, 0, 0);  // .w: bin 255 - 4l, .z, .y, .x: the next three down
+            for (int w = 0; w < kPickWaves; ++w) {
+                const uint4 h = *reinterpret_cast<const uint4*>(&sh.hist[w][252 - 4 * lane]);
+                c.x += h.x;
+                c.y += h.y;
+                c.z += h.z;
+                c.w += h.w;
+            }
+            const uint32_t mine = c.x + c.y + c.z + c.w;
+            uint32_t through = mine;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(through), off));
+                if (lane >= off) through += o;
+            }
+            const int64_t need = sh.remaining;
+            const int64_t before = through - mine;
+            if (before < need && through >= need) {
+                const uint32_t bins[4] = {c.w, c.z, c.y, c.x};
+                int64_t run = before;
+                int q = 0;
+                while (q < 3 && run + bins[q] < need) run += bins[q++];
+                sh.chosen = static_cast<uint32_t>(255 - 4 * lane - q);
+                sh.remaining = need - run;
+            }
         }
         __syncthreads();
         prefix |= sh.chosen << shift;
@@ -749,40 +767,38 @@ __device__ __forceinline__ uint32_t radix_select(const Visit& visit, int64_t ran
     return prefix;
 }
 
-// Lists the lane's items j < groups (item j of lane t stands for j * kPickThreads + t) for which
-// keep(j) holds, in item order, which is (j, wave, lane) order: a count per (j, wave), an
-// exclusive scan of the counts, then each wave's items in lane order, emit(j, position, total)
-// writing one. Returns the total; every thread of the workgroup calls it.
-template <class Keep, class Emit>
-__device__ __forceinline__ int64_t ordered_compact(int groups, const Keep& keep, const Emit& emit, PickShared& sh) {
+// Lists the lane's items j (item j of lane t stands for j * kPickThreads + t) whose bit j of
+// `mine` is set, in item order, which is (j, wave, lane) order: a count per (j, wave) over the
+// items any lane of the wave keeps, an exclusive scan of the counts, then each wave's items in
+// lane order, emit(j, position, total) writing one. Returns the total; every thread of the
+// workgroup calls it.
+template <class Emit>
+__device__ __forceinline__ int64_t ordered_compact(uint64_t mine, const Emit& emit, PickShared& sh) {
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    uint64_t mine = 0;  // bit j: item j kept
-#pragma unroll
-    for (int j = 0; j < kPickSlots; ++j) {
-        if (j < groups) {
-            const bool k = keep(j);
-            mine |= uint64_t{k} << j;
-            const uint64_t lanes = __ballot(k);
-            if (lane == 0) sh.counts[j * kPickWaves + wave] = static_cast<uint32_t>(__popcll(lanes));
-        }
-    }
-    __syncthreads();
-    const int64_t c = tid / kPickWaves < groups ? sh.counts[tid] : 0;
-    const int64_t through = block_inclusive_scan(c, kPickThreads, sh.wave_totals);
-    sh.counts[tid] = static_cast<uint32_t>(through - c);
-    if (tid == kPickThreads - 1) sh.total = through;
-    __syncthreads();
-    const int64_t total = sh.total;
+    static_assert(kPickSlots * kPickWaves == kPickThreads);
+    sh.counts[tid] = 0;
     uint64_t wave_items = mine;
     for (int off = 32; off > 0; off >>= 1) {
         const uint32_t lo = __shfl_xor(static_cast<uint32_t>(wave_items), off);
         const uint32_t hi = __shfl_xor(static_cast<uint32_t>(wave_items >> 32), off);
         wave_items |= (uint64_t{hi} << 32) | lo;
     }
+    __syncthreads();
+    for (uint64_t rest = wave_items; rest != 0; rest &= rest - 1) {
+        const int j = __ffsll(static_cast<unsigned long long>(rest)) - 1;
+        const uint64_t lanes = __ballot((mine >> j) & 1);
+        if (lane == 0) sh.counts[j * kPickWaves + wave] = static_cast<uint32_t>(__popcll(lanes));
+    }
+    __syncthreads();
+    const int64_t c = sh.counts[tid];
+    const int64_t through = block_inclusive_scan(c, kPickThreads, sh.wave_totals);
+    sh.counts[tid] = static_cast<uint32_t>(through - c);
+    if (tid == kPickThreads - 1) sh.total = through;
+    __syncthreads();
+    const int64_t total = sh.total;
     const uint64_t below = (uint64_t{1} << lane) - 1;
-    while (wave_items != 0) {
-        const int j = __ffsll(static_cast<unsigned long long>(wave_items)) - 1;
-        wave_items &= wave_items - 1;
+    for (uint64_t rest = wave_items; rest != 0; rest &= rest - 1) {
+        const int j = __ffsll(static_cast<unsigned long long>(rest)) - 1;
         const bool k = (mine >> j) & 1;
         const uint64_t lanes = __ballot(k);
         if (k) emit(j, sh.counts[j * kPickWaves + wave] + __popcll(lanes & below), total);
@@ -795,28 +811,29 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     __shared__ PickShared sh;
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int64_t V = a.vocab;
-    const int slots = static_cast<int>((V + kPickThreads - 1) / kPickThreads);
     const int64_t top_k = a.sp->top_k;
-    // the keys, slot s of lane t holding index s * 1024 + t (0 past the vocabulary, below every
-    // finite x's key; each phase reads them again from L2 rather than holding 64 registers over the
-    // barriers); the lane's largest, and the smallest over the vocabulary
-    // (buffer loads: one lane offset and a scalar offset per slot, where 64 global addresses would
-    // hold 128 registers over the passes)
-    const __amdgpu_buffer_rsrc_t keys_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(a.keys), 0, static_cast<int32_t>(V * sizeof(uint32_t)), kRawBufferWord3);
+    // this pick's draw, read now so that its loads overlap the selection
+    const int64_t draw = a.sp->draw, draws = a.sp->draws;
+    const double u = draw < draws ? a.uniforms[draw] : 0.0;
+    // The keys, slot s of lane t holding index s * 1024 + t; the buffer holds all 64 slots with
+    // zeros past the vocabulary (below every finite x's key), so the loads need no branches and
+    // all go out at once. Buffer loads: one lane offset and a scalar offset per slot, where 64
+    // global addresses would take 128 registers.
+    const __amdgpu_buffer_rsrc_t keys_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.keys), 0,
+                                          int32_t{kPickSlots * kPickThreads * sizeof(uint32_t)}, kRawBufferWord3);
     const auto key_at = [&](int s) -> uint32_t {
-        return int64_t{s} * kPickThreads + tid < V
-                   ? __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, tid * 4, s * kPickThreads * 4, 0)
-                   : 0u;
+        return __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, tid * 4, s * kPickThreads * 4, 0);
     };
+    uint32_t key[kPickSlots];
+#pragma unroll
+    for (int s = 0; s < kPickSlots; ++s) key[s] = key_at(s);
+    // the lane's largest key; the smallest over the vocabulary
     uint32_t tmax = 0, tmin = ~0u;
 #pragma unroll
     for (int s = 0; s < kPickSlots; ++s) {
-        if (s < slots) {
-            const uint32_t k = key_at(s);
-            tmax = max(tmax, k);
-            if (int64_t{s} * kPickThreads + tid < V) tmin = min(tmin, k);
-        }
+        tmax = max(tmax, key[s]);
+        tmin = min(tmin, int64_t{s} * kPickThreads + tid < V ? key[s] : ~0u);
     }
     uint32_t wm = tmax, wn = tmin;
     for (int off = 32; off > 0; off >>= 1) {
@@ -837,12 +854,16 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     // kept): for k <= 1024 the k-th largest lane maximum; the keys at or above it listed in index
     // order with their indices when they fit the LDS
     uint32_t low = 1;
+    if (top_k <= kPickThreads) low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh));
+    uint64_t above = 0;  // bit s: slot s's key >= low (the keys loaded again: holding them across
+                         // the selection would spill)
+#pragma unroll
+    for (int s = 0; s < kPickSlots; ++s) above |= uint64_t{key_at(s) >= low} << s;
     bool listed = false;
     int64_t listed_n = 0;
     if (top_k <= kPickThreads) {
-        low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh));
         listed_n = ordered_compact(
-            slots, [&](int s) { return key_at(s) >= low; },
+            above,
             [&](int s, int64_t at, int64_t total) {
                 if (total <= kPickLdsKept) {
                     const int32_t i = s * kPickThreads + tid;
@@ -854,23 +875,27 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
         listed = listed_n <= kPickLdsKept;
     }
     // the k-th largest key and the kept entries (keys at or above it) in index order
+    constexpr int kListGroups = kPickLdsKept / kPickThreads;
     int64_t m;
     int32_t* kept;
     float* kept_e;
     if (listed) {
-        const int groups = static_cast<int>((listed_n + kPickThreads - 1) / kPickThreads);
         const auto listed_key = [&](int j) {
             const int64_t r = int64_t{j} * kPickThreads + tid;
             return r < listed_n ? sh.cand_key[r] : 0u;
         };
+        const int groups = static_cast<int>((listed_n + kPickThreads - 1) / kPickThreads);
         const uint32_t kth = radix_select(
             [&](const auto& f) {
                 for (int j = 0; j < groups; ++j) f(listed_key(j), int64_t{j} * kPickThreads + tid < listed_n);
             },
             top_k, sh);
+        uint64_t keep = 0;
+#pragma unroll
+        for (int j = 0; j < kListGroups; ++j)
+            keep |= uint64_t{int64_t{j} * kPickThreads + tid < listed_n && listed_key(j) >= kth} << j;
         m = ordered_compact(
-            groups, [&](int j) { return int64_t{j} * kPickThreads + tid < listed_n && listed_key(j) >= kth; },
-            [&](int j, int64_t at, int64_t) { sh.kept_i[at] = sh.cand_idx[j * kPickThreads + tid]; }, sh);
+            keep, [&](int j, int64_t at, int64_t) { sh.kept_i[at] = sh.cand_idx[j * kPickThreads + tid]; }, sh);
         kept = sh.kept_i;
         kept_e = sh.kept_e;
     } else {
@@ -878,15 +903,16 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
                                           [&](const auto& f) {
 #pragma unroll
                                               for (int s = 0; s < kPickSlots; ++s) {
-                                                  if (s < slots) {
-                                                      const uint32_t k = key_at(s);
-                                                      f(k, k >= low);
-                                                  }
+                                                  const uint32_t k = key_at(s);
+                                                  f(k, k >= low);
                                               }
                                           },
                                           top_k, sh));
+        uint64_t keep = 0;
+#pragma unroll
+        for (int s = 0; s < kPickSlots; ++s) keep |= uint64_t{key_at(s) >= kth} << s;
         m = ordered_compact(
-            slots, [&](int s) { return key_at(s) >= kth; },
+            keep,
             [&](int s, int64_t at, int64_t total) {
                 (total <= kPickLdsKept ? sh.kept_i : a.kept)[at] = s * kPickThreads + tid;
             },
@@ -909,13 +935,11 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
         return static_cast<double>(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j)));
     };
     Sampler& sp = *a.sp;
-    const int64_t draw = sp.draw;
-    if (nonfinite || draw >= sp.draws) {
+    if (nonfinite || draw >= draws) {
         if (lane == 0) sp.error = nonfinite ? 1 : 2;
         token = 0;
         return;
     }
-    const double u = a.uniforms[draw];
     if (lane == 0) sp.draw = draw + 1;
     // the sum of e in double in index order, rounded to f32
     double sum = 0.0;
@@ -1260,7 +1284,7 @@ struct Engine {
     double* uniforms = nullptr;  // [max_positions + 1] draws for sampled picks
     int32_t* kept = nullptr;     // [vocab] sampling scratch
     float* kept_e = nullptr;     // [vocab]
-    uint32_t* keys = nullptr;    // [vocab] order keys of the sampled pick's x
+    uint32_t* keys = nullptr;    // [65536] order keys of the sampled pick's x, zero past the vocabulary
     Sampler host_sp{0.f, 0, 0, 0, 0};
     hipGraphExec_t graph = nullptr;
     int64_t host_pos = 0;     // mirror of st->pos: positions in the KV cache
@@ -1709,7 +1733,8 @@ int create(Engine& e, const kd_gpt_config& c) {
     if (int rc = alloc(&e.uniforms, c.max_positions + 1)) return rc;
     if (int rc = alloc(&e.kept, c.vocab_size)) return rc;
     if (int rc = alloc(&e.kept_e, c.vocab_size)) return rc;
-    if (int rc = alloc(&e.keys, c.vocab_size)) return rc;
+    if (int rc = alloc(&e.keys, int64_t{kPickSlots} * kPickThreads)) return rc;
+    KD_HIP(hipMemset(e.keys, 0, size_t{kPickSlots} * kPickThreads * sizeof(uint32_t)));  // past the vocabulary: 0
     KD_HIP(hipMemcpy(e.sp, &e.host_sp, sizeof(Sampler), hipMemcpyHostToDevice));  // greedy
     return KD_OK;
 }
