@@ -1128,11 +1128,11 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
 // ---- batched prefill ---------------------------------------------------------------------------
 //
 // The prompt's T positions pass each layer together: row LayerNorms, the four Linear products
-// as GEMMs on the MFMA matmul path (activation rows padded to whole 128-row tiles, weights in
-// [in, out] copies made once so that both operands are row-major and few-tile products get
-// split K), epilogue kernels for the bias, residual, GELU and the K/V rows into the cache, and a
-// causal attention kernel. Same arithmetic as the decode step; only the summation order of the
-// dot products differs.
+// as GEMMs on the MFMA matmul path (weights in [in, out] copies made once so that both operands
+// are row-major; prompts of up to 128 positions as split-K partial products on 64x64 tiles, longer
+// ones on the backend's matmul path with rows padded to 128), epilogue kernels for the partial
+// sums, the bias, residual, GELU and the K/V rows into the cache, and a causal attention kernel.
+// Same arithmetic as the decode step; only the summation order of the dot products differs.
 
 // X[t] = wte[seq[t]] + wpe[t].
 __global__ __launch_bounds__(kThreads) void prefill_embed_kernel(const int64_t* seq, const float* wte, const float* wpe,
@@ -1152,20 +1152,32 @@ __global__ __launch_bounds__(kThreads) void ln_rows_kernel(const float* X, const
     ln_finish(r, d, H + t * d);
 }
 
-// y = P[t, n] + bias[n] for the T x N product P (row stride N), then by epilogue:
+// y = P[t, n] + bias[n] for the T x N product P (row stride N; with split K, P[t, n] is the sum
+// of the `splits` partial products P + s * split_stride in split order), then by epilogue:
 //   kQkv       query part -> Q[t, n]; key and value parts -> the cache rows of position t
 //   kResidual  X[t, n] = X[t, n] + y
 //   kGelu*     F[t, n] = gelu(y)
 template <int Epi>
-__global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float* P, const float* bias, float* out, int64_t T,
-                                                                    int64_t N, int64_t d, int64_t head_dim,
-                                                                    int64_t max_positions, float* kcache, float* vcache) {
+__global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float* P, int64_t splits, int64_t split_stride,
+                                                                    const float* bias, float* out, int64_t T, int64_t N,
+                                                                    int64_t d, int64_t head_dim, int64_t max_positions,
+                                                                    float* kcache, float* vcache) {
     const int64_t total = T * N;
     for (int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; e < total;
          e += static_cast<int64_t>(gridDim.x) * kThreads) {
         const int64_t t = e / N;
         const int64_t n = e - t * N;
-        const float y = __fadd_rn(P[e], bias[n]);
+        float p = P[e];
+        int64_t s = 1;
+        for (; s + 8 <= splits; s += 8) {  // eight partials' loads in flight, added in split order
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = P[(s + j) * split_stride + e];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) p = __fadd_rn(p, v[j]);
+        }
+        for (; s < splits; ++s) p = __fadd_rn(p, P[s * split_stride + e]);
+        const float y = __fadd_rn(p, bias[n]);
         if constexpr (Epi == kQkv) {
             const int64_t part = n / d;
             const int64_t within = n - part * d;
@@ -1299,6 +1311,7 @@ struct Engine {
     float* pf_a = nullptr;    // [pf_rows, d] attention output
     float* pf_f = nullptr;    // [pf_rows, ff] GELU output
     float* pf_p = nullptr;    // [pf_rows, max(3d, ff)] product before its epilogue
+    float* pf_parts = nullptr;  // split-K partial products of prompts of at most 128 positions
     float* wt = nullptr;      // per layer: qkv^T [d, 3d], proj^T [d, d], fc1^T [d, ff], fc2^T [ff, d]
     bool wt_valid = false;    // cleared by every parameter upload
 
@@ -1474,8 +1487,26 @@ struct Engine {
         void* mem = nullptr;
         KD_HIP(hipMalloc(&mem, static_cast<size_t>(cfg.layers * layer_t_floats()) * sizeof(float)));
         wt = static_cast<float*>(mem);
+        mem = nullptr;
+        KD_HIP(hipMalloc(&mem, static_cast<size_t>(parts_floats()) * sizeof(float)));
+        pf_parts = static_cast<float*>(mem);
         return KD_OK;
     }
+
+    // Prompts of at most kShortPrompt positions: rows padded to 64 and the products split over K
+    // into pf_parts (at most one 64x64-tile workgroup per CU, or one whole product), which the
+    // epilogue adds in split order.
+    static constexpr int64_t kShortPrompt = 128;
+    int64_t parts_floats() const {
+        return std::max<int64_t>(int64_t{compute_units()} * 64 * 64, kShortPrompt * std::max(3 * d, ff));
+    }
+
+    // A product ready for its epilogue: P (row stride N), or `splits` partials `stride` apart.
+    struct Product {
+        const float* P;
+        int64_t splits;
+        int64_t stride;
+    };
 
     // dst [K, N] row-major = transpose of src [N, K] row-major (kael's Linear weight).
     static int transpose_into(float* dst, const float* src, int64_t N, int64_t K) {
@@ -1507,18 +1538,36 @@ struct Engine {
         return KD_OK;
     }
 
-    // P[rows, N] = A[rows, K] . Wt[K, N] on the backend's matmul path (rows = T rounded up to
-    // 128; the padding rows hold leftovers of earlier rows and their products are ignored).
-    static int product(const float* A, const float* Wt, float* P, int64_t rows, int64_t K, int64_t N) {
-        kd_matmul_sizes sz{1, rows, K, N};
-        return kd_matmul(KD_F32, A, Wt, P, &sz);
+    // A[T, K] . Wt[K, N] for the T positions of the prompt. Up to kShortPrompt positions with N a
+    // multiple of 64 and K of 32: rows padded to 64, K split so that the 64x64-tile grid holds up to
+    // one workgroup per CU (GPT-2 small at T = 64: qkv 36 tiles x 6, proj 12 x 12, fc1 48 x 4,
+    // fc2 12 x 16; measured against two and four per CU and against a half and three quarters of
+    // the CUs: 0.79 ms for the 64-token prefill against 0.87, 0.94, 0.89 and 0.80), the partials
+    // left for the epilogue to add; each product reads its weights once. Otherwise the backend's matmul path on rows padded to 128. Padding rows hold leftovers
+    // of earlier rows; their products are ignored.
+    int product(const float* A, const float* Wt, int64_t T, int64_t K, int64_t N, Product* out) const {
+        const auto aligned = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+        if (T <= kShortPrompt && N % 64 == 0 && K % 32 == 0 && aligned(A) && aligned(Wt)) {
+            const int64_t rows = (T + 63) / 64 * 64;
+            const int64_t tiles = rows / 64 * (N / 64);
+            const int64_t steps = K / 32;
+            int64_t splits = 1;
+            for (int64_t c = 1; c <= steps; ++c)
+                if (steps % c == 0 && tiles * c <= compute_units()) splits = c;
+            *out = Product{pf_parts, splits, rows * N};
+            return kd::matmul_split_parts(A, Wt, pf_parts, rows, N, K, K, N, splits);
+        }
+        kd_matmul_sizes sz{1, (T + 127) / 128 * 128, K, N};
+        *out = Product{pf_p, 1, 0};
+        return kd_matmul(KD_F32, A, Wt, pf_p, &sz);
     }
 
-    template <int Epi> void epilogue(const float* bias, float* out, int64_t T, int64_t N, float* kc, float* vc) const {
+    template <int Epi>
+    void epilogue(const Product& pr, const float* bias, float* out, int64_t T, int64_t N, float* kc, float* vc) const {
         const int64_t total = T * N;
         const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{compute_units()} * 16);
         hipLaunchKernelGGL((prefill_epilogue_kernel<Epi>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, kd::stream(),
-                           pf_p, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
+                           pr.P, pr.splits, pr.stride, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
     }
 
     // Positions 0..T-1 of seq (already on the device) through every layer at once; then the
@@ -1527,7 +1576,7 @@ struct Engine {
         if (int rc = ensure_prefill_buffers()) return rc;
         if (int rc = refresh_transposed()) return rc;
         hipStream_t s = kd::stream();
-        const int64_t rows = (T + 127) / 128 * 128;
+        Product pr{};
         const float divisor = static_cast<float>(std::sqrt(static_cast<double>(hd)));
         hipLaunchKernelGGL(prefill_embed_kernel, dim3(static_cast<uint32_t>((d + kThreads - 1) / kThreads), static_cast<uint32_t>(T)),
                            dim3(kThreads), 0, s, seq, p("token_embedding.weight"), p("position_embedding.weight"), pf_x, d);
@@ -1538,20 +1587,20 @@ struct Engine {
             float* vc = vcache + l * cfg.heads * cfg.max_positions * hd;
             hipLaunchKernelGGL(ln_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pf_x, p(b + "ln1.weight"),
                                p(b + "ln1.bias"), pf_h, d);
-            if (int rc = product(pf_h, wt_qkv(l), pf_p, rows, d, 3 * d)) return rc;
-            epilogue<kQkv>(p(b + "attn.qkv.bias"), pf_q, T, 3 * d, kc, vc);
+            if (int rc = product(pf_h, wt_qkv(l), T, d, 3 * d, &pr)) return rc;
+            epilogue<kQkv>(pr, p(b + "attn.qkv.bias"), pf_q, T, 3 * d, kc, vc);
             hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<uint32_t>(cfg.heads), static_cast<uint32_t>(T)),
                                dim3(kThreads), static_cast<size_t>(T) * sizeof(float), s, pf_q, kc, vc, pf_a, d, hd,
                                cfg.max_positions, divisor);
-            if (int rc = product(pf_a, wt_proj(l), pf_p, rows, d, d)) return rc;
-            epilogue<kResidual>(p(b + "attn.proj.bias"), pf_x, T, d, nullptr, nullptr);
+            if (int rc = product(pf_a, wt_proj(l), T, d, d, &pr)) return rc;
+            epilogue<kResidual>(pr, p(b + "attn.proj.bias"), pf_x, T, d, nullptr, nullptr);
             hipLaunchKernelGGL(ln_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pf_x, p(b + "ln2.weight"),
                                p(b + "ln2.bias"), pf_h, d);
-            if (int rc = product(pf_h, wt_fc1(l), pf_p, rows, d, ff)) return rc;
-            if (cfg.tanh_gelu) epilogue<kGeluTanh>(p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
-            else epilogue<kGeluExact>(p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
-            if (int rc = product(pf_f, wt_fc2(l), pf_p, rows, ff, d)) return rc;
-            epilogue<kResidual>(p(b + "mlp.fc2.bias"), pf_x, T, d, nullptr, nullptr);
+            if (int rc = product(pf_h, wt_fc1(l), T, d, ff, &pr)) return rc;
+            if (cfg.tanh_gelu) epilogue<kGeluTanh>(pr, p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
+            else epilogue<kGeluExact>(pr, p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
+            if (int rc = product(pf_f, wt_fc2(l), T, ff, d, &pr)) return rc;
+            epilogue<kResidual>(pr, p(b + "mlp.fc2.bias"), pf_x, T, d, nullptr, nullptr);
             KD_LAUNCH_CHECK();
         }
         GemvArgs head = base();
@@ -1636,7 +1685,7 @@ struct Engine {
     ~Engine() {
         if (graph) (void)hipGraphExecDestroy(graph);
         for (void* ptr : {static_cast<void*>(pf_x), static_cast<void*>(pf_h), static_cast<void*>(pf_q),
-                          static_cast<void*>(pf_a), static_cast<void*>(pf_f), static_cast<void*>(pf_p),
+                          static_cast<void*>(pf_a), static_cast<void*>(pf_f), static_cast<void*>(pf_p), static_cast<void*>(pf_parts),
                           static_cast<void*>(wt)})
             if (ptr) (void)hipFree(ptr);
         for (void* ptr : {static_cast<void*>(params), static_cast<void*>(kcache), static_cast<void*>(vcache),

@@ -52,6 +52,14 @@ struct Workspace {
 };
 int workspace(Workspace& lease, size_t bytes);
 
+// Split-K partial products for callers inside the library (the GPT-2 engine's prefill): with
+// row-major A [M, K] (row stride lda) and B [K, N] (row stride ldb), parts[s][m][n] (row stride N,
+// split stride M * N) is the product over K range [s * K / splits, (s + 1) * K / splits), on the
+// 64x64 MFMA tiles, for s < splits. M and N multiples of 64, K a multiple of 32 * splits, lda and
+// ldb multiples of 4 with 16-byte aligned operands; the caller adds the partials in split order.
+int matmul_split_parts(const float* a, const float* b, float* parts, int64_t M, int64_t N, int64_t K, int64_t lda,
+                       int64_t ldb, int64_t splits);
+
 inline int64_t dtype_size(int dtype) {
     switch (dtype) {
     case KD_F32: return 4;

@@ -1698,6 +1698,22 @@ int dispatch(int dtype, const void* a, const void* b, void* out, const MatmulArg
 
 } // namespace
 
+int matmul_split_parts(const float* a, const float* b, float* parts, int64_t M, int64_t N, int64_t K, int64_t lda,
+                       int64_t ldb, int64_t splits) {
+    constexpr int64_t kMax = int64_t{1} << 31;
+    if (M <= 0 || N <= 0 || splits < 1 || M % kT64 != 0 || N % kT64 != 0 || K % (kT64K * splits) != 0 || lda % 4 != 0 ||
+        ldb % 4 != 0 || !aligned16(a) || !aligned16(b) || !aligned16(parts) || M * lda >= kMax || K * ldb >= kMax ||
+        splits * M * N >= kMax || splits > 65535)
+        return fail(KD_E_INVALID, "matmul_split_parts: operands outside the 64x64 split-K kernel's bounds");
+    const int64_t tiles = (M / kT64) * (N / kT64);
+    const int64_t kc = K / splits;
+    hipLaunchKernelGGL((mfma_f32_t64_kernel<false, false>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
+                       dim3(kThreads), 0, stream(), a, b, parts, static_cast<int>(M), static_cast<int>(N),
+                       static_cast<int>(kc), static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(N),
+                       batch_strides(kc, kc * ldb, M * N));
+    return launch_status();
+}
+
 } // namespace kd
 
 using namespace kd;

@@ -202,15 +202,16 @@ def test_small_model_batched_prefill(kdb, refdev, prompt_len):
 
 
 def test_gpt2_small_batched_prefill(kdb, refdev):
-    """Config C5 with prompts of 64, 300 (three 128-row tiles) and 600 positions (decode steps
-    past 512 cached keys): the prompt's last logits and three decode steps within 1e-4 of the
-    largest logit, kael's greedy tokens."""
+    """Config C5 with prompts of 1, 64 and 100 positions (split-K partial products on 64-row
+    tiles, one and two of them), 129, 300 (128-row tiles) and 600 positions (decode steps past
+    512 cached keys): the prompt's last logits and three decode steps within 1e-4 of the largest
+    logit, kael's greedy tokens."""
     ref = refdev
     ref.ref_set_threads(min(16, max(1, __import__("os").cpu_count() or 1)))
     h, g = build(kdb, ref, 50257, 1024, 12, 12, 768, 4)
     try:
         rng = np.random.default_rng(5)
-        for prompt_len in (64, 300, 600):
+        for prompt_len in (1, 64, 100, 129, 300, 600):
             check_prefill_and_steps(g, ref, h, rng.integers(0, 50257, prompt_len), 3, 50257, 1e-4)
     finally:
         ref.ref_gpt_destroy(h)
