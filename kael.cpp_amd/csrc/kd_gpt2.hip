@@ -1134,29 +1134,99 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
 // sums, the bias, residual, GELU and the K/V rows into the cache, and a causal attention kernel.
 // Same arithmetic as the decode step; only the summation order of the dot products differs.
 
-// X[t] = wte[seq[t]] + wpe[t].
-__global__ __launch_bounds__(kThreads) void prefill_embed_kernel(const int64_t* seq, const float* wte, const float* wpe,
-                                                                 float* X, int64_t d) {
-    const int64_t t = blockIdx.y;
-    const int64_t tok = seq[t];
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < d;
-         i += static_cast<int64_t>(gridDim.x) * kThreads)
-        X[t * d + i] = __fadd_rn(wte[tok * d + i], wpe[t * d + i]);
+// The row LayerNorm H[t] = LayerNorm(X[t]) of a row that lane i of the workgroup has just
+// computed at elements i, i + 256, ... (x[j], j < 4), as ln_load and ln_finish compute it from
+// memory: the pivot x[0] passes through LDS.
+__device__ __forceinline__ void ln_row_from_lanes(const float (&x)[4], int64_t d, const float* w, const float* b,
+                                                  float* h) {
+    __shared__ float pivot;
+    LnIn r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        r.x[j] = i < d ? x[j] : 0.f;
+        r.w[j] = i < d ? w[i] : 0.f;
+        r.b[j] = i < d ? b[i] : 0.f;
+    }
+    if (threadIdx.x == 0) pivot = x[0];
+    __syncthreads();
+    r.c = pivot;
+    ln_finish(r, d, h);
 }
 
-// H[t] = LayerNorm(X[t]), one workgroup per row.
-__global__ __launch_bounds__(kThreads) void ln_rows_kernel(const float* X, const float* w, const float* b, float* H,
-                                                           int64_t d) {
+// X[t] = wte[seq[t]] + wpe[t], and H[t] = LayerNorm(X[t]) with the first block's ln1; one
+// workgroup per row.
+__global__ __launch_bounds__(kThreads) void prefill_embed_kernel(const int64_t* seq, const float* wte, const float* wpe,
+                                                                 float* X, const float* ln_w, const float* ln_b,
+                                                                 float* H, int64_t d) {
     const int64_t t = blockIdx.x;
-    const LnIn r = ln_load(X + t * d, d, w, b);
-    ln_finish(r, d, H + t * d);
+    const int64_t tok = seq[t];
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        x[j] = 0.f;
+        if (i < d) {
+            x[j] = __fadd_rn(wte[tok * d + i], wpe[t * d + i]);
+            X[t * d + i] = x[j];
+        }
+    }
+    ln_row_from_lanes(x, d, ln_w, ln_b, H + t * d);
+}
+
+// The residual epilogue of a d-wide product, one workgroup per row: X[t, n] += P[t, n] + bias[n]
+// (P the sum of `splits` partials `split_stride` apart, added in split order), then, with ln_w,
+// H[t] = LayerNorm(X[t]) for the next product (the following LayerNorm, computed in the same
+// workgroup instead of a launch of its own).
+__global__ __launch_bounds__(kThreads) void prefill_residual_kernel(const float* P, int64_t splits, int64_t split_stride,
+                                                                    const float* bias, float* X, const float* ln_w,
+                                                                    const float* ln_b, float* H, int64_t d) {
+    const int64_t t = blockIdx.x;
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        p[j] = i < d ? P[t * d + i] : 0.f;
+    }
+    int64_t s = 1;
+    for (; s + 4 <= splits; s += 4) {  // the partials' loads in flight together, added in split order
+        float v[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t i = threadIdx.x + j * kThreads;
+                v[q][j] = i < d ? P[(s + q) * split_stride + t * d + i] : 0.f;
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = __fadd_rn(p[j], v[q][j]);
+    }
+    for (; s < splits; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t i = threadIdx.x + j * kThreads;
+            if (i < d) p[j] = __fadd_rn(p[j], P[s * split_stride + t * d + i]);
+        }
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        x[j] = 0.f;
+        if (i < d) {
+            x[j] = __fadd_rn(X[t * d + i], __fadd_rn(p[j], bias[i]));
+            X[t * d + i] = x[j];
+        }
+    }
+    if (ln_w != nullptr) ln_row_from_lanes(x, d, ln_w, ln_b, H + t * d);
 }
 
 // y = P[t, n] + bias[n] for the T x N product P (row stride N; with split K, P[t, n] is the sum
 // of the `splits` partial products P + s * split_stride in split order), then by epilogue:
 //   kQkv       query part -> Q[t, n]; key and value parts -> the cache rows of position t
-//   kResidual  X[t, n] = X[t, n] + y
 //   kGelu*     F[t, n] = gelu(y)
+// (the residual products take prefill_residual_kernel, which also computes the next LayerNorm).
 template <int Epi>
 __global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float* P, int64_t splits, int64_t split_stride,
                                                                     const float* bias, float* out, int64_t T, int64_t N,
@@ -1189,9 +1259,8 @@ __global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float*
                 float* cache = part == 1 ? kcache : vcache;
                 cache[(head * max_positions + t) * head_dim + dim] = y;
             }
-        } else if constexpr (Epi == kResidual) {
-            out[e] = __fadd_rn(out[e], y);
         } else {
+            static_assert(Epi == kGeluTanh || Epi == kGeluExact);
             out[e] = gelu_of<Epi>(y);
         }
     }
@@ -1578,29 +1647,34 @@ struct Engine {
         hipStream_t s = kd::stream();
         Product pr{};
         const float divisor = static_cast<float>(std::sqrt(static_cast<double>(hd)));
-        hipLaunchKernelGGL(prefill_embed_kernel, dim3(static_cast<uint32_t>((d + kThreads - 1) / kThreads), static_cast<uint32_t>(T)),
-                           dim3(kThreads), 0, s, seq, p("token_embedding.weight"), p("position_embedding.weight"), pf_x, d);
+        hipLaunchKernelGGL(prefill_embed_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, seq,
+                           p("token_embedding.weight"), p("position_embedding.weight"), pf_x, p("blocks.0.ln1.weight"),
+                           p("blocks.0.ln1.bias"), pf_h, d);
         KD_LAUNCH_CHECK();
+        // X += P + bias per row, then H = the next LayerNorm of X (none after the last block: the
+        // head kernel normalises the last row itself)
+        const auto residual = [&](const float* bias, const float* ln_w, const float* ln_b) {
+            hipLaunchKernelGGL(prefill_residual_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pr.P, pr.splits,
+                               pr.stride, bias, pf_x, ln_w, ln_b, pf_h, d);
+        };
         for (int64_t l = 0; l < cfg.layers; ++l) {
             const std::string b = "blocks." + std::to_string(l) + ".";
+            const std::string next = "blocks." + std::to_string(l + 1) + ".";
+            const bool last = l + 1 == cfg.layers;
             float* kc = kcache + l * cfg.heads * cfg.max_positions * hd;
             float* vc = vcache + l * cfg.heads * cfg.max_positions * hd;
-            hipLaunchKernelGGL(ln_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pf_x, p(b + "ln1.weight"),
-                               p(b + "ln1.bias"), pf_h, d);
             if (int rc = product(pf_h, wt_qkv(l), T, d, 3 * d, &pr)) return rc;
             epilogue<kQkv>(pr, p(b + "attn.qkv.bias"), pf_q, T, 3 * d, kc, vc);
             hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<uint32_t>(cfg.heads), static_cast<uint32_t>(T)),
                                dim3(kThreads), static_cast<size_t>(T) * sizeof(float), s, pf_q, kc, vc, pf_a, d, hd,
                                cfg.max_positions, divisor);
             if (int rc = product(pf_a, wt_proj(l), T, d, d, &pr)) return rc;
-            epilogue<kResidual>(pr, p(b + "attn.proj.bias"), pf_x, T, d, nullptr, nullptr);
-            hipLaunchKernelGGL(ln_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kThreads), 0, s, pf_x, p(b + "ln2.weight"),
-                               p(b + "ln2.bias"), pf_h, d);
+            residual(p(b + "attn.proj.bias"), p(b + "ln2.weight"), p(b + "ln2.bias"));
             if (int rc = product(pf_h, wt_fc1(l), T, d, ff, &pr)) return rc;
             if (cfg.tanh_gelu) epilogue<kGeluTanh>(pr, p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
             else epilogue<kGeluExact>(pr, p(b + "mlp.fc1.bias"), pf_f, T, ff, nullptr, nullptr);
             if (int rc = product(pf_f, wt_fc2(l), T, ff, d, &pr)) return rc;
-            epilogue<kResidual>(pr, p(b + "mlp.fc2.bias"), pf_x, T, d, nullptr, nullptr);
+            residual(p(b + "mlp.fc2.bias"), last ? nullptr : p(next + "ln1.weight"), last ? nullptr : p(next + "ln1.bias"));
             KD_LAUNCH_CHECK();
         }
         GemvArgs head = base();
