@@ -649,6 +649,7 @@ constexpr int kPickLdsKept = 4096;     // listed entries staged in LDS; more kep
 static_assert(int64_t{kPickThreads} * kPickSlots == KD_GPT_SAMPLE_MAX_VOCAB);
 static_assert(kPickLdsKept % kPickThreads == 0 && kPickLdsKept / kPickThreads <= kPickSlots);
 constexpr int32_t kRawBufferWord3 = 0x00020000;  // buffer descriptor word 3: 32-bit data format
+constexpr int64_t kRankList = 256;  // candidate lists up to this long: k-th key by rank counting
 
 struct PickArgs {
     Step* st;
@@ -669,14 +670,17 @@ struct PickArgs {
 struct alignas(16) PickShared {  // hist rows are read 16 bytes at a time
     uint32_t hist[kPickWaves][256];
     uint32_t counts[kPickSlots * kPickWaves];  // per (item group, wave), then their offsets
+    uint32_t wave_items[kPickWaves][2];       // per wave: the item groups any lane keeps
     int64_t wave_totals[kPickWaves];
+    uint32_t wave_totals32[kPickWaves];
     uint32_t wmax[kPickWaves];
     uint32_t wmin[kPickWaves];
     uint32_t chosen;
     int64_t remaining;
     int64_t total;
-    uint32_t cand_key[kPickLdsKept];  // listed keys >= the lower bound, in index order
-    int32_t cand_idx[kPickLdsKept];
+    alignas(16) uint32_t cand_key[kPickLdsKept + 4];  // listed keys >= the lower bound, zeros after them
+    alignas(16) int32_t cand_idx[kPickLdsKept + 4];   // their indices
+    uint32_t appended;                                // keys appended to the unordered short list
     float kept_e[kPickLdsKept];       // kept entries, when at most kPickLdsKept
     int32_t kept_i[kPickLdsKept];
 };
@@ -694,6 +698,23 @@ __device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int n, int64_
     __syncthreads();
     int64_t before = 0;
     for (int w = 0; w < wave && w < n / 64; ++w) before += wave_totals[w];
+    __syncthreads();
+    return v + before;
+}
+
+// Inclusive prefix sum of 32-bit v over the whole workgroup (sums below 2^32); every thread of
+// the workgroup must call it.
+__device__ __forceinline__ uint32_t block_inclusive_scan32(uint32_t v, uint32_t* wave_totals) {
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(v), off));
+        if (lane >= off) v += o;
+    }
+    if (lane == 63) wave_totals[wave] = v;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_totals[w];
     __syncthreads();
     return v + before;
 }
@@ -716,17 +737,18 @@ __device__ __forceinline__ void wave_histogram_add(uint32_t* hist, uint32_t bin,
 }
 
 // The rank-th largest (1-based) of the keys the lanes offer: visit(f) calls f(key, counted) for
-// each of the lane's keys, equally often in every lane of a wave. Four 8-bit digits from the top
+// each of the lane's keys, equally often in every lane of a wave (with fewer than four digits, its
+// top 8 * digits bits and zeros below: a lower bound). 8-bit digits from the top
 // with per-wave histograms; wave 0 finds each digit (lane l sums bins 255 - 4l .. 252 - 4l over the
 // waves, a scan over the lanes finds the bin where the count from the top reaches the remaining
 // rank). Every thread of the workgroup calls it; rank must not exceed the number of counted keys.
 template <class Visit>
-__device__ __forceinline__ uint32_t radix_select(const Visit& visit, int64_t rank, PickShared& sh) {
+__device__ __forceinline__ uint32_t radix_select(const Visit& visit, int64_t rank, PickShared& sh, int digits = 4) {
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     if (tid == 0) sh.remaining = rank;
     uint32_t prefix = 0, mask = 0;
 #pragma unroll 1
-    for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int shift = 24; shift >= 32 - 8 * digits; shift -= 8) {
         for (int b = lane; b < 256; b += 64) sh.hist[wave][b] = 0;
         __syncthreads();
         visit([&](uint32_t key, bool counted) {
@@ -777,22 +799,23 @@ __device__ __forceinline__ int64_t ordered_compact(uint64_t mine, const Emit& em
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     static_assert(kPickSlots * kPickWaves == kPickThreads);
     sh.counts[tid] = 0;
-    uint64_t wave_items = mine;
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(wave_items), off);
-        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(wave_items >> 32), off);
-        wave_items |= (uint64_t{hi} << 32) | lo;
+    if (lane == 0) sh.wave_items[wave][0] = sh.wave_items[wave][1] = 0;
+    __syncthreads();
+    if (mine != 0) {  // the wave's union of items: LDS ORs from the (usually few) lanes that keep some
+        atomicOr(&sh.wave_items[wave][0], static_cast<uint32_t>(mine));
+        atomicOr(&sh.wave_items[wave][1], static_cast<uint32_t>(mine >> 32));
     }
     __syncthreads();
+    const uint64_t wave_items = (uint64_t{sh.wave_items[wave][1]} << 32) | sh.wave_items[wave][0];
     for (uint64_t rest = wave_items; rest != 0; rest &= rest - 1) {
         const int j = __ffsll(static_cast<unsigned long long>(rest)) - 1;
         const uint64_t lanes = __ballot((mine >> j) & 1);
         if (lane == 0) sh.counts[j * kPickWaves + wave] = static_cast<uint32_t>(__popcll(lanes));
     }
     __syncthreads();
-    const int64_t c = sh.counts[tid];
-    const int64_t through = block_inclusive_scan(c, kPickThreads, sh.wave_totals);
-    sh.counts[tid] = static_cast<uint32_t>(through - c);
+    const uint32_t c = sh.counts[tid];
+    const uint32_t through = block_inclusive_scan32(c, sh.wave_totals32);
+    sh.counts[tid] = through - c;
     if (tid == kPickThreads - 1) sh.total = through;
     __syncthreads();
     const int64_t total = sh.total;
@@ -854,25 +877,50 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     // kept): for k <= 1024 the k-th largest lane maximum; the keys at or above it listed in index
     // order with their indices when they fit the LDS
     uint32_t low = 1;
-    if (top_k <= kPickThreads) low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh));
-    uint64_t above = 0;  // bit s: slot s's key >= low (the keys loaded again: holding them across
-                         // the selection would spill)
+    const bool bounded = top_k <= kPickThreads;
+    // (two digits: the bound's top 16 bits, enough to leave about k keys above it)
+    if (bounded) low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh, 2));
+    // The keys at or above the bound, loaded again (holding them across the selection would
+    // spill): bit s of `above` for slot s, and, with a bound, appended to an unordered list
+    // through an LDS counter (usually about k of them).
+    if (tid == 0) sh.appended = 0;
+    __syncthreads();
+    uint64_t above = 0;
 #pragma unroll
     for (int s = 0; s < kPickSlots; ++s) above |= uint64_t{key_at(s) >= low} << s;
+    if (bounded) {
+        for (uint64_t rest = above; rest != 0; rest &= rest - 1) {  // this lane's few candidates
+            const int slot = __ffsll(static_cast<unsigned long long>(rest)) - 1;
+            const uint32_t at = atomicAdd(&sh.appended, 1u);
+            if (at < kRankList) {
+                sh.cand_key[at] = __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, (slot * kPickThreads + tid) * 4, 0, 0);
+                sh.cand_idx[at] = slot * kPickThreads + tid;
+            }
+            if (at >= kRankList) break;  // the list is long: the ordered path takes over
+        }
+    }
+    __syncthreads();
+    const uint32_t appended = __builtin_amdgcn_readfirstlane(sh.appended);  // LDS values are uniform
+    const bool unordered = bounded && appended <= kRankList;  // the short list, in no order
     bool listed = false;
     int64_t listed_n = 0;
-    if (top_k <= kPickThreads) {
+    if (unordered) {
+        listed_n = appended;
+        listed = true;
+    } else if (bounded) {  // a longer list, in index order
         listed_n = ordered_compact(
             above,
             [&](int s, int64_t at, int64_t total) {
-                if (total <= kPickLdsKept) {
-                    const int32_t i = s * kPickThreads + tid;
-                    sh.cand_idx[at] = i;
-                    sh.cand_key[at] = a.keys[i];
-                }
+                if (total <= kPickLdsKept) sh.cand_idx[at] = s * kPickThreads + tid;
             },
             sh);
         listed = listed_n <= kPickLdsKept;
+        if (listed)  // the listed keys, all loads at once
+            for (int64_t r = tid; r < listed_n; r += kPickThreads) sh.cand_key[r] = a.keys[sh.cand_idx[r]];
+    }
+    if (listed) {  // zeros after the list to a multiple of 4
+        if (tid < 4) sh.cand_key[listed_n + tid] = 0u;
+        __syncthreads();
     }
     // the k-th largest key and the kept entries (keys at or above it) in index order
     constexpr int kListGroups = kPickLdsKept / kPickThreads;
@@ -885,19 +933,59 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
             return r < listed_n ? sh.cand_key[r] : 0u;
         };
         const int groups = static_cast<int>((listed_n + kPickThreads - 1) / kPickThreads);
-        const uint32_t kth = radix_select(
-            [&](const auto& f) {
-                for (int j = 0; j < groups; ++j) f(listed_key(j), int64_t{j} * kPickThreads + tid < listed_n);
-            },
-            top_k, sh);
-        uint64_t keep = 0;
-#pragma unroll
-        for (int j = 0; j < kListGroups; ++j)
-            keep |= uint64_t{int64_t{j} * kPickThreads + tid < listed_n && listed_key(j) >= kth} << j;
-        m = ordered_compact(
-            keep, [&](int j, int64_t at, int64_t) { sh.kept_i[at] = sh.cand_idx[j * kPickThreads + tid]; }, sh);
+        uint32_t kth;
+        if (listed_n <= kRankList) {
+            // Short lists: the k-th largest is the listed key k with #(keys > k) < top_k <=
+            // #(keys >= k); every lane holding one counts over the list (broadcast LDS reads, four
+            // keys a read; the zeros after the list count in neither).
+            if (tid < listed_n) {
+                const uint32_t mine = sh.cand_key[tid];
+                int64_t gt = 0, ge = 0;
+                for (int64_t j = 0; j < listed_n; j += 4) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(&sh.cand_key[j]);
+                    gt += (q.x > mine) + (q.y > mine) + (q.z > mine) + (q.w > mine);
+                    ge += (q.x >= mine) + (q.y >= mine) + (q.z >= mine) + (q.w >= mine);
+                }
+                if (gt < top_k && top_k <= ge) sh.chosen = mine;  // lanes with equal keys write the same value
+            }
+            __syncthreads();
+            kth = sh.chosen;
+        } else {
+            kth = radix_select(
+                [&](const auto& f) {
+                    for (int j = 0; j < groups; ++j) f(listed_key(j), int64_t{j} * kPickThreads + tid < listed_n);
+                },
+                top_k, sh);
+        }
         kept = sh.kept_i;
         kept_e = sh.kept_e;
+        if (unordered) {
+            // The kept entries of the unordered list in index order: each kept lane's position is
+            // the number of kept entries with a smaller index (indices are distinct).
+            if (tid < listed_n) {  // the lanes holding entries (the waves past the list skip the loop)
+                const uint32_t key_mine = sh.cand_key[tid];
+                const int32_t idx_mine = sh.cand_idx[tid];
+                uint32_t total = 0, before = 0;
+                for (int j = 0; j < static_cast<int>(listed_n); j += 4) {
+                    const uint4 kq = *reinterpret_cast<const uint4*>(&sh.cand_key[j]);
+                    const int4 iq = *reinterpret_cast<const int4*>(&sh.cand_idx[j]);
+                    total += (kq.x >= kth) + (kq.y >= kth) + (kq.z >= kth) + (kq.w >= kth);
+                    before += (kq.x >= kth && iq.x < idx_mine) + (kq.y >= kth && iq.y < idx_mine) +
+                              (kq.z >= kth && iq.z < idx_mine) + (kq.w >= kth && iq.w < idx_mine);
+                }
+                if (key_mine >= kth) sh.kept_i[before] = idx_mine;
+                if (tid == 0) sh.total = total;
+            }
+            __syncthreads();
+            m = listed_n == 0 ? 0 : sh.total;  // an empty list (every key a NaN) keeps nothing
+        } else {
+            uint64_t keep = 0;
+#pragma unroll
+            for (int j = 0; j < kListGroups; ++j)
+                keep |= uint64_t{int64_t{j} * kPickThreads + tid < listed_n && listed_key(j) >= kth} << j;
+            m = ordered_compact(
+                keep, [&](int j, int64_t at, int64_t) { sh.kept_i[at] = sh.cand_idx[j * kPickThreads + tid]; }, sh);
+        }
     } else {
         const uint32_t kth = max(low, radix_select(
                                           [&](const auto& f) {
@@ -931,9 +1019,7 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     // The sums below run in index order in double, as kael's CPU loops do: wave 0 loads 64 entries
     // at a time, one per lane, and folds them in lane order through readlane, so only one load per
     // 64 entries stands in the dependent chain.
-    const auto lane_value = [](float v, int j) {
-        return static_cast<double>(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j)));
-    };
+    const auto entry = [](float v, int j) { return static_cast<double>(lane_value(v, j)); };
     Sampler& sp = *a.sp;
     if (nonfinite || draw >= draws) {
         if (lane == 0) sp.error = nonfinite ? 1 : 2;
@@ -941,12 +1027,57 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
         return;
     }
     if (lane == 0) sp.draw = draw + 1;
+    m = __builtin_amdgcn_readfirstlane(static_cast<int>(m));  // uniform: the loops below index lanes by it
+    if (m <= 64) {
+        // One load group, lane j holding entry j. Where every positive value is at least 2^-24 (and
+        // at most 1: e = exp(x - max) <= 1, and p = e / sum <= e as sum >= 1), each value is a whole
+        // multiple of 2^-47 and every partial sum of at most 64 of them a whole multiple of 2^-47
+        // below 2^53 of them, so each double addition is exact and any order gives the sequential
+        // sums bit for bit: a wave sum and a wave prefix sum then stand in for the loops. Otherwise
+        // the loops run. Lane j's running sum is the walk's sum after entry j, so the first sum
+        // past the point and the last positive weight are ballots.
+        const bool in = lane < m;
+        const auto exact = [&](float v) { return -wave_max(in && v > 0.f ? -v : -1.f) >= 0x1p-24f; };
+        const float e = in ? kept_e[lane] : 0.f;
+        double sum = 0.0;
+        if (exact(e)) {
+            sum = wave_sum(static_cast<double>(e));
+        } else {
+            for (int j = 0; j < m; ++j) sum += entry(e, j);
+        }
+        const float denominator = static_cast<float>(sum);
+        const float p = in ? __fdiv_rn(e, denominator) : 0.f;
+        double mine = static_cast<double>(p), cumulative = 0.0;
+        if (exact(p)) {
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(mine, off);
+                if (lane >= off) mine += o;
+            }
+            cumulative = lane_value(mine, static_cast<int>(m) - 1);
+        } else {
+            for (int j = 0; j < m; ++j) {
+                cumulative += entry(p, j);
+                if (lane == j) mine = cumulative;
+            }
+        }
+        // multinomial (src/random.cpp:143-151): point = u * total, upper_bound, and the step back
+        // to a positive weight when the point is past every sum
+        const double point = u * cumulative;
+        const int32_t index = in ? kept[lane] : 0;
+        const uint64_t past = __ballot(in && mine > point);
+        const uint64_t positive = __ballot(in && p > 0.f);
+        if (past != 0) token = __builtin_amdgcn_readlane(index, __ffsll(static_cast<unsigned long long>(past)) - 1);
+        else if (positive != 0) token = __builtin_amdgcn_readlane(index, 63 - __clzll(static_cast<long long>(positive)));
+        else token = kept[0];
+        return;
+    }
     // the sum of e in double in index order, rounded to f32
     double sum = 0.0;
     for (int64_t base = 0; base < m; base += 64) {
         const float e = base + lane < m ? kept_e[base + lane] : 0.f;
         const int n = static_cast<int>(min<int64_t>(64, m - base));
-        for (int j = 0; j < n; ++j) sum += lane_value(e, j);
+        for (int j = 0; j < n; ++j) sum += entry(e, j);
     }
     const float denominator = static_cast<float>(sum);
     // multinomial (src/random.cpp:143-151): the cumulative sum in double, point = u * total,
@@ -955,7 +1086,7 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     for (int64_t base = 0; base < m; base += 64) {
         const float p = base + lane < m ? __fdiv_rn(kept_e[base + lane], denominator) : 0.f;
         const int n = static_cast<int>(min<int64_t>(64, m - base));
-        for (int j = 0; j < n; ++j) cumulative += lane_value(p, j);
+        for (int j = 0; j < n; ++j) cumulative += entry(p, j);
     }
     const double point = u * cumulative;
     double run = 0.0;
@@ -966,7 +1097,7 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
         const int32_t index = in ? kept[base + lane] : 0;
         const int n = static_cast<int>(min<int64_t>(64, m - base));
         for (int j = 0; j < n; ++j) {
-            const double pj = lane_value(p, j);
+            const double pj = entry(p, j);
             const int32_t ij = __builtin_amdgcn_readlane(index, j);
             run += pj;
             if (pj > 0.0) last_positive = ij;

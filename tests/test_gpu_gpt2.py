@@ -274,12 +274,14 @@ def oracle_pick(oracle, logits, temperature, top_k, u):
     return tok.value
 
 
-@pytest.mark.parametrize("vocab, temperature, top_k", [(11, 0.8, 3), (97, 1.3, 40), (97, 0.5, 96), (97, 2.0, 1)],
-                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1"])
+@pytest.mark.parametrize("vocab, temperature, top_k", [(11, 0.8, 3), (97, 1.3, 40), (97, 0.5, 96), (97, 2.0, 1),
+                                                        (97, 0.004, 40)],
+                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1", "v97_k40_cold"])
 def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature, top_k):
     """kael's sample_next on the device (kd_gpt_set_sampling, kd_gpt_set_uniforms): after the prefill and
     after every decode step the engine's pick equals the oracle's restatement of sample_next on the
-    same logits with the same draw, and the draws are used one per token."""
+    same logits with the same draw, and the draws are used one per token. The cold case spreads
+    the kept weights below 2^-24, where the device sums in sequence instead of across the wave."""
     ref = refdev
     h, g = build(kdb, ref, vocab, 32, 2, 2, 8, 13)
     try:
@@ -296,7 +298,7 @@ def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature,
             picks.extend(g.decode(1))
             assert picks[-1] == oracle_pick(oracle, g.logits(), temperature, top_k, u[s]), s
         assert g.draws_used() == steps + 1
-        if top_k > 1:
+        if top_k > 1 and temperature >= 0.1:  # (the cold case nearly always picks the largest)
             assert len(set(picks)) > 1
         # the same draws in one decode call give the same tokens
         g.set_uniforms(u)
