@@ -851,12 +851,16 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     uint32_t key[kPickSlots];
 #pragma unroll
     for (int s = 0; s < kPickSlots; ++s) key[s] = key_at(s);
-    // the lane's largest key; the smallest over the vocabulary
+    // the lane's largest key; the smallest over the vocabulary; the keys' top 16 bits, two slots a
+    // register (all the bound's test needs below: its low 16 bits are zero)
     uint32_t tmax = 0, tmin = ~0u;
+    uint32_t top16[kPickSlots / 2];
 #pragma unroll
     for (int s = 0; s < kPickSlots; ++s) {
         tmax = max(tmax, key[s]);
         tmin = min(tmin, int64_t{s} * kPickThreads + tid < V ? key[s] : ~0u);
+        if (s % 2 == 0) top16[s / 2] = key[s] >> 16;
+        else top16[s / 2] |= key[s] & 0xffff0000u;
     }
     uint32_t wm = tmax, wn = tmin;
     for (int off = 32; off > 0; off >>= 1) {
@@ -873,6 +877,8 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
         kmax = max(kmax, sh.wmax[w]);
         kmin = min(kmin, sh.wmin[w]);
     }
+    kmax = __builtin_amdgcn_readfirstlane(kmax);  // uniform: scalar registers, not 32 vector ones
+    kmin = __builtin_amdgcn_readfirstlane(kmin);  // held until the end
     // a lower bound of the k-th largest key (a key of 0, past the vocabulary or a NaN, is never
     // kept): for k <= 1024 the k-th largest lane maximum; the keys at or above it listed in index
     // order with their indices when they fit the LDS
@@ -885,9 +891,15 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     // through an LDS counter (usually about k of them).
     if (tid == 0) sh.appended = 0;
     __syncthreads();
+    // key >= low exactly when key's top 16 bits >= low's (low's low 16 bits are zero); a top of 0
+    // (past the vocabulary, or a NaN) is never a candidate
     uint64_t above = 0;
+    const uint32_t low16 = max(low >> 16, 1u);
 #pragma unroll
-    for (int s = 0; s < kPickSlots; ++s) above |= uint64_t{key_at(s) >= low} << s;
+    for (int s = 0; s < kPickSlots; ++s) {
+        const uint32_t t = s % 2 == 0 ? top16[s / 2] & 0xffffu : top16[s / 2] >> 16;
+        above |= uint64_t{t >= low16} << s;
+    }
     if (bounded) {
         for (uint64_t rest = above; rest != 0; rest &= rest - 1) {  // this lane's few candidates
             const int slot = __ffsll(static_cast<unsigned long long>(rest)) - 1;
