@@ -340,9 +340,11 @@ struct GemvArgs {
     float* best_v;
     int64_t* best_i;
     Step* st;
-    // head_kernel when the sampler samples (top_k > 0): every row's order key of logit / temperature
+    // head_kernel when the sampler samples (top_k > 0): every row's order key of logit / temperature,
+    // and each workgroup's largest and smallest key (key_parts[2g], key_parts[2g + 1])
     const Sampler* sp;
     uint32_t* keys;
+    uint32_t* key_parts;
 };
 
 constexpr int kMaxK = 4096;
@@ -579,6 +581,7 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
         h[i] = j < k4 ? hs4[j] : zero;
     }
     Best best{-INFINITY, INT64_MAX};
+    uint32_t key_hi = 0, key_lo = ~0u;  // sampled: the largest and smallest key this lane writes
     for (; p < pairs; p += stride) {
         float4 n0[kHeadVec], n1[kHeadVec];
         if (p + stride < pairs) load(p + stride, n0, n1);
@@ -594,8 +597,13 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
         if (lane == 0) a.out[n] = a0;
         if (lane == 1 && n + 1 < N) a.out[n + 1] = a1;
         if (keyed) {  // x = logits / temperature as kael's sample_next divides (f32)
-            if (lane == 0) a.keys[n] = order_key(__fdiv_rn(a0, temperature));
-            if (lane == 1 && n + 1 < N) a.keys[n + 1] = order_key(__fdiv_rn(a1, temperature));
+            const bool writes = lane == 0 || (lane == 1 && n + 1 < N);
+            if (writes) {
+                const uint32_t k = order_key(__fdiv_rn(lane == 0 ? a0 : a1, temperature));
+                a.keys[n + lane] = k;
+                key_hi = max(key_hi, k);
+                key_lo = min(key_lo, k);
+            }
         }
         const Best o0{a0, n};
         if (better(o0, best)) best = o0;
@@ -609,11 +617,26 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
             c1[i] = n1[i];
         }
     }
+    __shared__ uint32_t khi[kThreads / 64][2], klo[kThreads / 64][2];
     if (lane == 0) {
         bv[wave] = best.v;
         bi[wave] = best.i;
     }
+    if (keyed && lane < 2) {
+        khi[wave][lane] = key_hi;
+        klo[wave][lane] = key_lo;
+    }
     __syncthreads();
+    if (keyed && threadIdx.x == 0) {  // the workgroup's key extremes, for the sampled pick's bound
+        uint32_t hi = 0, lo = ~0u;
+        for (int w = 0; w < kThreads / 64; ++w)
+            for (int l = 0; l < 2; ++l) {
+                hi = max(hi, khi[w][l]);
+                lo = min(lo, klo[w][l]);
+            }
+        a.key_parts[2 * blockIdx.x] = hi;
+        a.key_parts[2 * blockIdx.x + 1] = lo;
+    }
     if (threadIdx.x == 0) {
         Best r{bv[0], bi[0]};
         for (int w = 1; w < kThreads / 64; ++w) {
@@ -627,16 +650,15 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
 
 // Picks the next token, appends it to the sequence unless the next position is teacher-forced,
 // and advances the position. One workgroup of 1024 lanes.
-//   Greedy (sampler top_k 0): the first maximum among the head's workgroup partials (GPT-2's
-//   6283 partials take 7 loads per lane).
+//   Greedy (sampler top_k 0): the first maximum among the head's workgroup partials (one per
+//   head workgroup: 1024 for GPT-2 small).
 //   Sampled: kael's sample_next (reference src/nn/transformer.cpp:39-50) and multinomial
 //   (src/random.cpp:106-160) for 0 < top_k < vocab: x = logits / temperature (f32 division, in
-//   head_kernel, which writes x's order-preserving 32-bit keys); the k-th largest x by radix
-//   selects (four 8-bit digits, per-wave histograms) over the keys, lane t holding those of
-//   indices t, t + 1024, ... in registers. For k <= 1024 the k-th largest of the lanes' maxima
-//   bounds the k-th largest key from below (k lanes hold a key at least that large), so only the
-//   keys at or above it (about k of them) are listed and selected from; otherwise, or when more
-//   than kPickLdsKept are, every key is. The kept entries (x >= the k-th largest: masked_fill's
+//   head_kernel, which writes x's order-preserving 32-bit keys and each workgroup's extremes);
+//   a lower bound of the k-th largest key from the k-th largest head-workgroup maximum (or, in
+//   the full scan, lane maximum), the keys at or above it (about k) listed, the k-th largest among
+//   them by rank counting or radix selects (8-bit digits, per-wave histograms); for k > 1024 a
+//   radix select over every key. The kept entries (x >= the k-th largest: masked_fill's
 //   complement) are listed in index order with their e = exp(x - max); then, in kael's order, the
 //   sum of e in double rounded to f32, p = e / sum, the cumulative double sum of p, point = u *
 //   sum, the first kept entry whose cumulative sum exceeds the point (upper_bound; the masked
@@ -650,6 +672,7 @@ static_assert(int64_t{kPickThreads} * kPickSlots == KD_GPT_SAMPLE_MAX_VOCAB);
 static_assert(kPickLdsKept % kPickThreads == 0 && kPickLdsKept / kPickThreads <= kPickSlots);
 constexpr int32_t kRawBufferWord3 = 0x00020000;  // buffer descriptor word 3: 32-bit data format
 constexpr int64_t kRankList = 256;  // candidate lists up to this long: k-th key by rank counting
+constexpr int kPickParts = 256;     // head workgroups whose rows the pick reads, at most
 
 struct PickArgs {
     Step* st;
@@ -665,6 +688,7 @@ struct PickArgs {
     float* kept_e;   // [vocab] scratch: their exponentials
     const uint32_t* keys;  // [kPickSlots * kPickThreads] head_kernel's order keys of x = logits /
                            // temperature, zero past the vocabulary
+    const uint32_t* key_parts;  // [2 * parts] each head workgroup's largest and smallest key
 };
 
 struct alignas(16) PickShared {  // hist rows are read 16 bytes at a time
@@ -681,6 +705,8 @@ struct alignas(16) PickShared {  // hist rows are read 16 bytes at a time
     alignas(16) uint32_t cand_key[kPickLdsKept + 4];  // listed keys >= the lower bound, zeros after them
     alignas(16) int32_t cand_idx[kPickLdsKept + 4];   // their indices
     uint32_t appended;                                // keys appended to the unordered short list
+    uint32_t nparts;                                  // head workgroups that may hold candidates
+    int32_t cand_parts[kPickParts];
     float kept_e[kPickLdsKept];       // kept entries, when at most kPickLdsKept
     int32_t kept_i[kPickLdsKept];
 };
@@ -848,87 +874,173 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
     const auto key_at = [&](int s) -> uint32_t {
         return __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, tid * 4, s * kPickThreads * 4, 0);
     };
-    uint32_t key[kPickSlots];
-#pragma unroll
-    for (int s = 0; s < kPickSlots; ++s) key[s] = key_at(s);
-    // the lane's largest key; the smallest over the vocabulary; the keys' top 16 bits, two slots a
-    // register (all the bound's test needs below: its low 16 bits are zero)
-    uint32_t tmax = 0, tmin = ~0u;
-    uint32_t top16[kPickSlots / 2];
-#pragma unroll
-    for (int s = 0; s < kPickSlots; ++s) {
-        tmax = max(tmax, key[s]);
-        tmin = min(tmin, int64_t{s} * kPickThreads + tid < V ? key[s] : ~0u);
-        if (s % 2 == 0) top16[s / 2] = key[s] >> 16;
-        else top16[s / 2] |= key[s] & 0xffff0000u;
-    }
-    uint32_t wm = tmax, wn = tmin;
-    for (int off = 32; off > 0; off >>= 1) {
-        wm = max(wm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wm), off)));
-        wn = min(wn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wn), off)));
-    }
-    if (lane == 0) {
-        sh.wmax[wave] = wm;
-        sh.wmin[wave] = wn;
-    }
-    __syncthreads();
-    uint32_t kmax = sh.wmax[0], kmin = sh.wmin[0];
-    for (int w = 1; w < kPickWaves; ++w) {
-        kmax = max(kmax, sh.wmax[w]);
-        kmin = min(kmin, sh.wmin[w]);
-    }
-    kmax = __builtin_amdgcn_readfirstlane(kmax);  // uniform: scalar registers, not 32 vector ones
-    kmin = __builtin_amdgcn_readfirstlane(kmin);  // held until the end
-    // a lower bound of the k-th largest key (a key of 0, past the vocabulary or a NaN, is never
-    // kept): for k <= 1024 the k-th largest lane maximum; the keys at or above it listed in index
-    // order with their indices when they fit the LDS
-    uint32_t low = 1;
     const bool bounded = top_k <= kPickThreads;
-    // (two digits: the bound's top 16 bits, enough to leave about k keys above it)
-    if (bounded) low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh, 2));
-    // The keys at or above the bound, loaded again (holding them across the selection would
-    // spill): bit s of `above` for slot s, and, with a bound, appended to an unordered list
-    // through an LDS counter (usually about k of them).
-    if (tid == 0) sh.appended = 0;
-    __syncthreads();
-    // key >= low exactly when key's top 16 bits >= low's (low's low 16 bits are zero); a top of 0
-    // (past the vocabulary, or a NaN) is never a candidate
-    uint64_t above = 0;
-    const uint32_t low16 = max(low >> 16, 1u);
-#pragma unroll
-    for (int s = 0; s < kPickSlots; ++s) {
-        const uint32_t t = s % 2 == 0 ? top16[s / 2] & 0xffffu : top16[s / 2] >> 16;
-        above |= uint64_t{t >= low16} << s;
-    }
-    if (bounded) {
-        for (uint64_t rest = above; rest != 0; rest &= rest - 1) {  // this lane's few candidates
-            const int slot = __ffsll(static_cast<unsigned long long>(rest)) - 1;
-            const uint32_t at = atomicAdd(&sh.appended, 1u);
-            if (at < kRankList) {
-                sh.cand_key[at] = __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, (slot * kPickThreads + tid) * 4, 0, 0);
-                sh.cand_idx[at] = slot * kPickThreads + tid;
-            }
-            if (at >= kRankList) break;  // the list is long: the ordered path takes over
-        }
-    }
-    __syncthreads();
-    const uint32_t appended = __builtin_amdgcn_readfirstlane(sh.appended);  // LDS values are uniform
-    const bool unordered = bounded && appended <= kRankList;  // the short list, in no order
-    bool listed = false;
+    uint32_t kmax = 0, kmin = ~0u, low = 1;
+    uint64_t above = 0;  // (the full scan) bit s: slot s's key is at or above the bound
+    bool unordered = false, listed = false;
     int64_t listed_n = 0;
-    if (unordered) {
-        listed_n = appended;
-        listed = true;
-    } else if (bounded) {  // a longer list, in index order
-        listed_n = ordered_compact(
-            above,
-            [&](int s, int64_t at, int64_t total) {
-                if (total <= kPickLdsKept) sh.cand_idx[at] = s * kPickThreads + tid;
-            },
-            sh);
-        listed = listed_n <= kPickLdsKept;
-        if (listed)  // the listed keys, all loads at once
-            for (int64_t r = tid; r < listed_n; r += kPickThreads) sh.cand_key[r] = a.keys[sh.cand_idx[r]];
+    // From the head kernel's workgroup extremes (for k at most the number of its workgroups): the
+    // k-th largest workgroup maximum bounds the k-th largest key from below (k workgroups hold a
+    // key at least that large), and only the workgroups whose maximum reaches the bound can hold a
+    // key at or above it, so only their rows are read (head workgroup g wrote the rows of row
+    // pairs g * 4 + w + j * 4 * parts, w < 4). Too many such workgroups or keys: the full scan.
+    const int64_t parts = a.parts;
+    bool from_parts = top_k <= parts && parts <= kPickThreads;
+    if (from_parts) {
+        const bool mine = tid < parts;
+        const uint32_t phi = mine ? a.key_parts[2 * tid] : 0u;
+        const uint32_t plo = mine ? a.key_parts[2 * tid + 1] : ~0u;
+        uint32_t wm = phi, wn = plo;
+        for (int off = 32; off > 0; off >>= 1) {
+            wm = max(wm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wm), off)));
+            wn = min(wn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wn), off)));
+        }
+        if (lane == 0) {
+            sh.wmax[wave] = wm;
+            sh.wmin[wave] = wn;
+        }
+        if (tid == 0) {
+            sh.appended = 0;
+            sh.nparts = 0;
+        }
+        __syncthreads();
+        kmax = sh.wmax[0];
+        kmin = sh.wmin[0];
+        for (int w = 1; w < kPickWaves; ++w) {
+            kmax = max(kmax, sh.wmax[w]);
+            kmin = min(kmin, sh.wmin[w]);
+        }
+        kmax = __builtin_amdgcn_readfirstlane(kmax);
+        kmin = __builtin_amdgcn_readfirstlane(kmin);
+        low = max(1u, radix_select([&](const auto& f) { f(phi, mine); }, top_k, sh, 2));
+        if (mine && phi >= low) {
+            const uint32_t at = atomicAdd(&sh.nparts, 1u);
+            if (at < kPickParts) sh.cand_parts[at] = tid;
+        }
+        __syncthreads();
+        const uint32_t np = __builtin_amdgcn_readfirstlane(sh.nparts);
+        if (np <= kPickParts) {
+            const int64_t pairs = (V + 1) / 2, stride = parts * (kThreads / 64);
+            const int64_t per_part = 2 * (kThreads / 64) * ((pairs + stride - 1) / stride);  // rows, at most
+            const int64_t items = int64_t{np} * per_part;
+            for (int64_t base = 0; base < items; base += 4 * kPickThreads) {
+                uint32_t k[4];
+                int64_t n[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {  // four rows' keys in flight
+                    const int64_t i = base + q * kPickThreads + tid;
+                    n[q] = -1;
+                    k[q] = 0;
+                    if (i < items) {
+                        const int64_t g = sh.cand_parts[i / per_part], r = i % per_part;
+                        const int64_t pair = g * (kThreads / 64) + (r / 2) % (kThreads / 64) + r / (2 * (kThreads / 64)) * stride;
+                        const int64_t row = 2 * pair + r % 2;
+                        if (pair < pairs && row < V) {
+                            n[q] = row;
+                            k[q] = a.keys[row];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (n[q] >= 0 && k[q] >= low) {
+                        const uint32_t at = atomicAdd(&sh.appended, 1u);
+                        if (at < kRankList) {
+                            sh.cand_key[at] = k[q];
+                            sh.cand_idx[at] = static_cast<int32_t>(n[q]);
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            const uint32_t appended = __builtin_amdgcn_readfirstlane(sh.appended);
+            if (appended <= kRankList) {
+                unordered = listed = true;
+                listed_n = appended;
+            }
+        }
+        from_parts = unordered;
+    }
+    if (!from_parts) {  // the full scan
+        uint32_t key[kPickSlots];
+#pragma unroll
+        for (int s = 0; s < kPickSlots; ++s) key[s] = key_at(s);
+        // the lane's largest key; the smallest over the vocabulary; the keys' top 16 bits, two slots a
+        // register (all the bound's test needs below: its low 16 bits are zero)
+        uint32_t tmax = 0, tmin = ~0u;
+        uint32_t top16[kPickSlots / 2];
+#pragma unroll
+        for (int s = 0; s < kPickSlots; ++s) {
+            tmax = max(tmax, key[s]);
+            tmin = min(tmin, int64_t{s} * kPickThreads + tid < V ? key[s] : ~0u);
+            if (s % 2 == 0) top16[s / 2] = key[s] >> 16;
+            else top16[s / 2] |= key[s] & 0xffff0000u;
+        }
+        uint32_t wm = tmax, wn = tmin;
+        for (int off = 32; off > 0; off >>= 1) {
+            wm = max(wm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wm), off)));
+            wn = min(wn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wn), off)));
+        }
+        if (lane == 0) {
+            sh.wmax[wave] = wm;
+            sh.wmin[wave] = wn;
+        }
+        __syncthreads();
+        kmax = sh.wmax[0];
+        kmin = sh.wmin[0];
+        for (int w = 1; w < kPickWaves; ++w) {
+            kmax = max(kmax, sh.wmax[w]);
+            kmin = min(kmin, sh.wmin[w]);
+        }
+        kmax = __builtin_amdgcn_readfirstlane(kmax);  // uniform: scalar registers, not 32 vector ones
+        kmin = __builtin_amdgcn_readfirstlane(kmin);  // held until the end
+        // a lower bound of the k-th largest key (a key of 0, past the vocabulary or a NaN, is never
+        // kept): for k <= 1024 the k-th largest lane maximum; the keys at or above it listed in index
+        // order with their indices when they fit the LDS
+        low = 1;
+        // (two digits: the bound's top 16 bits, enough to leave about k keys above it)
+        if (bounded) low = max(low, radix_select([&](const auto& f) { f(tmax, true); }, top_k, sh, 2));
+        // The keys at or above the bound, loaded again (holding them across the selection would
+        // spill): bit s of `above` for slot s, and, with a bound, appended to an unordered list
+        // through an LDS counter (usually about k of them).
+        if (tid == 0) sh.appended = 0;
+        __syncthreads();
+        // key >= low exactly when key's top 16 bits >= low's (low's low 16 bits are zero); a top of 0
+        // (past the vocabulary, or a NaN) is never a candidate
+        const uint32_t low16 = max(low >> 16, 1u);
+#pragma unroll
+        for (int s = 0; s < kPickSlots; ++s) {
+            const uint32_t t = s % 2 == 0 ? top16[s / 2] & 0xffffu : top16[s / 2] >> 16;
+            above |= uint64_t{t >= low16} << s;
+        }
+        if (bounded) {
+            for (uint64_t rest = above; rest != 0; rest &= rest - 1) {  // this lane's few candidates
+                const int slot = __ffsll(static_cast<unsigned long long>(rest)) - 1;
+                const uint32_t at = atomicAdd(&sh.appended, 1u);
+                if (at < kRankList) {
+                    sh.cand_key[at] = __builtin_amdgcn_raw_buffer_load_b32(keys_rsrc, (slot * kPickThreads + tid) * 4, 0, 0);
+                    sh.cand_idx[at] = slot * kPickThreads + tid;
+                }
+                if (at >= kRankList) break;  // the list is long: the ordered path takes over
+            }
+        }
+        __syncthreads();
+        const uint32_t appended = __builtin_amdgcn_readfirstlane(sh.appended);  // LDS values are uniform
+        unordered = bounded && appended <= kRankList;  // the short list, in no order
+        if (unordered) {
+            listed_n = appended;
+            listed = true;
+        } else if (bounded) {  // a longer list, in index order
+            listed_n = ordered_compact(
+                above,
+                [&](int s, int64_t at, int64_t total) {
+                    if (total <= kPickLdsKept) sh.cand_idx[at] = s * kPickThreads + tid;
+                },
+                sh);
+            listed = listed_n <= kPickLdsKept;
+            if (listed)  // the listed keys, all loads at once
+                for (int64_t r = tid; r < listed_n; r += kPickThreads) sh.cand_key[r] = a.keys[sh.cand_idx[r]];
+        }
     }
     if (listed) {  // zeros after the list to a multiple of 4
         if (tid < 4) sh.cand_key[listed_n + tid] = 0u;
@@ -1509,6 +1621,7 @@ struct Engine {
     int32_t* kept = nullptr;     // [vocab] sampling scratch
     float* kept_e = nullptr;     // [vocab]
     uint32_t* keys = nullptr;    // [65536] order keys of the sampled pick's x, zero past the vocabulary
+    uint32_t* key_parts = nullptr;  // [2 * head workgroups] their largest and smallest keys
     Sampler host_sp{0.f, 0, 0, 0, 0};
     hipGraphExec_t graph = nullptr;
     int64_t host_pos = 0;     // mirror of st->pos: positions in the KV cache
@@ -1539,7 +1652,7 @@ struct Engine {
     }
 
     PickArgs pick_args() const {
-        return PickArgs{st, seq, pv, pi, head_groups(), logits, cfg.vocab_size, sp, uniforms, kept, kept_e, keys};
+        return PickArgs{st, seq, pv, pi, head_groups(), logits, cfg.vocab_size, sp, uniforms, kept, kept_e, keys, key_parts};
     }
 
     // Workgroups of head_kernel: 4 per CU, fewer when the vocabulary has fewer row pairs than
@@ -1630,6 +1743,7 @@ struct Engine {
         head.best_i = pi;
         head.sp = sp;
         head.keys = keys;
+        head.key_parts = key_parts;
         const int64_t parts = head_groups();
         hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
         hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kPickThreads), 0, s, pick_args());
@@ -1832,6 +1946,7 @@ struct Engine {
         head.best_i = pi;
         head.sp = sp;
         head.keys = keys;
+        head.key_parts = key_parts;
         const int64_t parts = head_groups();
         hipLaunchKernelGGL(head_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kThreads), 0, s, head);
         hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kPickThreads), 0, s, pick_args());
@@ -1911,7 +2026,7 @@ struct Engine {
                           static_cast<void*>(f), static_cast<void*>(logits), static_cast<void*>(pv),
                           static_cast<void*>(pi), static_cast<void*>(seq), static_cast<void*>(st),
                           static_cast<void*>(sp), static_cast<void*>(uniforms), static_cast<void*>(kept),
-                          static_cast<void*>(kept_e), static_cast<void*>(keys)})
+                          static_cast<void*>(kept_e), static_cast<void*>(keys), static_cast<void*>(key_parts)})
             if (ptr) (void)hipFree(ptr);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -2001,6 +2116,7 @@ int create(Engine& e, const kd_gpt_config& c) {
     if (int rc = alloc(&e.kept_e, c.vocab_size)) return rc;
     if (int rc = alloc(&e.keys, int64_t{kPickSlots} * kPickThreads)) return rc;
     KD_HIP(hipMemset(e.keys, 0, size_t{kPickSlots} * kPickThreads * sizeof(uint32_t)));  // past the vocabulary: 0
+    if (int rc = alloc(&e.key_parts, 2 * e.head_groups())) return rc;
     KD_HIP(hipMemcpy(e.sp, &e.host_sp, sizeof(Sampler), hipMemcpyHostToDevice));  // greedy
     return KD_OK;
 }
