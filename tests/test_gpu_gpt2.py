@@ -275,13 +275,16 @@ def oracle_pick(oracle, logits, temperature, top_k, u):
 
 
 @pytest.mark.parametrize("vocab, temperature, top_k", [(11, 0.8, 3), (97, 1.3, 40), (97, 0.5, 96), (97, 2.0, 1),
-                                                        (97, 0.004, 40)],
-                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1", "v97_k40_cold"])
+                                                        (97, 0.004, 40), (50257, 0.8, 40), (50257, 1.0, 500)],
+                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1", "v97_k40_cold", "v50257_k40", "v50257_k500"])
 def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature, top_k):
     """kael's sample_next on the device (kd_gpt_set_sampling, kd_gpt_set_uniforms): after the prefill and
     after every decode step the engine's pick equals the oracle's restatement of sample_next on the
     same logits with the same draw, and the draws are used one per token. The cold case spreads
-    the kept weights below 2^-24, where the device sums in sequence instead of across the wave."""
+    the kept weights below 2^-24, where the device sums in sequence instead of across the wave;
+    GPT-2's vocabulary takes the bound from the head kernel's 1024 workgroup maxima (k = 40) or,
+    with more candidate workgroups than the pick reads, the full scan and the sequential sums over
+    more than 64 kept entries (k = 500)."""
     ref = refdev
     h, g = build(kdb, ref, vocab, 32, 2, 2, 8, 13)
     try:
