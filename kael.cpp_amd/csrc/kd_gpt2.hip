@@ -1,10 +1,10 @@
-// kd_gpt2.hip - GPT-2 greedy decode engine (benchmark config C5) for gfx950.
+// kd_gpt2.hip - GPT-2 decode engine (benchmark config C5) for gfx950.
 //
 // Workload of reference examples/gpt2_generate.cpp: kael's GPT (src/nn/transformer.cpp:103-237)
-// generating greedily with a KV cache (nn::generate, :256-295), batch 1, f32. kael runs it as ~700
-// device calls per token with blocking host syncs (embedding index checks, host argmax). This
-// engine keeps kael's parameters in kael's layout and its arithmetic, and runs one token per
-// replay of a captured HIP graph:
+// generating with a KV cache (nn::generate, :256-295), greedily or with sample_next's temperature
+// and top-k, batch 1, f32. kael runs it as ~700 device calls per token with blocking host syncs
+// (embedding index checks, the pick on the host). This engine keeps kael's parameters in kael's
+// layout and its arithmetic, and runs one token per replay of a captured HIP graph:
 //
 //   embed       x = wte[token] + wpe[pos]                                      (1 launch)
 //   per layer   qkv GEMV on ln1(x) (+bias; K/V appended to the cache)
@@ -13,16 +13,18 @@
 //               -> proj GEMV on the combined attention output (+bias, +residual into x)
 //               -> fc1 GEMV on ln2(x) (+bias, GELU)
 //               -> fc2 GEMV (+bias, +residual into x)                          (5 launches)
-//   head        ln_final -> logits = wte . h with per-workgroup best rows -> greedy pick of
-//               the first maximum, which writes the next token and advances the position in
-//               device memory                                                 (3 launches)
+//   head        ln_final -> logits = wte . h with per-workgroup best rows (and, sampling, the
+//               keys of logits / temperature) -> the pick (the first maximum, or kael's
+//               sample_next), which writes the next token and advances the position in device
+//               memory                                                        (2 launches)
 // The LayerNorm feeding a GEMV is recomputed by each of its workgroups into LDS (768 values):
 // cheaper than a separate launch. A "last workgroup finishes" epilogue was measured and
 // rejected: same-address device-scope atomics serialise at about 100 ns each on this part.
 //
 // The prompt goes through a batched prefill instead: all of its positions pass each layer
-// together (row LayerNorms, GEMMs on the MFMA matmul path, a causal attention kernel), and the
-// last position's logits and greedy token come from the same head and pick kernels.
+// together (GEMMs on the MFMA matmul path, per-row epilogues that also compute the next
+// LayerNorm, a causal attention kernel), and the last position's logits and token come from the
+// same head and pick kernels.
 //
 // All step-dependent values (position, token) live in device memory, so the graph is static.
 // Weights keep kael's [out, in] row-major layout: every Linear is a row-dot GEMV reading whole
