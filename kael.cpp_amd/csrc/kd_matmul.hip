@@ -755,13 +755,15 @@ constexpr int kT64Bld = kT64 + 4;   // B tile [k][n], row stride 68 floats
 // (row / 4) % 8 so that those writes do not collide. Each output element accumulates K in the same
 // (k, k + 4) MFMA pairs and order as the 128x128 kernels, so without split K the results are
 // theirs bit for bit. Batches (or K splits: their offsets as batch strides) take blockIdx.y.
-template <bool AT, bool BT>
+// Ragged: M a multiple of 4 but not of 64 (the tied LM head's 96-row weight gradient): the last
+// tile row loads zeros past M and stores only rows below it.
+template <bool AT, bool BT, bool Ragged = false>
 __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                                 float* __restrict__ out, int M, int N, int K, int lda,
                                                                 int ldb, int ldo, BatchStrides bs) {
     __shared__ float As[2][kT64 * kT64Ald];
     __shared__ float Bs[2][kT64K * kT64Bld];
-    const int tiles_m = M / kT64;
+    const int tiles_m = (M + kT64 - 1) / kT64;
     const int tiles_n = N / kT64;
     int64_t tm64, tn64;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm64, tn64);
@@ -813,9 +815,18 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
     }
     const int g_step = loads_a ? (AT ? kT64K * lda : kT64K) : (BT ? kT64K : kT64K * ldb);
     const float* src = loads_a ? a : b;
+    // Ragged: whether load j of this thread stays inside A's M rows (A^T: its four columns, all in or
+    // all out as M is a multiple of 4; A: its row)
+    const auto inside = [&](int j) {
+        if constexpr (!Ragged) return true;
+        else if (!loads_a) return true;
+        else if (AT) return m0 + 4 * (u % 16) < M;
+        else return m0 + u / 8 + 16 * j < M;
+    };
     const auto fetch = [&](f4 (&r)[4], int ks) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const f4*>(src + g_off + ks * g_step + j * g_row);
+        for (int j = 0; j < 4; ++j)
+            r[j] = inside(j) ? *reinterpret_cast<const f4*>(src + g_off + ks * g_step + j * g_row) : f4{0.f, 0.f, 0.f, 0.f};
     };
     const auto stash = [&](const f4 (&r)[4], int buf) {
         if (loads_a) {
@@ -889,14 +900,14 @@ __global__ __launch_bounds__(kThreads) void mfma_f32_t64_kernel(const float* __r
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
             const int row = m0 + wm * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
-            out[row * ldo + col] = acc[rr];
+            if (!Ragged || row < M) out[row * ldo + col] = acc[rr];
         }
     } else {
         const float bv = bs.bias[col];
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
             const int row = m0 + wm * 32 + 8 * (rr / 4) + 4 * lh + (rr % 4);
-            out[row * ldo + col] = add_sep(acc[rr], bv);
+            if (!Ragged || row < M) out[row * ldo + col] = add_sep(acc[rr], bv);
         }
     }
 }
@@ -1225,8 +1236,11 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
     const int64_t ldb = BT ? p.sb.c : p.sb.r;
     const int64_t a_extent = AT ? p.K * lda + p.M : p.M * lda + p.K;
     const int64_t b_extent = BT ? p.N * ldb + p.K : p.K * ldb + p.N;
-    if (p.M % kT64 != 0 || p.N % kT64 != 0 || p.K % kT64K != 0 || p.K == 0 || p.so.c != 1 || a_extent >= kMax ||
-        b_extent >= kMax || p.M * p.so.r + p.N >= kMax)
+    // a ragged last tile row (M a multiple of 4, one product): the tied LM head's 96 x 4096 x 256
+    // weight gradient, 20 us on the general kernel's split K
+    const bool ragged = p.M % kT64 != 0;
+    if ((ragged && (p.M % 4 != 0 || p.batches != 1)) || p.N % kT64 != 0 || p.K % kT64K != 0 || p.K == 0 ||
+        p.so.c != 1 || a_extent >= kMax || b_extent >= kMax || p.M * p.so.r + p.N >= kMax)
         return false;
     const int cus = compute_units();
     const bool whole128 = p.M % kBM == 0 && p.N % kBN == 0 && p.K % kBK == 0;
@@ -1241,7 +1255,7 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
     // gradient: 28.7 us against 32.1 on 64x64 tiles split 4 ways); with at most 4 the 64x64 grid
     // wins (256 x 4096 x 256: 13 us against 21).
     if (whole128 && p.batches == 1 && tiles128 > 4) return false;
-    const int64_t tiles = (rows / kT64) * (p.N / kT64);
+    const int64_t tiles = (rows + kT64 - 1) / kT64 * (p.N / kT64);
     if (batches > 65535) return false;
     if (batches == 1 && tiles * 2 <= cus && p.K >= 512) {
         int64_t splits = std::min<int64_t>(p.K / 256, (cus + tiles - 1) / tiles);
@@ -1251,10 +1265,18 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
             Workspace ws;  // held until split_sum_kernel is enqueued
             if ((*rc = workspace(ws, static_cast<size_t>(splits * per) * sizeof(float)))) return true;
             const int64_t kc = p.K / splits;
-            hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
-                               dim3(kThreads), 0, stream(), a, b, static_cast<float*>(ws.ptr), static_cast<int>(rows),
-                               static_cast<int>(p.N), static_cast<int>(kc), static_cast<int>(lda), static_cast<int>(ldb),
-                               static_cast<int>(p.N), batch_strides(AT ? kc * lda : kc, BT ? kc : kc * ldb, per));
+            const dim3 grid(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits));
+            const BatchStrides bs = batch_strides(AT ? kc * lda : kc, BT ? kc : kc * ldb, per);
+            if (ragged)
+                hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT, true>), grid, dim3(kThreads), 0, stream(), a, b,
+                                   static_cast<float*>(ws.ptr), static_cast<int>(rows), static_cast<int>(p.N),
+                                   static_cast<int>(kc), static_cast<int>(lda), static_cast<int>(ldb),
+                                   static_cast<int>(p.N), bs);
+            else
+                hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), grid, dim3(kThreads), 0, stream(), a, b,
+                                   static_cast<float*>(ws.ptr), static_cast<int>(rows), static_cast<int>(p.N),
+                                   static_cast<int>(kc), static_cast<int>(lda), static_cast<int>(ldb),
+                                   static_cast<int>(p.N), bs);
             if ((*rc = launch_status())) return true;
             MatmulArgs flat = p;
             flat.batches = 1;
@@ -1266,10 +1288,15 @@ template <bool AT, bool BT> bool launch_t64(const float* a, const float* b, floa
             return true;
         }
     }
-    hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(batches)),
-                       dim3(kThreads), 0, stream(), a, b, out, static_cast<int>(rows), static_cast<int>(p.N),
-                       static_cast<int>(p.K), static_cast<int>(lda), static_cast<int>(ldb), static_cast<int>(p.so.r),
-                       batch_strides(p));
+    const dim3 grid(static_cast<uint32_t>(tiles), static_cast<uint32_t>(batches));
+    if (ragged)
+        hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT, true>), grid, dim3(kThreads), 0, stream(), a, b, out,
+                           static_cast<int>(rows), static_cast<int>(p.N), static_cast<int>(p.K), static_cast<int>(lda),
+                           static_cast<int>(ldb), static_cast<int>(p.so.r), batch_strides(p));
+    else
+        hipLaunchKernelGGL((mfma_f32_t64_kernel<AT, BT>), grid, dim3(kThreads), 0, stream(), a, b, out,
+                           static_cast<int>(rows), static_cast<int>(p.N), static_cast<int>(p.K), static_cast<int>(lda),
+                           static_cast<int>(ldb), static_cast<int>(p.so.r), batch_strides(p));
     *rc = launch_status();
     return true;
 }

@@ -266,13 +266,19 @@ def test_split_k_on_64_tiles(kdb):
 
 @pytest.mark.parametrize("m, k, n, sa, sb", [
     (96, 4096, 256, (0, 1, 96), (0, 256, 1)),       # kael's tied LM-head weight gradient (A read transposed)
+    (100, 1024, 128, (0, 1024, 1), (0, 128, 1)),    # ragged M on 64x64 tiles, A row-major
+    (36, 2048, 64, (0, 1, 36), (0, 64, 1)),         # one ragged tile row, A read transposed
+    (68, 96, 192, (0, 96, 1), (0, 1, 96)),          # ragged M, short K (no split), B read transposed
     (130, 3072, 70, (0, 3072, 1), (0, 1, 3072)),    # ragged M and N, B read transposed
     (33, 2560, 200, (0, 2, 67), (0, 200, 1)),       # generic A strides
-], ids=["head_96x4096x256", "ragged_130x3072x70", "generic_33x2560x200"])
-def test_split_k_on_the_general_kernel(kdb, m, k, n, sa, sb):
-    """Few ragged tiles with a long K: the general kernel splits K over the device (the splits in its
-    batch slot) and split_sum_kernel adds the partials in split order: within 1e-4 of the largest
-    |element| of the float64 product, and the same bits on a second run."""
+], ids=["head_96x4096x256", "ragged_100x1024x128", "ragged_36x2048x64", "ragged_68x96x192", "ragged_130x3072x70",
+        "generic_33x2560x200"])
+def test_split_k_on_ragged_tiles(kdb, m, k, n, sa, sb):
+    """Few ragged tiles with a long K: K split over the device (the splits in the kernel's batch
+    slot; 64x64 tiles whose last tile row loads zeros past M and stores only rows below it when M
+    is a multiple of 4 and N of 64, else the general kernel) and split_sum_kernel adding the
+    partials in split order: within 1e-4 of the largest |element| of the float64 product, and the
+    same bits on a second run."""
     rng = np.random.default_rng(m + k + n)
 
     def extent(shape, st):
