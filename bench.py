@@ -439,7 +439,9 @@ def bench_replay(backend, name, steps):
 
     step_ms: HIP-event time per replayed step (K repetitions of the last traced step, Python issuing
     the calls); kernel_ms: the sum of per-call event times, one pass with events around every call;
-    matmul: the per-call times of the step's products and their FLOPs."""
+    matmul: the step's products and their FLOPs; ms sums each product's own time (its call
+    repeated back to back on the step's operands), in_step_ms the event pairs around the products
+    inside the step pass (which include the GPU's wait for Python to issue each call)."""
     import replay
 
     recs = replay.load(ROOT / "tests" / "golden" / f"{name}_step_calls.jsonl.gz")
@@ -494,9 +496,26 @@ def bench_replay(backend, name, steps):
         per_call.append((r, ms.value))
         lib.kd_event_destroy(e0)
         lib.kd_event_destroy(e1)
-    mm = [(r, ms) for r, ms in per_call
-          if r["op"] in ("matmul", "matmul_strided", "matmul_strided_heads", "matmul_strided_bias")]
-    mm_ms = sum(ms for _, ms in mm)
+    products = ("matmul", "matmul_strided", "matmul_strided_heads", "matmul_strided_bias")
+    mm = [(r, ms) for r, ms in per_call if r["op"] in products]
+    in_step_ms = sum(ms for _, ms in mm)
+    # The pair around a call in the step also spans the time the GPU waits for Python to issue
+    # that call (the step blocks at its index checks and loss read, so the host never runs far
+    # ahead). Each product is therefore also timed alone: its own call, on the step's operands,
+    # `repeat` times back to back between one event pair, after one untimed call.
+    bound = []
+    rp.run(last, checked=False, on_call=lambda r, call: (call(), bound.append((r, call))))
+    repeat = 10
+    mm_ms = 0.0
+    for r, call in bound:
+        if r["op"] not in products:
+            continue
+        call()
+        with Timer(backend) as t:
+            for _ in range(repeat):
+                call()
+        mm_ms += t.ms / repeat
+    backend.synchronize()
     # row kernels: algorithmic bytes = the row arrays each one reads and writes once
     arrays = {"softmax_rows": 2, "standardize_rows": 2, "softmax_rows_backward": 3, "standardize_rows_backward": 4,
               "cross_entropy_rows": 1, "cross_entropy_grad": 2, "layer_norm_rows": 3, "layer_norm_rows_backward": 4}
@@ -509,7 +528,7 @@ def bench_replay(backend, name, steps):
         counts[r["op"]] = counts.get(r["op"], 0) + 1
     return {"step_ms": step_ms, "wall_ms": wall_ms, "kernel_ms": sum(ms for _, ms in per_call),
             "calls_per_step": len(last), "calls": counts,
-            "matmul": {"count": len(mm), "ms": mm_ms, "gflop": flops / 1e9,
+            "matmul": {"count": len(mm), "ms": mm_ms, "in_step_ms": in_step_ms, "gflop": flops / 1e9,
                        "tflops": flops / (mm_ms * 1e-3) / 1e12 if mm_ms else None,
                        "frac_peak": flops / (mm_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if mm_ms else None},
             "row_kernels": {"count": len(rows), "ms": row_ms, "gbytes": row_bytes / 1e9,

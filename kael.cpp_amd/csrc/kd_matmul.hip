@@ -1074,8 +1074,9 @@ __global__ __launch_bounds__(kThreads) void split_sum_kernel(const float* __rest
         const int64_t batch = idx / per_batch;
         const int64_t mn = idx % per_batch;
         // The partials come from memory (written by other XCDs): a batch of them is loaded before
-        // the first add, one round trip per batch; they are added in split order.
-        constexpr int kBatch = 8;
+        // the first add, one round trip per batch (C4's products split K at most 16 ways); they
+        // are added in split order.
+        constexpr int kBatch = 16;
         float v = 0.f;
         for (int64_t s0 = 0; s0 < splits; s0 += kBatch) {
             float x[kBatch];

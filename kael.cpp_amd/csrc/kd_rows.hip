@@ -210,13 +210,25 @@ __global__ __launch_bounds__(kThreads) void standardize_wave4_kernel(T* __restri
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
     if (row >= rows) return;
     const T* x = in + row * cols;
-    Quad<T> v[V4];
+    Quad<T> v[V4], wq[V4], bq[V4];
     double total = 0.0;
+    // the affine weight and bias are loaded with the row, so that their latency overlaps the row's
+    // instead of following the reductions
 #pragma unroll
     for (int j = 0; j < V4; ++j) {
         const int64_t c = 4 * (lane + 64 * j);
         if (c < cols) {
             v[j] = ld4<NT>(x + c);
+            if (w != nullptr) {
+                wq[j] = ld4<false>(w + c);
+                bq[j] = ld4<false>(b + c);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int64_t c = 4 * (lane + 64 * j);
+        if (c < cols) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) total += static_cast<double>(v[j].v[e]);
         }
@@ -248,10 +260,8 @@ __global__ __launch_bounds__(kThreads) void standardize_wave4_kernel(T* __restri
             for (int e = 0; e < 4; ++e) o.v[e] = static_cast<T>((static_cast<double>(v[j].v[e]) - center) * rscale);
             if (yhat != nullptr) st4<NT>(yhat + row * cols + c, o);
             if (w != nullptr) {
-                const Quad<T> wq = ld4<false>(w + c);
-                const Quad<T> bq = ld4<false>(b + c);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o.v[e] = add_rn(mul_rn(o.v[e], wq.v[e]), bq.v[e]);
+                for (int e = 0; e < 4; ++e) o.v[e] = add_rn(mul_rn(o.v[e], wq[j].v[e]), bq[j].v[e]);
             }
             st4<NT>(y + c, o);
         }
@@ -658,18 +668,18 @@ int row_backward_typed(T* out, const T* x, const T* y, const T* g, int64_t rows,
 //   grad_weight = sum over rows of g * y (each product rounded, summed in double),
 //   grad_bias   = sum over rows of g (in double).
 // ln_backward_wave4_kernel does all three in one pass for rows of <= 1024 (cols % 4 == 0): workgroup
-// s takes the rows [s * rs, s * rs + rs), wave w the rows s * rs + w + 4 i in increasing order;
-// each lane keeps the column sums of its columns in registers, the four waves add theirs in LDS in
+// s of W waves takes the rows [s * rs, s * rs + rs), wave w the rows s * rs + w + W i in increasing
+// order; each lane keeps the column sums of its columns in registers, the waves add theirs in LDS in
 // wave order, and the workgroup writes its partials (double) for ln_combine_kernel, which adds the
 // segments in order. Other shapes: ln_backward_block_kernel (a workgroup per row) for grad_in and
 // ln_columns_kernel for the column partials.
-template <typename T, int V4, bool NT>
-__global__ __launch_bounds__(kThreads) void ln_backward_wave4_kernel(T* __restrict__ grad_in, double* __restrict__ pw,
-                                                                     double* __restrict__ pb, const T* __restrict__ xin,
-                                                                     const T* __restrict__ yin, const T* __restrict__ gin,
-                                                                     const T* __restrict__ w, int64_t rows, int64_t cols,
-                                                                     int64_t rows_per_segment, double eps) {
-    constexpr int kWaves = kThreads / 64;
+template <typename T, int V4, bool NT, int Waves>
+__global__ __launch_bounds__(Waves * 64) void ln_backward_wave4_kernel(T* __restrict__ grad_in, double* __restrict__ pw,
+                                                                       double* __restrict__ pb, const T* __restrict__ xin,
+                                                                       const T* __restrict__ yin, const T* __restrict__ gin,
+                                                                       const T* __restrict__ w, int64_t rows, int64_t cols,
+                                                                       int64_t rows_per_segment, double eps) {
+    constexpr int kWaves = Waves;
     __shared__ double lds[kWaves][2][V4 * 4][64];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_segment;
@@ -903,14 +913,18 @@ int ln_backward_typed(T* grad_in, T* grad_w, T* grad_b, const T* x, const T* y, 
     if (quads) {
         const bool nt = rows * cols * static_cast<int64_t>(sizeof(T)) >= (int64_t{16} << 20);
         const dim3 grid(static_cast<uint32_t>(segments));
-#define KD_LN4(V4)                                                                                                      \
-    if (nt) hipLaunchKernelGGL((ln_backward_wave4_kernel<T, V4, true>), grid, block, 0, stream(), grad_in, pw, pb, x, y, g, w, \
-                               rows, cols, rows_per_segment, eps);                                                      \
-    else hipLaunchKernelGGL((ln_backward_wave4_kernel<T, V4, false>), grid, block, 0, stream(), grad_in, pw, pb, x, y, g, w, \
-                            rows, cols, rows_per_segment, eps);
-        if (cols <= 256) { KD_LN4(1) }
-        else if (cols <= 512) { KD_LN4(2) }
-        else { KD_LN4(4) }
+#define KD_LN4(V4, W)                                                                                                   \
+    if (nt) hipLaunchKernelGGL((ln_backward_wave4_kernel<T, V4, true, W>), grid, dim3(64 * W), 0, stream(), grad_in, pw, pb, \
+                               x, y, g, w, rows, cols, rows_per_segment, eps);                                          \
+    else hipLaunchKernelGGL((ln_backward_wave4_kernel<T, V4, false, W>), grid, dim3(64 * W), 0, stream(), grad_in, pw, pb, \
+                            x, y, g, w, rows, cols, rows_per_segment, eps);
+        // Rows of <= 256 columns: 16 waves per workgroup, so that a segment of 16 rows gives each
+        // wave one row (C4's 4096 x 256: the row chains of the four waves of a 256-thread group ran
+        // one after another, four rows each). Longer rows: 4 waves (their column partials in LDS
+        // would not fit 16).
+        if (cols <= 256) { KD_LN4(1, 16) }
+        else if (cols <= 512) { KD_LN4(2, 4) }
+        else { KD_LN4(4, 4) }
 #undef KD_LN4
         KD_LAUNCH_CHECK();
     } else {

@@ -21,7 +21,11 @@ pytestmark = pytest.mark.gpu
 
 P = support.ptr
 EPS = 1e-5
-SHAPES = [(4096, 256), (64, 768), (8, 1024), (33, 1000), (5, 7), (3, 1030), (1, 256), (300, 512)]
+# The backward's row groups (a wave loads 4 rows of <= 256 columns, 2 of <= 512, 1 of <= 1024
+# before it processes them): 4096 x 256 and 300 x 512 fill them, 200 x 256 and 20000 x 256 leave a
+# partial last group, 1 x 256 a group of one row.
+SHAPES = [(4096, 256), (64, 768), (8, 1024), (33, 1000), (5, 7), (3, 1030), (1, 256), (300, 512), (200, 256),
+          (20000, 256)]
 
 
 def inputs(rows, cols, npd, seed):
