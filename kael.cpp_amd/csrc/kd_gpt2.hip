@@ -1394,22 +1394,40 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const Step* st, con
 // The row LayerNorm H[t] = LayerNorm(X[t]) of a row that lane i of the workgroup has just
 // computed at elements i, i + 256, ... (x[j], j < 4), as ln_load and ln_finish compute it from
 // memory: the pivot x[0] passes through LDS.
-__device__ __forceinline__ void ln_row_from_lanes(const float (&x)[4], int64_t d, const float* w, const float* b,
-                                                  float* h) {
+// The weight and bias elements of lane i (i, i + 256, ...) are given already loaded.
+__device__ __forceinline__ void ln_row_from_lanes(const float (&x)[4], int64_t d, const float (&w)[4],
+                                                  const float (&b)[4], float* h) {
     __shared__ float pivot;
     LnIn r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t i = threadIdx.x + j * kThreads;
         r.x[j] = i < d ? x[j] : 0.f;
-        r.w[j] = i < d ? w[i] : 0.f;
-        r.b[j] = i < d ? b[i] : 0.f;
+        r.w[j] = i < d ? w[j] : 0.f;
+        r.b[j] = i < d ? b[j] : 0.f;
     }
     if (threadIdx.x == 0) pivot = x[0];
     __syncthreads();
     r.c = pivot;
     ln_finish(r, d, h);
 }
+
+__device__ __forceinline__ void ln_row_from_lanes(const float (&x)[4], int64_t d, const float* w, const float* b,
+                                                  float* h) {
+    float wl[4], bl[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t i = threadIdx.x + j * kThreads;
+        wl[j] = i < d ? w[i] : 0.f;
+        bl[j] = i < d ? b[i] : 0.f;
+    }
+    ln_row_from_lanes(x, d, wl, bl, h);
+}
+
+// Split-K partial products whose loads a thread issues together: one memory round trip for up to
+// this many splits (the prefill's products split K at most 16 ways on 256 CUs). The loads read
+// clamped, always valid addresses, so that no branch separates them.
+constexpr int kSplitBatch = 16;
 
 // X[t] = wte[seq[t]] + wpe[t], and H[t] = LayerNorm(X[t]) with the first block's ln1; one
 // workgroup per row.
@@ -1439,44 +1457,53 @@ __global__ __launch_bounds__(kThreads) void prefill_residual_kernel(const float*
                                                                     const float* bias, float* X, const float* ln_w,
                                                                     const float* ln_b, float* H, int64_t d) {
     const int64_t t = blockIdx.x;
-    float p[4];
+    // every load first: the residual row, the bias, the next LayerNorm's parameters (the bias
+    // again, unused, without one), the partials
+    const float* lwp = ln_w != nullptr ? ln_w : bias;
+    const float* lbp = ln_w != nullptr ? ln_b : bias;
+    float xr[4], bs[4], lw[4], lb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t i = threadIdx.x + j * kThreads;
-        p[j] = i < d ? P[t * d + i] : 0.f;
+        const int64_t i = std::min<int64_t>(threadIdx.x + j * kThreads, d - 1);
+        xr[j] = X[t * d + i];
+        bs[j] = bias[i];
+        lw[j] = lwp[i];
+        lb[j] = lbp[i];
     }
-    int64_t s = 1;
-    for (; s + 4 <= splits; s += 4) {  // the partials' loads in flight together, added in split order
-        float v[4][4];
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
+    if (splits == 1) {  // one product (longer prompts)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int j = 0; j < 4; ++j) p[j] = P[t * d + std::min<int64_t>(threadIdx.x + j * kThreads, d - 1)];
+    }
+    for (int64_t s0 = 0; s0 < splits && splits > 1; s0 += kSplitBatch) {
+        float v[kSplitBatch][4];
+#pragma unroll
+        for (int q = 0; q < kSplitBatch; ++q) {
+            const int64_t sq = std::min<int64_t>(s0 + q, splits - 1);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int64_t i = threadIdx.x + j * kThreads;
-                v[q][j] = i < d ? P[(s + q) * split_stride + t * d + i] : 0.f;
+                const int64_t i = std::min<int64_t>(threadIdx.x + j * kThreads, d - 1);
+                v[q][j] = P[sq * split_stride + t * d + i];
             }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] = __fadd_rn(p[j], v[q][j]);
-    }
-    for (; s < splits; ++s)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t i = threadIdx.x + j * kThreads;
-            if (i < d) p[j] = __fadd_rn(p[j], P[s * split_stride + t * d + i]);
         }
+#pragma unroll
+        for (int q = 0; q < kSplitBatch; ++q)  // added in split order
+            if (s0 + q < splits) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) p[j] = s0 + q == 0 ? v[q][j] : __fadd_rn(p[j], v[q][j]);
+            }
+    }
     float x[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t i = threadIdx.x + j * kThreads;
         x[j] = 0.f;
         if (i < d) {
-            x[j] = __fadd_rn(X[t * d + i], __fadd_rn(p[j], bias[i]));
+            x[j] = __fadd_rn(xr[j], __fadd_rn(p[j], bs[j]));
             X[t * d + i] = x[j];
         }
     }
-    if (ln_w != nullptr) ln_row_from_lanes(x, d, ln_w, ln_b, H + t * d);
+    if (ln_w != nullptr) ln_row_from_lanes(x, d, lw, lb, H + t * d);
 }
 
 // y = P[t, n] + bias[n] for the T x N product P (row stride N; with split K, P[t, n] is the sum
@@ -1484,7 +1511,7 @@ __global__ __launch_bounds__(kThreads) void prefill_residual_kernel(const float*
 //   kQkv       query part -> Q[t, n]; key and value parts -> the cache rows of position t
 //   kGelu*     F[t, n] = gelu(y)
 // (the residual products take prefill_residual_kernel, which also computes the next LayerNorm).
-template <int Epi>
+template <int Epi, int Batch>
 __global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float* P, int64_t splits, int64_t split_stride,
                                                                     const float* bias, float* out, int64_t T, int64_t N,
                                                                     int64_t d, int64_t head_dim, int64_t max_positions,
@@ -1494,17 +1521,17 @@ __global__ __launch_bounds__(kThreads) void prefill_epilogue_kernel(const float*
          e += static_cast<int64_t>(gridDim.x) * kThreads) {
         const int64_t t = e / N;
         const int64_t n = e - t * N;
-        float p = P[e];
-        int64_t s = 1;
-        for (; s + 8 <= splits; s += 8) {  // eight partials' loads in flight, added in split order
-            float v[8];
+        const float bn = bias[n];
+        float p = splits == 1 ? P[e] : 0.f;  // one product (longer prompts) or split partials
+        for (int64_t s0 = 0; s0 < splits && splits > 1; s0 += Batch) {
+            float v[Batch];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = P[(s + j) * split_stride + e];
+            for (int q = 0; q < Batch; ++q) v[q] = P[std::min<int64_t>(s0 + q, splits - 1) * split_stride + e];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) p = __fadd_rn(p, v[j]);
+            for (int q = 0; q < Batch; ++q)  // added in split order
+                if (s0 + q < splits) p = s0 + q == 0 ? v[q] : __fadd_rn(p, v[q]);
         }
-        for (; s < splits; ++s) p = __fadd_rn(p, P[s * split_stride + e]);
-        const float y = __fadd_rn(p, bias[n]);
+        const float y = __fadd_rn(p, bn);
         if constexpr (Epi == kQkv) {
             const int64_t part = n / d;
             const int64_t within = n - part * d;
@@ -1894,8 +1921,18 @@ struct Engine {
     void epilogue(const Product& pr, const float* bias, float* out, int64_t T, int64_t N, float* kc, float* vc) const {
         const int64_t total = T * N;
         const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, int64_t{compute_units()} * 16);
-        hipLaunchKernelGGL((prefill_epilogue_kernel<Epi>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, kd::stream(),
-                           pr.P, pr.splits, pr.stride, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
+        // partial loads in flight per element: the fewest of 4, 8, 16 that cover the splits (each
+        // load past the last split repeats it: measured 0.5 us slower per launch at 4 splits with 16)
+        const dim3 grid(static_cast<uint32_t>(blocks));
+        if (pr.splits <= 4)
+            hipLaunchKernelGGL((prefill_epilogue_kernel<Epi, 4>), grid, dim3(kThreads), 0, kd::stream(), pr.P, pr.splits,
+                               pr.stride, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
+        else if (pr.splits <= 8)
+            hipLaunchKernelGGL((prefill_epilogue_kernel<Epi, 8>), grid, dim3(kThreads), 0, kd::stream(), pr.P, pr.splits,
+                               pr.stride, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
+        else
+            hipLaunchKernelGGL((prefill_epilogue_kernel<Epi, kSplitBatch>), grid, dim3(kThreads), 0, kd::stream(), pr.P,
+                               pr.splits, pr.stride, bias, out, T, N, d, hd, cfg.max_positions, kc, vc);
     }
 
     // Positions 0..T-1 of seq (already on the device) through every layer at once; then the
