@@ -833,22 +833,29 @@ __global__ __launch_bounds__(kThreads) void ln_columns_kernel(double* __restrict
     }
 }
 
-// The weight and bias gradients from the segment partials: 16 waves per 64 columns, wave v adding
-// the contiguous segments [v q, v q + q) (8 loads of each array in flight per lane), the waves in
-// order in LDS, so every column sums its segments in order.
+// The weight and bias gradients from the segment partials: a workgroup of 16 waves per 16 columns
+// (C4's 256 columns: 16 workgroups), lane i of wave w on column i % 16 and the contiguous segment
+// range r = 4 w + i / 16 of 64 (8 loads of each array in flight per lane). Each range is summed in
+// segment order, a wave's four ranges in order, then the 16 waves' sums in order: every column in
+// the same fixed order.
 constexpr int kCombineThreads = 1024;
+constexpr int kCombineCols = 16;
 template <typename T>
 __global__ __launch_bounds__(kCombineThreads) void ln_combine_kernel(T* __restrict__ grad_w, T* __restrict__ grad_b,
                                                                      const double* __restrict__ pw,
                                                                      const double* __restrict__ pb, int64_t segments,
                                                                      int64_t cols) {
     constexpr int kWaves = kCombineThreads / 64;
+    constexpr int kRanges = kWaves * (64 / kCombineCols);
     constexpr int kBatch = 8;
-    __shared__ double lds[kWaves][2][64];
+    __shared__ double ranges[2][kRanges][kCombineCols];
+    __shared__ double waves[2][kWaves][kCombineCols];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
-    const int64_t q = (segments + kWaves - 1) / kWaves;
-    const int64_t s0 = std::min<int64_t>(segments, wave * q);
+    const int ci = lane % kCombineCols;
+    const int r = wave * (64 / kCombineCols) + lane / kCombineCols;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kCombineCols + ci;
+    const int64_t q = (segments + kRanges - 1) / kRanges;
+    const int64_t s0 = std::min<int64_t>(segments, r * q);
     const int64_t s1 = std::min<int64_t>(segments, s0 + q);
     double sw = 0.0, sb = 0.0;
     if (c < cols) {
@@ -868,16 +875,28 @@ __global__ __launch_bounds__(kCombineThreads) void ln_combine_kernel(T* __restri
                 }
         }
     }
-    lds[wave][0][lane] = sw;
-    lds[wave][1][lane] = sb;
+    ranges[0][r][ci] = sw;
+    ranges[1][r][ci] = sb;
     __syncthreads();
-    if (wave == 0 && c < cols) {
-        for (int v = 1; v < kWaves; ++v) {
-            sw += lds[v][0][lane];
-            sb += lds[v][1][lane];
+    if (lane < kCombineCols) {  // the wave's four ranges, in order
+        double w4 = ranges[0][r][ci], b4 = ranges[1][r][ci];
+#pragma unroll
+        for (int k = 1; k < 64 / kCombineCols; ++k) {
+            w4 += ranges[0][r + k][ci];
+            b4 += ranges[1][r + k][ci];
         }
-        if (grad_w != nullptr) grad_w[c] = static_cast<T>(sw);
-        if (grad_b != nullptr) grad_b[c] = static_cast<T>(sb);
+        waves[0][wave][ci] = w4;
+        waves[1][wave][ci] = b4;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kCombineCols && c < cols) {
+        double tw = waves[0][0][ci], tb = waves[1][0][ci];
+        for (int v = 1; v < kWaves; ++v) {
+            tw += waves[0][v][ci];
+            tb += waves[1][v][ci];
+        }
+        if (grad_w != nullptr) grad_w[c] = static_cast<T>(tw);
+        if (grad_b != nullptr) grad_b[c] = static_cast<T>(tb);
     }
 }
 
@@ -941,7 +960,7 @@ int ln_backward_typed(T* grad_in, T* grad_w, T* grad_b, const T* x, const T* y, 
         }
     }
     if (columns) {
-        const int64_t col_blocks = (cols + 63) / 64;
+        const int64_t col_blocks = (cols + kCombineCols - 1) / kCombineCols;
         if (col_blocks > int64_t{0xffffffff}) return fail(KD_E_INVALID, "layer norm backward: too many columns");
         hipLaunchKernelGGL((ln_combine_kernel<T>), dim3(static_cast<uint32_t>(col_blocks)), dim3(kCombineThreads), 0,
                            stream(), grad_w, grad_b, static_cast<const double*>(pw), static_cast<const double*>(pb),
