@@ -546,13 +546,14 @@ int kd_gpt_sequence(void* handle, int64_t* ids, int64_t capacity, int64_t* lengt
  * generate returns tokens only); for parity checks of the prefill paths. */
 int kd_gpt_logits(void* handle, float* logits);
 /* The pick of every following prefill and decode step: temperature 0 is the greedy pick (the
- * default); temperature > 0 with 0 < top_k < vocab_size is kael's sample_next (reference
- * src/nn/transformer.cpp:39-50: logits / temperature, the top_k largest kept, softmax,
- * multinomial of one sample, src/random.cpp:106-160) on the device, drawing the next uniform
- * given by kd_gpt_set_uniforms for each sampled token. Without a top-k, kael's multinomial sums
- * every probability of the vocabulary in sequence: KD_E_UNSUPPORTED (kael's own loop samples); so
- * is a vocabulary above KD_GPT_SAMPLE_MAX_VOCAB, whose keys no longer fit the picking workgroup's
- * registers. */
+ * default); temperature > 0 is kael's sample_next (reference src/nn/transformer.cpp:39-50:
+ * logits / temperature, with 0 < top_k < vocab_size the top_k largest kept, otherwise (top_k 0,
+ * kael's default, or top_k >= vocab_size) every entry, softmax, multinomial of one sample,
+ * src/random.cpp:106-160) on the device, drawing the next uniform given by kd_gpt_set_uniforms
+ * for each sampled token. Without a top-k the softmax and multinomial sums run over the whole
+ * vocabulary in index order, as kael's do, in one wave (about 0.5 ms per token for GPT-2's).
+ * A vocabulary above KD_GPT_SAMPLE_MAX_VOCAB, whose keys no longer fit the picking workgroup's
+ * registers, is KD_E_UNSUPPORTED when sampled (kael's own loop samples). */
 #define KD_GPT_SAMPLE_MAX_VOCAB 65536
 int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k);
 /* The uniform draws in [0, 1) for the next `count` sampled picks, in order (at most

@@ -655,12 +655,12 @@ __global__ __launch_bounds__(kThreads) void head_kernel(GemvArgs a) {
 //   Greedy (sampler top_k 0): the first maximum among the head's workgroup partials (one per
 //   head workgroup: 1024 for GPT-2 small).
 //   Sampled: kael's sample_next (reference src/nn/transformer.cpp:39-50) and multinomial
-//   (src/random.cpp:106-160) for 0 < top_k < vocab: x = logits / temperature (f32 division, in
-//   head_kernel, which writes x's order-preserving 32-bit keys and each workgroup's extremes);
-//   a lower bound of the k-th largest key from the k-th largest head-workgroup maximum (or, in
-//   the full scan, lane maximum), the keys at or above it (about k) listed, the k-th largest among
-//   them by rank counting or radix selects (8-bit digits, per-wave histograms); for k > 1024 a
-//   radix select over every key. The kept entries (x >= the k-th largest: masked_fill's
+//   (src/random.cpp:106-160): x = logits / temperature (f32 division, in head_kernel, which
+//   writes x's order-preserving 32-bit keys and each workgroup's extremes); a lower bound of the
+//   k-th largest key from the k-th largest head-workgroup maximum (or, in the full scan, lane
+//   maximum), the keys at or above it (about k) listed, the k-th largest among them by rank
+//   counting or radix selects (8-bit digits, per-wave histograms); for k > 1024 a radix select
+//   over every key; without a top-k (k = vocab, kael's masking skipped) every entry. The kept entries (x >= the k-th largest: masked_fill's
 //   complement) are listed in index order with their e = exp(x - max); then, in kael's order, the
 //   sum of e in double rounded to f32, p = e / sum, the cumulative double sum of p, point = u *
 //   sum, the first kept entry whose cumulative sum exceeds the point (upper_bound; the masked
@@ -1113,15 +1113,17 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
                 keep, [&](int j, int64_t at, int64_t) { sh.kept_i[at] = sh.cand_idx[j * kPickThreads + tid]; }, sh);
         }
     } else {
-        const uint32_t kth = max(low, radix_select(
-                                          [&](const auto& f) {
+        // without a top-k (top_k = the vocabulary) every entry is kept: the cut is the smallest key
+        const uint32_t kth = top_k >= V ? kmin
+                                        : max(low, radix_select(
+                                                       [&](const auto& f) {
 #pragma unroll
-                                              for (int s = 0; s < kPickSlots; ++s) {
-                                                  const uint32_t k = key_at(s);
-                                                  f(k, k >= low);
-                                              }
-                                          },
-                                          top_k, sh));
+                                                           for (int s = 0; s < kPickSlots; ++s) {
+                                                               const uint32_t k = key_at(s);
+                                                               f(k, k >= low);
+                                                           }
+                                                       },
+                                                       top_k, sh));
         uint64_t keep = 0;
 #pragma unroll
         for (int s = 0; s < kPickSlots; ++s) keep |= uint64_t{key_at(s) >= kth} << s;
@@ -1198,41 +1200,95 @@ __device__ __forceinline__ void sample_pick(const PickArgs& a, int64_t& token) {
         else token = kept[0];
         return;
     }
+    // Whole groups of 64 fold with the lane index a constant (unrolled: no loop counter or
+    // computed lane select in the dependent chain of additions), the last group in a loop. The
+    // group is widened to double once, so each entry is two lane reads into scalar registers,
+    // off the chain, and one addition.
+    const auto fold = [&](float v, int64_t base, auto&& add) {
+        const double w = static_cast<double>(v);
+        if (m - base >= 64) {
+#pragma unroll
+            for (int j0 = 0; j0 < 64; j0 += 16) {  // 16 entries read ahead of their additions
+                double x[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) x[j] = lane_value(w, j0 + j);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) add(j0 + j, x[j]);
+            }
+        } else {
+            const int n = static_cast<int>(m - base);
+            for (int j = 0; j < n; ++j) add(j, lane_value(w, j));
+        }
+    };
+    // The groups in index order, lane j holding entry base + j (0 past the list): the loads of
+    // the next kAhead groups go out before the current kAhead groups fold, since a list longer
+    // than the LDS stage lives in global memory, a round trip away. The loads read clamped, always
+    // valid, indices, so that no branch separates them.
+    constexpr int kAhead = 4;
+    const auto groups = [&](auto&& body) {  // body(e, index, base) for each group
+        float ec[kAhead], en[kAhead];
+        int32_t ic[kAhead], in_[kAhead];
+        const auto load = [&](int64_t base, float (&e)[kAhead], int32_t (&ix)[kAhead]) {
+#pragma unroll
+            for (int g = 0; g < kAhead; ++g) {
+                const int64_t i = base + g * 64 + lane;
+                const int64_t c = min<int64_t>(i, m - 1);
+                e[g] = kept_e[c];
+                ix[g] = kept[c];
+                if (i >= m) e[g] = 0.f;
+            }
+        };
+        load(0, ec, ic);
+        for (int64_t base = 0; base < m; base += kAhead * 64) {
+            load(base + kAhead * 64, en, in_);  // (past the list: clamped, unused)
+#pragma unroll
+            for (int g = 0; g < kAhead; ++g)
+                if (base + g * 64 < m && !body(ec[g], ic[g], base + g * 64)) return;
+#pragma unroll
+            for (int g = 0; g < kAhead; ++g) {
+                ec[g] = en[g];
+                ic[g] = in_[g];
+            }
+        }
+    };
     // the sum of e in double in index order, rounded to f32
     double sum = 0.0;
-    for (int64_t base = 0; base < m; base += 64) {
-        const float e = base + lane < m ? kept_e[base + lane] : 0.f;
-        const int n = static_cast<int>(min<int64_t>(64, m - base));
-        for (int j = 0; j < n; ++j) sum += entry(e, j);
-    }
+    groups([&](float e, int32_t, int64_t base) {
+        fold(e, base, [&](int, double x) { sum += x; });
+        return true;
+    });
     const float denominator = static_cast<float>(sum);
     // multinomial (src/random.cpp:143-151): the cumulative sum in double, point = u * total,
     // upper_bound, and the step back to a positive weight when the point is past every sum
     double cumulative = 0.0;
-    for (int64_t base = 0; base < m; base += 64) {
-        const float p = base + lane < m ? __fdiv_rn(kept_e[base + lane], denominator) : 0.f;
-        const int n = static_cast<int>(min<int64_t>(64, m - base));
-        for (int j = 0; j < n; ++j) cumulative += entry(p, j);
-    }
+    groups([&](float e, int32_t, int64_t base) {
+        fold(__fdiv_rn(e, denominator), base, [&](int, double x) { cumulative += x; });
+        return true;
+    });
     const double point = u * cumulative;
+    // the walk: each group's running sums are the previous group's end plus a prefix in order,
+    // so the first group whose end passes the point holds the pick
     double run = 0.0;
     int64_t pick = -1, last_positive = kept[0];
-    for (int64_t base = 0; base < m && pick < 0; base += 64) {
-        const bool in = base + lane < m;
-        const float p = in ? __fdiv_rn(kept_e[base + lane], denominator) : 0.f;
-        const int32_t index = in ? kept[base + lane] : 0;
-        const int n = static_cast<int>(min<int64_t>(64, m - base));
-        for (int j = 0; j < n; ++j) {
-            const double pj = entry(p, j);
-            const int32_t ij = __builtin_amdgcn_readlane(index, j);
-            run += pj;
-            if (pj > 0.0) last_positive = ij;
-            if (run > point) {
-                pick = ij;
-                break;
+    groups([&](float e, int32_t index, int64_t base) {
+        const float p = __fdiv_rn(e, denominator);  // 0 past the list
+        double end = run;
+        fold(p, base, [&](int, double x) { end += x; });
+        const uint64_t positive = __ballot(p > 0.f);
+        if (end > point) {  // the pick is in this group: walk it entry by entry
+            const int n = static_cast<int>(min<int64_t>(64, m - base));
+            for (int j = 0; j < n; ++j) {
+                run += lane_value(static_cast<double>(p), j);
+                if (run > point) {
+                    pick = __builtin_amdgcn_readlane(index, j);
+                    return false;
+                }
             }
         }
-    }
+        run = end;
+        if (positive != 0) last_positive = __builtin_amdgcn_readlane(index, 63 - __clzll(static_cast<long long>(positive)));
+        return true;
+    });
     token = pick >= 0 ? pick : last_positive;
 }
 
@@ -2340,10 +2396,6 @@ int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k) {
     auto* e = static_cast<Engine*>(handle);
     if (e == nullptr || !(temperature >= 0.0) || top_k < 0)
         return fail(KD_E_INVALID, "kd_gpt_set_sampling: needs a temperature >= 0 and top_k >= 0");
-    if (temperature > 0.0 && (top_k == 0 || top_k >= e->cfg.vocab_size))
-        return fail(KD_E_UNSUPPORTED,
-                    "kd_gpt_set_sampling: sampling on the device needs 0 < top_k < vocab_size (without a top-k, kael "
-                    "sums every probability of the vocabulary in sequence)");
     if (temperature > 0.0 && e->cfg.vocab_size > KD_GPT_SAMPLE_MAX_VOCAB)
         return fail(KD_E_UNSUPPORTED, "kd_gpt_set_sampling: sampling on the device takes vocabularies of at most "
                                       "KD_GPT_SAMPLE_MAX_VOCAB (65536) entries");
@@ -2352,7 +2404,9 @@ int kd_gpt_set_sampling(void* handle, double temperature, int64_t top_k) {
         return fail(KD_E_INVALID, "kd_gpt_set_sampling: the temperature does not round to a positive finite float");
     KD_HIP(hipStreamSynchronize(e->stream));
     KD_HIP(hipStreamSynchronize(kd::stream()));
-    e->host_sp = Sampler{t, 0, temperature > 0.0 ? top_k : 0, 0, 0};
+    // top_k 0 or >= the vocabulary: kael masks nothing, which keeping all vocab_size entries restates
+    const int64_t keep = top_k == 0 || top_k >= e->cfg.vocab_size ? e->cfg.vocab_size : top_k;
+    e->host_sp = Sampler{t, 0, temperature > 0.0 ? keep : 0, 0, 0};
     KD_HIP(hipMemcpy(e->sp, &e->host_sp, sizeof(Sampler), hipMemcpyHostToDevice));
     return KD_OK;
 }

@@ -569,15 +569,17 @@ STANDARDIZE_BACKWARD_BRANCH = """                if (auto fused = fused_standard
                 }
 """
 
-GENERATE_HELPER = """// MI355X: greedy generation with a KV cache of a batch-1 prompt on the device runs on the backend's
-// decode engine (one captured step per token, the greedy pick on the device) when the engine
-// takes the model's shape; no value otherwise, and the loop of generate() runs.
+GENERATE_HELPER = """// MI355X: generation with a KV cache of a batch-1 prompt on the device runs on the backend's
+// decode engine (one captured step per token, the greedy pick or sample_next on the device) when
+// the engine takes the model's shape and the temperature (0, or a positive finite float); no
+// value otherwise, and the loop of generate() runs.
 std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const GenerateOptions& options) {
     const GptConfig& config = model.config();
     const bool sampled = options.temperature != 0.0;
+    const float temperature = static_cast<float>(options.temperature);
     if (prompt.device() == Device::CPU || !options.use_cache || prompt.size(0) != 1 || options.max_new_tokens == 0 ||
         config.dtype != DType::F32 || prompt.dtype() != DType::I64 ||
-        (sampled && (options.top_k <= 0 || options.top_k >= config.vocab_size ||
+        (sampled && (!(temperature > 0.0f) || !std::isfinite(temperature) ||
                      config.vocab_size > device::kGptSampleMaxVocab))) {
         return std::nullopt;
     }
@@ -606,7 +608,9 @@ std::optional<Tensor> device_generate(GPT& model, const Tensor& prompt, const Ge
     // Sampled picks take kael's generator's next draws in order (one per token, as multinomial
     // takes them), handed to the engine in runs of at most one context; the generator is then
     // advanced by exactly the draws used.
-    device::gpt_engine_set_sampling(engine.handle, options.temperature, sampled ? options.top_k : 0);
+    // sample_next masks only for 0 < top_k < vocab: any other top_k keeps every entry (the engine's top_k 0)
+    device::gpt_engine_set_sampling(engine.handle, options.temperature,
+                                    sampled && options.top_k > 0 ? options.top_k : 0);
     const std::int64_t run = config.max_positions + 1;
     const auto hand_over = [&](std::int64_t picks) {
         if (sampled) {

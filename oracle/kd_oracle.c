@@ -1017,10 +1017,10 @@ int oracle_cached_attention(int dtype, void* out, const void* q, const int64_t* 
 
 /* ---- sampled next token: kael's sample_next with a top-k -------------------------------------
  *
- * Reference src/nn/transformer.cpp:39-50 for one row of `vocab` logits with temperature > 0 and
- * 0 < top_k < vocab: x = logits / temperature (kael's scalar converted to f32, one f32
- * division); topk(x, k) (src/ops/sequence.cpp:124-128) gives the k-th largest value t; x < t is
- * masked_fill'ed with -inf; softmax's CPU row kernel (src/ops/nn.cpp:60-71: largest, f32
+ * Reference src/nn/transformer.cpp:39-50 for one row of `vocab` logits with temperature > 0:
+ * x = logits / temperature (kael's scalar converted to f32, one f32 division); for
+ * 0 < top_k < vocab, topk(x, k) (src/ops/sequence.cpp:124-128) gives the k-th largest value t and
+ * x < t is masked_fill'ed with -inf (top_k 0 or >= vocab: nothing is masked); softmax's CPU row kernel (src/ops/nn.cpp:60-71: largest, f32
  * exponentials of x - largest, their sum in double in index order rounded to f32, each divided
  * by it); multinomial of one sample with the draw u (src/random.cpp:117-155: the weights as
  * double, partial_sum, point = u * total, upper_bound, the end mapped to the last entry, then
@@ -1032,8 +1032,10 @@ static int descending_float(const void* a, const void* b) {
 
 int oracle_sample_topk(const float* logits, int64_t vocab, double temperature, int64_t top_k, double uniform,
                        int64_t* token) {
-    if (logits == NULL || token == NULL || vocab < 2 || top_k <= 0 || top_k >= vocab || !(temperature > 0.0))
-        return fail("sample_topk: needs vocab >= 2, 0 < top_k < vocab and temperature > 0");
+    if (logits == NULL || token == NULL || vocab < 2 || top_k < 0 || !(temperature > 0.0))
+        return fail("sample_topk: needs vocab >= 2, top_k >= 0 and temperature > 0");
+    /* kael masks below the k-th largest only for 0 < top_k < vocab (top_k 0 is its default) */
+    const int masked = top_k > 0 && top_k < vocab;
     if (!(uniform >= 0.0 && uniform < 1.0)) return fail("sample_topk: the draw must lie in [0, 1)");
     const float t = (float)temperature;
     float* x = (float*)malloc((size_t)vocab * sizeof(float));
@@ -1047,7 +1049,7 @@ int oracle_sample_topk(const float* logits, int64_t vocab, double temperature, i
     }
     if (rc == KD_OK) {
         qsort(sorted, (size_t)vocab, sizeof(float), descending_float);
-        const float kth = sorted[top_k - 1];
+        const float kth = masked ? sorted[top_k - 1] : sorted[vocab - 1];
         float largest = -INFINITY;
         for (int64_t i = 0; i < vocab; ++i) {
             if (x[i] < kth) x[i] = -INFINITY;

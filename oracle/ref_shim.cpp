@@ -1069,8 +1069,9 @@ int ref_attention_module(int device, int64_t batch, int64_t length, int64_t dim,
 // kael's sample_next for one row of logits (reference src/nn/transformer.cpp:39-50, the
 // function is internal to that file, so its four ops are called here as it calls them) with
 // temperature > 0 and top_k, on the CPU path: manual_seed(seed), `skip` uniform draws
-// (kael::rand of that many f64 values), then logits / temperature, topk, masked_fill, softmax
-// and multinomial of one sample. Writes the picked id.
+// (kael::rand of that many f64 values), then logits / temperature, topk and masked_fill when
+// 0 < top_k < vocab (as sample_next tests it), softmax and multinomial of one sample. Writes the
+// picked id.
 int ref_sample_next(uint64_t seed, int64_t skip, const float* logits, int64_t vocab, double temperature, int64_t top_k,
                     int64_t* token) {
     return guarded([&] {
@@ -1078,9 +1079,11 @@ int ref_sample_next(uint64_t seed, int64_t skip, const float* logits, int64_t vo
         if (skip > 0) (void)kael::rand({skip}, kael::DType::F64);
         const kael::Tensor last = host_tensor(logits, {1, vocab}, kael::DType::F32);
         kael::Tensor scaled = last / temperature;
-        const kael::Tensor smallest_kept = kael::topk(scaled, top_k).values.select(-1, top_k - 1);
-        scaled = kael::masked_fill(scaled, scaled < smallest_kept.unsqueeze(-1),
-                                   -std::numeric_limits<double>::infinity());
+        if (top_k > 0 && top_k < vocab) {  // sample_next's condition: top_k 0 (its default) masks nothing
+            const kael::Tensor smallest_kept = kael::topk(scaled, top_k).values.select(-1, top_k - 1);
+            scaled = kael::masked_fill(scaled, scaled < smallest_kept.unsqueeze(-1),
+                                       -std::numeric_limits<double>::infinity());
+        }
         const kael::Tensor next = kael::multinomial(kael::softmax(scaled, -1), 1, true);
         *token = next.item<std::int64_t>();
     });

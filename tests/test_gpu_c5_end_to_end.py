@@ -256,20 +256,23 @@ def test_kael_sampled_generate_with_its_cache_on_the_device(request, variant):
 
 
 @pytest.mark.timeout(300)
-def test_kael_sampled_generate_on_the_engine(kael_hip_fused):
-    """The reference example's sampling (examples/gpt2_generate.cpp: temperature 0.8, top-k 40) through
-    kael's nn::generate: the fused build runs it on the decode engine with the device sampler, the
-    draws taken from kael's generator; the tokens must equal kael's CPU generate with the same seed
-    (its sample_next on the host), for 64 tokens after a 16-token prompt, and the generator's next draw
-    afterwards must be the same (the engine used exactly one draw per token)."""
+@pytest.mark.parametrize("temperature, top_k", [(0.8, 40), (1.0, 0)], ids=["example_t0.8_k40", "default_t1_none"])
+def test_kael_sampled_generate_on_the_engine(kael_hip_fused, temperature, top_k):
+    """The reference example's sampling (examples/gpt2_generate.cpp: temperature 0.8, top-k 40), and
+    GenerateOptions' defaults (temperature 1, top_k 0: nothing masked, the whole vocabulary summed),
+    through kael's nn::generate: the fused build runs it on the decode engine with the device
+    sampler, the draws taken from kael's generator; the tokens must equal kael's CPU generate with
+    the same seed (its sample_next on the host), for 64 tokens after a 16-token prompt, and the
+    generator's next draw afterwards must be the same (the engine used exactly one draw per token)."""
     lib = kael_hip_fused
     lib.ref_set_threads(threads())
     prompt = np.random.default_rng(11).integers(0, VOCAB, 16)
     new = 64
-    cpu, cpu_s, cpu_next = sampled(lib, 0, prompt, 1, new, 0.8, 40, 5)
-    dev, dev_s, dev_next = sampled(lib, 1, prompt, 1, new, 0.8, 40, 5)
+    cpu, cpu_s, cpu_next = sampled(lib, 0, prompt, 1, new, temperature, top_k, 5)
+    dev, dev_s, dev_next = sampled(lib, 1, prompt, 1, new, temperature, top_k, 5)
     np.testing.assert_array_equal(dev, cpu)
     assert dev_next == cpu_next
     assert len(set(cpu[0, 16:].tolist())) > 8  # sampled, not one repeated token
-    print(f"\nkael nn::generate, temperature 0.8, top-k 40, on the MI355X decode engine: {new} tokens in {dev_s:.2f} s "
-          f"= {new / dev_s:.1f} tokens/s (engine set-up and prefill included); kael CPU {new / cpu_s:.2f} tokens/s")
+    print(f"\nkael nn::generate, temperature {temperature}, top-k {top_k}, on the MI355X decode engine: {new} tokens in "
+          f"{dev_s:.2f} s = {new / dev_s:.1f} tokens/s (engine set-up and prefill included); kael CPU "
+          f"{new / cpu_s:.2f} tokens/s")

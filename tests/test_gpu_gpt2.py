@@ -275,8 +275,10 @@ def oracle_pick(oracle, logits, temperature, top_k, u):
 
 
 @pytest.mark.parametrize("vocab, temperature, top_k", [(11, 0.8, 3), (97, 1.3, 40), (97, 0.5, 96), (97, 2.0, 1),
-                                                        (97, 0.004, 40), (50257, 0.8, 40), (50257, 1.0, 500)],
-                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1", "v97_k40_cold", "v50257_k40", "v50257_k500"])
+                                                        (97, 0.004, 40), (50257, 0.8, 40), (50257, 1.0, 500),
+                                                        (11, 0.8, 0), (97, 1.0, 97), (50257, 1.0, 0)],
+                         ids=["v11_k3", "v97_k40", "v97_k96", "v97_k1", "v97_k40_cold", "v50257_k40", "v50257_k500",
+                              "v11_none", "v97_k_vocab", "v50257_none"])
 def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature, top_k):
     """kael's sample_next on the device (kd_gpt_set_sampling, kd_gpt_set_uniforms): after the prefill and
     after every decode step the engine's pick equals the oracle's restatement of sample_next on the
@@ -284,7 +286,8 @@ def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature,
     the kept weights below 2^-24, where the device sums in sequence instead of across the wave;
     GPT-2's vocabulary takes the bound from the head kernel's 1024 workgroup maxima (k = 40) or,
     with more candidate workgroups than the pick reads, the full scan and the sequential sums over
-    more than 64 kept entries (k = 500)."""
+    more than 64 kept entries (k = 500). Without a top-k (top_k 0, kael's default, or top_k =
+    vocab) nothing is masked: every entry is kept and summed in index order."""
     ref = refdev
     h, g = build(kdb, ref, vocab, 32, 2, 2, 8, 13)
     try:
@@ -301,7 +304,7 @@ def test_sampled_picks_match_the_oracle(kdb, refdev, oracle, vocab, temperature,
             picks.extend(g.decode(1))
             assert picks[-1] == oracle_pick(oracle, g.logits(), temperature, top_k, u[s]), s
         assert g.draws_used() == steps + 1
-        if top_k > 1 and temperature >= 0.1:  # (the cold case nearly always picks the largest)
+        if (top_k > 1 or top_k == 0) and temperature >= 0.1:  # (the cold case nearly always picks the largest)
             assert len(set(picks)) > 1
         # the same draws in one decode call give the same tokens
         g.set_uniforms(u)
@@ -379,7 +382,7 @@ def test_sampling_arguments_and_missing_draws_fail(kdb, refdev):
     del big
     h, g = build(kdb, ref, 11, 16, 1, 2, 8, 3)
     try:
-        for t, k in [(0.8, 0), (0.8, 11), (-1.0, 3)]:
+        for t, k in [(0.8, -1), (-1.0, 3)]:
             with pytest.raises(kd.KdError):
                 g.set_sampling(t, k)
         with pytest.raises(kd.KdError):
