@@ -2,7 +2,7 @@
 //
 // Workload of reference examples/gpt2_generate.cpp: kael's GPT (src/nn/transformer.cpp:103-237)
 // generating with a KV cache (nn::generate, :256-295), greedily or with sample_next's temperature
-// and top-k, batch 1, f32. kael runs it as ~700 device calls per token with blocking host syncs
+// (with or without a top-k), batch 1, f32. kael runs it as ~700 device calls per token with blocking host syncs
 // (embedding index checks, the pick on the host). This engine keeps kael's parameters in kael's
 // layout and its arithmetic, and runs one token per replay of a captured HIP graph:
 //
